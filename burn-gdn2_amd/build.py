@@ -1,0 +1,48 @@
+#!/usr/bin/env python3
+"""Build libgdn2_amd.so for gfx950 in-tree (burn-gdn2_amd/libgdn2_amd.so).
+
+All HIP sources in csrc/ are compiled by one hipcc invocation.  Flags:
+  --offload-arch=gfx950       MI355X only
+  -packed-fp32-ops (disabled) no v_pk_*_f32 generation
+"""
+import glob
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+OUT = os.path.join(HERE, "libgdn2_amd.so")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fvisibility=hidden",
+    "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc"),
+]
+LIBS = []
+
+
+def sources():
+    return sorted(glob.glob(os.path.join(HERE, "csrc", "*.hip")) + glob.glob(os.path.join(HERE, "csrc", "*.cpp")))
+
+
+def build(verbose=False):
+    tmp = OUT + ".tmp"
+    cmd = [HIPCC] + FLAGS + sources() + ["-o", tmp] + LIBS
+    if verbose:
+        print(" ".join(cmd))
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    msgs = [l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l]
+    if r.returncode != 0:
+        sys.stderr.write("\n".join(msgs) + "\n")
+        raise RuntimeError("hipcc failed building libgdn2_amd.so")
+    if msgs and verbose:
+        print("\n".join(msgs))
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

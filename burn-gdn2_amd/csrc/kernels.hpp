@@ -1,0 +1,42 @@
+// Kernel parameter blocks and launchers (internal to libgdn2_amd).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace gdn2 {
+
+// Per-token scan over T tokens (T = 1 is the decode step).
+struct ScanParams {
+    const float *q, *k, *g, *b; // [B, Hk, T, K] strided
+    const float *v, *w;         // [B, HV, T, V] strided
+    const float *state_in;      // [B, HV, K, V]
+    float *state_out;           // [B, HV, K, V] (may equal state_in)
+    float *out;                 // [B, HV, T, V] strided
+    int B, HV, rep, T, K, V;
+    int64_t sqb, sqh, sqt;
+    int64_t svb, svh, svt;
+    int64_t sob, soh, sot;
+    float scale;
+};
+
+// Fused single-token decode.
+struct DecodeParams {
+    const float *q_raw, *k_raw, *f_raw, *b_raw; // [B, kd]
+    const float *v_raw, *w_raw, *gate;          // [B, vd]
+    const float *conv_q_in, *conv_k_in, *conv_v_in;
+    float *conv_q_out, *conv_k_out, *conv_v_out;
+    const float *q_conv_w, *k_conv_w, *v_conv_w;
+    const float *a_log, *dt_bias, *decay_factors, *o_norm_weight;
+    float *state; // [B, HV, K, V] in place
+    float *out;   // [B, vd]
+    int B, H, HV, rep, K, V;
+    int use_short_conv, allow_neg_eigval;
+    float min_decay, one_minus_min_decay, norm_eps, scale;
+};
+
+hipError_t launch_scan(const ScanParams &p, hipStream_t s);
+hipError_t launch_decode(const DecodeParams &p, hipStream_t s);
+
+}  // namespace gdn2

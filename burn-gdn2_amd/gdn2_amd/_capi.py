@@ -1,0 +1,114 @@
+"""ctypes declarations of include/gdn2.h and the loader of libgdn2_amd.so.
+
+The library is built in-tree (burn-gdn2_amd/libgdn2_amd.so) by
+burn-gdn2_amd/build.py.  Loading fails loudly when it is missing: there is
+no CPU fallback in this package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_ROOT, "libgdn2_amd.so")
+
+GDN2_OK = 0
+GDN2_NOT_APPLICABLE = 1
+GDN2_EINVAL = 2
+GDN2_EHIP = 3
+
+_fp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_dbl = ctypes.c_double
+
+
+class StepArgs(ctypes.Structure):
+    _fields_ = [("q", _fp), ("k", _fp), ("g", _fp), ("b", _fp), ("v", _fp), ("w", _fp),
+                ("state_in", _fp), ("state_out", _fp), ("out", _fp),
+                ("batch", _i64), ("num_heads", _i64), ("num_v_heads", _i64), ("head_dim", _i64),
+                ("head_v_dim", _i64),
+                ("stride_qk_b", _i64), ("stride_qk_h", _i64), ("stride_vw_b", _i64), ("stride_vw_h", _i64),
+                ("stride_o_b", _i64), ("stride_o_h", _i64), ("scale", _dbl)]
+
+
+class RecurrentArgs(ctypes.Structure):
+    _fields_ = [("q", _fp), ("k", _fp), ("g", _fp), ("b", _fp), ("v", _fp), ("w", _fp),
+                ("state_in", _fp), ("state_out", _fp), ("out", _fp),
+                ("batch", _i64), ("num_heads", _i64), ("num_v_heads", _i64), ("seq_len", _i64),
+                ("head_dim", _i64), ("head_v_dim", _i64),
+                ("stride_qk_b", _i64), ("stride_qk_h", _i64), ("stride_qk_t", _i64),
+                ("stride_vw_b", _i64), ("stride_vw_h", _i64), ("stride_vw_t", _i64),
+                ("stride_o_b", _i64), ("stride_o_h", _i64), ("stride_o_t", _i64),
+                ("scale", _dbl)]
+
+
+class ChunkArgs(ctypes.Structure):
+    _fields_ = [("q", _fp), ("k", _fp), ("g", _fp), ("b", _fp), ("v", _fp), ("w", _fp),
+                ("state", _fp), ("out", _fp),
+                ("batch", _i64), ("num_heads", _i64), ("num_v_heads", _i64), ("seq_len", _i64),
+                ("head_dim", _i64), ("head_v_dim", _i64),
+                ("stride_qk_b", _i64), ("stride_qk_h", _i64), ("stride_qk_t", _i64),
+                ("stride_vw_b", _i64), ("stride_vw_h", _i64), ("stride_vw_t", _i64),
+                ("stride_o_b", _i64), ("stride_o_h", _i64), ("stride_o_t", _i64),
+                ("scale", _dbl), ("chunk_size", _i64),
+                ("workspace", _fp), ("workspace_bytes", ctypes.c_size_t)]
+
+
+class LayerParams(ctypes.Structure):
+    _fields_ = [("q_conv_w", _fp), ("k_conv_w", _fp), ("v_conv_w", _fp), ("a_log", _fp), ("dt_bias", _fp),
+                ("decay_factors", _fp), ("o_norm_weight", _fp), ("min_decay", _dbl), ("norm_eps", _dbl),
+                ("use_short_conv", ctypes.c_int32), ("allow_neg_eigval", ctypes.c_int32)]
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [("q_raw", _fp), ("k_raw", _fp), ("f_raw", _fp), ("b_raw", _fp), ("v_raw", _fp),
+                ("w_raw", _fp), ("gate", _fp),
+                ("conv_q_in", _fp), ("conv_k_in", _fp), ("conv_v_in", _fp),
+                ("conv_q_out", _fp), ("conv_k_out", _fp), ("conv_v_out", _fp),
+                ("state", _fp), ("out", _fp),
+                ("batch", _i64), ("num_heads", _i64), ("num_v_heads", _i64), ("head_dim", _i64),
+                ("head_v_dim", _i64), ("scale", _dbl), ("params", ctypes.POINTER(LayerParams))]
+
+
+# Every symbol include/gdn2.h declares (checked by tests/test_capi_exports.py).
+EXPORTS = ("gdn2_last_error", "gdn2_hip_available", "gdn2_recurrent_step_f32", "gdn2_recurrent_fwd_f32",
+           "gdn2_chunk_workspace_bytes", "gdn2_chunk_fwd_f32", "gdn2_decode_fused_f32")
+
+_lib = None
+
+
+class Gdn2Error(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"gdn2 status {status}: {msg}")
+        self.status = status
+
+
+def lib():
+    """Load libgdn2_amd.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with burn-gdn2_amd/build.py "
+                               "(or __graft_entry__.build()); there is no CPU fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        L.gdn2_last_error.restype = ctypes.c_char_p
+        L.gdn2_hip_available.restype = ctypes.c_int
+        for name, st in (("gdn2_recurrent_step_f32", StepArgs), ("gdn2_recurrent_fwd_f32", RecurrentArgs),
+                         ("gdn2_chunk_fwd_f32", ChunkArgs), ("gdn2_decode_fused_f32", DecodeArgs)):
+            fn = getattr(L, name)
+            fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
+            fn.restype = ctypes.c_int
+        L.gdn2_chunk_workspace_bytes.argtypes = [ctypes.POINTER(ChunkArgs)]
+        L.gdn2_chunk_workspace_bytes.restype = ctypes.c_size_t
+        _lib = L
+    return _lib
+
+
+def check(status: int, allow_not_applicable=False) -> bool:
+    """Raise on error statuses; return False for GDN2_NOT_APPLICABLE when allowed."""
+    if status == GDN2_OK:
+        return True
+    msg = lib().gdn2_last_error().decode(errors="replace")
+    if status == GDN2_NOT_APPLICABLE and allow_not_applicable:
+        return False
+    raise Gdn2Error(status, msg)

@@ -1,0 +1,165 @@
+"""Kernel-level operators on device tensors, named after the reference
+functions they replace.  Each builds the C-ABI argument block from torch
+tensors (device memory and the current stream only) and calls
+libgdn2_amd.so.
+
+  fused_step               src/kernel/fused_recurrent_cube.rs:108-172
+  fused_recurrent_forward  src/kernel/fused_recurrent.rs:11-55
+  chunk_wy_forward         src/forward.rs:44-278 (+ fused_chunk_forward,
+                           src/kernel/chunk_cube.rs:781-952)
+  decode_fused             forward() at T == 1, src/module.rs:224-316
+
+Tensor conventions follow the reference: q, k, g, b [B, Hk, T, K];
+v, w [B, HV, T, V]; state [B, HV, K, V]; out [B, HV, T, V].  Hk may be
+smaller than HV (value head hv reads key head hv // (HV // Hk)); the
+reference always materialises Hk == HV.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _capi as C
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _check_f32_cuda(*ts):
+    for t in ts:
+        if t is None:
+            continue
+        if t.dtype != torch.float32 or not t.is_cuda:
+            raise TypeError("gdn2_amd operators take float32 device tensors")
+
+
+def _strides3(t: torch.Tensor):
+    if t.stride(3) != 1:
+        raise ValueError("the last (channel) dimension must be contiguous")
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def hip_available() -> bool:
+    return bool(C.lib().gdn2_hip_available())
+
+
+def fused_step(q, k, v, g, b, w, state, scale: float, out_state=None) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+    """One decode step (T == 1).  Returns (out [B,HV,1,V], new_state), or
+    None when the kernel does not apply (the reference's `None`)."""
+    _check_f32_cuda(q, k, v, g, b, w, state)
+    B, Hk, T, K = q.shape
+    HV, V = v.shape[1], v.shape[3]
+    if T != 1:
+        raise ValueError("fused_step takes one token")
+    state = state.contiguous()
+    new_state = torch.empty_like(state) if out_state is None else out_state
+    out = torch.empty((B, HV, 1, V), device=q.device, dtype=torch.float32)
+    sq, sv = _strides3(q), _strides3(v)
+    for t in (k, g, b):
+        if _strides3(t) != sq:
+            raise ValueError("q, k, g, b must share one layout")
+    if _strides3(w) != sv:
+        raise ValueError("v and w must share one layout")
+    a = C.StepArgs(_p(q), _p(k), _p(g), _p(b), _p(v), _p(w), _p(state), _p(new_state), _p(out),
+                   B, Hk, HV, K, V, sq[0], sq[1], sv[0], sv[1], out.stride(0), out.stride(1), float(scale))
+    if not C.check(C.lib().gdn2_recurrent_step_f32(ctypes.byref(a), _stream()), allow_not_applicable=True):
+        return None
+    return out, new_state
+
+
+def fused_recurrent_forward(q, k, v, g, b, w, state, scale: float, out=None, in_place=False):
+    """Per-token scan over T tokens in one launch.  Returns (out, new_state)."""
+    _check_f32_cuda(q, k, v, g, b, w, state)
+    B, Hk, T, K = q.shape
+    HV, V = v.shape[1], v.shape[3]
+    state = state.contiguous()
+    new_state = state if in_place else torch.empty_like(state)
+    if out is None:
+        out = torch.empty((B, HV, T, V), device=q.device, dtype=torch.float32)
+    sq, sv, so = _strides3(q), _strides3(v), _strides3(out)
+    for t in (k, g, b):
+        if _strides3(t) != sq:
+            raise ValueError("q, k, g, b must share one layout")
+    if _strides3(w) != sv:
+        raise ValueError("v and w must share one layout")
+    a = C.RecurrentArgs(_p(q), _p(k), _p(g), _p(b), _p(v), _p(w), _p(state), _p(new_state), _p(out),
+                        B, Hk, HV, T, K, V, *sq, *sv, *so, float(scale))
+    C.check(C.lib().gdn2_recurrent_fwd_f32(ctypes.byref(a), _stream()))
+    return out, new_state
+
+
+def chunk_args(q, k, v, g, b, w, state, out, scale, chunk_size, workspace=None):
+    B, Hk, T, K = q.shape
+    HV, V = v.shape[1], v.shape[3]
+    sq, sv, so = _strides3(q), _strides3(v), _strides3(out)
+    for t in (k, g, b):
+        if _strides3(t) != sq:
+            raise ValueError("q, k, g, b must share one layout")
+    if _strides3(w) != sv:
+        raise ValueError("v and w must share one layout")
+    ws_ptr = None if workspace is None else _p(workspace)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    return C.ChunkArgs(_p(q), _p(k), _p(g), _p(b), _p(v), _p(w), _p(state), _p(out), B, Hk, HV, T, K, V,
+                       *sq, *sv, *so, float(scale), int(chunk_size), ws_ptr, ws_bytes)
+
+
+def chunk_workspace_bytes(q, k, v, g, b, w, state, out, scale, chunk_size) -> int:
+    a = chunk_args(q, k, v, g, b, w, state, out, scale, chunk_size)
+    return int(C.lib().gdn2_chunk_workspace_bytes(ctypes.byref(a)))
+
+
+def chunk_wy_forward(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64, out=None, workspace=None,
+                     in_place=False):
+    """Chunked forward over the whole sequence.  Returns (out, new_state),
+    or None when the chunk kernels do not apply (K, V or chunk size outside
+    their limits)."""
+    _check_f32_cuda(q, k, v, g, b, w, state)
+    B, Hk, T, K = q.shape
+    HV, V = v.shape[1], v.shape[3]
+    st = state.contiguous()
+    if not in_place:
+        st = st.clone()
+    if out is None:
+        out = torch.empty((B, HV, T, V), device=q.device, dtype=torch.float32)
+    need = chunk_workspace_bytes(q, k, v, g, b, w, st, out, scale, chunk_size)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    a = chunk_args(q, k, v, g, b, w, st, out, scale, chunk_size, workspace)
+    if not C.check(C.lib().gdn2_chunk_fwd_f32(ctypes.byref(a), _stream()), allow_not_applicable=True):
+        return None
+    return out, st
+
+
+def decode_fused(raw: dict, params: dict, state, conv_in, conv_out, *, num_heads, num_v_heads, head_dim,
+                 head_v_dim, scale, min_decay=None, norm_eps=1e-5, use_short_conv=True, allow_neg_eigval=False,
+                 out=None):
+    """Fused single-token decode.  raw: q_raw, k_raw, f_raw, b_raw [B, kd];
+    v_raw, w_raw, gate [B, vd].  params: q/k/v_conv_w, a_log, dt_bias,
+    decay_factors (optional), o_norm_weight.  conv_in: (q, k, v) caches
+    [B, 3, kd|vd] or None (no prior state); conv_out: output caches.
+    Updates state in place; returns out [B, vd] (input of o_proj)."""
+    B = raw["q_raw"].shape[0]
+    vd = num_v_heads * head_v_dim
+    if out is None:
+        out = torch.empty((B, vd), device=raw["q_raw"].device, dtype=torch.float32)
+    lp = C.LayerParams(_p(params.get("q_conv_w")), _p(params.get("k_conv_w")), _p(params.get("v_conv_w")),
+                       _p(params["a_log"]), _p(params["dt_bias"]), _p(params.get("decay_factors")),
+                       _p(params["o_norm_weight"]), float(min_decay or 0.0), float(norm_eps),
+                       int(use_short_conv), int(allow_neg_eigval))
+    ci = conv_in if conv_in is not None else (None, None, None)
+    co = conv_out if conv_out is not None else (None, None, None)
+    a = C.DecodeArgs(_p(raw["q_raw"]), _p(raw["k_raw"]), _p(raw["f_raw"]), _p(raw["b_raw"]), _p(raw["v_raw"]),
+                     _p(raw["w_raw"]), _p(raw["gate"]), _p(ci[0]), _p(ci[1]), _p(ci[2]), _p(co[0]), _p(co[1]),
+                     _p(co[2]), _p(state), _p(out), B, num_heads, num_v_heads, head_dim, head_v_dim, float(scale),
+                     ctypes.pointer(lp))
+    C.check(C.lib().gdn2_decode_fused_f32(ctypes.byref(a), _stream()))
+    return out

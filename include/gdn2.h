@@ -1,0 +1,191 @@
+/*
+ * gdn2.h -- C ABI of the MI355X (gfx950) GDN-2 forward path.
+ *
+ * The entry points replace burn-gdn2's backend-gated kernel launchers:
+ *
+ *   gdn2_recurrent_step_f32  <- fused_step            src/kernel/fused_recurrent_cube.rs:108-172
+ *   gdn2_chunk_fwd_f32       <- fused_chunk_forward   src/kernel/chunk_cube.rs:781-952
+ *                               (and the tensor path chunk_wy_forward, src/forward.rs:44-278,
+ *                                which is the only live chunk path in the reference)
+ *   gdn2_decode_fused_f32    <- GatedDeltaNet2::forward at T == 1 between project() and
+ *                               o_proj: short conv (src/short_conv.rs:22-65), gates
+ *                               (src/module.rs:417-443), L2 norm (src/l2norm.rs:13-16),
+ *                               the step, rms_norm_gate_per_head (src/module.rs:501-517)
+ *   gdn2_hip_available       <- is_cuda / CudaBare TypeId gate
+ *                               src/kernel/fused_recurrent_cube.rs:74-78
+ *
+ * Status GDN2_NOT_APPLICABLE plays the role of the reference's `None`: the
+ * shapes or layout are outside what the kernels take, nothing was launched,
+ * and the caller uses its own tensor path.  Every pointer is a device
+ * pointer owned by the caller; no entry point allocates device memory except
+ * where stated.  Launches are asynchronous on `stream` (NULL = the default
+ * stream) and the calls are re-entrant across streams.
+ *
+ * Layout of strided operands: the last (channel) dimension is contiguous;
+ * strides are in elements for (batch, head, time).  The reference's
+ * contiguous [B, H, T, D] tensors have strides {H*T*D, T*D, D}; the
+ * projection layout [B, T, H, D] has {T*H*D, D, H*D}.
+ * Value head hv reads key head hv / (num_v_heads / num_heads).
+ */
+#ifndef GDN2_H_
+#define GDN2_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__) || defined(__clang__)
+#define GDN2_API __attribute__((visibility("default")))
+#else
+#define GDN2_API
+#endif
+
+typedef enum gdn2_status {
+    GDN2_OK = 0,
+    GDN2_NOT_APPLICABLE = 1, /* outside the kernels' limits: fall back (reference `None`) */
+    GDN2_EINVAL = 2,         /* invalid arguments (null pointer, inconsistent shapes) */
+    GDN2_EHIP = 3,           /* HIP runtime error; see gdn2_last_error() */
+} gdn2_status;
+
+/* hipStream_t, passed opaquely so that this header needs no HIP include. */
+typedef void *gdn2_stream_t;
+
+/* Message of the last non-OK status returned on the calling thread. */
+GDN2_API const char *gdn2_last_error(void);
+
+/* 1 when a gfx950 device is current and usable, else 0.
+ * Replaces the TypeId == CudaBare gate (fused_recurrent_cube.rs:76-78). */
+GDN2_API int gdn2_hip_available(void);
+
+/* ------------------------------------------------------------------------
+ * One recurrent step for every (batch, value head)      -- fused_step
+ * (src/kernel/fused_recurrent_cube.rs:108-172, math :14-57):
+ *   S' = diag(exp g) S;  v_new = w*v - S'^T (b*k);  S'' = S' + k v_new^T;
+ *   out = scale * S''^T q
+ * q,k,g,b: [B, Hk, K] with stride_qk_b / stride_qk_h (last dim contiguous)
+ * v,w:     [B, HV, V] with stride_vw_b / stride_vw_h
+ * out:     [B, HV, V] with stride_o_b / stride_o_h
+ * state_in / state_out: [B, HV, K, V] contiguous; may be the same buffer
+ * (in-place update; the reference returns a new buffer).
+ * Limits (else GDN2_NOT_APPLICABLE): K, V <= 1024, same as the reference.
+ * ---------------------------------------------------------------------- */
+typedef struct gdn2_step_args {
+    const float *q, *k, *g, *b;
+    const float *v, *w;
+    const float *state_in;
+    float *state_out;
+    float *out;
+    int64_t batch, num_heads, num_v_heads, head_dim, head_v_dim;
+    int64_t stride_qk_b, stride_qk_h;
+    int64_t stride_vw_b, stride_vw_h;
+    int64_t stride_o_b, stride_o_h;
+    double scale;
+} gdn2_step_args;
+
+GDN2_API gdn2_status gdn2_recurrent_step_f32(const gdn2_step_args *args, gdn2_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Per-token scan over T tokens in one launch       -- fused_recurrent_forward
+ * (src/kernel/fused_recurrent.rs:11-55), the FusedRecurrent-mode path and
+ * the rule for sequences of at most 64 tokens (src/module.rs:245-249).
+ * q,k,g,b: [B, Hk, T, K] strided; v,w: [B, HV, T, V] strided;
+ * out: [B, HV, T, V] strided; state_in/out: [B, HV, K, V] contiguous, may
+ * alias.  S is read once and written once whatever T is.
+ * Limits (else GDN2_NOT_APPLICABLE): K, V <= 1024.
+ * ---------------------------------------------------------------------- */
+typedef struct gdn2_recurrent_args {
+    const float *q, *k, *g, *b;
+    const float *v, *w;
+    const float *state_in;
+    float *state_out;
+    float *out;
+    int64_t batch, num_heads, num_v_heads, seq_len, head_dim, head_v_dim;
+    int64_t stride_qk_b, stride_qk_h, stride_qk_t;
+    int64_t stride_vw_b, stride_vw_h, stride_vw_t;
+    int64_t stride_o_b, stride_o_h, stride_o_t;
+    double scale;
+} gdn2_recurrent_args;
+
+GDN2_API gdn2_status gdn2_recurrent_fwd_f32(const gdn2_recurrent_args *args, gdn2_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Chunked forward over a whole sequence                  -- fused_chunk_forward
+ * (src/kernel/chunk_cube.rs:781-952; semantics of src/forward.rs:44-278):
+ * out[t] and the final state equal T steps of the recurrence above.
+ * q,k,g,b: [B, Hk, T, K] strided;  v,w: [B, HV, T, V] strided
+ * out:     [B, HV, T, V] strided (e.g. [B, T, HV, V] to skip a permute)
+ * state:   [B, HV, K, V] contiguous, read as S0 and overwritten with S_T
+ *          (in place, like the reference's chunk path).
+ * T need not be a multiple of chunk_size.  chunk_size selects the kernel
+ * tile (64 for chunk_size <= 64, else 128); the result does not depend on it
+ * beyond rounding, as in the reference.
+ * workspace: device memory of at least gdn2_chunk_workspace_bytes(args)
+ * bytes, 256-byte aligned.
+ * Limits (else GDN2_NOT_APPLICABLE): K in {64, 128}, V a multiple of 64 up
+ * to 512, chunk_size <= 128.
+ * ---------------------------------------------------------------------- */
+typedef struct gdn2_chunk_args {
+    const float *q, *k, *g, *b;
+    const float *v, *w;
+    float *state;
+    float *out;
+    int64_t batch, num_heads, num_v_heads, seq_len, head_dim, head_v_dim;
+    int64_t stride_qk_b, stride_qk_h, stride_qk_t;
+    int64_t stride_vw_b, stride_vw_h, stride_vw_t;
+    int64_t stride_o_b, stride_o_h, stride_o_t;
+    double scale;
+    int64_t chunk_size;
+    void *workspace;
+    size_t workspace_bytes;
+} gdn2_chunk_args;
+
+GDN2_API size_t gdn2_chunk_workspace_bytes(const gdn2_chunk_args *args);
+GDN2_API gdn2_status gdn2_chunk_fwd_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Fused decode of one token for every batch row           -- forward at T=1
+ * Inputs are the raw projections of one token (outputs of the Linear
+ * layers, src/module.rs:400-402,417-418,442-443,474-475):
+ *   q_raw, k_raw, f_raw, b_raw: [B, kd]   (f_raw = f_proj_1(f_proj_0(x)))
+ *   v_raw, w_raw, gate:         [B, vd]   (gate = g_proj_1(g_proj_0(x)) + bias)
+ * Conv caches [B, 3, kd|vd] hold the last 3 pre-conv rows (oldest first).
+ * conv_*_in NULL means no prior state (src/short_conv.rs:42-54: the token
+ * is replicated).  conv_*_out must not alias conv_*_in.
+ * state [B, HV, K, V] is updated in place.
+ * out [B, vd] = rms_norm_gate_per_head(o) (input of o_proj).
+ * Limits (else GDN2_NOT_APPLICABLE): K <= 256, V <= 1024.
+ * ---------------------------------------------------------------------- */
+typedef struct gdn2_layer_params {
+    const float *q_conv_w, *k_conv_w, *v_conv_w; /* [kd,4],[kd,4],[vd,4]; unused without short conv */
+    const float *a_log;                          /* [H] */
+    const float *dt_bias;                        /* [kd] */
+    const float *decay_factors;                  /* [H*K], NULL when min_decay is None */
+    const float *o_norm_weight;                  /* [V] */
+    double min_decay;
+    double norm_eps;
+    int32_t use_short_conv;
+    int32_t allow_neg_eigval;
+} gdn2_layer_params;
+
+typedef struct gdn2_decode_args {
+    const float *q_raw, *k_raw, *f_raw, *b_raw;
+    const float *v_raw, *w_raw, *gate;
+    const float *conv_q_in, *conv_k_in, *conv_v_in;
+    float *conv_q_out, *conv_k_out, *conv_v_out;
+    float *state;
+    float *out;
+    int64_t batch, num_heads, num_v_heads, head_dim, head_v_dim;
+    double scale;
+    const gdn2_layer_params *params;
+} gdn2_decode_args;
+
+GDN2_API gdn2_status gdn2_decode_fused_f32(const gdn2_decode_args *args, gdn2_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN2_H_ */

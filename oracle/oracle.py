@@ -1,0 +1,284 @@
+"""ctypes front end of the CPU oracle (oracle/gdn2_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the product package.  Each function
+names the reference code it restates; the C file documents how each one is
+pinned.
+
+Array conventions (numpy, C-contiguous):
+  q, k, g, b  [B, Hk, T, K]   (g, b may have last dim 1)
+  v, w        [B, HV, T, V]
+  S           [B, HV, K, V]
+  out         [B, HV, T, V]
+Value head hv reads key head hv // (HV // Hk).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libgdn2_oracle.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_vp = ctypes.c_void_p
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc, OpenMP)."""
+    import subprocess
+
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        i, d = ctypes.c_int, ctypes.c_double
+        L.gdn2o_recurrent_f64.argtypes = [_vp] * 7 + [i] * 8 + [d, _vp, _vp]
+        L.gdn2o_recurrent_f32.argtypes = [_vp] * 7 + [i] * 8 + [d, _vp, _vp]
+        L.gdn2o_chunk_wy_f32.argtypes = [_vp] * 7 + [i] * 8 + [d, i, _vp, _vp]
+        L.gdn2o_short_conv.argtypes = [_vp, _vp, _vp, i, i, i, _vp, _vp]
+        L.gdn2o_l2norm_rows.argtypes = [_vp, ctypes.c_long, i, d]
+        L.gdn2o_rmsnorm_gate.argtypes = [_vp, _vp, _vp, ctypes.c_long, i, d, _vp]
+        L.gdn2o_layer_forward.argtypes = [_vp, _vp, _vp, i, i, i] + [_vp] * 13
+        L.gdn2o_layer_from_raw.argtypes = [_vp, _vp] + [_vp] * 7 + [i, i, i] + [_vp] * 12
+        L.gdn2o_num_threads.restype = i
+        L.gdn2o_set_num_threads.argtypes = [i]
+        _lib = L
+    return _lib
+
+
+def num_threads() -> int:
+    return lib().gdn2o_num_threads()
+
+
+def set_num_threads(n: int) -> None:
+    lib().gdn2o_set_num_threads(int(n))
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _scan_shapes(q, k, v, g, b, w):
+    B, Hk, T, K = q.shape
+    HV, V = v.shape[1], v.shape[3]
+    assert k.shape == q.shape and w.shape == v.shape
+    assert v.shape[0] == B and v.shape[2] == T
+    assert HV % Hk == 0
+    gdim, bdim = g.shape[3], b.shape[3]
+    assert g.shape[:3] == (B, Hk, T) and b.shape[:3] == (B, Hk, T)
+    assert gdim in (1, K) and bdim in (1, K)
+    return B, HV, Hk, T, K, V, gdim, bdim
+
+
+def recurrent_f64(q, k, v, g, b, w, S0=None, scale=1.0):
+    """Per-token scan in double (src/kernel/fused_recurrent.rs:27-52)."""
+    q, k, v, g, b, w = (_c(a, np.float32) for a in (q, k, v, g, b, w))
+    B, HV, Hk, T, K, V, gdim, bdim = _scan_shapes(q, k, v, g, b, w)
+    S0 = None if S0 is None else _c(S0, np.float64)
+    out = np.empty((B, HV, T, V), np.float64)
+    S = np.empty((B, HV, K, V), np.float64)
+    lib().gdn2o_recurrent_f64(*(_ptr(a) for a in (q, k, v, g, b, w, S0)), B, HV, Hk, T, K, V, gdim, bdim,
+                              float(scale), _ptr(out), _ptr(S))
+    return out, S
+
+
+def recurrent_f32(q, k, v, g, b, w, S0=None, scale=1.0):
+    """Per-token scan with the reference's f32 op order (src/kernel/fused_recurrent.rs:25-52)."""
+    q, k, v, g, b, w = (_c(a, np.float32) for a in (q, k, v, g, b, w))
+    B, HV, Hk, T, K, V, gdim, bdim = _scan_shapes(q, k, v, g, b, w)
+    S0 = None if S0 is None else _c(S0, np.float32)
+    out = np.empty((B, HV, T, V), np.float32)
+    S = np.empty((B, HV, K, V), np.float32)
+    lib().gdn2o_recurrent_f32(*(_ptr(a) for a in (q, k, v, g, b, w, S0)), B, HV, Hk, T, K, V, gdim, bdim,
+                              float(scale), _ptr(out), _ptr(S))
+    return out, S
+
+
+def chunk_wy_f32(q, k, v, g, b, w, S0=None, scale=1.0, chunk_size=64):
+    """Chunked WY forward, 16-tile log-space decay, f32 (src/forward.rs:44-278)."""
+    q, k, v, g, b, w = (_c(a, np.float32) for a in (q, k, v, g, b, w))
+    B, HV, Hk, T, K, V, gdim, bdim = _scan_shapes(q, k, v, g, b, w)
+    S0 = None if S0 is None else _c(S0, np.float32)
+    out = np.empty((B, HV, T, V), np.float32)
+    S = np.empty((B, HV, K, V), np.float32)
+    lib().gdn2o_chunk_wy_f32(*(_ptr(a) for a in (q, k, v, g, b, w, S0)), B, HV, Hk, T, K, V, gdim, bdim,
+                             float(scale), int(chunk_size), _ptr(out), _ptr(S))
+    return out, S
+
+
+def short_conv(x, wconv, cache=None):
+    """Causal depthwise conv k=4 + SiLU (src/short_conv.rs:22-65). x [B,T,C]."""
+    x = _c(x, np.float64)
+    wconv = _c(wconv, np.float32)
+    B, T, C = x.shape
+    assert wconv.shape == (C, 4)
+    cache = None if cache is None else _c(cache, np.float64)
+    y = np.empty((B, T, C), np.float64)
+    nc = np.empty((B, 3, C), np.float64)
+    lib().gdn2o_short_conv(_ptr(x), _ptr(wconv), _ptr(cache), B, T, C, _ptr(y), _ptr(nc))
+    return y, nc
+
+
+def l2norm(x, eps=1e-6):
+    """x / sqrt(sum x^2 + eps) over the last dim (src/l2norm.rs:13-16)."""
+    y = np.array(x, dtype=np.float64, order="C", copy=True)
+    n = y.shape[-1]
+    lib().gdn2o_l2norm_rows(_ptr(y), y.size // n, n, float(eps))
+    return y
+
+
+def rmsnorm_gate(x, gate, weight, eps):
+    """x / sqrt(mean x^2 + eps) * weight * silu(gate) (src/module.rs:501-517)."""
+    x = _c(x, np.float64)
+    gate = _c(gate, np.float64)
+    weight = _c(weight, np.float32)
+    n = x.shape[-1]
+    y = np.empty_like(x)
+    lib().gdn2o_rmsnorm_gate(_ptr(x), _ptr(gate), _ptr(weight), x.size // n, n, float(eps), _ptr(y))
+    return y
+
+
+# ---------------------------------------------------------------------------
+# Layer (src/module.rs, src/config.rs)
+# ---------------------------------------------------------------------------
+class _Cfg(ctypes.Structure):
+    _fields_ = [
+        ("hidden", ctypes.c_int), ("heads", ctypes.c_int), ("head_dim", ctypes.c_int),
+        ("num_v_heads", ctypes.c_int), ("head_v_dim", ctypes.c_int),
+        ("use_short_conv", ctypes.c_int), ("allow_neg_eigval", ctypes.c_int),
+        ("mode_chunk", ctypes.c_int), ("chunk_size", ctypes.c_int), ("has_min_decay", ctypes.c_int),
+        ("min_decay", ctypes.c_double), ("norm_eps", ctypes.c_double), ("gva_scrambled", ctypes.c_int),
+    ]
+
+
+WEIGHT_NAMES = ("q_proj", "k_proj", "v_proj", "f_proj_0", "f_proj_1", "b_proj", "w_proj", "g_proj_0",
+                "g_proj_1", "g_proj_1_bias", "a_log", "dt_bias", "o_norm_weight", "o_proj", "q_conv_w",
+                "k_conv_w", "v_conv_w", "decay_factors")
+
+
+class _W(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in WEIGHT_NAMES]
+
+
+@dataclass
+class OracleState:
+    """Gdn2State (src/module.rs:30-63) in double: recurrent [B,HV,K,V], conv caches [B,3,kd|vd]."""
+    recurrent: np.ndarray
+    conv_q: np.ndarray
+    conv_k: np.ndarray
+    conv_v: np.ndarray
+
+
+@dataclass
+class LayerResult:
+    out: np.ndarray
+    o_core: np.ndarray
+    proj: dict = field(default_factory=dict)
+
+
+def layer_forward(cfg, weights: dict, x, state: Optional[OracleState] = None, gva_scrambled=False,
+                  want_proj=False):
+    """GatedDeltaNet2::forward(x, &mut state, true) / forward_train(x) in double.
+
+    cfg: object with hidden_size, num_heads, head_dim, expand_v, num_v_heads,
+    use_short_conv, allow_neg_eigval, norm_eps, chunk_size, min_decay.
+    state None = Option::None on entry (forward_train is the same call with
+    the returned state discarded).  Returns (LayerResult, new OracleState).
+    """
+    H, K = cfg.num_heads, cfg.head_dim
+    HV = cfg.num_v_heads or H
+    V = int(K * cfg.expand_v)
+    kd, vd = H * K, HV * V
+    x = _c(x, np.float32)
+    B, T, D = x.shape
+    c = _Cfg(D, H, K, HV, V, int(cfg.use_short_conv), int(cfg.allow_neg_eigval), 1, int(cfg.chunk_size),
+             int(cfg.min_decay is not None), float(cfg.min_decay or 0.0), float(cfg.norm_eps),
+             int(gva_scrambled))
+    keep = {n: (None if weights.get(n) is None else _c(weights[n], np.float32)) for n in WEIGHT_NAMES}
+    wst = _W(**{n: (None if a is None else a.ctypes.data) for n, a in keep.items()})
+    if state is None:
+        S = np.zeros((B, HV, K, V), np.float64)
+        cq = np.zeros((B, 3, kd), np.float64)
+        ck = np.zeros((B, 3, kd), np.float64)
+        cv = np.zeros((B, 3, vd), np.float64)
+        has = 0
+    else:
+        S = np.array(state.recurrent, np.float64, order="C", copy=True)
+        cq = np.array(state.conv_q, np.float64, order="C", copy=True)
+        ck = np.array(state.conv_k, np.float64, order="C", copy=True)
+        cv = np.array(state.conv_v, np.float64, order="C", copy=True)
+        has = 1
+    out = np.empty((B, T, D), np.float64)
+    oc = np.empty((B, HV, T, V), np.float64)
+    Hk = HV if (gva_scrambled and HV > H) else H
+    proj = {}
+    if want_proj:
+        proj = {n: np.empty((B, Hk, T, K), np.float64) for n in ("q", "k", "g", "b")}
+        proj.update({n: np.empty((B, HV, T, V), np.float64) for n in ("v", "w")})
+        proj["gate"] = np.empty((B, T, HV, V), np.float64)
+    pp = [_ptr(proj.get(n)) for n in ("q", "k", "g", "b", "v", "w", "gate")]
+    lib().gdn2o_layer_forward(ctypes.byref(c), ctypes.byref(wst), _ptr(x), B, T, has, _ptr(S), _ptr(cq),
+                              _ptr(ck), _ptr(cv), _ptr(out), _ptr(oc), *pp)
+    if not cfg.use_short_conv and state is not None:
+        cq, ck, cv = state.conv_q, state.conv_k, state.conv_v
+    return LayerResult(out, oc, proj), OracleState(S, cq, ck, cv)
+
+
+def _cfg_struct(cfg, gva_scrambled):
+    H, K = cfg.num_heads, cfg.head_dim
+    HV = cfg.num_v_heads or H
+    V = int(K * cfg.expand_v)
+    return _Cfg(cfg.hidden_size, H, K, HV, V, int(cfg.use_short_conv), int(cfg.allow_neg_eigval), 1,
+                int(cfg.chunk_size), int(cfg.min_decay is not None), float(cfg.min_decay or 0.0),
+                float(cfg.norm_eps), int(gva_scrambled)), H, K, HV, V
+
+
+RAW_NAMES = ("q_raw", "k_raw", "f_raw", "b_raw", "v_raw", "w_raw", "gate")
+
+
+def layer_from_raw(cfg, weights: dict, raw: dict, state: Optional[OracleState] = None, gva_scrambled=False):
+    """The layer after its Linear layers (src/module.rs:404-476, :244-312), in double.
+
+    raw: Linear outputs [B, T, n]: q_raw, k_raw, f_raw, b_raw (n = kd) and
+    v_raw, w_raw, gate (n = vd, gate with the g_proj_1 bias).  Returns
+    (o_norm [B, T, vd] = input of o_proj, o_core [B, HV, T, V], new state).
+    """
+    c, H, K, HV, V = _cfg_struct(cfg, gva_scrambled)
+    kd, vd = H * K, HV * V
+    rr = {n: _c(raw[n], np.float64) for n in RAW_NAMES}
+    B, T = rr["q_raw"].shape[:2]
+    keep = {n: (None if weights.get(n) is None else _c(weights[n], np.float32)) for n in WEIGHT_NAMES}
+    wst = _W(**{n: (None if a is None else a.ctypes.data) for n, a in keep.items()})
+    if state is None:
+        S = np.zeros((B, HV, K, V), np.float64)
+        cq, ck, cv = (np.zeros((B, 3, n), np.float64) for n in (kd, kd, vd))
+        has = 0
+    else:
+        S = np.array(state.recurrent, np.float64, order="C", copy=True)
+        cq = np.array(state.conv_q, np.float64, order="C", copy=True)
+        ck = np.array(state.conv_k, np.float64, order="C", copy=True)
+        cv = np.array(state.conv_v, np.float64, order="C", copy=True)
+        has = 1
+    on = np.empty((B, T, vd), np.float64)
+    oc = np.empty((B, HV, T, V), np.float64)
+    lib().gdn2o_layer_from_raw(ctypes.byref(c), ctypes.byref(wst), *(_ptr(rr[n]) for n in RAW_NAMES), B, T, has,
+                               _ptr(S), _ptr(cq), _ptr(ck), _ptr(cv), _ptr(on), _ptr(oc),
+                               None, None, None, None, None, None)
+    return on, oc, OracleState(S, cq, ck, cv)
