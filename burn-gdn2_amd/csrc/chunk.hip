@@ -1,11 +1,485 @@
-// Chunked forward: entry points (kernels follow).
+// Chunked GDN-2 forward on gfx950.
+//
+// Semantics: src/forward.rs:44-278 (chunk_wy_forward).  Per chunk of C = 64
+// tokens with G = cumsum_t g (per key channel, from the chunk start):
+//   A_qk[r,s] = scale sum_c q_r k_s exp(G_r - G_s)   (s <= r)
+//   A_kk[r,s] =       sum_c b_r k_r k_s exp(G_r - G_s) (s <  r)
+//   W = (I + A_kk)^-1 (b k exp(G)),  U = (I + A_kk)^-1 (w v)
+//   v_new = U - W S,  out = A_qk v_new + scale (q exp(G)) S
+//   S <- exp(G_last) S + (k exp(G_last - G))^T v_new
+// The inter-chunk part is rewritten as out = P - M S with P = A_qk U and
+// M = A_qk W - scale (q exp(G)), so the sequential kernel does three
+// C x K x V products per chunk and no C x C one.
+//
+// Numerical scheme (every exponent fed to exp2 is <= 0 except where noted):
+//  * A_qk / A_kk off-diagonal 16x16 blocks (row tile p > column tile q):
+//    exp(G_r - G_s) = exp(G_r - Gb_p) * exp(Gb_p - G_s), Gb_p = G at the
+//    last row of tile p-1; both factors <= 1.  One MFMA product per block.
+//  * diagonal blocks: the same split, whose column factor exp(Gb_p - G_s)
+//    is >= 1 but bounded by exp(span) with span = Gb_p - G at the tile end.
+//    Channels with span <= 96 (log2 units) keep the MFMA product; channels
+//    above that (e.g. |g| ~ 30 per token) are zeroed in the MFMA operand
+//    and added exactly with pairwise exp2(G_r - G_s), r >= s.
+//  * WY solve per 16-row tile (src/forward.rs:192-261): the 16x16 diagonal
+//    blocks of I + A_kk are inverted by forward substitution and the tiles
+//    are eliminated in order, never as one 64x64 solve.
+//
+// MFMA mapping (v_mfma_f32_16x16x4_f32, see common.hpp): an accumulator tile
+// holds rows 4*(lane/16)+i, column lane%16; with the contraction label
+// k = 4*(lane/16) + step inside a 16-wide block it is directly the B operand
+// of the next product.  The solve, A_qk [W|U] and, in the inter kernel, the
+// state S and v_new therefore never leave registers.
 #include "common.hpp"
 #include "kernels.hpp"
 
+namespace gdn2 {
+
+namespace {
+
+constexpr int C = kChunk;
+constexpr int NT = C / 16;
+static_assert(NT == 4, "the diagonal-block inverse maps 4 tiles x 16 columns onto one wave");
+constexpr float kSafeSpan = 96.0f; // log2 units
+
+__device__ __forceinline__ float4 ld4(const float *base, int64_t rs, int row, int valid, int col) {
+    if (row >= valid) return make_float4(0.f, 0.f, 0.f, 0.f);
+    return *reinterpret_cast<const float4 *>(base + (int64_t)row * rs + col);
+}
+
+__device__ __forceinline__ float ld1(const float *base, int64_t rs, int row, int valid, int col) {
+    return row < valid ? base[(int64_t)row * rs + col] : 0.f;
+}
+
+__device__ __forceinline__ floatx4 mfma4(float4 a, floatx4 b, floatx4 c) {
+    c = mfma16(a.x, b[0], c);
+    c = mfma16(a.y, b[1], c);
+    c = mfma16(a.z, b[2], c);
+    c = mfma16(a.w, b[3], c);
+    return c;
+}
+
+__device__ __forceinline__ floatx4 mfma4n(float4 a, floatx4 b, floatx4 c) {
+    c = mfma16(-a.x, b[0], c);
+    c = mfma16(-a.y, b[1], c);
+    c = mfma16(-a.z, b[2], c);
+    c = mfma16(-a.w, b[3], c);
+    return c;
+}
+
+// ---------------------------------------------------------------------------
+// chunk-intra: one workgroup (4 waves) per (b, hv, chunk).
+// ---------------------------------------------------------------------------
+template <int K, int V>
+__global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
+    constexpr int KP = K + 4, CP = C + 4;
+    constexpr int NKT = K / 16, NVT = V / 16, NTOT = NKT + NVT, NTW = NTOT / 4;
+    static_assert(NTOT % 4 == 0, "K + V must be a multiple of 64");
+    constexpr int NSEG = 256 / K, RPS = C / NSEG;
+    static_assert(256 % K == 0 && C % NSEG == 0, "K");
+
+    __shared__ __attribute__((aligned(16))) float sG[C][KP];
+    __shared__ __attribute__((aligned(16))) float sAqk[C][CP];
+    __shared__ __attribute__((aligned(16))) float sAkk[C][CP];
+    __shared__ __attribute__((aligned(16))) float sAinv[NT][16][20];
+    __shared__ float sTot[NSEG][K];
+    __shared__ uint32_t sMask[NT][K / 32];
+
+    const int ci = blockIdx.x;
+    const int bh = ci / p.NC, n = ci % p.NC;
+    const int bi = bh / p.HV, hv = bh % p.HV, hk = hv / p.rep;
+    const int t0 = n * C;
+    const int cv = min(C, p.T - t0);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int64_t sqt = p.sqt, svt = p.svt;
+
+    const int64_t kofs = (int64_t)bi * p.sqb + (int64_t)hk * p.sqh + (int64_t)t0 * sqt;
+    const int64_t vofs = (int64_t)bi * p.svb + (int64_t)hv * p.svh + (int64_t)t0 * svt;
+    const float *qc = p.q + kofs, *kc = p.k + kofs, *gc = p.g + kofs, *bc = p.b + kofs;
+    const float *vc = p.v + vofs, *wc = p.w + vofs;
+
+    // 1. G = cumsum_t g per channel, stored in log2 units; rows past the end
+    //    of a ragged last chunk have g = 0 (zero padding, src/forward.rs:94-99).
+    {
+        const int c = tid % K, seg = tid / K;
+        float vals[RPS];
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < RPS; ++i) vals[i] = ld1(gc, sqt, seg * RPS + i, cv, c);
+#pragma unroll
+        for (int i = 0; i < RPS; ++i) {
+            acc += vals[i];
+            vals[i] = acc;
+        }
+        sTot[seg][c] = acc;
+        if (tid < NT * (K / 32)) (&sMask[0][0])[tid] = 0u;
+        __syncthreads();
+        float off = 0.f;
+        for (int s2 = 0; s2 < seg; ++s2) off += sTot[s2][c];
+#pragma unroll
+        for (int i = 0; i < RPS; ++i) sG[seg * RPS + i][c] = (vals[i] + off) * kLog2e;
+        __syncthreads();
+    }
+    for (int idx = tid; idx < NT * K; idx += 256) {
+        const int pt = idx / K, c = idx % K;
+        const float gb = pt ? sG[16 * pt - 1][c] : 0.f;
+        if (gb - sG[16 * pt + 15][c] > kSafeSpan) atomicOr(&sMask[pt][c >> 5], 1u << (c & 31));
+    }
+    __syncthreads();
+
+    // 2. A_qk (waves 0, 1) and A_kk (waves 2, 3); each wave takes two row
+    //    tiles {i, NT-1-i} so that all waves do the same number of blocks.
+    {
+        const int mat = wave >> 1, half = wave & 1;
+#pragma unroll
+        for (int pi = 0; pi < 2; ++pi) {
+            const int pt = pi ? (NT - 1 - half) : half;
+            floatx4 acc[NT];
+#pragma unroll
+            for (int q = 0; q < NT; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+            const int row = 16 * pt + lr;
+#pragma unroll 2
+            for (int m = 0; m < NKT; ++m) {
+                const int c0 = 16 * m + 4 * lg;
+                const float4 gr = *reinterpret_cast<const float4 *>(&sG[row][c0]);
+                float4 gb = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (pt > 0) gb = *reinterpret_cast<const float4 *>(&sG[16 * pt - 1][c0]);
+                float4 a;
+                if (mat == 0) {
+                    a = ld4(qc, sqt, row, cv, c0);
+                } else {
+                    const float4 bb = ld4(bc, sqt, row, cv, c0), kk = ld4(kc, sqt, row, cv, c0);
+                    a = make_float4(bb.x * kk.x, bb.y * kk.y, bb.z * kk.z, bb.w * kk.w);
+                }
+                a.x *= fast_exp2(gr.x - gb.x);
+                a.y *= fast_exp2(gr.y - gb.y);
+                a.z *= fast_exp2(gr.z - gb.z);
+                a.w *= fast_exp2(gr.w - gb.w);
+                const uint32_t mw = sMask[pt][c0 >> 5] >> (c0 & 31);
+#pragma unroll
+                for (int q = 0; q < NT; ++q) {
+                    if (q <= pt) {
+                        const int srow = 16 * q + lr;
+                        const float4 gs = *reinterpret_cast<const float4 *>(&sG[srow][c0]);
+                        const float4 kv = ld4(kc, sqt, srow, cv, c0);
+                        float4 bv;
+                        bv.x = kv.x * fast_exp2(gb.x - gs.x);
+                        bv.y = kv.y * fast_exp2(gb.y - gs.y);
+                        bv.z = kv.z * fast_exp2(gb.z - gs.z);
+                        bv.w = kv.w * fast_exp2(gb.w - gs.w);
+                        if (q == pt) {
+                            if (mw & 1u) bv.x = 0.f;
+                            if (mw & 2u) bv.y = 0.f;
+                            if (mw & 4u) bv.z = 0.f;
+                            if (mw & 8u) bv.w = 0.f;
+                        }
+                        acc[q] = mfma16(a.x, bv.x, acc[q]);
+                        acc[q] = mfma16(a.y, bv.y, acc[q]);
+                        acc[q] = mfma16(a.z, bv.z, acc[q]);
+                        acc[q] = mfma16(a.w, bv.w, acc[q]);
+                    }
+                }
+            }
+            // Diagonal block, channels outside the safe span: exact pairwise terms.
+#pragma unroll
+            for (int q = 0; q < NT; ++q) {
+                if (q == pt) {
+                    for (int wd = 0; wd < K / 32; ++wd) {
+                        uint32_t mw = sMask[pt][wd];
+                        while (mw) {
+                            const int c = wd * 32 + __builtin_ctz(mw);
+                            mw &= mw - 1u;
+                            const int srow = 16 * pt + lr;
+                            const float ks = ld1(kc, sqt, srow, cv, c);
+                            const float gs = sG[srow][c];
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const int r = 4 * lg + i;
+                                if (mat == 0 ? (r >= lr) : (r > lr)) {
+                                    const int rrow = 16 * pt + r;
+                                    const float xr = (mat == 0)
+                                                         ? ld1(qc, sqt, rrow, cv, c)
+                                                         : ld1(bc, sqt, rrow, cv, c) * ld1(kc, sqt, rrow, cv, c);
+                                    acc[q][i] += xr * ks * fast_exp2(sG[rrow][c] - gs);
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < NT; ++q) {
+                if (q <= pt) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = 4 * lg + i;
+                        float val = acc[q][i];
+                        if (mat == 0) {
+                            val *= p.scale;
+                            if (q == pt && r < lr) val = 0.f;
+                            sAqk[16 * pt + r][16 * q + lr] = val;
+                        } else {
+                            if (q == pt && r <= lr) val = 0.f;
+                            sAkk[16 * pt + r][16 * q + lr] = val;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // 3. (I + A_kk_pp)^-1 for the four diagonal 16x16 blocks: lane = (tile, column).
+    if (wave == 0) {
+        const int pt = lane >> 4, j = lane & 15;
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float s = (i == j) ? 1.f : 0.f;
+#pragma unroll
+            for (int m = 0; m < i; ++m) s -= sAkk[16 * pt + i][16 * pt + m] * x[m];
+            x[i] = s;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sAinv[pt][i][j] = x[i];
+    }
+    __syncthreads();
+
+    // 4. Blocked solve of (I + A_kk) [W | U] = [b k exp(G) | w v] and
+    //    Y = A_qk [W | U]; wave w owns column tiles w, w+4, ... of [W | U].
+    const size_t cid = (size_t)ci;
+    float *Wc = p.ws_w + cid * C * K, *Mc = p.ws_m + cid * C * K;
+    float *Uc = p.ws_u + cid * C * V, *Pc = p.ws_p + cid * C * V;
+    floatx4 X[NTW][NT];
+#pragma unroll
+    for (int pt = 0; pt < NT; ++pt) {
+#pragma unroll
+        for (int u = 0; u < NTW; ++u) {
+            const int nt = wave + 4 * u;
+            const bool kcol = nt < NKT;
+            floatx4 R;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * pt + 4 * lg + i;
+                if (kcol) {
+                    const int c = 16 * nt + lr;
+                    R[i] = ld1(bc, sqt, t, cv, c) * ld1(kc, sqt, t, cv, c) * fast_exp2(sG[t][c]);
+                } else {
+                    const int c = 16 * (nt - NKT) + lr;
+                    R[i] = ld1(wc, svt, t, cv, c) * ld1(vc, svt, t, cv, c);
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < NT; ++q)
+                if (q < pt)
+                    R = mfma4n(*reinterpret_cast<const float4 *>(&sAkk[16 * pt + lr][16 * q + 4 * lg]), X[u][q], R);
+            floatx4 Xp = mfma4(*reinterpret_cast<const float4 *>(&sAinv[pt][lr][4 * lg]), R,
+                               floatx4{0.f, 0.f, 0.f, 0.f});
+            X[u][pt] = Xp;
+            floatx4 Y = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < NT; ++q)
+                if (q <= pt) Y = mfma4(*reinterpret_cast<const float4 *>(&sAqk[16 * pt + lr][16 * q + 4 * lg]), X[u][q], Y);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * pt + 4 * lg + i;
+                if (kcol) {
+                    const int c = 16 * nt + lr;
+                    Wc[t * K + c] = Xp[i];
+                    Mc[t * K + c] = Y[i] - p.scale * ld1(qc, sqt, t, cv, c) * fast_exp2(sG[t][c]);
+                } else {
+                    const int c = 16 * (nt - NKT) + lr;
+                    Uc[t * V + c] = Xp[i];
+                    Pc[t * V + c] = Y[i];
+                }
+            }
+        }
+    }
+
+    // 5. (k exp(G_last - G))^T and exp(G_last) for the state update.
+    float *Kc = p.ws_kdt + cid * K * C;
+    for (int idx = tid; idx < K * C; idx += 256) {
+        const int c = idx / C, t = idx % C;
+        Kc[idx] = ld1(kc, sqt, t, cv, c) * fast_exp2(sG[C - 1][c] - sG[t][c]);
+    }
+    if (tid < K) p.ws_gam[cid * K + tid] = fast_exp2(sG[C - 1][tid]);
+}
+
+// ---------------------------------------------------------------------------
+// chunk-inter: one workgroup per (b, hv, 64 value columns); wave w owns 16
+// columns.  S[:, cols] stays in MFMA accumulators for the whole sequence.
+// Per chunk: X1 = W S, X2 = M S (C x K x 16 each), v_new = U - X1,
+// out = P - X2, S = exp(G_last) S + Kd^T v_new (K x C x 16).
+// ---------------------------------------------------------------------------
+template <int K>
+__global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
+    constexpr int NKT = K / 16;
+    const int V = p.V;
+    const int nvs = V / 64;
+    const int bh = blockIdx.x / nvs, vs = blockIdx.x % nvs;
+    const int bi = bh / p.HV, hv = bh % p.HV;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int col = vs * 64 + 16 * wave + lr;
+
+    float *Sg = p.state + (size_t)bh * K * V;
+    floatx4 S[NKT];
+#pragma unroll
+    for (int kb = 0; kb < NKT; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S[kb][i] = Sg[(size_t)(16 * kb + 4 * lg + i) * V + col];
+
+    float *ob = p.out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + col;
+    for (int n = 0; n < p.NC; ++n) {
+        const size_t cid = (size_t)bh * p.NC + n;
+        const float *Wc = p.ws_w + cid * C * K, *Mc = p.ws_m + cid * C * K;
+        const float *Uc = p.ws_u + cid * C * V + col, *Pc = p.ws_p + cid * C * V + col;
+        const float *Kc = p.ws_kdt + cid * K * C, *gam = p.ws_gam + cid * K;
+        const int cv = min(C, p.T - n * C);
+
+        floatx4 X1[NT], X2[NT];
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt) X1[mt] = X2[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < NKT; ++kb)
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt) {
+                const int off = (16 * mt + lr) * K + 16 * kb + 4 * lg;
+                X1[mt] = mfma4(*reinterpret_cast<const float4 *>(Wc + off), S[kb], X1[mt]);
+                X2[mt] = mfma4(*reinterpret_cast<const float4 *>(Mc + off), S[kb], X2[mt]);
+            }
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * mt + 4 * lg + i;
+                X1[mt][i] = Uc[t * V] - X1[mt][i];
+                const float o = Pc[t * V] - X2[mt][i];
+                if (t < cv) ob[(int64_t)(n * C + t) * p.sot] = o;
+            }
+#pragma unroll
+        for (int kb = 0; kb < NKT; ++kb) {
+            const float4 gm = *reinterpret_cast<const float4 *>(gam + 16 * kb + 4 * lg);
+            S[kb][0] *= gm.x;
+            S[kb][1] *= gm.y;
+            S[kb][2] *= gm.z;
+            S[kb][3] *= gm.w;
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt)
+                S[kb] = mfma4(*reinterpret_cast<const float4 *>(Kc + (16 * kb + lr) * C + 16 * tt + 4 * lg), X1[tt],
+                              S[kb]);
+        }
+    }
+#pragma unroll
+    for (int kb = 0; kb < NKT; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Sg[(size_t)(16 * kb + 4 * lg + i) * V + col] = S[kb][i];
+}
+
+template <int K, int V>
+hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s) {
+    const int nchunks = p.B * p.HV * p.NC;
+    hipLaunchKernelGGL((chunk_intra_kernel<K, V>), dim3(nchunks), dim3(256), 0, s, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((chunk_inter_kernel<K>), dim3(p.B * p.HV * (V / 64)), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool chunk_supported(int K, int V) {
+    return (K == 64 || K == 128) && (V == 64 || V == 128 || V == 256);
+}
+
+hipError_t launch_chunk(const ChunkParams &p, hipStream_t s) {
+    if (p.K == 128 && p.V == 128) return launch_chunk_t<128, 128>(p, s);
+    if (p.K == 128 && p.V == 256) return launch_chunk_t<128, 256>(p, s);
+    if (p.K == 128 && p.V == 64) return launch_chunk_t<128, 64>(p, s);
+    if (p.K == 64 && p.V == 64) return launch_chunk_t<64, 64>(p, s);
+    if (p.K == 64 && p.V == 128) return launch_chunk_t<64, 128>(p, s);
+    if (p.K == 64 && p.V == 256) return launch_chunk_t<64, 256>(p, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace gdn2
+
 using namespace gdn2;
 
-extern "C" size_t gdn2_chunk_workspace_bytes(const gdn2_chunk_args *a) { return 0; }
+namespace {
 
+struct WsLayout {
+    size_t w, m, u, p, kdt, gam, total;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+WsLayout ws_layout(int64_t nchunks, int64_t K, int64_t V) {
+    WsLayout L;
+    size_t off = 0;
+    L.w = off; off = align256(off + sizeof(float) * nchunks * kChunk * K);
+    L.m = off; off = align256(off + sizeof(float) * nchunks * kChunk * K);
+    L.u = off; off = align256(off + sizeof(float) * nchunks * kChunk * V);
+    L.p = off; off = align256(off + sizeof(float) * nchunks * kChunk * V);
+    L.kdt = off; off = align256(off + sizeof(float) * nchunks * kChunk * K);
+    L.gam = off; off = align256(off + sizeof(float) * nchunks * K);
+    L.total = off;
+    return L;
+}
+
+int64_t num_chunks(const gdn2_chunk_args *a) {
+    return a->batch * a->num_v_heads * ((a->seq_len + kChunk - 1) / kChunk);
+}
+
+bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" size_t gdn2_chunk_workspace_bytes(const gdn2_chunk_args *a) {
+    if (!a || a->batch <= 0 || a->num_v_heads <= 0 || a->seq_len <= 0 || a->head_dim <= 0 || a->head_v_dim <= 0)
+        return 0;
+    return ws_layout(num_chunks(a), a->head_dim, a->head_v_dim).total;
+}
+
+// fused_chunk_forward (src/kernel/chunk_cube.rs:781-952) / chunk_wy_forward
+// (src/forward.rs:44-278).  Limits: K in {64, 128}, V in {64, 128, 256},
+// 16-byte aligned q, k, b with strides that are multiples of 4 elements.
 extern "C" gdn2_status gdn2_chunk_fwd_f32(const gdn2_chunk_args *a, gdn2_stream_t stream) {
-    return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_fwd_f32: chunk kernels not built yet");
+    if (!a) return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: null args");
+    if (!a->q || !a->k || !a->g || !a->b || !a->v || !a->w || !a->state || !a->out)
+        return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: null tensor pointer");
+    if (a->batch <= 0 || a->num_heads <= 0 || a->num_v_heads <= 0 || a->head_dim <= 0 || a->head_v_dim <= 0 ||
+        a->seq_len < 0)
+        return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: invalid dimensions");
+    if (a->chunk_size <= 0) return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: chunk_size must be > 0");
+    if (a->num_v_heads % a->num_heads != 0)
+        return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: num_v_heads must be a multiple of num_heads");
+    if (!chunk_supported((int)a->head_dim, (int)a->head_v_dim))
+        return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_fwd_f32: (K, V) outside the chunk kernels' instances");
+    if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->b) || (a->stride_qk_b % 4) || (a->stride_qk_h % 4) ||
+        (a->stride_qk_t % 4))
+        return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_fwd_f32: q/k/b need 16-byte aligned rows");
+    if (a->seq_len == 0) return GDN2_OK;
+    const WsLayout L = ws_layout(num_chunks(a), a->head_dim, a->head_v_dim);
+    if (!a->workspace || a->workspace_bytes < L.total || (reinterpret_cast<uintptr_t>(a->workspace) & 255u))
+        return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: workspace missing, too small or not 256-byte aligned");
+    ChunkParams p{};
+    p.q = a->q; p.k = a->k; p.g = a->g; p.b = a->b; p.v = a->v; p.w = a->w;
+    p.state = a->state; p.out = a->out;
+    p.B = (int)a->batch; p.HV = (int)a->num_v_heads; p.rep = (int)(a->num_v_heads / a->num_heads);
+    p.T = (int)a->seq_len; p.K = (int)a->head_dim; p.V = (int)a->head_v_dim;
+    p.NC = (int)((a->seq_len + kChunk - 1) / kChunk);
+    p.sqb = a->stride_qk_b; p.sqh = a->stride_qk_h; p.sqt = a->stride_qk_t;
+    p.svb = a->stride_vw_b; p.svh = a->stride_vw_h; p.svt = a->stride_vw_t;
+    p.sob = a->stride_o_b; p.soh = a->stride_o_h; p.sot = a->stride_o_t;
+    p.scale = (float)a->scale;
+    char *ws = static_cast<char *>(a->workspace);
+    p.ws_w = reinterpret_cast<float *>(ws + L.w);
+    p.ws_m = reinterpret_cast<float *>(ws + L.m);
+    p.ws_u = reinterpret_cast<float *>(ws + L.u);
+    p.ws_p = reinterpret_cast<float *>(ws + L.p);
+    p.ws_kdt = reinterpret_cast<float *>(ws + L.kdt);
+    p.ws_gam = reinterpret_cast<float *>(ws + L.gam);
+    GDN2_HIP_CHECK(launch_chunk(p, (hipStream_t)stream));
+    return GDN2_OK;
 }

@@ -36,7 +36,31 @@ struct DecodeParams {
     float min_decay, one_minus_min_decay, norm_eps, scale;
 };
 
+// Chunked forward (two kernels: chunk-intra, then chunk-inter).
+struct ChunkParams {
+    const float *q, *k, *g, *b; // [B, Hk, T, K] strided
+    const float *v, *w;         // [B, HV, T, V] strided
+    float *state;               // [B, HV, K, V] in/out
+    float *out;                 // [B, HV, T, V] strided
+    int B, HV, rep, T, K, V, NC; // NC = number of chunks per sequence
+    int64_t sqb, sqh, sqt;
+    int64_t svb, svh, svt;
+    int64_t sob, soh, sot;
+    float scale;
+    // workspace (per chunk, chunk id = (b * HV + hv) * NC + n):
+    float *ws_w;   // [nchunks][C][K]  W = (I + A_kk)^-1 (b*k*gamma)
+    float *ws_m;   // [nchunks][C][K]  M = A_qk W - scale * (q * gamma)
+    float *ws_u;   // [nchunks][C][V]  U = (I + A_kk)^-1 (w*v)
+    float *ws_p;   // [nchunks][C][V]  P = A_qk U
+    float *ws_kdt; // [nchunks][K][C]  (k * exp(G_last - G))^T
+    float *ws_gam; // [nchunks][K]     exp(G_last)
+};
+
+constexpr int kChunk = 64; // chunk length of the kernels (four 16-row tiles)
+
 hipError_t launch_scan(const ScanParams &p, hipStream_t s);
 hipError_t launch_decode(const DecodeParams &p, hipStream_t s);
+bool chunk_supported(int K, int V);
+hipError_t launch_chunk(const ChunkParams &p, hipStream_t s);
 
 }  // namespace gdn2

@@ -82,9 +82,11 @@ def fused_recurrent_forward(q, k, v, g, b, w, state, scale: float, out=None, in_
     B, Hk, T, K = q.shape
     HV, V = v.shape[1], v.shape[3]
     state = state.contiguous()
-    new_state = state if in_place else torch.empty_like(state)
     if out is None:
         out = torch.empty((B, HV, T, V), device=q.device, dtype=torch.float32)
+    if T == 0:
+        return out, (state if in_place else state.clone())
+    new_state = state if in_place else torch.empty_like(state)
     sq, sv, so = _strides3(q), _strides3(v), _strides3(out)
     for t in (k, g, b):
         if _strides3(t) != sq:
@@ -130,6 +132,8 @@ def chunk_wy_forward(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64
         st = st.clone()
     if out is None:
         out = torch.empty((B, HV, T, V), device=q.device, dtype=torch.float32)
+    if T == 0:
+        return out, st
     need = chunk_workspace_bytes(q, k, v, g, b, w, st, out, scale, chunk_size)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)

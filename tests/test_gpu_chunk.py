@@ -1,0 +1,124 @@
+"""GPU parity of the chunk kernels (chunk-intra + chunk-inter).
+
+Reference points: the double per-token recurrence (ground truth) and the
+f32 restatement of chunk_wy_forward (the reference tensor path) where that
+one stays finite.  Tolerance: max |error| <= 1e-4 on outputs and the final
+state (tests/test_chunk.rs:254-255)."""
+import numpy as np
+import pytest
+
+from conftest import rand_inputs
+from gdn2_testutil import maxabs
+from oracle import oracle as O
+
+TOL = 1e-4
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(gpu, *arrs):
+    import torch
+
+    return [torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(gpu) for a in arrs]
+
+
+CASES = [
+    # B, Hk, HV, T, K, V, g range, b_hi, S0 scale
+    (2, 2, 2, 64, 128, 128, (-0.3, -0.02), 1.0, 0.0),
+    (1, 2, 2, 130, 128, 128, (-0.15, -0.01), 1.0, 1.0),   # ragged, nonzero S0 (tests/test_chunk.rs:200-256)
+    (2, 1, 1, 200, 128, 128, (-5.0, -0.5), 1.0, 0.5),     # strong decay (tests/stable_chunk.rs:70-73)
+    (1, 2, 2, 256, 128, 128, (-31.0, -0.05), 1.0, 0.5),   # |g| up to 31: in-tile spans beyond f32 exp range
+    (1, 2, 4, 150, 128, 256, (-0.4, -0.01), 2.0, 0.5),    # GVA rep 2, V = 2K, negative eigenvalues
+    (2, 2, 2, 97, 64, 64, (-0.3, -0.02), 1.0, 0.5),       # K = V = 64 (config 1 shape)
+    (1, 1, 1, 1, 128, 128, (-0.3, -0.02), 1.0, 1.0),      # T = 1
+    (1, 1, 2, 63, 64, 128, (-1.0, -0.1), 2.0, 0.3),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}g{c[6][0]}" for c in CASES])
+def test_chunk_matches_recurrence(gpu, case):
+    import gdn2_amd
+
+    B, Hk, HV, T, K, V, (glo, ghi), bhi, s0 = case
+    rng = np.random.default_rng(1000 + T + K + V)
+    q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=glo, g_hi=ghi, b_hi=bhi)
+    q *= K ** -0.5 * 4  # keep |q| comparable to the module's L2-normalised queries
+    S0 = (rng.standard_normal((B, HV, K, V)) * s0).astype(np.float32)
+    scale = K ** -0.5
+    o_ref, S_ref = O.recurrent_f64(q, k, v, g, b, w, S0=S0, scale=scale)
+    d = _dev(gpu, q, k, v, g, b, w, S0)
+    res = gdn2_amd.chunk_wy_forward(*d, scale, chunk_size=64)
+    assert res is not None
+    o, S = res
+    eo, es = maxabs(o.cpu().numpy(), o_ref), maxabs(S.cpu().numpy(), S_ref)
+    print(f"max|out err|={eo:.2e} max|S err|={es:.2e}")
+    assert eo < TOL and es < TOL
+    # the reference tensor path (f32 restatement) agrees wherever it is finite
+    o32, S32 = O.chunk_wy_f32(q, k, v, g, b, w, S0=S0, scale=scale, chunk_size=64)
+    if np.all(np.isfinite(o32)) and np.all(np.isfinite(S32)):
+        assert maxabs(o.cpu().numpy(), o32) < TOL and maxabs(S.cpu().numpy(), S32) < TOL
+
+
+def test_chunk_strided_views_and_in_place_state(gpu):
+    """q/k/g/b/v/w as [B, H, T, D] views of [B, T, H, D] storage and out
+    written straight into [B, T, HV, V] (no permute copies)."""
+    import torch
+
+    import gdn2_amd
+
+    rng = np.random.default_rng(5)
+    B, H, T, K, V = 2, 3, 140, 128, 128
+    q, k, v, g, b, w = rand_inputs(rng, B, H, H, T, K, V)
+    q *= 0.3
+    o_ref, S_ref = O.recurrent_f64(q, k, v, g, b, w, scale=0.2)
+    bt = [torch.from_numpy(np.ascontiguousarray(a.transpose(0, 2, 1, 3))).to(gpu) for a in (q, k, v, g, b, w)]
+    views = [x.permute(0, 2, 1, 3) for x in bt]
+    S = torch.zeros((B, H, K, V), device=gpu)
+    out = torch.empty((B, T, H, V), device=gpu)
+    res = gdn2_amd.chunk_wy_forward(*views, S, 0.2, out=out.permute(0, 2, 1, 3), in_place=True)
+    assert res is not None
+    assert maxabs(out.permute(0, 2, 1, 3).cpu().numpy(), o_ref) < TOL
+    assert maxabs(S.cpu().numpy(), S_ref) < TOL
+
+
+def test_chunk_continuation_equals_one_pass(gpu):
+    """Two calls carrying the state (T1 + T2 tokens) == one call over T1 + T2."""
+    import torch
+
+    import gdn2_amd
+
+    rng = np.random.default_rng(6)
+    B, H, T, K, V = 1, 2, 300, 128, 128
+    q, k, v, g, b, w = rand_inputs(rng, B, H, H, T, K, V)
+    q *= 0.3
+    d = _dev(gpu, q, k, v, g, b, w)
+    S = torch.zeros((B, H, K, V), device=gpu)
+    o_full, S_full = gdn2_amd.chunk_wy_forward(*d, S, 0.1)
+    cut = 100
+    o1, S1 = gdn2_amd.chunk_wy_forward(*[x[:, :, :cut] for x in d], S, 0.1)
+    o2, S2 = gdn2_amd.chunk_wy_forward(*[x[:, :, cut:] for x in d], S1, 0.1)
+    assert maxabs(torch.cat([o1, o2], 2).cpu().numpy(), o_full.cpu().numpy()) < TOL
+    assert maxabs(S2.cpu().numpy(), S_full.cpu().numpy()) < TOL
+
+
+def test_chunk_not_applicable_outside_instances(gpu):
+    """K = 16 is outside the chunk kernels: the reference's `None`."""
+    import torch
+
+    import gdn2_amd
+
+    rng = np.random.default_rng(7)
+    d = _dev(gpu, *rand_inputs(rng, 1, 1, 1, 20, 16, 8))
+    assert gdn2_amd.chunk_wy_forward(*d, torch.zeros((1, 1, 16, 8), device=gpu), 0.25) is None
+
+
+def test_chunk_empty_sequence_keeps_state(gpu):
+    import torch
+
+    import gdn2_amd
+
+    rng = np.random.default_rng(8)
+    d = _dev(gpu, *rand_inputs(rng, 1, 1, 1, 0, 128, 128))
+    S0 = torch.randn((1, 1, 128, 128), device=gpu)
+    o, S = gdn2_amd.chunk_wy_forward(*d, S0, 0.1)
+    assert o.shape == (1, 1, 0, 128) and torch.equal(S, S0)
