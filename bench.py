@@ -1,0 +1,302 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X GDN-2 forward path (one JSON line on stdout).
+
+Headline workload (`value`): chunked prefill of the default layer,
+hidden 2048, 16 heads, head_dim 128, expand_v 1, chunk 64, x ~ N(0,1) of
+shape [8, 4096, 2048] through seeded random-init weights (the reference's
+initialisers, src/module.rs:121-187).  One step = one chunked forward of
+the recurrence core (chunk-intra + chunk-inter kernels) over all
+8 x 16 x 4096 token-heads, inputs already resident in HBM.  The projected
+operands (q, k, g, b, v, w) are produced once, outside the timed region.
+
+Also reported: B = 64 fused decode (short conv + gates + L2 norm + step +
+gated RMSNorm per token), timed over 256 tokens with 5 rotating state
+buffers (335 MB, larger than the 256 MB MALL; the kernel's time does not
+depend on the state values), and the CPU oracle on a bounded sample of the
+same prefill workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "burn-gdn2_amd"), os.path.join(ROOT, "tests")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "prefill tokens/s + decode tokens/s (H=16,d=128); % of MFMA/HBM roofline"
+PEAK_F32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--seq", type=int, default=4096)
+    ap.add_argument("--decode-batch", type=int, default=64)
+    ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--decode-rotate", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-batch", type=int, default=2)
+    return ap.parse_args()
+
+
+def project_inputs(torch, W, x, cfg):
+    """Layer projections of x (src/module.rs:381-495) on the device, in f32,
+    as input preparation: returns q, k, g, b [B, H, T, K] and v, w
+    [B, HV, T, V] contiguous."""
+    B, T, D = x.shape
+    H, K, HV, V = cfg.num_heads, cfg.head_dim, cfg.hv, cfg.v_head
+    x2 = x.reshape(B * T, D)
+
+    def conv_silu(raw, wconv):
+        r = raw.reshape(B, T, -1)
+        xp = torch.cat([r[:, :1].expand(B, 3, r.shape[2]), r], dim=1)
+        y = sum(xp[:, i:i + T] * wconv[:, i] for i in range(4))
+        return torch.nn.functional.silu(y)
+
+    q = conv_silu(x2 @ W["q_proj"], W["q_conv_w"])
+    k = conv_silu(x2 @ W["k_proj"], W["k_conv_w"])
+    v = conv_silu(x2 @ W["v_proj"], W["v_conv_w"])
+    f = (x2 @ W["f_proj_0"]) @ W["f_proj_1"]
+    a = torch.exp(W["a_log"]).repeat_interleave(K)
+    g = (-a * torch.nn.functional.softplus(f + W["dt_bias"])).reshape(B, T, -1)
+    b = torch.sigmoid(x2 @ W["b_proj"]).reshape(B, T, -1)
+    w = torch.sigmoid(x2 @ W["w_proj"]).reshape(B, T, -1)
+
+    def heads(t, n, d):
+        return t.reshape(B, T, n, d).permute(0, 2, 1, 3).contiguous()
+
+    q, k = heads(q, H, K), heads(k, H, K)
+    q = q / torch.sqrt((q * q).sum(-1, keepdim=True) + 1e-6)
+    k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+    return q, k, heads(v, HV, V), heads(g, H, K), heads(b, H, K), heads(w, HV, V)
+
+
+def load_traffic(name):
+    """HBM bytes per launch measured by rocprofv3 --pmc (profiles/*.json), if present."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        return json.load(fh)
+
+
+def bench_prefill(torch, gdn2_amd, args, dev):
+    from gdn2_testutil import Cfg, init_weights
+
+    cfg = Cfg(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0, chunk_size=64, mode="chunk")
+    B, T, H, K, V, C = args.batch, args.seq, cfg.num_heads, cfg.head_dim, cfg.v_head, 64
+    Wn = init_weights(cfg, seed=1337)
+    W = {n: torch.from_numpy(a).to(dev) for n, a in Wn.items() if a is not None}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(42)
+    x = torch.randn((B, T, cfg.hidden_size), generator=gen, device=dev, dtype=torch.float32)
+    with torch.no_grad():
+        q, k, v, g, b, w = project_inputs(torch, W, x, cfg)
+    del x
+    state = torch.zeros((B, H, K, V), device=dev)
+    out = torch.empty((B, H, T, V), device=dev)
+    scale = K ** -0.5
+    from gdn2_amd import _capi as CA
+    from gdn2_amd.ops import _stream, chunk_args
+
+    need = gdn2_amd.chunk_workspace_bytes(q, k, v, g, b, w, state, out, scale, C)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    cargs = chunk_args(q, k, v, g, b, w, state, out, scale, C, ws)
+    import ctypes
+
+    L = CA.lib()
+    stream = _stream()
+    pa = ctypes.byref(cargs)
+
+    def step():
+        CA.check(L.gdn2_chunk_intra_f32(pa, stream))
+        CA.check(L.gdn2_chunk_inter_f32(pa, stream))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+            torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for e0, e1, e2 in evs:
+        e0.record()
+        CA.check(L.gdn2_chunk_intra_f32(pa, stream))
+        e1.record()
+        CA.check(L.gdn2_chunk_inter_f32(pa, stream))
+        e2.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    intra_ms = sum(e0.elapsed_time(e1) for e0, e1, _ in evs) / args.steps
+    inter_ms = sum(e1.elapsed_time(e2) for _, e1, e2 in evs) / args.steps
+    ms_per_step = wall * 1e3 / args.steps
+    tokens = B * T
+    intra_gflop = B * H * T * 2 * C * (3 * K + V) / 1e9
+    inter_gflop = B * H * T * (6 * K * V + 2 * C * V) / 1e9
+    kernels = {
+        "chunk_intra": {"ms": intra_ms, "gflop": intra_gflop,
+                        "tflops": intra_gflop / intra_ms, "frac_f32_mfma": intra_gflop / intra_ms / PEAK_F32_TFLOPS},
+        "chunk_inter": {"ms": inter_ms, "gflop": inter_gflop,
+                        "tflops": inter_gflop / inter_ms, "frac_f32_mfma": inter_gflop / inter_ms / PEAK_F32_TFLOPS},
+    }
+    dom = "chunk_intra" if intra_ms >= inter_ms else "chunk_inter"
+    tr = load_traffic(f"{dom}_b8_t4096_traffic.json")
+    roof = {"kernel": dom, "bound": "mfma", "achieved": kernels[dom]["tflops"], "peak": PEAK_F32_TFLOPS,
+            "unit": "TFLOP/s", "frac": kernels[dom]["frac_f32_mfma"],
+            "traffic": None if tr is None else tr.get("hbm_bytes_per_launch"),
+            "per_launch_gflop": kernels[dom]["gflop"]}
+    host = {"q": q[:args.cpu_batch].cpu().numpy(), "k": k[:args.cpu_batch].cpu().numpy(),
+            "v": v[:args.cpu_batch].cpu().numpy(), "g": g[:args.cpu_batch].cpu().numpy(),
+            "b": b[:args.cpu_batch].cpu().numpy(), "w": w[:args.cpu_batch].cpu().numpy()}
+    del q, k, v, g, b, w, ws
+    return {"tokens": tokens, "ms_per_step": ms_per_step, "value": tokens / (ms_per_step / 1e3),
+            "kernels": kernels, "roofline": roof, "host_sample": host, "scale": scale, "cfg": cfg}
+
+
+def bench_decode(torch, gdn2_amd, args, dev):
+    from gdn2_testutil import Cfg, init_weights
+
+    cfg = Cfg(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0)
+    Bd, H, K, V = args.decode_batch, cfg.num_heads, cfg.head_dim, cfg.v_head
+    kd, vd = cfg.kd, cfg.vd
+    Wn = init_weights(cfg, seed=1337)
+    W = {n: torch.from_numpy(a).to(dev) for n, a in Wn.items() if a is not None}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(43)
+    steps = args.decode_steps
+    # raw projections of the generated tokens (Linear outputs), prepared up front
+    x = torch.randn((steps, Bd, cfg.hidden_size), generator=gen, device=dev)
+    with torch.no_grad():
+        raw = {"q_raw": x @ W["q_proj"], "k_raw": x @ W["k_proj"], "v_raw": x @ W["v_proj"],
+               "f_raw": (x @ W["f_proj_0"]) @ W["f_proj_1"], "b_raw": x @ W["b_proj"], "w_raw": x @ W["w_proj"],
+               "gate": (x @ W["g_proj_0"]) @ W["g_proj_1"] + W["g_proj_1_bias"]}
+    del x
+    nrot = max(1, args.decode_rotate)
+    # state as after a prefill: a random symmetric-ish bounded state
+    states = [torch.randn((Bd, H, K, V), generator=gen, device=dev) * 0.05 for _ in range(nrot)]
+    conv = [tuple(torch.randn((Bd, 3, n), generator=gen, device=dev) for n in (kd, kd, vd)) for _ in range(2)]
+    out = torch.empty((Bd, vd), device=dev)
+    params = {n: W[n] for n in ("q_conv_w", "k_conv_w", "v_conv_w", "a_log", "dt_bias", "o_norm_weight")}
+
+    import ctypes
+
+    from gdn2_amd import _capi as CA
+    from gdn2_amd.ops import _stream, decode_args
+
+    # argument blocks built up front: the timed loop is one C call per token
+    blocks = [decode_args({n: a[t] for n, a in raw.items()}, params, states[t % nrot], conv[t % 2],
+                          conv[(t + 1) % 2], out, num_heads=H, num_v_heads=H, head_dim=K, head_v_dim=V,
+                          scale=K ** -0.5, norm_eps=cfg.norm_eps) for t in range(steps)]
+    L, stream = CA.lib(), _stream()
+    fn = L.gdn2_decode_fused_f32
+    for t in range(min(8, steps)):
+        CA.check(fn(ctypes.byref(blocks[t]), stream))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for t in range(steps):
+        fn(ctypes.byref(blocks[t]), stream)
+    e1.record()
+    torch.cuda.synchronize()
+    CA.check(fn(ctypes.byref(blocks[0]), stream))  # surfaces any launch error of the timed loop
+    ms = e0.elapsed_time(e1) / steps
+    state_bytes = 2 * Bd * H * K * V * 4
+    io_bytes = Bd * (4 * kd + 3 * vd) * 4 + 2 * Bd * 3 * (2 * kd + vd) * 4 + Bd * vd * 4
+    param_bytes = (4 * (2 * kd + vd) + H + kd + V) * 4
+    bytes_step = state_bytes + io_bytes + param_bytes
+    gbs = bytes_step / (ms / 1e3) / 1e9
+    return {"batch": Bd, "tokens_per_s": Bd / (ms / 1e3), "ms_per_token_step": ms, "bytes_per_step": bytes_step,
+            "core_bytes_per_step": 2 * Bd * H * K * V * 4 + Bd * (4 * H * K + 3 * H * V) * 4,
+            "achieved_GBs": gbs, "peak_GBs": PEAK_HBM_GBS, "frac_hbm": gbs / PEAK_HBM_GBS,
+            "rotating_state_buffers": nrot, "kernel": "gdn2_decode_fused_f32"}
+
+
+def cpu_baseline(pre, args):
+    """The oracle's f32 restatement of chunk_wy_forward (the reference's
+    Chunk-mode tensor path) on the host cores, on the first cpu_batch
+    sequences of the same projected inputs."""
+    from oracle import oracle as O
+
+    hs = pre["host_sample"]
+    n = hs["q"].shape[0]
+    O.chunk_wy_f32(*(a[:, :, :256] for a in (hs["q"], hs["k"], hs["v"], hs["g"], hs["b"], hs["w"])),
+                   scale=pre["scale"], chunk_size=64)  # warm-up
+    t0 = time.perf_counter()
+    O.chunk_wy_f32(hs["q"], hs["k"], hs["v"], hs["g"], hs["b"], hs["w"], scale=pre["scale"], chunk_size=64)
+    dt = time.perf_counter() - t0
+    T = hs["q"].shape[2]
+    cores = O.num_threads()
+    return {"value": n * T / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{n} of 8 sequences x {T} tokens x 16 heads, f32 chunk_wy_forward restatement "
+                      f"(oracle/gdn2_oracle.c), {cores} OpenMP threads, {dt:.2f} s",
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the GDN-2 path shards over (batch, value head) with no "
+              f"communication, so multi-GPU throughput is N x the one-GPU figure; --gpus {args.gpus} "
+              f"is not run here.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import gdn2_amd
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = torch.device("cuda:0")
+    if not gdn2_amd.hip_available():
+        raise SystemExit("no gfx950 device: bench.py needs an MI355X")
+    pre = bench_prefill(torch, gdn2_amd, args, dev)
+    dec = None if args.no_decode else bench_decode(torch, gdn2_amd, args, dev)
+    cpu = None if args.no_cpu else cpu_baseline(pre, args)
+    line = {
+        "metric": METRIC,
+        "value": pre["value"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": pre["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: x ~ N(0,1) through seeded random-init layer weights (reference initialisers)",
+        "config": {"workload": f"chunked prefill, recurrence core (chunk-intra + chunk-inter), B={args.batch} "
+                               f"T={args.seq} H=16 K=V=128 chunk=64",
+                   "batch": args.batch, "seq_len": args.seq, "heads": 16, "head_dim": 128, "head_v_dim": 128,
+                   "chunk_size": 64},
+        "roofline": pre["roofline"],
+        "cpu_baseline": cpu,
+        "kernels": pre["kernels"],
+        "decode": dec,
+        "decode_tokens_per_s": None if dec is None else dec["tokens_per_s"],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -377,13 +377,18 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
 }
 
 template <int K, int V>
-hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s) {
-    const int nchunks = p.B * p.HV * p.NC;
-    hipLaunchKernelGGL((chunk_intra_kernel<K, V>), dim3(nchunks), dim3(256), 0, s, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((chunk_inter_kernel<K>), dim3(p.B * p.HV * (V / 64)), dim3(256), 0, s, p);
-    return hipGetLastError();
+hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
+    if (phases & 1) {
+        const int nchunks = p.B * p.HV * p.NC;
+        hipLaunchKernelGGL((chunk_intra_kernel<K, V>), dim3(nchunks), dim3(256), 0, s, p);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (phases & 2) {
+        hipLaunchKernelGGL((chunk_inter_kernel<K>), dim3(p.B * p.HV * (V / 64)), dim3(256), 0, s, p);
+        return hipGetLastError();
+    }
+    return hipSuccess;
 }
 
 }  // namespace
@@ -392,13 +397,13 @@ bool chunk_supported(int K, int V) {
     return (K == 64 || K == 128) && (V == 64 || V == 128 || V == 256);
 }
 
-hipError_t launch_chunk(const ChunkParams &p, hipStream_t s) {
-    if (p.K == 128 && p.V == 128) return launch_chunk_t<128, 128>(p, s);
-    if (p.K == 128 && p.V == 256) return launch_chunk_t<128, 256>(p, s);
-    if (p.K == 128 && p.V == 64) return launch_chunk_t<128, 64>(p, s);
-    if (p.K == 64 && p.V == 64) return launch_chunk_t<64, 64>(p, s);
-    if (p.K == 64 && p.V == 128) return launch_chunk_t<64, 128>(p, s);
-    if (p.K == 64 && p.V == 256) return launch_chunk_t<64, 256>(p, s);
+hipError_t launch_chunk(const ChunkParams &p, hipStream_t s, int phases) {
+    if (p.K == 128 && p.V == 128) return launch_chunk_t<128, 128>(p, s, phases);
+    if (p.K == 128 && p.V == 256) return launch_chunk_t<128, 256>(p, s, phases);
+    if (p.K == 128 && p.V == 64) return launch_chunk_t<128, 64>(p, s, phases);
+    if (p.K == 64 && p.V == 64) return launch_chunk_t<64, 64>(p, s, phases);
+    if (p.K == 64 && p.V == 128) return launch_chunk_t<64, 128>(p, s, phases);
+    if (p.K == 64 && p.V == 256) return launch_chunk_t<64, 256>(p, s, phases);
     return hipErrorInvalidValue;
 }
 
@@ -444,7 +449,7 @@ extern "C" size_t gdn2_chunk_workspace_bytes(const gdn2_chunk_args *a) {
 // fused_chunk_forward (src/kernel/chunk_cube.rs:781-952) / chunk_wy_forward
 // (src/forward.rs:44-278).  Limits: K in {64, 128}, V in {64, 128, 256},
 // 16-byte aligned q, k, b with strides that are multiples of 4 elements.
-extern "C" gdn2_status gdn2_chunk_fwd_f32(const gdn2_chunk_args *a, gdn2_stream_t stream) {
+static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, int phases) {
     if (!a) return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: null args");
     if (!a->q || !a->k || !a->g || !a->b || !a->v || !a->w || !a->state || !a->out)
         return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: null tensor pointer");
@@ -480,6 +485,18 @@ extern "C" gdn2_status gdn2_chunk_fwd_f32(const gdn2_chunk_args *a, gdn2_stream_
     p.ws_p = reinterpret_cast<float *>(ws + L.p);
     p.ws_kdt = reinterpret_cast<float *>(ws + L.kdt);
     p.ws_gam = reinterpret_cast<float *>(ws + L.gam);
-    GDN2_HIP_CHECK(launch_chunk(p, (hipStream_t)stream));
+    GDN2_HIP_CHECK(launch_chunk(p, (hipStream_t)stream, phases));
     return GDN2_OK;
+}
+
+extern "C" gdn2_status gdn2_chunk_fwd_f32(const gdn2_chunk_args *a, gdn2_stream_t stream) {
+    return chunk_call(a, stream, 3);
+}
+
+extern "C" gdn2_status gdn2_chunk_intra_f32(const gdn2_chunk_args *a, gdn2_stream_t stream) {
+    return chunk_call(a, stream, 1);
+}
+
+extern "C" gdn2_status gdn2_chunk_inter_f32(const gdn2_chunk_args *a, gdn2_stream_t stream) {
+    return chunk_call(a, stream, 2);
 }

@@ -61,6 +61,6 @@ constexpr int kChunk = 64; // chunk length of the kernels (four 16-row tiles)
 hipError_t launch_scan(const ScanParams &p, hipStream_t s);
 hipError_t launch_decode(const DecodeParams &p, hipStream_t s);
 bool chunk_supported(int K, int V);
-hipError_t launch_chunk(const ChunkParams &p, hipStream_t s);
+hipError_t launch_chunk(const ChunkParams &p, hipStream_t s, int phases); // bit 0: intra, bit 1: inter
 
 }  // namespace gdn2

@@ -72,7 +72,8 @@ class DecodeArgs(ctypes.Structure):
 
 # Every symbol include/gdn2.h declares (checked by tests/test_capi_exports.py).
 EXPORTS = ("gdn2_last_error", "gdn2_hip_available", "gdn2_recurrent_step_f32", "gdn2_recurrent_fwd_f32",
-           "gdn2_chunk_workspace_bytes", "gdn2_chunk_fwd_f32", "gdn2_decode_fused_f32")
+           "gdn2_chunk_workspace_bytes", "gdn2_chunk_fwd_f32", "gdn2_chunk_intra_f32", "gdn2_chunk_inter_f32",
+           "gdn2_decode_fused_f32")
 
 _lib = None
 
@@ -94,7 +95,8 @@ def lib():
         L.gdn2_last_error.restype = ctypes.c_char_p
         L.gdn2_hip_available.restype = ctypes.c_int
         for name, st in (("gdn2_recurrent_step_f32", StepArgs), ("gdn2_recurrent_fwd_f32", RecurrentArgs),
-                         ("gdn2_chunk_fwd_f32", ChunkArgs), ("gdn2_decode_fused_f32", DecodeArgs)):
+                         ("gdn2_chunk_fwd_f32", ChunkArgs), ("gdn2_chunk_intra_f32", ChunkArgs),
+                         ("gdn2_chunk_inter_f32", ChunkArgs), ("gdn2_decode_fused_f32", DecodeArgs)):
             fn = getattr(L, name)
             fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
             fn.restype = ctypes.c_int

@@ -143,6 +143,25 @@ def chunk_wy_forward(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64
     return out, st
 
 
+def decode_args(raw: dict, params: dict, state, conv_in, conv_out, out, *, num_heads, num_v_heads, head_dim,
+                head_v_dim, scale, min_decay=None, norm_eps=1e-5, use_short_conv=True, allow_neg_eigval=False):
+    """Build the gdn2_decode_args block (the LayerParams it points to is
+    kept alive as an attribute of the returned struct)."""
+    B = raw["q_raw"].shape[0]
+    lp = C.LayerParams(_p(params.get("q_conv_w")), _p(params.get("k_conv_w")), _p(params.get("v_conv_w")),
+                       _p(params["a_log"]), _p(params["dt_bias"]), _p(params.get("decay_factors")),
+                       _p(params["o_norm_weight"]), float(min_decay or 0.0), float(norm_eps),
+                       int(use_short_conv), int(allow_neg_eigval))
+    ci = conv_in if conv_in is not None else (None, None, None)
+    co = conv_out if conv_out is not None else (None, None, None)
+    a = C.DecodeArgs(_p(raw["q_raw"]), _p(raw["k_raw"]), _p(raw["f_raw"]), _p(raw["b_raw"]), _p(raw["v_raw"]),
+                     _p(raw["w_raw"]), _p(raw["gate"]), _p(ci[0]), _p(ci[1]), _p(ci[2]), _p(co[0]), _p(co[1]),
+                     _p(co[2]), _p(state), _p(out), B, num_heads, num_v_heads, head_dim, head_v_dim, float(scale),
+                     ctypes.pointer(lp))
+    a._keep = lp
+    return a
+
+
 def decode_fused(raw: dict, params: dict, state, conv_in, conv_out, *, num_heads, num_v_heads, head_dim,
                  head_v_dim, scale, min_decay=None, norm_eps=1e-5, use_short_conv=True, allow_neg_eigval=False,
                  out=None):
@@ -155,15 +174,8 @@ def decode_fused(raw: dict, params: dict, state, conv_in, conv_out, *, num_heads
     vd = num_v_heads * head_v_dim
     if out is None:
         out = torch.empty((B, vd), device=raw["q_raw"].device, dtype=torch.float32)
-    lp = C.LayerParams(_p(params.get("q_conv_w")), _p(params.get("k_conv_w")), _p(params.get("v_conv_w")),
-                       _p(params["a_log"]), _p(params["dt_bias"]), _p(params.get("decay_factors")),
-                       _p(params["o_norm_weight"]), float(min_decay or 0.0), float(norm_eps),
-                       int(use_short_conv), int(allow_neg_eigval))
-    ci = conv_in if conv_in is not None else (None, None, None)
-    co = conv_out if conv_out is not None else (None, None, None)
-    a = C.DecodeArgs(_p(raw["q_raw"]), _p(raw["k_raw"]), _p(raw["f_raw"]), _p(raw["b_raw"]), _p(raw["v_raw"]),
-                     _p(raw["w_raw"]), _p(raw["gate"]), _p(ci[0]), _p(ci[1]), _p(ci[2]), _p(co[0]), _p(co[1]),
-                     _p(co[2]), _p(state), _p(out), B, num_heads, num_v_heads, head_dim, head_v_dim, float(scale),
-                     ctypes.pointer(lp))
+    a = decode_args(raw, params, state, conv_in, conv_out, out, num_heads=num_heads, num_v_heads=num_v_heads,
+                    head_dim=head_dim, head_v_dim=head_v_dim, scale=scale, min_decay=min_decay, norm_eps=norm_eps,
+                    use_short_conv=use_short_conv, allow_neg_eigval=allow_neg_eigval)
     C.check(C.lib().gdn2_decode_fused_f32(ctypes.byref(a), _stream()))
     return out

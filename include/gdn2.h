@@ -145,6 +145,15 @@ typedef struct gdn2_chunk_args {
 GDN2_API size_t gdn2_chunk_workspace_bytes(const gdn2_chunk_args *args);
 GDN2_API gdn2_status gdn2_chunk_fwd_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
 
+/* The two phases of gdn2_chunk_fwd_f32, for phase-isolated timing; they
+ * replace the reference's diagnostics intra_launch_raw / inter_launch_raw
+ * (src/kernel/chunk_cube.rs:954-1137).  gdn2_chunk_intra_f32 (parallel over
+ * all chunks) fills the workspace; gdn2_chunk_inter_f32 (sequential over
+ * chunks) consumes it, writes out and updates state.  Called in this order
+ * on one stream with the same args they equal gdn2_chunk_fwd_f32. */
+GDN2_API gdn2_status gdn2_chunk_intra_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
+GDN2_API gdn2_status gdn2_chunk_inter_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Fused decode of one token for every batch row           -- forward at T=1
  * Inputs are the raw projections of one token (outputs of the Linear
