@@ -58,6 +58,19 @@ __device__ __forceinline__ floatx4 mfma4(float4 a, floatx4 b, floatx4 c) {
     return c;
 }
 
+// D = X^T for an accumulator tile X, i.e. the A-operand layout of X
+// (lane (g, r) gets X[r][4g..4g+3]): the accumulator is a valid A operand
+// of X^T under the k = 4g + step labelling, multiplied by the identity.
+// Exact in f32 (products with 1 and 0).
+__device__ __forceinline__ floatx4 transpose16(floatx4 x, int lr, int lg) {
+    floatx4 d = floatx4{0.f, 0.f, 0.f, 0.f};
+    d = mfma16(x[0], lr == 4 * lg + 0 ? 1.f : 0.f, d);
+    d = mfma16(x[1], lr == 4 * lg + 1 ? 1.f : 0.f, d);
+    d = mfma16(x[2], lr == 4 * lg + 2 ? 1.f : 0.f, d);
+    d = mfma16(x[3], lr == 4 * lg + 3 ? 1.f : 0.f, d);
+    return d;
+}
+
 __device__ __forceinline__ floatx4 mfma4n(float4 a, floatx4 b, floatx4 c) {
     c = mfma16(-a.x, b[0], c);
     c = mfma16(-a.y, b[1], c);
@@ -247,9 +260,16 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
 
     // 4. Blocked solve of (I + A_kk) [W | U] = [b k exp(G) | w v] and
     //    Y = A_qk [W | U]; wave w owns column tiles w, w+4, ... of [W | U].
+    //    Outputs go to the workspace in MFMA fragment order (one 1 KB block
+    //    of 64 lanes x float4 per 16x16 tile) so that every store here and
+    //    every load in chunk-inter is a contiguous 16-byte access per lane:
+    //      W, M : A-operand fragments (lane (g, r) holds rows r, cols 4g..4g+3)
+    //      U, P : accumulator fragments (lane (g, c) holds rows 4g..4g+3, col c)
     const size_t cid = (size_t)ci;
-    float *Wc = p.ws_w + cid * C * K, *Mc = p.ws_m + cid * C * K;
-    float *Uc = p.ws_u + cid * C * V, *Pc = p.ws_p + cid * C * V;
+    float4 *Wf = reinterpret_cast<float4 *>(p.ws_w) + cid * (C * K / 4);
+    float4 *Mf = reinterpret_cast<float4 *>(p.ws_m) + cid * (C * K / 4);
+    float4 *Uf = reinterpret_cast<float4 *>(p.ws_u) + cid * (C * V / 4);
+    float4 *Pf = reinterpret_cast<float4 *>(p.ws_p) + cid * (C * V / 4);
     floatx4 X[NTW][NT];
 #pragma unroll
     for (int pt = 0; pt < NT; ++pt) {
@@ -280,47 +300,87 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
 #pragma unroll
             for (int q = 0; q < NT; ++q)
                 if (q <= pt) Y = mfma4(*reinterpret_cast<const float4 *>(&sAqk[16 * pt + lr][16 * q + 4 * lg]), X[u][q], Y);
+            if (kcol) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * pt + 4 * lg + i;
-                if (kcol) {
-                    const int c = 16 * nt + lr;
-                    Wc[t * K + c] = Xp[i];
-                    Mc[t * K + c] = Y[i] - p.scale * ld1(qc, sqt, t, cv, c) * fast_exp2(sG[t][c]);
-                } else {
-                    const int c = 16 * (nt - NKT) + lr;
-                    Uc[t * V + c] = Xp[i];
-                    Pc[t * V + c] = Y[i];
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * pt + 4 * lg + i, c = 16 * nt + lr;
+                    Y[i] -= p.scale * ld1(qc, sqt, t, cv, c) * fast_exp2(sG[t][c]);
                 }
+                const floatx4 Wt = transpose16(Xp, lr, lg), Mt = transpose16(Y, lr, lg);
+                const int f = pt * NKT + nt;
+                Wf[f * 64 + lane] = make_float4(Wt[0], Wt[1], Wt[2], Wt[3]);
+                Mf[f * 64 + lane] = make_float4(Mt[0], Mt[1], Mt[2], Mt[3]);
+            } else {
+                const int f = (nt - NKT) * NT + pt;
+                Uf[f * 64 + lane] = make_float4(Xp[0], Xp[1], Xp[2], Xp[3]);
+                Pf[f * 64 + lane] = make_float4(Y[0], Y[1], Y[2], Y[3]);
             }
         }
     }
 
-    // 5. (k exp(G_last - G))^T and exp(G_last) for the state update.
-    float *Kc = p.ws_kdt + cid * K * C;
-    for (int idx = tid; idx < K * C; idx += 256) {
-        const int c = idx / C, t = idx % C;
-        Kc[idx] = ld1(kc, sqt, t, cv, c) * fast_exp2(sG[C - 1][c] - sG[t][c]);
+    // 5. Kd^T = (k exp(G_last - G))^T as A-operand fragments (kb, tt): lane
+    //    (g, r) holds Kd[16 tt + 4 g + j][16 kb + r], and exp(G_last).
+    float4 *Kf = reinterpret_cast<float4 *>(p.ws_kdt) + cid * (C * K / 4);
+    for (int f = wave; f < NKT * NT; f += 4) {
+        const int kb = f / NT, tt = f % NT, ch = 16 * kb + lr;
+        const float gl = sG[C - 1][ch];
+        float4 val;
+        val.x = ld1(kc, sqt, 16 * tt + 4 * lg + 0, cv, ch) * fast_exp2(gl - sG[16 * tt + 4 * lg + 0][ch]);
+        val.y = ld1(kc, sqt, 16 * tt + 4 * lg + 1, cv, ch) * fast_exp2(gl - sG[16 * tt + 4 * lg + 1][ch]);
+        val.z = ld1(kc, sqt, 16 * tt + 4 * lg + 2, cv, ch) * fast_exp2(gl - sG[16 * tt + 4 * lg + 2][ch]);
+        val.w = ld1(kc, sqt, 16 * tt + 4 * lg + 3, cv, ch) * fast_exp2(gl - sG[16 * tt + 4 * lg + 3][ch]);
+        Kf[f * 64 + lane] = val;
     }
     if (tid < K) p.ws_gam[cid * K + tid] = fast_exp2(sG[C - 1][tid]);
+}
+
+// Sequences are spread over the 8 XCDs (workgroup i runs on XCD i % 8) so
+// that the V-slices of one sequence, which read the same W, M and Kd^T,
+// land on the same XCD and share its L2.  Identity when the sequence count
+// is not a multiple of 8.
+__device__ __forceinline__ void inter_block(int blk, int nseq, int nvs, int *bh, int *vs) {
+    if (nseq % 8 == 0) {
+        const int x = blk % 8, j = blk / 8;
+        *bh = x + 8 * (j / nvs);
+        *vs = j % nvs;
+    } else {
+        *bh = blk / nvs;
+        *vs = blk % nvs;
+    }
 }
 
 // ---------------------------------------------------------------------------
 // chunk-inter: one workgroup per (b, hv, 64 value columns); wave w owns 16
 // columns.  S[:, cols] stays in MFMA accumulators for the whole sequence.
-// Per chunk: X1 = W S, X2 = M S (C x K x 16 each), v_new = U - X1,
-// out = P - X2, S = exp(G_last) S + Kd^T v_new (K x C x 16).
+// Per chunk n:
+//   A: X1 = W S, X2 = M S               (reads sW, sM)
+//   B: v_new = U - X1, out = P - X2
+//   C: S = exp(G_last) S + Kd^T v_new   (reads sKd, sGam)
+// LDS holds one chunk of W, M (2 C K floats) and Kd^T (K C floats).  Each
+// buffer is refilled while the other phase runs: Kd^T(n) is fetched during
+// A(n) and stored after it; W, M(n+1) are fetched during B, C(n) and stored
+// after C(n).  HBM latency is therefore off the sequential path without a
+// second copy of the buffers.
 // ---------------------------------------------------------------------------
 template <int K>
 __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
     constexpr int NKT = K / 16;
+    constexpr int FR = NKT * NT;   // 16x16 fragments per operand per chunk
+    constexpr int OPF4 = FR * 64;  // float4 per operand per chunk
+    constexpr int PFO = OPF4 / 256; // float4 per lane per operand
+    static_assert(OPF4 % 256 == 0, "K");
+    __shared__ floatx4 sW[OPF4], sM[OPF4], sKd[OPF4];
+    __shared__ floatx4 sGam[K / 4];
+
     const int V = p.V;
     const int nvs = V / 64;
-    const int bh = blockIdx.x / nvs, vs = blockIdx.x % nvs;
+    int bh, vs;
+    inter_block(blockIdx.x, p.B * p.HV, nvs, &bh, &vs);
     const int bi = bh / p.HV, hv = bh % p.HV;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
-    const int col = vs * 64 + 16 * wave + lr;
+    const int vt = vs * 4 + wave; // this wave's 16-column tile of V
+    const int col = 16 * vt + lr;
 
     float *Sg = p.state + (size_t)bh * K * V;
     floatx4 S[NKT];
@@ -329,45 +389,126 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) S[kb][i] = Sg[(size_t)(16 * kb + 4 * lg + i) * V + col];
 
+    const floatx4 *__restrict__ W4 = reinterpret_cast<const floatx4 *>(p.ws_w);
+    const floatx4 *__restrict__ M4 = reinterpret_cast<const floatx4 *>(p.ws_m);
+    const floatx4 *__restrict__ K4 = reinterpret_cast<const floatx4 *>(p.ws_kdt);
+    const floatx4 *__restrict__ U4 = reinterpret_cast<const floatx4 *>(p.ws_u);
+    const floatx4 *__restrict__ P4 = reinterpret_cast<const floatx4 *>(p.ws_p);
+    const floatx4 *__restrict__ G4 = reinterpret_cast<const floatx4 *>(p.ws_gam);
+    const size_t cid0 = (size_t)bh * p.NC;
+    const size_t uvf4 = (size_t)C * V / 4;
+
+    if (p.NC > 0) {
+#pragma unroll
+        for (int i = 0; i < PFO; ++i) {
+            sW[i * 256 + tid] = W4[cid0 * OPF4 + i * 256 + tid];
+            sM[i * 256 + tid] = M4[cid0 * OPF4 + i * 256 + tid];
+        }
+    }
+
     float *ob = p.out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + col;
     for (int n = 0; n < p.NC; ++n) {
-        const size_t cid = (size_t)bh * p.NC + n;
-        const float *Wc = p.ws_w + cid * C * K, *Mc = p.ws_m + cid * C * K;
-        const float *Uc = p.ws_u + cid * C * V + col, *Pc = p.ws_p + cid * C * V + col;
-        const float *Kc = p.ws_kdt + cid * K * C, *gam = p.ws_gam + cid * K;
-        const int cv = min(C, p.T - n * C);
+        const size_t cid = cid0 + n;
+        __syncthreads(); // sW, sM hold chunk n; every wave is done with sKd(n-1)
+        floatx4 kpre[PFO], u_cur[NT], p_cur[NT], g_cur = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < PFO; ++i) kpre[i] = K4[cid * OPF4 + i * 256 + tid];
+        if (tid < K / 4) g_cur = G4[cid * (K / 4) + tid];
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt) {
+            u_cur[mt] = U4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
+            p_cur[mt] = P4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
+        }
 
+        // A: X1 = W S, X2 = M S
         floatx4 X1[NT], X2[NT];
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) X1[mt] = X2[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kb = 0; kb < NKT; ++kb)
+        for (int kb = 0; kb < NKT; ++kb) {
+            floatx4 wa[NT], ma[NT];
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) {
-                const int off = (16 * mt + lr) * K + 16 * kb + 4 * lg;
-                X1[mt] = mfma4(*reinterpret_cast<const float4 *>(Wc + off), S[kb], X1[mt]);
-                X2[mt] = mfma4(*reinterpret_cast<const float4 *>(Mc + off), S[kb], X2[mt]);
+                wa[mt] = sW[(mt * NKT + kb) * 64 + lane];
+                ma[mt] = sM[(mt * NKT + kb) * 64 + lane];
+            }
+            // eight independent accumulator chains per k-step
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt) {
+                X1[mt] = mfma16(wa[mt][0], S[kb][0], X1[mt]);
+                X2[mt] = mfma16(ma[mt][0], S[kb][0], X2[mt]);
             }
 #pragma unroll
-        for (int mt = 0; mt < NT; ++mt)
+            for (int mt = 0; mt < NT; ++mt) {
+                X1[mt] = mfma16(wa[mt][1], S[kb][1], X1[mt]);
+                X2[mt] = mfma16(ma[mt][1], S[kb][1], X2[mt]);
+            }
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt) {
+                X1[mt] = mfma16(wa[mt][2], S[kb][2], X1[mt]);
+                X2[mt] = mfma16(ma[mt][2], S[kb][2], X2[mt]);
+            }
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt) {
+                X1[mt] = mfma16(wa[mt][3], S[kb][3], X1[mt]);
+                X2[mt] = mfma16(ma[mt][3], S[kb][3], X2[mt]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PFO; ++i) sKd[i * 256 + tid] = kpre[i];
+        if (tid < K / 4) sGam[tid] = g_cur;
+        __syncthreads(); // A done everywhere (sW, sM free); sKd(n) visible
+
+        // W, M of chunk n+1 (the last chunk re-fetches itself: harmless, and
+        // unconditional loads keep the staging registers out of scratch)
+        const size_t cnx = cid + (n + 1 < p.NC ? 1 : 0);
+        floatx4 wpre[PFO], mpre[PFO];
+#pragma unroll
+        for (int i = 0; i < PFO; ++i) {
+            wpre[i] = W4[cnx * OPF4 + i * 256 + tid];
+            mpre[i] = M4[cnx * OPF4 + i * 256 + tid];
+        }
+
+        // B: v_new = U - X1 (kept in X1), out = P - X2
+        const int cv = min(C, p.T - n * C);
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int t = 16 * mt + 4 * lg + i;
-                X1[mt][i] = Uc[t * V] - X1[mt][i];
-                const float o = Pc[t * V] - X2[mt][i];
-                if (t < cv) ob[(int64_t)(n * C + t) * p.sot] = o;
+                X1[mt][i] = u_cur[mt][i] - X1[mt][i];
+                if (t < cv) ob[(int64_t)(n * C + t) * p.sot] = p_cur[mt][i] - X2[mt][i];
             }
+        }
+
+        // C: S = exp(G_last) S + Kd^T v_new
 #pragma unroll
         for (int kb = 0; kb < NKT; ++kb) {
-            const float4 gm = *reinterpret_cast<const float4 *>(gam + 16 * kb + 4 * lg);
-            S[kb][0] *= gm.x;
-            S[kb][1] *= gm.y;
-            S[kb][2] *= gm.z;
-            S[kb][3] *= gm.w;
+            const floatx4 gm = sGam[4 * kb + lg];
+            S[kb][0] *= gm[0];
+            S[kb][1] *= gm[1];
+            S[kb][2] *= gm[2];
+            S[kb][3] *= gm[3];
+        }
 #pragma unroll
-            for (int tt = 0; tt < NT; ++tt)
-                S[kb] = mfma4(*reinterpret_cast<const float4 *>(Kc + (16 * kb + lr) * C + 16 * tt + 4 * lg), X1[tt],
-                              S[kb]);
+        for (int tt = 0; tt < NT; ++tt) {
+            floatx4 ka[NKT];
+#pragma unroll
+            for (int kb = 0; kb < NKT; ++kb) ka[kb] = sKd[(kb * NT + tt) * 64 + lane];
+            // NKT independent accumulator chains per k-step
+#pragma unroll
+            for (int kb = 0; kb < NKT; ++kb) S[kb] = mfma16(ka[kb][0], X1[tt][0], S[kb]);
+#pragma unroll
+            for (int kb = 0; kb < NKT; ++kb) S[kb] = mfma16(ka[kb][1], X1[tt][1], S[kb]);
+#pragma unroll
+            for (int kb = 0; kb < NKT; ++kb) S[kb] = mfma16(ka[kb][2], X1[tt][2], S[kb]);
+#pragma unroll
+            for (int kb = 0; kb < NKT; ++kb) S[kb] = mfma16(ka[kb][3], X1[tt][3], S[kb]);
+        }
+#pragma unroll
+        for (int i = 0; i < PFO; ++i) {
+            sW[i * 256 + tid] = wpre[i];
+            sM[i * 256 + tid] = mpre[i];
         }
     }
 #pragma unroll

@@ -47,13 +47,14 @@ struct ChunkParams {
     int64_t svb, svh, svt;
     int64_t sob, soh, sot;
     float scale;
-    // workspace (per chunk, chunk id = (b * HV + hv) * NC + n):
-    float *ws_w;   // [nchunks][C][K]  W = (I + A_kk)^-1 (b*k*gamma)
-    float *ws_m;   // [nchunks][C][K]  M = A_qk W - scale * (q * gamma)
-    float *ws_u;   // [nchunks][C][V]  U = (I + A_kk)^-1 (w*v)
-    float *ws_p;   // [nchunks][C][V]  P = A_qk U
-    float *ws_kdt; // [nchunks][K][C]  (k * exp(G_last - G))^T
-    float *ws_gam; // [nchunks][K]     exp(G_last)
+    // workspace, per chunk (chunk id = (b * HV + hv) * NC + n), in MFMA
+    // fragment order: 16x16 tiles of 64 lanes x float4 (see chunk.hip)
+    float *ws_w;   // C*K   W = (I + A_kk)^-1 (b*k*gamma), A-operand tiles (row tile, col tile)
+    float *ws_m;   // C*K   M = A_qk W - scale * (q * gamma), same order
+    float *ws_u;   // C*V   U = (I + A_kk)^-1 (w*v), accumulator tiles (col tile, row tile)
+    float *ws_p;   // C*V   P = A_qk U, same order
+    float *ws_kdt; // K*C   (k * exp(G_last - G))^T, A-operand tiles (key tile, time tile)
+    float *ws_gam; // K     exp(G_last)
 };
 
 constexpr int kChunk = 64; // chunk length of the kernels (four 16-row tiles)
