@@ -81,7 +81,21 @@ __device__ __forceinline__ floatx4 mfma4n(float4 a, floatx4 b, floatx4 c) {
 
 // ---------------------------------------------------------------------------
 // chunk-intra: one workgroup (4 waves) per (b, hv, chunk).
+// Every global load of a phase is issued before that phase's arithmetic
+// (g and k at the start, q / b rows before the score tiles, the right-hand
+// sides of row tile p+1 while tile p is solved, k for Kd^T in one batch), so
+// that a workgroup pays a handful of memory round trips instead of one per
+// loop iteration.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ floatx4 ld4v(const float *base, int64_t rs, int row, int valid, int col) {
+    if (row >= valid) return floatx4{0.f, 0.f, 0.f, 0.f};
+    return *reinterpret_cast<const floatx4 *>(base + (int64_t)row * rs + col);
+}
+
+__device__ __forceinline__ floatx4 exp2v(floatx4 x) {
+    return floatx4{fast_exp2(x[0]), fast_exp2(x[1]), fast_exp2(x[2]), fast_exp2(x[3])};
+}
+
 template <int K, int V>
 __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
     constexpr int KP = K + 4, CP = C + 4;
@@ -89,13 +103,18 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
     static_assert(NTOT % 4 == 0, "K + V must be a multiple of 64");
     constexpr int NSEG = 256 / K, RPS = C / NSEG;
     static_assert(256 % K == 0 && C % NSEG == 0, "K");
+    constexpr int KF4 = C * K / 4 / 256; // float4 of the chunk's k per lane
+    constexpr int RSZ = (C * KP > 2 * C * CP) ? C * KP : 2 * C * CP;
 
     __shared__ __attribute__((aligned(16))) float sG[C][KP];
-    __shared__ __attribute__((aligned(16))) float sAqk[C][CP];
-    __shared__ __attribute__((aligned(16))) float sAkk[C][CP];
+    // k (phases 1-2), then A_qk | A_kk (phases 2-4)
+    __shared__ __attribute__((aligned(16))) float sR[RSZ];
     __shared__ __attribute__((aligned(16))) float sAinv[NT][16][20];
     __shared__ float sTot[NSEG][K];
     __shared__ uint32_t sMask[NT][K / 32];
+    float(*sK)[KP] = reinterpret_cast<float(*)[KP]>(sR);
+    float(*sAqk)[CP] = reinterpret_cast<float(*)[CP]>(sR);
+    float(*sAkk)[CP] = reinterpret_cast<float(*)[CP]>(sR + C * CP);
 
     const int ci = blockIdx.x;
     const int bh = ci / p.NC, n = ci % p.NC;
@@ -111,9 +130,15 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
     const float *qc = p.q + kofs, *kc = p.k + kofs, *gc = p.g + kofs, *bc = p.b + kofs;
     const float *vc = p.v + vofs, *wc = p.w + vofs;
 
-    // 1. G = cumsum_t g per channel, stored in log2 units; rows past the end
-    //    of a ragged last chunk have g = 0 (zero padding, src/forward.rs:94-99).
+    // 1. k -> sK; G = cumsum_t g per channel -> sG in log2 units.  Rows past
+    //    the end of a ragged last chunk are zero (src/forward.rs:94-99).
     {
+        floatx4 kreg[KF4];
+#pragma unroll
+        for (int i = 0; i < KF4; ++i) {
+            const int f = i * 256 + tid, row = f / (K / 4), c4 = f % (K / 4);
+            kreg[i] = ld4v(kc, sqt, row, cv, 4 * c4);
+        }
         const int c = tid % K, seg = tid / K;
         float vals[RPS];
         float acc = 0.f;
@@ -126,6 +151,11 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
         }
         sTot[seg][c] = acc;
         if (tid < NT * (K / 32)) (&sMask[0][0])[tid] = 0u;
+#pragma unroll
+        for (int i = 0; i < KF4; ++i) {
+            const int f = i * 256 + tid, row = f / (K / 4), c4 = f % (K / 4);
+            *reinterpret_cast<floatx4 *>(&sK[row][4 * c4]) = kreg[i];
+        }
         __syncthreads();
         float off = 0.f;
         for (int s2 = 0; s2 < seg; ++s2) off += sTot[s2][c];
@@ -140,56 +170,50 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
     }
     __syncthreads();
 
-    // 2. A_qk (waves 0, 1) and A_kk (waves 2, 3); each wave takes two row
-    //    tiles {i, NT-1-i} so that all waves do the same number of blocks.
+    // 2. A_qk (waves 0, 1) and A_kk (waves 2, 3); each wave takes the two
+    //    row tiles {h, NT-1-h} so that all waves do the same number of blocks.
     {
         const int mat = wave >> 1, half = wave & 1;
+        floatx4 araw[2][NKT];
+#pragma unroll
+        for (int pi = 0; pi < 2; ++pi) {
+            const int row = 16 * (pi ? (NT - 1 - half) : half) + lr;
+#pragma unroll
+            for (int m = 0; m < NKT; ++m) araw[pi][m] = ld4v(mat == 0 ? qc : bc, sqt, row, cv, 16 * m + 4 * lg);
+        }
+        floatx4 acc[2][NT];
 #pragma unroll
         for (int pi = 0; pi < 2; ++pi) {
             const int pt = pi ? (NT - 1 - half) : half;
-            floatx4 acc[NT];
-#pragma unroll
-            for (int q = 0; q < NT; ++q) acc[q] = floatx4{0.f, 0.f, 0.f, 0.f};
             const int row = 16 * pt + lr;
-#pragma unroll 2
+#pragma unroll
+            for (int q = 0; q < NT; ++q) acc[pi][q] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
             for (int m = 0; m < NKT; ++m) {
                 const int c0 = 16 * m + 4 * lg;
-                const float4 gr = *reinterpret_cast<const float4 *>(&sG[row][c0]);
-                float4 gb = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (pt > 0) gb = *reinterpret_cast<const float4 *>(&sG[16 * pt - 1][c0]);
-                float4 a;
-                if (mat == 0) {
-                    a = ld4(qc, sqt, row, cv, c0);
-                } else {
-                    const float4 bb = ld4(bc, sqt, row, cv, c0), kk = ld4(kc, sqt, row, cv, c0);
-                    a = make_float4(bb.x * kk.x, bb.y * kk.y, bb.z * kk.z, bb.w * kk.w);
-                }
-                a.x *= fast_exp2(gr.x - gb.x);
-                a.y *= fast_exp2(gr.y - gb.y);
-                a.z *= fast_exp2(gr.z - gb.z);
-                a.w *= fast_exp2(gr.w - gb.w);
+                const floatx4 gr = *reinterpret_cast<const floatx4 *>(&sG[row][c0]);
+                floatx4 gb = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (pt > 0) gb = *reinterpret_cast<const floatx4 *>(&sG[16 * pt - 1][c0]);
+                floatx4 a = araw[pi][m];
+                if (mat == 1) a *= *reinterpret_cast<const floatx4 *>(&sK[row][c0]);
+                a *= exp2v(gr - gb);
                 const uint32_t mw = sMask[pt][c0 >> 5] >> (c0 & 31);
 #pragma unroll
                 for (int q = 0; q < NT; ++q) {
                     if (q <= pt) {
                         const int srow = 16 * q + lr;
-                        const float4 gs = *reinterpret_cast<const float4 *>(&sG[srow][c0]);
-                        const float4 kv = ld4(kc, sqt, srow, cv, c0);
-                        float4 bv;
-                        bv.x = kv.x * fast_exp2(gb.x - gs.x);
-                        bv.y = kv.y * fast_exp2(gb.y - gs.y);
-                        bv.z = kv.z * fast_exp2(gb.z - gs.z);
-                        bv.w = kv.w * fast_exp2(gb.w - gs.w);
+                        const floatx4 gs = *reinterpret_cast<const floatx4 *>(&sG[srow][c0]);
+                        floatx4 bv = *reinterpret_cast<const floatx4 *>(&sK[srow][c0]) * exp2v(gb - gs);
                         if (q == pt) {
-                            if (mw & 1u) bv.x = 0.f;
-                            if (mw & 2u) bv.y = 0.f;
-                            if (mw & 4u) bv.z = 0.f;
-                            if (mw & 8u) bv.w = 0.f;
+                            if (mw & 1u) bv[0] = 0.f;
+                            if (mw & 2u) bv[1] = 0.f;
+                            if (mw & 4u) bv[2] = 0.f;
+                            if (mw & 8u) bv[3] = 0.f;
                         }
-                        acc[q] = mfma16(a.x, bv.x, acc[q]);
-                        acc[q] = mfma16(a.y, bv.y, acc[q]);
-                        acc[q] = mfma16(a.z, bv.z, acc[q]);
-                        acc[q] = mfma16(a.w, bv.w, acc[q]);
+                        acc[pi][q] = mfma16(a[0], bv[0], acc[pi][q]);
+                        acc[pi][q] = mfma16(a[1], bv[1], acc[pi][q]);
+                        acc[pi][q] = mfma16(a[2], bv[2], acc[pi][q]);
+                        acc[pi][q] = mfma16(a[3], bv[3], acc[pi][q]);
                     }
                 }
             }
@@ -203,30 +227,34 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
                             const int c = wd * 32 + __builtin_ctz(mw);
                             mw &= mw - 1u;
                             const int srow = 16 * pt + lr;
-                            const float ks = ld1(kc, sqt, srow, cv, c);
+                            const float ks = sK[srow][c];
                             const float gs = sG[srow][c];
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
                                 const int r = 4 * lg + i;
                                 if (mat == 0 ? (r >= lr) : (r > lr)) {
                                     const int rrow = 16 * pt + r;
-                                    const float xr = (mat == 0)
-                                                         ? ld1(qc, sqt, rrow, cv, c)
-                                                         : ld1(bc, sqt, rrow, cv, c) * ld1(kc, sqt, rrow, cv, c);
-                                    acc[q][i] += xr * ks * fast_exp2(sG[rrow][c] - gs);
+                                    const float xr = (mat == 0) ? ld1(qc, sqt, rrow, cv, c)
+                                                                : ld1(bc, sqt, rrow, cv, c) * sK[rrow][c];
+                                    acc[pi][q][i] += xr * ks * fast_exp2(sG[rrow][c] - gs);
                                 }
                             }
                         }
                     }
                 }
             }
+        }
+        __syncthreads(); // every wave is done with sK: the region becomes A_qk | A_kk
+#pragma unroll
+        for (int pi = 0; pi < 2; ++pi) {
+            const int pt = pi ? (NT - 1 - half) : half;
 #pragma unroll
             for (int q = 0; q < NT; ++q) {
                 if (q <= pt) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int r = 4 * lg + i;
-                        float val = acc[q][i];
+                        float val = acc[pi][q][i];
                         if (mat == 0) {
                             val *= p.scale;
                             if (q == pt && r < lr) val = 0.f;
@@ -265,70 +293,93 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
     //    every load in chunk-inter is a contiguous 16-byte access per lane:
     //      W, M : A-operand fragments (lane (g, r) holds rows r, cols 4g..4g+3)
     //      U, P : accumulator fragments (lane (g, c) holds rows 4g..4g+3, col c)
+    //    The raw right-hand sides of row tile p+1 are loaded while tile p is
+    //    being solved.
     const size_t cid = (size_t)ci;
-    float4 *Wf = reinterpret_cast<float4 *>(p.ws_w) + cid * (C * K / 4);
-    float4 *Mf = reinterpret_cast<float4 *>(p.ws_m) + cid * (C * K / 4);
-    float4 *Uf = reinterpret_cast<float4 *>(p.ws_u) + cid * (C * V / 4);
-    float4 *Pf = reinterpret_cast<float4 *>(p.ws_p) + cid * (C * V / 4);
+    floatx4 *Wf = reinterpret_cast<floatx4 *>(p.ws_w) + cid * (C * K / 4);
+    floatx4 *Mf = reinterpret_cast<floatx4 *>(p.ws_m) + cid * (C * K / 4);
+    floatx4 *Uf = reinterpret_cast<floatx4 *>(p.ws_u) + cid * (C * V / 4);
+    floatx4 *Pf = reinterpret_cast<floatx4 *>(p.ws_p) + cid * (C * V / 4);
     floatx4 X[NTW][NT];
+    floatx4 r1[2][NTW], r2[2][NTW], qv[2][NTW];
 #pragma unroll
-    for (int pt = 0; pt < NT; ++pt) {
+    for (int pt = 0; pt <= NT; ++pt) {
+        if (pt < NT) { // issue the loads of row tile pt (consumed at iteration pt + 1)
+            const int sl = pt & 1;
+#pragma unroll
+            for (int u = 0; u < NTW; ++u) {
+                const int nt = wave + 4 * u;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * pt + 4 * lg + i;
+                    if (nt < NKT) {
+                        const int c = 16 * nt + lr;
+                        r1[sl][u][i] = ld1(bc, sqt, t, cv, c);
+                        r2[sl][u][i] = ld1(kc, sqt, t, cv, c);
+                        qv[sl][u][i] = ld1(qc, sqt, t, cv, c);
+                    } else {
+                        const int c = 16 * (nt - NKT) + lr;
+                        r1[sl][u][i] = ld1(wc, svt, t, cv, c);
+                        r2[sl][u][i] = ld1(vc, svt, t, cv, c);
+                        qv[sl][u][i] = 0.f;
+                    }
+                }
+            }
+        }
+        if (pt == 0) continue;
+        const int tp = pt - 1, sl = tp & 1; // the row tile solved in this iteration
 #pragma unroll
         for (int u = 0; u < NTW; ++u) {
             const int nt = wave + 4 * u;
             const bool kcol = nt < NKT;
-            floatx4 R;
+            floatx4 R = r1[sl][u] * r2[sl][u];
+            floatx4 eg = floatx4{1.f, 1.f, 1.f, 1.f};
+            if (kcol) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * pt + 4 * lg + i;
-                if (kcol) {
-                    const int c = 16 * nt + lr;
-                    R[i] = ld1(bc, sqt, t, cv, c) * ld1(kc, sqt, t, cv, c) * fast_exp2(sG[t][c]);
-                } else {
-                    const int c = 16 * (nt - NKT) + lr;
-                    R[i] = ld1(wc, svt, t, cv, c) * ld1(vc, svt, t, cv, c);
-                }
+                for (int i = 0; i < 4; ++i) eg[i] = fast_exp2(sG[16 * tp + 4 * lg + i][16 * nt + lr]);
+                R *= eg;
             }
 #pragma unroll
             for (int q = 0; q < NT; ++q)
-                if (q < pt)
-                    R = mfma4n(*reinterpret_cast<const float4 *>(&sAkk[16 * pt + lr][16 * q + 4 * lg]), X[u][q], R);
-            floatx4 Xp = mfma4(*reinterpret_cast<const float4 *>(&sAinv[pt][lr][4 * lg]), R,
+                if (q < tp) R = mfma4n(*reinterpret_cast<const float4 *>(&sAkk[16 * tp + lr][16 * q + 4 * lg]), X[u][q], R);
+            floatx4 Xp = mfma4(*reinterpret_cast<const float4 *>(&sAinv[tp][lr][4 * lg]), R,
                                floatx4{0.f, 0.f, 0.f, 0.f});
-            X[u][pt] = Xp;
+            X[u][tp] = Xp;
             floatx4 Y = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int q = 0; q < NT; ++q)
-                if (q <= pt) Y = mfma4(*reinterpret_cast<const float4 *>(&sAqk[16 * pt + lr][16 * q + 4 * lg]), X[u][q], Y);
+                if (q <= tp) Y = mfma4(*reinterpret_cast<const float4 *>(&sAqk[16 * tp + lr][16 * q + 4 * lg]), X[u][q], Y);
             if (kcol) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int t = 16 * pt + 4 * lg + i, c = 16 * nt + lr;
-                    Y[i] -= p.scale * ld1(qc, sqt, t, cv, c) * fast_exp2(sG[t][c]);
-                }
-                const floatx4 Wt = transpose16(Xp, lr, lg), Mt = transpose16(Y, lr, lg);
-                const int f = pt * NKT + nt;
-                Wf[f * 64 + lane] = make_float4(Wt[0], Wt[1], Wt[2], Wt[3]);
-                Mf[f * 64 + lane] = make_float4(Mt[0], Mt[1], Mt[2], Mt[3]);
+                Y -= p.scale * qv[sl][u] * eg;
+                const int f = tp * NKT + nt;
+                Wf[f * 64 + lane] = transpose16(Xp, lr, lg);
+                Mf[f * 64 + lane] = transpose16(Y, lr, lg);
             } else {
-                const int f = (nt - NKT) * NT + pt;
-                Uf[f * 64 + lane] = make_float4(Xp[0], Xp[1], Xp[2], Xp[3]);
-                Pf[f * 64 + lane] = make_float4(Y[0], Y[1], Y[2], Y[3]);
+                const int f = (nt - NKT) * NT + tp;
+                Uf[f * 64 + lane] = Xp;
+                Pf[f * 64 + lane] = Y;
             }
         }
     }
 
     // 5. Kd^T = (k exp(G_last - G))^T as A-operand fragments (kb, tt): lane
     //    (g, r) holds Kd[16 tt + 4 g + j][16 kb + r], and exp(G_last).
-    float4 *Kf = reinterpret_cast<float4 *>(p.ws_kdt) + cid * (C * K / 4);
-    for (int f = wave; f < NKT * NT; f += 4) {
-        const int kb = f / NT, tt = f % NT, ch = 16 * kb + lr;
+    floatx4 *Kf = reinterpret_cast<floatx4 *>(p.ws_kdt) + cid * (C * K / 4);
+    constexpr int KDF = NKT * NT / 4; // fragments per wave
+    floatx4 kk[KDF];
+#pragma unroll
+    for (int j = 0; j < KDF; ++j) {
+        const int f = wave + 4 * j, kb = f / NT, tt = f % NT, ch = 16 * kb + lr;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kk[j][i] = ld1(kc, sqt, 16 * tt + 4 * lg + i, cv, ch);
+    }
+#pragma unroll
+    for (int j = 0; j < KDF; ++j) {
+        const int f = wave + 4 * j, kb = f / NT, tt = f % NT, ch = 16 * kb + lr;
         const float gl = sG[C - 1][ch];
-        float4 val;
-        val.x = ld1(kc, sqt, 16 * tt + 4 * lg + 0, cv, ch) * fast_exp2(gl - sG[16 * tt + 4 * lg + 0][ch]);
-        val.y = ld1(kc, sqt, 16 * tt + 4 * lg + 1, cv, ch) * fast_exp2(gl - sG[16 * tt + 4 * lg + 1][ch]);
-        val.z = ld1(kc, sqt, 16 * tt + 4 * lg + 2, cv, ch) * fast_exp2(gl - sG[16 * tt + 4 * lg + 2][ch]);
-        val.w = ld1(kc, sqt, 16 * tt + 4 * lg + 3, cv, ch) * fast_exp2(gl - sG[16 * tt + 4 * lg + 3][ch]);
+        floatx4 val;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) val[i] = kk[j][i] * fast_exp2(gl - sG[16 * tt + 4 * lg + i][ch]);
         Kf[f * 64 + lane] = val;
     }
     if (tid < K) p.ws_gam[cid * K + tid] = fast_exp2(sG[C - 1][tid]);
