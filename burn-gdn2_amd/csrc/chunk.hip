@@ -41,13 +41,15 @@ constexpr int NT = C / 16;
 static_assert(NT == 4, "the diagonal-block inverse maps 4 tiles x 16 columns onto one wave");
 constexpr float kSafeSpan = 96.0f; // log2 units
 
-__device__ __forceinline__ float4 ld4(const float *base, int64_t rs, int row, int valid, int col) {
-    if (row >= valid) return make_float4(0.f, 0.f, 0.f, 0.f);
-    return *reinterpret_cast<const float4 *>(base + (int64_t)row * rs + col);
-}
-
+// Row loads of a chunk whose rows >= valid are zero padding.  The address is
+// clamped to a valid row (the data there is finite) and the value multiplied
+// by a 0/1 mask: a branch around the load would make the compiler wait for
+// every outstanding load at the join, serialising a phase's loads.
+// valid >= 1 always.
 __device__ __forceinline__ float ld1(const float *base, int64_t rs, int row, int valid, int col) {
-    return row < valid ? base[(int64_t)row * rs + col] : 0.f;
+    const int r = row < valid ? row : valid - 1;
+    const float x = base[(int64_t)r * rs + col];
+    return x * (row < valid ? 1.f : 0.f); // a product, so the load cannot be sunk into a branch
 }
 
 __device__ __forceinline__ floatx4 mfma4(float4 a, floatx4 b, floatx4 c) {
@@ -88,8 +90,9 @@ __device__ __forceinline__ floatx4 mfma4n(float4 a, floatx4 b, floatx4 c) {
 // loop iteration.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ floatx4 ld4v(const float *base, int64_t rs, int row, int valid, int col) {
-    if (row >= valid) return floatx4{0.f, 0.f, 0.f, 0.f};
-    return *reinterpret_cast<const floatx4 *>(base + (int64_t)row * rs + col);
+    const int r = row < valid ? row : valid - 1;
+    const floatx4 x = *reinterpret_cast<const floatx4 *>(base + (int64_t)r * rs + col);
+    return x * (row < valid ? 1.f : 0.f);
 }
 
 __device__ __forceinline__ floatx4 exp2v(floatx4 x) {
@@ -121,7 +124,8 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
     const int bi = bh / p.HV, hv = bh % p.HV, hk = hv / p.rep;
     const int t0 = n * C;
     const int cv = min(C, p.T - t0);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (scalar)
     const int lr = lane & 15, lg = lane >> 4;
     const int64_t sqt = p.sqt, svt = p.svt;
 
@@ -186,16 +190,17 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
         for (int pi = 0; pi < 2; ++pi) {
             const int pt = pi ? (NT - 1 - half) : half;
             const int row = 16 * pt + lr;
+            const int brow = pt > 0 ? 16 * pt - 1 : 0;    // G at the end of tile pt-1
+            const float bmul = pt > 0 ? 1.f : 0.f;         // (Gb = 0 for the first tile)
 #pragma unroll
             for (int q = 0; q < NT; ++q) acc[pi][q] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int m = 0; m < NKT; ++m) {
                 const int c0 = 16 * m + 4 * lg;
                 const floatx4 gr = *reinterpret_cast<const floatx4 *>(&sG[row][c0]);
-                floatx4 gb = floatx4{0.f, 0.f, 0.f, 0.f};
-                if (pt > 0) gb = *reinterpret_cast<const floatx4 *>(&sG[16 * pt - 1][c0]);
-                floatx4 a = araw[pi][m];
-                if (mat == 1) a *= *reinterpret_cast<const floatx4 *>(&sK[row][c0]);
+                const floatx4 gb = *reinterpret_cast<const floatx4 *>(&sG[brow][c0]) * bmul;
+                const floatx4 kr = *reinterpret_cast<const floatx4 *>(&sK[row][c0]);
+                floatx4 a = araw[pi][m] * (mat == 1 ? kr : floatx4{1.f, 1.f, 1.f, 1.f});
                 a *= exp2v(gr - gb);
                 const uint32_t mw = sMask[pt][c0 >> 5] >> (c0 & 31);
 #pragma unroll
@@ -204,12 +209,11 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
                         const int srow = 16 * q + lr;
                         const floatx4 gs = *reinterpret_cast<const floatx4 *>(&sG[srow][c0]);
                         floatx4 bv = *reinterpret_cast<const floatx4 *>(&sK[srow][c0]) * exp2v(gb - gs);
-                        if (q == pt) {
-                            if (mw & 1u) bv[0] = 0.f;
-                            if (mw & 2u) bv[1] = 0.f;
-                            if (mw & 4u) bv[2] = 0.f;
-                            if (mw & 8u) bv[3] = 0.f;
-                        }
+                        const bool diag = q == pt;
+                        bv[0] = (diag && (mw & 1u)) ? 0.f : bv[0];
+                        bv[1] = (diag && (mw & 2u)) ? 0.f : bv[1];
+                        bv[2] = (diag && (mw & 4u)) ? 0.f : bv[2];
+                        bv[3] = (diag && (mw & 8u)) ? 0.f : bv[3];
                         acc[pi][q] = mfma16(a[0], bv[0], acc[pi][q]);
                         acc[pi][q] = mfma16(a[1], bv[1], acc[pi][q]);
                         acc[pi][q] = mfma16(a[2], bv[2], acc[pi][q]);
@@ -217,7 +221,12 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
                     }
                 }
             }
-            // Diagonal block, channels outside the safe span: exact pairwise terms.
+        }
+        // Diagonal blocks, channels outside the safe span: exact pairwise terms
+        // (after both tiles' products, so no row load is outstanding here).
+#pragma unroll
+        for (int pi = 0; pi < 2; ++pi) {
+            const int pt = pi ? (NT - 1 - half) : half;
 #pragma unroll
             for (int q = 0; q < NT; ++q) {
                 if (q == pt) {
@@ -232,12 +241,11 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
                                 const int r = 4 * lg + i;
-                                if (mat == 0 ? (r >= lr) : (r > lr)) {
-                                    const int rrow = 16 * pt + r;
-                                    const float xr = (mat == 0) ? ld1(qc, sqt, rrow, cv, c)
-                                                                : ld1(bc, sqt, rrow, cv, c) * sK[rrow][c];
-                                    acc[pi][q][i] += xr * ks * fast_exp2(sG[rrow][c] - gs);
-                                }
+                                const int rrow = 16 * pt + r;
+                                const float xr = (mat == 0) ? ld1(qc, sqt, rrow, cv, c)
+                                                            : ld1(bc, sqt, rrow, cv, c) * sK[rrow][c];
+                                const float e = (mat == 0 ? (r >= lr) : (r > lr)) ? fast_exp2(sG[rrow][c] - gs) : 0.f;
+                                acc[pi][q][i] += xr * ks * e;
                             }
                         }
                     }
@@ -308,21 +316,19 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
             const int sl = pt & 1;
 #pragma unroll
             for (int u = 0; u < NTW; ++u) {
+                // branch-free operand selection (a branch here would make each
+                // group of loads wait for its own results before the join)
                 const int nt = wave + 4 * u;
+                const bool kcol = nt < NKT;
+                const float *p1 = kcol ? bc : wc, *p2 = kcol ? kc : vc;
+                const int64_t rs = kcol ? sqt : svt;
+                const int c = kcol ? 16 * nt + lr : 16 * (nt - NKT) + lr;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int t = 16 * pt + 4 * lg + i;
-                    if (nt < NKT) {
-                        const int c = 16 * nt + lr;
-                        r1[sl][u][i] = ld1(bc, sqt, t, cv, c);
-                        r2[sl][u][i] = ld1(kc, sqt, t, cv, c);
-                        qv[sl][u][i] = ld1(qc, sqt, t, cv, c);
-                    } else {
-                        const int c = 16 * (nt - NKT) + lr;
-                        r1[sl][u][i] = ld1(wc, svt, t, cv, c);
-                        r2[sl][u][i] = ld1(vc, svt, t, cv, c);
-                        qv[sl][u][i] = 0.f;
-                    }
+                    r1[sl][u][i] = ld1(p1, rs, t, cv, c);
+                    r2[sl][u][i] = ld1(p2, rs, t, cv, c);
+                    qv[sl][u][i] = ld1(qc, sqt, t, cv, kcol ? c : lr); // used by key columns only
                 }
             }
         }
@@ -333,12 +339,11 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
             const int nt = wave + 4 * u;
             const bool kcol = nt < NKT;
             floatx4 R = r1[sl][u] * r2[sl][u];
-            floatx4 eg = floatx4{1.f, 1.f, 1.f, 1.f};
-            if (kcol) {
+            floatx4 eg;
+            const int gcol = kcol ? 16 * nt + lr : 0;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) eg[i] = fast_exp2(sG[16 * tp + 4 * lg + i][16 * nt + lr]);
-                R *= eg;
-            }
+            for (int i = 0; i < 4; ++i) eg[i] = kcol ? fast_exp2(sG[16 * tp + 4 * lg + i][gcol]) : 1.f;
+            R *= eg;
 #pragma unroll
             for (int q = 0; q < NT; ++q)
                 if (q < tp) R = mfma4n(*reinterpret_cast<const float4 *>(&sAkk[16 * tp + lr][16 * q + 4 * lg]), X[u][q], R);
@@ -428,7 +433,8 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
     int bh, vs;
     inter_block(blockIdx.x, p.B * p.HV, nvs, &bh, &vs);
     const int bi = bh / p.HV, hv = bh % p.HV;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (scalar)
     const int lr = lane & 15, lg = lane >> 4;
     const int vt = vs * 4 + wave; // this wave's 16-column tile of V
     const int col = 16 * vt + lr;
