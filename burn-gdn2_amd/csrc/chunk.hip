@@ -95,6 +95,11 @@ __device__ __forceinline__ floatx4 ld4v(const float *base, int64_t rs, int row, 
     return x * (row < valid ? 1.f : 0.f);
 }
 
+// Streaming store: the workspace is read back by chunk-inter much later, so
+// keeping it out of L2 leaves room for the chunk's inputs, which chunk-intra
+// reads more than once.
+__device__ __forceinline__ void st_stream(floatx4 *dst, floatx4 v) { __builtin_nontemporal_store(v, dst); }
+
 __device__ __forceinline__ floatx4 exp2v(floatx4 x) {
     return floatx4{fast_exp2(x[0]), fast_exp2(x[1]), fast_exp2(x[2]), fast_exp2(x[3])};
 }
@@ -357,12 +362,12 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
             if (kcol) {
                 Y -= p.scale * qv[sl][u] * eg;
                 const int f = tp * NKT + nt;
-                Wf[f * 64 + lane] = transpose16(Xp, lr, lg);
-                Mf[f * 64 + lane] = transpose16(Y, lr, lg);
+                st_stream(Wf + f * 64 + lane, transpose16(Xp, lr, lg));
+                st_stream(Mf + f * 64 + lane, transpose16(Y, lr, lg));
             } else {
                 const int f = (nt - NKT) * NT + tp;
-                Uf[f * 64 + lane] = Xp;
-                Pf[f * 64 + lane] = Y;
+                st_stream(Uf + f * 64 + lane, Xp);
+                st_stream(Pf + f * 64 + lane, Y);
             }
         }
     }
@@ -385,7 +390,7 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
         floatx4 val;
 #pragma unroll
         for (int i = 0; i < 4; ++i) val[i] = kk[j][i] * fast_exp2(gl - sG[16 * tt + 4 * lg + i][ch]);
-        Kf[f * 64 + lane] = val;
+        st_stream(Kf + f * 64 + lane, val);
     }
     if (tid < K) p.ws_gam[cid * K + tid] = fast_exp2(sG[C - 1][tid]);
 }
