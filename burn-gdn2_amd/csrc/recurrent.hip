@@ -280,54 +280,120 @@ template <int K, int V>
 __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
     constexpr int TPR = V / 4, RPP = 256 / TPR, NP = K / RPP;
     static_assert(V % 4 == 0 && TPR <= 64 && 64 % TPR == 0, "V");
-    static_assert(K % RPP == 0 && K <= 256, "K");
+    static_assert(K % RPP == 0 && K <= 256 && V <= 256, "K, V");
     const int bh = blockIdx.x;
     const int bi = bh / p.HV, hv = bh % p.HV, hk = hv / p.rep;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cg = tid % TPR, r0 = tid / TPR;
+    const int kd = p.H * K, vd = p.HV * V;
+    const bool sc = p.use_short_conv != 0;
 
-    __shared__ float s_q[K], s_k[K], s_g[K], s_b[K];
-    __shared__ float s_eg[K], s_a1[K], s_a2[K];
+    __shared__ float s_q[K], s_k[K], s_eg[K], s_a1[K], s_a2[K];
     __shared__ float s_red[2][4][V];
     __shared__ float s_vn[V];
     __shared__ float red[3][4];
 
-    float4 S[NP];
-    const size_t sbase = (size_t)bh * K * V + cg * 4;
-#pragma unroll
-    for (int i = 0; i < NP; ++i) S[i] = *reinterpret_cast<const float4 *>(p.state + sbase + (size_t)(r0 + i * RPP) * V);
+    // Prologue operands first: the memory counter is in order, so anything
+    // loaded after the state would wait for the whole 16-row state slice.
+    // Every load is unconditional from a valid address (missing optional
+    // operands point at an input that is read anyway) and selected after.
+    const int r = tid % K;               // key channel (lanes >= K duplicate)
+    const int c = hk * K + r;
+    const int64_t xo = (int64_t)bi * kd + c;
+    const float qr = p.q_raw[xo], kr = p.k_raw[xo], fr = p.f_raw[xo], brw = p.b_raw[xo];
+    const float dtb = p.dt_bias[c], alog = p.a_log[hk];
+    const float dfv = (p.decay_factors ? p.decay_factors : p.dt_bias)[c];
+    const int64_t kcb = (int64_t)bi * 3 * kd + c;
+    const float *cqi = (sc && p.conv_q_in) ? p.conv_q_in + kcb : p.q_raw + xo;
+    const float *cki = (sc && p.conv_k_in) ? p.conv_k_in + kcb : p.k_raw + xo;
+    const int64_t cst = (sc && p.conv_q_in) ? kd : 0;
+    const float q0 = cqi[0], q1 = cqi[cst], q2 = cqi[2 * cst];
+    const float k0 = cki[0], k1 = cki[cst], k2 = cki[2 * cst];
+    const float *wq = sc ? p.q_conv_w + 4 * c : p.q_raw + xo;
+    const float *wk = sc ? p.k_conv_w + 4 * c : p.k_raw + xo;
+    const int wst = sc ? 1 : 0;
+    const float wq0 = wq[0], wq1 = wq[wst], wq2 = wq[2 * wst], wq3 = wq[3 * wst];
+    const float wk0 = wk[0], wk1 = wk[wst], wk2 = wk[2 * wst], wk3 = wk[3 * wst];
 
-    // prologue
-    float sq = 0.f, sk = 0.f;
-    const bool key_writer = (hv % p.rep) == 0;
-    if (tid < K) key_prologue(p, bi, hk, tid, key_writer, s_q, s_k, s_g, s_b, &sq, &sk);
-    float vv = 0.f, ww = 0.f;
-    if (tid < V) value_prologue(p, bi, hv, tid, &vv, &ww);
+    const int col = tid % V;             // value column (lanes >= V duplicate)
+    const int cvc = hv * V + col;
+    const int64_t vo = (int64_t)bi * vd + cvc;
+    const float vr = p.v_raw[vo], wr = p.w_raw[vo], gt = p.gate[vo], onw = p.o_norm_weight[col];
+    const int64_t vcb = (int64_t)bi * 3 * vd + cvc;
+    const float *cvi = (sc && p.conv_v_in) ? p.conv_v_in + vcb : p.v_raw + vo;
+    const int64_t vst = (sc && p.conv_v_in) ? vd : 0;
+    const float v0 = cvi[0], v1 = cvi[vst], v2 = cvi[2 * vst];
+    const float *wv = sc ? p.v_conv_w + 4 * cvc : p.v_raw + vo;
+    const float wv0 = wv[0], wv1 = wv[wst], wv2 = wv[2 * wst], wv3 = wv[3 * wst];
+
+    // The state slice: 16-byte loads, each row read exactly once.
+    float4 S[NP];
+    float *Sg = p.state + (size_t)bh * K * V + cg * 4;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) S[i] = *reinterpret_cast<const float4 *>(Sg + (size_t)(r0 + i * RPP) * V);
+
+    // Key side: conv + SiLU (src/short_conv.rs:22-65), gates
+    // (src/module.rs:417-443), then the L2 norms over K (src/l2norm.rs).
+    float qa = 0.f, ka = 0.f;
+    {
+        float aq = 0.f, ak = 0.f;
+        if (sc) {
+            aq += q0 * wq0; aq += q1 * wq1; aq += q2 * wq2; aq += qr * wq3;
+            ak += k0 * wk0; ak += k1 * wk1; ak += k2 * wk2; ak += kr * wk3;
+        } else {
+            aq = qr;
+            ak = kr;
+        }
+        qa = siluf_(aq);
+        ka = siluf_(ak);
+    }
+    float gv = -expf(alog) * softplusf_(fr + dtb);
+    if (p.decay_factors) gv = logf(sigmoidf_(dfv) * p.one_minus_min_decay * expf(gv) + p.min_decay);
+    float bv = sigmoidf_(brw);
+    if (p.allow_neg_eigval) bv *= 2.0f;
+    const bool klane = tid < K;
+    float sq = klane ? qa * qa : 0.f, sk = klane ? ka * ka : 0.f;
     sq = wave_sum(sq);
     sk = wave_sum(sk);
-    if (lane == 0) { red[0][wave] = sq; red[1][wave] = sk; }
+    if (lane == 0) {
+        red[0][wave] = sq;
+        red[1][wave] = sk;
+    }
     __syncthreads();
     const float qn = 1.0f / sqrtf(red[0][0] + red[0][1] + red[0][2] + red[0][3] + 1e-6f);
     const float kn = 1.0f / sqrtf(red[1][0] + red[1][1] + red[1][2] + red[1][3] + 1e-6f);
     float kq = 0.f;
-    if (tid < K) {
-        const float qq = s_q[tid] * qn, kk = s_k[tid] * kn;
-        const float eg = expf(s_g[tid]);
-        s_eg[tid] = eg;
-        s_a1[tid] = eg * (s_b[tid] * kk);
-        s_a2[tid] = eg * qq;
-        s_k[tid] = kk;
+    if (klane) {
+        const float qq = qa * qn, kk = ka * kn;
+        const float eg = expf(gv);
+        s_eg[r] = eg;
+        s_a1[r] = eg * (bv * kk);
+        s_a2[r] = eg * qq;
+        s_k[r] = kk;
         kq = kk * qq;
     }
     kq = wave_sum(kq);
     if (lane == 0) red[2][wave] = kq;
+    // Value side: conv + SiLU of v, w = sigmoid.
+    float vv;
+    {
+        float av = 0.f;
+        if (sc) {
+            av += v0 * wv0; av += v1 * wv1; av += v2 * wv2; av += vr * wv3;
+        } else {
+            av = vr;
+        }
+        vv = siluf_(av);
+    }
+    const float ww = sigmoidf_(wr);
     __syncthreads();
 
+    // Both K-reductions of the step from one pass over the registers.
     float e1[4] = {0.f, 0.f, 0.f, 0.f}, e2[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-        const int r = r0 + i * RPP;
-        const float a1 = s_a1[r], a2 = s_a2[r];
+        const int rr = r0 + i * RPP;
+        const float a1 = s_a1[rr], a2 = s_a2[rr];
         e1[0] += S[i].x * a1; e1[1] += S[i].y * a1; e1[2] += S[i].z * a1; e1[3] += S[i].w * a1;
         e2[0] += S[i].x * a2; e2[1] += S[i].y * a2; e2[2] += S[i].z * a2; e2[3] += S[i].w * a2;
     }
@@ -345,36 +411,52 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
             s_red[1][wave][cg * 4 + j] = e2[j];
         }
     __syncthreads();
+    const bool vlane = tid < V;
     float o = 0.f;
-    if (tid < V) {
-        const float E1 = s_red[0][0][tid] + s_red[0][1][tid] + s_red[0][2][tid] + s_red[0][3][tid];
-        const float E2 = s_red[1][0][tid] + s_red[1][1][tid] + s_red[1][2][tid] + s_red[1][3][tid];
+    {
+        const float E1 = s_red[0][0][col] + s_red[0][1][col] + s_red[0][2][col] + s_red[0][3][col];
+        const float E2 = s_red[1][0][col] + s_red[1][1][col] + s_red[1][2][col] + s_red[1][3][col];
         const float kqs = red[2][0] + red[2][1] + red[2][2] + red[2][3];
         const float vn = ww * vv - E1;
         o = p.scale * (E2 + vn * kqs);
-        s_vn[tid] = vn;
+        if (vlane) s_vn[col] = vn;
     }
     // gated RMSNorm over the V columns (src/module.rs:501-517)
-    float o2 = wave_sum(o * o);
+    float o2 = wave_sum(vlane ? o * o : 0.f);
     __syncthreads();
     if (lane == 0) red[0][wave] = o2;
     __syncthreads();
-    if (tid < V) {
-        const float ms = (red[0][0] + red[0][1] + red[0][2] + red[0][3]) / (float)V;
-        const float rms = sqrtf(ms + p.norm_eps);
-        const int64_t c = (int64_t)bi * p.HV * V + (int64_t)hv * V + tid;
-        p.out[c] = o / rms * p.o_norm_weight[tid] * siluf_(p.gate[c]);
-    }
-    const float4 vn = *reinterpret_cast<const float4 *>(&s_vn[cg * 4]);
+    const float4 vn4 = *reinterpret_cast<const float4 *>(&s_vn[cg * 4]);
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-        const int r = r0 + i * RPP;
-        const float eg = s_eg[r], kk = s_k[r];
-        S[i].x = S[i].x * eg + kk * vn.x;
-        S[i].y = S[i].y * eg + kk * vn.y;
-        S[i].z = S[i].z * eg + kk * vn.z;
-        S[i].w = S[i].w * eg + kk * vn.w;
-        *reinterpret_cast<float4 *>(p.state + sbase + (size_t)r * V) = S[i];
+        const int rr = r0 + i * RPP;
+        const float eg = s_eg[rr], kk = s_k[rr];
+        S[i].x = S[i].x * eg + kk * vn4.x;
+        S[i].y = S[i].y * eg + kk * vn4.y;
+        S[i].z = S[i].z * eg + kk * vn4.z;
+        S[i].w = S[i].w * eg + kk * vn4.w;
+        *reinterpret_cast<float4 *>(Sg + (size_t)rr * V) = S[i];
+    }
+    if (vlane) {
+        const float ms = (red[0][0] + red[0][1] + red[0][2] + red[0][3]) / (float)V;
+        p.out[vo] = o / sqrtf(ms + p.norm_eps) * onw * siluf_(gt);
+    }
+    // Conv caches: the last three pre-conv rows, oldest first.  Value caches
+    // are owned by this (b, hv); key caches by the first value head of hk.
+    if (sc) {
+        if (vlane) {
+            p.conv_v_out[vcb] = v1;
+            p.conv_v_out[vcb + vd] = v2;
+            p.conv_v_out[vcb + 2 * vd] = vr;
+        }
+        if (klane && (hv % p.rep) == 0) {
+            p.conv_q_out[kcb] = q1;
+            p.conv_q_out[kcb + kd] = q2;
+            p.conv_q_out[kcb + 2 * kd] = qr;
+            p.conv_k_out[kcb] = k1;
+            p.conv_k_out[kcb + kd] = k2;
+            p.conv_k_out[kcb + 2 * kd] = kr;
+        }
     }
 }
 
@@ -469,7 +551,6 @@ hipError_t launch_decode(const DecodeParams &p, hipStream_t s) {
     if (p.K == 128 && p.V == 256) return launch_decode_t<128, 256>(p, s);
     if (p.K == 64 && p.V == 64) return launch_decode_t<64, 64>(p, s);
     if (p.K == 64 && p.V == 128) return launch_decode_t<64, 128>(p, s);
-    if (p.K == 256 && p.V == 256) return launch_decode_t<256, 256>(p, s);
     const size_t lds = sizeof(float) * 7 * (size_t)p.K;
     hipLaunchKernelGGL(decode_fused_generic_kernel, dim3(p.B * p.HV), dim3(256), lds, s, p);
     return hipGetLastError();
