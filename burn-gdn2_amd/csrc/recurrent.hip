@@ -278,8 +278,12 @@ __device__ __forceinline__ void value_prologue(const DecodeParams &p, int bi, in
 
 template <int K, int V>
 __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
-    constexpr int TPR = V / 4, RPP = 256 / TPR, NP = K / RPP;
-    static_assert(V % 4 == 0 && TPR <= 64 && 64 % TPR == 0, "V");
+    // The V columns are processed in NH parts of VP columns: part h's state
+    // is reduced, updated and written back as soon as its own loads have
+    // arrived, while the next part's loads are still in flight.
+    constexpr int NH = V >= 128 ? 2 : 1, VP = V / NH;
+    constexpr int TPR = VP / 4, RPP = 256 / TPR, NP = K / RPP;
+    static_assert(VP % 4 == 0 && TPR <= 64 && 64 % TPR == 0, "V");
     static_assert(K % RPP == 0 && K <= 256 && V <= 256, "K, V");
     const int bh = blockIdx.x;
     const int bi = bh / p.HV, hv = bh % p.HV, hk = hv / p.rep;
@@ -289,9 +293,9 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
     const bool sc = p.use_short_conv != 0;
 
     __shared__ float s_q[K], s_k[K], s_eg[K], s_a1[K], s_a2[K];
-    __shared__ float s_red[2][4][V];
+    __shared__ float s_red[2][4][VP];
     __shared__ float s_vn[V];
-    __shared__ float red[3][4];
+    __shared__ float red[3][4], red_o2[4];
 
     // Prologue operands first: the memory counter is in order, so anything
     // loaded after the state would wait for the whole 16-row state slice.
@@ -326,11 +330,14 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
     const float *wv = sc ? p.v_conv_w + 4 * cvc : p.v_raw + vo;
     const float wv0 = wv[0], wv1 = wv[wst], wv2 = wv[2 * wst], wv3 = wv[3 * wst];
 
-    // The state slice: 16-byte loads, each row read exactly once.
-    float4 S[NP];
+    // The state slice: 16-byte loads, each row read exactly once, part 0 first.
+    floatx4 S[NH][NP];
     float *Sg = p.state + (size_t)bh * K * V + cg * 4;
 #pragma unroll
-    for (int i = 0; i < NP; ++i) S[i] = *reinterpret_cast<const float4 *>(Sg + (size_t)(r0 + i * RPP) * V);
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int i = 0; i < NP; ++i)
+            S[h][i] = *reinterpret_cast<const floatx4 *>(Sg + (size_t)(r0 + i * RPP) * V + h * VP);
 
     // Key side: conv + SiLU (src/short_conv.rs:22-65), gates
     // (src/module.rs:417-443), then the L2 norms over K (src/l2norm.rs).
@@ -388,57 +395,62 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
     const float ww = sigmoidf_(wr);
     __syncthreads();
 
-    // Both K-reductions of the step from one pass over the registers.
-    float e1[4] = {0.f, 0.f, 0.f, 0.f}, e2[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const int rr = r0 + i * RPP;
-        const float a1 = s_a1[rr], a2 = s_a2[rr];
-        e1[0] += S[i].x * a1; e1[1] += S[i].y * a1; e1[2] += S[i].z * a1; e1[3] += S[i].w * a1;
-        e2[0] += S[i].x * a2; e2[1] += S[i].y * a2; e2[2] += S[i].z * a2; e2[3] += S[i].w * a2;
-    }
-#pragma unroll
-    for (int off = TPR; off < 64; off <<= 1)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            e1[j] += __shfl_xor(e1[j], off, 64);
-            e2[j] += __shfl_xor(e2[j], off, 64);
-        }
-    if (lane < TPR)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            s_red[0][wave][cg * 4 + j] = e1[j];
-            s_red[1][wave][cg * 4 + j] = e2[j];
-        }
-    __syncthreads();
+    // Per part: both K-reductions of the step from one pass over the
+    // registers, v_new for the part's columns, then its state update and
+    // write-back.  Lane c < V holds column c's value-side operands.
+    const float kqs = red[2][0] + red[2][1] + red[2][2] + red[2][3];
     const bool vlane = tid < V;
     float o = 0.f;
-    {
-        const float E1 = s_red[0][0][col] + s_red[0][1][col] + s_red[0][2][col] + s_red[0][3][col];
-        const float E2 = s_red[1][0][col] + s_red[1][1][col] + s_red[1][2][col] + s_red[1][3][col];
-        const float kqs = red[2][0] + red[2][1] + red[2][2] + red[2][3];
-        const float vn = ww * vv - E1;
-        o = p.scale * (E2 + vn * kqs);
-        if (vlane) s_vn[col] = vn;
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        float e1[4] = {0.f, 0.f, 0.f, 0.f}, e2[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int rr = r0 + i * RPP;
+            const float a1 = s_a1[rr], a2 = s_a2[rr];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                e1[j] += S[h][i][j] * a1;
+                e2[j] += S[h][i][j] * a2;
+            }
+        }
+#pragma unroll
+        for (int off = TPR; off < 64; off <<= 1)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                e1[j] += __shfl_xor(e1[j], off, 64);
+                e2[j] += __shfl_xor(e2[j], off, 64);
+            }
+        if (lane < TPR)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                s_red[0][wave][cg * 4 + j] = e1[j];
+                s_red[1][wave][cg * 4 + j] = e2[j];
+            }
+        __syncthreads();
+        if (tid >= h * VP && tid < (h + 1) * VP) {
+            const int pc = tid - h * VP;
+            const float E1 = s_red[0][0][pc] + s_red[0][1][pc] + s_red[0][2][pc] + s_red[0][3][pc];
+            const float E2 = s_red[1][0][pc] + s_red[1][1][pc] + s_red[1][2][pc] + s_red[1][3][pc];
+            const float vn = ww * vv - E1;
+            o = p.scale * (E2 + vn * kqs);
+            s_vn[tid] = vn;
+        }
+        __syncthreads();
+        const floatx4 vn4 = *reinterpret_cast<const floatx4 *>(&s_vn[h * VP + cg * 4]);
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int rr = r0 + i * RPP;
+            const float eg = s_eg[rr], kk = s_k[rr];
+            *reinterpret_cast<floatx4 *>(Sg + (size_t)rr * V + h * VP) = S[h][i] * eg + kk * vn4;
+        }
     }
     // gated RMSNorm over the V columns (src/module.rs:501-517)
-    float o2 = wave_sum(vlane ? o * o : 0.f);
+    const float o2 = wave_sum(vlane ? o * o : 0.f);
+    if (lane == 0) red_o2[wave] = o2;
     __syncthreads();
-    if (lane == 0) red[0][wave] = o2;
-    __syncthreads();
-    const float4 vn4 = *reinterpret_cast<const float4 *>(&s_vn[cg * 4]);
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const int rr = r0 + i * RPP;
-        const float eg = s_eg[rr], kk = s_k[rr];
-        S[i].x = S[i].x * eg + kk * vn4.x;
-        S[i].y = S[i].y * eg + kk * vn4.y;
-        S[i].z = S[i].z * eg + kk * vn4.z;
-        S[i].w = S[i].w * eg + kk * vn4.w;
-        *reinterpret_cast<float4 *>(Sg + (size_t)rr * V) = S[i];
-    }
     if (vlane) {
-        const float ms = (red[0][0] + red[0][1] + red[0][2] + red[0][3]) / (float)V;
+        const float ms = (red_o2[0] + red_o2[1] + red_o2[2] + red_o2[3]) / (float)V;
         p.out[vo] = o / sqrtf(ms + p.norm_eps) * onw * siluf_(gt);
     }
     // Conv caches: the last three pre-conv rows, oldest first.  Value caches
