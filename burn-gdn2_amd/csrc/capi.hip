@@ -111,6 +111,9 @@ extern "C" gdn2_status gdn2_decode_fused_f32(const gdn2_decode_args *a, gdn2_str
     p.a_log = P->a_log; p.dt_bias = P->dt_bias; p.decay_factors = P->decay_factors;
     p.o_norm_weight = P->o_norm_weight;
     p.state = a->state; p.out = a->out;
+    const int64_t kd = a->num_heads * a->head_dim, vd = a->num_v_heads * a->head_v_dim;
+    p.ld_q = p.ld_k = p.ld_f = p.ld_b = kd;
+    p.ld_v = p.ld_w = p.ld_gate = p.ld_out = vd;
     p.B = (int)a->batch; p.H = (int)a->num_heads; p.HV = (int)a->num_v_heads;
     p.rep = (int)(a->num_v_heads / a->num_heads); p.K = (int)a->head_dim; p.V = (int)a->head_v_dim;
     p.use_short_conv = P->use_short_conv; p.allow_neg_eigval = P->allow_neg_eigval;

@@ -31,6 +31,8 @@ struct DecodeParams {
     const float *a_log, *dt_bias, *decay_factors, *o_norm_weight;
     float *state; // [B, HV, K, V] in place
     float *out;   // [B, vd]
+    // row strides (elements between batch rows) of the raw inputs and out
+    int64_t ld_q, ld_k, ld_f, ld_b, ld_v, ld_w, ld_gate, ld_out;
     int B, H, HV, rep, K, V;
     int use_short_conv, allow_neg_eigval;
     float min_decay, one_minus_min_decay, norm_eps, scale;
@@ -57,7 +59,42 @@ struct ChunkParams {
     float *ws_gam; // K     exp(G_last)
 };
 
+// Projection epilogue: raw Linear outputs -> kernel inputs, one token per
+// workgroup.  Y rows hold the fused input projection [q | k | b | v | w | ..]
+// at the given column offsets; F = f_proj_1 output.
+struct ProjectParams {
+    const float *Y;
+    int64_t ldY, off_q, off_k, off_b, off_v, off_w;
+    const float *F;
+    int64_t ldF;
+    const float *conv_q_in, *conv_k_in, *conv_v_in; // [B, 3, kd|vd]; null: pad with token 0
+    const float *q_conv_w, *k_conv_w, *v_conv_w;
+    const float *a_log, *dt_bias, *decay_factors; // decay_factors null without min_decay
+    float *q, *k, *g, *b; // [B*T, kd]
+    float *v, *w;         // [B*T, vd]
+    int B, T, H, K, HV, V;
+    int use_short_conv, allow_neg_eigval;
+    float min_decay, one_minus_min_decay;
+};
+
+// New conv caches [B, 3, kd|vd] from the raw projections (and the old caches).
+struct ConvCacheParams {
+    const float *Y;
+    int64_t ldY, off_q, off_k, off_v;
+    const float *in_q, *in_k, *in_v; // null: pad with token 0
+    float *out_q, *out_k, *out_v;
+    int B, T, kd, vd;
+};
+
 constexpr int kChunk = 64; // chunk length of the kernels (four 16-row tiles)
+
+size_t project_lds_bytes(int kd);
+hipError_t launch_project(const ProjectParams &p, hipStream_t s);
+hipError_t launch_conv_cache(const ConvCacheParams &p, hipStream_t s);
+hipError_t launch_rmsnorm_gate(float *out, int64_t ld_out, const float *x, int64_t ld_x, const float *gate,
+                               int64_t ld_gate, const float *weight, int64_t M, int HV, int V, float eps,
+                               hipStream_t s);
+hipError_t launch_fill_rows(float *y, int64_t ld, const float *row, int64_t M, int64_t N, hipStream_t s);
 
 hipError_t launch_scan(const ScanParams &p, hipStream_t s);
 hipError_t launch_decode(const DecodeParams &p, hipStream_t s);

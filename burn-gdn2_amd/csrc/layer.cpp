@@ -1,0 +1,756 @@
+// The GDN-2 layer on the device: Gdn2Config checks, parameter initialisation,
+// GatedDeltaNet2::{project, forward, forward_train} and Gdn2State
+// (src/config.rs, src/module.rs), driving rocBLAS for the Linear layers and
+// the HIP kernels of this library for everything else.
+//
+// Data flow of one call over M = B * T tokens (all buffers row-major):
+//   Y [M, ld_in] = x W_in            W_in = [q | k | b | v | w | f0 | g0] (one GEMM)
+//   F [M, kd]    = Y[:, f0] W_f1     G [M, vd] = bias + Y[:, g0] W_g1
+//   q, k, g, b [M, kd], v, w [M, vd] = project epilogue (conv, SiLU, gates, L2 norm)
+//   O [M, vd]    = recurrence (chunk or per-token scan) in the [B, T, HV, V] layout
+//   O            = rms_norm_gate(O, G)  (in place)
+//   out [M, D]   = O W_o
+// At T = 1 with a state the fused decode kernel replaces the epilogue, the
+// recurrence and the norm.
+#include <rocblas/rocblas.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "common.hpp"
+#include "gdn2_layer.h"
+#include "kernels.hpp"
+
+using namespace gdn2;
+
+namespace {
+
+// Parameter table: the reference's field order (src/module.rs:93-111).
+const char *const kParamNames[] = {
+    "q_proj", "k_proj", "v_proj", "f_proj_0", "f_proj_1", "b_proj", "w_proj", "g_proj_0", "g_proj_1",
+    "g_proj_1_bias", "a_log", "dt_bias", "o_norm_weight", "o_proj", "q_conv_w", "k_conv_w", "v_conv_w",
+    "decay_factors",
+};
+enum ParamId {
+    P_Q, P_K, P_V, P_F0, P_F1, P_B, P_W, P_G0, P_G1, P_G1_BIAS, P_A_LOG, P_DT_BIAS, P_O_NORM, P_O, P_QCONV,
+    P_KCONV, P_VCONV, P_DECAY, P_COUNT
+};
+
+struct Dims {
+    int64_t D, H, K, HV, V, kd, vd;
+};
+
+Dims dims_of(const gdn2_config &c) {
+    Dims d;
+    d.D = c.hidden_size;
+    d.H = c.num_heads;
+    d.K = c.head_dim;
+    d.HV = c.num_v_heads > 0 ? c.num_v_heads : c.num_heads;
+    d.V = (int64_t)((float)c.head_dim * c.expand_v);
+    d.kd = d.H * d.K;
+    d.vd = d.HV * d.V;
+    return d;
+}
+
+int param_id(const char *name) {
+    if (!name) return -1;
+    for (int i = 0; i < P_COUNT; ++i)
+        if (std::strcmp(name, kParamNames[i]) == 0) return i;
+    return -1;
+}
+
+// Shape of a parameter (rows x cols); numel 0 when absent.
+int64_t param_shape(const gdn2_config &c, int id, int64_t *rows, int64_t *cols) {
+    const Dims d = dims_of(c);
+    int64_t r = 0, k = 1;
+    switch (id) {
+        case P_Q: case P_K: case P_B: r = d.D; k = d.kd; break;
+        case P_V: case P_W: r = d.D; k = d.vd; break;
+        case P_F0: case P_G0: r = d.D; k = d.V; break;
+        case P_F1: r = d.V; k = d.kd; break;
+        case P_G1: r = d.V; k = d.vd; break;
+        case P_G1_BIAS: r = d.vd; break;
+        case P_A_LOG: r = d.H; break;
+        case P_DT_BIAS: r = d.kd; break;
+        case P_O_NORM: r = d.V; break;
+        case P_O: r = d.vd; k = d.D; break;
+        case P_QCONV: case P_KCONV: r = d.kd; k = 4; break;
+        case P_VCONV: r = d.vd; k = 4; break;
+        case P_DECAY:
+            if (c.has_min_decay) { r = d.H; k = d.K; } else { r = 0; k = 0; }
+            break;
+        default: return -1;
+    }
+    if (rows) *rows = r;
+    if (cols) *cols = k;
+    return r * k;
+}
+
+// SplitMix64 (Steele, Lea, Flood, "Fast splittable pseudorandom number
+// generators", OOPSLA 2014).  Each (seed, parameter) pair gets its own
+// mixed 64-bit key so that the streams of two parameters are not shifts of
+// one another; element i is the (i + 1)-th output of the key's stream.
+uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+double uniform01(uint64_t seed, int id, uint64_t i) {
+    const uint64_t key = mix64(seed ^ mix64(0xD1B54A32D192ED03ull * (uint64_t)(id + 1)));
+    const uint64_t z = mix64(key + 0x9E3779B97F4A7C15ull * (i + 1));
+    return (double)(z >> 11) * (1.0 / 9007199254740992.0);
+}
+
+void init_param(const gdn2_config &c, uint64_t seed, int id, float *out) {
+    int64_t rows = 0, cols = 0;
+    const int64_t n = param_shape(c, id, &rows, &cols);
+    auto U = [&](int64_t i, double lo, double hi) { return lo + (hi - lo) * uniform01(seed, id, (uint64_t)i); };
+    switch (id) {
+        case P_Q: case P_K: case P_V: case P_F0: case P_F1: case P_B: case P_W: case P_G0: case P_G1: case P_O: {
+            // Xavier uniform, gain 2^-2.5, fan_in = rows, fan_out = cols (src/module.rs:121-129)
+            const double bound = std::pow(2.0, -2.5) * std::sqrt(6.0 / (double)(rows + cols));
+            for (int64_t i = 0; i < n; ++i) out[i] = (float)U(i, -bound, bound);
+            break;
+        }
+        case P_G1_BIAS:  // zero bias (src/module.rs:130-138)
+            for (int64_t i = 0; i < n; ++i) out[i] = 0.0f;
+            break;
+        case P_A_LOG:  // U(ln 1, ln 16) (src/module.rs:151-155)
+            for (int64_t i = 0; i < n; ++i) out[i] = (float)U(i, std::log(1.0), std::log(16.0));
+            break;
+        case P_DT_BIAS:  // inverse softplus of dt (src/module.rs:157-166)
+            for (int64_t i = 0; i < n; ++i) {
+                const double dt = std::fmax(std::exp(U(i, std::log(0.001), std::log(0.1))), 1e-4);
+                out[i] = (float)(dt + std::log(-std::expm1(-dt)));
+            }
+            break;
+        case P_O_NORM:
+            for (int64_t i = 0; i < n; ++i) out[i] = 1.0f;
+            break;
+        case P_QCONV: case P_KCONV: case P_VCONV:  // U(-1/2, 1/2) (src/module.rs:142-149)
+            for (int64_t i = 0; i < n; ++i) out[i] = (float)U(i, -0.5, 0.5);
+            break;
+        case P_DECAY:  // 2.0 iff min_decay (src/module.rs:185-187)
+            for (int64_t i = 0; i < n; ++i) out[i] = 2.0f;
+            break;
+        default: break;
+    }
+}
+
+std::string fmt_f(double v) {
+    char buf[64];
+    std::snprintf(buf, sizeof buf, "%g", v);
+    return buf;
+}
+
+constexpr int kShortConvCache = 3;  // SHORT_CONV_CACHE (src/short_conv.rs:7)
+constexpr int64_t kFusedRecurrentMaxSeq = 64;  // FUSED_RECURRENT_MAX_SEQ (src/module.rs:16)
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+}  // namespace
+
+struct gdn2_layer {
+    gdn2_config cfg;
+    Dims d;
+    int device = 0;
+    rocblas_handle blas = nullptr;
+    // The input-side Linear weights share one [D, ld_in] matrix so that x is
+    // read by a single GEMM; column offsets of each block:
+    int64_t ld_in = 0, off_q = 0, off_k = 0, off_b = 0, off_v = 0, off_w = 0, off_f0 = 0, off_g0 = 0;
+    float *w_in = nullptr;
+    float *p[P_COUNT] = {};  // standalone parameters (null for those inside w_in)
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+
+    int64_t col_offset(int id) const {
+        switch (id) {
+            case P_Q: return off_q;
+            case P_K: return off_k;
+            case P_B: return off_b;
+            case P_V: return off_v;
+            case P_W: return off_w;
+            case P_F0: return off_f0;
+            case P_G0: return off_g0;
+            default: return -1;
+        }
+    }
+};
+
+struct gdn2_state {
+    const gdn2_layer *layer = nullptr;
+    int64_t batch = 0;
+    bool some = false;
+    float *S = nullptr;
+    float *conv[2][3] = {};  // ping-pong buffers of the q, k, v caches
+    int cur = 0;
+};
+
+namespace {
+
+// Y[M, N] = X[M, Kd] W[Kd, N] (+ beta Y), row-major, through column-major rocBLAS.
+gdn2_status gemm(rocblas_handle h, int64_t M, int64_t N, int64_t Kd, const float *X, int64_t ldx, const float *W,
+                 int64_t ldw, float *Y, int64_t ldy, float beta) {
+    if (M == 0 || N == 0) return GDN2_OK;
+    const float alpha = 1.0f;
+    const rocblas_status st = rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_none, (rocblas_int)N,
+                                            (rocblas_int)M, (rocblas_int)Kd, &alpha, W, (rocblas_int)ldw, X,
+                                            (rocblas_int)ldx, &beta, Y, (rocblas_int)ldy);
+    if (st != rocblas_status_success)
+        return fail(GDN2_EHIP, std::string("rocblas_sgemm: ") + rocblas_status_to_string(st));
+    return GDN2_OK;
+}
+
+struct Work {
+    float *Y, *F, *G, *q, *k, *g, *b, *v, *w, *O, *S0;
+    void *chunk;
+    size_t chunk_bytes;
+};
+
+gdn2_chunk_args chunk_args_for(const gdn2_layer &L, int64_t B, int64_t T, const Work &wk, float *S) {
+    const Dims &d = L.d;
+    gdn2_chunk_args a{};
+    a.q = wk.q; a.k = wk.k; a.g = wk.g; a.b = wk.b; a.v = wk.v; a.w = wk.w;
+    a.state = S; a.out = wk.O;
+    a.batch = B; a.num_heads = d.H; a.num_v_heads = d.HV; a.seq_len = T; a.head_dim = d.K; a.head_v_dim = d.V;
+    a.stride_qk_b = T * d.kd; a.stride_qk_h = d.K; a.stride_qk_t = d.kd;
+    a.stride_vw_b = T * d.vd; a.stride_vw_h = d.V; a.stride_vw_t = d.vd;
+    a.stride_o_b = T * d.vd; a.stride_o_h = d.V; a.stride_o_t = d.vd;
+    a.scale = std::pow((double)d.K, -0.5);
+    a.chunk_size = L.cfg.chunk_size;
+    return a;
+}
+
+// Carve the workspace for M = B * T tokens, growing it when needed.
+gdn2_status workspace(gdn2_layer &L, int64_t B, int64_t T, bool need_s0, Work *wk) {
+    const Dims &d = L.d;
+    const int64_t M = B * T;
+    Work tmp{};
+    gdn2_chunk_args ca = chunk_args_for(L, B, T, tmp, nullptr);
+    const size_t chunk_bytes = gdn2_chunk_workspace_bytes(&ca);
+    const size_t f = sizeof(float);
+    size_t sz[11] = {f * M * L.ld_in, f * M * d.kd, f * M * d.vd, f * M * d.kd, f * M * d.kd, f * M * d.kd,
+                     f * M * d.kd, f * M * d.vd, f * M * d.vd, f * M * d.vd,
+                     need_s0 ? f * B * d.HV * d.K * d.V : 0};
+    size_t total = 0;
+    for (size_t s : sz) total += align256(s);
+    total += align256(chunk_bytes);
+    if (total > L.ws_bytes) {
+        if (L.ws) {
+            GDN2_HIP_CHECK(hipDeviceSynchronize());
+            GDN2_HIP_CHECK(hipFree(L.ws));
+            L.ws = nullptr;
+            L.ws_bytes = 0;
+        }
+        GDN2_HIP_CHECK(hipMalloc(&L.ws, total));
+        L.ws_bytes = total;
+    }
+    char *base = static_cast<char *>(L.ws);
+    float **dst[10] = {&wk->Y, &wk->F, &wk->G, &wk->q, &wk->k, &wk->g, &wk->b, &wk->v, &wk->w, &wk->O};
+    for (int i = 0; i < 10; ++i) {
+        *dst[i] = reinterpret_cast<float *>(base);
+        base += align256(sz[i]);
+    }
+    wk->S0 = need_s0 ? reinterpret_cast<float *>(base) : nullptr;
+    base += align256(sz[10]);
+    wk->chunk = base;
+    wk->chunk_bytes = chunk_bytes;
+    return GDN2_OK;
+}
+
+// Linear layers of the input side: Y, F, G.
+gdn2_status input_gemms(gdn2_layer &L, const float *x, int64_t M, const Work &wk, hipStream_t s) {
+    const Dims &d = L.d;
+    rocblas_status bs = rocblas_set_stream(L.blas, s);
+    if (bs != rocblas_status_success) return fail(GDN2_EHIP, "rocblas_set_stream failed");
+    gdn2_status st;
+    if ((st = gemm(L.blas, M, L.ld_in, d.D, x, d.D, L.w_in, L.ld_in, wk.Y, L.ld_in, 0.0f)) != GDN2_OK) return st;
+    if ((st = gemm(L.blas, M, d.kd, d.V, wk.Y + L.off_f0, L.ld_in, L.p[P_F1], d.kd, wk.F, d.kd, 0.0f)) != GDN2_OK)
+        return st;
+    GDN2_HIP_CHECK(launch_fill_rows(wk.G, d.vd, L.p[P_G1_BIAS], M, d.vd, s));
+    return gemm(L.blas, M, d.vd, d.V, wk.Y + L.off_g0, L.ld_in, L.p[P_G1], d.vd, wk.G, d.vd, 1.0f);
+}
+
+gdn2_status project_epilogue(gdn2_layer &L, int64_t B, int64_t T, const float *const conv_in[3], const Work &wk,
+                             hipStream_t s) {
+    const Dims &d = L.d;
+    ProjectParams p{};
+    p.Y = wk.Y; p.ldY = L.ld_in;
+    p.off_q = L.off_q; p.off_k = L.off_k; p.off_b = L.off_b; p.off_v = L.off_v; p.off_w = L.off_w;
+    p.F = wk.F; p.ldF = d.kd;
+    p.conv_q_in = conv_in ? conv_in[0] : nullptr;
+    p.conv_k_in = conv_in ? conv_in[1] : nullptr;
+    p.conv_v_in = conv_in ? conv_in[2] : nullptr;
+    p.q_conv_w = L.p[P_QCONV]; p.k_conv_w = L.p[P_KCONV]; p.v_conv_w = L.p[P_VCONV];
+    p.a_log = L.p[P_A_LOG]; p.dt_bias = L.p[P_DT_BIAS];
+    p.decay_factors = L.cfg.has_min_decay ? L.p[P_DECAY] : nullptr;
+    p.q = wk.q; p.k = wk.k; p.g = wk.g; p.b = wk.b; p.v = wk.v; p.w = wk.w;
+    p.B = (int)B; p.T = (int)T; p.H = (int)d.H; p.K = (int)d.K; p.HV = (int)d.HV; p.V = (int)d.V;
+    p.use_short_conv = L.cfg.use_short_conv; p.allow_neg_eigval = L.cfg.allow_neg_eigval;
+    p.min_decay = (float)L.cfg.min_decay; p.one_minus_min_decay = (float)(1.0 - L.cfg.min_decay);
+    GDN2_HIP_CHECK(launch_project(p, s));
+    return GDN2_OK;
+}
+
+// The recurrence over the projected inputs into O; S is updated in place.
+gdn2_status recurrence(gdn2_layer &L, int64_t B, int64_t T, int mode, const Work &wk, float *S, hipStream_t s) {
+    gdn2_chunk_args ca = chunk_args_for(L, B, T, wk, S);
+    if (mode == GDN2_MODE_CHUNK) {
+        ca.workspace = wk.chunk;
+        ca.workspace_bytes = wk.chunk_bytes;
+        const gdn2_status st = gdn2_chunk_fwd_f32(&ca, s);
+        if (st != GDN2_NOT_APPLICABLE) return st;
+    }
+    gdn2_recurrent_args ra{};
+    ra.q = ca.q; ra.k = ca.k; ra.g = ca.g; ra.b = ca.b; ra.v = ca.v; ra.w = ca.w;
+    ra.state_in = S; ra.state_out = S; ra.out = ca.out;
+    ra.batch = B; ra.num_heads = ca.num_heads; ra.num_v_heads = ca.num_v_heads; ra.seq_len = T;
+    ra.head_dim = ca.head_dim; ra.head_v_dim = ca.head_v_dim;
+    ra.stride_qk_b = ca.stride_qk_b; ra.stride_qk_h = ca.stride_qk_h; ra.stride_qk_t = ca.stride_qk_t;
+    ra.stride_vw_b = ca.stride_vw_b; ra.stride_vw_h = ca.stride_vw_h; ra.stride_vw_t = ca.stride_vw_t;
+    ra.stride_o_b = ca.stride_o_b; ra.stride_o_h = ca.stride_o_h; ra.stride_o_t = ca.stride_o_t;
+    ra.scale = ca.scale;
+    return gdn2_recurrent_fwd_f32(&ra, s);
+}
+
+// Gated RMSNorm in place on O, then out = O W_o.
+gdn2_status output_side(gdn2_layer &L, int64_t M, bool norm, const Work &wk, float *out, hipStream_t s) {
+    const Dims &d = L.d;
+    if (norm)
+        GDN2_HIP_CHECK(launch_rmsnorm_gate(wk.O, d.vd, wk.O, d.vd, wk.G, d.vd, L.p[P_O_NORM], M, (int)d.HV, (int)d.V,
+                                           (float)L.cfg.norm_eps, s));
+    return gemm(L.blas, M, d.D, d.vd, wk.O, d.vd, L.p[P_O], d.D, out, d.D, 0.0f);
+}
+
+gdn2_status check_layer_call(const gdn2_layer *L, const float *x, int64_t B, int64_t T, const void *out,
+                             const char *who) {
+    if (!L || !x || !out) return fail(GDN2_EINVAL, std::string(who) + ": null argument");
+    if (B <= 0 || T < 0) return fail(GDN2_EINVAL, std::string(who) + ": batch must be > 0 and seq_len >= 0");
+    if (B * T > INT32_MAX / 4) return fail(GDN2_EINVAL, std::string(who) + ": batch * seq_len too large");
+    int dev = -1;
+    GDN2_HIP_CHECK(hipGetDevice(&dev));
+    if (dev != L->device)
+        return fail(GDN2_EINVAL, std::string(who) + ": the layer lives on device " + std::to_string(L->device) +
+                                     ", the current device is " + std::to_string(dev));
+    return GDN2_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Config
+// ---------------------------------------------------------------------------
+extern "C" void gdn2_config_default(gdn2_config *c) {
+    if (!c) return;
+    std::memset(c, 0, sizeof *c);
+    c->hidden_size = 2048;
+    c->num_heads = 16;
+    c->head_dim = 128;
+    c->expand_v = 1.0f;
+    c->num_v_heads = 0;
+    c->use_short_conv = 1;
+    c->allow_neg_eigval = 0;
+    c->norm_eps = 1e-5;
+    c->mode = GDN2_MODE_FUSED_RECURRENT;
+    c->chunk_size = 64;
+    c->has_min_decay = 0;
+    c->min_decay = 0.0;
+}
+
+// Gdn2Config::validate (src/config.rs:71-111): same checks, same order, same messages.
+extern "C" gdn2_status gdn2_config_validate(const gdn2_config *c) {
+    if (!c) return fail(GDN2_EINVAL, "gdn2_config_validate: null config");
+    const int64_t h = c->num_heads, hk = c->head_dim;
+    if (c->hidden_size <= 0)
+        return fail(GDN2_EINVAL, "hidden_size must be > 0, got " + std::to_string(c->hidden_size));
+    if (h <= 0) return fail(GDN2_EINVAL, "num_heads must be > 0, got " + std::to_string(h));
+    if (hk <= 0) return fail(GDN2_EINVAL, "head_dim must be > 0, got " + std::to_string(hk));
+    const float prod = (float)hk * c->expand_v;
+    if (!(c->expand_v > 0.0f && prod - std::trunc(prod) == 0.0f))
+        return fail(GDN2_EINVAL, "expand_v=" + fmt_f(c->expand_v) +
+                                     " must produce an integer head_v_dim when multiplied by head_dim=" +
+                                     std::to_string(hk) + " (got " + fmt_f(prod) + ")");
+    if (c->num_v_heads != 0) {
+        const int64_t hv = c->num_v_heads;
+        if (hv <= 0) return fail(GDN2_EINVAL, "num_v_heads must be > 0, got " + std::to_string(hv));
+        if (hv < h)
+            return fail(GDN2_EINVAL, "num_v_heads=" + std::to_string(hv) + " < num_heads=" + std::to_string(h) +
+                                         " is not supported; use num_v_heads >= num_heads (GVA repeats key-side "
+                                         "heads)");
+        if (hv % h != 0)
+            return fail(GDN2_EINVAL, "num_v_heads=" + std::to_string(hv) + " must be divisible by num_heads=" +
+                                         std::to_string(h));
+    }
+    if (c->chunk_size <= 0) return fail(GDN2_EINVAL, "chunk_size must be > 0, got " + std::to_string(c->chunk_size));
+    if (!(c->norm_eps > 0.0)) return fail(GDN2_EINVAL, "norm_eps must be > 0, got " + fmt_f(c->norm_eps));
+    if (c->mode != GDN2_MODE_FUSED_RECURRENT && c->mode != GDN2_MODE_CHUNK)
+        return fail(GDN2_EINVAL, "mode must be GDN2_MODE_FUSED_RECURRENT or GDN2_MODE_CHUNK");
+    return GDN2_OK;
+}
+
+extern "C" gdn2_status gdn2_config_dims(const gdn2_config *c, int64_t *hv, int64_t *v_head, int64_t *kd,
+                                        int64_t *vd) {
+    if (!c) return fail(GDN2_EINVAL, "gdn2_config_dims: null config");
+    const Dims d = dims_of(*c);
+    if (hv) *hv = d.HV;
+    if (v_head) *v_head = d.V;
+    if (kd) *kd = d.kd;
+    if (vd) *vd = d.vd;
+    return GDN2_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Parameters
+// ---------------------------------------------------------------------------
+extern "C" int gdn2_param_count(void) { return P_COUNT; }
+
+extern "C" const char *gdn2_param_name(int i) { return (i >= 0 && i < P_COUNT) ? kParamNames[i] : nullptr; }
+
+extern "C" int64_t gdn2_param_shape(const gdn2_config *c, const char *name, int64_t *rows, int64_t *cols) {
+    const int id = param_id(name);
+    if (!c || id < 0) return -1;
+    return param_shape(*c, id, rows, cols);
+}
+
+extern "C" gdn2_status gdn2_param_init(const gdn2_config *c, uint64_t seed, const char *name, float *host,
+                                       int64_t numel) {
+    const int id = param_id(name);
+    if (!c || !host) return fail(GDN2_EINVAL, "gdn2_param_init: null argument");
+    if (id < 0) return fail(GDN2_EINVAL, std::string("gdn2_param_init: unknown parameter ") + (name ? name : ""));
+    const int64_t n = param_shape(*c, id, nullptr, nullptr);
+    if (n != numel)
+        return fail(GDN2_EINVAL, std::string("gdn2_param_init: ") + name + " has " + std::to_string(n) +
+                                     " elements, got " + std::to_string(numel));
+    init_param(*c, seed, id, host);
+    return GDN2_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Layer
+// ---------------------------------------------------------------------------
+extern "C" void gdn2_layer_destroy(gdn2_layer *L) {
+    if (!L) return;
+    int prev = -1;
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(L->device);
+    (void)hipDeviceSynchronize();
+    if (L->blas) rocblas_destroy_handle(L->blas);
+    (void)hipFree(L->w_in);
+    for (float *p : L->p) (void)hipFree(p);
+    (void)hipFree(L->ws);
+    if (prev >= 0) (void)hipSetDevice(prev);
+    delete L;
+}
+
+extern "C" gdn2_status gdn2_layer_set_param(gdn2_layer *L, const char *name, const float *host, int64_t numel) {
+    if (!L || !host) return fail(GDN2_EINVAL, "gdn2_layer_set_param: null argument");
+    const int id = param_id(name);
+    if (id < 0) return fail(GDN2_EINVAL, std::string("gdn2_layer_set_param: unknown parameter ") + (name ? name : ""));
+    int64_t rows = 0, cols = 0;
+    const int64_t n = param_shape(L->cfg, id, &rows, &cols);
+    if (n == 0) return fail(GDN2_EINVAL, std::string("gdn2_layer_set_param: ") + name + " is absent in this config");
+    if (n != numel)
+        return fail(GDN2_EINVAL, std::string("gdn2_layer_set_param: ") + name + " has " + std::to_string(n) +
+                                     " elements, got " + std::to_string(numel));
+    const int64_t off = L->col_offset(id);
+    if (off >= 0)
+        GDN2_HIP_CHECK(hipMemcpy2D(L->w_in + off, sizeof(float) * L->ld_in, host, sizeof(float) * cols,
+                                   sizeof(float) * cols, rows, hipMemcpyHostToDevice));
+    else
+        GDN2_HIP_CHECK(hipMemcpy(L->p[id], host, sizeof(float) * n, hipMemcpyHostToDevice));
+    return GDN2_OK;
+}
+
+extern "C" gdn2_status gdn2_layer_get_param(const gdn2_layer *L, const char *name, float *host, int64_t numel) {
+    if (!L || !host) return fail(GDN2_EINVAL, "gdn2_layer_get_param: null argument");
+    const int id = param_id(name);
+    if (id < 0) return fail(GDN2_EINVAL, std::string("gdn2_layer_get_param: unknown parameter ") + (name ? name : ""));
+    int64_t rows = 0, cols = 0;
+    const int64_t n = param_shape(L->cfg, id, &rows, &cols);
+    if (n == 0) return fail(GDN2_EINVAL, std::string("gdn2_layer_get_param: ") + name + " is absent in this config");
+    if (n != numel)
+        return fail(GDN2_EINVAL, std::string("gdn2_layer_get_param: ") + name + " has " + std::to_string(n) +
+                                     " elements, got " + std::to_string(numel));
+    const int64_t off = L->col_offset(id);
+    if (off >= 0)
+        GDN2_HIP_CHECK(hipMemcpy2D(host, sizeof(float) * cols, L->w_in + off, sizeof(float) * L->ld_in,
+                                   sizeof(float) * cols, rows, hipMemcpyDeviceToHost));
+    else
+        GDN2_HIP_CHECK(hipMemcpy(host, L->p[id], sizeof(float) * n, hipMemcpyDeviceToHost));
+    return GDN2_OK;
+}
+
+extern "C" gdn2_status gdn2_layer_create(const gdn2_config *c, uint64_t seed, gdn2_layer **out) {
+    if (!out) return fail(GDN2_EINVAL, "gdn2_layer_create: null output");
+    *out = nullptr;
+    gdn2_status st = gdn2_config_validate(c);
+    if (st != GDN2_OK) return st;
+    if (!gdn2_hip_available()) return fail(GDN2_EHIP, "gdn2_layer_create: no gfx950 device is current");
+    const Dims d = dims_of(*c);
+    if (d.kd > 8192) return fail(GDN2_NOT_APPLICABLE, "gdn2_layer_create: num_heads * head_dim above 8192");
+    gdn2_layer *L = new gdn2_layer();
+    L->cfg = *c;
+    L->d = d;
+    if (hipGetDevice(&L->device) != hipSuccess) {
+        delete L;
+        return fail(GDN2_EHIP, "gdn2_layer_create: hipGetDevice failed");
+    }
+    // W_in column blocks, each starting at a multiple of 4 columns (16-byte rows for the kernels)
+    auto up4 = [](int64_t v) { return (v + 3) & ~(int64_t)3; };
+    int64_t col = 0;
+    L->off_q = col; col += up4(d.kd);
+    L->off_k = col; col += up4(d.kd);
+    L->off_b = col; col += up4(d.kd);
+    L->off_v = col; col += up4(d.vd);
+    L->off_w = col; col += up4(d.vd);
+    L->off_f0 = col; col += up4(d.V);
+    L->off_g0 = col; col += up4(d.V);
+    L->ld_in = (col + 15) & ~(int64_t)15;
+    auto cleanup = [&](gdn2_status s) {
+        gdn2_layer_destroy(L);
+        return s;
+    };
+    if (rocblas_create_handle(&L->blas) != rocblas_status_success)
+        return cleanup(fail(GDN2_EHIP, "gdn2_layer_create: rocblas_create_handle failed"));
+    if (hipMalloc(&L->w_in, sizeof(float) * d.D * L->ld_in) != hipSuccess ||
+        hipMemset(L->w_in, 0, sizeof(float) * d.D * L->ld_in) != hipSuccess)
+        return cleanup(fail(GDN2_EHIP, "gdn2_layer_create: hipMalloc failed"));
+    for (int id = 0; id < P_COUNT; ++id) {
+        const int64_t n = param_shape(*c, id, nullptr, nullptr);
+        if (n == 0) continue;
+        if (L->col_offset(id) < 0 && hipMalloc(&L->p[id], sizeof(float) * n) != hipSuccess)
+            return cleanup(fail(GDN2_EHIP, "gdn2_layer_create: hipMalloc failed"));
+        float *host = new float[n];
+        init_param(*c, seed, id, host);
+        st = gdn2_layer_set_param(L, kParamNames[id], host, n);
+        delete[] host;
+        if (st != GDN2_OK) return cleanup(st);
+    }
+    *out = L;
+    return GDN2_OK;
+}
+
+extern "C" const gdn2_config *gdn2_layer_config(const gdn2_layer *L) { return L ? &L->cfg : nullptr; }
+
+extern "C" gdn2_status gdn2_layer_forward_train_f32(gdn2_layer *L, const float *x, int64_t B, int64_t T, float *out,
+                                                    gdn2_stream_t stream) {
+    gdn2_status st = check_layer_call(L, x, B, T, out, "gdn2_layer_forward_train_f32");
+    if (st != GDN2_OK || T == 0) return st;
+    hipStream_t s = (hipStream_t)stream;
+    Work wk{};
+    if ((st = workspace(*L, B, T, true, &wk)) != GDN2_OK) return st;
+    const int64_t M = B * T;
+    if ((st = input_gemms(*L, x, M, wk, s)) != GDN2_OK) return st;
+    if ((st = project_epilogue(*L, B, T, nullptr, wk, s)) != GDN2_OK) return st;
+    GDN2_HIP_CHECK(launch_fill_rows(wk.S0, 0, nullptr, 1, B * L->d.HV * L->d.K * L->d.V, s));
+    if ((st = recurrence(*L, B, T, L->cfg.mode, wk, wk.S0, s)) != GDN2_OK) return st;
+    return output_side(*L, M, true, wk, out, s);
+}
+
+extern "C" gdn2_status gdn2_layer_forward_f32(gdn2_layer *L, const float *x, int64_t B, int64_t T, gdn2_state *S,
+                                              float *out, gdn2_stream_t stream) {
+    gdn2_status st = check_layer_call(L, x, B, T, out, "gdn2_layer_forward_f32");
+    if (st != GDN2_OK) return st;
+    if (!S || S->layer != L) return fail(GDN2_EINVAL, "gdn2_layer_forward_f32: state missing or made for another layer");
+    if (S->batch != B)
+        return fail(GDN2_EINVAL, "gdn2_layer_forward_f32: state batch " + std::to_string(S->batch) +
+                                     " != input batch " + std::to_string(B));
+    if (T == 0) return GDN2_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const Dims &d = L->d;
+    const bool sc = L->cfg.use_short_conv != 0;
+    Work wk{};
+    if ((st = workspace(*L, B, T, false, &wk)) != GDN2_OK) return st;
+    const int64_t M = B * T;
+    // Option::None: S = 0; Gdn2State::zeros caches when the conv does not replace them
+    if (!S->some) {
+        GDN2_HIP_CHECK(launch_fill_rows(S->S, 0, nullptr, 1, B * d.HV * d.K * d.V, s));
+        if (!sc)
+            for (int i = 0; i < 3; ++i)
+                GDN2_HIP_CHECK(launch_fill_rows(S->conv[S->cur][i], 0, nullptr, 1, B * 3 * (i < 2 ? d.kd : d.vd), s));
+    }
+    const float *conv_in[3] = {S->conv[S->cur][0], S->conv[S->cur][1], S->conv[S->cur][2]};
+    float *const *conv_out = S->conv[1 - S->cur];
+    const bool has_cache = S->some;
+    if ((st = input_gemms(*L, x, M, wk, s)) != GDN2_OK) return st;
+    if (T == 1 && d.K <= 256 && d.V <= 1024) {
+        gdn2_layer_params lp{};
+        lp.q_conv_w = L->p[P_QCONV]; lp.k_conv_w = L->p[P_KCONV]; lp.v_conv_w = L->p[P_VCONV];
+        lp.a_log = L->p[P_A_LOG]; lp.dt_bias = L->p[P_DT_BIAS];
+        lp.decay_factors = L->cfg.has_min_decay ? L->p[P_DECAY] : nullptr;
+        lp.o_norm_weight = L->p[P_O_NORM];
+        lp.min_decay = L->cfg.min_decay; lp.norm_eps = L->cfg.norm_eps;
+        lp.use_short_conv = L->cfg.use_short_conv; lp.allow_neg_eigval = L->cfg.allow_neg_eigval;
+        DecodeParams p{};
+        p.q_raw = wk.Y + L->off_q; p.k_raw = wk.Y + L->off_k; p.b_raw = wk.Y + L->off_b;
+        p.v_raw = wk.Y + L->off_v; p.w_raw = wk.Y + L->off_w; p.f_raw = wk.F; p.gate = wk.G;
+        p.ld_q = p.ld_k = p.ld_b = p.ld_v = p.ld_w = L->ld_in;
+        p.ld_f = d.kd; p.ld_gate = d.vd; p.ld_out = d.vd;
+        p.conv_q_in = has_cache ? conv_in[0] : nullptr;
+        p.conv_k_in = has_cache ? conv_in[1] : nullptr;
+        p.conv_v_in = has_cache ? conv_in[2] : nullptr;
+        p.conv_q_out = conv_out[0]; p.conv_k_out = conv_out[1]; p.conv_v_out = conv_out[2];
+        p.q_conv_w = lp.q_conv_w; p.k_conv_w = lp.k_conv_w; p.v_conv_w = lp.v_conv_w;
+        p.a_log = lp.a_log; p.dt_bias = lp.dt_bias; p.decay_factors = lp.decay_factors;
+        p.o_norm_weight = lp.o_norm_weight;
+        p.state = S->S; p.out = wk.O;
+        p.B = (int)B; p.H = (int)d.H; p.HV = (int)d.HV; p.rep = (int)(d.HV / d.H); p.K = (int)d.K; p.V = (int)d.V;
+        p.use_short_conv = lp.use_short_conv; p.allow_neg_eigval = lp.allow_neg_eigval;
+        p.min_decay = (float)lp.min_decay; p.one_minus_min_decay = (float)(1.0 - lp.min_decay);
+        p.norm_eps = (float)lp.norm_eps; p.scale = (float)std::pow((double)d.K, -0.5);
+        GDN2_HIP_CHECK(launch_decode(p, s));
+        if ((st = output_side(*L, M, false, wk, out, s)) != GDN2_OK) return st;
+    } else {
+        if ((st = project_epilogue(*L, B, T, has_cache ? conv_in : nullptr, wk, s)) != GDN2_OK) return st;
+        if (sc) {
+            ConvCacheParams cp{};
+            cp.Y = wk.Y; cp.ldY = L->ld_in; cp.off_q = L->off_q; cp.off_k = L->off_k; cp.off_v = L->off_v;
+            cp.in_q = has_cache ? conv_in[0] : nullptr;
+            cp.in_k = has_cache ? conv_in[1] : nullptr;
+            cp.in_v = has_cache ? conv_in[2] : nullptr;
+            cp.out_q = conv_out[0]; cp.out_k = conv_out[1]; cp.out_v = conv_out[2];
+            cp.B = (int)B; cp.T = (int)T; cp.kd = (int)d.kd; cp.vd = (int)d.vd;
+            GDN2_HIP_CHECK(launch_conv_cache(cp, s));
+        }
+        const int mode = T <= kFusedRecurrentMaxSeq ? GDN2_MODE_FUSED_RECURRENT : L->cfg.mode;
+        if ((st = recurrence(*L, B, T, mode, wk, S->S, s)) != GDN2_OK) return st;
+        if ((st = output_side(*L, M, true, wk, out, s)) != GDN2_OK) return st;
+    }
+    if (sc) S->cur = 1 - S->cur;
+    S->some = true;
+    return GDN2_OK;
+}
+
+extern "C" gdn2_status gdn2_layer_project_f32(gdn2_layer *L, const float *x, int64_t B, int64_t T,
+                                              const gdn2_state *S, float *q, float *k, float *g, float *b, float *v,
+                                              float *w, float *gate, gdn2_stream_t stream) {
+    gdn2_status st = check_layer_call(L, x, B, T, q, "gdn2_layer_project_f32");
+    if (st != GDN2_OK) return st;
+    if (!k || !g || !b || !v || !w || !gate) return fail(GDN2_EINVAL, "gdn2_layer_project_f32: null output");
+    if (S && (S->layer != L || S->batch != B))
+        return fail(GDN2_EINVAL, "gdn2_layer_project_f32: state made for another layer or batch");
+    if (T == 0) return GDN2_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const Dims &d = L->d;
+    Work wk{};
+    if ((st = workspace(*L, B, T, false, &wk)) != GDN2_OK) return st;
+    const int64_t M = B * T;
+    if ((st = input_gemms(*L, x, M, wk, s)) != GDN2_OK) return st;
+    const float *conv_in[3] = {};
+    const bool has_cache = S && S->some;
+    if (has_cache)
+        for (int i = 0; i < 3; ++i) conv_in[i] = S->conv[S->cur][i];
+    if ((st = project_epilogue(*L, B, T, has_cache ? conv_in : nullptr, wk, s)) != GDN2_OK) return st;
+    const size_t nk = sizeof(float) * M * d.kd, nv = sizeof(float) * M * d.vd;
+    GDN2_HIP_CHECK(hipMemcpyAsync(q, wk.q, nk, hipMemcpyDeviceToDevice, s));
+    GDN2_HIP_CHECK(hipMemcpyAsync(k, wk.k, nk, hipMemcpyDeviceToDevice, s));
+    GDN2_HIP_CHECK(hipMemcpyAsync(g, wk.g, nk, hipMemcpyDeviceToDevice, s));
+    GDN2_HIP_CHECK(hipMemcpyAsync(b, wk.b, nk, hipMemcpyDeviceToDevice, s));
+    GDN2_HIP_CHECK(hipMemcpyAsync(v, wk.v, nv, hipMemcpyDeviceToDevice, s));
+    GDN2_HIP_CHECK(hipMemcpyAsync(w, wk.w, nv, hipMemcpyDeviceToDevice, s));
+    GDN2_HIP_CHECK(hipMemcpyAsync(gate, wk.G, nv, hipMemcpyDeviceToDevice, s));
+    return GDN2_OK;
+}
+
+// ---------------------------------------------------------------------------
+// State
+// ---------------------------------------------------------------------------
+namespace {
+int64_t state_numel(const gdn2_state *S, int which) {
+    if (!S || !S->layer) return -1;
+    const Dims &d = S->layer->d;
+    switch (which) {
+        case GDN2_STATE_RECURRENT: return S->batch * d.HV * d.K * d.V;
+        case GDN2_STATE_CONV_Q: case GDN2_STATE_CONV_K: return S->batch * kShortConvCache * d.kd;
+        case GDN2_STATE_CONV_V: return S->batch * kShortConvCache * d.vd;
+        default: return -1;
+    }
+}
+
+float *state_ptr(const gdn2_state *S, int which) {
+    if (which == GDN2_STATE_RECURRENT) return S->S;
+    return S->conv[S->cur][which - 1];
+}
+}  // namespace
+
+extern "C" void gdn2_state_destroy(gdn2_state *S) {
+    if (!S) return;
+    (void)hipDeviceSynchronize();
+    (void)hipFree(S->S);
+    for (auto &buf : S->conv)
+        for (float *p : buf) (void)hipFree(p);
+    delete S;
+}
+
+extern "C" gdn2_status gdn2_state_create(const gdn2_layer *L, int64_t batch, gdn2_state **out) {
+    if (!L || !out) return fail(GDN2_EINVAL, "gdn2_state_create: null argument");
+    if (batch <= 0) return fail(GDN2_EINVAL, "gdn2_state_create: batch must be > 0");
+    *out = nullptr;
+    gdn2_state *S = new gdn2_state();
+    S->layer = L;
+    S->batch = batch;
+    bool ok = hipMalloc(&S->S, sizeof(float) * state_numel(S, GDN2_STATE_RECURRENT)) == hipSuccess;
+    for (int j = 0; j < 2 && ok; ++j)
+        for (int i = 0; i < 3 && ok; ++i) {
+            const size_t n = sizeof(float) * state_numel(S, i + 1);
+            ok = hipMalloc(&S->conv[j][i], n) == hipSuccess && hipMemset(S->conv[j][i], 0, n) == hipSuccess;
+        }
+    if (!ok || hipMemset(S->S, 0, sizeof(float) * state_numel(S, GDN2_STATE_RECURRENT)) != hipSuccess) {
+        gdn2_state_destroy(S);
+        return fail(GDN2_EHIP, "gdn2_state_create: device allocation failed");
+    }
+    *out = S;
+    return GDN2_OK;
+}
+
+extern "C" gdn2_status gdn2_state_set_zeros(gdn2_state *S) {
+    if (!S) return fail(GDN2_EINVAL, "gdn2_state_set_zeros: null state");
+    GDN2_HIP_CHECK(hipDeviceSynchronize());
+    GDN2_HIP_CHECK(hipMemset(S->S, 0, sizeof(float) * state_numel(S, GDN2_STATE_RECURRENT)));
+    for (int i = 0; i < 3; ++i)
+        GDN2_HIP_CHECK(hipMemset(S->conv[S->cur][i], 0, sizeof(float) * state_numel(S, i + 1)));
+    S->some = true;
+    return GDN2_OK;
+}
+
+extern "C" void gdn2_state_clear(gdn2_state *S) {
+    if (S) S->some = false;
+}
+
+extern "C" int gdn2_state_is_some(const gdn2_state *S) { return S && S->some ? 1 : 0; }
+
+extern "C" int64_t gdn2_state_batch(const gdn2_state *S) { return S ? S->batch : -1; }
+
+extern "C" int64_t gdn2_state_numel(const gdn2_state *S, int which) { return state_numel(S, which); }
+
+extern "C" float *gdn2_state_tensor(gdn2_state *S, int which) {
+    if (state_numel(S, which) < 0) return nullptr;
+    return state_ptr(S, which);
+}
+
+extern "C" gdn2_status gdn2_state_read(const gdn2_state *S, int which, float *host, int64_t numel) {
+    const int64_t n = state_numel(S, which);
+    if (n < 0 || !host) return fail(GDN2_EINVAL, "gdn2_state_read: bad state, tensor index or buffer");
+    if (n != numel) return fail(GDN2_EINVAL, "gdn2_state_read: expected " + std::to_string(n) + " elements");
+    GDN2_HIP_CHECK(hipDeviceSynchronize());
+    GDN2_HIP_CHECK(hipMemcpy(host, state_ptr(S, which), sizeof(float) * n, hipMemcpyDeviceToHost));
+    return GDN2_OK;
+}
+
+extern "C" gdn2_status gdn2_state_write(gdn2_state *S, int which, const float *host, int64_t numel) {
+    const int64_t n = state_numel(S, which);
+    if (n < 0 || !host) return fail(GDN2_EINVAL, "gdn2_state_write: bad state, tensor index or buffer");
+    if (n != numel) return fail(GDN2_EINVAL, "gdn2_state_write: expected " + std::to_string(n) + " elements");
+    GDN2_HIP_CHECK(hipDeviceSynchronize());
+    if (!S->some) {
+        GDN2_HIP_CHECK(hipMemset(S->S, 0, sizeof(float) * state_numel(S, GDN2_STATE_RECURRENT)));
+        for (int i = 0; i < 3; ++i)
+            GDN2_HIP_CHECK(hipMemset(S->conv[S->cur][i], 0, sizeof(float) * state_numel(S, i + 1)));
+    }
+    GDN2_HIP_CHECK(hipMemcpy(state_ptr(S, which), host, sizeof(float) * n, hipMemcpyHostToDevice));
+    S->some = true;
+    return GDN2_OK;
+}

@@ -220,8 +220,7 @@ __device__ __forceinline__ void key_prologue(const DecodeParams &p, int bi, int 
                                              float *sk_part) {
     const int kd = p.H * p.K;
     const int c = hk * p.K + r;
-    const int64_t xo = (int64_t)bi * kd + c;
-    const float qr = p.q_raw[xo], kr = p.k_raw[xo];
+    const float qr = p.q_raw[(int64_t)bi * p.ld_q + c], kr = p.k_raw[(int64_t)bi * p.ld_k + c];
     float qa, ka;
     if (p.use_short_conv) {
         const int64_t cb = (int64_t)bi * 3 * kd;
@@ -242,12 +241,12 @@ __device__ __forceinline__ void key_prologue(const DecodeParams &p, int bi, int 
         qa = siluf_(qr);
         ka = siluf_(kr);
     }
-    float gv = -expf(p.a_log[hk]) * softplusf_(p.f_raw[xo] + p.dt_bias[c]);
+    float gv = -expf(p.a_log[hk]) * softplusf_(p.f_raw[(int64_t)bi * p.ld_f + c] + p.dt_bias[c]);
     if (p.decay_factors) {
         const float f = sigmoidf_(p.decay_factors[c]) * p.one_minus_min_decay;
         gv = logf(f * expf(gv) + p.min_decay);
     }
-    float bv = sigmoidf_(p.b_raw[xo]);
+    float bv = sigmoidf_(p.b_raw[(int64_t)bi * p.ld_b + c]);
     if (p.allow_neg_eigval) bv *= 2.0f;
     s_q[r] = qa;
     s_k[r] = ka;
@@ -261,8 +260,7 @@ __device__ __forceinline__ void key_prologue(const DecodeParams &p, int bi, int 
 __device__ __forceinline__ void value_prologue(const DecodeParams &p, int bi, int hv, int col, float *v, float *w) {
     const int vd = p.HV * p.V;
     const int c = hv * p.V + col;
-    const int64_t xo = (int64_t)bi * vd + c;
-    const float vr = p.v_raw[xo];
+    const float vr = p.v_raw[(int64_t)bi * p.ld_v + c];
     if (p.use_short_conv) {
         const int64_t cb = (int64_t)bi * 3 * vd;
         float a0, a1, a2;
@@ -273,7 +271,7 @@ __device__ __forceinline__ void value_prologue(const DecodeParams &p, int bi, in
     } else {
         *v = siluf_(vr);
     }
-    *w = sigmoidf_(p.w_raw[xo]);
+    *w = sigmoidf_(p.w_raw[(int64_t)bi * p.ld_w + c]);
 }
 
 template <int K, int V>
@@ -303,31 +301,33 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
     // operands point at an input that is read anyway) and selected after.
     const int r = tid % K;               // key channel (lanes >= K duplicate)
     const int c = hk * K + r;
-    const int64_t xo = (int64_t)bi * kd + c;
-    const float qr = p.q_raw[xo], kr = p.k_raw[xo], fr = p.f_raw[xo], brw = p.b_raw[xo];
+    const int64_t xq = (int64_t)bi * p.ld_q + c, xk = (int64_t)bi * p.ld_k + c;
+    const float qr = p.q_raw[xq], kr = p.k_raw[xk];
+    const float fr = p.f_raw[(int64_t)bi * p.ld_f + c], brw = p.b_raw[(int64_t)bi * p.ld_b + c];
     const float dtb = p.dt_bias[c], alog = p.a_log[hk];
     const float dfv = (p.decay_factors ? p.decay_factors : p.dt_bias)[c];
     const int64_t kcb = (int64_t)bi * 3 * kd + c;
-    const float *cqi = (sc && p.conv_q_in) ? p.conv_q_in + kcb : p.q_raw + xo;
-    const float *cki = (sc && p.conv_k_in) ? p.conv_k_in + kcb : p.k_raw + xo;
+    const float *cqi = (sc && p.conv_q_in) ? p.conv_q_in + kcb : p.q_raw + xq;
+    const float *cki = (sc && p.conv_k_in) ? p.conv_k_in + kcb : p.k_raw + xk;
     const int64_t cst = (sc && p.conv_q_in) ? kd : 0;
     const float q0 = cqi[0], q1 = cqi[cst], q2 = cqi[2 * cst];
     const float k0 = cki[0], k1 = cki[cst], k2 = cki[2 * cst];
-    const float *wq = sc ? p.q_conv_w + 4 * c : p.q_raw + xo;
-    const float *wk = sc ? p.k_conv_w + 4 * c : p.k_raw + xo;
+    const float *wq = sc ? p.q_conv_w + 4 * c : p.q_raw + xq;
+    const float *wk = sc ? p.k_conv_w + 4 * c : p.k_raw + xk;
     const int wst = sc ? 1 : 0;
     const float wq0 = wq[0], wq1 = wq[wst], wq2 = wq[2 * wst], wq3 = wq[3 * wst];
     const float wk0 = wk[0], wk1 = wk[wst], wk2 = wk[2 * wst], wk3 = wk[3 * wst];
 
     const int col = tid % V;             // value column (lanes >= V duplicate)
     const int cvc = hv * V + col;
-    const int64_t vo = (int64_t)bi * vd + cvc;
-    const float vr = p.v_raw[vo], wr = p.w_raw[vo], gt = p.gate[vo], onw = p.o_norm_weight[col];
+    const int64_t xv = (int64_t)bi * p.ld_v + cvc;
+    const float vr = p.v_raw[xv], wr = p.w_raw[(int64_t)bi * p.ld_w + cvc];
+    const float gt = p.gate[(int64_t)bi * p.ld_gate + cvc], onw = p.o_norm_weight[col];
     const int64_t vcb = (int64_t)bi * 3 * vd + cvc;
-    const float *cvi = (sc && p.conv_v_in) ? p.conv_v_in + vcb : p.v_raw + vo;
+    const float *cvi = (sc && p.conv_v_in) ? p.conv_v_in + vcb : p.v_raw + xv;
     const int64_t vst = (sc && p.conv_v_in) ? vd : 0;
     const float v0 = cvi[0], v1 = cvi[vst], v2 = cvi[2 * vst];
-    const float *wv = sc ? p.v_conv_w + 4 * cvc : p.v_raw + vo;
+    const float *wv = sc ? p.v_conv_w + 4 * cvc : p.v_raw + xv;
     const float wv0 = wv[0], wv1 = wv[wst], wv2 = wv[2 * wst], wv3 = wv[3 * wst];
 
     // The state slice: 16-byte loads, each row read exactly once, part 0 first.
@@ -451,7 +451,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
     __syncthreads();
     if (vlane) {
         const float ms = (red_o2[0] + red_o2[1] + red_o2[2] + red_o2[3]) / (float)V;
-        p.out[vo] = o / sqrtf(ms + p.norm_eps) * onw * siluf_(gt);
+        p.out[(int64_t)bi * p.ld_out + cvc] = o / sqrtf(ms + p.norm_eps) * onw * siluf_(gt);
     }
     // Conv caches: the last three pre-conv rows, oldest first.  Value caches
     // are owned by this (b, hv); key caches by the first value head of hk.
@@ -524,8 +524,8 @@ __global__ __launch_bounds__(256) void decode_fused_generic_kernel(DecodeParams 
     const float rms = sqrtf(o2 / (float)V + p.norm_eps);
     n = 0;
     for (int c = tid; c < V; c += 256, ++n) {
-        const int64_t gi = (int64_t)bi * p.HV * V + (int64_t)hv * V + c;
-        p.out[gi] = ov[n] / rms * p.o_norm_weight[c] * siluf_(p.gate[gi]);
+        const int64_t ch = (int64_t)hv * V + c;
+        p.out[bi * p.ld_out + ch] = ov[n] / rms * p.o_norm_weight[c] * siluf_(p.gate[bi * p.ld_gate + ch]);
     }
 }
 

@@ -70,10 +70,28 @@ class DecodeArgs(ctypes.Structure):
                 ("head_v_dim", _i64), ("scale", _dbl), ("params", ctypes.POINTER(LayerParams))]
 
 
-# Every symbol include/gdn2.h declares (checked by tests/test_capi_exports.py).
+class Config(ctypes.Structure):
+    """gdn2_config (include/gdn2_layer.h) = Gdn2Config (src/config.rs:23-58)."""
+    _fields_ = [("hidden_size", _i64), ("num_heads", _i64), ("head_dim", _i64), ("expand_v", ctypes.c_float),
+                ("num_v_heads", _i64), ("use_short_conv", ctypes.c_int32), ("allow_neg_eigval", ctypes.c_int32),
+                ("norm_eps", _dbl), ("mode", ctypes.c_int32), ("chunk_size", _i64),
+                ("has_min_decay", ctypes.c_int32), ("min_decay", _dbl)]
+
+
+MODE_FUSED_RECURRENT = 0
+MODE_CHUNK = 1
+STATE_RECURRENT, STATE_CONV_Q, STATE_CONV_K, STATE_CONV_V = 0, 1, 2, 3
+
+# Every symbol include/*.h declares (checked by tests/test_capi_exports.py).
 EXPORTS = ("gdn2_last_error", "gdn2_hip_available", "gdn2_recurrent_step_f32", "gdn2_recurrent_fwd_f32",
            "gdn2_chunk_workspace_bytes", "gdn2_chunk_fwd_f32", "gdn2_chunk_intra_f32", "gdn2_chunk_inter_f32",
-           "gdn2_decode_fused_f32")
+           "gdn2_decode_fused_f32",
+           "gdn2_config_default", "gdn2_config_validate", "gdn2_config_dims", "gdn2_param_count",
+           "gdn2_param_name", "gdn2_param_shape", "gdn2_param_init", "gdn2_layer_create", "gdn2_layer_destroy",
+           "gdn2_layer_config", "gdn2_layer_set_param", "gdn2_layer_get_param", "gdn2_layer_forward_train_f32",
+           "gdn2_layer_forward_f32", "gdn2_layer_project_f32", "gdn2_state_create", "gdn2_state_destroy",
+           "gdn2_state_set_zeros", "gdn2_state_clear", "gdn2_state_is_some", "gdn2_state_batch",
+           "gdn2_state_numel", "gdn2_state_tensor", "gdn2_state_read", "gdn2_state_write")
 
 _lib = None
 
@@ -102,8 +120,45 @@ def lib():
             fn.restype = ctypes.c_int
         L.gdn2_chunk_workspace_bytes.argtypes = [ctypes.POINTER(ChunkArgs)]
         L.gdn2_chunk_workspace_bytes.restype = ctypes.c_size_t
+        _declare_layer(L)
         _lib = L
     return _lib
+
+
+def _declare_layer(L):
+    cfgp, vp, i64, i32, fp = ctypes.POINTER(Config), ctypes.c_void_p, _i64, ctypes.c_int, _fp
+    i64p = ctypes.POINTER(_i64)
+    sig = {
+        "gdn2_config_default": (None, [cfgp]),
+        "gdn2_config_validate": (i32, [cfgp]),
+        "gdn2_config_dims": (i32, [cfgp, i64p, i64p, i64p, i64p]),
+        "gdn2_param_count": (i32, []),
+        "gdn2_param_name": (ctypes.c_char_p, [i32]),
+        "gdn2_param_shape": (i64, [cfgp, ctypes.c_char_p, i64p, i64p]),
+        "gdn2_param_init": (i32, [cfgp, ctypes.c_uint64, ctypes.c_char_p, fp, i64]),
+        "gdn2_layer_create": (i32, [cfgp, ctypes.c_uint64, ctypes.POINTER(vp)]),
+        "gdn2_layer_destroy": (None, [vp]),
+        "gdn2_layer_config": (cfgp, [vp]),
+        "gdn2_layer_set_param": (i32, [vp, ctypes.c_char_p, fp, i64]),
+        "gdn2_layer_get_param": (i32, [vp, ctypes.c_char_p, fp, i64]),
+        "gdn2_layer_forward_train_f32": (i32, [vp, fp, i64, i64, fp, vp]),
+        "gdn2_layer_forward_f32": (i32, [vp, fp, i64, i64, vp, fp, vp]),
+        "gdn2_layer_project_f32": (i32, [vp, fp, i64, i64, vp, fp, fp, fp, fp, fp, fp, fp, vp]),
+        "gdn2_state_create": (i32, [vp, i64, ctypes.POINTER(vp)]),
+        "gdn2_state_destroy": (None, [vp]),
+        "gdn2_state_set_zeros": (i32, [vp]),
+        "gdn2_state_clear": (None, [vp]),
+        "gdn2_state_is_some": (i32, [vp]),
+        "gdn2_state_batch": (i64, [vp]),
+        "gdn2_state_numel": (i64, [vp, i32]),
+        "gdn2_state_tensor": (fp, [vp, i32]),
+        "gdn2_state_read": (i32, [vp, i32, fp, i64]),
+        "gdn2_state_write": (i32, [vp, i32, fp, i64]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
 
 
 def check(status: int, allow_not_applicable=False) -> bool:

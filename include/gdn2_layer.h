@@ -1,0 +1,170 @@
+/*
+ * gdn2_layer.h -- C ABI of the GDN-2 layer (config, parameters, state,
+ * forward) built on the kernels of gdn2.h.
+ *
+ * It mirrors burn-gdn2's public surface:
+ *
+ *   gdn2_config, gdn2_config_default   <- Gdn2Config, Default      src/config.rs:23-58, :114-130
+ *   gdn2_config_validate               <- Gdn2Config::validate     src/config.rs:71-111
+ *   gdn2_config_dims                   <- shape algebra             src/module.rs:113-119
+ *   gdn2_param_*, gdn2_layer_create    <- GatedDeltaNet2::new       src/module.rs:111-190
+ *   gdn2_layer_project_f32             <- GatedDeltaNet2::project   src/module.rs:381-495
+ *   gdn2_layer_forward_train_f32       <- forward_train             src/module.rs:326-375
+ *   gdn2_layer_forward_f32             <- forward(.., update_state = true)
+ *                                                                   src/module.rs:224-316
+ *   gdn2_state_*                       <- Gdn2State / Option<Gdn2State>
+ *                                                                   src/module.rs:30-63
+ *
+ * Status codes and gdn2_last_error() are those of gdn2.h.  Configuration
+ * errors return GDN2_EINVAL with the reference's panic message.  The layer
+ * owns its parameters and a workspace in device memory (allocated on the
+ * device current at gdn2_layer_create; the workspace grows on the first
+ * call at a larger batch x tokens).  x and out are caller-owned device
+ * buffers [B, T, hidden_size], contiguous f32.  Calls are asynchronous on
+ * `stream`; calls on one layer must not overlap (they share the workspace).
+ */
+#ifndef GDN2_LAYER_H_
+#define GDN2_LAYER_H_
+
+#include "gdn2.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum gdn2_mode {
+    GDN2_MODE_FUSED_RECURRENT = 0, /* Gdn2Mode::FusedRecurrent */
+    GDN2_MODE_CHUNK = 1,           /* Gdn2Mode::Chunk */
+} gdn2_mode;
+
+/* Gdn2Config (src/config.rs:23-58).  Option fields: num_v_heads = 0 is
+ * None; has_min_decay = 0 is None. */
+typedef struct gdn2_config {
+    int64_t hidden_size;
+    int64_t num_heads;
+    int64_t head_dim;
+    float expand_v;
+    int64_t num_v_heads;
+    int32_t use_short_conv;
+    int32_t allow_neg_eigval;
+    double norm_eps;
+    int32_t mode; /* gdn2_mode */
+    int64_t chunk_size;
+    int32_t has_min_decay;
+    double min_decay;
+} gdn2_config;
+
+/* Gdn2Config::default() (src/config.rs:114-130). */
+GDN2_API void gdn2_config_default(gdn2_config *cfg);
+
+/* Gdn2Config::validate() (src/config.rs:71-111): GDN2_EINVAL with the
+ * reference's panic message on the first failing check. */
+GDN2_API gdn2_status gdn2_config_validate(const gdn2_config *cfg);
+
+/* hv = num_v_heads or num_heads, head_v_dim = head_dim * expand_v,
+ * kd = num_heads * head_dim, vd = hv * head_v_dim (src/module.rs:113-119).
+ * Any output pointer may be NULL. */
+GDN2_API gdn2_status gdn2_config_dims(const gdn2_config *cfg, int64_t *hv, int64_t *head_v_dim, int64_t *kd,
+                                      int64_t *vd);
+
+/* ------------------------------------------------------------------------
+ * Parameters, by the reference's field names (src/module.rs:93-111):
+ *   q_proj [D, kd]  k_proj [D, kd]  v_proj [D, vd]  f_proj_0 [D, V]
+ *   f_proj_1 [V, kd]  b_proj [D, kd]  w_proj [D, vd]  g_proj_0 [D, V]
+ *   g_proj_1 [V, vd]  g_proj_1_bias [vd]  a_log [H]  dt_bias [kd]
+ *   o_norm_weight [V]  o_proj [vd, D]  q_conv_w [kd, 4]  k_conv_w [kd, 4]
+ *   v_conv_w [vd, 4]  decay_factors [H, K] (present iff min_decay is set)
+ * Linear weights are [in, out] (burn's layout: y = x W).  V = head_v_dim.
+ * ---------------------------------------------------------------------- */
+GDN2_API int gdn2_param_count(void);
+GDN2_API const char *gdn2_param_name(int index); /* NULL outside [0, count) */
+
+/* Number of elements of parameter `name` for `cfg` (0 when the parameter is
+ * absent, i.e. decay_factors without min_decay; -1 for an unknown name);
+ * rows/cols (nullable) receive its 2-D shape, cols = 1 for vectors. */
+GDN2_API int64_t gdn2_param_shape(const gdn2_config *cfg, const char *name, int64_t *rows, int64_t *cols);
+
+/* Host-side initial value of one parameter, drawn from the reference's
+ * initialisers (src/module.rs:121-187): Xavier-uniform with gain 2^-2.5 for
+ * the Linear weights, zero bias, U(-1/2, 1/2) conv weights, A_log ~
+ * U(ln 1, ln 16), dt_bias = dt + ln(1 - e^-dt) with dt = max(e^U(ln 1e-3,
+ * ln 0.1), 1e-4), ones for o_norm_weight, 2 for decay_factors.  The random
+ * stream is a counter-based SplitMix64 of (seed, parameter index, element
+ * index), so the values do not depend on the order of the calls.  burn's
+ * own RNG stream is not reproduced (it cannot be without burn). */
+GDN2_API gdn2_status gdn2_param_init(const gdn2_config *cfg, uint64_t seed, const char *name, float *host,
+                                     int64_t numel);
+
+/* ------------------------------------------------------------------------
+ * The layer.
+ * ---------------------------------------------------------------------- */
+typedef struct gdn2_layer gdn2_layer;
+typedef struct gdn2_state gdn2_state;
+
+/* GatedDeltaNet2::new (src/module.rs:111-190): validates cfg and
+ * initialises every parameter with gdn2_param_init(cfg, seed, ...). */
+GDN2_API gdn2_status gdn2_layer_create(const gdn2_config *cfg, uint64_t seed, gdn2_layer **out);
+GDN2_API void gdn2_layer_destroy(gdn2_layer *layer);
+GDN2_API const gdn2_config *gdn2_layer_config(const gdn2_layer *layer);
+
+/* Copy one parameter from / to host memory (synchronous).  numel must equal
+ * gdn2_param_shape(); an absent parameter is GDN2_EINVAL. */
+GDN2_API gdn2_status gdn2_layer_set_param(gdn2_layer *layer, const char *name, const float *host, int64_t numel);
+GDN2_API gdn2_status gdn2_layer_get_param(const gdn2_layer *layer, const char *name, float *host, int64_t numel);
+
+/* forward_train (src/module.rs:326-375): x [B, T, D] -> out [B, T, D],
+ * starting from S = 0 with no conv cache; the recurrence follows cfg->mode
+ * (Chunk falls back to the per-token scan kernel outside the chunk kernels'
+ * shapes: the same recurrence). */
+GDN2_API gdn2_status gdn2_layer_forward_train_f32(gdn2_layer *layer, const float *x, int64_t batch, int64_t seq_len,
+                                                  float *out, gdn2_stream_t stream);
+
+/* forward(x, &mut state, update_state = true) (src/module.rs:224-316):
+ * T <= 64 tokens use the per-token recurrence (T = 1: the fused decode
+ * kernel), longer inputs cfg->mode.  An empty state (Option::None) starts
+ * from S = 0 with the short conv padded by the first token and becomes
+ * non-empty; the conv caches are replaced only with use_short_conv.
+ * T = 0 is a no-op. */
+GDN2_API gdn2_status gdn2_layer_forward_f32(gdn2_layer *layer, const float *x, int64_t batch, int64_t seq_len,
+                                            gdn2_state *state, float *out, gdn2_stream_t stream);
+
+/* project (src/module.rs:381-495) without the GVA repeat: writes the
+ * kernel inputs q, k, g, b [B, T, H, K], v, w [B, T, HV, V] and the gate
+ * signal [B, T, HV, V] (each contiguous, caller-owned).  `state` (nullable,
+ * not modified) supplies the conv caches when non-empty.  The reference's
+ * [B, HV, T, K] tensors are these with the heads repeated and permuted. */
+GDN2_API gdn2_status gdn2_layer_project_f32(gdn2_layer *layer, const float *x, int64_t batch, int64_t seq_len,
+                                            const gdn2_state *state, float *q, float *k, float *g, float *b,
+                                            float *v, float *w, float *gate, gdn2_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * State: Option<Gdn2State> (src/module.rs:30-63) for one layer and batch.
+ * Tensors: 0 recurrent [B, HV, K, V], 1 conv_q [B, 3, kd], 2 conv_k
+ * [B, 3, kd], 3 conv_v [B, 3, vd] (oldest cached token first).
+ * ---------------------------------------------------------------------- */
+enum { GDN2_STATE_RECURRENT = 0, GDN2_STATE_CONV_Q = 1, GDN2_STATE_CONV_K = 2, GDN2_STATE_CONV_V = 3 };
+
+/* Allocates the state's device buffers; the state starts empty (None). */
+GDN2_API gdn2_status gdn2_state_create(const gdn2_layer *layer, int64_t batch, gdn2_state **out);
+GDN2_API void gdn2_state_destroy(gdn2_state *state);
+/* Some(Gdn2State::zeros(..)) (src/module.rs:49-62); synchronous. */
+GDN2_API gdn2_status gdn2_state_set_zeros(gdn2_state *state);
+/* Back to None. */
+GDN2_API void gdn2_state_clear(gdn2_state *state);
+GDN2_API int gdn2_state_is_some(const gdn2_state *state);
+GDN2_API int64_t gdn2_state_batch(const gdn2_state *state);
+/* Element count of tensor `which`, and its current device buffer (the conv
+ * caches alternate between two buffers, so the pointer changes after each
+ * forward call). */
+GDN2_API int64_t gdn2_state_numel(const gdn2_state *state, int which);
+GDN2_API float *gdn2_state_tensor(gdn2_state *state, int which);
+/* Synchronous host copies; a write makes the state non-empty (the tensors
+ * not written keep their values, zeros for a fresh state). */
+GDN2_API gdn2_status gdn2_state_read(const gdn2_state *state, int which, float *host, int64_t numel);
+GDN2_API gdn2_status gdn2_state_write(gdn2_state *state, int which, const float *host, int64_t numel);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN2_LAYER_H_ */

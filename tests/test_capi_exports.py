@@ -1,6 +1,7 @@
-"""The C-ABI library loads and exports every entry point include/gdn2.h
+"""The C-ABI library loads and exports every entry point include/*.h
 declares (no GPU needed; no compute calls)."""
 import ctypes
+import glob
 import os
 import re
 
@@ -8,14 +9,16 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def declared_symbols():
-    src = open(os.path.join(ROOT, "include", "gdn2.h")).read()
+    src = "".join(open(p).read() for p in sorted(glob.glob(os.path.join(ROOT, "include", "*.h"))))
     return sorted(set(re.findall(r"GDN2_API\s+[\w\s\*]*?\b(gdn2_\w+)\s*\(", src)))
 
 
 def test_header_declares_the_boundary():
     syms = declared_symbols()
     for s in ("gdn2_recurrent_step_f32", "gdn2_recurrent_fwd_f32", "gdn2_chunk_fwd_f32",
-              "gdn2_chunk_workspace_bytes", "gdn2_decode_fused_f32", "gdn2_hip_available", "gdn2_last_error"):
+              "gdn2_chunk_workspace_bytes", "gdn2_decode_fused_f32", "gdn2_hip_available", "gdn2_last_error",
+              "gdn2_config_validate", "gdn2_layer_create", "gdn2_layer_forward_f32", "gdn2_layer_forward_train_f32",
+              "gdn2_state_create"):
         assert s in syms
 
 
