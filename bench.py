@@ -4,16 +4,19 @@
 Headline workload (`value`): chunked prefill of the default layer,
 hidden 2048, 16 heads, head_dim 128, expand_v 1, chunk 64, x ~ N(0,1) of
 shape [8, 4096, 2048] through seeded random-init weights (the reference's
-initialisers, src/module.rs:121-187).  One step = one chunked forward of
-the recurrence core (chunk-intra + chunk-inter kernels) over all
-8 x 16 x 4096 token-heads, inputs already resident in HBM.  The projected
-operands (q, k, g, b, v, w) are produced once, outside the timed region.
+initialisers, src/module.rs:121-187, drawn by gdn2_param_init).  One step =
+one chunked forward of the recurrence core (chunk-intra + chunk-inter
+kernels) over all 8 x 16 x 4096 token-heads, inputs already resident in
+HBM.  The projected operands (q, k, g, b, v, w) come from the layer's own
+project() once, outside the timed region.
 
-Also reported: B = 64 fused decode (short conv + gates + L2 norm + step +
-gated RMSNorm per token), timed over 256 tokens with 5 rotating state
-buffers (335 MB, larger than the 256 MB MALL; the kernel's time does not
-depend on the state values), and the CPU oracle on a bounded sample of the
-same prefill workload.
+Also reported: the whole layer (rocBLAS Linear layers + kernels) for the
+same prefill; B = 64 fused decode (short conv + gates + L2 norm + step +
+gated RMSNorm per token), the kernel alone over 256 tokens with 5 rotating
+state buffers (335 MB, larger than the 256 MB MALL; the kernel's time does
+not depend on the state values) and the whole layer over a 2048-token
+prefill then 256 single-token steps; and the CPU oracle on the same prefill
+workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -25,7 +28,7 @@ import sys
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
-for _p in (ROOT, os.path.join(ROOT, "burn-gdn2_amd"), os.path.join(ROOT, "tests")):
+for _p in (ROOT, os.path.join(ROOT, "burn-gdn2_amd")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
@@ -46,40 +49,11 @@ def parse():
     ap.add_argument("--decode-rotate", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--cpu-batch", type=int, default=2)
+    ap.add_argument("--cpu-batch", type=int, default=8)
+    ap.add_argument("--no-layer", action="store_true")
+    ap.add_argument("--layer-steps", type=int, default=5)
+    ap.add_argument("--decode-prefill", type=int, default=2048)
     return ap.parse_args()
-
-
-def project_inputs(torch, W, x, cfg):
-    """Layer projections of x (src/module.rs:381-495) on the device, in f32,
-    as input preparation: returns q, k, g, b [B, H, T, K] and v, w
-    [B, HV, T, V] contiguous."""
-    B, T, D = x.shape
-    H, K, HV, V = cfg.num_heads, cfg.head_dim, cfg.hv, cfg.v_head
-    x2 = x.reshape(B * T, D)
-
-    def conv_silu(raw, wconv):
-        r = raw.reshape(B, T, -1)
-        xp = torch.cat([r[:, :1].expand(B, 3, r.shape[2]), r], dim=1)
-        y = sum(xp[:, i:i + T] * wconv[:, i] for i in range(4))
-        return torch.nn.functional.silu(y)
-
-    q = conv_silu(x2 @ W["q_proj"], W["q_conv_w"])
-    k = conv_silu(x2 @ W["k_proj"], W["k_conv_w"])
-    v = conv_silu(x2 @ W["v_proj"], W["v_conv_w"])
-    f = (x2 @ W["f_proj_0"]) @ W["f_proj_1"]
-    a = torch.exp(W["a_log"]).repeat_interleave(K)
-    g = (-a * torch.nn.functional.softplus(f + W["dt_bias"])).reshape(B, T, -1)
-    b = torch.sigmoid(x2 @ W["b_proj"]).reshape(B, T, -1)
-    w = torch.sigmoid(x2 @ W["w_proj"]).reshape(B, T, -1)
-
-    def heads(t, n, d):
-        return t.reshape(B, T, n, d).permute(0, 2, 1, 3).contiguous()
-
-    q, k = heads(q, H, K), heads(k, H, K)
-    q = q / torch.sqrt((q * q).sum(-1, keepdim=True) + 1e-6)
-    k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)
-    return q, k, heads(v, HV, V), heads(g, H, K), heads(b, H, K), heads(w, HV, V)
 
 
 def load_traffic(name):
@@ -91,26 +65,27 @@ def load_traffic(name):
         return json.load(fh)
 
 
-def bench_prefill(torch, gdn2_amd, args, dev):
-    from gdn2_testutil import Cfg, init_weights
-
-    cfg = Cfg(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0, chunk_size=64, mode="chunk")
+def bench_prefill(torch, G, args, dev):
+    """The recurrence core at the layer's own layout: the projected operands
+    come from GatedDeltaNet2.project (q, k, g, b [B, T, H, K] and v, w
+    [B, T, HV, V], read through strides), prepared once outside the timed
+    region; then the whole layer (forward_train) for comparison."""
+    cfg = G.Gdn2Config(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0, mode="chunk", chunk_size=64)
+    layer = G.GatedDeltaNet2(cfg, seed=1337)
     B, T, H, K, V, C = args.batch, args.seq, cfg.num_heads, cfg.head_dim, cfg.v_head, 64
-    Wn = init_weights(cfg, seed=1337)
-    W = {n: torch.from_numpy(a).to(dev) for n, a in Wn.items() if a is not None}
     gen = torch.Generator(device=dev)
     gen.manual_seed(42)
     x = torch.randn((B, T, cfg.hidden_size), generator=gen, device=dev, dtype=torch.float32)
-    with torch.no_grad():
-        q, k, v, g, b, w = project_inputs(torch, W, x, cfg)
-    del x
+    P = layer.project(x)
+    q, k, g, b = (P[n].permute(0, 2, 1, 3) for n in ("q", "k", "g", "b"))
+    v, w = (P[n].permute(0, 2, 1, 3) for n in ("v", "w"))
     state = torch.zeros((B, H, K, V), device=dev)
-    out = torch.empty((B, H, T, V), device=dev)
+    out = torch.empty((B, T, H, V), device=dev).permute(0, 2, 1, 3)
     scale = K ** -0.5
     from gdn2_amd import _capi as CA
     from gdn2_amd.ops import _stream, chunk_args
 
-    need = gdn2_amd.chunk_workspace_bytes(q, k, v, g, b, w, state, out, scale, C)
+    need = G.chunk_workspace_bytes(q, k, v, g, b, w, state, out, scale, C)
     ws = torch.empty(need, dtype=torch.uint8, device=dev)
     cargs = chunk_args(q, k, v, g, b, w, state, out, scale, C, ws)
     import ctypes
@@ -155,34 +130,55 @@ def bench_prefill(torch, gdn2_amd, args, dev):
             "unit": "TFLOP/s", "frac": kernels[dom]["frac_f32_mfma"],
             "traffic": None if tr is None else tr.get("hbm_bytes_per_launch"),
             "per_launch_gflop": kernels[dom]["gflop"]}
-    host = {"q": q[:args.cpu_batch].cpu().numpy(), "k": k[:args.cpu_batch].cpu().numpy(),
-            "v": v[:args.cpu_batch].cpu().numpy(), "g": g[:args.cpu_batch].cpu().numpy(),
-            "b": b[:args.cpu_batch].cpu().numpy(), "w": w[:args.cpu_batch].cpu().numpy()}
-    del q, k, v, g, b, w, ws
+    nb = min(args.cpu_batch, B)
+    host = {n: t[:nb].contiguous().cpu().numpy() for n, t in (("q", q), ("k", k), ("v", v), ("g", g), ("b", b),
+                                                                ("w", w))}
+    del q, k, v, g, b, w, ws, P, out, state
+    lay = None
+    if not args.no_layer:
+        lay = time_layer(torch, lambda: layer.forward_train(x), args.layer_steps, tokens)
+        lay["gemm_tflop"] = 2 * tokens * cfg.hidden_size * (3 * cfg.kd + 2 * cfg.vd + 2 * V) / 1e12 + \
+            2 * tokens * V * (cfg.kd + cfg.vd) / 1e12 + 2 * tokens * cfg.vd * cfg.hidden_size / 1e12
+    layer.close()
     return {"tokens": tokens, "ms_per_step": ms_per_step, "value": tokens / (ms_per_step / 1e3),
-            "kernels": kernels, "roofline": roof, "host_sample": host, "scale": scale, "cfg": cfg}
+            "kernels": kernels, "roofline": roof, "host_sample": host, "scale": scale, "layer": lay}
 
 
-def bench_decode(torch, gdn2_amd, args, dev):
-    from gdn2_testutil import Cfg, init_weights
+def time_layer(torch, fn, steps, tokens):
+    """Whole-layer forward calls (Linear GEMMs + kernels) timed with events."""
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"ms_per_step": ms, "tokens_per_s": tokens / (ms / 1e3), "steps": steps}
 
-    cfg = Cfg(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0)
+
+def bench_decode(torch, G, args, dev):
+    """Config 3: the default layer (FusedRecurrent, short conv) at B = 64.
+    (a) The fused decode kernel alone over 256 tokens whose raw projections
+    are prepared up front, with rotating state buffers (larger than the
+    256 MB MALL; the kernel's time does not depend on the state values).
+    (b) The whole layer: forward() over a 2048-token prefill, then 256
+    single-token forward() calls carrying the Gdn2State."""
+    cfg = G.Gdn2Config(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0)
     Bd, H, K, V = args.decode_batch, cfg.num_heads, cfg.head_dim, cfg.v_head
     kd, vd = cfg.kd, cfg.vd
-    Wn = init_weights(cfg, seed=1337)
+    Wn = G.init_params(cfg, seed=1337)
     W = {n: torch.from_numpy(a).to(dev) for n, a in Wn.items() if a is not None}
     gen = torch.Generator(device=dev)
     gen.manual_seed(43)
     steps = args.decode_steps
-    # raw projections of the generated tokens (Linear outputs), prepared up front
     x = torch.randn((steps, Bd, cfg.hidden_size), generator=gen, device=dev)
     with torch.no_grad():
         raw = {"q_raw": x @ W["q_proj"], "k_raw": x @ W["k_proj"], "v_raw": x @ W["v_proj"],
                "f_raw": (x @ W["f_proj_0"]) @ W["f_proj_1"], "b_raw": x @ W["b_proj"], "w_raw": x @ W["w_proj"],
                "gate": (x @ W["g_proj_0"]) @ W["g_proj_1"] + W["g_proj_1_bias"]}
-    del x
     nrot = max(1, args.decode_rotate)
-    # state as after a prefill: a random symmetric-ish bounded state
     states = [torch.randn((Bd, H, K, V), generator=gen, device=dev) * 0.05 for _ in range(nrot)]
     conv = [tuple(torch.randn((Bd, 3, n), generator=gen, device=dev) for n in (kd, kd, vd)) for _ in range(2)]
     out = torch.empty((Bd, vd), device=dev)
@@ -193,7 +189,6 @@ def bench_decode(torch, gdn2_amd, args, dev):
     from gdn2_amd import _capi as CA
     from gdn2_amd.ops import _stream, decode_args
 
-    # argument blocks built up front: the timed loop is one C call per token
     blocks = [decode_args({n: a[t] for n, a in raw.items()}, params, states[t % nrot], conv[t % 2],
                           conv[(t + 1) % 2], out, num_heads=H, num_v_heads=H, head_dim=K, head_v_dim=V,
                           scale=K ** -0.5, norm_eps=cfg.norm_eps) for t in range(steps)]
@@ -215,10 +210,38 @@ def bench_decode(torch, gdn2_amd, args, dev):
     param_bytes = (4 * (2 * kd + vd) + H + kd + V) * 4
     bytes_step = state_bytes + io_bytes + param_bytes
     gbs = bytes_step / (ms / 1e3) / 1e9
-    return {"batch": Bd, "tokens_per_s": Bd / (ms / 1e3), "ms_per_token_step": ms, "bytes_per_step": bytes_step,
-            "core_bytes_per_step": 2 * Bd * H * K * V * 4 + Bd * (4 * H * K + 3 * H * V) * 4,
-            "achieved_GBs": gbs, "peak_GBs": PEAK_HBM_GBS, "frac_hbm": gbs / PEAK_HBM_GBS,
-            "rotating_state_buffers": nrot, "kernel": "gdn2_decode_fused_f32"}
+    res = {"batch": Bd, "tokens_per_s": Bd / (ms / 1e3), "ms_per_token_step": ms, "bytes_per_step": bytes_step,
+           "core_bytes_per_step": 2 * Bd * H * K * V * 4 + Bd * (4 * H * K + 3 * H * V) * 4,
+           "achieved_GBs": gbs, "peak_GBs": PEAK_HBM_GBS, "frac_hbm": gbs / PEAK_HBM_GBS,
+           "rotating_state_buffers": nrot, "kernel": "gdn2_decode_fused_f32"}
+    del blocks, states, conv, raw, x, W
+    if not args.no_layer:
+        layer = G.GatedDeltaNet2(cfg, seed=1337)
+        xp = torch.randn((Bd, args.decode_prefill, cfg.hidden_size), generator=gen, device=dev)
+        xs = torch.randn((steps, Bd, 1, cfg.hidden_size), generator=gen, device=dev)
+        torch.cuda.synchronize()
+        e0.record()
+        _, st = layer.forward(xp)
+        e1.record()
+        torch.cuda.synchronize()
+        pre_ms = e0.elapsed_time(e1)
+        del xp
+        for t in range(min(4, steps)):  # warm-up, then restart from the prefill state is not needed for timing
+            _, st = layer.forward(xs[t], st)
+        torch.cuda.synchronize()
+        e0.record()
+        for t in range(steps):
+            _, st = layer.forward(xs[t], st)
+        e1.record()
+        torch.cuda.synchronize()
+        lms = e0.elapsed_time(e1) / steps
+        res["layer"] = {"prefill_tokens": Bd * args.decode_prefill, "prefill_ms": pre_ms,
+                        "prefill_tokens_per_s": Bd * args.decode_prefill / (pre_ms / 1e3),
+                        "decode_ms_per_token_step": lms, "decode_tokens_per_s": Bd / (lms / 1e3),
+                        "weight_bytes_per_step": sum(a.nbytes for a in Wn.values() if a is not None)}
+        del st
+        layer.close()
+    return res
 
 
 def cpu_baseline(pre, args):
@@ -263,14 +286,14 @@ def main():
         sys.exit(2)
     import torch
 
-    import gdn2_amd
+    import gdn2_amd as G
 
     torch.backends.cuda.matmul.allow_tf32 = False
     dev = torch.device("cuda:0")
-    if not gdn2_amd.hip_available():
+    if not G.hip_available():
         raise SystemExit("no gfx950 device: bench.py needs an MI355X")
-    pre = bench_prefill(torch, gdn2_amd, args, dev)
-    dec = None if args.no_decode else bench_decode(torch, gdn2_amd, args, dev)
+    pre = bench_prefill(torch, G, args, dev)
+    dec = None if args.no_decode else bench_decode(torch, G, args, dev)
     cpu = None if args.no_cpu else cpu_baseline(pre, args)
     line = {
         "metric": METRIC,
@@ -294,6 +317,7 @@ def main():
         "kernels": pre["kernels"],
         "decode": dec,
         "decode_tokens_per_s": None if dec is None else dec["tokens_per_s"],
+        "layer": {"prefill": pre["layer"], "decode": None if dec is None else dec.get("layer")},
     }
     print(json.dumps(line), flush=True)
 

@@ -58,8 +58,8 @@ def test_validate_accepts_the_benchmark_configs():
 
 CONFIGS = {
     "C1": G.Gdn2Config(hidden_size=256, num_heads=4, head_dim=64, mode="chunk"),
-    "C2": G.Gdn2Config(mode="chunk", use_short_conv=False),
-    "C3": G.Gdn2Config(use_short_conv=False),
+    "C2": G.Gdn2Config(mode="chunk"),
+    "C3": G.Gdn2Config(),
     "C4": G.Gdn2Config(num_heads=8, num_v_heads=16, expand_v=2.0, allow_neg_eigval=True, min_decay=0.9, mode="chunk"),
     "C5": G.Gdn2Config(mode="chunk", chunk_size=128),
 }
