@@ -53,6 +53,13 @@ def parse():
     ap.add_argument("--no-layer", action="store_true")
     ap.add_argument("--layer-steps", type=int, default=5)
     ap.add_argument("--decode-prefill", type=int, default=2048)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="end with a 1 GiB device-to-device copy (reference kernel for HBM counters)")
+    ap.add_argument("--stats-summary", metavar="KERNEL_STATS_CSV",
+                    help="host only: print a rocprofv3 --stats kernel table as markdown and exit")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="host only: per-launch HBM bytes from two rocprofv3 --pmc runs (FETCH_SIZE, "
+                         "WRITE_SIZE) of this script with --copy-calibration; writes profiles/*_traffic.json")
     return ap.parse_args()
 
 
@@ -276,8 +283,83 @@ def _cpu_model():
     return "unknown"
 
 
+COPY_BYTES = 1 << 30
+KERNELS = {"chunk_intra": "chunk_intra_kernel", "chunk_inter": "chunk_inter_kernel",
+           "decode": "decode_fused_kernel"}
+
+
+def _short(name):
+    import re
+
+    m = re.search(r"gdn2::\(anonymous namespace\)::(\w+(<[^>]*>)?)", name)
+    if m:
+        return m.group(1)
+    return name.split("(")[0].replace("void ", "")[:70]
+
+
+def stats_summary(path):
+    import csv
+
+    rows = list(csv.DictReader(open(path)))
+    print("| kernel | calls | avg us | total us | % of GPU time |")
+    print("|---|---|---|---|---|")
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:12]:
+        print(f"| `{_short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+              f"{float(r['TotalDurationNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
+
+
+def traffic_summary(fetch_csv, write_csv):
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) per kernel, scaled so that
+    the 1 GiB copy reads and writes 1 GiB."""
+    import csv
+
+    def per_kernel(path, counter):
+        acc = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            acc.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]) * 1024.0)
+        return acc
+
+    fetch, write = per_kernel(fetch_csv, "FETCH_SIZE"), per_kernel(write_csv, "WRITE_SIZE")
+
+    def copy_bytes(acc):
+        # the largest single dispatch of a copy kernel is the 1 GiB calibration copy
+        best = 0.0
+        for name, vals in acc.items():
+            if "copy" in name.lower() or "elementwise" in name:
+                best = max(best, max(vals))
+        return best
+
+    f_fac = COPY_BYTES / copy_bytes(fetch)
+    w_fac = COPY_BYTES / copy_bytes(write)
+    print(f"calibration: FETCH_SIZE x {f_fac:.3f}, WRITE_SIZE x {w_fac:.3f} (1 GiB copy)")
+    print("| kernel | dispatches | HBM read GB/launch | HBM write GB/launch | total GB/launch |")
+    print("|---|---|---|---|---|")
+    out = {}
+    for key, frag in KERNELS.items():
+        fv = [v for n, vals in fetch.items() if frag in n for v in vals]
+        wv = [v for n, vals in write.items() if frag in n for v in vals]
+        if not fv or not wv:
+            continue
+        rd, wr = sum(fv) / len(fv) * f_fac, sum(wv) / len(wv) * w_fac
+        out[key] = {"hbm_bytes_per_launch": rd + wr, "read_bytes": rd, "write_bytes": wr,
+                    "dispatches": len(fv), "fetch_factor": f_fac, "write_factor": w_fac}
+        print(f"| `{key}` | {len(fv)} | {rd / 1e9:.3f} | {wr / 1e9:.3f} | {(rd + wr) / 1e9:.3f} |")
+        suffix = "b64_decode" if key == "decode" else "b8_t4096"
+        with open(os.path.join(ROOT, "profiles", f"{key}_{suffix}_traffic.json"), "w") as fh:
+            json.dump(out[key], fh, indent=1)
+    return out
+
+
 def main():
     args = parse()
+    if args.stats_summary:
+        stats_summary(args.stats_summary)
+        return
+    if args.traffic_summary:
+        traffic_summary(*args.traffic_summary)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: the GDN-2 path shards over (batch, value head) with no "
@@ -295,6 +377,12 @@ def main():
     pre = bench_prefill(torch, G, args, dev)
     dec = None if args.no_decode else bench_decode(torch, G, args, dev)
     cpu = None if args.no_cpu else cpu_baseline(pre, args)
+    if args.copy_calibration:
+        src = torch.empty(COPY_BYTES // 4, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     line = {
         "metric": METRIC,
         "value": pre["value"],

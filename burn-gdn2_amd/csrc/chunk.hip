@@ -105,22 +105,28 @@ __device__ __forceinline__ floatx4 exp2v(floatx4 x) {
 }
 
 template <int K, int V>
-__global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
+__global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
+    constexpr int NW = 8; // waves per workgroup; two workgroups per CU = four waves per SIMD
     constexpr int KP = K + 4, CP = C + 4;
-    constexpr int NKT = K / 16, NVT = V / 16, NTOT = NKT + NVT, NTW = NTOT / 4;
-    static_assert(NTOT % 4 == 0, "K + V must be a multiple of 64");
-    constexpr int NSEG = 256 / K, RPS = C / NSEG;
-    static_assert(256 % K == 0 && C % NSEG == 0, "K");
-    constexpr int KF4 = C * K / 4 / 256; // float4 of the chunk's k per lane
+    constexpr int NKT = K / 16, NVT = V / 16, NTOT = NKT + NVT;
+    static_assert(NKT % 2 == 0 && NKT <= NW, "K in {32, 64, 96, 128}");
+    constexpr int NTW = (NTOT + NW - 1) / NW; // column tiles per wave in the solve (nt = wave + NW u)
+    constexpr int NKH = NKT / 2;              // 16-channel blocks per wave in the score products
+    constexpr int NSEG = 512 / K, RPS = C / NSEG;
+    static_assert(512 % K == 0 && C % NSEG == 0, "K");
+    constexpr int KF4 = C * K / 4 / 512; // float4 of the chunk's k per lane
     constexpr int RSZ = (C * KP > 2 * C * CP) ? C * KP : 2 * C * CP;
 
+    // Region A: G (phases 1-2), then b k exp(G) (staging for the solve).
     __shared__ __attribute__((aligned(16))) float sG[C][KP];
-    // k (phases 1-2), then A_qk | A_kk (phases 2-4)
+    // Region B: k (phases 1-2), then q exp(G) (staging), then A_qk | A_kk (phases 3-4).
     __shared__ __attribute__((aligned(16))) float sR[RSZ];
     __shared__ __attribute__((aligned(16))) float sAinv[NT][16][20];
     __shared__ float sTot[NSEG][K];
     __shared__ uint32_t sMask[NT][K / 32];
     float(*sK)[KP] = reinterpret_cast<float(*)[KP]>(sR);
+    float(*sQG)[KP] = reinterpret_cast<float(*)[KP]>(sR);
+    float(*sBKG)[KP] = sG;
     float(*sAqk)[CP] = reinterpret_cast<float(*)[CP]>(sR);
     float(*sAkk)[CP] = reinterpret_cast<float(*)[CP]>(sR + C * CP);
 
@@ -138,6 +144,7 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
     const int64_t vofs = (int64_t)bi * p.svb + (int64_t)hv * p.svh + (int64_t)t0 * svt;
     const float *qc = p.q + kofs, *kc = p.k + kofs, *gc = p.g + kofs, *bc = p.b + kofs;
     const float *vc = p.v + vofs, *wc = p.w + vofs;
+    const size_t cid = (size_t)ci;
 
     // 1. k -> sK; G = cumsum_t g per channel -> sG in log2 units.  Rows past
     //    the end of a ragged last chunk are zero (src/forward.rs:94-99).
@@ -145,7 +152,7 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
         floatx4 kreg[KF4];
 #pragma unroll
         for (int i = 0; i < KF4; ++i) {
-            const int f = i * 256 + tid, row = f / (K / 4), c4 = f % (K / 4);
+            const int f = i * 512 + tid, row = f / (K / 4), c4 = f % (K / 4);
             kreg[i] = ld4v(kc, sqt, row, cv, 4 * c4);
         }
         const int c = tid % K, seg = tid / K;
@@ -162,7 +169,7 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
         if (tid < NT * (K / 32)) (&sMask[0][0])[tid] = 0u;
 #pragma unroll
         for (int i = 0; i < KF4; ++i) {
-            const int f = i * 256 + tid, row = f / (K / 4), c4 = f % (K / 4);
+            const int f = i * 512 + tid, row = f / (K / 4), c4 = f % (K / 4);
             *reinterpret_cast<floatx4 *>(&sK[row][4 * c4]) = kreg[i];
         }
         __syncthreads();
@@ -172,23 +179,49 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
         for (int i = 0; i < RPS; ++i) sG[seg * RPS + i][c] = (vals[i] + off) * kLog2e;
         __syncthreads();
     }
-    for (int idx = tid; idx < NT * K; idx += 256) {
+    // Kd^T = (k exp(G_last - G))^T as A-operand fragments (kb, tt): lane
+    // (g, r) holds Kd[16 tt + 4 g + j][16 kb + r]; and exp(G_last).  k comes
+    // from LDS, so the chunk's k is read from memory once.
+    {
+        floatx4 *Kf = reinterpret_cast<floatx4 *>(p.ws_kdt) + cid * (C * K / 4);
+        constexpr int KDF = NKT * NT / NW; // fragments per wave
+#pragma unroll
+        for (int j = 0; j < KDF; ++j) {
+            const int f = wave + NW * j, kb = f / NT, tt = f % NT, ch = 16 * kb + lr;
+            const float gl = sG[C - 1][ch];
+            floatx4 val;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * tt + 4 * lg + i;
+                val[i] = sK[t][ch] * fast_exp2(gl - sG[t][ch]);
+            }
+            st_stream(Kf + f * 64 + lane, val);
+        }
+        if (tid < K) p.ws_gam[cid * K + tid] = fast_exp2(sG[C - 1][tid]);
+    }
+    for (int idx = tid; idx < NT * K; idx += 512) {
         const int pt = idx / K, c = idx % K;
         const float gb = pt ? sG[16 * pt - 1][c] : 0.f;
         if (gb - sG[16 * pt + 15][c] > kSafeSpan) atomicOr(&sMask[pt][c >> 5], 1u << (c & 31));
     }
     __syncthreads();
 
-    // 2. A_qk (waves 0, 1) and A_kk (waves 2, 3); each wave takes the two
-    //    row tiles {h, NT-1-h} so that all waves do the same number of blocks.
+    // 2. A_qk (waves 0-3) and A_kk (waves 4-7).  Wave (mat, h, kh) takes the
+    //    row tiles {h, NT-1-h}, so that all waves do the same number of
+    //    blocks, over the channel half kh; the two halves are summed through
+    //    LDS below.  The row operands, with exp(G) applied, are kept for the
+    //    solve: q exp(G) (A_qk waves) and b k exp(G) (A_kk waves).
+    floatx4 stR[NT], stQ[NT]; // the solve's key-column operands (staged below)
     {
-        const int mat = wave >> 1, half = wave & 1;
-        floatx4 araw[2][NKT];
+        const int mat = wave >> 2, half = (wave >> 1) & 1, kh = wave & 1;
+        const int m0 = kh * NKH;
+        floatx4 araw[2][NKH];
 #pragma unroll
         for (int pi = 0; pi < 2; ++pi) {
             const int row = 16 * (pi ? (NT - 1 - half) : half) + lr;
 #pragma unroll
-            for (int m = 0; m < NKT; ++m) araw[pi][m] = ld4v(mat == 0 ? qc : bc, sqt, row, cv, 16 * m + 4 * lg);
+            for (int m = 0; m < NKH; ++m)
+                araw[pi][m] = ld4v(mat == 0 ? qc : bc, sqt, row, cv, 16 * (m0 + m) + 4 * lg);
         }
         floatx4 acc[2][NT];
 #pragma unroll
@@ -200,8 +233,8 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
 #pragma unroll
             for (int q = 0; q < NT; ++q) acc[pi][q] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int m = 0; m < NKT; ++m) {
-                const int c0 = 16 * m + 4 * lg;
+            for (int m = 0; m < NKH; ++m) {
+                const int c0 = 16 * (m0 + m) + 4 * lg;
                 const floatx4 gr = *reinterpret_cast<const floatx4 *>(&sG[row][c0]);
                 const floatx4 gb = *reinterpret_cast<const floatx4 *>(&sG[brow][c0]) * bmul;
                 const floatx4 kr = *reinterpret_cast<const floatx4 *>(&sK[row][c0]);
@@ -210,7 +243,7 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
                 const uint32_t mw = sMask[pt][c0 >> 5] >> (c0 & 31);
 #pragma unroll
                 for (int q = 0; q < NT; ++q) {
-                    if (q <= pt) {
+                    if (q <= pt && (pi == 1 || q < NT / 2)) { // pi = 0: row tile h < NT/2
                         const int srow = 16 * q + lr;
                         const floatx4 gs = *reinterpret_cast<const floatx4 *>(&sG[srow][c0]);
                         floatx4 bv = *reinterpret_cast<const floatx4 *>(&sK[srow][c0]) * exp2v(gb - gs);
@@ -227,15 +260,15 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
                 }
             }
         }
-        // Diagonal blocks, channels outside the safe span: exact pairwise terms
-        // (after both tiles' products, so no row load is outstanding here).
+        // Diagonal blocks, channels (of this half) outside the safe span: exact
+        // pairwise terms (after the products, so no row load is outstanding here).
 #pragma unroll
         for (int pi = 0; pi < 2; ++pi) {
             const int pt = pi ? (NT - 1 - half) : half;
 #pragma unroll
             for (int q = 0; q < NT; ++q) {
-                if (q == pt) {
-                    for (int wd = 0; wd < K / 32; ++wd) {
+                if (q == pt && (pi == 1 || q < NT / 2)) {
+                    for (int wd = kh * (K / 64); wd < (kh + 1) * (K / 64); ++wd) {
                         uint32_t mw = sMask[pt][wd];
                         while (mw) {
                             const int c = wd * 32 + __builtin_ctz(mw);
@@ -257,24 +290,94 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
                 }
             }
         }
-        __syncthreads(); // every wave is done with sK: the region becomes A_qk | A_kk
+        // The solve's row operands x exp(G_r) (x = q, or b k), from a second
+        // read of the rows (recent, so served by the caches) rather than
+        // registers held across the products.
+        floatx4 stg[2][NKH];
+        {
+            floatx4 ar2[2][NKH];
 #pragma unroll
-        for (int pi = 0; pi < 2; ++pi) {
-            const int pt = pi ? (NT - 1 - half) : half;
+            for (int pi = 0; pi < 2; ++pi) {
+                const int row = 16 * (pi ? (NT - 1 - half) : half) + lr;
 #pragma unroll
-            for (int q = 0; q < NT; ++q) {
-                if (q <= pt) {
+                for (int m = 0; m < NKH; ++m)
+                    ar2[pi][m] = ld4v(mat == 0 ? qc : bc, sqt, row, cv, 16 * (m0 + m) + 4 * lg);
+            }
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int r = 4 * lg + i;
-                        float val = acc[pi][q][i];
-                        if (mat == 0) {
-                            val *= p.scale;
-                            if (q == pt && r < lr) val = 0.f;
-                            sAqk[16 * pt + r][16 * q + lr] = val;
-                        } else {
-                            if (q == pt && r <= lr) val = 0.f;
-                            sAkk[16 * pt + r][16 * q + lr] = val;
+            for (int pi = 0; pi < 2; ++pi) {
+                const int row = 16 * (pi ? (NT - 1 - half) : half) + lr;
+#pragma unroll
+                for (int m = 0; m < NKH; ++m) {
+                    const int c0 = 16 * (m0 + m) + 4 * lg;
+                    const floatx4 gr = *reinterpret_cast<const floatx4 *>(&sG[row][c0]);
+                    const floatx4 kr = *reinterpret_cast<const floatx4 *>(&sK[row][c0]);
+                    stg[pi][m] = ar2[pi][m] * (mat == 1 ? kr : floatx4{1.f, 1.f, 1.f, 1.f}) * exp2v(gr);
+                }
+            }
+        }
+        __syncthreads(); // sK and sG are dead: stage the row operands in their place
+        {
+            float(*dst)[KP] = mat == 0 ? sQG : sBKG;
+#pragma unroll
+            for (int pi = 0; pi < 2; ++pi) {
+                const int row = 16 * (pi ? (NT - 1 - half) : half) + lr;
+#pragma unroll
+                for (int m = 0; m < NKH; ++m)
+                    *reinterpret_cast<floatx4 *>(&dst[row][16 * (m0 + m) + 4 * lg]) = stg[pi][m];
+            }
+        }
+        __syncthreads();
+        // The solve's owner of key column tile nt = wave reads its columns in
+        // accumulator layout (rows 4 g + i, column r of each 16 x 16 tile).
+        if (wave < NKT) {
+            const int col = 16 * wave + lr;
+#pragma unroll
+            for (int tp = 0; tp < NT; ++tp)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    stR[tp][i] = sBKG[16 * tp + 4 * lg + i][col];
+                    stQ[tp][i] = sQG[16 * tp + 4 * lg + i][col];
+                }
+        }
+        __syncthreads(); // the staging is consumed: region B becomes A_qk | A_kk
+        // channel half 1 leaves its partial sums, half 0 completes them
+        if (kh == 1) {
+#pragma unroll
+            for (int pi = 0; pi < 2; ++pi) {
+                const int pt = pi ? (NT - 1 - half) : half;
+#pragma unroll
+                for (int q = 0; q < NT; ++q)
+                    if (q <= pt && (pi == 1 || q < NT / 2))
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            float *dst = mat == 0 ? &sAqk[16 * pt + 4 * lg + i][16 * q + lr]
+                                                  : &sAkk[16 * pt + 4 * lg + i][16 * q + lr];
+                            *dst = acc[pi][q][i];
+                        }
+            }
+        }
+        __syncthreads();
+        if (kh == 0) {
+#pragma unroll
+            for (int pi = 0; pi < 2; ++pi) {
+                const int pt = pi ? (NT - 1 - half) : half;
+#pragma unroll
+                for (int q = 0; q < NT; ++q) {
+                    if (q <= pt && (pi == 1 || q < NT / 2)) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int r = 4 * lg + i;
+                            if (mat == 0) {
+                                float *dst = &sAqk[16 * pt + r][16 * q + lr];
+                                float val = (acc[pi][q][i] + *dst) * p.scale;
+                                if (q == pt && r < lr) val = 0.f;
+                                *dst = val;
+                            } else {
+                                float *dst = &sAkk[16 * pt + r][16 * q + lr];
+                                float val = acc[pi][q][i] + *dst;
+                                if (q == pt && r <= lr) val = 0.f;
+                                *dst = val;
+                            }
                         }
                     }
                 }
@@ -300,40 +403,37 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
     __syncthreads();
 
     // 4. Blocked solve of (I + A_kk) [W | U] = [b k exp(G) | w v] and
-    //    Y = A_qk [W | U]; wave w owns column tiles w, w+4, ... of [W | U].
-    //    Outputs go to the workspace in MFMA fragment order (one 1 KB block
-    //    of 64 lanes x float4 per 16x16 tile) so that every store here and
-    //    every load in chunk-inter is a contiguous 16-byte access per lane:
+    //    Y = A_qk [W | U]; wave w owns column tiles w, w + 8, ... of [W | U]
+    //    (key columns first, whose right-hand sides were staged above; the
+    //    value columns' w, v rows of tile p+1 are loaded while tile p is
+    //    solved).  Outputs go to the workspace in MFMA fragment order (one
+    //    1 KB block of 64 lanes x float4 per 16x16 tile) so that every store
+    //    here and every load in chunk-inter is a contiguous 16-byte access per
+    //    lane:
     //      W, M : A-operand fragments (lane (g, r) holds rows r, cols 4g..4g+3)
     //      U, P : accumulator fragments (lane (g, c) holds rows 4g..4g+3, col c)
-    //    The raw right-hand sides of row tile p+1 are loaded while tile p is
-    //    being solved.
-    const size_t cid = (size_t)ci;
     floatx4 *Wf = reinterpret_cast<floatx4 *>(p.ws_w) + cid * (C * K / 4);
     floatx4 *Mf = reinterpret_cast<floatx4 *>(p.ws_m) + cid * (C * K / 4);
     floatx4 *Uf = reinterpret_cast<floatx4 *>(p.ws_u) + cid * (C * V / 4);
     floatx4 *Pf = reinterpret_cast<floatx4 *>(p.ws_p) + cid * (C * V / 4);
     floatx4 X[NTW][NT];
-    floatx4 r1[2][NTW], r2[2][NTW], qv[2][NTW];
+    floatx4 r1[2][NTW], r2[2][NTW];
 #pragma unroll
     for (int pt = 0; pt <= NT; ++pt) {
-        if (pt < NT) { // issue the loads of row tile pt (consumed at iteration pt + 1)
+        if (pt < NT) { // issue the value-column loads of row tile pt (consumed at iteration pt + 1)
             const int sl = pt & 1;
 #pragma unroll
             for (int u = 0; u < NTW; ++u) {
-                // branch-free operand selection (a branch here would make each
-                // group of loads wait for its own results before the join)
-                const int nt = wave + 4 * u;
-                const bool kcol = nt < NKT;
-                const float *p1 = kcol ? bc : wc, *p2 = kcol ? kc : vc;
-                const int64_t rs = kcol ? sqt : svt;
-                const int c = kcol ? 16 * nt + lr : 16 * (nt - NKT) + lr;
+                const int nt = wave + NW * u;
+                const bool kcol = u == 0 && (NKT >= NW || wave < NKT);
+                if (nt < NTOT && !kcol) {
+                    const int c = 16 * (nt - NKT) + lr;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int t = 16 * pt + 4 * lg + i;
-                    r1[sl][u][i] = ld1(p1, rs, t, cv, c);
-                    r2[sl][u][i] = ld1(p2, rs, t, cv, c);
-                    qv[sl][u][i] = ld1(qc, sqt, t, cv, kcol ? c : lr); // used by key columns only
+                    for (int i = 0; i < 4; ++i) {
+                        const int t = 16 * pt + 4 * lg + i;
+                        r1[sl][u][i] = ld1(wc, svt, t, cv, c);
+                        r2[sl][u][i] = ld1(vc, svt, t, cv, c);
+                    }
                 }
             }
         }
@@ -341,14 +441,10 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
         const int tp = pt - 1, sl = tp & 1; // the row tile solved in this iteration
 #pragma unroll
         for (int u = 0; u < NTW; ++u) {
-            const int nt = wave + 4 * u;
-            const bool kcol = nt < NKT;
-            floatx4 R = r1[sl][u] * r2[sl][u];
-            floatx4 eg;
-            const int gcol = kcol ? 16 * nt + lr : 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) eg[i] = kcol ? fast_exp2(sG[16 * tp + 4 * lg + i][gcol]) : 1.f;
-            R *= eg;
+            const int nt = wave + NW * u;
+            const bool kcol = u == 0 && (NKT >= NW || wave < NKT);
+            if (nt >= NTOT) continue;
+            floatx4 R = kcol ? stR[tp] : r1[sl][u] * r2[sl][u];
 #pragma unroll
             for (int q = 0; q < NT; ++q)
                 if (q < tp) R = mfma4n(*reinterpret_cast<const float4 *>(&sAkk[16 * tp + lr][16 * q + 4 * lg]), X[u][q], R);
@@ -360,7 +456,7 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
             for (int q = 0; q < NT; ++q)
                 if (q <= tp) Y = mfma4(*reinterpret_cast<const float4 *>(&sAqk[16 * tp + lr][16 * q + 4 * lg]), X[u][q], Y);
             if (kcol) {
-                Y -= p.scale * qv[sl][u] * eg;
+                Y -= p.scale * stQ[tp];
                 const int f = tp * NKT + nt;
                 st_stream(Wf + f * 64 + lane, transpose16(Xp, lr, lg));
                 st_stream(Mf + f * 64 + lane, transpose16(Y, lr, lg));
@@ -371,28 +467,6 @@ __global__ __launch_bounds__(256, 2) void chunk_intra_kernel(ChunkParams p) {
             }
         }
     }
-
-    // 5. Kd^T = (k exp(G_last - G))^T as A-operand fragments (kb, tt): lane
-    //    (g, r) holds Kd[16 tt + 4 g + j][16 kb + r], and exp(G_last).
-    floatx4 *Kf = reinterpret_cast<floatx4 *>(p.ws_kdt) + cid * (C * K / 4);
-    constexpr int KDF = NKT * NT / 4; // fragments per wave
-    floatx4 kk[KDF];
-#pragma unroll
-    for (int j = 0; j < KDF; ++j) {
-        const int f = wave + 4 * j, kb = f / NT, tt = f % NT, ch = 16 * kb + lr;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kk[j][i] = ld1(kc, sqt, 16 * tt + 4 * lg + i, cv, ch);
-    }
-#pragma unroll
-    for (int j = 0; j < KDF; ++j) {
-        const int f = wave + 4 * j, kb = f / NT, tt = f % NT, ch = 16 * kb + lr;
-        const float gl = sG[C - 1][ch];
-        floatx4 val;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) val[i] = kk[j][i] * fast_exp2(gl - sG[16 * tt + 4 * lg + i][ch]);
-        st_stream(Kf + f * 64 + lane, val);
-    }
-    if (tid < K) p.ws_gam[cid * K + tid] = fast_exp2(sG[C - 1][tid]);
 }
 
 // Sequences are spread over the 8 XCDs (workgroup i runs on XCD i % 8) so
@@ -583,7 +657,7 @@ template <int K, int V>
 hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
     if (phases & 1) {
         const int nchunks = p.B * p.HV * p.NC;
-        hipLaunchKernelGGL((chunk_intra_kernel<K, V>), dim3(nchunks), dim3(256), 0, s, p);
+        hipLaunchKernelGGL((chunk_intra_kernel<K, V>), dim3(nchunks), dim3(512), 0, s, p);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
