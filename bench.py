@@ -217,7 +217,9 @@ def bench_decode(torch, G, args, dev):
     param_bytes = (4 * (2 * kd + vd) + H + kd + V) * 4
     bytes_step = state_bytes + io_bytes + param_bytes
     gbs = bytes_step / (ms / 1e3) / 1e9
+    tr = load_traffic("decode_b64_traffic.json")
     res = {"batch": Bd, "tokens_per_s": Bd / (ms / 1e3), "ms_per_token_step": ms, "bytes_per_step": bytes_step,
+           "traffic": None if tr is None else tr.get("hbm_bytes_per_launch"),
            "core_bytes_per_step": 2 * Bd * H * K * V * 4 + Bd * (4 * H * K + 3 * H * V) * 4,
            "achieved_GBs": gbs, "peak_GBs": PEAK_HBM_GBS, "frac_hbm": gbs / PEAK_HBM_GBS,
            "rotating_state_buffers": nrot, "kernel": "gdn2_decode_fused_f32"}
@@ -346,7 +348,7 @@ def traffic_summary(fetch_csv, write_csv):
         out[key] = {"hbm_bytes_per_launch": rd + wr, "read_bytes": rd, "write_bytes": wr,
                     "dispatches": len(fv), "fetch_factor": f_fac, "write_factor": w_fac}
         print(f"| `{key}` | {len(fv)} | {rd / 1e9:.3f} | {wr / 1e9:.3f} | {(rd + wr) / 1e9:.3f} |")
-        suffix = "b64_decode" if key == "decode" else "b8_t4096"
+        suffix = "b64" if key == "decode" else "b8_t4096"
         with open(os.path.join(ROOT, "profiles", f"{key}_{suffix}_traffic.json"), "w") as fh:
             json.dump(out[key], fh, indent=1)
     return out

@@ -119,13 +119,13 @@ GDN2_API gdn2_status gdn2_recurrent_fwd_f32(const gdn2_recurrent_args *args, gdn
  * out:     [B, HV, T, V] strided (e.g. [B, T, HV, V] to skip a permute)
  * state:   [B, HV, K, V] contiguous, read as S0 and overwritten with S_T
  *          (in place, like the reference's chunk path).
- * T need not be a multiple of chunk_size.  chunk_size selects the kernel
- * tile (64 for chunk_size <= 64, else 128); the result does not depend on it
- * beyond rounding, as in the reference.
+ * T need not be a multiple of chunk_size.  The kernels always work on
+ * 64-token chunks of four 16-row tiles; any chunk_size > 0 is accepted, since
+ * the result does not depend on it beyond rounding, as in the reference.
  * workspace: device memory of at least gdn2_chunk_workspace_bytes(args)
  * bytes, 256-byte aligned.
- * Limits (else GDN2_NOT_APPLICABLE): K in {64, 128}, V a multiple of 64 up
- * to 512, chunk_size <= 128.
+ * Limits (else GDN2_NOT_APPLICABLE): K in {64, 128}, V in {64, 128, 256};
+ * q, k, b rows 16-byte aligned (strides multiples of 4 elements).
  * ---------------------------------------------------------------------- */
 typedef struct gdn2_chunk_args {
     const float *q, *k, *g, *b;
