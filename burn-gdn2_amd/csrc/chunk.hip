@@ -7,9 +7,9 @@
 //   W = (I + A_kk)^-1 (b k exp(G)),  U = (I + A_kk)^-1 (w v)
 //   v_new = U - W S,  out = A_qk v_new + scale (q exp(G)) S
 //   S <- exp(G_last) S + (k exp(G_last - G))^T v_new
-// The inter-chunk part is rewritten as out = P - M S with P = A_qk U and
-// M = A_qk W - scale (q exp(G)), so the sequential kernel does three
-// C x K x V products per chunk and no C x C one.
+// chunk-intra writes W, U, Kd^T = (k exp(G_last - G))^T, exp(G_last), A_qk
+// and scale (q exp(G)); chunk-inter runs the recurrence and the output
+// out = A_qk v_new + scale (q exp(G)) S of each chunk (src/forward.rs:264-274).
 //
 // Numerical scheme (every exponent fed to exp2 is <= 0 except where noted):
 //  * A_qk / A_kk off-diagonal 16x16 blocks (row tile p > column tile q):
@@ -211,7 +211,8 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
     //    blocks, over the channel half kh; the two halves are summed through
     //    LDS below.  The row operands, with exp(G) applied, are kept for the
     //    solve: q exp(G) (A_qk waves) and b k exp(G) (A_kk waves).
-    floatx4 stR[NT], stQ[NT]; // the solve's key-column operands (staged below)
+    floatx4 stR[NT]; // the solve's key-column right-hand sides (staged below)
+    floatx4 *QGf = reinterpret_cast<floatx4 *>(p.ws_qg) + cid * (C * K / 4);
     {
         const int mat = wave >> 2, half = (wave >> 1) & 1, kh = wave & 1;
         const int m0 = kh * NKH;
@@ -240,6 +241,8 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
                 const floatx4 kr = *reinterpret_cast<const floatx4 *>(&sK[row][c0]);
                 floatx4 a = araw[pi][m] * (mat == 1 ? kr : floatx4{1.f, 1.f, 1.f, 1.f});
                 a *= exp2v(gr - gb);
+                // scale q exp(G_r): the sequential kernel's A operand, fragment (pt, m0 + m)
+                if (mat == 0) st_stream(QGf + (pt * NKT + m0 + m) * 64 + lane, a * exp2v(gb) * p.scale);
                 const uint32_t mw = sMask[pt][c0 >> 5] >> (c0 & 31);
 #pragma unroll
                 for (int q = 0; q < NT; ++q) {
@@ -290,18 +293,17 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
                 }
             }
         }
-        // The solve's row operands x exp(G_r) (x = q, or b k), from a second
-        // read of the rows (recent, so served by the caches) rather than
+        // The solve's right-hand sides b k exp(G_r) (A_kk waves), from a second
+        // read of the b rows (recent, so served by the caches) rather than
         // registers held across the products.
         floatx4 stg[2][NKH];
-        {
+        if (mat == 1) {
             floatx4 ar2[2][NKH];
 #pragma unroll
             for (int pi = 0; pi < 2; ++pi) {
                 const int row = 16 * (pi ? (NT - 1 - half) : half) + lr;
 #pragma unroll
-                for (int m = 0; m < NKH; ++m)
-                    ar2[pi][m] = ld4v(mat == 0 ? qc : bc, sqt, row, cv, 16 * (m0 + m) + 4 * lg);
+                for (int m = 0; m < NKH; ++m) ar2[pi][m] = ld4v(bc, sqt, row, cv, 16 * (m0 + m) + 4 * lg);
             }
 #pragma unroll
             for (int pi = 0; pi < 2; ++pi) {
@@ -311,36 +313,21 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
                     const int c0 = 16 * (m0 + m) + 4 * lg;
                     const floatx4 gr = *reinterpret_cast<const floatx4 *>(&sG[row][c0]);
                     const floatx4 kr = *reinterpret_cast<const floatx4 *>(&sK[row][c0]);
-                    stg[pi][m] = ar2[pi][m] * (mat == 1 ? kr : floatx4{1.f, 1.f, 1.f, 1.f}) * exp2v(gr);
+                    stg[pi][m] = ar2[pi][m] * kr * exp2v(gr);
                 }
             }
         }
-        __syncthreads(); // sK and sG are dead: stage the row operands in their place
-        {
-            float(*dst)[KP] = mat == 0 ? sQG : sBKG;
+        __syncthreads(); // sK and sG are dead
+        // region A <- the right-hand sides; region B <- channel half 1's partial sums
+        if (mat == 1) {
 #pragma unroll
             for (int pi = 0; pi < 2; ++pi) {
                 const int row = 16 * (pi ? (NT - 1 - half) : half) + lr;
 #pragma unroll
                 for (int m = 0; m < NKH; ++m)
-                    *reinterpret_cast<floatx4 *>(&dst[row][16 * (m0 + m) + 4 * lg]) = stg[pi][m];
+                    *reinterpret_cast<floatx4 *>(&sBKG[row][16 * (m0 + m) + 4 * lg]) = stg[pi][m];
             }
         }
-        __syncthreads();
-        // The solve's owner of key column tile nt = wave reads its columns in
-        // accumulator layout (rows 4 g + i, column r of each 16 x 16 tile).
-        if (wave < NKT) {
-            const int col = 16 * wave + lr;
-#pragma unroll
-            for (int tp = 0; tp < NT; ++tp)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    stR[tp][i] = sBKG[16 * tp + 4 * lg + i][col];
-                    stQ[tp][i] = sQG[16 * tp + 4 * lg + i][col];
-                }
-        }
-        __syncthreads(); // the staging is consumed: region B becomes A_qk | A_kk
-        // channel half 1 leaves its partial sums, half 0 completes them
         if (kh == 1) {
 #pragma unroll
             for (int pi = 0; pi < 2; ++pi) {
@@ -357,6 +344,16 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
             }
         }
         __syncthreads();
+        // The solve's owner of key column tile nt = wave reads its columns in
+        // accumulator layout (rows 4 g + i, column r of each 16 x 16 tile);
+        // channel half 0 completes the score matrices.
+        if (wave < NKT) {
+            const int col = 16 * wave + lr;
+#pragma unroll
+            for (int tp = 0; tp < NT; ++tp)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) stR[tp][i] = sBKG[16 * tp + 4 * lg + i][col];
+        }
         if (kh == 0) {
 #pragma unroll
             for (int pi = 0; pi < 2; ++pi) {
@@ -386,6 +383,18 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
     }
     __syncthreads();
 
+    // A_qk -> the sequential kernel as A-operand fragments (mt, qt), zero above the diagonal.
+    {
+        floatx4 *Af = reinterpret_cast<floatx4 *>(p.ws_aqk) + cid * (C * C / 4);
+#pragma unroll
+        for (int j = 0; j < NT * NT / NW; ++j) {
+            const int f = wave + NW * j, mt = f / NT, qt = f % NT;
+            floatx4 val = *reinterpret_cast<const floatx4 *>(&sAqk[16 * mt + lr][16 * qt + 4 * lg]);
+            if (qt > mt) val = floatx4{0.f, 0.f, 0.f, 0.f};
+            st_stream(Af + f * 64 + lane, val);
+        }
+    }
+
     // 3. (I + A_kk_pp)^-1 for the four diagonal 16x16 blocks: lane = (tile, column).
     if (wave == 0) {
         const int pt = lane >> 4, j = lane & 15;
@@ -402,20 +411,18 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
     }
     __syncthreads();
 
-    // 4. Blocked solve of (I + A_kk) [W | U] = [b k exp(G) | w v] and
-    //    Y = A_qk [W | U]; wave w owns column tiles w, w + 8, ... of [W | U]
+    // 4. Blocked solve of (I + A_kk) [W | U] = [b k exp(G) | w v]; wave w owns
+    //    column tiles w, w + 8, ... of [W | U]
     //    (key columns first, whose right-hand sides were staged above; the
     //    value columns' w, v rows of tile p+1 are loaded while tile p is
     //    solved).  Outputs go to the workspace in MFMA fragment order (one
     //    1 KB block of 64 lanes x float4 per 16x16 tile) so that every store
     //    here and every load in chunk-inter is a contiguous 16-byte access per
     //    lane:
-    //      W, M : A-operand fragments (lane (g, r) holds rows r, cols 4g..4g+3)
-    //      U, P : accumulator fragments (lane (g, c) holds rows 4g..4g+3, col c)
+    //      W : A-operand fragments (lane (g, r) holds rows r, cols 4g..4g+3)
+    //      U : accumulator fragments (lane (g, c) holds rows 4g..4g+3, col c)
     floatx4 *Wf = reinterpret_cast<floatx4 *>(p.ws_w) + cid * (C * K / 4);
-    floatx4 *Mf = reinterpret_cast<floatx4 *>(p.ws_m) + cid * (C * K / 4);
     floatx4 *Uf = reinterpret_cast<floatx4 *>(p.ws_u) + cid * (C * V / 4);
-    floatx4 *Pf = reinterpret_cast<floatx4 *>(p.ws_p) + cid * (C * V / 4);
     floatx4 X[NTW][NT];
     floatx4 r1[2][NTW], r2[2][NTW];
 #pragma unroll
@@ -451,20 +458,10 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
             floatx4 Xp = mfma4(*reinterpret_cast<const float4 *>(&sAinv[tp][lr][4 * lg]), R,
                                floatx4{0.f, 0.f, 0.f, 0.f});
             X[u][tp] = Xp;
-            floatx4 Y = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int q = 0; q < NT; ++q)
-                if (q <= tp) Y = mfma4(*reinterpret_cast<const float4 *>(&sAqk[16 * tp + lr][16 * q + 4 * lg]), X[u][q], Y);
-            if (kcol) {
-                Y -= p.scale * stQ[tp];
-                const int f = tp * NKT + nt;
-                st_stream(Wf + f * 64 + lane, transpose16(Xp, lr, lg));
-                st_stream(Mf + f * 64 + lane, transpose16(Y, lr, lg));
-            } else {
-                const int f = (nt - NKT) * NT + tp;
-                st_stream(Uf + f * 64 + lane, Xp);
-                st_stream(Pf + f * 64 + lane, Y);
-            }
+            if (kcol)
+                st_stream(Wf + (tp * NKT + nt) * 64 + lane, transpose16(Xp, lr, lg));
+            else
+                st_stream(Uf + ((nt - NKT) * NT + tp) * 64 + lane, Xp);
         }
     }
 }
@@ -488,14 +485,15 @@ __device__ __forceinline__ void inter_block(int blk, int nseq, int nvs, int *bh,
 // chunk-inter: one workgroup per (b, hv, 64 value columns); wave w owns 16
 // columns.  S[:, cols] stays in MFMA accumulators for the whole sequence.
 // Per chunk n:
-//   A: X1 = W S, X2 = M S               (reads sW, sM)
-//   B: v_new = U - X1, out = P - X2
-//   C: S = exp(G_last) S + Kd^T v_new   (reads sKd, sGam)
-// LDS holds one chunk of W, M (2 C K floats) and Kd^T (K C floats).  Each
-// buffer is refilled while the other phase runs: Kd^T(n) is fetched during
-// A(n) and stored after it; W, M(n+1) are fetched during B, C(n) and stored
-// after C(n).  HBM latency is therefore off the sequential path without a
-// second copy of the buffers.
+//   A: X1 = W S, X2 = scale (q exp(G)) S      (reads sW, sQ)
+//   B: v_new = U - X1
+//   C: S = exp(G_last) S + Kd^T v_new         (reads sKd, sGam)
+//   D: out = X2 + A_qk v_new                  (reads sA; independent of C)
+// LDS holds one chunk of W, q exp(G) (2 C K floats), Kd^T (K C) and A_qk
+// (C C).  Each buffer is refilled while another phase runs: Kd^T(n) and
+// A_qk(n) are fetched during A(n) and stored after it; W, q exp(G)(n+1) are
+// fetched during B-D(n) and stored after them.  HBM latency is therefore off
+// the sequential path without a second copy of the buffers.
 // ---------------------------------------------------------------------------
 template <int K>
 __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
@@ -504,7 +502,9 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
     constexpr int OPF4 = FR * 64;  // float4 per operand per chunk
     constexpr int PFO = OPF4 / 256; // float4 per lane per operand
     static_assert(OPF4 % 256 == 0, "K");
-    __shared__ floatx4 sW[OPF4], sM[OPF4], sKd[OPF4];
+    constexpr int AF4 = NT * NT * 64; // float4 of A_qk per chunk
+    constexpr int APF = AF4 / 256;
+    __shared__ floatx4 sW[OPF4], sQ[OPF4], sKd[OPF4], sA[AF4];
     __shared__ floatx4 sGam[K / 4];
 
     const int V = p.V;
@@ -526,10 +526,10 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
         for (int i = 0; i < 4; ++i) S[kb][i] = Sg[(size_t)(16 * kb + 4 * lg + i) * V + col];
 
     const floatx4 *__restrict__ W4 = reinterpret_cast<const floatx4 *>(p.ws_w);
-    const floatx4 *__restrict__ M4 = reinterpret_cast<const floatx4 *>(p.ws_m);
+    const floatx4 *__restrict__ Q4 = reinterpret_cast<const floatx4 *>(p.ws_qg);
     const floatx4 *__restrict__ K4 = reinterpret_cast<const floatx4 *>(p.ws_kdt);
     const floatx4 *__restrict__ U4 = reinterpret_cast<const floatx4 *>(p.ws_u);
-    const floatx4 *__restrict__ P4 = reinterpret_cast<const floatx4 *>(p.ws_p);
+    const floatx4 *__restrict__ A4 = reinterpret_cast<const floatx4 *>(p.ws_aqk);
     const floatx4 *__restrict__ G4 = reinterpret_cast<const floatx4 *>(p.ws_gam);
     const size_t cid0 = (size_t)bh * p.NC;
     const size_t uvf4 = (size_t)C * V / 4;
@@ -538,25 +538,24 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
             sW[i * 256 + tid] = W4[cid0 * OPF4 + i * 256 + tid];
-            sM[i * 256 + tid] = M4[cid0 * OPF4 + i * 256 + tid];
+            sQ[i * 256 + tid] = Q4[cid0 * OPF4 + i * 256 + tid];
         }
     }
 
     float *ob = p.out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + col;
     for (int n = 0; n < p.NC; ++n) {
         const size_t cid = cid0 + n;
-        __syncthreads(); // sW, sM hold chunk n; every wave is done with sKd(n-1)
-        floatx4 kpre[PFO], u_cur[NT], p_cur[NT], g_cur = floatx4{0.f, 0.f, 0.f, 0.f};
+        __syncthreads(); // sW, sQ hold chunk n; every wave is done with sKd, sA (n-1)
+        floatx4 kpre[PFO], apre[APF], u_cur[NT], g_cur = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < PFO; ++i) kpre[i] = K4[cid * OPF4 + i * 256 + tid];
+#pragma unroll
+        for (int i = 0; i < APF; ++i) apre[i] = A4[cid * AF4 + i * 256 + tid];
         if (tid < K / 4) g_cur = G4[cid * (K / 4) + tid];
 #pragma unroll
-        for (int mt = 0; mt < NT; ++mt) {
-            u_cur[mt] = U4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
-            p_cur[mt] = P4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
-        }
+        for (int mt = 0; mt < NT; ++mt) u_cur[mt] = U4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
 
-        // A: X1 = W S, X2 = M S
+        // A: X1 = W S, X2 = scale (q exp(G)) S
         floatx4 X1[NT], X2[NT];
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) X1[mt] = X2[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -566,7 +565,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) {
                 wa[mt] = sW[(mt * NKT + kb) * 64 + lane];
-                ma[mt] = sM[(mt * NKT + kb) * 64 + lane];
+                ma[mt] = sQ[(mt * NKT + kb) * 64 + lane];
             }
             // eight independent accumulator chains per k-step
 #pragma unroll
@@ -592,28 +591,42 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
         }
 #pragma unroll
         for (int i = 0; i < PFO; ++i) sKd[i * 256 + tid] = kpre[i];
+#pragma unroll
+        for (int i = 0; i < APF; ++i) sA[i * 256 + tid] = apre[i];
         if (tid < K / 4) sGam[tid] = g_cur;
-        __syncthreads(); // A done everywhere (sW, sM free); sKd(n) visible
+        __syncthreads(); // A done everywhere (sW, sQ free); sKd(n), sA(n) visible
 
-        // W, M of chunk n+1 (the last chunk re-fetches itself: harmless, and
-        // unconditional loads keep the staging registers out of scratch)
+        // W, q exp(G) of chunk n+1 (the last chunk re-fetches itself: harmless,
+        // and unconditional loads keep the staging registers out of scratch)
         const size_t cnx = cid + (n + 1 < p.NC ? 1 : 0);
-        floatx4 wpre[PFO], mpre[PFO];
+        floatx4 wpre[PFO], qpre[PFO];
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
             wpre[i] = W4[cnx * OPF4 + i * 256 + tid];
-            mpre[i] = M4[cnx * OPF4 + i * 256 + tid];
+            qpre[i] = Q4[cnx * OPF4 + i * 256 + tid];
         }
 
-        // B: v_new = U - X1 (kept in X1), out = P - X2
+        // B: v_new = U - X1 (kept in X1)
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt) X1[mt] = u_cur[mt] - X1[mt];
+
+        // D: out = X2 + A_qk v_new (A_qk is lower block-triangular)
         const int cv = min(C, p.T - n * C);
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) {
+            floatx4 o = X2[mt];
+#pragma unroll
+            for (int qt = 0; qt <= mt; ++qt) {
+                const floatx4 aa = sA[(mt * NT + qt) * 64 + lane];
+                o = mfma16(aa[0], X1[qt][0], o);
+                o = mfma16(aa[1], X1[qt][1], o);
+                o = mfma16(aa[2], X1[qt][2], o);
+                o = mfma16(aa[3], X1[qt][3], o);
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int t = 16 * mt + 4 * lg + i;
-                X1[mt][i] = u_cur[mt][i] - X1[mt][i];
-                if (t < cv) ob[(int64_t)(n * C + t) * p.sot] = p_cur[mt][i] - X2[mt][i];
+                if (t < cv) ob[(int64_t)(n * C + t) * p.sot] = o[i];
             }
         }
 
@@ -644,7 +657,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
             sW[i * 256 + tid] = wpre[i];
-            sM[i * 256 + tid] = mpre[i];
+            sQ[i * 256 + tid] = qpre[i];
         }
     }
 #pragma unroll
@@ -691,7 +704,7 @@ using namespace gdn2;
 namespace {
 
 struct WsLayout {
-    size_t w, m, u, p, kdt, gam, total;
+    size_t w, qg, u, aqk, kdt, gam, total;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -700,9 +713,9 @@ WsLayout ws_layout(int64_t nchunks, int64_t K, int64_t V) {
     WsLayout L;
     size_t off = 0;
     L.w = off; off = align256(off + sizeof(float) * nchunks * kChunk * K);
-    L.m = off; off = align256(off + sizeof(float) * nchunks * kChunk * K);
+    L.qg = off; off = align256(off + sizeof(float) * nchunks * kChunk * K);
     L.u = off; off = align256(off + sizeof(float) * nchunks * kChunk * V);
-    L.p = off; off = align256(off + sizeof(float) * nchunks * kChunk * V);
+    L.aqk = off; off = align256(off + sizeof(float) * nchunks * kChunk * kChunk);
     L.kdt = off; off = align256(off + sizeof(float) * nchunks * kChunk * K);
     L.gam = off; off = align256(off + sizeof(float) * nchunks * K);
     L.total = off;
@@ -757,9 +770,9 @@ static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, in
     p.scale = (float)a->scale;
     char *ws = static_cast<char *>(a->workspace);
     p.ws_w = reinterpret_cast<float *>(ws + L.w);
-    p.ws_m = reinterpret_cast<float *>(ws + L.m);
+    p.ws_qg = reinterpret_cast<float *>(ws + L.qg);
     p.ws_u = reinterpret_cast<float *>(ws + L.u);
-    p.ws_p = reinterpret_cast<float *>(ws + L.p);
+    p.ws_aqk = reinterpret_cast<float *>(ws + L.aqk);
     p.ws_kdt = reinterpret_cast<float *>(ws + L.kdt);
     p.ws_gam = reinterpret_cast<float *>(ws + L.gam);
     GDN2_HIP_CHECK(launch_chunk(p, (hipStream_t)stream, phases));

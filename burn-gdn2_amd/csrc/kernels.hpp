@@ -52,9 +52,9 @@ struct ChunkParams {
     // workspace, per chunk (chunk id = (b * HV + hv) * NC + n), in MFMA
     // fragment order: 16x16 tiles of 64 lanes x float4 (see chunk.hip)
     float *ws_w;   // C*K   W = (I + A_kk)^-1 (b*k*gamma), A-operand tiles (row tile, col tile)
-    float *ws_m;   // C*K   M = A_qk W - scale * (q * gamma), same order
+    float *ws_qg;  // C*K   scale * (q * gamma), same order
     float *ws_u;   // C*V   U = (I + A_kk)^-1 (w*v), accumulator tiles (col tile, row tile)
-    float *ws_p;   // C*V   P = A_qk U, same order
+    float *ws_aqk; // C*C   A_qk (scale included, zero above the diagonal), A-operand tiles (row tile, col tile)
     float *ws_kdt; // K*C   (k * exp(G_last - G))^T, A-operand tiles (key tile, time tile)
     float *ws_gam; // K     exp(G_last)
 };
