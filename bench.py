@@ -73,19 +73,19 @@ def load_traffic(name):
 
 
 def bench_prefill(torch, G, args, dev):
-    """The recurrence core at the layer's own layout: the projected operands
-    come from GatedDeltaNet2.project (q, k, g, b [B, T, H, K] and v, w
-    [B, T, HV, V], read through strides), prepared once outside the timed
-    region; then the whole layer (forward_train) for comparison."""
+    """The recurrence core on the layer's own operands: q, k, g, b
+    [B, H, T, K] and v, w [B, HV, T, V] from GatedDeltaNet2.project, prepared
+    once outside the timed region; out [B, T, HV, V] as the layer writes it;
+    then the whole layer (forward_train) for comparison."""
     cfg = G.Gdn2Config(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0, mode="chunk", chunk_size=64)
     layer = G.GatedDeltaNet2(cfg, seed=1337)
     B, T, H, K, V, C = args.batch, args.seq, cfg.num_heads, cfg.head_dim, cfg.v_head, 64
     gen = torch.Generator(device=dev)
     gen.manual_seed(42)
     x = torch.randn((B, T, cfg.hidden_size), generator=gen, device=dev, dtype=torch.float32)
-    P = layer.project(x)
-    q, k, g, b = (P[n].permute(0, 2, 1, 3) for n in ("q", "k", "g", "b"))
-    v, w = (P[n].permute(0, 2, 1, 3) for n in ("v", "w"))
+    P = layer.project(x)  # q, k, g, b [B, H, T, K]; v, w [B, HV, T, V]
+    q, k, g, b = (P[n] for n in ("q", "k", "g", "b"))
+    v, w = (P[n] for n in ("v", "w"))
     state = torch.zeros((B, H, K, V), device=dev)
     out = torch.empty((B, T, H, V), device=dev).permute(0, 2, 1, 3)
     scale = K ** -0.5

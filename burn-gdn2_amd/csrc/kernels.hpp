@@ -70,8 +70,8 @@ struct ProjectParams {
     const float *conv_q_in, *conv_k_in, *conv_v_in; // [B, 3, kd|vd]; null: pad with token 0
     const float *q_conv_w, *k_conv_w, *v_conv_w;
     const float *a_log, *dt_bias, *decay_factors; // decay_factors null without min_decay
-    float *q, *k, *g, *b; // [B*T, kd]
-    float *v, *w;         // [B*T, vd]
+    float *q, *k, *g, *b; // [B, H, T, K]
+    float *v, *w;         // [B, HV, T, V]
     int B, T, H, K, HV, V;
     int use_short_conv, allow_neg_eigval;
     float min_decay, one_minus_min_decay;

@@ -6,7 +6,7 @@
 // Data flow of one call over M = B * T tokens (all buffers row-major):
 //   Y [M, ld_in] = x W_in            W_in = [q | k | b | v | w | f0 | g0] (one GEMM)
 //   F [M, kd]    = Y[:, f0] W_f1     G [M, vd] = bias + Y[:, g0] W_g1
-//   q, k, g, b [M, kd], v, w [M, vd] = project epilogue (conv, SiLU, gates, L2 norm)
+//   q, k, g, b [B, H, T, K], v, w [B, HV, T, V] = project epilogue (conv, SiLU, gates, L2 norm)
 //   O [M, vd]    = recurrence (chunk or per-token scan) in the [B, T, HV, V] layout
 //   O            = rms_norm_gate(O, G)  (in place)
 //   out [M, D]   = O W_o
@@ -216,8 +216,10 @@ gdn2_chunk_args chunk_args_for(const gdn2_layer &L, int64_t B, int64_t T, const 
     a.q = wk.q; a.k = wk.k; a.g = wk.g; a.b = wk.b; a.v = wk.v; a.w = wk.w;
     a.state = S; a.out = wk.O;
     a.batch = B; a.num_heads = d.H; a.num_v_heads = d.HV; a.seq_len = T; a.head_dim = d.K; a.head_v_dim = d.V;
-    a.stride_qk_b = T * d.kd; a.stride_qk_h = d.K; a.stride_qk_t = d.kd;
-    a.stride_vw_b = T * d.vd; a.stride_vw_h = d.V; a.stride_vw_t = d.vd;
+    // q, k, g, b [B, H, T, K] and v, w [B, HV, T, V] (head-major, so that a
+    // chunk's rows are one contiguous block); out [B, T, HV, V] for the norm
+    a.stride_qk_b = d.H * T * d.K; a.stride_qk_h = T * d.K; a.stride_qk_t = d.K;
+    a.stride_vw_b = d.HV * T * d.V; a.stride_vw_h = T * d.V; a.stride_vw_t = d.V;
     a.stride_o_b = T * d.vd; a.stride_o_h = d.V; a.stride_o_t = d.vd;
     a.scale = std::pow((double)d.K, -0.5);
     a.chunk_size = L.cfg.chunk_size;

@@ -1,6 +1,8 @@
 // Layer kernels around the recurrence: the projection epilogue (short conv,
-// SiLU, gates, L2 norm, written in the kernels' [B, T, H, D] layout), the
-// conv-cache update, the gated RMSNorm and a row fill for Linear biases.
+// SiLU, gates, L2 norm; written head-major [B, H, T, D], as the reference's
+// project() returns them, so that each chunk of a head is one contiguous
+// block), the conv-cache update, the gated RMSNorm and a row fill for Linear
+// biases.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -67,8 +69,9 @@ __global__ __launch_bounds__(256) void project_kernel(ProjectParams p) {
         if (p.decay_factors) gv = logf(sigmoid_(p.decay_factors[c]) * p.one_minus_min_decay * expf(gv) + p.min_decay);
         float bv = sigmoid_(Y[p.off_b + c]);
         if (p.allow_neg_eigval) bv *= 2.0f;
-        p.g[m * kd + c] = gv;
-        p.b[m * kd + c] = bv;
+        const int64_t o = ((int64_t)bi * p.H + c / p.K) * p.T * p.K + (int64_t)t * p.K + c % p.K;
+        p.g[o] = gv;
+        p.b[o] = bv;
     }
     // v = SiLU(conv(v_raw)), w = sigmoid(w_raw)
     for (int c = tid; c < vd; c += 256) {
@@ -79,8 +82,9 @@ __global__ __launch_bounds__(256) void project_kernel(ProjectParams p) {
         } else {
             av = Y[p.off_v + c];
         }
-        p.v[m * vd + c] = silu_(av);
-        p.w[m * vd + c] = sigmoid_(Y[p.off_w + c]);
+        const int64_t o = ((int64_t)bi * p.HV + c / p.V) * p.T * p.V + (int64_t)t * p.V + c % p.V;
+        p.v[o] = silu_(av);
+        p.w[o] = sigmoid_(Y[p.off_w + c]);
     }
     __syncthreads();
     // L2 norm per head over K channels (src/l2norm.rs:13-16): one wave per head.
@@ -94,9 +98,10 @@ __global__ __launch_bounds__(256) void project_kernel(ProjectParams p) {
         sq = wave_sum(sq);
         sk = wave_sum(sk);
         const float nq = sqrtf(sq + 1e-6f), nk = sqrtf(sk + 1e-6f);
+        const int64_t o = ((int64_t)bi * p.H + h) * p.T * p.K + (int64_t)t * p.K;
         for (int i = lane; i < p.K; i += 64) {
-            p.q[m * kd + h * p.K + i] = s_q[h * p.K + i] / nq;
-            p.k[m * kd + h * p.K + i] = s_k[h * p.K + i] / nk;
+            p.q[o + i] = s_q[h * p.K + i] / nq;
+            p.k[o + i] = s_k[h * p.K + i] / nk;
         }
     }
 }

@@ -270,14 +270,16 @@ class GatedDeltaNet2:
 
     def project(self, x, state: Optional[Gdn2State] = None) -> Dict[str, "torch.Tensor"]:
         """project (src/module.rs:381-495) without the GVA repeat: q, k, g, b
-        [B, T, H, K], v, w and gate [B, T, HV, V]."""
+        [B, H, T, K], v, w [B, HV, T, V] (the reference's layouts) and gate
+        [B, T, HV, V]."""
         import torch
 
         x = self._check_x(x)
         cfg = self.config
         B, T = x.shape[:2]
-        o = {n: torch.empty((B, T, cfg.num_heads, cfg.head_dim), device=x.device) for n in ("q", "k", "g", "b")}
-        o.update({n: torch.empty((B, T, cfg.hv, cfg.v_head), device=x.device) for n in ("v", "w", "gate")})
+        o = {n: torch.empty((B, cfg.num_heads, T, cfg.head_dim), device=x.device) for n in ("q", "k", "g", "b")}
+        o.update({n: torch.empty((B, cfg.hv, T, cfg.v_head), device=x.device) for n in ("v", "w")})
+        o["gate"] = torch.empty((B, T, cfg.hv, cfg.v_head), device=x.device)
         C.check(C.lib().gdn2_layer_project_f32(self._h, x.data_ptr(), B, T, state._h if state is not None else None,
                                                *(o[n].data_ptr() for n in ("q", "k", "g", "b", "v", "w", "gate")),
                                                _stream()))

@@ -129,10 +129,11 @@ GDN2_API gdn2_status gdn2_layer_forward_f32(gdn2_layer *layer, const float *x, i
                                             gdn2_state *state, float *out, gdn2_stream_t stream);
 
 /* project (src/module.rs:381-495) without the GVA repeat: writes the
- * kernel inputs q, k, g, b [B, T, H, K], v, w [B, T, HV, V] and the gate
+ * kernel inputs q, k, g, b [B, H, T, K], v, w [B, HV, T, V] and the gate
  * signal [B, T, HV, V] (each contiguous, caller-owned).  `state` (nullable,
  * not modified) supplies the conv caches when non-empty.  The reference's
- * [B, HV, T, K] tensors are these with the heads repeated and permuted. */
+ * [B, HV, T, K] key-side tensors are these with each head repeated
+ * num_v_heads / num_heads times. */
 GDN2_API gdn2_status gdn2_layer_project_f32(gdn2_layer *layer, const float *x, int64_t batch, int64_t seq_len,
                                             const gdn2_state *state, float *q, float *k, float *g, float *b,
                                             float *v, float *w, float *gate, gdn2_stream_t stream);

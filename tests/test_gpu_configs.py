@@ -37,8 +37,8 @@ def _x(torch, gpu, seed, shape):
 
 
 def _core_views(P):
-    """project() outputs as the reference's [B, H, T, D] views."""
-    return [P[n].permute(0, 2, 1, 3) for n in ("q", "k", "v", "g", "b", "w")]
+    """project() outputs, already in the reference's [B, H, T, D] layout."""
+    return [P[n] for n in ("q", "k", "v", "g", "b", "w")]
 
 
 def _check_core(G, cfg, P, chunk_size, sample, S0=None):
@@ -160,8 +160,8 @@ def test_config5_long_context_strong_decay(gpu):
                         chunk_size=128)
     x = _x(torch, gpu, 45, (1, 65536, 2048))
     P = layer.project(x)
-    g = P["g"]  # [1, T, H, K]
-    span = float(-g[0, :128].sum(0).min())  # cumulative decay over the first 128-token chunk
+    g = P["g"]  # [1, H, T, K]
+    span = float(-g[0, :, :128].sum(1).min())  # cumulative decay over the first 128-token chunk
     print(f"cumulative log-decay over one chunk reaches -{span:.1f}", flush=True)
     assert span > 88.0
     _check_core(G, cfg, P, 128, sample=[(0, 0), (0, 13)])

@@ -80,8 +80,7 @@ def test_project_matches_oracle(gpu):
     p = {n: t.cpu().numpy() for n, t in layer.project(x).items()}
     ref, _ = O.layer_forward(cfg, W, xh, want_proj=True)
     for n in ("q", "k", "g", "b", "v", "w"):
-        got = p[n].transpose(0, 2, 1, 3)  # [B, T, H, D] -> the reference's [B, H, T, D]
-        e = maxabs(got, ref.proj[n])
+        e = maxabs(p[n], ref.proj[n])  # both [B, H, T, D]
         print(f"{n}: {e:.2e}")
         assert e < TOL, n
     assert maxabs(p["gate"], ref.proj["gate"]) < TOL
