@@ -331,13 +331,15 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
     const float wv0 = wv[0], wv1 = wv[wst], wv2 = wv[2 * wst], wv3 = wv[3 * wst];
 
     // The state slice: 16-byte loads, each row read exactly once, part 0 first.
+    // State traffic is streamed (non-temporal loads and stores): at B = 64 it
+    // is 67 MB per token each way and would only evict the caches' reuse.
     floatx4 S[NH][NP];
     float *Sg = p.state + (size_t)bh * K * V + cg * 4;
 #pragma unroll
     for (int h = 0; h < NH; ++h)
 #pragma unroll
         for (int i = 0; i < NP; ++i)
-            S[h][i] = *reinterpret_cast<const floatx4 *>(Sg + (size_t)(r0 + i * RPP) * V + h * VP);
+            S[h][i] = __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(Sg + (size_t)(r0 + i * RPP) * V + h * VP));
 
     // Key side: conv + SiLU (src/short_conv.rs:22-65), gates
     // (src/module.rs:417-443), then the L2 norms over K (src/l2norm.rs).
@@ -442,7 +444,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
         for (int i = 0; i < NP; ++i) {
             const int rr = r0 + i * RPP;
             const float eg = s_eg[rr], kk = s_k[rr];
-            *reinterpret_cast<floatx4 *>(Sg + (size_t)rr * V + h * VP) = S[h][i] * eg + kk * vn4;
+            __builtin_nontemporal_store(S[h][i] * eg + kk * vn4, reinterpret_cast<floatx4 *>(Sg + (size_t)rr * V + h * VP));
         }
     }
     // gated RMSNorm over the V columns (src/module.rs:501-517)
