@@ -41,15 +41,23 @@ constexpr int NT = C / 16;
 static_assert(NT == 4, "the diagonal-block inverse maps 4 tiles x 16 columns onto one wave");
 constexpr float kSafeSpan = 96.0f; // log2 units
 
-// Row loads of a chunk whose rows >= valid are zero padding.  The address is
-// clamped to a valid row (the data there is finite) and the value multiplied
-// by a 0/1 mask: a branch around the load would make the compiler wait for
-// every outstanding load at the join, serialising a phase's loads.
-// valid >= 1 always.
-__device__ __forceinline__ float ld1(const float *base, int64_t rs, int row, int valid, int col) {
-    const int r = row < valid ? row : valid - 1;
-    const float x = base[(int64_t)r * rs + col];
-    return x * (row < valid ? 1.f : 0.f); // a product, so the load cannot be sunk into a branch
+// Rows [0, valid) of a row-strided f32 matrix (row stride rs, rowlen
+// elements used per row) as a buffer resource.  The hardware's range check
+// returns 0 for every load past the last valid row, which is the zero padding
+// of a ragged last chunk (src/forward.rs:94-99), so a load needs neither a
+// clamp nor a mask, and its offset is a 32-bit element index.  Requires
+// rs >= rowlen and ((valid - 1) rs + rowlen) * 4 < 2^31 (checked on the host).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float *base, int rs, int valid, int rowlen) {
+    const int bytes = ((valid - 1) * rs + rowlen) * 4;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ float bld1(__amdgpu_buffer_rsrc_t r, int idx) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, idx * 4, 0, 0));
+}
+
+__device__ __forceinline__ floatx4 bld4(__amdgpu_buffer_rsrc_t r, int idx) {
+    return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, idx * 4, 0, 0));
 }
 
 __device__ __forceinline__ floatx4 mfma4(float4 a, floatx4 b, floatx4 c) {
@@ -89,12 +97,6 @@ __device__ __forceinline__ floatx4 mfma4n(float4 a, floatx4 b, floatx4 c) {
 // that a workgroup pays a handful of memory round trips instead of one per
 // loop iteration.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ floatx4 ld4v(const float *base, int64_t rs, int row, int valid, int col) {
-    const int r = row < valid ? row : valid - 1;
-    const floatx4 x = *reinterpret_cast<const floatx4 *>(base + (int64_t)r * rs + col);
-    return x * (row < valid ? 1.f : 0.f);
-}
-
 // Streaming store: the workspace is read back by chunk-inter much later, so
 // keeping it out of L2 leaves room for the chunk's inputs, which chunk-intra
 // reads more than once.
@@ -145,21 +147,29 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
     const float *qc = p.q + kofs, *kc = p.k + kofs, *gc = p.g + kofs, *bc = p.b + kofs;
     const float *vc = p.v + vofs, *wc = p.w + vofs;
     const size_t cid = (size_t)ci;
+    // Row loads go through range-checked buffer resources (rows >= cv read 0)
+    // with 32-bit offsets: row * stride + column, the row part split into a
+    // per-lane term computed once and a wave-uniform term.
+    const int rq = (int)sqt, rv = (int)svt;
+    const __amdgpu_buffer_rsrc_t Rq = rows_rsrc(qc, rq, cv, K), Rk = rows_rsrc(kc, rq, cv, K);
+    const __amdgpu_buffer_rsrc_t Rg = rows_rsrc(gc, rq, cv, K), Rb = rows_rsrc(bc, rq, cv, K);
+    const __amdgpu_buffer_rsrc_t Rv = rows_rsrc(vc, rv, cv, V), Rw = rows_rsrc(wc, rv, cv, V);
+    const int lr_q = lr * rq;      // row lr of a tile, q/k/g/b
+    const int lg_q = 4 * lg * rq;  // row 4 lg of a tile, q/k/g/b
+    const int lg_v = 4 * lg * rv;  // row 4 lg of a tile, v/w
 
     // 1. k -> sK; G = cumsum_t g per channel -> sG in log2 units.  Rows past
     //    the end of a ragged last chunk are zero (src/forward.rs:94-99).
     {
         floatx4 kreg[KF4];
 #pragma unroll
-        for (int i = 0; i < KF4; ++i) {
-            const int f = i * 512 + tid, row = f / (K / 4), c4 = f % (K / 4);
-            kreg[i] = ld4v(kc, sqt, row, cv, 4 * c4);
-        }
-        const int c = tid % K, seg = tid / K;
+        for (int i = 0; i < KF4; ++i) // 512 % (K / 4) == 0: row = i 512 / (K / 4) + tid / (K / 4)
+            kreg[i] = bld4(Rk, (tid / (K / 4)) * rq + 4 * (tid % (K / 4)) + i * (512 / (K / 4)) * rq);
+        const int c = tid % K, seg = wave * 64 / K; // tid / K, wave-uniform
         float vals[RPS];
         float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < RPS; ++i) vals[i] = ld1(gc, sqt, seg * RPS + i, cv, c);
+        for (int i = 0; i < RPS; ++i) vals[i] = bld1(Rg, c + (seg * RPS + i) * rq);
 #pragma unroll
         for (int i = 0; i < RPS; ++i) {
             acc += vals[i];
@@ -222,7 +232,7 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
             const int row = 16 * (pi ? (NT - 1 - half) : half) + lr;
 #pragma unroll
             for (int m = 0; m < NKH; ++m)
-                araw[pi][m] = ld4v(mat == 0 ? qc : bc, sqt, row, cv, 16 * (m0 + m) + 4 * lg);
+                araw[pi][m] = bld4(mat == 0 ? Rq : Rb, lr_q + (row - lr) * rq + 16 * (m0 + m) + 4 * lg);
         }
         floatx4 acc[2][NT];
 #pragma unroll
@@ -283,8 +293,8 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
                             for (int i = 0; i < 4; ++i) {
                                 const int r = 4 * lg + i;
                                 const int rrow = 16 * pt + r;
-                                const float xr = (mat == 0) ? ld1(qc, sqt, rrow, cv, c)
-                                                            : ld1(bc, sqt, rrow, cv, c) * sK[rrow][c];
+                                const int ro = lg_q + (16 * pt + i) * rq + c; // row rrow
+                                const float xr = (mat == 0) ? bld1(Rq, ro) : bld1(Rb, ro) * sK[rrow][c];
                                 const float e = (mat == 0 ? (r >= lr) : (r > lr)) ? fast_exp2(sG[rrow][c] - gs) : 0.f;
                                 acc[pi][q][i] += xr * ks * e;
                             }
@@ -303,7 +313,7 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
             for (int pi = 0; pi < 2; ++pi) {
                 const int row = 16 * (pi ? (NT - 1 - half) : half) + lr;
 #pragma unroll
-                for (int m = 0; m < NKH; ++m) ar2[pi][m] = ld4v(bc, sqt, row, cv, 16 * (m0 + m) + 4 * lg);
+                for (int m = 0; m < NKH; ++m) ar2[pi][m] = bld4(Rb, lr_q + (row - lr) * rq + 16 * (m0 + m) + 4 * lg);
             }
 #pragma unroll
             for (int pi = 0; pi < 2; ++pi) {
@@ -438,8 +448,8 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int t = 16 * pt + 4 * lg + i;
-                        r1[sl][u][i] = ld1(wc, svt, t, cv, c);
-                        r2[sl][u][i] = ld1(vc, svt, t, cv, c);
+                        r1[sl][u][i] = bld1(Rw, lg_v + (t - 4 * lg) * rv + c);
+                        r2[sl][u][i] = bld1(Rv, lg_v + (t - 4 * lg) * rv + c);
                     }
                 }
             }
@@ -542,7 +552,8 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
         }
     }
 
-    float *ob = p.out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + col;
+    // row 4 lg of each 16-row tile; the rest of the row offset is wave-uniform
+    float *ob = p.out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + col + (int64_t)(4 * lg) * p.sot;
     for (int n = 0; n < p.NC; ++n) {
         const size_t cid = cid0 + n;
         __syncthreads(); // sW, sQ hold chunk n; every wave is done with sKd, sA (n-1)
@@ -625,8 +636,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int t = 16 * mt + 4 * lg + i;
-                if (t < cv) ob[(int64_t)(n * C + t) * p.sot] = o[i];
+                if (16 * mt + 4 * lg + i < cv) ob[(int64_t)(n * C + 16 * mt + i) * p.sot] = o[i];
             }
         }
 
@@ -754,6 +764,13 @@ static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, in
     if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->b) || (a->stride_qk_b % 4) || (a->stride_qk_h % 4) ||
         (a->stride_qk_t % 4))
         return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_fwd_f32: q/k/b need 16-byte aligned rows");
+    // The intra kernel reads a chunk's rows through 32-bit range-checked
+    // buffer offsets: token rows must not overlap, and one chunk of rows must
+    // span less than 2 GiB.
+    if (a->stride_qk_t < a->head_dim || a->stride_vw_t < a->head_v_dim ||
+        ((kChunk - 1) * a->stride_qk_t + a->head_dim) * 4 >= (int64_t(1) << 31) ||
+        ((kChunk - 1) * a->stride_vw_t + a->head_v_dim) * 4 >= (int64_t(1) << 31))
+        return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_fwd_f32: token strides outside the chunk kernels' range");
     if (a->seq_len == 0) return GDN2_OK;
     const WsLayout L = ws_layout(num_chunks(a), a->head_dim, a->head_v_dim);
     if (!a->workspace || a->workspace_bytes < L.total || (reinterpret_cast<uintptr_t>(a->workspace) & 255u))
