@@ -132,7 +132,8 @@ def bench_prefill(torch, G, args, dev):
                         "tflops": inter_gflop / inter_ms, "frac_f32_mfma": inter_gflop / inter_ms / PEAK_F32_TFLOPS},
     }
     dom = "chunk_intra" if intra_ms >= inter_ms else "chunk_inter"
-    tr = load_traffic(f"{dom}_b8_t4096_traffic.json")
+    # measured HBM bytes exist for the default workload's shape only
+    tr = load_traffic(f"{dom}_b8_t4096_traffic.json") if (B, T) == (8, 4096) else None
     roof = {"kernel": dom, "bound": "mfma", "achieved": kernels[dom]["tflops"], "peak": PEAK_F32_TFLOPS,
             "unit": "TFLOP/s", "frac": kernels[dom]["frac_f32_mfma"],
             "traffic": None if tr is None else tr.get("hbm_bytes_per_launch"),
@@ -217,7 +218,7 @@ def bench_decode(torch, G, args, dev):
     param_bytes = (4 * (2 * kd + vd) + H + kd + V) * 4
     bytes_step = state_bytes + io_bytes + param_bytes
     gbs = bytes_step / (ms / 1e3) / 1e9
-    tr = load_traffic("decode_b64_traffic.json")
+    tr = load_traffic("decode_b64_traffic.json") if Bd == 64 else None
     res = {"batch": Bd, "tokens_per_s": Bd / (ms / 1e3), "ms_per_token_step": ms, "bytes_per_step": bytes_step,
            "traffic": None if tr is None else tr.get("hbm_bytes_per_launch"),
            "core_bytes_per_step": 2 * Bd * H * K * V * 4 + Bd * (4 * H * K + 3 * H * V) * 4,

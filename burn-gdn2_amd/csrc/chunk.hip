@@ -504,9 +504,22 @@ __device__ __forceinline__ void inter_block(int blk, int nseq, int nvs, int *bh,
 // A_qk(n) are fetched during A(n) and stored after it; W, q exp(G)(n+1) are
 // fetched during B-D(n) and stored after them.  HBM latency is therefore off
 // the sequential path without a second copy of the buffers.
+//
+// Segmented form (NSEG > 1, few long sequences).  Over one segment the
+// recurrence is affine in its entering state:
+//   S_out = P S_in + Q,  P = prod_n (diag(exp(G_last)) - Kd^T W)  (K x K),
+// and Q is the segment run from S_in = 0.  P is the same recurrence run on
+// the K columns of an identity with U = 0.  So:
+//   pass 1 (OUT = false): every segment but the last, from S = 0 on the V
+//     value columns and from S = I, U = 0 on K extra columns; no output;
+//     the results go to ws_qseg / ws_pseg;
+//   pass 2 (chunk_chain_kernel): S_in(j + 1) = P_j S_in(j) + Q_j, in order;
+//   pass 3 (OUT = true): every segment from its S_in, with the output; the
+//     last segment writes the final state.
+// With NSEG = 1 pass 3 alone is the plain sequential kernel.
 // ---------------------------------------------------------------------------
-template <int K>
-__global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
+template <int K, bool OUT>
+__global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int nseg_launch) {
     constexpr int NKT = K / 16;
     constexpr int FR = NKT * NT;   // 16x16 fragments per operand per chunk
     constexpr int OPF4 = FR * 64;  // float4 per operand per chunk
@@ -514,26 +527,39 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
     static_assert(OPF4 % 256 == 0, "K");
     constexpr int AF4 = NT * NT * 64; // float4 of A_qk per chunk
     constexpr int APF = AF4 / 256;
-    __shared__ floatx4 sW[OPF4], sQ[OPF4], sKd[OPF4], sA[AF4];
+    __shared__ floatx4 sW[OPF4], sKd[OPF4];
+    __shared__ floatx4 sQ[OUT ? OPF4 : 1], sA[OUT ? AF4 : 1];
     __shared__ floatx4 sGam[K / 4];
 
     const int V = p.V;
-    const int nvs = V / 64;
-    int bh, vs;
-    inter_block(blockIdx.x, p.B * p.HV, nvs, &bh, &vs);
+    const int nvv = V / 64;                   // value slices
+    const int nvs = OUT ? nvv : nvv + K / 64; // pass 1 adds the slices of P
+    int sq, vs;
+    inter_block(blockIdx.x, p.B * p.HV * nseg_launch, nvs, &sq, &vs);
+    const int bh = sq / nseg_launch, seg = sq % nseg_launch;
     const int bi = bh / p.HV, hv = bh % p.HV;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (scalar)
     const int lr = lane & 15, lg = lane >> 4;
-    const int vt = vs * 4 + wave; // this wave's 16-column tile of V
+    const bool pcol = !OUT && vs >= nvv;           // a slice of P (wave-uniform)
+    const int vt = (pcol ? vs - nvv : vs) * 4 + wave; // this wave's 16-column tile
     const int col = 16 * vt + lr;
+    const int n0 = seg * p.SEGL;
+    const int n1 = min(p.NC, n0 + p.SEGL);
 
-    float *Sg = p.state + (size_t)bh * K * V;
+    // entering state: S0 (one segment), the chained state (pass 3; slot 0 is a
+    // copy of S0, so that no workgroup reads the state that the last segment
+    // overwrites), 0 (pass 1 value columns) or the identity (pass 1, P columns)
+    const float *Sin = nullptr;
+    if (OUT) Sin = p.NSEG == 1 ? p.state + (size_t)bh * K * V : p.ws_qseg + ((size_t)bh * p.NSEG + seg) * K * V;
     floatx4 S[NKT];
 #pragma unroll
     for (int kb = 0; kb < NKT; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) S[kb][i] = Sg[(size_t)(16 * kb + 4 * lg + i) * V + col];
+        for (int i = 0; i < 4; ++i) {
+            const int row = 16 * kb + 4 * lg + i;
+            S[kb][i] = OUT ? Sin[(size_t)row * V + col] : (pcol && row == col ? 1.f : 0.f);
+        }
 
     const floatx4 *__restrict__ W4 = reinterpret_cast<const floatx4 *>(p.ws_w);
     const floatx4 *__restrict__ Q4 = reinterpret_cast<const floatx4 *>(p.ws_qg);
@@ -544,27 +570,30 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
     const size_t cid0 = (size_t)bh * p.NC;
     const size_t uvf4 = (size_t)C * V / 4;
 
-    if (p.NC > 0) {
+    if (n1 > n0) {
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
-            sW[i * 256 + tid] = W4[cid0 * OPF4 + i * 256 + tid];
-            sQ[i * 256 + tid] = Q4[cid0 * OPF4 + i * 256 + tid];
+            sW[i * 256 + tid] = W4[(cid0 + n0) * OPF4 + i * 256 + tid];
+            if (OUT) sQ[i * 256 + tid] = Q4[(cid0 + n0) * OPF4 + i * 256 + tid];
         }
     }
 
     // row 4 lg of each 16-row tile; the rest of the row offset is wave-uniform
     float *ob = p.out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + col + (int64_t)(4 * lg) * p.sot;
-    for (int n = 0; n < p.NC; ++n) {
+    for (int n = n0; n < n1; ++n) {
         const size_t cid = cid0 + n;
         __syncthreads(); // sW, sQ hold chunk n; every wave is done with sKd, sA (n-1)
-        floatx4 kpre[PFO], apre[APF], u_cur[NT], g_cur = floatx4{0.f, 0.f, 0.f, 0.f};
+        floatx4 kpre[PFO], apre[OUT ? APF : 1], u_cur[NT], g_cur = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < PFO; ++i) kpre[i] = K4[cid * OPF4 + i * 256 + tid];
+        if (OUT) {
 #pragma unroll
-        for (int i = 0; i < APF; ++i) apre[i] = A4[cid * AF4 + i * 256 + tid];
+            for (int i = 0; i < APF; ++i) apre[i] = A4[cid * AF4 + i * 256 + tid];
+        }
         if (tid < K / 4) g_cur = G4[cid * (K / 4) + tid];
 #pragma unroll
-        for (int mt = 0; mt < NT; ++mt) u_cur[mt] = U4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
+        for (int mt = 0; mt < NT; ++mt)
+            u_cur[mt] = pcol ? floatx4{0.f, 0.f, 0.f, 0.f} : U4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
 
         // A: X1 = W S, X2 = scale (q exp(G)) S
         floatx4 X1[NT], X2[NT];
@@ -576,45 +605,34 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) {
                 wa[mt] = sW[(mt * NKT + kb) * 64 + lane];
-                ma[mt] = sQ[(mt * NKT + kb) * 64 + lane];
+                if (OUT) ma[mt] = sQ[(mt * NKT + kb) * 64 + lane];
             }
-            // eight independent accumulator chains per k-step
+            // eight (pass 1: four) independent accumulator chains per k-step
 #pragma unroll
-            for (int mt = 0; mt < NT; ++mt) {
-                X1[mt] = mfma16(wa[mt][0], S[kb][0], X1[mt]);
-                X2[mt] = mfma16(ma[mt][0], S[kb][0], X2[mt]);
-            }
+            for (int st = 0; st < 4; ++st)
 #pragma unroll
-            for (int mt = 0; mt < NT; ++mt) {
-                X1[mt] = mfma16(wa[mt][1], S[kb][1], X1[mt]);
-                X2[mt] = mfma16(ma[mt][1], S[kb][1], X2[mt]);
-            }
-#pragma unroll
-            for (int mt = 0; mt < NT; ++mt) {
-                X1[mt] = mfma16(wa[mt][2], S[kb][2], X1[mt]);
-                X2[mt] = mfma16(ma[mt][2], S[kb][2], X2[mt]);
-            }
-#pragma unroll
-            for (int mt = 0; mt < NT; ++mt) {
-                X1[mt] = mfma16(wa[mt][3], S[kb][3], X1[mt]);
-                X2[mt] = mfma16(ma[mt][3], S[kb][3], X2[mt]);
-            }
+                for (int mt = 0; mt < NT; ++mt) {
+                    X1[mt] = mfma16(wa[mt][st], S[kb][st], X1[mt]);
+                    if (OUT) X2[mt] = mfma16(ma[mt][st], S[kb][st], X2[mt]);
+                }
         }
 #pragma unroll
         for (int i = 0; i < PFO; ++i) sKd[i * 256 + tid] = kpre[i];
+        if (OUT) {
 #pragma unroll
-        for (int i = 0; i < APF; ++i) sA[i * 256 + tid] = apre[i];
+            for (int i = 0; i < APF; ++i) sA[i * 256 + tid] = apre[i];
+        }
         if (tid < K / 4) sGam[tid] = g_cur;
         __syncthreads(); // A done everywhere (sW, sQ free); sKd(n), sA(n) visible
 
         // W, q exp(G) of chunk n+1 (the last chunk re-fetches itself: harmless,
         // and unconditional loads keep the staging registers out of scratch)
-        const size_t cnx = cid + (n + 1 < p.NC ? 1 : 0);
-        floatx4 wpre[PFO], qpre[PFO];
+        const size_t cnx = cid + (n + 1 < n1 ? 1 : 0);
+        floatx4 wpre[PFO], qpre[OUT ? PFO : 1];
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
             wpre[i] = W4[cnx * OPF4 + i * 256 + tid];
-            qpre[i] = Q4[cnx * OPF4 + i * 256 + tid];
+            if (OUT) qpre[i] = Q4[cnx * OPF4 + i * 256 + tid];
         }
 
         // B: v_new = U - X1 (kept in X1)
@@ -622,21 +640,22 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
         for (int mt = 0; mt < NT; ++mt) X1[mt] = u_cur[mt] - X1[mt];
 
         // D: out = X2 + A_qk v_new (A_qk is lower block-triangular)
-        const int cv = min(C, p.T - n * C);
+        if (OUT) {
+            const int cv = min(C, p.T - n * C);
 #pragma unroll
-        for (int mt = 0; mt < NT; ++mt) {
-            floatx4 o = X2[mt];
+            for (int mt = 0; mt < NT; ++mt) {
+                floatx4 o = X2[mt];
 #pragma unroll
-            for (int qt = 0; qt <= mt; ++qt) {
-                const floatx4 aa = sA[(mt * NT + qt) * 64 + lane];
-                o = mfma16(aa[0], X1[qt][0], o);
-                o = mfma16(aa[1], X1[qt][1], o);
-                o = mfma16(aa[2], X1[qt][2], o);
-                o = mfma16(aa[3], X1[qt][3], o);
-            }
+                for (int qt = 0; qt <= mt; ++qt) {
+                    const floatx4 aa = sA[(mt * NT + qt) * 64 + lane];
+                    o = mfma16(aa[0], X1[qt][0], o);
+                    o = mfma16(aa[1], X1[qt][1], o);
+                    o = mfma16(aa[2], X1[qt][2], o);
+                    o = mfma16(aa[3], X1[qt][3], o);
+                }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (16 * mt + 4 * lg + i < cv) ob[(int64_t)(n * C + 16 * mt + i) * p.sot] = o[i];
+                for (int i = 0; i < 4; ++i)
+                    if (16 * mt + 4 * lg + i < cv) ob[(int64_t)(n * C + 16 * mt + i) * p.sot] = o[i];
             }
         }
 
@@ -667,13 +686,82 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p) {
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
             sW[i * 256 + tid] = wpre[i];
-            sQ[i * 256 + tid] = qpre[i];
+            if (OUT) sQ[i * 256 + tid] = qpre[i];
         }
     }
+
+    // leaving state: the final state (last segment), Q_j or P_j (pass 1)
+    float *Sout = nullptr;
+    int ld = V;
+    if (OUT) {
+        if (seg == p.NSEG - 1) Sout = p.state + (size_t)bh * K * V;
+    } else if (pcol) {
+        Sout = p.ws_pseg + ((size_t)bh * (p.NSEG - 1) + seg) * K * K;
+        ld = K;
+    } else {
+        Sout = p.ws_qseg + ((size_t)bh * p.NSEG + seg + 1) * K * V;
+    }
+    if (Sout) {
+#pragma unroll
+        for (int kb = 0; kb < NKT; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Sout[(size_t)(16 * kb + 4 * lg + i) * ld + col] = S[kb][i];
+    }
+}
+
+// Pass 2 of the segmented form.  ws_qseg holds NSEG slots of K x V per
+// (b, hv): slot 0 <- S0, then slot j + 1 (Q_j from pass 1) <- S_in(j + 1) =
+// P_j S_in(j) + Q_j for j = 0 .. NSEG - 2.  One workgroup per (b, hv, 64 value
+// columns); S in MFMA accumulators, P_j read as A-operand fragments
+// (lane (g, r): row r of a 16-row tile, columns 4g .. 4g + 3) from L2.
+template <int K>
+__global__ __launch_bounds__(256, 1) void chunk_chain_kernel(ChunkParams p) {
+    constexpr int NKT = K / 16;
+    const int V = p.V, nvv = V / 64;
+    int bh, vs;
+    inter_block(blockIdx.x, p.B * p.HV, nvv, &bh, &vs);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
+    const int col = 16 * (vs * 4 + wave) + lr;
+
+    const float *S0 = p.state + (size_t)bh * K * V;
+    float *slot0 = p.ws_qseg + (size_t)bh * p.NSEG * K * V;
+    floatx4 S[NKT];
 #pragma unroll
     for (int kb = 0; kb < NKT; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) Sg[(size_t)(16 * kb + 4 * lg + i) * V + col] = S[kb][i];
+        for (int i = 0; i < 4; ++i) {
+            const size_t o = (size_t)(16 * kb + 4 * lg + i) * V + col;
+            S[kb][i] = S0[o];
+            slot0[o] = S[kb][i];
+        }
+    for (int j = 0; j + 1 < p.NSEG; ++j) {
+        const float *P = p.ws_pseg + ((size_t)bh * (p.NSEG - 1) + j) * K * K;
+        float *Q = slot0 + (size_t)(j + 1) * K * V;
+        floatx4 N[NKT];
+#pragma unroll
+        for (int it = 0; it < NKT; ++it)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) N[it][i] = Q[(size_t)(16 * it + 4 * lg + i) * V + col];
+#pragma unroll
+        for (int kb = 0; kb < NKT; ++kb) {
+            floatx4 pa[NKT];
+#pragma unroll
+            for (int it = 0; it < NKT; ++it)
+                pa[it] = *reinterpret_cast<const floatx4 *>(P + (size_t)(16 * it + lr) * K + 16 * kb + 4 * lg);
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int it = 0; it < NKT; ++it) N[it] = mfma16(pa[it][st], S[kb][st], N[it]);
+        }
+#pragma unroll
+        for (int it = 0; it < NKT; ++it) {
+            S[it] = N[it];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Q[(size_t)(16 * it + 4 * lg + i) * V + col] = N[it][i];
+        }
+    }
 }
 
 template <int K, int V>
@@ -685,7 +773,18 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
         if (e != hipSuccess) return e;
     }
     if (phases & 2) {
-        hipLaunchKernelGGL((chunk_inter_kernel<K>), dim3(p.B * p.HV * (V / 64)), dim3(256), 0, s, p);
+        const int seqs = p.B * p.HV;
+        if (p.NSEG > 1) {
+            hipLaunchKernelGGL((chunk_inter_kernel<K, false>), dim3(seqs * (p.NSEG - 1) * ((V + K) / 64)), dim3(256),
+                               0, s, p, p.NSEG - 1);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL((chunk_chain_kernel<K>), dim3(seqs * (V / 64)), dim3(256), 0, s, p);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL((chunk_inter_kernel<K, true>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0, s, p,
+                           p.NSEG);
         return hipGetLastError();
     }
     return hipSuccess;
@@ -714,12 +813,36 @@ using namespace gdn2;
 namespace {
 
 struct WsLayout {
-    size_t w, qg, u, aqk, kdt, gam, total;
+    size_t w, qg, u, aqk, kdt, gam, pseg, qseg, total;
 };
+
+// Segments per sequence for chunk-inter.  Few long sequences are split so
+// that the output pass runs about one workgroup per compute unit (an MI355X
+// has 256); a segment keeps at least 16 chunks, so that the two extra passes
+// stay small against the work they spread.
+constexpr int64_t kInterWorkgroups = 256;
+constexpr int64_t kMinSegmentChunks = 16;
+
+struct Segments {
+    int nseg, segl;
+};
+
+Segments inter_segments(int64_t B, int64_t HV, int64_t V, int64_t NC) {
+    const int64_t w = B * HV * (V / 64);
+    if (w <= 0 || NC <= 0) return {1, (int)NC}; // (K, V) outside the chunk kernels, or no tokens
+    int64_t n = kInterWorkgroups / w;
+    if (n > NC / kMinSegmentChunks) n = NC / kMinSegmentChunks;
+    if (n < 2) return {1, (int)NC};
+    const int64_t L = (NC + n - 1) / n;
+    return {(int)((NC + L - 1) / L), (int)L};
+}
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-WsLayout ws_layout(int64_t nchunks, int64_t K, int64_t V) {
+WsLayout ws_layout(int64_t seqs, int64_t NC, int64_t K, int64_t V) {
+    const int64_t nchunks = seqs * NC;
+    const int64_t nseg = inter_segments(seqs, 1, V, NC).nseg;
+    const int64_t np = nseg > 1 ? seqs * (nseg - 1) : 0, nq = nseg > 1 ? seqs * nseg : 0;
     WsLayout L;
     size_t off = 0;
     L.w = off; off = align256(off + sizeof(float) * nchunks * kChunk * K);
@@ -728,12 +851,14 @@ WsLayout ws_layout(int64_t nchunks, int64_t K, int64_t V) {
     L.aqk = off; off = align256(off + sizeof(float) * nchunks * kChunk * kChunk);
     L.kdt = off; off = align256(off + sizeof(float) * nchunks * kChunk * K);
     L.gam = off; off = align256(off + sizeof(float) * nchunks * K);
+    L.pseg = off; off = align256(off + sizeof(float) * np * K * K);
+    L.qseg = off; off = align256(off + sizeof(float) * nq * K * V);
     L.total = off;
     return L;
 }
 
-int64_t num_chunks(const gdn2_chunk_args *a) {
-    return a->batch * a->num_v_heads * ((a->seq_len + kChunk - 1) / kChunk);
+WsLayout ws_layout(const gdn2_chunk_args *a) {
+    return ws_layout(a->batch * a->num_v_heads, (a->seq_len + kChunk - 1) / kChunk, a->head_dim, a->head_v_dim);
 }
 
 bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
@@ -743,7 +868,7 @@ bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 extern "C" size_t gdn2_chunk_workspace_bytes(const gdn2_chunk_args *a) {
     if (!a || a->batch <= 0 || a->num_v_heads <= 0 || a->seq_len <= 0 || a->head_dim <= 0 || a->head_v_dim <= 0)
         return 0;
-    return ws_layout(num_chunks(a), a->head_dim, a->head_v_dim).total;
+    return ws_layout(a).total;
 }
 
 // fused_chunk_forward (src/kernel/chunk_cube.rs:781-952) / chunk_wy_forward
@@ -772,7 +897,7 @@ static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, in
         ((kChunk - 1) * a->stride_vw_t + a->head_v_dim) * 4 >= (int64_t(1) << 31))
         return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_fwd_f32: token strides outside the chunk kernels' range");
     if (a->seq_len == 0) return GDN2_OK;
-    const WsLayout L = ws_layout(num_chunks(a), a->head_dim, a->head_v_dim);
+    const WsLayout L = ws_layout(a);
     if (!a->workspace || a->workspace_bytes < L.total || (reinterpret_cast<uintptr_t>(a->workspace) & 255u))
         return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: workspace missing, too small or not 256-byte aligned");
     ChunkParams p{};
@@ -792,6 +917,11 @@ static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, in
     p.ws_aqk = reinterpret_cast<float *>(ws + L.aqk);
     p.ws_kdt = reinterpret_cast<float *>(ws + L.kdt);
     p.ws_gam = reinterpret_cast<float *>(ws + L.gam);
+    p.ws_pseg = reinterpret_cast<float *>(ws + L.pseg);
+    p.ws_qseg = reinterpret_cast<float *>(ws + L.qseg);
+    const Segments sg = inter_segments(p.B * p.HV, 1, p.V, p.NC);
+    p.NSEG = sg.nseg;
+    p.SEGL = sg.segl;
     GDN2_HIP_CHECK(launch_chunk(p, (hipStream_t)stream, phases));
     return GDN2_OK;
 }

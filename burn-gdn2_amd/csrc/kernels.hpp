@@ -57,6 +57,12 @@ struct ChunkParams {
     float *ws_aqk; // C*C   A_qk (scale included, zero above the diagonal), A-operand tiles (row tile, col tile)
     float *ws_kdt; // K*C   (k * exp(G_last - G))^T, A-operand tiles (key tile, time tile)
     float *ws_gam; // K     exp(G_last)
+    // Segmented recurrence for few long sequences (NSEG > 1): the chunks of a
+    // sequence are split into NSEG runs of SEGL chunks.  Per (b, hv):
+    float *ws_pseg; // (NSEG-1) x K*K  transition of segments 0 .. NSEG-2 (row-major)
+    float *ws_qseg; // NSEG x K*V      state entering each segment (slot j + 1 first
+                    //                 holds segment j's state from S = 0)
+    int NSEG, SEGL;
 };
 
 // Projection epilogue: raw Linear outputs -> kernel inputs, one token per

@@ -37,3 +37,33 @@ def test_library_has_no_oracle_dependency():
 
     data = open(_capi.LIB_PATH, "rb").read()
     assert b"gdn2o_" not in data and b"libgdn2_oracle" not in data
+
+
+def _chunk_ws(B, HV, T, K, V):
+    from gdn2_amd import _capi
+
+    lib = ctypes.CDLL(_capi.LIB_PATH)
+    lib.gdn2_chunk_workspace_bytes.restype = ctypes.c_size_t
+    lib.gdn2_chunk_workspace_bytes.argtypes = [ctypes.POINTER(_capi.ChunkArgs)]
+    a = _capi.ChunkArgs()
+    a.batch, a.num_heads, a.num_v_heads, a.seq_len, a.head_dim, a.head_v_dim = B, HV, HV, T, K, V
+    a.chunk_size = 64
+    return lib.gdn2_chunk_workspace_bytes(ctypes.byref(a))
+
+
+def _per_chunk_ws(B, HV, T, K, V):
+    al = lambda x: (x + 255) // 256 * 256
+    n = B * HV * ((T + 63) // 64)
+    return sum(al(4 * n * e) for e in (64 * K, 64 * K, 64 * V, 64 * 64, 64 * K, K))
+
+
+def test_chunk_workspace_sizes():
+    """Host-only sizing: the per-chunk buffers, plus the segment buffers
+    (transitions and entering states) only for few long sequences; shapes
+    outside the kernels' instances size without faulting."""
+    assert _chunk_ws(8, 16, 4096, 128, 128) == _per_chunk_ws(8, 16, 4096, 128, 128)
+    # 1 x 16 heads x 65536 tokens: eight segments of 128 chunks
+    seg = _chunk_ws(1, 16, 65536, 128, 128) - _per_chunk_ws(1, 16, 65536, 128, 128)
+    assert seg == 4 * 16 * (7 * 128 * 128 + 8 * 128 * 128)
+    assert _chunk_ws(1, 1, 20, 16, 8) > 0
+    assert _chunk_ws(0, 1, 20, 128, 128) == 0

@@ -59,6 +59,50 @@ def test_chunk_matches_recurrence(gpu, case):
         assert maxabs(o.cpu().numpy(), o32) < TOL and maxabs(S.cpu().numpy(), S32) < TOL
 
 
+def _base_workspace_bytes(B, HV, T, K, V):
+    """Workspace of the per-chunk buffers alone (W, q e^G, U, A_qk, Kd^T, e^G_last)."""
+    al = lambda x: (x + 255) // 256 * 256
+    n = B * HV * ((T + 63) // 64)
+    return sum(al(4 * n * e) for e in (64 * K, 64 * K, 64 * V, 64 * 64, 64 * K, K))
+
+
+SEG_CASES = [
+    # few long sequences: chunk-inter splits each sequence into segments.  Slow
+    # decays keep a segment's transition P far from 0 (exp(g * 1280) ~ 0.02-0.5
+    # over a 20-chunk segment), so that S0 and the chaining both reach the output.
+    (1, 2, 2, 2530, 128, 128, (-0.003, -0.0005), 1.0, 1.0),  # 40 chunks, ragged end
+    (1, 1, 2, 6400, 64, 128, (-0.002, 0.0), 2.0, 1.0),       # GVA, negative eigenvalues, 100 chunks
+    (1, 2, 2, 2100, 128, 128, (-0.3, -0.02), 1.0, 0.5),
+    (1, 2, 2, 2560, 128, 128, (-0.001, 0.0), 0.0, 1.0),      # b = 0: P = diag(exp(G)) ~ 0.3-1, S0 carried whole
+    (1, 1, 1, 4100, 128, 256, (-5.0, -0.5), 1.0, 1.0),       # strong decay, V = 2K
+]
+
+
+@pytest.mark.parametrize("case", SEG_CASES, ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}" for c in SEG_CASES])
+def test_chunk_segmented_matches_recurrence(gpu, case):
+    """Segmented chunk-inter (per-segment transition, chained entering
+    states, output pass) == the per-token recurrence, with nonzero S0."""
+    import torch
+
+    import gdn2_amd
+
+    B, Hk, HV, T, K, V, (glo, ghi), bhi, s0 = case
+    rng = np.random.default_rng(2000 + T + K + V)
+    q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=glo, g_hi=ghi, b_hi=bhi)
+    q *= K ** -0.5 * 4
+    S0 = (rng.standard_normal((B, HV, K, V)) * s0).astype(np.float32)
+    scale = K ** -0.5
+    o_ref, S_ref = O.recurrent_f64(q, k, v, g, b, w, S0=S0, scale=scale)
+    d = _dev(gpu, q, k, v, g, b, w, S0)
+    out = torch.empty((B, HV, T, V), device=gpu)
+    # the segment buffers are present: the segmented form runs for this shape
+    assert gdn2_amd.chunk_workspace_bytes(*d, out, scale, 64) > _base_workspace_bytes(B, HV, T, K, V)
+    o, S = gdn2_amd.chunk_wy_forward(*d, scale, chunk_size=64)
+    eo, es = maxabs(o.cpu().numpy(), o_ref), maxabs(S.cpu().numpy(), S_ref)
+    print(f"max|out err|={eo:.2e} max|S err|={es:.2e}")
+    assert eo < TOL and es < TOL
+
+
 def test_chunk_strided_views_and_in_place_state(gpu):
     """q/k/g/b/v/w as [B, H, T, D] views of [B, T, H, D] storage and out
     written straight into [B, T, HV, V] (no permute copies)."""
