@@ -8,6 +8,11 @@
  * Contents and the reference code each function restates:
  *   gdn2o_recurrent_f64   per-token scan, evaluated in double
  *                         (src/kernel/fused_recurrent.rs:27-52)     -- ground truth
+ *   gdn2o_recurrent_bwd_f64  its adjoint (gradients of q, k, g, b, v, w,
+ *                         S0), in double -- the gradients the reference's
+ *                         training path gets from autodiff of the same scan
+ *                         (tests/autodiff.rs:153-206; WIP fused backward
+ *                         src/kernel/chunk_adjoint_cube.rs:464-707)
  *   gdn2o_recurrent_f32   the same scan with the reference's f32 op order
  *                         (src/kernel/fused_recurrent.rs:25-52)
  *   gdn2o_chunk_wy_f32    chunked WY forward with tile-local (16) log-space
@@ -28,6 +33,9 @@
  *   recurrent_f64/f32  closed forms (b=0,g=0 linear attention; T=1 rank-1
  *                      step; b=0 gated linear attention), golden vectors of
  *                      the reference's own torch model (tests/golden/)
+ *   recurrent_bwd_f64  central finite differences of recurrent_f64 on
+ *                      every input (tests/test_oracle_bwd.py); the
+ *                      b=0, g=0 closed form
  *   chunk_wy_f32       chunk == recurrence invariant for C in {4..128},
  *                      ragged T, non-zero S0, broadcast g/b
  *   short_conv         brute-force convolution on tiny inputs + cache
@@ -129,6 +137,144 @@ GDN2O_EXPORT void gdn2o_recurrent_f64(const float *q, const float *k, const floa
         if (S_out) memcpy(S_out + (size_t)bh * K * V, S, sizeof(double) * (size_t)K * V);
         free(S);
         free(vnew);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Adjoint of the per-token recurrence above, in double: the exact gradient  */
+/* of L = sum(d_out * out) + sum(d_ST * S_T) with respect to q, k, g, b, v,  */
+/* w and S0.  The reference's training path differentiates the same          */
+/* recurrence through burn's autodiff (tests/autodiff.rs:153-206), and its   */
+/* WIP fused backward (src/kernel/chunk_adjoint_cube.rs:464-707) returns      */
+/* the same seven gradients.  Per token t, backwards (S1 = diag(e^g) S_prev, */
+/* kb = b*k, S2 = S1 + k vnew^T = S_t):                                      */
+/*   dS2 = dS + scale q dO^T;  dq = scale S2 dO                               */
+/*   dk += dS2 vnew;  dvnew = dS2^T k;  dw = dvnew*v;  dv = dvnew*w          */
+/*   dS1 = dS2 - kb dvnew^T;  dkb = -S1 dvnew;  db = dkb*k;  dk += dkb*b     */
+/*   dg = rowsum(dS1 * S1);  dS = diag(e^g) dS1                               */
+/* Key-side gradients (dq, dk, dg, db) of a key head sum over its value      */
+/* heads; with gdim / bdim = 1 they sum over channels.  d_ST may be NULL     */
+/* (zero).  dS0 receives the gradient of S0 (zero S0 when S0 is NULL).       */
+/* ------------------------------------------------------------------------ */
+GDN2O_EXPORT void gdn2o_recurrent_bwd_f64(const float *q, const float *k, const float *v, const float *g,
+                                          const float *b, const float *w, const double *S0, const double *d_out,
+                                          const double *d_ST, int B, int HV, int Hk, int T, int K, int V, int gdim,
+                                          int bdim, double scale, double *dq, double *dk, double *dg, double *db,
+                                          double *dv, double *dw, double *dS0) {
+    const int rep = HV / Hk;
+    memset(dq, 0, sizeof(double) * (size_t)B * Hk * T * K);
+    memset(dk, 0, sizeof(double) * (size_t)B * Hk * T * K);
+    memset(dg, 0, sizeof(double) * (size_t)B * Hk * T * gdim);
+    memset(db, 0, sizeof(double) * (size_t)B * Hk * T * bdim);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int bk = 0; bk < B * Hk; ++bk) {
+        const int bi = bk / Hk, hk = bk % Hk;
+        const size_t KV = (size_t)K * V;
+        double *Sall = (double *)malloc(sizeof(double) * KV * (size_t)(T + 1));
+        double *S1 = (double *)malloc(sizeof(double) * KV);
+        double *dS = (double *)malloc(sizeof(double) * KV);
+        double *vnew = (double *)malloc(sizeof(double) * (size_t)V);
+        double *dvn = (double *)malloc(sizeof(double) * (size_t)V);
+        double *eg = (double *)malloc(sizeof(double) * (size_t)K);
+        double *kb = (double *)malloc(sizeof(double) * (size_t)K);
+        for (int hv = hk * rep; hv < (hk + 1) * rep; ++hv) {
+            const size_t bh = (size_t)bi * HV + hv;
+            /* forward, keeping every state S_0 .. S_T */
+            if (S0)
+                memcpy(Sall, S0 + bh * KV, sizeof(double) * KV);
+            else
+                memset(Sall, 0, sizeof(double) * KV);
+            for (int t = 0; t < T; ++t) {
+                const float *kt = k + idx4(bi, Hk, hk, T, t, K, 0);
+                const float *gt = g + idx4(bi, Hk, hk, T, t, gdim, 0);
+                const float *bt = b + idx4(bi, Hk, hk, T, t, bdim, 0);
+                const float *vt = v + idx4(bi, HV, hv, T, t, V, 0);
+                const float *wt = w + idx4(bi, HV, hv, T, t, V, 0);
+                const double *Sp = Sall + (size_t)t * KV;
+                double *Sn = Sall + (size_t)(t + 1) * KV;
+                for (int i = 0; i < K; ++i) {
+                    const double e = exp((double)gt[i % gdim]);
+                    for (int j = 0; j < V; ++j) Sn[(size_t)i * V + j] = Sp[(size_t)i * V + j] * e;
+                }
+                for (int j = 0; j < V; ++j) vnew[j] = (double)wt[j] * (double)vt[j];
+                for (int i = 0; i < K; ++i) {
+                    const double bki = (double)bt[i % bdim] * (double)kt[i];
+                    for (int j = 0; j < V; ++j) vnew[j] -= Sn[(size_t)i * V + j] * bki;
+                }
+                for (int i = 0; i < K; ++i)
+                    for (int j = 0; j < V; ++j) Sn[(size_t)i * V + j] += (double)kt[i] * vnew[j];
+            }
+            /* backward */
+            if (d_ST)
+                memcpy(dS, d_ST + bh * KV, sizeof(double) * KV);
+            else
+                memset(dS, 0, sizeof(double) * KV);
+            for (int t = T - 1; t >= 0; --t) {
+                const float *qt = q + idx4(bi, Hk, hk, T, t, K, 0);
+                const float *kt = k + idx4(bi, Hk, hk, T, t, K, 0);
+                const float *gt = g + idx4(bi, Hk, hk, T, t, gdim, 0);
+                const float *bt = b + idx4(bi, Hk, hk, T, t, bdim, 0);
+                const float *vt = v + idx4(bi, HV, hv, T, t, V, 0);
+                const float *wt = w + idx4(bi, HV, hv, T, t, V, 0);
+                const double *dOt = d_out + idx4(bi, HV, hv, T, t, V, 0);
+                const double *Sp = Sall + (size_t)t * KV, *S2 = Sall + (size_t)(t + 1) * KV;
+                double *dqt = dq + idx4(bi, Hk, hk, T, t, K, 0), *dkt = dk + idx4(bi, Hk, hk, T, t, K, 0);
+                double *dgt = dg + idx4(bi, Hk, hk, T, t, gdim, 0), *dbt = db + idx4(bi, Hk, hk, T, t, bdim, 0);
+                double *dvt = dv + idx4(bi, HV, hv, T, t, V, 0), *dwt = dw + idx4(bi, HV, hv, T, t, V, 0);
+                for (int i = 0; i < K; ++i) {
+                    eg[i] = exp((double)gt[i % gdim]);
+                    kb[i] = (double)bt[i % bdim] * (double)kt[i];
+                    for (int j = 0; j < V; ++j) S1[(size_t)i * V + j] = Sp[(size_t)i * V + j] * eg[i];
+                }
+                for (int j = 0; j < V; ++j) vnew[j] = (double)wt[j] * (double)vt[j];
+                for (int i = 0; i < K; ++i)
+                    for (int j = 0; j < V; ++j) vnew[j] -= S1[(size_t)i * V + j] * kb[i];
+                /* o_t = scale S2^T q_t */
+                for (int i = 0; i < K; ++i) {
+                    double a = 0.0;
+                    for (int j = 0; j < V; ++j) {
+                        dS[(size_t)i * V + j] += scale * (double)qt[i] * dOt[j];
+                        a += S2[(size_t)i * V + j] * dOt[j];
+                    }
+                    dqt[i] += scale * a;
+                }
+                /* S2 = S1 + k vnew^T */
+                for (int j = 0; j < V; ++j) dvn[j] = 0.0;
+                for (int i = 0; i < K; ++i) {
+                    double a = 0.0;
+                    for (int j = 0; j < V; ++j) {
+                        a += dS[(size_t)i * V + j] * vnew[j];
+                        dvn[j] += dS[(size_t)i * V + j] * (double)kt[i];
+                    }
+                    dkt[i] += a;
+                }
+                /* vnew = w v - S1^T kb */
+                for (int j = 0; j < V; ++j) {
+                    dwt[j] = dvn[j] * (double)vt[j];
+                    dvt[j] = dvn[j] * (double)wt[j];
+                }
+                for (int i = 0; i < K; ++i) {
+                    double dkb = 0.0, dgi = 0.0;
+                    for (int j = 0; j < V; ++j) {
+                        dkb -= S1[(size_t)i * V + j] * dvn[j];
+                        dS[(size_t)i * V + j] -= kb[i] * dvn[j];
+                        dgi += dS[(size_t)i * V + j] * S1[(size_t)i * V + j];
+                        dS[(size_t)i * V + j] *= eg[i];
+                    }
+                    dbt[i % bdim] += dkb * (double)kt[i];
+                    dkt[i] += dkb * (double)bt[i % bdim];
+                    dgt[i % gdim] += dgi;
+                }
+            }
+            memcpy(dS0 + bh * KV, dS, sizeof(double) * KV);
+        }
+        free(Sall);
+        free(S1);
+        free(dS);
+        free(vnew);
+        free(dvn);
+        free(eg);
+        free(kb);
     }
 }
 

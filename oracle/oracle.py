@@ -47,6 +47,7 @@ def lib():
         i, d = ctypes.c_int, ctypes.c_double
         L.gdn2o_recurrent_f64.argtypes = [_vp] * 7 + [i] * 8 + [d, _vp, _vp]
         L.gdn2o_recurrent_f32.argtypes = [_vp] * 7 + [i] * 8 + [d, _vp, _vp]
+        L.gdn2o_recurrent_bwd_f64.argtypes = [_vp] * 9 + [i] * 8 + [d] + [_vp] * 7
         L.gdn2o_chunk_wy_f32.argtypes = [_vp] * 7 + [i] * 8 + [d, i, _vp, _vp]
         L.gdn2o_short_conv.argtypes = [_vp, _vp, _vp, i, i, i, _vp, _vp]
         L.gdn2o_l2norm_rows.argtypes = [_vp, ctypes.c_long, i, d]
@@ -97,6 +98,26 @@ def recurrent_f64(q, k, v, g, b, w, S0=None, scale=1.0):
     lib().gdn2o_recurrent_f64(*(_ptr(a) for a in (q, k, v, g, b, w, S0)), B, HV, Hk, T, K, V, gdim, bdim,
                               float(scale), _ptr(out), _ptr(S))
     return out, S
+
+
+def recurrent_bwd_f64(q, k, v, g, b, w, d_out, S0=None, d_ST=None, scale=1.0):
+    """Adjoint of the per-token scan in double: gradients of
+    L = sum(d_out * out) + sum(d_ST * S_T) (the gradients the reference's
+    training path takes through autodiff of the same scan, tests/autodiff.rs:153-206;
+    the seven outputs of src/kernel/chunk_adjoint_cube.rs:464-707).
+    Returns dict dq, dk, dg, db (key-head shapes of q, k, g, b), dv, dw, dS0."""
+    q, k, v, g, b, w = (_c(a, np.float32) for a in (q, k, v, g, b, w))
+    B, HV, Hk, T, K, V, gdim, bdim = _scan_shapes(q, k, v, g, b, w)
+    S0 = None if S0 is None else _c(S0, np.float64)
+    d_out = _c(d_out, np.float64)
+    assert d_out.shape == (B, HV, T, V)
+    d_ST = None if d_ST is None else _c(d_ST, np.float64)
+    r = {"dq": np.empty(q.shape), "dk": np.empty(k.shape), "dg": np.empty(g.shape), "db": np.empty(b.shape),
+         "dv": np.empty(v.shape), "dw": np.empty(w.shape), "dS0": np.empty((B, HV, K, V))}
+    lib().gdn2o_recurrent_bwd_f64(*(_ptr(a) for a in (q, k, v, g, b, w, S0, d_out, d_ST)), B, HV, Hk, T, K, V,
+                                  gdim, bdim, float(scale), *(_ptr(r[n]) for n in ("dq", "dk", "dg", "db", "dv",
+                                                                                   "dw", "dS0")))
+    return r
 
 
 def recurrent_f32(q, k, v, g, b, w, S0=None, scale=1.0):
