@@ -29,84 +29,25 @@
 // k = 4*(lane/16) + step inside a 16-wide block it is directly the B operand
 // of the next product.  The solve, A_qk [W|U] and, in the inter kernel, the
 // state S and v_new therefore never leave registers.
-#include "common.hpp"
-#include "kernels.hpp"
+#include "chunk_common.hpp"
 
 namespace gdn2 {
 
 namespace {
 
-constexpr int C = kChunk;
-constexpr int NT = C / 16;
 static_assert(NT == 4, "the diagonal-block inverse maps 4 tiles x 16 columns onto one wave");
 constexpr float kSafeSpan = 96.0f; // log2 units
 
-// Rows [0, valid) of a row-strided f32 matrix (row stride rs, rowlen
-// elements used per row) as a buffer resource.  The hardware's range check
-// returns 0 for every load past the last valid row, which is the zero padding
-// of a ragged last chunk (src/forward.rs:94-99), so a load needs neither a
-// clamp nor a mask, and its offset is a 32-bit element index.  Requires
-// rs >= rowlen and ((valid - 1) rs + rowlen) * 4 < 2^31 (checked on the host).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float *base, int rs, int valid, int rowlen) {
-    const int bytes = ((valid - 1) * rs + rowlen) * 4;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, bytes, 0x00020000);
-}
-
-__device__ __forceinline__ float bld1(__amdgpu_buffer_rsrc_t r, int idx) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, idx * 4, 0, 0));
-}
-
-__device__ __forceinline__ floatx4 bld4(__amdgpu_buffer_rsrc_t r, int idx) {
-    return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, idx * 4, 0, 0));
-}
-
-__device__ __forceinline__ floatx4 mfma4(float4 a, floatx4 b, floatx4 c) {
-    c = mfma16(a.x, b[0], c);
-    c = mfma16(a.y, b[1], c);
-    c = mfma16(a.z, b[2], c);
-    c = mfma16(a.w, b[3], c);
-    return c;
-}
-
-// D = X^T for an accumulator tile X, i.e. the A-operand layout of X
-// (lane (g, r) gets X[r][4g..4g+3]): the accumulator is a valid A operand
-// of X^T under the k = 4g + step labelling, multiplied by the identity.
-// Exact in f32 (products with 1 and 0).
-__device__ __forceinline__ floatx4 transpose16(floatx4 x, int lr, int lg) {
-    floatx4 d = floatx4{0.f, 0.f, 0.f, 0.f};
-    d = mfma16(x[0], lr == 4 * lg + 0 ? 1.f : 0.f, d);
-    d = mfma16(x[1], lr == 4 * lg + 1 ? 1.f : 0.f, d);
-    d = mfma16(x[2], lr == 4 * lg + 2 ? 1.f : 0.f, d);
-    d = mfma16(x[3], lr == 4 * lg + 3 ? 1.f : 0.f, d);
-    return d;
-}
-
-__device__ __forceinline__ floatx4 mfma4n(float4 a, floatx4 b, floatx4 c) {
-    c = mfma16(-a.x, b[0], c);
-    c = mfma16(-a.y, b[1], c);
-    c = mfma16(-a.z, b[2], c);
-    c = mfma16(-a.w, b[3], c);
-    return c;
-}
-
 // ---------------------------------------------------------------------------
-// chunk-intra: one workgroup (4 waves) per (b, hv, chunk).
+// chunk-intra: one workgroup (8 waves) per (b, hv, chunk).
 // Every global load of a phase is issued before that phase's arithmetic
 // (g and k at the start, q / b rows before the score tiles, the right-hand
 // sides of row tile p+1 while tile p is solved, k for Kd^T in one batch), so
 // that a workgroup pays a handful of memory round trips instead of one per
 // loop iteration.
 // ---------------------------------------------------------------------------
-// Streaming store: the workspace is read back by chunk-inter much later, so
-// keeping it out of L2 leaves room for the chunk's inputs, which chunk-intra
-// reads more than once.
-__device__ __forceinline__ void st_stream(floatx4 *dst, floatx4 v) { __builtin_nontemporal_store(v, dst); }
-
-__device__ __forceinline__ floatx4 exp2v(floatx4 x) {
-    return floatx4{fast_exp2(x[0]), fast_exp2(x[1]), fast_exp2(x[2]), fast_exp2(x[3])};
-}
-
-template <int K, int V>
+// TRAIN adds the backward's operands (ws_wt, ws_qgt, ws_kd, ws_aqkt, ws_akk).
+template <int K, int V, bool TRAIN>
 __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
     constexpr int NW = 8; // waves per workgroup; two workgroups per CU = four waves per SIMD
     constexpr int KP = K + 4, CP = C + 4;
@@ -208,6 +149,17 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
             st_stream(Kf + f * 64 + lane, val);
         }
         if (tid < K) p.ws_gam[cid * K + tid] = fast_exp2(sG[C - 1][tid]);
+        if (TRAIN) { // Kd as A-operand fragments (tt, kb): lane (g, r) holds Kd[16 tt + r][16 kb + 4 g + j]
+            floatx4 *Kdf = reinterpret_cast<floatx4 *>(p.ws_kd) + cid * (C * K / 4);
+#pragma unroll
+            for (int j = 0; j < KDF; ++j) {
+                const int f = wave + NW * j, tt = f / NKT, kb = f % NKT, c0 = 16 * kb + 4 * lg, t = 16 * tt + lr;
+                const floatx4 gl = *reinterpret_cast<const floatx4 *>(&sG[C - 1][c0]);
+                const floatx4 gt = *reinterpret_cast<const floatx4 *>(&sG[t][c0]);
+                const floatx4 kt = *reinterpret_cast<const floatx4 *>(&sK[t][c0]);
+                st_stream(Kdf + f * 64 + lane, kt * exp2v(gl - gt));
+            }
+        }
     }
     for (int idx = tid; idx < NT * K; idx += 512) {
         const int pt = idx / K, c = idx % K;
@@ -252,7 +204,14 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
                 floatx4 a = araw[pi][m] * (mat == 1 ? kr : floatx4{1.f, 1.f, 1.f, 1.f});
                 a *= exp2v(gr - gb);
                 // scale q exp(G_r): the sequential kernel's A operand, fragment (pt, m0 + m)
-                if (mat == 0) st_stream(QGf + (pt * NKT + m0 + m) * 64 + lane, a * exp2v(gb) * p.scale);
+                if (mat == 0) {
+                    const floatx4 qg = a * exp2v(gb) * p.scale;
+                    st_stream(QGf + (pt * NKT + m0 + m) * 64 + lane, qg);
+                    if (TRAIN) // (q exp(G))^T fragment (m0 + m, pt)
+                        st_stream(reinterpret_cast<floatx4 *>(p.ws_qgt) + cid * (C * K / 4) +
+                                      ((m0 + m) * NT + pt) * 64 + lane,
+                                  transpose16(qg, lr, lg));
+                }
                 const uint32_t mw = sMask[pt][c0 >> 5] >> (c0 & 31);
 #pragma unroll
                 for (int q = 0; q < NT; ++q) {
@@ -403,6 +362,25 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
             if (qt > mt) val = floatx4{0.f, 0.f, 0.f, 0.f};
             st_stream(Af + f * 64 + lane, val);
         }
+        if (TRAIN) {
+            // A_qk^T fragments (st, rt): lane (g, r) holds A_qk[16 rt + 4 g + j][16 st + r]
+            floatx4 *ATf = reinterpret_cast<floatx4 *>(p.ws_aqkt) + cid * (C * C / 4);
+#pragma unroll
+            for (int j = 0; j < NT * NT / NW; ++j) {
+                const int f = wave + NW * j, st = f / NT, rt = f % NT;
+                floatx4 val = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (rt >= st)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) val[i] = sAqk[16 * rt + 4 * lg + i][16 * st + lr];
+                st_stream(ATf + f * 64 + lane, val);
+            }
+            // A_kk row-major, strictly lower (the upper blocks of sAkk are never written)
+            float *Akf = p.ws_akk + cid * (C * C);
+            for (int idx = tid; idx < C * C; idx += 512) {
+                const int r = idx / C, s = idx % C;
+                Akf[idx] = s < r ? sAkk[r][s] : 0.f;
+            }
+        }
     }
 
     // 3. (I + A_kk_pp)^-1 for the four diagonal 16x16 blocks: lane = (tile, column).
@@ -468,26 +446,14 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
             floatx4 Xp = mfma4(*reinterpret_cast<const float4 *>(&sAinv[tp][lr][4 * lg]), R,
                                floatx4{0.f, 0.f, 0.f, 0.f});
             X[u][tp] = Xp;
-            if (kcol)
+            if (kcol) {
                 st_stream(Wf + (tp * NKT + nt) * 64 + lane, transpose16(Xp, lr, lg));
-            else
+                if (TRAIN) // W^T fragment (nt, tp): the accumulator layout of W's tile
+                    st_stream(reinterpret_cast<floatx4 *>(p.ws_wt) + cid * (C * K / 4) + (nt * NT + tp) * 64 + lane,
+                              Xp);
+            } else
                 st_stream(Uf + ((nt - NKT) * NT + tp) * 64 + lane, Xp);
         }
-    }
-}
-
-// Sequences are spread over the 8 XCDs (workgroup i runs on XCD i % 8) so
-// that the V-slices of one sequence, which read the same W, M and Kd^T,
-// land on the same XCD and share its L2.  Identity when the sequence count
-// is not a multiple of 8.
-__device__ __forceinline__ void inter_block(int blk, int nseq, int nvs, int *bh, int *vs) {
-    if (nseq % 8 == 0) {
-        const int x = blk % 8, j = blk / 8;
-        *bh = x + 8 * (j / nvs);
-        *vs = j % nvs;
-    } else {
-        *bh = blk / nvs;
-        *vs = blk % nvs;
     }
 }
 
@@ -517,9 +483,16 @@ __device__ __forceinline__ void inter_block(int blk, int nseq, int nvs, int *bh,
 //   pass 3 (OUT = true): every segment from its S_in, with the output; the
 //     last segment writes the final state.
 // With NSEG = 1 pass 3 alone is the plain sequential kernel.
+//
+// MODE: kInterOut (pass 3), kInterLocal (pass 1) or kInterStates, pass 3 for
+// the backward: no output and no final state; instead the state entering
+// every chunk (ws_sn) and every chunk's v_new (ws_vn).
 // ---------------------------------------------------------------------------
-template <int K, bool OUT>
+constexpr int kInterOut = 0, kInterLocal = 1, kInterStates = 2;
+
+template <int K, int MODE>
 __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int nseg_launch) {
+    constexpr bool OUT = MODE == kInterOut, LOCAL = MODE == kInterLocal, STATES = MODE == kInterStates;
     constexpr int NKT = K / 16;
     constexpr int FR = NKT * NT;   // 16x16 fragments per operand per chunk
     constexpr int OPF4 = FR * 64;  // float4 per operand per chunk
@@ -533,7 +506,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
 
     const int V = p.V;
     const int nvv = V / 64;                   // value slices
-    const int nvs = OUT ? nvv : nvv + K / 64; // pass 1 adds the slices of P
+    const int nvs = LOCAL ? nvv + K / 64 : nvv; // pass 1 adds the slices of P
     int sq, vs;
     inter_block(blockIdx.x, p.B * p.HV * nseg_launch, nvs, &sq, &vs);
     const int bh = sq / nseg_launch, seg = sq % nseg_launch;
@@ -541,7 +514,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (scalar)
     const int lr = lane & 15, lg = lane >> 4;
-    const bool pcol = !OUT && vs >= nvv;           // a slice of P (wave-uniform)
+    const bool pcol = LOCAL && vs >= nvv;          // a slice of P (wave-uniform)
     const int vt = (pcol ? vs - nvv : vs) * 4 + wave; // this wave's 16-column tile
     const int col = 16 * vt + lr;
     const int n0 = seg * p.SEGL;
@@ -551,14 +524,14 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     // copy of S0, so that no workgroup reads the state that the last segment
     // overwrites), 0 (pass 1 value columns) or the identity (pass 1, P columns)
     const float *Sin = nullptr;
-    if (OUT) Sin = p.NSEG == 1 ? p.state + (size_t)bh * K * V : p.ws_qseg + ((size_t)bh * p.NSEG + seg) * K * V;
+    if (!LOCAL) Sin = p.NSEG == 1 ? p.state + (size_t)bh * K * V : p.ws_qseg + ((size_t)bh * p.NSEG + seg) * K * V;
     floatx4 S[NKT];
 #pragma unroll
     for (int kb = 0; kb < NKT; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 16 * kb + 4 * lg + i;
-            S[kb][i] = OUT ? Sin[(size_t)row * V + col] : (pcol && row == col ? 1.f : 0.f);
+            S[kb][i] = !LOCAL ? Sin[(size_t)row * V + col] : (pcol && row == col ? 1.f : 0.f);
         }
 
     const floatx4 *__restrict__ W4 = reinterpret_cast<const floatx4 *>(p.ws_w);
@@ -594,6 +567,13 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt)
             u_cur[mt] = pcol ? floatx4{0.f, 0.f, 0.f, 0.f} : U4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
+        if (STATES) { // the state entering chunk n
+            float *Sn = p.ws_sn + cid * K * V;
+#pragma unroll
+            for (int kb = 0; kb < NKT; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) Sn[(size_t)(16 * kb + 4 * lg + i) * V + col] = S[kb][i];
+        }
 
         // A: X1 = W S, X2 = scale (q exp(G)) S
         floatx4 X1[NT], X2[NT];
@@ -638,6 +618,13 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         // B: v_new = U - X1 (kept in X1)
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) X1[mt] = u_cur[mt] - X1[mt];
+        if (STATES) {
+            float *Vn = p.ws_vn + cid * C * V;
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) Vn[(size_t)(16 * mt + 4 * lg + i) * V + col] = X1[mt][i];
+        }
 
         // D: out = X2 + A_qk v_new (A_qk is lower block-triangular)
         if (OUT) {
@@ -695,10 +682,10 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     int ld = V;
     if (OUT) {
         if (seg == p.NSEG - 1) Sout = p.state + (size_t)bh * K * V;
-    } else if (pcol) {
+    } else if (LOCAL && pcol) {
         Sout = p.ws_pseg + ((size_t)bh * (p.NSEG - 1) + seg) * K * K;
         ld = K;
-    } else {
+    } else if (LOCAL) {
         Sout = p.ws_qseg + ((size_t)bh * p.NSEG + seg + 1) * K * V;
     }
     if (Sout) {
@@ -768,23 +755,30 @@ template <int K, int V>
 hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
     if (phases & 1) {
         const int nchunks = p.B * p.HV * p.NC;
-        hipLaunchKernelGGL((chunk_intra_kernel<K, V>), dim3(nchunks), dim3(512), 0, s, p);
+        if (p.ws_akk)
+            hipLaunchKernelGGL((chunk_intra_kernel<K, V, true>), dim3(nchunks), dim3(512), 0, s, p);
+        else
+            hipLaunchKernelGGL((chunk_intra_kernel<K, V, false>), dim3(nchunks), dim3(512), 0, s, p);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    if (phases & 2) {
+    if (phases & 6) {
         const int seqs = p.B * p.HV;
         if (p.NSEG > 1) {
-            hipLaunchKernelGGL((chunk_inter_kernel<K, false>), dim3(seqs * (p.NSEG - 1) * ((V + K) / 64)), dim3(256),
-                               0, s, p, p.NSEG - 1);
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal>), dim3(seqs * (p.NSEG - 1) * ((V + K) / 64)),
+                               dim3(256), 0, s, p, p.NSEG - 1);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL((chunk_chain_kernel<K>), dim3(seqs * (V / 64)), dim3(256), 0, s, p);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
-        hipLaunchKernelGGL((chunk_inter_kernel<K, true>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0, s, p,
-                           p.NSEG);
+        if (phases & 2)
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOut>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0, s,
+                               p, p.NSEG);
+        else
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterStates>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0,
+                               s, p, p.NSEG);
         return hipGetLastError();
     }
     return hipSuccess;
@@ -871,57 +865,76 @@ extern "C" size_t gdn2_chunk_workspace_bytes(const gdn2_chunk_args *a) {
     return ws_layout(a).total;
 }
 
-// fused_chunk_forward (src/kernel/chunk_cube.rs:781-952) / chunk_wy_forward
-// (src/forward.rs:44-278).  Limits: K in {64, 128}, V in {64, 128, 256},
-// 16-byte aligned q, k, b with strides that are multiples of 4 elements.
-static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, int phases) {
-    if (!a) return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: null args");
-    if (!a->q || !a->k || !a->g || !a->b || !a->v || !a->w || !a->state || !a->out)
-        return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: null tensor pointer");
+namespace gdn2 {
+
+// Checks shared by the chunked forward and backward; fills p's shapes and
+// strides.  Limits: K in {64, 128}, V in {64, 128, 256}, 16-byte aligned q,
+// k, b with strides that are multiples of 4 elements, token strides within
+// the range-checked row loads.
+gdn2_status chunk_setup(const gdn2_chunk_args *a, const char *who, bool need_out, ChunkParams *p) {
+    const std::string w = std::string(who) + ": ";
+    if (!a) return fail(GDN2_EINVAL, w + "null args");
+    if (!a->q || !a->k || !a->g || !a->b || !a->v || !a->w || !a->state || (need_out && !a->out))
+        return fail(GDN2_EINVAL, w + "null tensor pointer");
     if (a->batch <= 0 || a->num_heads <= 0 || a->num_v_heads <= 0 || a->head_dim <= 0 || a->head_v_dim <= 0 ||
         a->seq_len < 0)
-        return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: invalid dimensions");
-    if (a->chunk_size <= 0) return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: chunk_size must be > 0");
-    if (a->num_v_heads % a->num_heads != 0)
-        return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: num_v_heads must be a multiple of num_heads");
+        return fail(GDN2_EINVAL, w + "invalid dimensions");
+    if (a->chunk_size <= 0) return fail(GDN2_EINVAL, w + "chunk_size must be > 0");
+    if (a->num_v_heads % a->num_heads != 0) return fail(GDN2_EINVAL, w + "num_v_heads must be a multiple of num_heads");
     if (!chunk_supported((int)a->head_dim, (int)a->head_v_dim))
-        return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_fwd_f32: (K, V) outside the chunk kernels' instances");
+        return fail(GDN2_NOT_APPLICABLE, w + "(K, V) outside the chunk kernels' instances");
     if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->b) || (a->stride_qk_b % 4) || (a->stride_qk_h % 4) ||
         (a->stride_qk_t % 4))
-        return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_fwd_f32: q/k/b need 16-byte aligned rows");
+        return fail(GDN2_NOT_APPLICABLE, w + "q/k/b need 16-byte aligned rows");
     // The intra kernel reads a chunk's rows through 32-bit range-checked
     // buffer offsets: token rows must not overlap, and one chunk of rows must
     // span less than 2 GiB.
     if (a->stride_qk_t < a->head_dim || a->stride_vw_t < a->head_v_dim ||
         ((kChunk - 1) * a->stride_qk_t + a->head_dim) * 4 >= (int64_t(1) << 31) ||
         ((kChunk - 1) * a->stride_vw_t + a->head_v_dim) * 4 >= (int64_t(1) << 31))
-        return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_fwd_f32: token strides outside the chunk kernels' range");
-    if (a->seq_len == 0) return GDN2_OK;
+        return fail(GDN2_NOT_APPLICABLE, w + "token strides outside the chunk kernels' range");
+    *p = ChunkParams{};
+    p->q = a->q; p->k = a->k; p->g = a->g; p->b = a->b; p->v = a->v; p->w = a->w;
+    p->state = a->state; p->out = a->out;
+    p->B = (int)a->batch; p->HV = (int)a->num_v_heads; p->rep = (int)(a->num_v_heads / a->num_heads);
+    p->T = (int)a->seq_len; p->K = (int)a->head_dim; p->V = (int)a->head_v_dim;
+    p->NC = (int)((a->seq_len + kChunk - 1) / kChunk);
+    p->sqb = a->stride_qk_b; p->sqh = a->stride_qk_h; p->sqt = a->stride_qk_t;
+    p->svb = a->stride_vw_b; p->svh = a->stride_vw_h; p->svt = a->stride_vw_t;
+    p->sob = a->stride_o_b; p->soh = a->stride_o_h; p->sot = a->stride_o_t;
+    p->scale = (float)a->scale;
+    const Segments sg = inter_segments(p->B * p->HV, 1, p->V, p->NC);
+    p->NSEG = sg.nseg;
+    p->SEGL = sg.segl;
+    return GDN2_OK;
+}
+
+size_t chunk_fwd_ws_bytes(const gdn2_chunk_args *a) { return ws_layout(a).total; }
+
+void chunk_bind_ws(const gdn2_chunk_args *a, char *ws, ChunkParams *p) {
     const WsLayout L = ws_layout(a);
-    if (!a->workspace || a->workspace_bytes < L.total || (reinterpret_cast<uintptr_t>(a->workspace) & 255u))
+    p->ws_w = reinterpret_cast<float *>(ws + L.w);
+    p->ws_qg = reinterpret_cast<float *>(ws + L.qg);
+    p->ws_u = reinterpret_cast<float *>(ws + L.u);
+    p->ws_aqk = reinterpret_cast<float *>(ws + L.aqk);
+    p->ws_kdt = reinterpret_cast<float *>(ws + L.kdt);
+    p->ws_gam = reinterpret_cast<float *>(ws + L.gam);
+    p->ws_pseg = reinterpret_cast<float *>(ws + L.pseg);
+    p->ws_qseg = reinterpret_cast<float *>(ws + L.qseg);
+}
+
+}  // namespace gdn2
+
+// fused_chunk_forward (src/kernel/chunk_cube.rs:781-952) / chunk_wy_forward
+// (src/forward.rs:44-278).
+static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, int phases) {
+    ChunkParams p;
+    const gdn2_status st = chunk_setup(a, "gdn2_chunk_fwd_f32", true, &p);
+    if (st != GDN2_OK) return st;
+    if (a->seq_len == 0) return GDN2_OK;
+    if (!a->workspace || a->workspace_bytes < chunk_fwd_ws_bytes(a) || (reinterpret_cast<uintptr_t>(a->workspace) & 255u))
         return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: workspace missing, too small or not 256-byte aligned");
-    ChunkParams p{};
-    p.q = a->q; p.k = a->k; p.g = a->g; p.b = a->b; p.v = a->v; p.w = a->w;
-    p.state = a->state; p.out = a->out;
-    p.B = (int)a->batch; p.HV = (int)a->num_v_heads; p.rep = (int)(a->num_v_heads / a->num_heads);
-    p.T = (int)a->seq_len; p.K = (int)a->head_dim; p.V = (int)a->head_v_dim;
-    p.NC = (int)((a->seq_len + kChunk - 1) / kChunk);
-    p.sqb = a->stride_qk_b; p.sqh = a->stride_qk_h; p.sqt = a->stride_qk_t;
-    p.svb = a->stride_vw_b; p.svh = a->stride_vw_h; p.svt = a->stride_vw_t;
-    p.sob = a->stride_o_b; p.soh = a->stride_o_h; p.sot = a->stride_o_t;
-    p.scale = (float)a->scale;
-    char *ws = static_cast<char *>(a->workspace);
-    p.ws_w = reinterpret_cast<float *>(ws + L.w);
-    p.ws_qg = reinterpret_cast<float *>(ws + L.qg);
-    p.ws_u = reinterpret_cast<float *>(ws + L.u);
-    p.ws_aqk = reinterpret_cast<float *>(ws + L.aqk);
-    p.ws_kdt = reinterpret_cast<float *>(ws + L.kdt);
-    p.ws_gam = reinterpret_cast<float *>(ws + L.gam);
-    p.ws_pseg = reinterpret_cast<float *>(ws + L.pseg);
-    p.ws_qseg = reinterpret_cast<float *>(ws + L.qseg);
-    const Segments sg = inter_segments(p.B * p.HV, 1, p.V, p.NC);
-    p.NSEG = sg.nseg;
-    p.SEGL = sg.segl;
+    chunk_bind_ws(a, static_cast<char *>(a->workspace), &p);
     GDN2_HIP_CHECK(launch_chunk(p, (hipStream_t)stream, phases));
     return GDN2_OK;
 }

@@ -1,0 +1,91 @@
+// Device helpers shared by the chunked forward (chunk.hip) and backward
+// (chunk_bwd.hip) kernels: chunk geometry, MFMA fragment helpers, the
+// range-checked row loads and the XCD-aware workgroup mapping.
+#pragma once
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace gdn2 {
+
+constexpr int C = kChunk;   // chunk length of the kernels
+constexpr int NT = C / 16;  // 16-row tiles per chunk
+
+// Rows [0, valid) of a row-strided f32 matrix (row stride rs, rowlen
+// elements used per row) as a buffer resource.  The hardware's range check
+// returns 0 for every load past the last valid row, which is the zero padding
+// of a ragged last chunk (src/forward.rs:94-99), so a load needs neither a
+// clamp nor a mask, and its offset is a 32-bit element index.  Requires
+// rs >= rowlen and ((valid - 1) rs + rowlen) * 4 < 2^31 (checked on the host).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const float *base, int rs, int valid, int rowlen) {
+    const int bytes = ((valid - 1) * rs + rowlen) * 4;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ float bld1(__amdgpu_buffer_rsrc_t r, int idx) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, idx * 4, 0, 0));
+}
+
+__device__ __forceinline__ floatx4 bld4(__amdgpu_buffer_rsrc_t r, int idx) {
+    return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, idx * 4, 0, 0));
+}
+
+__device__ __forceinline__ floatx4 mfma4(float4 a, floatx4 b, floatx4 c) {
+    c = mfma16(a.x, b[0], c);
+    c = mfma16(a.y, b[1], c);
+    c = mfma16(a.z, b[2], c);
+    c = mfma16(a.w, b[3], c);
+    return c;
+}
+
+// D = X^T for an accumulator tile X, i.e. the A-operand layout of X
+// (lane (g, r) gets X[r][4g..4g+3]): the accumulator is a valid A operand
+// of X^T under the k = 4g + step labelling, multiplied by the identity.
+// Exact in f32 (products with 1 and 0).
+__device__ __forceinline__ floatx4 transpose16(floatx4 x, int lr, int lg) {
+    floatx4 d = floatx4{0.f, 0.f, 0.f, 0.f};
+    d = mfma16(x[0], lr == 4 * lg + 0 ? 1.f : 0.f, d);
+    d = mfma16(x[1], lr == 4 * lg + 1 ? 1.f : 0.f, d);
+    d = mfma16(x[2], lr == 4 * lg + 2 ? 1.f : 0.f, d);
+    d = mfma16(x[3], lr == 4 * lg + 3 ? 1.f : 0.f, d);
+    return d;
+}
+
+__device__ __forceinline__ floatx4 mfma4n(float4 a, floatx4 b, floatx4 c) {
+    c = mfma16(-a.x, b[0], c);
+    c = mfma16(-a.y, b[1], c);
+    c = mfma16(-a.z, b[2], c);
+    c = mfma16(-a.w, b[3], c);
+    return c;
+}
+
+// Streaming store: the workspace is read back by chunk-inter much later, so
+// keeping it out of L2 leaves room for the chunk's inputs, which chunk-intra
+// reads more than once.
+__device__ __forceinline__ void st_stream(floatx4 *dst, floatx4 v) { __builtin_nontemporal_store(v, dst); }
+
+__device__ __forceinline__ floatx4 exp2v(floatx4 x) {
+    return floatx4{fast_exp2(x[0]), fast_exp2(x[1]), fast_exp2(x[2]), fast_exp2(x[3])};
+}
+
+// Sequences are spread over the 8 XCDs (workgroup i runs on XCD i % 8) so
+// that the V-slices of one sequence, which read the same W, M and Kd^T,
+// land on the same XCD and share its L2.  Identity when the sequence count
+// is not a multiple of 8.
+__device__ __forceinline__ void inter_block(int blk, int nseq, int nvs, int *bh, int *vs) {
+    if (nseq % 8 == 0) {
+        const int x = blk % 8, j = blk / 8;
+        *bh = x + 8 * (j / nvs);
+        *vs = j % nvs;
+    } else {
+        *bh = blk / nvs;
+        *vs = blk % nvs;
+    }
+}
+
+// Host side of the chunked forward, shared with the backward (chunk.hip).
+gdn2_status chunk_setup(const gdn2_chunk_args *a, const char *who, bool need_out, ChunkParams *p);
+size_t chunk_fwd_ws_bytes(const gdn2_chunk_args *a);
+void chunk_bind_ws(const gdn2_chunk_args *a, char *ws, ChunkParams *p);
+
+}  // namespace gdn2

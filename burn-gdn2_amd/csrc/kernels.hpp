@@ -63,6 +63,14 @@ struct ChunkParams {
     float *ws_qseg; // NSEG x K*V      state entering each segment (slot j + 1 first
                     //                 holds segment j's state from S = 0)
     int NSEG, SEGL;
+    // Training forward (null in inference): the operands of the backward.
+    float *ws_wt;   // C*K  W^T as A-operand tiles (key tile, time tile)
+    float *ws_qgt;  // C*K  (scale q exp(G))^T, same order
+    float *ws_kd;   // C*K  Kd as A-operand tiles (time tile, key tile)
+    float *ws_aqkt; // C*C  A_qk^T as A-operand tiles (column tile, row tile)
+    float *ws_akk;  // C*C  A_kk row-major (strictly lower, zero elsewhere)
+    float *ws_sn;   // K*V  state entering each chunk (row-major)
+    float *ws_vn;   // C*V  v_new of each chunk (row-major)
 };
 
 // Projection epilogue: raw Linear outputs -> kernel inputs, one token per
@@ -105,6 +113,9 @@ hipError_t launch_fill_rows(float *y, int64_t ld, const float *row, int64_t M, i
 hipError_t launch_scan(const ScanParams &p, hipStream_t s);
 hipError_t launch_decode(const DecodeParams &p, hipStream_t s);
 bool chunk_supported(int K, int V);
-hipError_t launch_chunk(const ChunkParams &p, hipStream_t s, int phases); // bit 0: intra, bit 1: inter
+// phases: bit 0 intra (with the training outputs when ws_akk is set), bit 1
+// inter with the output, bit 2 inter writing ws_sn / ws_vn instead of the
+// output and the final state.
+hipError_t launch_chunk(const ChunkParams &p, hipStream_t s, int phases);
 
 }  // namespace gdn2

@@ -143,6 +143,36 @@ def chunk_wy_forward(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64
     return out, st
 
 
+def chunk_wy_backward(q, k, v, g, b, w, state0, d_out, scale: float, chunk_size: int = 64, d_state=None,
+                      workspace=None):
+    """Gradients of the chunked forward (fused_chunk_backward,
+    src/kernel/chunk_adjoint_cube.rs:464-707): for
+    L = <d_out, out> + <d_state, S_T> returns dict dq, dk, dg, db (shapes of
+    q, k, g, b), dv, dw (shapes of v, w) and dS0, or None when the chunk
+    kernels do not apply.  Gradient tensors take the layouts of their inputs."""
+    _check_f32_cuda(q, k, v, g, b, w, state0, d_out)
+    B, Hk, T, K = q.shape
+    HV, V = v.shape[1], v.shape[3]
+    st = state0.contiguous()
+    grads = {n: torch.empty_strided(t.shape, t.stride(), device=t.device, dtype=torch.float32)
+             for n, t in (("dq", q), ("dk", k), ("dg", g), ("db", b), ("dv", v), ("dw", w))}
+    grads["dS0"] = torch.empty((B, HV, K, V), device=q.device, dtype=torch.float32)
+    ds = None if d_state is None else d_state.contiguous()
+    if T == 0:  # no tokens: only the state gradient passes through
+        grads["dS0"] = ds.clone() if ds is not None else torch.zeros_like(grads["dS0"])
+        return grads
+    fwd = chunk_args(q, k, v, g, b, w, st, d_out, scale, chunk_size)
+    a = C.ChunkBwdArgs(fwd, _p(d_out), _p(ds), *(_p(grads[n]) for n in ("dq", "dk", "dg", "db", "dv", "dw", "dS0")),
+                       None, 0)
+    need = int(C.lib().gdn2_chunk_bwd_workspace_bytes(ctypes.byref(a)))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    a.workspace, a.workspace_bytes = _p(workspace), workspace.numel() * workspace.element_size()
+    if not C.check(C.lib().gdn2_chunk_bwd_f32(ctypes.byref(a), _stream()), allow_not_applicable=True):
+        return None
+    return grads
+
+
 def decode_args(raw: dict, params: dict, state, conv_in, conv_out, out, *, num_heads, num_v_heads, head_dim,
                 head_v_dim, scale, min_decay=None, norm_eps=1e-5, use_short_conv=True, allow_neg_eigval=False):
     """Build the gdn2_decode_args block (the LayerParams it points to is

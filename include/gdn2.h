@@ -1,5 +1,6 @@
 /*
- * gdn2.h -- C ABI of the MI355X (gfx950) GDN-2 forward path.
+ * gdn2.h -- C ABI of the MI355X (gfx950) GDN-2 forward path and its chunked
+ * backward.
  *
  * The entry points replace burn-gdn2's backend-gated kernel launchers:
  *
@@ -7,6 +8,9 @@
  *   gdn2_chunk_fwd_f32       <- fused_chunk_forward   src/kernel/chunk_cube.rs:781-952
  *                               (and the tensor path chunk_wy_forward, src/forward.rs:44-278,
  *                                which is the only live chunk path in the reference)
+ *   gdn2_chunk_bwd_f32       <- fused_chunk_backward  src/kernel/chunk_adjoint_cube.rs:464-707
+ *                               (gradients of the chunked forward; the reference's training
+ *                                path otherwise takes them through autodiff)
  *   gdn2_decode_fused_f32    <- GatedDeltaNet2::forward at T == 1 between project() and
  *                               o_proj: short conv (src/short_conv.rs:22-65), gates
  *                               (src/module.rs:417-443), L2 norm (src/l2norm.rs:13-16),
@@ -155,6 +159,38 @@ GDN2_API gdn2_status gdn2_chunk_fwd_f32(const gdn2_chunk_args *args, gdn2_stream
  * on one stream with the same args they equal gdn2_chunk_fwd_f32. */
 GDN2_API gdn2_status gdn2_chunk_intra_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
 GDN2_API gdn2_status gdn2_chunk_inter_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Chunked backward                                     -- fused_chunk_backward
+ * (src/kernel/chunk_adjoint_cube.rs:464-707; the reference's training path
+ * otherwise differentiates chunk_wy_forward through autodiff): the gradients
+ * of L = <d_out, out> + <d_state_out, S_T> for the forward of `fwd`.
+ *   fwd          the forward's arguments: q, k, g, b, v, w, state = S0 (read
+ *                only), strides, scale, chunk_size; out, workspace unused
+ *   d_out        strided like out (fwd.stride_o_*), 16-byte aligned rows
+ *   d_state_out  [B, HV, K, V] contiguous, or NULL (zero)
+ *   dq, dk, dg, db  strided like q (fwd.stride_qk_*); with num_v_heads >
+ *                num_heads the sum over the value heads of each key head
+ *   dv, dw       strided like v (fwd.stride_vw_*)
+ *   d_state0     [B, HV, K, V] contiguous
+ * It recomputes the forward's per-chunk quantities (the reference's
+ * FusedBackwardInputs) in its own workspace of
+ * gdn2_chunk_bwd_workspace_bytes(args) bytes, 256-byte aligned.
+ * Limits as gdn2_chunk_fwd_f32 (else GDN2_NOT_APPLICABLE).
+ * ---------------------------------------------------------------------- */
+typedef struct gdn2_chunk_bwd_args {
+    gdn2_chunk_args fwd;
+    const float *d_out;
+    const float *d_state_out;
+    float *dq, *dk, *dg, *db;
+    float *dv, *dw;
+    float *d_state0;
+    void *workspace;
+    size_t workspace_bytes;
+} gdn2_chunk_bwd_args;
+
+GDN2_API size_t gdn2_chunk_bwd_workspace_bytes(const gdn2_chunk_bwd_args *args);
+GDN2_API gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *args, gdn2_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Fused decode of one token for every batch row           -- forward at T=1

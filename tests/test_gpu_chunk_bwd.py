@@ -1,0 +1,106 @@
+"""GPU parity of the chunked backward (gdn2_chunk_bwd_f32) against the
+oracle's f64 adjoint of the recurrence (itself pinned by finite differences
+in test_oracle_bwd.py).  Tolerance per gradient tensor: max |error| <=
+1e-4 * max(1, max |reference|) -- f32 kernels against the f64 adjoint over
+the whole sequence (the forward's 1e-4 bound, scaled to the gradient's
+magnitude, which grows with the sequence)."""
+import numpy as np
+import pytest
+
+from conftest import rand_inputs
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ("dq", "dk", "dg", "db", "dv", "dw", "dS0")
+
+
+def _dev(gpu, *arrs):
+    import torch
+
+    return [torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(gpu) for a in arrs]
+
+
+def _compare(got, ref, label):
+    worst = {}
+    for n in NAMES:
+        g = got[n].cpu().numpy().astype(np.float64)
+        r = ref[n]
+        err = float(np.abs(g - r).max()) if r.size else 0.0
+        bound = 1e-4 * max(1.0, float(np.abs(r).max()) if r.size else 0.0)
+        worst[n] = (err, bound)
+    print(label, " ".join(f"{n}={e:.1e}/{b:.0e}" for n, (e, b) in worst.items()))
+    for n, (e, b) in worst.items():
+        assert e <= b, (label, n, e, b)
+
+
+CASES = [
+    # B, Hk, HV, T, K, V, g range, b_hi, S0 scale, d_state_out
+    (1, 1, 1, 64, 128, 128, (-0.3, -0.02), 1.0, 0.5, True),
+    (2, 2, 2, 130, 128, 128, (-0.3, -0.02), 1.0, 0.5, True),    # ragged last chunk
+    (1, 1, 2, 150, 128, 256, (-0.4, -0.01), 2.0, 0.5, True),    # GVA rep 2, V = 2K, negative eigenvalues
+    (2, 2, 2, 97, 64, 64, (-0.3, -0.02), 1.0, 0.0, False),      # K = V = 64, no state gradient in
+    (1, 2, 2, 200, 128, 128, (-5.0, -0.5), 1.0, 0.5, True),     # strong decay
+    (1, 1, 1, 1, 128, 128, (-0.3, -0.02), 1.0, 1.0, True),      # T = 1
+    (1, 1, 2, 63, 64, 128, (-1.0, -0.1), 2.0, 0.3, True),
+    (1, 2, 2, 2100, 128, 128, (-0.003, -0.0005), 1.0, 1.0, True),  # slow decay; segmented forward states
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}g{c[6][0]}" for c in CASES])
+def test_chunk_bwd_matches_adjoint(gpu, case):
+    import torch
+
+    import gdn2_amd
+
+    B, Hk, HV, T, K, V, (glo, ghi), bhi, s0, dst = case
+    rng = np.random.default_rng(3000 + T + K + V)
+    q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=glo, g_hi=ghi, b_hi=bhi)
+    q *= K ** -0.5 * 4
+    S0 = (rng.standard_normal((B, HV, K, V)) * s0).astype(np.float32)
+    dO = rng.standard_normal((B, HV, T, V)).astype(np.float32)
+    dST = rng.standard_normal((B, HV, K, V)).astype(np.float32) if dst else None
+    scale = K ** -0.5
+    ref = O.recurrent_bwd_f64(q, k, v, g, b, w, dO, S0=S0, d_ST=dST, scale=scale)
+    d = _dev(gpu, q, k, v, g, b, w, S0, dO)
+    ds = None if dST is None else _dev(gpu, dST)[0]
+    got = gdn2_amd.chunk_wy_backward(*d[:7], d[7], scale, 64, d_state=ds)
+    assert got is not None
+    torch.cuda.synchronize()
+    _compare(got, ref, str(case[:6]))
+
+
+def test_chunk_bwd_strided_views(gpu):
+    """q/k/g/b/v/w and d_out as [B, H, T, D] views of [B, T, H, D] storage:
+    the gradients come back in the same layouts."""
+    import torch
+
+    import gdn2_amd
+
+    rng = np.random.default_rng(9)
+    B, H, T, K, V = 2, 3, 140, 128, 128
+    q, k, v, g, b, w = rand_inputs(rng, B, H, H, T, K, V)
+    q *= 0.3
+    dO = rng.standard_normal((B, H, T, V)).astype(np.float32)
+    ref = O.recurrent_bwd_f64(q, k, v, g, b, w, dO, scale=0.2)
+    bt = [torch.from_numpy(np.ascontiguousarray(a.transpose(0, 2, 1, 3))).to(gpu) for a in (q, k, v, g, b, w, dO)]
+    views = [x.permute(0, 2, 1, 3) for x in bt]
+    S0 = torch.zeros((B, H, K, V), device=gpu)
+    got = gdn2_amd.chunk_wy_backward(*views[:6], S0, views[6], 0.2)
+    assert got is not None
+    assert got["dq"].stride() == views[0].stride() and got["dv"].stride() == views[2].stride()
+    _compare(got, ref, "strided")
+
+
+def test_chunk_bwd_empty_sequence(gpu):
+    import torch
+
+    import gdn2_amd
+
+    rng = np.random.default_rng(10)
+    d = _dev(gpu, *rand_inputs(rng, 1, 1, 1, 0, 128, 128))
+    S0 = torch.randn((1, 1, 128, 128), device=gpu)
+    dST = torch.randn((1, 1, 128, 128), device=gpu)
+    dO = torch.empty((1, 1, 0, 128), device=gpu)
+    got = gdn2_amd.chunk_wy_backward(*d, S0, dO, 0.1, d_state=dST)
+    assert torch.equal(got["dS0"], dST)
