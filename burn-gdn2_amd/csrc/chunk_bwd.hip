@@ -214,19 +214,20 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp) {
 // Per-chunk products over the value dimension (MFMA, four waves):
 //   dQG = dO S^T, dW = -dv_new S^T, dKd = v_new dS'^T       (C x K)
 //   dA_qk = tril(dO v_new^T), dUU = strict_tril(dv_new U^T)  (C x C)
-// and dgam = rowsum(dS' * S).  A tile (rt, ct) of X Y^T takes rows 16 rt + r
-// of X and 16 ct + r of Y as A and B fragments (16-byte loads along V).
+// and dgam = rowsum(dS' * S).  Wave w owns the 16 rows of time tile w of
+// every product, so its A fragments (rows of dO, dv_new, v_new) are its own;
+// the B fragments (rows of S, dS', v_new, U) are shared through L2.  The
+// accumulators of all of the wave's tiles stay in registers over the V loop.
 // ---------------------------------------------------------------------------
 template <int K, int V>
-__global__ __launch_bounds__(256) void bwd_gemm_kernel(BwdParams bp) {
+__global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(BwdParams bp) {
     const ChunkParams &p = bp.f;
     constexpr int NKT = K / 16, NVB = V / 16;
-    constexpr int NJ1 = 3 * NT * NKT, NJ = NJ1 + 2 * NT * NT;
     const int cid = blockIdx.x, bh = cid / p.NC, n = cid % p.NC;
     const int bi = bh / p.HV, hv = bh % p.HV;
     const int cv = min(C, p.T - n * C);
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // = the time tile
     const int lr = lane & 15, lg = lane >> 4;
 
     const float *dO = bp.d_out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + (int64_t)(n * C) * p.sot;
@@ -235,60 +236,68 @@ __global__ __launch_bounds__(256) void bwd_gemm_kernel(BwdParams bp) {
     const float *Sn = p.ws_sn + (size_t)cid * K * V, *dSn = bp.ws_dsn + (size_t)cid * K * V;
     const float *vn = p.ws_vn + (size_t)cid * C * V, *dvn = bp.ws_dvn + (size_t)cid * C * V;
     const float *Uf = p.ws_u + (size_t)cid * C * V; // accumulator fragments (column tile, row tile)
+    const int arow = 16 * wave + lr;
 
-    for (int j = wave; j < NJ; j += 4) {
-        int mat, rt, ct;
-        if (j < NJ1) {
-            mat = j / (NT * NKT);
-            rt = (j % (NT * NKT)) / NKT;
-            ct = j % NKT;
-        } else {
-            const int jj = j - NJ1;
-            mat = 3 + jj / (NT * NT);
-            rt = (jj % (NT * NT)) / NT;
-            ct = jj % NT;
+    floatx4 aQ[NKT], aW[NKT], aK[NKT], aA[NT], aU[NT];
+#pragma unroll
+    for (int t = 0; t < NKT; ++t) aQ[t] = aW[t] = aK[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < NT; ++t) aA[t] = aU[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll 1
+    for (int vb = 0; vb < NVB; ++vb) {
+        const int c0 = 16 * vb + 4 * lg;
+        const floatx4 fO = bld4(RdO, arow * ro + c0);
+        const floatx4 fD = *reinterpret_cast<const floatx4 *>(dvn + arow * V + c0);
+        const floatx4 fV = *reinterpret_cast<const floatx4 *>(vn + arow * V + c0);
+        floatx4 bS[NKT], bD[NKT];
+#pragma unroll
+        for (int t = 0; t < NKT; ++t) {
+            bS[t] = *reinterpret_cast<const floatx4 *>(Sn + (16 * t + lr) * V + c0);
+            bD[t] = *reinterpret_cast<const floatx4 *>(dSn + (16 * t + lr) * V + c0);
         }
-        floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-        if (mat < 3 || ct <= rt) {
-            const int arow = 16 * rt + lr, brow = 16 * ct + lr;
+        floatx4 bV[NT], bU[NT];
 #pragma unroll
-            for (int vb = 0; vb < NVB; ++vb) {
-                const int c0 = 16 * vb + 4 * lg;
-                floatx4 a, b;
-                if (mat == 0 || mat == 3)
-                    a = bld4(RdO, arow * ro + c0);
-                else if (mat == 1 || mat == 4)
-                    a = *reinterpret_cast<const floatx4 *>(dvn + arow * V + c0);
-                else
-                    a = *reinterpret_cast<const floatx4 *>(vn + arow * V + c0);
-                if (mat <= 1)
-                    b = *reinterpret_cast<const floatx4 *>(Sn + brow * V + c0);
-                else if (mat == 2)
-                    b = *reinterpret_cast<const floatx4 *>(dSn + brow * V + c0);
-                else if (mat == 3)
-                    b = *reinterpret_cast<const floatx4 *>(vn + brow * V + c0);
-                else // U[brow][c0 + i]: tile (vb, ct), lane (lr / 4, 4 lg + i), component lr % 4
+        for (int st = 0; st < NT; ++st) {
+            bV[st] = bU[st] = floatx4{0.f, 0.f, 0.f, 0.f};
+            if (st <= wave) {
+                bV[st] = *reinterpret_cast<const floatx4 *>(vn + (16 * st + lr) * V + c0);
+                // U[16 st + lr][c0 + i]: tile (vb, st), lane (lr / 4, 4 lg + i), component lr % 4
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        b[i] = Uf[((vb * NT + ct) * 64 + (lr >> 2) * 16 + 4 * lg + i) * 4 + (lr & 3)];
-                acc = mfma4x(a, b, acc);
+                for (int i = 0; i < 4; ++i) bU[st][i] = Uf[((vb * NT + st) * 64 + (lr >> 2) * 16 + 4 * lg + i) * 4 + (lr & 3)];
             }
         }
-        float *dst;
-        int ld = K;
-        if (mat == 0) dst = bp.ws_dqg + (size_t)cid * C * K;
-        else if (mat == 1) dst = bp.ws_dwm + (size_t)cid * C * K;
-        else if (mat == 2) dst = bp.ws_dkd + (size_t)cid * C * K;
-        else if (mat == 3) { dst = bp.ws_daqk + (size_t)cid * C * C; ld = C; }
-        else { dst = bp.ws_duu + (size_t)cid * C * C; ld = C; }
-        const int s = 16 * ct + lr;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 16 * rt + 4 * lg + i;
-            float val = mat == 1 ? -acc[i] : acc[i];
-            if (mat == 3 && s > r) val = 0.f;
-            if (mat == 4 && s >= r) val = 0.f;
-            dst[r * ld + s] = val;
+        for (int t = 0; t < NKT; ++t) {
+            aQ[t] = mfma4x(fO, bS[t], aQ[t]);
+            aW[t] = mfma4x(fD, bS[t], aW[t]);
+            aK[t] = mfma4x(fV, bD[t], aK[t]);
+        }
+#pragma unroll
+        for (int st = 0; st < NT; ++st) {
+            if (st <= wave) {
+                aA[st] = mfma4x(fO, bV[st], aA[st]);
+                aU[st] = mfma4x(fD, bU[st], aU[st]);
+            }
+        }
+    }
+    float *oQ = bp.ws_dqg + (size_t)cid * C * K, *oW = bp.ws_dwm + (size_t)cid * C * K;
+    float *oK = bp.ws_dkd + (size_t)cid * C * K;
+    float *oA = bp.ws_daqk + (size_t)cid * C * C, *oU = bp.ws_duu + (size_t)cid * C * C;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 16 * wave + 4 * lg + i;
+#pragma unroll
+        for (int t = 0; t < NKT; ++t) {
+            oQ[r * K + 16 * t + lr] = aQ[t][i];
+            oW[r * K + 16 * t + lr] = -aW[t][i];
+            oK[r * K + 16 * t + lr] = aK[t][i];
+        }
+#pragma unroll
+        for (int st = 0; st < NT; ++st) {
+            const int s = 16 * st + lr;
+            oA[r * C + s] = s <= r ? aA[st][i] : 0.f;
+            oU[r * C + s] = s < r ? aU[st][i] : 0.f;
         }
     }
 
@@ -297,6 +306,7 @@ __global__ __launch_bounds__(256) void bwd_gemm_kernel(BwdParams bp) {
     {
         const int c = tid / TPR, part = tid % TPR;
         float acc = 0.f;
+#pragma unroll 4
         for (int v = part; v < V; v += TPR) acc += dSn[(size_t)c * V + v] * Sn[(size_t)c * V + v];
 #pragma unroll
         for (int off = 1; off < TPR; off <<= 1) acc += __shfl_xor(acc, off, 64);
@@ -306,134 +316,327 @@ __global__ __launch_bounds__(256) void bwd_gemm_kernel(BwdParams bp) {
 
 // ---------------------------------------------------------------------------
 // Per-chunk solve adjoint (four waves):
-//   Ai = (I + A_kk)^-1 by column-wise forward substitution (thread j: column j)
-//   dRk = Ai^T dW;  dRv = Ai^T dv_new -> dv = dRv * w, dw = dRv * v
-//   dA_kk = strict_tril(-(dRk W^T + Ai^T dUU))
+//   Ai = (I + A_kk)^-1, blocked by 16-row tiles: the diagonal inverses by
+//     forward substitution, then Ai_pq = -D_p sum_{q<=m<p} A_kk,pm Ai_mq
+//   [dRk | dRv] = Ai^T [dW | dv_new]   (MFMA; dv = dRv * w, dw = dRv * v)
+//   dA_kk = strict_tril(-(dRk W^T + Ai^T dUU))   (MFMA)
+// Ai^T A fragments come from LDS (lane (g, r): Ai[16 st + 4 g + j][16 rt + r]);
+// W's stored A fragments are the B fragments of W^T.
 // ---------------------------------------------------------------------------
 template <int K, int V>
-__global__ __launch_bounds__(256) void bwd_solve_kernel(BwdParams bp) {
+__global__ __launch_bounds__(256, 2) void bwd_solve_kernel(BwdParams bp) {
     const ChunkParams &p = bp.f;
-    constexpr int NKT = K / 16;
-    constexpr int TW = (K > V ? K : V) + 1;
-    __shared__ float sM[C][C + 1];  // A_kk, then dv_new U^T
-    __shared__ float sAi[C][C + 1]; // (I + A_kk)^-1
-    __shared__ float sR[C][K + 1];  // dRk
-    __shared__ float sT[C][TW];     // dW, then dv_new, then W
+    constexpr int NKT = K / 16, NVT = V / 16, NCT = NKT + NVT;
+    constexpr int CP = C + 4, KP = K + 4;
+    __shared__ __attribute__((aligned(16))) float sM[C][CP];  // A_kk
+    __shared__ float sAi[C][CP]; // (I + A_kk)^-1
+    __shared__ __attribute__((aligned(16))) float sU[C * KP];
+    float(*sX)[CP] = reinterpret_cast<float(*)[CP]>(sU); // off-diagonal block products (the inverse)
+    float(*sR)[KP] = reinterpret_cast<float(*)[KP]>(sU); // dRk (after the inverse)
+    static_assert(KP >= CP, "sX fits in sU");
     const int cid = blockIdx.x, bh = cid / p.NC, n = cid % p.NC;
     const int bi = bh / p.HV, hv = bh % p.HV;
     const int cv = min(C, p.T - n * C);
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
 
     {
-        const float *Akk = p.ws_akk + (size_t)cid * C * C;
-        for (int idx = tid; idx < C * C; idx += 256) sM[idx / C][idx % C] = Akk[idx];
-        const float *dWm = bp.ws_dwm + (size_t)cid * C * K;
-        for (int idx = tid; idx < C * K; idx += 256) sT[idx / K][idx % K] = dWm[idx];
-    }
-    __syncthreads();
-    if (tid < C) { // column j of Ai: x_i = [i == j] - sum_{j <= m < i} A_kk[i][m] x_m
-        const int j = tid;
-        for (int i = 0; i < C; ++i) {
-            float x = i == j ? 1.f : 0.f;
-            for (int m = j; m < i; ++m) x -= sM[i][m] * sAi[m][j];
-            sAi[i][j] = i < j ? 0.f : x;
+        const floatx4 *Akk = reinterpret_cast<const floatx4 *>(p.ws_akk + (size_t)cid * C * C);
+        floatx4 a[C * C / 4 / 256];
+#pragma unroll
+        for (int i = 0; i < C * C / 4 / 256; ++i) a[i] = Akk[i * 256 + tid];
+#pragma unroll
+        for (int i = 0; i < C * C / 4 / 256; ++i) {
+            const int f = i * 256 + tid, r = f / (C / 4), c4 = f % (C / 4);
+            *reinterpret_cast<floatx4 *>(&sM[r][4 * c4]) = a[i];
         }
     }
     __syncthreads();
-    {
-        float *drk = bp.ws_drk + (size_t)cid * C * K;
-        for (int idx = tid; idx < C * K; idx += 256) {
-            const int r = idx / K, c = idx % K;
+    if (wave == 0) { // diagonal inverses: lane = (tile, column)
+        const int pt = lane >> 4, j = lane & 15;
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float v = (i == j) ? 1.f : 0.f;
+#pragma unroll
+            for (int m = 0; m < i; ++m) v -= sM[16 * pt + i][16 * pt + m] * x[m];
+            x[i] = v;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sAi[16 * pt + i][16 * pt + j] = x[i];
+    } else { // zero the upper blocks
+        for (int idx = tid - 64; idx < C * C; idx += 192) {
+            const int r = idx / C, c = idx % C;
+            if ((c >> 4) > (r >> 4)) sAi[r][c] = 0.f;
+        }
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int d = 1; d < NT; ++d) { // block diagonal d: Ai_{q+d, q}
+        const int nb = NT - d;
+        // X = sum_{m=q}^{q+d-1} A_kk[q+d][m] Ai[m][q] (16 x 16 per block)
+        for (int e = tid; e < nb * 256; e += 256) {
+            const int q = e >> 8, r = (e >> 4) & 15, c = e & 15, pb = q + d;
             float acc = 0.f;
-            for (int s = r; s < C; ++s) acc += sAi[s][r] * sT[s][c];
-            sR[r][c] = acc;
-            drk[idx] = acc;
+            for (int m = 16 * q; m < 16 * pb; ++m) acc += sM[16 * pb + r][m] * sAi[m][16 * q + c];
+            sX[16 * pb + r][16 * q + c] = acc;
         }
-    }
-    __syncthreads();
-    {
-        const float *dvn = bp.ws_dvn + (size_t)cid * C * V;
-        for (int idx = tid; idx < C * V; idx += 256) sT[idx / V][idx % V] = dvn[idx];
-    }
-    __syncthreads();
-    {
-        const int64_t vo = (int64_t)bi * p.svb + (int64_t)hv * p.svh + (int64_t)(n * C) * p.svt;
-        for (int idx = tid; idx < C * V; idx += 256) {
-            const int r = idx / V, j = idx % V;
-            if (r >= cv) continue;
+        __syncthreads();
+        for (int e = tid; e < nb * 256; e += 256) {
+            const int q = e >> 8, r = (e >> 4) & 15, c = e & 15, pb = q + d;
             float acc = 0.f;
-            for (int s = r; s < C; ++s) acc += sAi[s][r] * sT[s][j];
-            const int64_t o = vo + (int64_t)r * p.svt + j;
-            bp.dv[o] = acc * p.w[o];
-            bp.dw[o] = acc * p.v[o];
+#pragma unroll
+            for (int m = 0; m < 16; ++m) acc += sAi[16 * pb + r][16 * pb + m] * sX[16 * pb + m][16 * q + c];
+            sAi[16 * pb + r][16 * q + c] = -acc;
         }
+        __syncthreads();
     }
-    __syncthreads();
-    {
-        const float *Wf = p.ws_w + (size_t)cid * C * K; // A-operand fragments (row tile, key tile)
-        for (int idx = tid; idx < C * K; idx += 256) {
-            const int s = idx / K, c = idx % K;
-            sT[s][c] = Wf[((s >> 4) * NKT + (c >> 4)) * 256 + (((c & 15) >> 2) * 16 + (s & 15)) * 4 + (c & 3)];
-        }
-        const float *duu = bp.ws_duu + (size_t)cid * C * C;
-        for (int idx = tid; idx < C * C; idx += 256) sM[idx / C][idx % C] = duu[idx];
-    }
-    __syncthreads();
-    {
-        float *dakk = bp.ws_dakk + (size_t)cid * C * C;
-        for (int idx = tid; idx < C * C; idx += 256) {
-            const int r = idx / C, s = idx % C;
-            float val = 0.f;
-            if (s < r) {
-                float a = 0.f, b = 0.f;
-                for (int c = 0; c < K; ++c) a += sR[r][c] * sT[s][c];
-                for (int m = r; m < C; ++m) b += sAi[m][r] * sM[m][s];
-                val = -(a + b);
+
+    // [dRk | dRv] = Ai^T [dW | dv_new]: wave w takes column tiles w, w + 4, ...
+    const float *dWm = bp.ws_dwm + (size_t)cid * C * K, *dvn = bp.ws_dvn + (size_t)cid * C * V;
+    float *drk = bp.ws_drk + (size_t)cid * C * K;
+    const int64_t vo = (int64_t)bi * p.svb + (int64_t)hv * p.svh + (int64_t)(n * C) * p.svt;
+#pragma unroll 1
+    for (int ct = wave; ct < NCT; ct += 4) {
+        const bool kcol = ct < NKT;
+        const float *X = kcol ? dWm + 16 * ct : dvn + 16 * (ct - NKT);
+        const int ld = kcol ? K : V;
+        floatx4 xb[NT]; // B fragments: X[16 st + 4 g + j][column lr]
+#pragma unroll
+        for (int st = 0; st < NT; ++st)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xb[st][j] = X[(16 * st + 4 * lg + j) * ld + lr];
+#pragma unroll
+        for (int rt = 0; rt < NT; ++rt) {
+            floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = rt; st < NT; ++st) {
+                floatx4 a;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a[j] = sAi[16 * st + 4 * lg + j][16 * rt + lr];
+                acc = mfma4x(a, xb[st], acc);
             }
-            dakk[idx] = val;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * rt + 4 * lg + i;
+                if (kcol) {
+                    drk[r * K + 16 * ct + lr] = acc[i];
+                    sR[r][16 * ct + lr] = acc[i];
+                } else if (r < cv) {
+                    const int64_t o = vo + (int64_t)r * p.svt + 16 * (ct - NKT) + lr;
+                    bp.dv[o] = acc[i] * p.w[o];
+                    bp.dw[o] = acc[i] * p.v[o];
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // dA_kk tiles (rt, st), st <= rt: -(dRk W^T + Ai^T dUU), strictly lower
+    const floatx4 *Wf = reinterpret_cast<const floatx4 *>(p.ws_w) + (size_t)cid * (C * K / 4);
+    const float *duu = bp.ws_duu + (size_t)cid * C * C;
+    float *dakk = bp.ws_dakk + (size_t)cid * C * C;
+#pragma unroll 1
+    for (int tt = wave; tt < NT * NT; tt += 4) {
+        const int rt = tt / NT, st = tt % NT;
+        floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (st <= rt) {
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) // A: dRk rows 16 rt + lr; B: W^T = W's A fragment (st, kt)
+                acc = mfma4x(*reinterpret_cast<const floatx4 *>(&sR[16 * rt + lr][16 * kt + 4 * lg]),
+                             Wf[(st * NKT + kt) * 64 + lane], acc);
+#pragma unroll
+            for (int mt = rt; mt < NT; ++mt) { // A: Ai^T; B: dUU[16 mt + 4 g + j][16 st + lr]
+                floatx4 a, b;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    a[j] = sAi[16 * mt + 4 * lg + j][16 * rt + lr];
+                    b[j] = duu[(16 * mt + 4 * lg + j) * C + 16 * st + lr];
+                }
+                acc = mfma4x(a, b, acc);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 16 * rt + 4 * lg + i, s = 16 * st + lr;
+            dakk[r * C + s] = s < r ? -acc[i] : 0.f;
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Per-chunk decay-weighted terms and the elementwise chain (four waves), in
-// blocks of 32 key channels staged in LDS with G = cumsum g (log2 units).
-// For channel c and row r (E_rs = exp(G_r - G_s) <= 1 for s <= r):
-//   rq_r  = sum_{s<=r} dA_qk[r][s] k_s E_rs      (dq from A_qk, before scale)
-//   rkb_r = sum_{s<r}  dA_kk[r][s] k_s E_rs      (d(b k) from A_kk)
-//   ck_r  = sum_{t>=r} (scale dA_qk[t][r] q_t + [t>r] dA_kk[t][r] b_t k_t) E_tr
-//   dq  = scale (e^G dQG + rq)
-//   dkb = e^G dRk + rkb,  db = dkb k
-//   dk  = e^{G_last - G} dKd + ck + dkb b
-//   dG  = dQG QG + dRk Rk - dKd Kd + scale q rq + b k rkb - k ck
-//         (+ sum_s dKd_s Kd_s + dgam e^{G_last} at the last row)
-//   dg_t = sum_{r>=t} dG_r
+// Per-chunk decay-weighted terms and the elementwise chain.  One workgroup
+// of K/16 waves per chunk; wave w owns key channels 16 w .. 16 w + 15 for all
+// 64 rows.  With G = cumsum g (log2 units) and E_rs = exp(G_r - G_s), r >= s:
+//   rq_r  = sum_{s<=r} dA_qk[r][s] k_s E_rs        rkb_r = sum_{s<r} dA_kk[r][s] k_s E_rs
+//   ck_s  = sum_{r>=s} (scale dA_qk[r][s] q_r + dA_kk[r][s] b_r k_r) E_rs
+// as MFMA products over the time tiles, with the forward's split around the
+// row tile's reference Gb_p (G at the end of tile p-1):
+//   E_rs = exp(G_r - Gb_p) exp(Gb_p - G_s),
+// both factors <= 1 off the diagonal block; on it the second is bounded by
+// the tile's decay span, and channels whose span exceeds 96 take the exact
+// pairwise terms instead.  Then, per (row r, channel c):
+//   dq = scale (e^G dQG + rq),  dkb = e^G dRk + rkb,  db = dkb k
+//   dk = e^{G_last - G} dKd + ck + dkb b
+//   dG = scale q e^G dQG + b k e^G dRk - k e^{G_last - G} dKd + scale q rq + b k rkb - k ck
+//        (+ sum_s k_s e^{G_last - G_s} dKd_s + e^{G_last} dgam at the last row)
+//   dg_t = sum_{r >= t} dG_r.
+// Lane (g, n) holds channel 16 w + n at rows 16 t + 4 g + j of every tile t:
+// the rows of its B fragments, accumulator rows and elementwise terms.
 // ---------------------------------------------------------------------------
 template <int K, int V>
-__global__ __launch_bounds__(256) void bwd_decay_kernel(BwdParams bp) {
+__global__ __launch_bounds__(K * 4) void bwd_decay_kernel(BwdParams bp) {
     const ChunkParams &p = bp.f;
-    constexpr int CB = 32, RPT = C * CB / 256; // channels per block, rows per thread
-    __shared__ float sDA[C][C + 1], sDK[C][C + 1];
-    __shared__ float sG[C][CB + 1], sQ[C][CB + 1], sKk[C][CB + 1], sB[C][CB + 1];
-    __shared__ float sDG[C][CB + 1], sKT[C][CB + 1];
+    constexpr int NTH = K * 4, NSEG = NTH / K, RPS = C / NSEG; // cumsum: NSEG row segments per channel
+    constexpr int KP = K + 4, CP = C + 4;
+    __shared__ __attribute__((aligned(16))) float sG[C][KP]; // G (log2 units), then dG
+    __shared__ __attribute__((aligned(16))) float sDA[C][CP], sDK[C][CP];
+    __shared__ float sTot[NSEG][K];
     const int cid = blockIdx.x, bh = cid / p.NC, n = cid % p.NC;
     const int bi = bh / p.HV, hv = bh % p.HV, hk = hv / p.rep;
     const int cv = min(C, p.T - n * C);
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
     const float scale = p.scale;
+    const int ch = 16 * wave + lr; // this lane's channel
 
-    {
-        const float *daqk = bp.ws_daqk + (size_t)cid * C * C, *dakk = bp.ws_dakk + (size_t)cid * C * C;
-        for (int idx = tid; idx < C * C; idx += 256) {
-            sDA[idx / C][idx % C] = daqk[idx];
-            sDK[idx / C][idx % C] = dakk[idx];
-        }
-    }
     const int64_t ko = (int64_t)bi * p.sqb + (int64_t)hk * p.sqh + (int64_t)(n * C) * p.sqt;
     const int rq_ = (int)p.sqt;
     const __amdgpu_buffer_rsrc_t Rq = rows_rsrc(p.q + ko, rq_, cv, K), Rk = rows_rsrc(p.k + ko, rq_, cv, K);
     const __amdgpu_buffer_rsrc_t Rg = rows_rsrc(p.g + ko, rq_, cv, K), Rb = rows_rsrc(p.b + ko, rq_, cv, K);
-    // outputs: the caller's tensors (one value head per key head) or per value head for the GVA sum
+
+    // this lane's q, k, b at rows 16 t + 4 lg + j
+    float qv[NT][4], kv[NT][4], bv[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int o = (16 * t + 4 * lg + j) * rq_ + ch;
+            qv[t][j] = bld1(Rq, o);
+            kv[t][j] = bld1(Rk, o);
+            bv[t][j] = bld1(Rb, o);
+        }
+    // G = cumsum_t g per channel, in log2 units; dA_qk, dA_kk to LDS
+    {
+        const int c = tid % K, seg = tid / K;
+        float vals[RPS];
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < RPS; ++i) vals[i] = bld1(Rg, (seg * RPS + i) * rq_ + c);
+#pragma unroll
+        for (int i = 0; i < RPS; ++i) {
+            acc += vals[i];
+            vals[i] = acc;
+        }
+        sTot[seg][c] = acc;
+        const floatx4 *da = reinterpret_cast<const floatx4 *>(bp.ws_daqk + (size_t)cid * C * C);
+        const floatx4 *dk = reinterpret_cast<const floatx4 *>(bp.ws_dakk + (size_t)cid * C * C);
+        for (int f = tid; f < C * C / 4; f += NTH) {
+            const int r = f / (C / 4), c4 = f % (C / 4);
+            *reinterpret_cast<floatx4 *>(&sDA[r][4 * c4]) = da[f];
+            *reinterpret_cast<floatx4 *>(&sDK[r][4 * c4]) = dk[f];
+        }
+        __syncthreads();
+        float off = 0.f;
+        for (int s2 = 0; s2 < seg; ++s2) off += sTot[s2][c];
+#pragma unroll
+        for (int i = 0; i < RPS; ++i) sG[seg * RPS + i][c] = (vals[i] + off) * kLog2e;
+        __syncthreads();
+    }
+    float gv[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gv[t][j] = sG[16 * t + 4 * lg + j][ch];
+    const float gl = sG[C - 1][ch];
+    float gb[NT]; // Gb_t: G at the end of tile t-1
+    bool msk[NT]; // diagonal block of tile t beyond the safe span
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        gb[t] = t ? sG[16 * t - 1][ch] : 0.f;
+        msk[t] = gb[t] - sG[16 * t + 15][ch] > 96.f;
+    }
+
+    // row sums rq, rkb (accumulator rows 16 p + 4 lg + i, column = channel)
+    floatx4 rq[NT], rkb[NT], ck[NT];
+#pragma unroll
+    for (int pt = 0; pt < NT; ++pt) {
+        floatx4 aq = floatx4{0.f, 0.f, 0.f, 0.f}, ab = aq;
+#pragma unroll
+        for (int qt = 0; qt <= pt; ++qt) {
+            floatx4 kt;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float e = fast_exp2(gb[pt] - gv[qt][j]);
+                kt[j] = (qt == pt && msk[pt]) ? 0.f : kv[qt][j] * e;
+            }
+            aq = mfma4x(*reinterpret_cast<const floatx4 *>(&sDA[16 * pt + lr][16 * qt + 4 * lg]), kt, aq);
+            ab = mfma4x(*reinterpret_cast<const floatx4 *>(&sDK[16 * pt + lr][16 * qt + 4 * lg]), kt, ab);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float e = fast_exp2(gv[pt][i] - gb[pt]);
+            rq[pt][i] = aq[i] * e;
+            rkb[pt][i] = ab[i] * e;
+        }
+        if (msk[pt]) { // exact diagonal-block terms of this channel
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * pt + 4 * lg + i;
+                float sq = 0.f, sb = 0.f;
+                for (int s2 = 16 * pt; s2 <= r; ++s2) {
+                    const float ke = sG[s2][ch]; // G_s
+                    const float e = fast_exp2(gv[pt][i] - ke) * bld1(Rk, s2 * rq_ + ch);
+                    sq += sDA[r][s2] * e;
+                    sb += sDK[r][s2] * e;
+                }
+                rq[pt][i] += sq;
+                rkb[pt][i] += sb;
+            }
+        }
+    }
+    // column sums ck (accumulator rows 16 q + 4 lg + i)
+#pragma unroll
+    for (int qt = 0; qt < NT; ++qt) {
+        floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int pt = qt; pt < NT; ++pt) {
+            floatx4 bq, bb, a1, a2;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float e = fast_exp2(gv[pt][j] - gb[pt]);
+                bq[j] = scale * qv[pt][j] * e;
+                bb[j] = bv[pt][j] * kv[pt][j] * e;
+                a1[j] = sDA[16 * pt + 4 * lg + j][16 * qt + lr];
+                a2[j] = sDK[16 * pt + 4 * lg + j][16 * qt + lr];
+            }
+            floatx4 tmp = mfma4x(a1, bq, floatx4{0.f, 0.f, 0.f, 0.f});
+            tmp = mfma4x(a2, bb, tmp);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float e = (pt == qt && msk[qt]) ? 0.f : fast_exp2(gb[pt] - gv[qt][i]);
+                acc[i] += tmp[i] * e;
+            }
+        }
+        if (msk[qt]) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int s2 = 16 * qt + 4 * lg + i;
+                float sc = 0.f;
+                for (int r = s2; r < 16 * qt + 16; ++r) {
+                    const float e = fast_exp2(sG[r][ch] - gv[qt][i]);
+                    const int o = r * rq_ + ch;
+                    sc += (scale * sDA[r][s2] * bld1(Rq, o) + sDK[r][s2] * bld1(Rb, o) * bld1(Rk, o)) * e;
+                }
+                acc[i] += sc;
+            }
+        }
+        ck[qt] = acc;
+    }
+
+    // elementwise chain; dG to sG (this wave's own channels), dG_last partial sums
     float *oq, *okk, *og, *ob;
     int64_t ot, obase;
     if (p.rep == 1) {
@@ -447,66 +650,33 @@ __global__ __launch_bounds__(256) void bwd_decay_kernel(BwdParams bp) {
         obase = (int64_t)cid * C * K;
     }
     const float *dqg = bp.ws_dqg + (size_t)cid * C * K, *dkd = bp.ws_dkd + (size_t)cid * C * K;
-    const float *drk = bp.ws_drk + (size_t)cid * C * K, *dgam = bp.ws_dgam + (size_t)cid * K;
-
-    const int c = tid % CB, r0 = tid / CB; // rows r0 + 8 j
-    for (int cb = 0; cb < K; cb += CB) {
-        __syncthreads(); // the previous block's LDS is consumed
-        for (int idx = tid; idx < C * CB; idx += 256) {
-            const int r = idx / CB, cc = idx % CB, o = r * rq_ + cb + cc;
-            sQ[r][cc] = bld1(Rq, o);
-            sKk[r][cc] = bld1(Rk, o);
-            sB[r][cc] = bld1(Rb, o);
-            sG[r][cc] = bld1(Rg, o);
-        }
-        __syncthreads();
-        if (tid < CB) {
-            float acc = 0.f;
-            for (int r = 0; r < C; ++r) {
-                acc += sG[r][tid];
-                sG[r][tid] = acc * kLog2e;
-            }
-        }
-        __syncthreads();
-        const float gl = sG[C - 1][c];
-#pragma unroll 1
-        for (int jr = 0; jr < RPT; ++jr) {
-            const int r = r0 + 8 * jr;
-            const float Gr = sG[r][c], qr = sQ[r][c], kr = sKk[r][c], br = sB[r][c];
-            float rq = 0.f, rkb = 0.f, ck = 0.f;
-            for (int s = 0; s <= r; ++s) {
-                const float ke = sKk[s][c] * fast_exp2(Gr - sG[s][c]);
-                rq += sDA[r][s] * ke;
-                rkb += sDK[r][s] * ke; // dA_kk is zero on the diagonal
-            }
-            for (int t = r; t < C; ++t) {
-                const float e = fast_exp2(sG[t][c] - Gr);
-                ck += (scale * sDA[t][r] * sQ[t][c] + sDK[t][r] * sB[t][c] * sKk[t][c]) * e;
-            }
-            const int ch = cb + c;
-            const float eG = fast_exp2(Gr), eKd = fast_exp2(gl - Gr);
+    const float *drk = bp.ws_drk + (size_t)cid * C * K;
+    float kt_sum = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 16 * t + 4 * lg + i;
+            const float eG = fast_exp2(gv[t][i]), eKd = fast_exp2(gl - gv[t][i]);
             const float vqg = dqg[r * K + ch], vkd = dkd[r * K + ch], vrk = drk[r * K + ch];
-            const float dkb = eG * vrk + rkb;
-            const float dq = scale * (eG * vqg + rq);
-            const float dk = eKd * vkd + ck + dkb * br;
-            const float db = dkb * kr;
+            const float qr = qv[t][i], kr = kv[t][i], br = bv[t][i];
+            const float dkb = eG * vrk + rkb[t][i];
             const float kd = kr * eKd;
-            sDG[r][c] = vqg * scale * qr * eG + vrk * br * kr * eG - vkd * kd + scale * qr * rq + br * kr * rkb - kr * ck;
-            sKT[r][c] = vkd * kd;
             if (r < cv) {
-                oq[obase + r * ot + ch] = dq;
-                okk[obase + r * ot + ch] = dk;
-                ob[obase + r * ot + ch] = db;
+                oq[obase + r * ot + ch] = scale * (eG * vqg + rq[t][i]);
+                okk[obase + r * ot + ch] = eKd * vkd + ck[t][i] + dkb * br;
+                ob[obase + r * ot + ch] = dkb * kr;
             }
+            sG[r][ch] = scale * qr * (eG * vqg + rq[t][i]) + br * kr * (eG * vrk + rkb[t][i]) - vkd * kd - kr * ck[t][i];
+            kt_sum += vkd * kd;
         }
-        __syncthreads();
-        if (tid < CB) { // dG_last, then dg = reverse cumulative sum of dG
-            float run = dgam[cb + tid] * fast_exp2(sG[C - 1][tid]);
-            for (int r = 0; r < C; ++r) run += sKT[r][tid];
-            for (int r = C - 1; r >= 0; --r) {
-                run += sDG[r][tid];
-                if (r < cv) og[obase + r * ot + cb + tid] = run;
-            }
+    kt_sum += __shfl_xor(kt_sum, 16, 64);
+    kt_sum += __shfl_xor(kt_sum, 32, 64);
+    if (lg == 0) { // dG_last, then dg = reverse cumulative sum of dG (this lane's channel)
+        float run = kt_sum + bp.ws_dgam[(size_t)cid * K + ch] * fast_exp2(gl);
+        for (int r = C - 1; r >= 0; --r) {
+            run += sG[r][ch];
+            if (r < cv) og[obase + r * ot + ch] = run;
         }
     }
 }
@@ -548,7 +718,7 @@ hipError_t launch_bwd_t(const BwdParams &bp, hipStream_t s) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_solve_kernel<K, V>), dim3(nch), dim3(256), 0, s, bp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_decay_kernel<K, V>), dim3(nch), dim3(256), 0, s, bp);
+    hipLaunchKernelGGL((bwd_decay_kernel<K, V>), dim3(nch), dim3(K * 4), 0, s, bp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (p.rep > 1) {
         const int64_t total = (int64_t)p.B * (p.HV / p.rep) * p.T * p.K;
