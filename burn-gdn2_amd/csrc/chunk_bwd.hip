@@ -215,14 +215,20 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp) {
 //   dQG = dO S^T, dW = -dv_new S^T, dKd = v_new dS'^T       (C x K)
 //   dA_qk = tril(dO v_new^T), dUU = strict_tril(dv_new U^T)  (C x C)
 // and dgam = rowsum(dS' * S).  Wave w owns the 16 rows of time tile w of
-// every product, so its A fragments (rows of dO, dv_new, v_new) are its own;
-// the B fragments (rows of S, dS', v_new, U) are shared through L2.  The
-// accumulators of all of the wave's tiles stay in registers over the V loop.
+// every product: its A fragments (rows of dO, dv_new, v_new) come straight
+// from memory, and its accumulators stay in registers over the V loop.  The
+// B operands (16 columns of S, dS', v_new and U per step) are read once per
+// workgroup into a double-buffered LDS slice; the slice loads of step vb+1
+// are issued before step vb's products.
 // ---------------------------------------------------------------------------
 template <int K, int V>
 __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(BwdParams bp) {
     const ChunkParams &p = bp.f;
     constexpr int NKT = K / 16, NVB = V / 16;
+    constexpr int SP = 20;                            // padded row of a 16-column slice
+    constexpr int SF4 = K * 4 / 256, VF4 = C * 4 / 256; // float4 per thread: S (and dS') slice, v_new slice
+    __shared__ __attribute__((aligned(16))) float sS[2][K][SP], sD[2][K][SP], sV[2][C][SP];
+    __shared__ __attribute__((aligned(16))) floatx4 sU[2][NT * 64]; // U's fragments of this column block
     const int cid = blockIdx.x, bh = cid / p.NC, n = cid % p.NC;
     const int bi = bh / p.HV, hv = bh % p.HV;
     const int cv = min(C, p.T - n * C);
@@ -235,7 +241,7 @@ __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(BwdParams bp) {
     const __amdgpu_buffer_rsrc_t RdO = rows_rsrc(dO, ro, cv, V);
     const float *Sn = p.ws_sn + (size_t)cid * K * V, *dSn = bp.ws_dsn + (size_t)cid * K * V;
     const float *vn = p.ws_vn + (size_t)cid * C * V, *dvn = bp.ws_dvn + (size_t)cid * C * V;
-    const float *Uf = p.ws_u + (size_t)cid * C * V; // accumulator fragments (column tile, row tile)
+    const floatx4 *Uf = reinterpret_cast<const floatx4 *>(p.ws_u + (size_t)cid * C * V);
     const int arow = 16 * wave + lr;
 
     floatx4 aQ[NKT], aW[NKT], aK[NKT], aA[NT], aU[NT];
@@ -243,42 +249,78 @@ __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(BwdParams bp) {
     for (int t = 0; t < NKT; ++t) aQ[t] = aW[t] = aK[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < NT; ++t) aA[t] = aU[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float gam[SF4]; // dS' * S partial sums of the rows this thread stages
+#pragma unroll
+    for (int i = 0; i < SF4; ++i) gam[i] = 0.f;
 
+    floatx4 ls[SF4], ld_[SF4], lv[VF4], lu;
+    auto load_slice = [&](int vb) {
+#pragma unroll
+        for (int i = 0; i < SF4; ++i) {
+            const int f = i * 256 + tid, r = f >> 2, c4 = f & 3;
+            ls[i] = *reinterpret_cast<const floatx4 *>(Sn + r * V + 16 * vb + 4 * c4);
+            ld_[i] = *reinterpret_cast<const floatx4 *>(dSn + r * V + 16 * vb + 4 * c4);
+        }
+#pragma unroll
+        for (int i = 0; i < VF4; ++i) {
+            const int f = i * 256 + tid, r = f >> 2, c4 = f & 3;
+            lv[i] = *reinterpret_cast<const floatx4 *>(vn + r * V + 16 * vb + 4 * c4);
+        }
+        lu = Uf[vb * NT * 64 + tid]; // tiles (vb, 0 .. NT-1): NT * 64 float4 = 256
+    };
+    auto store_slice = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < SF4; ++i) {
+            const int f = i * 256 + tid, r = f >> 2, c4 = f & 3;
+            *reinterpret_cast<floatx4 *>(&sS[buf][r][4 * c4]) = ls[i];
+            *reinterpret_cast<floatx4 *>(&sD[buf][r][4 * c4]) = ld_[i];
+            const floatx4 pr = ls[i] * ld_[i];
+            gam[i] += pr[0] + pr[1] + pr[2] + pr[3];
+        }
+#pragma unroll
+        for (int i = 0; i < VF4; ++i) {
+            const int f = i * 256 + tid, r = f >> 2, c4 = f & 3;
+            *reinterpret_cast<floatx4 *>(&sV[buf][r][4 * c4]) = lv[i];
+        }
+        sU[buf][tid] = lu;
+    };
+    static_assert(NT * 64 == 256, "one U fragment per thread");
+
+    load_slice(0);
+    store_slice(0);
+    __syncthreads();
 #pragma unroll 1
     for (int vb = 0; vb < NVB; ++vb) {
+        const int buf = vb & 1;
+        if (vb + 1 < NVB) load_slice(vb + 1);
         const int c0 = 16 * vb + 4 * lg;
         const floatx4 fO = bld4(RdO, arow * ro + c0);
         const floatx4 fD = *reinterpret_cast<const floatx4 *>(dvn + arow * V + c0);
         const floatx4 fV = *reinterpret_cast<const floatx4 *>(vn + arow * V + c0);
-        floatx4 bS[NKT], bD[NKT];
 #pragma unroll
         for (int t = 0; t < NKT; ++t) {
-            bS[t] = *reinterpret_cast<const floatx4 *>(Sn + (16 * t + lr) * V + c0);
-            bD[t] = *reinterpret_cast<const floatx4 *>(dSn + (16 * t + lr) * V + c0);
-        }
-        floatx4 bV[NT], bU[NT];
-#pragma unroll
-        for (int st = 0; st < NT; ++st) {
-            bV[st] = bU[st] = floatx4{0.f, 0.f, 0.f, 0.f};
-            if (st <= wave) {
-                bV[st] = *reinterpret_cast<const floatx4 *>(vn + (16 * st + lr) * V + c0);
-                // U[16 st + lr][c0 + i]: tile (vb, st), lane (lr / 4, 4 lg + i), component lr % 4
-#pragma unroll
-                for (int i = 0; i < 4; ++i) bU[st][i] = Uf[((vb * NT + st) * 64 + (lr >> 2) * 16 + 4 * lg + i) * 4 + (lr & 3)];
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < NKT; ++t) {
-            aQ[t] = mfma4x(fO, bS[t], aQ[t]);
-            aW[t] = mfma4x(fD, bS[t], aW[t]);
-            aK[t] = mfma4x(fV, bD[t], aK[t]);
+            const floatx4 bS = *reinterpret_cast<const floatx4 *>(&sS[buf][16 * t + lr][4 * lg]);
+            const floatx4 bD = *reinterpret_cast<const floatx4 *>(&sD[buf][16 * t + lr][4 * lg]);
+            aQ[t] = mfma4x(fO, bS, aQ[t]);
+            aW[t] = mfma4x(fD, bS, aW[t]);
+            aK[t] = mfma4x(fV, bD, aK[t]);
         }
 #pragma unroll
         for (int st = 0; st < NT; ++st) {
             if (st <= wave) {
-                aA[st] = mfma4x(fO, bV[st], aA[st]);
-                aU[st] = mfma4x(fD, bU[st], aU[st]);
+                const floatx4 bV = *reinterpret_cast<const floatx4 *>(&sV[buf][16 * st + lr][4 * lg]);
+                // U[16 st + lr][16 vb + 4 lg + j]: fragment st, lane (lr / 4, 4 lg + j), component lr % 4
+                const float *uf = reinterpret_cast<const float *>(&sU[buf][st * 64]);
+                floatx4 bU;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bU[j] = uf[((lr >> 2) * 16 + 4 * lg + j) * 4 + (lr & 3)];
+                aA[st] = mfma4x(fO, bV, aA[st]);
+                aU[st] = mfma4x(fD, bU, aU[st]);
             }
+        }
+        if (vb + 1 < NVB) {
+            store_slice(buf ^ 1);
+            __syncthreads();
         }
     }
     float *oQ = bp.ws_dqg + (size_t)cid * C * K, *oW = bp.ws_dwm + (size_t)cid * C * K;
@@ -300,17 +342,13 @@ __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(BwdParams bp) {
             oU[r * C + s] = s < r ? aU[st][i] : 0.f;
         }
     }
-
-    // dgam[c] = sum_v dS'[c][v] S[c][v]: 256 / K threads per row
-    constexpr int TPR = 256 / K;
-    {
-        const int c = tid / TPR, part = tid % TPR;
-        float acc = 0.f;
-#pragma unroll 4
-        for (int v = part; v < V; v += TPR) acc += dSn[(size_t)c * V + v] * Sn[(size_t)c * V + v];
+    // dgam: the four threads that staged a row's 16-column pieces are lanes 4m .. 4m + 3
 #pragma unroll
-        for (int off = 1; off < TPR; off <<= 1) acc += __shfl_xor(acc, off, 64);
-        if (part == 0) bp.ws_dgam[(size_t)cid * K + c] = acc;
+    for (int i = 0; i < SF4; ++i) {
+        float g = gam[i];
+        g += __shfl_xor(g, 1, 64);
+        g += __shfl_xor(g, 2, 64);
+        if ((tid & 3) == 0) bp.ws_dgam[(size_t)cid * K + ((i * 256 + tid) >> 2)] = g;
     }
 }
 
