@@ -524,7 +524,7 @@ __global__ __launch_bounds__(256, 2) void bwd_solve_kernel(BwdParams bp) {
 // the rows of its B fragments, accumulator rows and elementwise terms.
 // ---------------------------------------------------------------------------
 template <int K, int V>
-__global__ __launch_bounds__(K * 4) void bwd_decay_kernel(BwdParams bp) {
+__global__ __launch_bounds__(K * 4, K / 32) void bwd_decay_kernel(BwdParams bp) {
     const ChunkParams &p = bp.f;
     constexpr int NTH = K * 4, NSEG = NTH / K, RPS = C / NSEG; // cumsum: NSEG row segments per channel
     constexpr int KP = K + 4, CP = C + 4;
@@ -545,17 +545,12 @@ __global__ __launch_bounds__(K * 4) void bwd_decay_kernel(BwdParams bp) {
     const __amdgpu_buffer_rsrc_t Rq = rows_rsrc(p.q + ko, rq_, cv, K), Rk = rows_rsrc(p.k + ko, rq_, cv, K);
     const __amdgpu_buffer_rsrc_t Rg = rows_rsrc(p.g + ko, rq_, cv, K), Rb = rows_rsrc(p.b + ko, rq_, cv, K);
 
-    // this lane's q, k, b at rows 16 t + 4 lg + j
-    float qv[NT][4], kv[NT][4], bv[NT][4];
+    // this lane's k at rows 16 t + 4 lg + j (q and b are loaded where used)
+    float kv[NT][4];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int o = (16 * t + 4 * lg + j) * rq_ + ch;
-            qv[t][j] = bld1(Rq, o);
-            kv[t][j] = bld1(Rk, o);
-            bv[t][j] = bld1(Rb, o);
-        }
+        for (int j = 0; j < 4; ++j) kv[t][j] = bld1(Rk, (16 * t + 4 * lg + j) * rq_ + ch);
     // G = cumsum_t g per channel, in log2 units; dA_qk, dA_kk to LDS
     {
         const int c = tid % K, seg = tid / K;
@@ -597,84 +592,6 @@ __global__ __launch_bounds__(K * 4) void bwd_decay_kernel(BwdParams bp) {
         msk[t] = gb[t] - sG[16 * t + 15][ch] > 96.f;
     }
 
-    // row sums rq, rkb (accumulator rows 16 p + 4 lg + i, column = channel)
-    floatx4 rq[NT], rkb[NT], ck[NT];
-#pragma unroll
-    for (int pt = 0; pt < NT; ++pt) {
-        floatx4 aq = floatx4{0.f, 0.f, 0.f, 0.f}, ab = aq;
-#pragma unroll
-        for (int qt = 0; qt <= pt; ++qt) {
-            floatx4 kt;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float e = fast_exp2(gb[pt] - gv[qt][j]);
-                kt[j] = (qt == pt && msk[pt]) ? 0.f : kv[qt][j] * e;
-            }
-            aq = mfma4x(*reinterpret_cast<const floatx4 *>(&sDA[16 * pt + lr][16 * qt + 4 * lg]), kt, aq);
-            ab = mfma4x(*reinterpret_cast<const floatx4 *>(&sDK[16 * pt + lr][16 * qt + 4 * lg]), kt, ab);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float e = fast_exp2(gv[pt][i] - gb[pt]);
-            rq[pt][i] = aq[i] * e;
-            rkb[pt][i] = ab[i] * e;
-        }
-        if (msk[pt]) { // exact diagonal-block terms of this channel
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 16 * pt + 4 * lg + i;
-                float sq = 0.f, sb = 0.f;
-                for (int s2 = 16 * pt; s2 <= r; ++s2) {
-                    const float ke = sG[s2][ch]; // G_s
-                    const float e = fast_exp2(gv[pt][i] - ke) * bld1(Rk, s2 * rq_ + ch);
-                    sq += sDA[r][s2] * e;
-                    sb += sDK[r][s2] * e;
-                }
-                rq[pt][i] += sq;
-                rkb[pt][i] += sb;
-            }
-        }
-    }
-    // column sums ck (accumulator rows 16 q + 4 lg + i)
-#pragma unroll
-    for (int qt = 0; qt < NT; ++qt) {
-        floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int pt = qt; pt < NT; ++pt) {
-            floatx4 bq, bb, a1, a2;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float e = fast_exp2(gv[pt][j] - gb[pt]);
-                bq[j] = scale * qv[pt][j] * e;
-                bb[j] = bv[pt][j] * kv[pt][j] * e;
-                a1[j] = sDA[16 * pt + 4 * lg + j][16 * qt + lr];
-                a2[j] = sDK[16 * pt + 4 * lg + j][16 * qt + lr];
-            }
-            floatx4 tmp = mfma4x(a1, bq, floatx4{0.f, 0.f, 0.f, 0.f});
-            tmp = mfma4x(a2, bb, tmp);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float e = (pt == qt && msk[qt]) ? 0.f : fast_exp2(gb[pt] - gv[qt][i]);
-                acc[i] += tmp[i] * e;
-            }
-        }
-        if (msk[qt]) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int s2 = 16 * qt + 4 * lg + i;
-                float sc = 0.f;
-                for (int r = s2; r < 16 * qt + 16; ++r) {
-                    const float e = fast_exp2(sG[r][ch] - gv[qt][i]);
-                    const int o = r * rq_ + ch;
-                    sc += (scale * sDA[r][s2] * bld1(Rq, o) + sDK[r][s2] * bld1(Rb, o) * bld1(Rk, o)) * e;
-                }
-                acc[i] += sc;
-            }
-        }
-        ck[qt] = acc;
-    }
-
-    // elementwise chain; dG to sG (this wave's own channels), dG_last partial sums
     float *oq, *okk, *og, *ob;
     int64_t ot, obase;
     if (p.rep == 1) {
@@ -690,24 +607,106 @@ __global__ __launch_bounds__(K * 4) void bwd_decay_kernel(BwdParams bp) {
     const float *dqg = bp.ws_dqg + (size_t)cid * C * K, *dkd = bp.ws_dkd + (size_t)cid * C * K;
     const float *drk = bp.ws_drk + (size_t)cid * C * K;
     float kt_sum = 0.f;
+
+    // Tile by tile: the row sums of row tile t (rows 16 t + 4 lg + i, column =
+    // channel), the column sums of column tile t, then tile t's elementwise
+    // terms, whose dG overwrites tile t's rows of G (only this wave reads
+    // this channel's G, and every later use of tile t's G is from registers).
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+    for (int t = 0; t < NT; ++t) {
+        floatx4 rq, rkb, ck;
+        {
+            floatx4 aq = floatx4{0.f, 0.f, 0.f, 0.f}, ab = aq;
+#pragma unroll
+            for (int qt = 0; qt <= t; ++qt) {
+                floatx4 kt;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float e = fast_exp2(gb[t] - gv[qt][j]);
+                    kt[j] = (qt == t && msk[t]) ? 0.f : kv[qt][j] * e;
+                }
+                aq = mfma4x(*reinterpret_cast<const floatx4 *>(&sDA[16 * t + lr][16 * qt + 4 * lg]), kt, aq);
+                ab = mfma4x(*reinterpret_cast<const floatx4 *>(&sDK[16 * t + lr][16 * qt + 4 * lg]), kt, ab);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float e = fast_exp2(gv[t][i] - gb[t]);
+                rq[i] = aq[i] * e;
+                rkb[i] = ab[i] * e;
+            }
+            if (msk[t]) { // exact diagonal-block terms of this channel
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 16 * t + 4 * lg + i;
+                    float sq = 0.f, sb = 0.f;
+                    for (int s2 = 16 * t; s2 <= r; ++s2) {
+                        const float e = fast_exp2(gv[t][i] - sG[s2][ch]) * bld1(Rk, s2 * rq_ + ch);
+                        sq += sDA[r][s2] * e;
+                        sb += sDK[r][s2] * e;
+                    }
+                    rq[i] += sq;
+                    rkb[i] += sb;
+                }
+            }
+        }
+        {
+            floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int pt = t; pt < NT; ++pt) {
+                floatx4 bq, bb, a1, a2;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float e = fast_exp2(gv[pt][j] - gb[pt]);
+                    const int o = (16 * pt + 4 * lg + j) * rq_ + ch;
+                    bq[j] = scale * bld1(Rq, o) * e;
+                    bb[j] = bld1(Rb, o) * kv[pt][j] * e;
+                    a1[j] = sDA[16 * pt + 4 * lg + j][16 * t + lr];
+                    a2[j] = sDK[16 * pt + 4 * lg + j][16 * t + lr];
+                }
+                floatx4 tmp = mfma4x(a1, bq, floatx4{0.f, 0.f, 0.f, 0.f});
+                tmp = mfma4x(a2, bb, tmp);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float e = (pt == t && msk[t]) ? 0.f : fast_exp2(gb[pt] - gv[t][i]);
+                    acc[i] += tmp[i] * e;
+                }
+            }
+            if (msk[t]) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int s2 = 16 * t + 4 * lg + i;
+                    float sc = 0.f;
+                    for (int r = s2; r < 16 * t + 16; ++r) {
+                        const float e = fast_exp2(sG[r][ch] - gv[t][i]);
+                        const int o = r * rq_ + ch;
+                        sc += (scale * sDA[r][s2] * bld1(Rq, o) + sDK[r][s2] * bld1(Rb, o) * bld1(Rk, o)) * e;
+                    }
+                    acc[i] += sc;
+                }
+            }
+            ck = acc;
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 16 * t + 4 * lg + i;
             const float eG = fast_exp2(gv[t][i]), eKd = fast_exp2(gl - gv[t][i]);
             const float vqg = dqg[r * K + ch], vkd = dkd[r * K + ch], vrk = drk[r * K + ch];
-            const float qr = qv[t][i], kr = kv[t][i], br = bv[t][i];
-            const float dkb = eG * vrk + rkb[t][i];
+            const int o = r * rq_ + ch;
+            const float qr = bld1(Rq, o), kr = kv[t][i], br = bld1(Rb, o);
+            const float dkb = eG * vrk + rkb[i];
             const float kd = kr * eKd;
             if (r < cv) {
-                oq[obase + r * ot + ch] = scale * (eG * vqg + rq[t][i]);
-                okk[obase + r * ot + ch] = eKd * vkd + ck[t][i] + dkb * br;
+                oq[obase + r * ot + ch] = scale * (eG * vqg + rq[i]);
+                okk[obase + r * ot + ch] = eKd * vkd + ck[i] + dkb * br;
                 ob[obase + r * ot + ch] = dkb * kr;
             }
-            sG[r][ch] = scale * qr * (eG * vqg + rq[t][i]) + br * kr * (eG * vrk + rkb[t][i]) - vkd * kd - kr * ck[t][i];
             kt_sum += vkd * kd;
+            const float dG = scale * qr * (eG * vqg + rq[i]) + br * kr * dkb - vkd * kd - kr * ck[i];
+            // tile t's G rows are read by this lane's column-pass pairwise terms of
+            // tile t only (done above), so they can be overwritten now
+            sG[r][ch] = dG;
         }
+    }
     kt_sum += __shfl_xor(kt_sum, 16, 64);
     kt_sum += __shfl_xor(kt_sum, 32, 64);
     if (lg == 0) { // dG_last, then dg = reverse cumulative sum of dG (this lane's channel)
