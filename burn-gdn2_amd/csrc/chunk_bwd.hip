@@ -36,14 +36,19 @@ struct BwdParams {
     float *dq, *dk, *dg, *db;         // strided like q (f.sqb, f.sqh, f.sqt)
     float *dv, *dw;                   // strided like v (f.svb, f.svh, f.svt)
     float *d_state0;                  // [B, HV, K, V]
-    // per chunk (chunk id = (b * HV + hv) * NC + n), row-major
-    float *ws_dsn;                    // K*V  dL/d(state leaving the chunk)
-    float *ws_dvn;                    // C*V  dL/dv_new
-    float *ws_dqg, *ws_dwm, *ws_dkd;  // C*K  dL/dQG, dL/dW, dL/dKd
-    float *ws_daqk, *ws_duu;          // C*C  dL/dA_qk (lower), dv_new U^T (strictly lower)
+    // per chunk (chunk id = (b * HV + hv) * NC + n).  "Row-major" or
+    // "fragments": 16 x 16 tiles (row tile, column tile) in row-major tile order,
+    // each 64 lanes x float4 in accumulator layout (lane (g, c) holds rows
+    // 4 g .. 4 g + 3 of column c), so that every access is one 16-byte load.
+    float *ws_dsn;                    // K*V  dL/d(state leaving the chunk), row-major
+    float *ws_dvn;                    // C*V  dL/dv_new, row-major
+    float *ws_dvnf;                   // C*V  dL/dv_new, fragments
+    float *ws_dqg, *ws_dwm, *ws_dkd;  // C*K  dL/dQG, dL/dW, dL/dKd, fragments
+    float *ws_daqk;                   // C*C  dL/dA_qk (lower), row-major
+    float *ws_duu;                    // C*C  dv_new U^T (strictly lower), fragments
     float *ws_dgam;                   // K    dL/d e^{G_last}
-    float *ws_drk;                    // C*K  dL/dRk
-    float *ws_dakk;                   // C*C  dL/dA_kk (strictly lower)
+    float *ws_drk;                    // C*K  dL/dRk, fragments
+    float *ws_dakk;                   // C*C  dL/dA_kk (strictly lower), row-major
     float *ws_kgrad;                  // rep > 1: 4 x (C*K per chunk): dq, dk, dg, db per value head
 };
 
@@ -157,6 +162,10 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp) {
             for (int st = 0; st < NT; ++st)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) Dvn[(size_t)(16 * st + 4 * lg + i) * V + col] = dvn[st][i];
+            floatx4 *Dvf = reinterpret_cast<floatx4 *>(bp.ws_dvnf) + cid * (C * V / 4);
+            const int vt = vs * 4 + wave, nvt = V / 16;
+#pragma unroll
+            for (int st = 0; st < NT; ++st) Dvf[(st * nvt + vt) * 64 + lane] = dvn[st];
         }
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
@@ -323,24 +332,27 @@ __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(BwdParams bp) {
             __syncthreads();
         }
     }
-    float *oQ = bp.ws_dqg + (size_t)cid * C * K, *oW = bp.ws_dwm + (size_t)cid * C * K;
-    float *oK = bp.ws_dkd + (size_t)cid * C * K;
-    float *oA = bp.ws_daqk + (size_t)cid * C * C, *oU = bp.ws_duu + (size_t)cid * C * C;
+    floatx4 *oQ = reinterpret_cast<floatx4 *>(bp.ws_dqg) + (size_t)cid * (C * K / 4);
+    floatx4 *oW = reinterpret_cast<floatx4 *>(bp.ws_dwm) + (size_t)cid * (C * K / 4);
+    floatx4 *oK = reinterpret_cast<floatx4 *>(bp.ws_dkd) + (size_t)cid * (C * K / 4);
+    floatx4 *oU = reinterpret_cast<floatx4 *>(bp.ws_duu) + (size_t)cid * (C * C / 4);
+    float *oA = bp.ws_daqk + (size_t)cid * C * C;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = 16 * wave + 4 * lg + i;
+    for (int t = 0; t < NKT; ++t) {
+        oQ[(wave * NKT + t) * 64 + lane] = aQ[t];
+        oW[(wave * NKT + t) * 64 + lane] = -aW[t];
+        oK[(wave * NKT + t) * 64 + lane] = aK[t];
+    }
 #pragma unroll
-        for (int t = 0; t < NKT; ++t) {
-            oQ[r * K + 16 * t + lr] = aQ[t][i];
-            oW[r * K + 16 * t + lr] = -aW[t][i];
-            oK[r * K + 16 * t + lr] = aK[t][i];
+    for (int st = 0; st < NT; ++st) {
+        floatx4 u = aU[st];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 16 * wave + 4 * lg + i, sc = 16 * st + lr;
+            oA[r * C + sc] = sc <= r ? aA[st][i] : 0.f;
+            u[i] = sc < r ? u[i] : 0.f;
         }
-#pragma unroll
-        for (int st = 0; st < NT; ++st) {
-            const int s = 16 * st + lr;
-            oA[r * C + s] = s <= r ? aA[st][i] : 0.f;
-            oU[r * C + s] = s < r ? aU[st][i] : 0.f;
-        }
+        oU[(wave * NT + st) * 64 + lane] = u;
     }
     // dgam: the four threads that staged a row's 16-column pieces are lanes 4m .. 4m + 3
 #pragma unroll
@@ -432,19 +444,18 @@ __global__ __launch_bounds__(256, 2) void bwd_solve_kernel(BwdParams bp) {
     }
 
     // [dRk | dRv] = Ai^T [dW | dv_new]: wave w takes column tiles w, w + 4, ...
-    const float *dWm = bp.ws_dwm + (size_t)cid * C * K, *dvn = bp.ws_dvn + (size_t)cid * C * V;
-    float *drk = bp.ws_drk + (size_t)cid * C * K;
+    // (B fragments: the accumulator-layout tiles of dW and dv_new)
+    const floatx4 *dWf = reinterpret_cast<const floatx4 *>(bp.ws_dwm) + (size_t)cid * (C * K / 4);
+    const floatx4 *dVf = reinterpret_cast<const floatx4 *>(bp.ws_dvnf) + (size_t)cid * (C * V / 4);
+    floatx4 *drk = reinterpret_cast<floatx4 *>(bp.ws_drk) + (size_t)cid * (C * K / 4);
     const int64_t vo = (int64_t)bi * p.svb + (int64_t)hv * p.svh + (int64_t)(n * C) * p.svt;
 #pragma unroll 1
     for (int ct = wave; ct < NCT; ct += 4) {
         const bool kcol = ct < NKT;
-        const float *X = kcol ? dWm + 16 * ct : dvn + 16 * (ct - NKT);
-        const int ld = kcol ? K : V;
         floatx4 xb[NT]; // B fragments: X[16 st + 4 g + j][column lr]
 #pragma unroll
         for (int st = 0; st < NT; ++st)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) xb[st][j] = X[(16 * st + 4 * lg + j) * ld + lr];
+            xb[st] = kcol ? dWf[(st * NKT + ct) * 64 + lane] : dVf[(st * NVT + ct - NKT) * 64 + lane];
 #pragma unroll
         for (int rt = 0; rt < NT; ++rt) {
             floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -455,11 +466,11 @@ __global__ __launch_bounds__(256, 2) void bwd_solve_kernel(BwdParams bp) {
                 for (int j = 0; j < 4; ++j) a[j] = sAi[16 * st + 4 * lg + j][16 * rt + lr];
                 acc = mfma4x(a, xb[st], acc);
             }
+            if (kcol) drk[(rt * NKT + ct) * 64 + lane] = acc;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = 16 * rt + 4 * lg + i;
                 if (kcol) {
-                    drk[r * K + 16 * ct + lr] = acc[i];
                     sR[r][16 * ct + lr] = acc[i];
                 } else if (r < cv) {
                     const int64_t o = vo + (int64_t)r * p.svt + 16 * (ct - NKT) + lr;
@@ -473,7 +484,7 @@ __global__ __launch_bounds__(256, 2) void bwd_solve_kernel(BwdParams bp) {
 
     // dA_kk tiles (rt, st), st <= rt: -(dRk W^T + Ai^T dUU), strictly lower
     const floatx4 *Wf = reinterpret_cast<const floatx4 *>(p.ws_w) + (size_t)cid * (C * K / 4);
-    const float *duu = bp.ws_duu + (size_t)cid * C * C;
+    const floatx4 *duu = reinterpret_cast<const floatx4 *>(bp.ws_duu) + (size_t)cid * (C * C / 4);
     float *dakk = bp.ws_dakk + (size_t)cid * C * C;
 #pragma unroll 1
     for (int tt = wave; tt < NT * NT; tt += 4) {
@@ -485,14 +496,11 @@ __global__ __launch_bounds__(256, 2) void bwd_solve_kernel(BwdParams bp) {
                 acc = mfma4x(*reinterpret_cast<const floatx4 *>(&sR[16 * rt + lr][16 * kt + 4 * lg]),
                              Wf[(st * NKT + kt) * 64 + lane], acc);
 #pragma unroll
-            for (int mt = rt; mt < NT; ++mt) { // A: Ai^T; B: dUU[16 mt + 4 g + j][16 st + lr]
-                floatx4 a, b;
+            for (int mt = rt; mt < NT; ++mt) { // A: Ai^T; B: dUU's tile (mt, st)
+                floatx4 a;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    a[j] = sAi[16 * mt + 4 * lg + j][16 * rt + lr];
-                    b[j] = duu[(16 * mt + 4 * lg + j) * C + 16 * st + lr];
-                }
-                acc = mfma4x(a, b, acc);
+                for (int j = 0; j < 4; ++j) a[j] = sAi[16 * mt + 4 * lg + j][16 * rt + lr];
+                acc = mfma4x(a, duu[(mt * NT + st) * 64 + lane], acc);
             }
         }
 #pragma unroll
@@ -604,8 +612,11 @@ __global__ __launch_bounds__(K * 4, K / 32) void bwd_decay_kernel(BwdParams bp) 
         ot = K;
         obase = (int64_t)cid * C * K;
     }
-    const float *dqg = bp.ws_dqg + (size_t)cid * C * K, *dkd = bp.ws_dkd + (size_t)cid * C * K;
-    const float *drk = bp.ws_drk + (size_t)cid * C * K;
+    // dQG, dKd, dRk tiles (t, wave): lane (lg, lr) holds rows 16 t + 4 lg + i of channel ch
+    const floatx4 *dqg = reinterpret_cast<const floatx4 *>(bp.ws_dqg) + (size_t)cid * (C * K / 4);
+    const floatx4 *dkd = reinterpret_cast<const floatx4 *>(bp.ws_dkd) + (size_t)cid * (C * K / 4);
+    const floatx4 *drk = reinterpret_cast<const floatx4 *>(bp.ws_drk) + (size_t)cid * (C * K / 4);
+    constexpr int NKT = K / 16;
     float kt_sum = 0.f;
 
     // Tile by tile: the row sums of row tile t (rows 16 t + 4 lg + i, column =
@@ -686,11 +697,13 @@ __global__ __launch_bounds__(K * 4, K / 32) void bwd_decay_kernel(BwdParams bp) 
             }
             ck = acc;
         }
+        const floatx4 fqg = dqg[(t * NKT + wave) * 64 + lane], fkd = dkd[(t * NKT + wave) * 64 + lane];
+        const floatx4 frk = drk[(t * NKT + wave) * 64 + lane];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 16 * t + 4 * lg + i;
             const float eG = fast_exp2(gv[t][i]), eKd = fast_exp2(gl - gv[t][i]);
-            const float vqg = dqg[r * K + ch], vkd = dkd[r * K + ch], vrk = drk[r * K + ch];
+            const float vqg = fqg[i], vkd = fkd[i], vrk = frk[i];
             const int o = r * rq_ + ch;
             const float qr = bld1(Rq, o), kr = kv[t][i], br = bld1(Rb, o);
             const float dkb = eG * vrk + rkb[i];
@@ -782,7 +795,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // The backward's workspace after the forward's: the training operands of the
 // forward, then the backward's per-chunk arrays.
 struct BwdLayout {
-    size_t fwd, wt, qgt, kd, aqkt, akk, sn, vn, dsn, dvn, dqg, dwm, dkd, daqk, duu, dgam, drk, dakk, kgrad, total;
+    size_t fwd, wt, qgt, kd, aqkt, akk, sn, vn, dsn, dvn, dvnf, dqg, dwm, dkd, daqk, duu, dgam, drk, dakk, kgrad, total;
 };
 
 BwdLayout bwd_layout(const gdn2_chunk_args *a) {
@@ -801,6 +814,7 @@ BwdLayout bwd_layout(const gdn2_chunk_args *a) {
     L.vn = take(Cs * V);
     L.dsn = take(K * V);
     L.dvn = take(Cs * V);
+    L.dvnf = take(Cs * V);
     L.dqg = take(Cs * K);
     L.dwm = take(Cs * K);
     L.dkd = take(Cs * K);
@@ -868,6 +882,7 @@ extern "C" gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *a, gdn2_str
     bp.d_state0 = a->d_state0;
     bp.ws_dsn = reinterpret_cast<float *>(ws + L.dsn);
     bp.ws_dvn = reinterpret_cast<float *>(ws + L.dvn);
+    bp.ws_dvnf = reinterpret_cast<float *>(ws + L.dvnf);
     bp.ws_dqg = reinterpret_cast<float *>(ws + L.dqg);
     bp.ws_dwm = reinterpret_cast<float *>(ws + L.dwm);
     bp.ws_dkd = reinterpret_cast<float *>(ws + L.dkd);
