@@ -53,6 +53,7 @@ def parse():
     ap.add_argument("--no-layer", action="store_true")
     ap.add_argument("--layer-steps", type=int, default=5)
     ap.add_argument("--decode-prefill", type=int, default=2048)
+    ap.add_argument("--no-backward", action="store_true", help="skip the chunked backward timing")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="end with a 1 GiB device-to-device copy (reference kernel for HBM counters)")
     ap.add_argument("--stats-summary", metavar="KERNEL_STATS_CSV",
@@ -355,6 +356,54 @@ def traffic_summary(fetch_csv, write_csv):
     return out
 
 
+def bench_backward(torch, G, args, dev):
+    """gdn2_chunk_bwd_f32 on the prefill workload's operands (the layer's own
+    project() outputs, d_out ~ N(0,1)): the gradients of q, k, g, b, v, w and
+    S0, recomputing the forward's per-chunk quantities.  Outputs and the
+    workspace are allocated before the timed region."""
+    import ctypes
+
+    from gdn2_amd import _capi as CA
+    from gdn2_amd.ops import _p, _stream, chunk_args
+
+    cfg = G.Gdn2Config(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0, mode="chunk", chunk_size=64)
+    layer = G.GatedDeltaNet2(cfg, seed=1337)
+    B, T, H, K, V = args.batch, args.seq, cfg.num_heads, cfg.head_dim, cfg.v_head
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(42)
+    x = torch.randn((B, T, cfg.hidden_size), generator=gen, device=dev, dtype=torch.float32)
+    P = layer.project(x)
+    del x, layer
+    q, k, g, b, v, w = (P[n] for n in ("q", "k", "g", "b", "v", "w"))
+    S0 = torch.zeros((B, H, K, V), device=dev)
+    dO = torch.randn((B, H, T, V), generator=gen, device=dev)
+    grads = [torch.empty_like(t) for t in (q, k, g, b, v, w)] + [torch.empty_like(S0)]
+    fwd = chunk_args(q, k, v, g, b, w, S0, dO, K ** -0.5, 64)
+    a = CA.ChunkBwdArgs(fwd, _p(dO), None, *(_p(t) for t in grads), None, 0)
+    L = CA.lib()
+    need = int(L.gdn2_chunk_bwd_workspace_bytes(ctypes.byref(a)))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    a.workspace, a.workspace_bytes = _p(ws), need
+    stream = _stream()
+    for _ in range(args.warmup):
+        CA.check(L.gdn2_chunk_bwd_f32(ctypes.byref(a), stream))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        L.gdn2_chunk_bwd_f32(ctypes.byref(a), stream)
+    e1.record()
+    torch.cuda.synchronize()
+    CA.check(L.gdn2_chunk_bwd_f32(ctypes.byref(a), stream))
+    ms = e0.elapsed_time(e1) / args.steps
+    res = {"workload": f"chunked backward (gradients of q, k, g, b, v, w, S0), B={B} T={T} H=16 K=V=128",
+           "ms_per_step": ms, "tokens_per_s": B * T / (ms / 1e3), "workspace_bytes": need,
+           "kernel": "gdn2_chunk_bwd_f32"}
+    del P, q, k, g, b, v, w, S0, dO, grads, ws
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     args = parse()
     if args.stats_summary:
@@ -379,6 +428,7 @@ def main():
         raise SystemExit("no gfx950 device: bench.py needs an MI355X")
     pre = bench_prefill(torch, G, args, dev)
     dec = None if args.no_decode else bench_decode(torch, G, args, dev)
+    bwd = None if args.no_backward else bench_backward(torch, G, args, dev)
     cpu = None if args.no_cpu else cpu_baseline(pre, args)
     if args.copy_calibration:
         src = torch.empty(COPY_BYTES // 4, device=dev)
@@ -409,6 +459,7 @@ def main():
         "decode": dec,
         "decode_tokens_per_s": None if dec is None else dec["tokens_per_s"],
         "layer": {"prefill": pre["layer"], "decode": None if dec is None else dec.get("layer")},
+        "backward": bwd,
     }
     print(json.dumps(line), flush=True)
 
