@@ -288,8 +288,10 @@ def _cpu_model():
 
 
 COPY_BYTES = 1 << 30
-KERNELS = {"chunk_intra": "chunk_intra_kernel", "chunk_inter": "chunk_inter_kernel",
-           "decode": "decode_fused_kernel"}
+# the inference instances at the benchmarked shape (the backward's training
+# variants, chunk_intra_kernel<..., true> and chunk_inter_kernel<128, 2>, are others)
+KERNELS = {"chunk_intra": "chunk_intra_kernel<128, 128, false>", "chunk_inter": "chunk_inter_kernel<128, 0>",
+           "decode": "decode_fused_kernel<128, 128>"}
 
 
 def _short(name):
