@@ -46,7 +46,8 @@ constexpr float kSafeSpan = 96.0f; // log2 units
 // that a workgroup pays a handful of memory round trips instead of one per
 // loop iteration.
 // ---------------------------------------------------------------------------
-// TRAIN adds the backward's operands (ws_wt, ws_qgt, ws_kd, ws_aqkt, ws_akk).
+// TRAIN adds the backward's operands (ws_wt, ws_qgt, ws_kd, ws_aqkt, and
+// (I + A_kk)^-1 in ws_akk).
 template <int K, int V, bool TRAIN>
 __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
     constexpr int NW = 8; // waves per workgroup; two workgroups per CU = four waves per SIMD
@@ -374,12 +375,6 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
                     for (int i = 0; i < 4; ++i) val[i] = sAqk[16 * rt + 4 * lg + i][16 * st + lr];
                 st_stream(ATf + f * 64 + lane, val);
             }
-            // A_kk row-major, strictly lower (the upper blocks of sAkk are never written)
-            float *Akf = p.ws_akk + cid * (C * C);
-            for (int idx = tid; idx < C * C; idx += 512) {
-                const int r = idx / C, s = idx % C;
-                Akf[idx] = s < r ? sAkk[r][s] : 0.f;
-            }
         }
     }
 
@@ -453,6 +448,27 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
                               Xp);
             } else
                 st_stream(Uf + ((nt - NKT) * NT + tp) * 64 + lane, Xp);
+        }
+    }
+    if (TRAIN && wave < NT) {
+        // Ai = (I + A_kk)^-1 for the backward: the same blocked solve with the
+        // identity's column tile `wave` as right-hand side; tile (tp, it) stored in
+        // accumulator layout (lane (g, c) holds Ai[16 tp + 4 g + i][16 it + c]).
+        const int it = wave;
+        floatx4 *Aif = reinterpret_cast<floatx4 *>(p.ws_akk) + cid * (C * C / 4);
+        floatx4 Xi[NT];
+#pragma unroll
+        for (int tp = 0; tp < NT; ++tp) {
+            floatx4 R;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) R[i] = (tp == it && 4 * lg + i == lr) ? 1.f : 0.f;
+#pragma unroll
+            for (int q = 0; q < NT; ++q)
+                if (q < tp) R = mfma4n(*reinterpret_cast<const float4 *>(&sAkk[16 * tp + lr][16 * q + 4 * lg]), Xi[q], R);
+            Xi[tp] = tp < it ? floatx4{0.f, 0.f, 0.f, 0.f}
+                             : mfma4(*reinterpret_cast<const float4 *>(&sAinv[tp][lr][4 * lg]), R,
+                                     floatx4{0.f, 0.f, 0.f, 0.f});
+            st_stream(Aif + (tp * NT + it) * 64 + lane, Xi[tp]);
         }
     }
 }

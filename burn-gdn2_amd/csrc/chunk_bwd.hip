@@ -17,11 +17,11 @@
 // dq, dk, db and dG; dg is the reverse cumulative sum of dG over the chunk.
 //
 // Kernels (in launch order):
-//   chunk_intra_kernel<K, V, true>       the forward operands plus W^T, QG^T, Kd, A_qk^T, A_kk
+//   chunk_intra_kernel<K, V, true>       the forward operands plus W^T, QG^T, Kd, A_qk^T, (I + A_kk)^-1
 //   chunk_inter_kernel<K, kInterStates>  the state entering every chunk and v_new
 //   bwd_inter_kernel   the reverse recurrence (one workgroup per (b, hv, 64 columns))
 //   bwd_gemm_kernel    dQG, dW, dKd, dA_qk, dv_new U^T (MFMA) and dgam, per chunk
-//   bwd_solve_kernel   Ai, dRk, dRv -> dv, dw; dA_kk, per chunk
+//   bwd_solve_kernel   dRk, dRv -> dv, dw; dA_kk, per chunk
 //   bwd_decay_kernel   dq, dk, db, dg, per chunk
 //   bwd_gva_kernel     key-side gradients summed over the value heads of a key head
 #include "chunk_common.hpp"
@@ -365,25 +365,21 @@ __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(BwdParams bp) {
 }
 
 // ---------------------------------------------------------------------------
-// Per-chunk solve adjoint (four waves):
-//   Ai = (I + A_kk)^-1, blocked by 16-row tiles: the diagonal inverses by
-//     forward substitution, then Ai_pq = -D_p sum_{q<=m<p} A_kk,pm Ai_mq
+// Per-chunk solve adjoint (four waves), with Ai = (I + A_kk)^-1 from the
+// training forward (accumulator-layout tiles, i.e. the A fragments of Ai^T):
 //   [dRk | dRv] = Ai^T [dW | dv_new]   (MFMA; dv = dRv * w, dw = dRv * v)
 //   dA_kk = strict_tril(-(dRk W^T + Ai^T dUU))   (MFMA)
-// Ai^T A fragments come from LDS (lane (g, r): Ai[16 st + 4 g + j][16 rt + r]);
-// W's stored A fragments are the B fragments of W^T.
+// W's stored A fragments are the B fragments of W^T; dRk goes through LDS
+// (rows as A fragments) for the second product.
 // ---------------------------------------------------------------------------
 template <int K, int V>
-__global__ __launch_bounds__(256, 2) void bwd_solve_kernel(BwdParams bp) {
+__global__ __launch_bounds__(256) void bwd_solve_kernel(BwdParams bp) {
     const ChunkParams &p = bp.f;
+    constexpr int NW = 4;
     constexpr int NKT = K / 16, NVT = V / 16, NCT = NKT + NVT;
-    constexpr int CP = C + 4, KP = K + 4;
-    __shared__ __attribute__((aligned(16))) float sM[C][CP];  // A_kk
-    __shared__ float sAi[C][CP]; // (I + A_kk)^-1
-    __shared__ __attribute__((aligned(16))) float sU[C * KP];
-    float(*sX)[CP] = reinterpret_cast<float(*)[CP]>(sU); // off-diagonal block products (the inverse)
-    float(*sR)[KP] = reinterpret_cast<float(*)[KP]>(sU); // dRk (after the inverse)
-    static_assert(KP >= CP, "sX fits in sU");
+    constexpr int NLT = NT * (NT + 1) / 2; // lower tiles
+    constexpr int KP = K + 4;
+    __shared__ __attribute__((aligned(16))) float sR[C][KP]; // dRk
     const int cid = blockIdx.x, bh = cid / p.NC, n = cid % p.NC;
     const int bi = bh / p.HV, hv = bh % p.HV;
     const int cv = min(C, p.T - n * C);
@@ -391,122 +387,93 @@ __global__ __launch_bounds__(256, 2) void bwd_solve_kernel(BwdParams bp) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
 
-    {
-        const floatx4 *Akk = reinterpret_cast<const floatx4 *>(p.ws_akk + (size_t)cid * C * C);
-        floatx4 a[C * C / 4 / 256];
+    // Ai^T A fragments (rt, st), st >= rt: Ai's tile (st, rt)
+    const floatx4 *Aif = reinterpret_cast<const floatx4 *>(p.ws_akk) + (size_t)cid * (C * C / 4);
+    floatx4 ai[NLT];
 #pragma unroll
-        for (int i = 0; i < C * C / 4 / 256; ++i) a[i] = Akk[i * 256 + tid];
+    for (int rt = 0, f = 0; rt < NT; ++rt)
 #pragma unroll
-        for (int i = 0; i < C * C / 4 / 256; ++i) {
-            const int f = i * 256 + tid, r = f / (C / 4), c4 = f % (C / 4);
-            *reinterpret_cast<floatx4 *>(&sM[r][4 * c4]) = a[i];
-        }
-    }
-    __syncthreads();
-    if (wave == 0) { // diagonal inverses: lane = (tile, column)
-        const int pt = lane >> 4, j = lane & 15;
-        float x[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float v = (i == j) ? 1.f : 0.f;
-#pragma unroll
-            for (int m = 0; m < i; ++m) v -= sM[16 * pt + i][16 * pt + m] * x[m];
-            x[i] = v;
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sAi[16 * pt + i][16 * pt + j] = x[i];
-    } else { // zero the upper blocks
-        for (int idx = tid - 64; idx < C * C; idx += 192) {
-            const int r = idx / C, c = idx % C;
-            if ((c >> 4) > (r >> 4)) sAi[r][c] = 0.f;
-        }
-    }
-    __syncthreads();
-#pragma unroll 1
-    for (int d = 1; d < NT; ++d) { // block diagonal d: Ai_{q+d, q}
-        const int nb = NT - d;
-        // X = sum_{m=q}^{q+d-1} A_kk[q+d][m] Ai[m][q] (16 x 16 per block)
-        for (int e = tid; e < nb * 256; e += 256) {
-            const int q = e >> 8, r = (e >> 4) & 15, c = e & 15, pb = q + d;
-            float acc = 0.f;
-            for (int m = 16 * q; m < 16 * pb; ++m) acc += sM[16 * pb + r][m] * sAi[m][16 * q + c];
-            sX[16 * pb + r][16 * q + c] = acc;
-        }
-        __syncthreads();
-        for (int e = tid; e < nb * 256; e += 256) {
-            const int q = e >> 8, r = (e >> 4) & 15, c = e & 15, pb = q + d;
-            float acc = 0.f;
-#pragma unroll
-            for (int m = 0; m < 16; ++m) acc += sAi[16 * pb + r][16 * pb + m] * sX[16 * pb + m][16 * q + c];
-            sAi[16 * pb + r][16 * q + c] = -acc;
-        }
-        __syncthreads();
-    }
+        for (int st = rt; st < NT; ++st, ++f) ai[f] = Aif[(st * NT + rt) * 64 + lane];
+    auto aiT = [&](int rt, int st) -> floatx4 { // index of (rt, st) in the list above
+        return ai[rt * NT - rt * (rt - 1) / 2 + (st - rt)];
+    };
 
-    // [dRk | dRv] = Ai^T [dW | dv_new]: wave w takes column tiles w, w + 4, ...
-    // (B fragments: the accumulator-layout tiles of dW and dv_new)
     const floatx4 *dWf = reinterpret_cast<const floatx4 *>(bp.ws_dwm) + (size_t)cid * (C * K / 4);
     const floatx4 *dVf = reinterpret_cast<const floatx4 *>(bp.ws_dvnf) + (size_t)cid * (C * V / 4);
     floatx4 *drk = reinterpret_cast<floatx4 *>(bp.ws_drk) + (size_t)cid * (C * K / 4);
     const int64_t vo = (int64_t)bi * p.svb + (int64_t)hv * p.svh + (int64_t)(n * C) * p.svt;
+    const int rv = (int)p.svt;
+    const __amdgpu_buffer_rsrc_t Rv = rows_rsrc(p.v + vo, rv, cv, V), Rw = rows_rsrc(p.w + vo, rv, cv, V);
 #pragma unroll 1
-    for (int ct = wave; ct < NCT; ct += 4) {
+    for (int ct = wave; ct < NCT; ct += NW) {
         const bool kcol = ct < NKT;
-        floatx4 xb[NT]; // B fragments: X[16 st + 4 g + j][column lr]
+        floatx4 xb[NT]; // B fragments X[16 st + 4 g + j][column lr]
 #pragma unroll
         for (int st = 0; st < NT; ++st)
             xb[st] = kcol ? dWf[(st * NKT + ct) * 64 + lane] : dVf[(st * NVT + ct - NKT) * 64 + lane];
+        float vv[NT][4], ww[NT][4];
+        if (!kcol) {
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int o = (16 * rt + 4 * lg + i) * rv + 16 * (ct - NKT) + lr;
+                    vv[rt][i] = bld1(Rv, o);
+                    ww[rt][i] = bld1(Rw, o);
+                }
+        }
 #pragma unroll
         for (int rt = 0; rt < NT; ++rt) {
             floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int st = rt; st < NT; ++st) {
-                floatx4 a;
+            for (int st = rt; st < NT; ++st) acc = mfma4x(aiT(rt, st), xb[st], acc);
+            if (kcol) {
+                drk[(rt * NKT + ct) * 64 + lane] = acc;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) a[j] = sAi[16 * st + 4 * lg + j][16 * rt + lr];
-                acc = mfma4x(a, xb[st], acc);
-            }
-            if (kcol) drk[(rt * NKT + ct) * 64 + lane] = acc;
+                for (int i = 0; i < 4; ++i) sR[16 * rt + 4 * lg + i][16 * ct + lr] = acc[i];
+            } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 16 * rt + 4 * lg + i;
-                if (kcol) {
-                    sR[r][16 * ct + lr] = acc[i];
-                } else if (r < cv) {
-                    const int64_t o = vo + (int64_t)r * p.svt + 16 * (ct - NKT) + lr;
-                    bp.dv[o] = acc[i] * p.w[o];
-                    bp.dw[o] = acc[i] * p.v[o];
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 16 * rt + 4 * lg + i;
+                    if (r < cv) {
+                        const int64_t o = vo + (int64_t)r * p.svt + 16 * (ct - NKT) + lr;
+                        bp.dv[o] = acc[i] * ww[rt][i];
+                        bp.dw[o] = acc[i] * vv[rt][i];
+                    }
                 }
             }
         }
     }
     __syncthreads();
 
-    // dA_kk tiles (rt, st), st <= rt: -(dRk W^T + Ai^T dUU), strictly lower
+    // dA_kk tiles (rt, st): -(dRk W^T + Ai^T dUU) on the lower tiles, zero above
     const floatx4 *Wf = reinterpret_cast<const floatx4 *>(p.ws_w) + (size_t)cid * (C * K / 4);
     const floatx4 *duu = reinterpret_cast<const floatx4 *>(bp.ws_duu) + (size_t)cid * (C * C / 4);
     float *dakk = bp.ws_dakk + (size_t)cid * C * C;
 #pragma unroll 1
-    for (int tt = wave; tt < NT * NT; tt += 4) {
-        const int rt = tt / NT, st = tt % NT;
+    for (int tl = wave; tl < NT * NT; tl += NW) {
+        const int rt = tl / NT, st = tl % NT;
         floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
         if (st <= rt) {
+            floatx4 wb[NKT], ub[NT], ab[NT];
+#pragma unroll
+            for (int kt = 0; kt < NKT; ++kt) wb[kt] = Wf[(st * NKT + kt) * 64 + lane];
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt) {
+                ub[mt] = mt >= rt ? duu[(mt * NT + st) * 64 + lane] : floatx4{0.f, 0.f, 0.f, 0.f};
+                ab[mt] = mt >= rt ? Aif[(mt * NT + rt) * 64 + lane] : floatx4{0.f, 0.f, 0.f, 0.f}; // Ai^T (rt, mt)
+            }
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt) // A: dRk rows 16 rt + lr; B: W^T = W's A fragment (st, kt)
-                acc = mfma4x(*reinterpret_cast<const floatx4 *>(&sR[16 * rt + lr][16 * kt + 4 * lg]),
-                             Wf[(st * NKT + kt) * 64 + lane], acc);
+                acc = mfma4x(*reinterpret_cast<const floatx4 *>(&sR[16 * rt + lr][16 * kt + 4 * lg]), wb[kt], acc);
 #pragma unroll
-            for (int mt = rt; mt < NT; ++mt) { // A: Ai^T; B: dUU's tile (mt, st)
-                floatx4 a;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) a[j] = sAi[16 * mt + 4 * lg + j][16 * rt + lr];
-                acc = mfma4x(a, duu[(mt * NT + st) * 64 + lane], acc);
-            }
+            for (int mt = 0; mt < NT; ++mt)
+                if (mt >= rt) acc = mfma4x(ab[mt], ub[mt], acc);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int r = 16 * rt + 4 * lg + i, s = 16 * st + lr;
-            dakk[r * C + s] = s < r ? -acc[i] : 0.f;
+            const int r = 16 * rt + 4 * lg + i, s2 = 16 * st + lr;
+            dakk[r * C + s2] = s2 < r ? -acc[i] : 0.f;
         }
     }
 }

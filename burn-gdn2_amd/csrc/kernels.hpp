@@ -68,7 +68,7 @@ struct ChunkParams {
     float *ws_qgt;  // C*K  (scale q exp(G))^T, same order
     float *ws_kd;   // C*K  Kd as A-operand tiles (time tile, key tile)
     float *ws_aqkt; // C*C  A_qk^T as A-operand tiles (column tile, row tile)
-    float *ws_akk;  // C*C  A_kk row-major (strictly lower, zero elsewhere)
+    float *ws_akk;  // C*C  (I + A_kk)^-1, accumulator-layout tiles (row tile, column tile)
     float *ws_sn;   // K*V  state entering each chunk (row-major)
     float *ws_vn;   // C*V  v_new of each chunk (row-major)
 };
