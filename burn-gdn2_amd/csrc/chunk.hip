@@ -207,7 +207,7 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
                 // scale q exp(G_r): the sequential kernel's A operand, fragment (pt, m0 + m)
                 if (mat == 0) {
                     const floatx4 qg = a * exp2v(gb) * p.scale;
-                    st_stream(QGf + (pt * NKT + m0 + m) * 64 + lane, qg);
+                    if (!TRAIN) st_stream(QGf + (pt * NKT + m0 + m) * 64 + lane, qg); // the backward takes QG^T only
                     if (TRAIN) // (q exp(G))^T fragment (m0 + m, pt)
                         st_stream(reinterpret_cast<floatx4 *>(p.ws_qgt) + cid * (C * K / 4) +
                                       ((m0 + m) * NT + pt) * 64 + lane,
@@ -353,11 +353,12 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
     }
     __syncthreads();
 
-    // A_qk -> the sequential kernel as A-operand fragments (mt, qt), zero above the diagonal.
+    // A_qk -> the sequential kernel as A-operand fragments (mt, qt), zero above the
+    // diagonal (the backward takes A_qk^T only).
     {
         floatx4 *Af = reinterpret_cast<floatx4 *>(p.ws_aqk) + cid * (C * C / 4);
 #pragma unroll
-        for (int j = 0; j < NT * NT / NW; ++j) {
+        for (int j = 0; j < (TRAIN ? 0 : NT * NT / NW); ++j) {
             const int f = wave + NW * j, mt = f / NT, qt = f % NT;
             floatx4 val = *reinterpret_cast<const floatx4 *>(&sAqk[16 * mt + lr][16 * qt + 4 * lg]);
             if (qt > mt) val = floatx4{0.f, 0.f, 0.f, 0.f};
