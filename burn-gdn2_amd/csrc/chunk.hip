@@ -928,6 +928,8 @@ gdn2_status chunk_setup(const gdn2_chunk_args *a, const char *who, bool need_out
 
 size_t chunk_fwd_ws_bytes(const gdn2_chunk_args *a) { return ws_layout(a).total; }
 
+int chunk_segments(int64_t seqs, int64_t V, int64_t NC) { return inter_segments(seqs, 1, V, NC).nseg; }
+
 void chunk_bind_ws(const gdn2_chunk_args *a, char *ws, ChunkParams *p) {
     const WsLayout L = ws_layout(a);
     p->ws_w = reinterpret_cast<float *>(ws + L.w);

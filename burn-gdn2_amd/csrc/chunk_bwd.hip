@@ -50,6 +50,10 @@ struct BwdParams {
     float *ws_drk;                    // C*K  dL/dRk, fragments
     float *ws_dakk;                   // C*C  dL/dA_kk (strictly lower), row-major
     float *ws_kgrad;                  // rep > 1: 4 x (C*K per chunk): dq, dk, dg, db per value head
+    // segmented reverse recurrence (NSEG > 1), per (b, hv):
+    float *ws_ptseg;                  // NSEG x K*K  P_j^T of segments 1 .. NSEG-1 (row-major)
+    float *ws_rseg;                   // NSEG x K*V  the gradient leaving each segment (slot j - 1
+                                      //             first holds R_j of segment j)
 };
 
 __device__ __forceinline__ floatx4 mfma4x(floatx4 a, floatx4 b, floatx4 c) {
@@ -63,17 +67,30 @@ __device__ __forceinline__ floatx4 mfma4x(floatx4 a, floatx4 b, floatx4 c) {
 // ---------------------------------------------------------------------------
 // Reverse recurrence.  One workgroup per (b, hv, 64 value columns), wave w
 // owns 16 columns; dS' stays in MFMA accumulators (key rows x 16 columns).
-// Per chunk n = NC-1 .. 0:
+// Per chunk n, last to first:
 //   1: dv_new = A_qk^T dO + Kd dS'         (reads sAT, sKd)
 //      dS' and dv_new go to the workspace for the per-chunk kernels
 //   2: dS' <- e^{G_last} dS' + QG^T dO - W^T dv_new   (reads sQT, sWT, sGam)
 // The operands are A-operand fragments written by the training forward, so
 // every product has the shape of the forward's chunk-inter products.  As
 // there, each LDS buffer is refilled while the other phase runs.
+//
+// Segmented form (NSEG > 1), the mirror of the forward's: over a segment the
+// map from the gradient leaving it to the gradient entering it is affine,
+//   dS_in = P^T dS_out + R,
+// with P the segment's forward transition and R the segment run from
+// dS' = 0; P^T is the same recurrence run on the K columns of an identity
+// with dO = 0.  Pass 1 (kRevLocal) computes R and P^T of every segment but
+// the first, bwd_chain_kernel chains the segments from the last, and pass 3
+// (kRevOut) re-runs every segment from its gradient with the stores; the
+// first segment writes dS0.
 // ---------------------------------------------------------------------------
-template <int K>
-__global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp) {
+constexpr int kRevOut = 0, kRevLocal = 1;
+
+template <int K, int MODE>
+__global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg0, int nseg_launch) {
     const ChunkParams &p = bp.f;
+    constexpr bool LOCAL = MODE == kRevLocal;
     constexpr int NKT = K / 16;
     constexpr int OPF4 = NKT * NT * 64, PFO = OPF4 / 256;
     constexpr int AF4 = NT * NT * 64, APF = AF4 / 256;
@@ -81,21 +98,31 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp) {
     __shared__ floatx4 sGam[K / 4];
 
     const int V = p.V, nvv = V / 64;
-    int bh, vs;
-    inter_block(blockIdx.x, p.B * p.HV, nvv, &bh, &vs);
+    const int nvs = LOCAL ? nvv + K / 64 : nvv; // pass 1 adds the slices of P^T
+    int sq, vs;
+    inter_block(blockIdx.x, p.B * p.HV * nseg_launch, nvs, &sq, &vs);
+    const int bh = sq / nseg_launch, seg = seg0 + sq % nseg_launch;
     const int bi = bh / p.HV, hv = bh % p.HV;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
-    const int col = 16 * (vs * 4 + wave) + lr;
+    const bool pcol = LOCAL && vs >= nvv; // a slice of P^T (wave-uniform): no d_out
+    const int col = 16 * ((pcol ? vs - nvv : vs) * 4 + wave) + lr;
+    const int n0 = seg * p.SEGL, n1 = min(p.NC, n0 + p.SEGL);
 
+    // the gradient leaving the segment: d_state_out (one segment), the chained
+    // gradient (pass 3), 0 (pass 1 value columns) or the identity (pass 1, P^T)
     floatx4 dS[NKT];
+    const float *din = nullptr;
+    if (!LOCAL) din = p.NSEG == 1 ? bp.d_state_out : bp.ws_rseg + ((size_t)bh * p.NSEG + seg) * K * V;
 #pragma unroll
     for (int kb = 0; kb < NKT; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            dS[kb][i] = bp.d_state_out ? bp.d_state_out[(size_t)bh * K * V + (size_t)(16 * kb + 4 * lg + i) * V + col]
-                                       : 0.f;
+        for (int i = 0; i < 4; ++i) {
+            const int row = 16 * kb + 4 * lg + i;
+            dS[kb][i] = LOCAL ? (pcol && row == col ? 1.f : 0.f)
+                              : (din ? din[(p.NSEG == 1 ? (size_t)bh * K * V : 0) + (size_t)row * V + col] : 0.f);
+        }
 
     const floatx4 *__restrict__ KD4 = reinterpret_cast<const floatx4 *>(p.ws_kd);
     const floatx4 *__restrict__ AT4 = reinterpret_cast<const floatx4 *>(p.ws_aqkt);
@@ -104,8 +131,8 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp) {
     const floatx4 *__restrict__ G4 = reinterpret_cast<const floatx4 *>(p.ws_gam);
     const size_t cid0 = (size_t)bh * p.NC;
 
-    if (p.NC > 0) {
-        const size_t cl = cid0 + p.NC - 1;
+    if (n1 > n0) {
+        const size_t cl = cid0 + n1 - 1;
 #pragma unroll
         for (int i = 0; i < PFO; ++i) sKd[i * 256 + tid] = KD4[cl * OPF4 + i * 256 + tid];
 #pragma unroll
@@ -114,7 +141,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp) {
     // row 4 lg of each 16-row tile of d_out; the rest of the row offset is wave-uniform
     const float *dob = bp.d_out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + col + (int64_t)(4 * lg) * p.sot;
 
-    for (int n = p.NC - 1; n >= 0; --n) {
+    for (int n = n1 - 1; n >= n0; --n) {
         const size_t cid = cid0 + n;
         __syncthreads(); // sKd, sAT hold chunk n; every wave is done with sQT, sWT (n+1)
         floatx4 qpre[PFO], wpre[PFO], g_cur = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -130,7 +157,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp) {
         for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                dO[mt][i] = (16 * mt + 4 * lg + i < cv) ? dob[(int64_t)(n * C + 16 * mt + i) * p.sot] : 0.f;
+                dO[mt][i] = (!pcol && 16 * mt + 4 * lg + i < cv) ? dob[(int64_t)(n * C + 16 * mt + i) * p.sot] : 0.f;
 
         // 1: dv_new = Kd dS' + A_qk^T dO (A_qk^T is upper block-triangular)
         floatx4 dvn[NT];
@@ -146,12 +173,14 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp) {
 #pragma unroll
                 for (int st = 0; st < NT; ++st) dvn[st] = mfma16(ka[st][j], dS[kb][j], dvn[st]);
         }
+        if (!pcol) {
 #pragma unroll
-        for (int st = 0; st < NT; ++st)
+            for (int st = 0; st < NT; ++st)
 #pragma unroll
-            for (int rt = st; rt < NT; ++rt) dvn[st] = mfma4x(sAT[(st * NT + rt) * 64 + lane], dO[rt], dvn[st]);
+                for (int rt = st; rt < NT; ++rt) dvn[st] = mfma4x(sAT[(st * NT + rt) * 64 + lane], dO[rt], dvn[st]);
+        }
 
-        {
+        if (!LOCAL) {
             float *Dsn = bp.ws_dsn + cid * K * V;
 #pragma unroll
             for (int kb = 0; kb < NKT; ++kb)
@@ -175,8 +204,8 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp) {
         if (tid < K / 4) sGam[tid] = g_cur;
         __syncthreads(); // phase 1 done everywhere (sKd, sAT free); sQT, sWT, sGam (n) visible
 
-        // Kd, A_qk^T of chunk n-1 (the first chunk re-fetches itself)
-        const size_t cpv = cid - (n > 0 ? 1 : 0);
+        // Kd, A_qk^T of chunk n-1 (the segment's first chunk re-fetches itself)
+        const size_t cpv = cid - (n > n0 ? 1 : 0);
         floatx4 kpre[PFO], apre[APF];
 #pragma unroll
         for (int i = 0; i < PFO; ++i) kpre[i] = KD4[cpv * OPF4 + i * 256 + tid];
@@ -204,7 +233,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp) {
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int kb = 0; kb < NKT; ++kb) {
-                    dS[kb] = mfma16(qa[kb][j], dO[tt][j], dS[kb]);
+                    dS[kb] = mfma16(qa[kb][j], dO[tt][j], dS[kb]); // dO = 0 for P^T columns
                     dS[kb] = mfma16(-wa[kb][j], dvn[tt][j], dS[kb]);
                 }
         }
@@ -213,10 +242,77 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp) {
 #pragma unroll
         for (int i = 0; i < APF; ++i) sAT[i * 256 + tid] = apre[i];
     }
+    // the gradient entering the segment: dS0 (first segment), R_j or P_j^T (pass 1)
+    float *out = nullptr;
+    int ld = V;
+    if (!LOCAL) {
+        if (seg == 0) out = bp.d_state0 + (size_t)bh * K * V;
+    } else if (pcol) {
+        out = bp.ws_ptseg + ((size_t)bh * p.NSEG + seg) * K * K;
+        ld = K;
+    } else {
+        out = bp.ws_rseg + ((size_t)bh * p.NSEG + seg - 1) * K * V;
+    }
+    if (out) {
+#pragma unroll
+        for (int kb = 0; kb < NKT; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) out[(size_t)(16 * kb + 4 * lg + i) * ld + col] = dS[kb][i];
+    }
+}
+
+// Pass 2 of the segmented reverse recurrence.  ws_rseg holds NSEG slots of
+// K x V per (b, hv): slot NSEG-1 <- d_state_out (or 0), then slot j - 1 (R_j
+// from pass 1) <- P_j^T slot j + R_j for j = NSEG-1 .. 1: the gradient leaving
+// every segment.  Same MFMA layout as the forward's chunk_chain_kernel.
+template <int K>
+__global__ __launch_bounds__(256, 1) void bwd_chain_kernel(BwdParams bp) {
+    const ChunkParams &p = bp.f;
+    constexpr int NKT = K / 16;
+    const int V = p.V, nvv = V / 64;
+    int bh, vs;
+    inter_block(blockIdx.x, p.B * p.HV, nvv, &bh, &vs);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
+    const int col = 16 * (vs * 4 + wave) + lr;
+    float *slot0 = bp.ws_rseg + (size_t)bh * p.NSEG * K * V;
+    float *last = slot0 + (size_t)(p.NSEG - 1) * K * V;
+    floatx4 S[NKT];
 #pragma unroll
     for (int kb = 0; kb < NKT; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) bp.d_state0[(size_t)bh * K * V + (size_t)(16 * kb + 4 * lg + i) * V + col] = dS[kb][i];
+        for (int i = 0; i < 4; ++i) {
+            const size_t o = (size_t)(16 * kb + 4 * lg + i) * V + col;
+            S[kb][i] = bp.d_state_out ? bp.d_state_out[(size_t)bh * K * V + o] : 0.f;
+            last[o] = S[kb][i];
+        }
+    for (int j = p.NSEG - 1; j >= 1; --j) {
+        const float *P = bp.ws_ptseg + ((size_t)bh * p.NSEG + j) * K * K; // P_j^T, row-major
+        float *Q = slot0 + (size_t)(j - 1) * K * V;
+        floatx4 N[NKT];
+#pragma unroll
+        for (int it = 0; it < NKT; ++it)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) N[it][i] = Q[(size_t)(16 * it + 4 * lg + i) * V + col];
+#pragma unroll
+        for (int kb = 0; kb < NKT; ++kb) {
+            floatx4 pa[NKT];
+#pragma unroll
+            for (int it = 0; it < NKT; ++it)
+                pa[it] = *reinterpret_cast<const floatx4 *>(P + (size_t)(16 * it + lr) * K + 16 * kb + 4 * lg);
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int it = 0; it < NKT; ++it) N[it] = mfma16(pa[it][st], S[kb][st], N[it]);
+        }
+#pragma unroll
+        for (int it = 0; it < NKT; ++it) {
+            S[it] = N[it];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Q[(size_t)(16 * it + 4 * lg + i) * V + col] = N[it][i];
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -728,9 +824,17 @@ template <int K, int V>
 hipError_t launch_bwd_t(const BwdParams &bp, hipStream_t s) {
     const ChunkParams &p = bp.f;
     const int seqs = p.B * p.HV, nch = seqs * p.NC;
-    hipLaunchKernelGGL((bwd_inter_kernel<K>), dim3(seqs * (V / 64)), dim3(256), 0, s, bp);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    hipError_t e;
+    if (p.NSEG > 1) {
+        hipLaunchKernelGGL((bwd_inter_kernel<K, kRevLocal>), dim3(seqs * (p.NSEG - 1) * ((V + K) / 64)), dim3(256), 0,
+                           s, bp, 1, p.NSEG - 1);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        hipLaunchKernelGGL((bwd_chain_kernel<K>), dim3(seqs * (V / 64)), dim3(256), 0, s, bp);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((bwd_inter_kernel<K, kRevOut>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0, s, bp, 0,
+                       p.NSEG);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_gemm_kernel<K, V>), dim3(nch), dim3(256), 0, s, bp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_solve_kernel<K, V>), dim3(nch), dim3(256), 0, s, bp);
@@ -762,7 +866,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // The backward's workspace after the forward's: the training operands of the
 // forward, then the backward's per-chunk arrays.
 struct BwdLayout {
-    size_t fwd, wt, qgt, kd, aqkt, akk, sn, vn, dsn, dvn, dvnf, dqg, dwm, dkd, daqk, duu, dgam, drk, dakk, kgrad, total;
+    size_t fwd, wt, qgt, kd, aqkt, akk, sn, vn, dsn, dvn, dvnf, dqg, ptseg, rseg, dwm, dkd, daqk, duu, dgam, drk, dakk, kgrad, total;
 };
 
 BwdLayout bwd_layout(const gdn2_chunk_args *a) {
@@ -791,6 +895,13 @@ BwdLayout bwd_layout(const gdn2_chunk_args *a) {
     L.drk = take(Cs * K);
     L.dakk = take(Cs * Cs);
     L.kgrad = take(a->num_v_heads != a->num_heads ? 4 * Cs * K : 0);
+    { // segment buffers of the reverse recurrence, per sequence (not per chunk)
+        const size_t seqs = (size_t)a->batch * a->num_v_heads, NC = (a->seq_len + kChunk - 1) / kChunk;
+        const size_t nseg = (size_t)chunk_segments(seqs, V, NC);
+        const size_t ns = nseg > 1 ? seqs * nseg : 0;
+        L.ptseg = off; off = align256(off + f * ns * K * K);
+        L.rseg = off; off = align256(off + f * ns * K * V);
+    }
     L.total = off;
     return L;
 }
@@ -859,6 +970,8 @@ extern "C" gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *a, gdn2_str
     bp.ws_drk = reinterpret_cast<float *>(ws + L.drk);
     bp.ws_dakk = reinterpret_cast<float *>(ws + L.dakk);
     bp.ws_kgrad = p.rep > 1 ? reinterpret_cast<float *>(ws + L.kgrad) : nullptr;
+    bp.ws_ptseg = reinterpret_cast<float *>(ws + L.ptseg);
+    bp.ws_rseg = reinterpret_cast<float *>(ws + L.rseg);
     // forward: per-chunk operands (training outputs), then the state entering every chunk
     GDN2_HIP_CHECK(launch_chunk(p, s, 1 | 4));
     GDN2_HIP_CHECK(launch_bwd(bp, s));

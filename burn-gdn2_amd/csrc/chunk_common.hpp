@@ -86,6 +86,8 @@ __device__ __forceinline__ void inter_block(int blk, int nseq, int nvs, int *bh,
 // Host side of the chunked forward, shared with the backward (chunk.hip).
 gdn2_status chunk_setup(const gdn2_chunk_args *a, const char *who, bool need_out, ChunkParams *p);
 size_t chunk_fwd_ws_bytes(const gdn2_chunk_args *a);
+// Segments per sequence of the sequential kernels (1 = unsegmented).
+int chunk_segments(int64_t seqs, int64_t V, int64_t NC);
 void chunk_bind_ws(const gdn2_chunk_args *a, char *ws, ChunkParams *p);
 
 }  // namespace gdn2

@@ -43,12 +43,16 @@ CASES = [
     (1, 2, 2, 200, 128, 128, (-5.0, -0.5), 1.0, 0.5, True),     # strong decay
     (1, 1, 1, 1, 128, 128, (-0.3, -0.02), 1.0, 1.0, True),      # T = 1
     (1, 1, 2, 63, 64, 128, (-1.0, -0.1), 2.0, 0.3, True),
-    (1, 2, 2, 2100, 128, 128, (-0.003, -0.0005), 1.0, 1.0, True),  # slow decay; segmented forward states
+    (1, 2, 2, 2100, 128, 128, (-0.003, -0.0005), 1.0, 1.0, True),  # slow decay; two segments
+    (1, 2, 2, 2560, 128, 128, (-0.001, 0.0), 0.0, 1.0, True),       # b = 0: S0 and d_state carried through
+    (1, 1, 2, 6400, 64, 128, (-0.002, 0.0), 2.0, 1.0, True),        # six segments, GVA, negative eigenvalues
 ]
 
 
 @pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}g{c[6][0]}" for c in CASES])
 def test_chunk_bwd_matches_adjoint(gpu, case):
+    """Sequences of 2048+ tokens at one or two sequences x heads run the
+    segmented forward and reverse recurrences (per-segment transitions)."""
     import torch
 
     import gdn2_amd
