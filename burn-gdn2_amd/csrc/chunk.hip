@@ -495,7 +495,8 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
 // the K columns of an identity with U = 0.  So:
 //   pass 1 (OUT = false): every segment but the last, from S = 0 on the V
 //     value columns and from S = I, U = 0 on K extra columns; no output;
-//     the results go to ws_qseg / ws_pseg;
+//     the results go to ws_qseg / ws_pseg (the training forward also runs the
+//     last segment, for its P only);
 //   pass 2 (chunk_chain_kernel): S_in(j + 1) = P_j S_in(j) + Q_j, in order;
 //   pass 3 (OUT = true): every segment from its S_in, with the output; the
 //     last segment writes the final state.
@@ -700,9 +701,9 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     if (OUT) {
         if (seg == p.NSEG - 1) Sout = p.state + (size_t)bh * K * V;
     } else if (LOCAL && pcol) {
-        Sout = p.ws_pseg + ((size_t)bh * (p.NSEG - 1) + seg) * K * K;
+        Sout = p.ws_pseg + ((size_t)bh * p.NSEG + seg) * K * K;
         ld = K;
-    } else if (LOCAL) {
+    } else if (LOCAL && seg + 1 < p.NSEG) { // (the last segment runs for its P only: training)
         Sout = p.ws_qseg + ((size_t)bh * p.NSEG + seg + 1) * K * V;
     }
     if (Sout) {
@@ -741,7 +742,7 @@ __global__ __launch_bounds__(256, 1) void chunk_chain_kernel(ChunkParams p) {
             slot0[o] = S[kb][i];
         }
     for (int j = 0; j + 1 < p.NSEG; ++j) {
-        const float *P = p.ws_pseg + ((size_t)bh * (p.NSEG - 1) + j) * K * K;
+        const float *P = p.ws_pseg + ((size_t)bh * p.NSEG + j) * K * K;
         float *Q = slot0 + (size_t)(j + 1) * K * V;
         floatx4 N[NKT];
 #pragma unroll
@@ -782,8 +783,11 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
     if (phases & 6) {
         const int seqs = p.B * p.HV;
         if (p.NSEG > 1) {
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal>), dim3(seqs * (p.NSEG - 1) * ((V + K) / 64)),
-                               dim3(256), 0, s, p, p.NSEG - 1);
+            // the training forward (phases & 4) also takes the last segment's P, which
+            // the backward's reverse chain uses
+            const int nl = (phases & 4) ? p.NSEG : p.NSEG - 1;
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal>), dim3(seqs * nl * ((V + K) / 64)), dim3(256), 0,
+                               s, p, nl);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL((chunk_chain_kernel<K>), dim3(seqs * (V / 64)), dim3(256), 0, s, p);
@@ -853,7 +857,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 WsLayout ws_layout(int64_t seqs, int64_t NC, int64_t K, int64_t V) {
     const int64_t nchunks = seqs * NC;
     const int64_t nseg = inter_segments(seqs, 1, V, NC).nseg;
-    const int64_t np = nseg > 1 ? seqs * (nseg - 1) : 0, nq = nseg > 1 ? seqs * nseg : 0;
+    const int64_t np = nseg > 1 ? seqs * nseg : 0, nq = np;
     WsLayout L;
     size_t off = 0;
     L.w = off; off = align256(off + sizeof(float) * nchunks * kChunk * K);

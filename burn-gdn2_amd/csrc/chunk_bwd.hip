@@ -51,7 +51,6 @@ struct BwdParams {
     float *ws_dakk;                   // C*C  dL/dA_kk (strictly lower), row-major
     float *ws_kgrad;                  // rep > 1: 4 x (C*K per chunk): dq, dk, dg, db per value head
     // segmented reverse recurrence (NSEG > 1), per (b, hv):
-    float *ws_ptseg;                  // NSEG x K*K  P_j^T of segments 1 .. NSEG-1 (row-major)
     float *ws_rseg;                   // NSEG x K*V  the gradient leaving each segment (slot j - 1
                                       //             first holds R_j of segment j)
 };
@@ -78,12 +77,11 @@ __device__ __forceinline__ floatx4 mfma4x(floatx4 a, floatx4 b, floatx4 c) {
 // Segmented form (NSEG > 1), the mirror of the forward's: over a segment the
 // map from the gradient leaving it to the gradient entering it is affine,
 //   dS_in = P^T dS_out + R,
-// with P the segment's forward transition and R the segment run from
-// dS' = 0; P^T is the same recurrence run on the K columns of an identity
-// with dO = 0.  Pass 1 (kRevLocal) computes R and P^T of every segment but
-// the first, bwd_chain_kernel chains the segments from the last, and pass 3
-// (kRevOut) re-runs every segment from its gradient with the stores; the
-// first segment writes dS0.
+// with P the segment's forward transition (from the training forward's
+// segment pass) and R the segment run from dS' = 0.  Pass 1 (kRevLocal)
+// computes R of every segment but the first, bwd_chain_kernel chains the
+// segments from the last, and pass 3 (kRevOut) re-runs every segment from
+// its gradient with the stores; the first segment writes dS0.
 // ---------------------------------------------------------------------------
 constexpr int kRevOut = 0, kRevLocal = 1;
 
@@ -98,20 +96,18 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
     __shared__ floatx4 sGam[K / 4];
 
     const int V = p.V, nvv = V / 64;
-    const int nvs = LOCAL ? nvv + K / 64 : nvv; // pass 1 adds the slices of P^T
     int sq, vs;
-    inter_block(blockIdx.x, p.B * p.HV * nseg_launch, nvs, &sq, &vs);
+    inter_block(blockIdx.x, p.B * p.HV * nseg_launch, nvv, &sq, &vs);
     const int bh = sq / nseg_launch, seg = seg0 + sq % nseg_launch;
     const int bi = bh / p.HV, hv = bh % p.HV;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
-    const bool pcol = LOCAL && vs >= nvv; // a slice of P^T (wave-uniform): no d_out
-    const int col = 16 * ((pcol ? vs - nvv : vs) * 4 + wave) + lr;
+    const int col = 16 * (vs * 4 + wave) + lr;
     const int n0 = seg * p.SEGL, n1 = min(p.NC, n0 + p.SEGL);
 
     // the gradient leaving the segment: d_state_out (one segment), the chained
-    // gradient (pass 3), 0 (pass 1 value columns) or the identity (pass 1, P^T)
+    // gradient (pass 3) or 0 (pass 1)
     floatx4 dS[NKT];
     const float *din = nullptr;
     if (!LOCAL) din = p.NSEG == 1 ? bp.d_state_out : bp.ws_rseg + ((size_t)bh * p.NSEG + seg) * K * V;
@@ -120,8 +116,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 16 * kb + 4 * lg + i;
-            dS[kb][i] = LOCAL ? (pcol && row == col ? 1.f : 0.f)
-                              : (din ? din[(p.NSEG == 1 ? (size_t)bh * K * V : 0) + (size_t)row * V + col] : 0.f);
+            dS[kb][i] = LOCAL ? 0.f : (din ? din[(p.NSEG == 1 ? (size_t)bh * K * V : 0) + (size_t)row * V + col] : 0.f);
         }
 
     const floatx4 *__restrict__ KD4 = reinterpret_cast<const floatx4 *>(p.ws_kd);
@@ -157,7 +152,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
         for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                dO[mt][i] = (!pcol && 16 * mt + 4 * lg + i < cv) ? dob[(int64_t)(n * C + 16 * mt + i) * p.sot] : 0.f;
+                dO[mt][i] = (16 * mt + 4 * lg + i < cv) ? dob[(int64_t)(n * C + 16 * mt + i) * p.sot] : 0.f;
 
         // 1: dv_new = Kd dS' + A_qk^T dO (A_qk^T is upper block-triangular)
         floatx4 dvn[NT];
@@ -173,12 +168,10 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
 #pragma unroll
                 for (int st = 0; st < NT; ++st) dvn[st] = mfma16(ka[st][j], dS[kb][j], dvn[st]);
         }
-        if (!pcol) {
 #pragma unroll
-            for (int st = 0; st < NT; ++st)
+        for (int st = 0; st < NT; ++st)
 #pragma unroll
-                for (int rt = st; rt < NT; ++rt) dvn[st] = mfma4x(sAT[(st * NT + rt) * 64 + lane], dO[rt], dvn[st]);
-        }
+            for (int rt = st; rt < NT; ++rt) dvn[st] = mfma4x(sAT[(st * NT + rt) * 64 + lane], dO[rt], dvn[st]);
 
         if (!LOCAL) {
             float *Dsn = bp.ws_dsn + cid * K * V;
@@ -233,7 +226,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int kb = 0; kb < NKT; ++kb) {
-                    dS[kb] = mfma16(qa[kb][j], dO[tt][j], dS[kb]); // dO = 0 for P^T columns
+                    dS[kb] = mfma16(qa[kb][j], dO[tt][j], dS[kb]);
                     dS[kb] = mfma16(-wa[kb][j], dvn[tt][j], dS[kb]);
                 }
         }
@@ -242,14 +235,10 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
 #pragma unroll
         for (int i = 0; i < APF; ++i) sAT[i * 256 + tid] = apre[i];
     }
-    // the gradient entering the segment: dS0 (first segment), R_j or P_j^T (pass 1)
+    // the gradient entering the segment: dS0 (first segment) or R_j (pass 1)
     float *out = nullptr;
-    int ld = V;
     if (!LOCAL) {
         if (seg == 0) out = bp.d_state0 + (size_t)bh * K * V;
-    } else if (pcol) {
-        out = bp.ws_ptseg + ((size_t)bh * p.NSEG + seg) * K * K;
-        ld = K;
     } else {
         out = bp.ws_rseg + ((size_t)bh * p.NSEG + seg - 1) * K * V;
     }
@@ -257,14 +246,15 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
 #pragma unroll
         for (int kb = 0; kb < NKT; ++kb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) out[(size_t)(16 * kb + 4 * lg + i) * ld + col] = dS[kb][i];
+            for (int i = 0; i < 4; ++i) out[(size_t)(16 * kb + 4 * lg + i) * V + col] = dS[kb][i];
     }
 }
 
 // Pass 2 of the segmented reverse recurrence.  ws_rseg holds NSEG slots of
 // K x V per (b, hv): slot NSEG-1 <- d_state_out (or 0), then slot j - 1 (R_j
 // from pass 1) <- P_j^T slot j + R_j for j = NSEG-1 .. 1: the gradient leaving
-// every segment.  Same MFMA layout as the forward's chunk_chain_kernel.
+// every segment.  Same MFMA layout as the forward's chunk_chain_kernel, with
+// P_j^T's A fragments gathered from the forward's row-major P_j.
 template <int K>
 __global__ __launch_bounds__(256, 1) void bwd_chain_kernel(BwdParams bp) {
     const ChunkParams &p = bp.f;
@@ -288,7 +278,7 @@ __global__ __launch_bounds__(256, 1) void bwd_chain_kernel(BwdParams bp) {
             last[o] = S[kb][i];
         }
     for (int j = p.NSEG - 1; j >= 1; --j) {
-        const float *P = bp.ws_ptseg + ((size_t)bh * p.NSEG + j) * K * K; // P_j^T, row-major
+        const float *P = p.ws_pseg + ((size_t)bh * p.NSEG + j) * K * K; // P_j, row-major
         float *Q = slot0 + (size_t)(j - 1) * K * V;
         floatx4 N[NKT];
 #pragma unroll
@@ -299,8 +289,9 @@ __global__ __launch_bounds__(256, 1) void bwd_chain_kernel(BwdParams bp) {
         for (int kb = 0; kb < NKT; ++kb) {
             floatx4 pa[NKT];
 #pragma unroll
-            for (int it = 0; it < NKT; ++it)
-                pa[it] = *reinterpret_cast<const floatx4 *>(P + (size_t)(16 * it + lr) * K + 16 * kb + 4 * lg);
+            for (int it = 0; it < NKT; ++it) // P_j^T[16 it + lr][16 kb + 4 lg + st] = P_j[16 kb + 4 lg + st][16 it + lr]
+#pragma unroll
+                for (int st = 0; st < 4; ++st) pa[it][st] = P[(size_t)(16 * kb + 4 * lg + st) * K + 16 * it + lr];
 #pragma unroll
             for (int st = 0; st < 4; ++st)
 #pragma unroll
@@ -826,8 +817,8 @@ hipError_t launch_bwd_t(const BwdParams &bp, hipStream_t s) {
     const int seqs = p.B * p.HV, nch = seqs * p.NC;
     hipError_t e;
     if (p.NSEG > 1) {
-        hipLaunchKernelGGL((bwd_inter_kernel<K, kRevLocal>), dim3(seqs * (p.NSEG - 1) * ((V + K) / 64)), dim3(256), 0,
-                           s, bp, 1, p.NSEG - 1);
+        hipLaunchKernelGGL((bwd_inter_kernel<K, kRevLocal>), dim3(seqs * (p.NSEG - 1) * (V / 64)), dim3(256), 0, s, bp,
+                           1, p.NSEG - 1);
         if ((e = hipGetLastError()) != hipSuccess) return e;
         hipLaunchKernelGGL((bwd_chain_kernel<K>), dim3(seqs * (V / 64)), dim3(256), 0, s, bp);
         if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -866,7 +857,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // The backward's workspace after the forward's: the training operands of the
 // forward, then the backward's per-chunk arrays.
 struct BwdLayout {
-    size_t fwd, wt, qgt, kd, aqkt, akk, sn, vn, dsn, dvn, dvnf, dqg, ptseg, rseg, dwm, dkd, daqk, duu, dgam, drk, dakk, kgrad, total;
+    size_t fwd, wt, qgt, kd, aqkt, akk, sn, vn, dsn, dvn, dvnf, dqg, rseg, dwm, dkd, daqk, duu, dgam, drk, dakk, kgrad, total;
 };
 
 BwdLayout bwd_layout(const gdn2_chunk_args *a) {
@@ -899,7 +890,6 @@ BwdLayout bwd_layout(const gdn2_chunk_args *a) {
         const size_t seqs = (size_t)a->batch * a->num_v_heads, NC = (a->seq_len + kChunk - 1) / kChunk;
         const size_t nseg = (size_t)chunk_segments(seqs, V, NC);
         const size_t ns = nseg > 1 ? seqs * nseg : 0;
-        L.ptseg = off; off = align256(off + f * ns * K * K);
         L.rseg = off; off = align256(off + f * ns * K * V);
     }
     L.total = off;
@@ -970,7 +960,6 @@ extern "C" gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *a, gdn2_str
     bp.ws_drk = reinterpret_cast<float *>(ws + L.drk);
     bp.ws_dakk = reinterpret_cast<float *>(ws + L.dakk);
     bp.ws_kgrad = p.rep > 1 ? reinterpret_cast<float *>(ws + L.kgrad) : nullptr;
-    bp.ws_ptseg = reinterpret_cast<float *>(ws + L.ptseg);
     bp.ws_rseg = reinterpret_cast<float *>(ws + L.rseg);
     // forward: per-chunk operands (training outputs), then the state entering every chunk
     GDN2_HIP_CHECK(launch_chunk(p, s, 1 | 4));

@@ -59,7 +59,8 @@ struct ChunkParams {
     float *ws_gam; // K     exp(G_last)
     // Segmented recurrence for few long sequences (NSEG > 1): the chunks of a
     // sequence are split into NSEG runs of SEGL chunks.  Per (b, hv):
-    float *ws_pseg; // (NSEG-1) x K*K  transition of segments 0 .. NSEG-2 (row-major)
+    float *ws_pseg; // NSEG x K*K      transition of each segment (row-major; the last
+                    //                 one only in the training forward)
     float *ws_qseg; // NSEG x K*V      state entering each segment (slot j + 1 first
                     //                 holds segment j's state from S = 0)
     int NSEG, SEGL;

@@ -62,8 +62,9 @@ def test_chunk_workspace_sizes():
     (transitions and entering states) only for few long sequences; shapes
     outside the kernels' instances size without faulting."""
     assert _chunk_ws(8, 16, 4096, 128, 128) == _per_chunk_ws(8, 16, 4096, 128, 128)
-    # 1 x 16 heads x 65536 tokens: eight segments of 128 chunks
+    # 1 x 16 heads x 65536 tokens: eight segments of 128 chunks, each with its
+    # transition (K x K) and entering state (K x V)
     seg = _chunk_ws(1, 16, 65536, 128, 128) - _per_chunk_ws(1, 16, 65536, 128, 128)
-    assert seg == 4 * 16 * (7 * 128 * 128 + 8 * 128 * 128)
+    assert seg == 4 * 16 * (8 * 128 * 128 + 8 * 128 * 128)
     assert _chunk_ws(1, 1, 20, 16, 8) > 0
     assert _chunk_ws(0, 1, 20, 128, 128) == 0
