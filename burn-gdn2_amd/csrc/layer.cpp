@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "common.hpp"
 #include "gdn2_layer.h"
@@ -753,6 +754,202 @@ extern "C" gdn2_status gdn2_state_write(gdn2_state *S, int which, const float *h
             GDN2_HIP_CHECK(hipMemset(S->conv[S->cur][i], 0, sizeof(float) * state_numel(S, i + 1)));
     }
     GDN2_HIP_CHECK(hipMemcpy(state_ptr(S, which), host, sizeof(float) * n, hipMemcpyHostToDevice));
+    S->some = true;
+    return GDN2_OK;
+}
+
+// ---------------------------------------------------------------------------
+// State interchange: safetensors (8-byte little-endian header length, JSON
+// header padded with spaces to an 8-byte boundary, raw little-endian data).
+// Tensor names are the reference's Gdn2State fields (src/module.rs:30-40).
+// ---------------------------------------------------------------------------
+namespace {
+
+const char *const kStateNames[4] = {"recurrent", "conv_q", "conv_k", "conv_v"};
+
+std::vector<int64_t> state_shape(const gdn2_state *S, int which) {
+    const Dims &d = S->layer->d;
+    if (which == GDN2_STATE_RECURRENT) return {S->batch, d.HV, d.K, d.V};
+    return {S->batch, kShortConvCache, which == GDN2_STATE_CONV_V ? d.vd : d.kd};
+}
+
+// A minimal JSON reader for safetensors headers: objects, arrays, strings and
+// non-negative integers.  Values are kept as raw text spans; objects map keys
+// to spans.
+struct Json {
+    const char *p, *end;
+    bool ok = true;
+    void ws() {
+        while (p < end && (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t')) ++p;
+    }
+    bool eat(char c) {
+        ws();
+        if (p < end && *p == c) { ++p; return true; }
+        return false;
+    }
+    std::string str() {
+        ws();
+        std::string s;
+        if (p >= end || *p != '"') { ok = false; return s; }
+        for (++p; p < end && *p != '"'; ++p) {
+            if (*p == '\\') { // escapes: keep the escaped character
+                if (++p >= end) break;
+            }
+            s.push_back(*p);
+        }
+        if (p >= end) { ok = false; return s; }
+        ++p;
+        return s;
+    }
+    int64_t integer() {
+        ws();
+        int64_t v = 0;
+        if (p >= end || *p < '0' || *p > '9') { ok = false; return 0; }
+        for (; p < end && *p >= '0' && *p <= '9'; ++p) {
+            if (v > (int64_t(1) << 58)) { ok = false; return 0; }
+            v = v * 10 + (*p - '0');
+        }
+        return v;
+    }
+    // skips any value (used for unknown metadata entries)
+    void skip() {
+        ws();
+        if (p >= end) { ok = false; return; }
+        if (*p == '"') { str(); return; }
+        if (*p == '{' || *p == '[') {
+            const char open = *p, close = open == '{' ? '}' : ']';
+            ++p;
+            if (eat(close)) return;
+            do {
+                if (open == '{') { str(); if (!eat(':')) { ok = false; return; } }
+                skip();
+                if (!ok) return;
+            } while (eat(','));
+            if (!eat(close)) ok = false;
+            return;
+        }
+        while (p < end && *p != ',' && *p != '}' && *p != ']') ++p; // number / literal
+    }
+};
+
+struct TensorEntry {
+    std::string dtype;
+    std::vector<int64_t> shape;
+    int64_t begin = -1, end = -1;
+};
+
+}  // namespace
+
+// Gdn2State interchange (the reference keeps the state as four tensors,
+// src/module.rs:30-40): serialised as safetensors with those names.
+extern "C" gdn2_status gdn2_state_serialize(const gdn2_state *S, void *buf, size_t cap, size_t *len) {
+    if (!S || !len) return fail(GDN2_EINVAL, "gdn2_state_serialize: null argument");
+    if (!S->some) return fail(GDN2_EINVAL, "gdn2_state_serialize: the state is empty (None)");
+    const Dims &d = S->layer->d;
+    std::string h = "{\"__metadata__\":{\"format\":\"gdn2_state\",\"num_heads\":\"" + std::to_string(d.H) +
+                    "\",\"num_v_heads\":\"" + std::to_string(d.HV) + "\",\"head_dim\":\"" + std::to_string(d.K) +
+                    "\",\"head_v_dim\":\"" + std::to_string(d.V) + "\"}";
+    int64_t off = 0;
+    for (int w = 0; w < 4; ++w) {
+        const std::vector<int64_t> sh = state_shape(S, w);
+        const int64_t bytes = 4 * state_numel(S, w);
+        h += ",\"" + std::string(kStateNames[w]) + "\":{\"dtype\":\"F32\",\"shape\":[";
+        for (size_t i = 0; i < sh.size(); ++i) h += (i ? "," : "") + std::to_string(sh[i]);
+        h += "],\"data_offsets\":[" + std::to_string(off) + "," + std::to_string(off + bytes) + "]}";
+        off += bytes;
+    }
+    h += "}";
+    while ((8 + h.size()) % 8) h.push_back(' ');
+    const size_t total = 8 + h.size() + (size_t)off;
+    *len = total;
+    if (!buf) return GDN2_OK;
+    if (cap < total) return fail(GDN2_EINVAL, "gdn2_state_serialize: buffer too small (" + std::to_string(total) +
+                                                  " bytes needed)");
+    unsigned char *b = static_cast<unsigned char *>(buf);
+    const uint64_t hn = h.size();
+    for (int i = 0; i < 8; ++i) b[i] = (unsigned char)(hn >> (8 * i));
+    std::memcpy(b + 8, h.data(), h.size());
+    GDN2_HIP_CHECK(hipDeviceSynchronize());
+    unsigned char *data = b + 8 + h.size();
+    for (int w = 0; w < 4; ++w) { // f32 is little-endian on the host and the device
+        const size_t bytes = 4 * (size_t)state_numel(S, w);
+        GDN2_HIP_CHECK(hipMemcpy(data, state_ptr(S, w), bytes, hipMemcpyDeviceToHost));
+        data += bytes;
+    }
+    return GDN2_OK;
+}
+
+extern "C" gdn2_status gdn2_state_deserialize(gdn2_state *S, const void *buf, size_t len) {
+    const std::string who = "gdn2_state_deserialize: ";
+    if (!S || !buf) return fail(GDN2_EINVAL, who + "null argument");
+    const unsigned char *b = static_cast<const unsigned char *>(buf);
+    if (len < 8) return fail(GDN2_EINVAL, who + "truncated header");
+    uint64_t hn = 0;
+    for (int i = 0; i < 8; ++i) hn |= (uint64_t)b[i] << (8 * i);
+    if (hn > len - 8) return fail(GDN2_EINVAL, who + "header length beyond the buffer");
+    const size_t data_len = len - 8 - (size_t)hn;
+    Json js{reinterpret_cast<const char *>(b + 8), reinterpret_cast<const char *>(b + 8 + hn)};
+    TensorEntry ent[4];
+    bool seen[4] = {false, false, false, false};
+    if (!js.eat('{')) return fail(GDN2_EINVAL, who + "header is not a JSON object");
+    if (!js.eat('}')) {
+        do {
+            const std::string key = js.str();
+            if (!js.ok || !js.eat(':')) return fail(GDN2_EINVAL, who + "malformed header");
+            int w = -1;
+            for (int i = 0; i < 4; ++i)
+                if (key == kStateNames[i]) w = i;
+            if (key == "__metadata__") {
+                js.skip();
+            } else if (w < 0) {
+                return fail(GDN2_EINVAL, who + "unexpected tensor '" + key + "'");
+            } else {
+                if (seen[w]) return fail(GDN2_EINVAL, who + "tensor '" + key + "' twice");
+                seen[w] = true;
+                if (!js.eat('{')) return fail(GDN2_EINVAL, who + "malformed entry for '" + key + "'");
+                do {
+                    const std::string f = js.str();
+                    if (!js.ok || !js.eat(':')) return fail(GDN2_EINVAL, who + "malformed entry for '" + key + "'");
+                    if (f == "dtype") {
+                        ent[w].dtype = js.str();
+                    } else if (f == "shape" || f == "data_offsets") {
+                        std::vector<int64_t> v;
+                        if (!js.eat('[')) return fail(GDN2_EINVAL, who + "malformed " + f);
+                        if (!js.eat(']')) {
+                            do v.push_back(js.integer());
+                            while (js.ok && js.eat(','));
+                            if (!js.eat(']')) return fail(GDN2_EINVAL, who + "malformed " + f);
+                        }
+                        if (f == "shape") {
+                            ent[w].shape = v;
+                        } else if (v.size() == 2) {
+                            ent[w].begin = v[0];
+                            ent[w].end = v[1];
+                        }
+                    } else {
+                        js.skip();
+                    }
+                    if (!js.ok) return fail(GDN2_EINVAL, who + "malformed entry for '" + key + "'");
+                } while (js.eat(','));
+                if (!js.eat('}')) return fail(GDN2_EINVAL, who + "malformed entry for '" + key + "'");
+            }
+            if (!js.ok) return fail(GDN2_EINVAL, who + "malformed header");
+        } while (js.eat(','));
+        if (!js.eat('}')) return fail(GDN2_EINVAL, who + "malformed header");
+    }
+    for (int w = 0; w < 4; ++w) {
+        const std::string nm = kStateNames[w];
+        if (!seen[w]) return fail(GDN2_EINVAL, who + "tensor '" + nm + "' missing");
+        if (ent[w].dtype != "F32") return fail(GDN2_EINVAL, who + "'" + nm + "' is " + ent[w].dtype + ", not F32");
+        if (ent[w].shape != state_shape(S, w)) return fail(GDN2_EINVAL, who + "'" + nm + "' has the wrong shape");
+        if (ent[w].begin < 0 || ent[w].end - ent[w].begin != 4 * state_numel(S, w) || (size_t)ent[w].end > data_len)
+            return fail(GDN2_EINVAL, who + "'" + nm + "' has bad data offsets");
+    }
+    GDN2_HIP_CHECK(hipDeviceSynchronize());
+    const unsigned char *data = b + 8 + hn;
+    for (int w = 0; w < 4; ++w)
+        GDN2_HIP_CHECK(hipMemcpy(state_ptr(S, w), data + ent[w].begin, 4 * (size_t)state_numel(S, w),
+                                 hipMemcpyHostToDevice));
     S->some = true;
     return GDN2_OK;
 }

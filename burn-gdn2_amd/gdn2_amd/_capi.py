@@ -97,7 +97,8 @@ EXPORTS = ("gdn2_last_error", "gdn2_hip_available", "gdn2_recurrent_step_f32", "
            "gdn2_layer_config", "gdn2_layer_set_param", "gdn2_layer_get_param", "gdn2_layer_forward_train_f32",
            "gdn2_layer_forward_f32", "gdn2_layer_project_f32", "gdn2_state_create", "gdn2_state_destroy",
            "gdn2_state_set_zeros", "gdn2_state_clear", "gdn2_state_is_some", "gdn2_state_batch",
-           "gdn2_state_numel", "gdn2_state_tensor", "gdn2_state_read", "gdn2_state_write")
+           "gdn2_state_numel", "gdn2_state_tensor", "gdn2_state_read", "gdn2_state_write", "gdn2_state_serialize",
+           "gdn2_state_deserialize")
 
 _lib = None
 
@@ -163,6 +164,8 @@ def _declare_layer(L):
         "gdn2_state_tensor": (fp, [vp, i32]),
         "gdn2_state_read": (i32, [vp, i32, fp, i64]),
         "gdn2_state_write": (i32, [vp, i32, fp, i64]),
+        "gdn2_state_serialize": (i32, [vp, vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]),
+        "gdn2_state_deserialize": (i32, [vp, vp, ctypes.c_size_t]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -170,6 +170,42 @@ class Gdn2State:
             raise ValueError(f"expected shape {self._shape(which)}, got {a.shape}")
         C.check(C.lib().gdn2_state_write(self._h, which, a.ctypes.data_as(ctypes.c_void_p), a.size))
 
+    # -- interchange (safetensors; tensor names are the reference's fields) --
+    def to_bytes(self) -> bytes:
+        """The state as safetensors bytes: "recurrent", "conv_q", "conv_k",
+        "conv_v" (src/module.rs:30-40) plus a __metadata__ block."""
+        n = ctypes.c_size_t()
+        C.check(C.lib().gdn2_state_serialize(self._h, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(n.value)
+        C.check(C.lib().gdn2_state_serialize(self._h, buf, n.value, ctypes.byref(n)))
+        return buf.raw[:n.value]
+
+    def load_bytes(self, data: bytes) -> None:
+        """Fill this state from safetensors bytes (shapes must match)."""
+        buf = ctypes.create_string_buffer(bytes(data), len(data))
+        C.check(C.lib().gdn2_state_deserialize(self._h, buf, len(data)))
+
+    @classmethod
+    def from_bytes(cls, layer: "GatedDeltaNet2", data: bytes) -> "Gdn2State":
+        """A new state of `layer` from safetensors bytes; the batch comes from
+        the "recurrent" tensor's shape."""
+        import json
+
+        hn = int.from_bytes(data[:8], "little")
+        batch = json.loads(data[8:8 + hn])["recurrent"]["shape"][0]
+        s = cls(layer, batch)
+        s.load_bytes(data)
+        return s
+
+    def save(self, path: str) -> None:
+        with open(path, "wb") as fh:
+            fh.write(self.to_bytes())
+
+    @classmethod
+    def load(cls, layer: "GatedDeltaNet2", path: str) -> "Gdn2State":
+        with open(path, "rb") as fh:
+            return cls.from_bytes(layer, fh.read())
+
     @property
     def recurrent(self) -> np.ndarray:
         return self.read(self.RECURRENT)

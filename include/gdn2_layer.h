@@ -14,6 +14,7 @@
  *                                                                   src/module.rs:224-316
  *   gdn2_state_*                       <- Gdn2State / Option<Gdn2State>
  *                                                                   src/module.rs:30-63
+ *   gdn2_state_serialize / _deserialize   Gdn2State interchange (safetensors)
  *
  * Status codes and gdn2_last_error() are those of gdn2.h.  Configuration
  * errors return GDN2_EINVAL with the reference's panic message.  The layer
@@ -163,6 +164,26 @@ GDN2_API float *gdn2_state_tensor(gdn2_state *state, int which);
  * not written keep their values, zeros for a fresh state). */
 GDN2_API gdn2_status gdn2_state_read(const gdn2_state *state, int which, float *host, int64_t numel);
 GDN2_API gdn2_status gdn2_state_write(gdn2_state *state, int which, const float *host, int64_t numel);
+
+/* Gdn2State interchange.  The state as a safetensors byte stream: an 8-byte
+ * little-endian header length, a JSON header padded with spaces to an 8-byte
+ * boundary, then raw little-endian f32 data.  The tensors carry the
+ * reference's field names (src/module.rs:30-40):
+ *   "recurrent" [B, HV, K, V], "conv_q" and "conv_k" [B, 3, kd],
+ *   "conv_v" [B, 3, vd].
+ * __metadata__ holds {format: "gdn2_state", num_heads, num_v_heads,
+ * head_dim, head_v_dim}.  Any safetensors reader can read it, for instance
+ * the Rust safetensors crate that burn's recorders use; a state written by
+ * one can be read here.
+ * gdn2_state_serialize: with buf = NULL it only sets *len to the size;
+ * otherwise cap must be at least that size.  An empty state (None) is
+ * GDN2_EINVAL.
+ * gdn2_state_deserialize: the four tensors must be present, F32, and of this
+ * state's shapes (unknown tensors are GDN2_EINVAL; __metadata__ is not
+ * checked).  The state becomes non-empty.
+ * Both are synchronous host copies. */
+GDN2_API gdn2_status gdn2_state_serialize(const gdn2_state *state, void *buf, size_t cap, size_t *len);
+GDN2_API gdn2_status gdn2_state_deserialize(gdn2_state *state, const void *buf, size_t len);
 
 #ifdef __cplusplus
 }
