@@ -101,6 +101,56 @@ struct ConvCacheParams {
     int B, T, kd, vd;
 };
 
+// Adjoint of the gated RMSNorm over rows of V values (rows = M * HV, each
+// row contiguous).  y = O / rms * weight * silu(G) is recomputed on the way.
+struct NormBwdParams {
+    const float *O, *G, *weight;
+    float *dy;     // in: gradient of y; out: dy * (O / rms) * silu(G) (weight-gradient terms)
+    float *y;      // out: y (input of o_proj)
+    float *dO, *dG;
+    int64_t rows;
+    int V;
+    float eps;
+};
+
+// Adjoint of the projection epilogue for one token per workgroup: recomputes
+// the conv / SiLU pre-activations and the gates from Y and F, and maps the
+// gradients of q, k, g, b [B, H, T, K] and v, w [B, HV, T, V] back to the
+// Linear outputs.
+struct ProjectBwdParams {
+    const float *Y;
+    int64_t ldY, off_q, off_k, off_b, off_v, off_w;
+    const float *F;
+    int64_t ldF;
+    const float *conv_q_in, *conv_k_in, *conv_v_in; // null: pad with token 0
+    const float *q_conv_w, *k_conv_w, *v_conv_w;
+    const float *a_log, *dt_bias, *decay_factors;
+    const float *dq, *dk, *dg, *db, *dv, *dw;
+    float *dY;     // [M, ldY]: b and w columns; q, k, v columns without short conv
+    float *DU;     // [M, 2 kd + vd]: gradient of the conv outputs (pre-SiLU), with short conv
+    float *dF;     // [M, kd]: gradient of f_proj_1's output
+    float *PA;     // [M, kd]: A_log gradient terms (dg_pre * g_pre)
+    float *PD;     // [M, kd]: decay_factors gradient terms, null without min_decay
+    int B, T, H, K, HV, V;
+    int use_short_conv, allow_neg_eigval;
+    float min_decay, one_minus_min_decay;
+};
+
+// Adjoint of the four-tap causal conv: columns of DU (q | k | v channels)
+// back to the raw Linear outputs, the conv caches and the conv weights.
+struct ConvBwdParams {
+    const float *Y;
+    int64_t ldY, off_q, off_k, off_v;
+    const float *DU;
+    const float *cache_q, *cache_k, *cache_v;        // caches on entry, null: pad with token 0
+    const float *d_out_q, *d_out_k, *d_out_v;        // gradients of the caches after the call, or null
+    const float *q_conv_w, *k_conv_w, *v_conv_w;
+    float *dY;
+    float *d_in_q, *d_in_k, *d_in_v;                 // gradients of the caches on entry, or null
+    float *wpart;  // [B * nblk, (2 kd + vd) * 4] per-block conv weight gradients
+    int B, T, kd, vd, tblock;
+};
+
 constexpr int kChunk = 64; // chunk length of the kernels (four 16-row tiles)
 
 size_t project_lds_bytes(int kd);
@@ -110,6 +160,14 @@ hipError_t launch_rmsnorm_gate(float *out, int64_t ld_out, const float *x, int64
                                int64_t ld_gate, const float *weight, int64_t M, int HV, int V, float eps,
                                hipStream_t s);
 hipError_t launch_fill_rows(float *y, int64_t ld, const float *row, int64_t M, int64_t N, hipStream_t s);
+hipError_t launch_rmsnorm_gate_bwd(const NormBwdParams &p, hipStream_t s);
+hipError_t launch_project_bwd(const ProjectBwdParams &p, hipStream_t s);
+int conv_bwd_blocks(int T, int tblock);
+hipError_t launch_conv_bwd(const ConvBwdParams &p, hipStream_t s);
+// out[j] (+)= sum over rows of A[r, c] for c in [j * group, (j + 1) * group),
+// j < N / group; deterministic (fixed split over rows into `parts`).
+hipError_t launch_colsum(const float *A, int64_t rows, int64_t N, int64_t lda, int group, float *out, bool accumulate,
+                         float *part, int parts, hipStream_t s);
 
 hipError_t launch_scan(const ScanParams &p, hipStream_t s);
 hipError_t launch_decode(const DecodeParams &p, hipStream_t s);

@@ -14,6 +14,7 @@
 // recurrence and the norm.
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -166,6 +167,8 @@ struct gdn2_layer {
     float *p[P_COUNT] = {};  // standalone parameters (null for those inside w_in)
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    void *bws = nullptr;  // backward workspace, grown on demand
+    size_t bws_bytes = 0;
 
     int64_t col_offset(int id) const {
         switch (id) {
@@ -444,6 +447,7 @@ extern "C" void gdn2_layer_destroy(gdn2_layer *L) {
     (void)hipFree(L->w_in);
     for (float *p : L->p) (void)hipFree(p);
     (void)hipFree(L->ws);
+    (void)hipFree(L->bws);
     if (prev >= 0) (void)hipSetDevice(prev);
     delete L;
 }
@@ -951,5 +955,352 @@ extern "C" gdn2_status gdn2_state_deserialize(gdn2_state *S, const void *buf, si
         GDN2_HIP_CHECK(hipMemcpy(state_ptr(S, w), data + ent[w].begin, 4 * (size_t)state_numel(S, w),
                                  hipMemcpyHostToDevice));
     S->some = true;
+    return GDN2_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Backward: the gradients burn's autodiff takes through forward /
+// forward_train (tests/autodiff.rs:153-205), with the chunked recurrence
+// adjoint of gdn2_chunk_bwd_f32 in the middle.  Everything is recomputed from
+// x; nothing is kept from the forward call.
+//
+//   dy [M, vd]       = d_out W_o^T                      dW_o   (+)= y^T d_out
+//   dO, dG           = rms_norm_gate adjoint            d o_norm_weight (+)= column sums
+//   dq .. dw         = gdn2_chunk_bwd_f32(dO, d_state)  dS0
+//   dY [M, ld_in]    = projection epilogue + short-conv adjoints (q|k|b|v|w columns)
+//   dY[:, f0] = dF W_f1^T, dY[:, g0] = dG W_g1^T        dW_f1, dW_g1, bias, dt_bias, A_log, decay
+//   dW_in (+)= x^T dY,  dx = dY W_in^T
+// ---------------------------------------------------------------------------
+struct gdn2_layer_grads {
+    const gdn2_layer *layer = nullptr;
+    float *g_in = nullptr;   // [D, ld_in]: gradient of W_in, same column blocks
+    float *p[P_COUNT] = {};  // gradients of the standalone parameters
+};
+
+namespace {
+
+constexpr int kColParts = 64;   // row split of the column sums
+constexpr int kConvTBlock = 64; // tokens per thread in the short-conv adjoint
+
+// Row-major C[M, N] = op(A) op(B) (+ beta C), op(A) [M, Kd], op(B) [Kd, N];
+// ta: A is stored [Kd, M]; tb: B is stored [N, Kd].
+gdn2_status gemm_t(rocblas_handle h, bool ta, bool tb, int64_t M, int64_t N, int64_t Kd, const float *A, int64_t lda,
+                   const float *B, int64_t ldb, float *C, int64_t ldc, float beta) {
+    if (M == 0 || N == 0) return GDN2_OK;
+    const float alpha = 1.0f;
+    const rocblas_status st =
+        rocblas_sgemm(h, tb ? rocblas_operation_transpose : rocblas_operation_none,
+                      ta ? rocblas_operation_transpose : rocblas_operation_none, (rocblas_int)N, (rocblas_int)M,
+                      (rocblas_int)Kd, &alpha, B, (rocblas_int)ldb, A, (rocblas_int)lda, &beta, C, (rocblas_int)ldc);
+    if (st != rocblas_status_success)
+        return fail(GDN2_EHIP, std::string("rocblas_sgemm: ") + rocblas_status_to_string(st));
+    return GDN2_OK;
+}
+
+struct BwdWork {
+    Work fw;                      // the forward's buffers (Y, F, G, q .. w, O) and the chunk workspace
+    float *S0, *Sf;               // state entering the call; the forward's working copy
+    float *y, *dy, *dO, *dG;      // [M, vd]
+    float *dq, *dk, *dg, *db;     // [B, H, T, K]
+    float *dv, *dw;               // [B, HV, T, V]
+    float *dY;                    // [M, ld_in]
+    float *DU;                    // [M, 2 kd + vd], short conv only
+    float *dF, *PA, *PD;          // [M, kd]; PD with min_decay only
+    float *dS0;                   // dS0 when the caller takes none
+    float *wpart;                 // conv weight partials, short conv only
+    float *part;                  // column-sum partials
+};
+
+gdn2_status bwd_workspace(gdn2_layer &L, int64_t B, int64_t T, BwdWork *bw) {
+    const Dims &d = L.d;
+    const int64_t M = B * T;
+    const bool sc = L.cfg.use_short_conv != 0, md = L.cfg.has_min_decay != 0;
+    const int64_t ctot = 2 * d.kd + d.vd, nblk = (T + kConvTBlock - 1) / kConvTBlock;
+    Work tmp{};
+    gdn2_chunk_args ca = chunk_args_for(L, B, T, tmp, nullptr);
+    gdn2_chunk_bwd_args ba{};
+    ba.fwd = ca;
+    const size_t chunk_bytes = std::max(gdn2_chunk_workspace_bytes(&ca), gdn2_chunk_bwd_workspace_bytes(&ba));
+    const size_t f = sizeof(float), nS = f * B * d.HV * d.K * d.V;
+    const size_t nk = f * M * d.kd, nv = f * M * d.vd, nY = f * M * L.ld_in;
+    const int64_t part_cols = std::max<int64_t>(std::max(d.kd, d.vd), 4 * ctot);
+    struct Slot {
+        float **ptr;
+        size_t bytes;
+    } slots[] = {
+        {&bw->fw.Y, nY}, {&bw->fw.F, nk}, {&bw->fw.G, nv}, {&bw->fw.q, nk}, {&bw->fw.k, nk}, {&bw->fw.g, nk},
+        {&bw->fw.b, nk}, {&bw->fw.v, nv}, {&bw->fw.w, nv}, {&bw->fw.O, nv},
+        {&bw->S0, nS}, {&bw->Sf, nS}, {&bw->dS0, nS},
+        {&bw->y, nv}, {&bw->dy, nv}, {&bw->dO, nv}, {&bw->dG, nv},
+        {&bw->dq, nk}, {&bw->dk, nk}, {&bw->dg, nk}, {&bw->db, nk}, {&bw->dv, nv}, {&bw->dw, nv},
+        {&bw->dY, nY}, {&bw->DU, sc ? f * M * ctot : 0}, {&bw->dF, nk}, {&bw->PA, nk}, {&bw->PD, md ? nk : 0},
+        {&bw->wpart, sc ? f * B * nblk * 4 * ctot : 0}, {&bw->part, f * kColParts * part_cols},
+    };
+    size_t total = align256(chunk_bytes);
+    for (const Slot &sl : slots) total += align256(sl.bytes);
+    if (total > L.bws_bytes) {
+        if (L.bws) {
+            GDN2_HIP_CHECK(hipDeviceSynchronize());
+            GDN2_HIP_CHECK(hipFree(L.bws));
+            L.bws = nullptr;
+            L.bws_bytes = 0;
+        }
+        GDN2_HIP_CHECK(hipMalloc(&L.bws, total));
+        L.bws_bytes = total;
+    }
+    char *base = static_cast<char *>(L.bws);
+    bw->fw.chunk = base;
+    bw->fw.chunk_bytes = chunk_bytes;
+    base += align256(chunk_bytes);
+    for (const Slot &sl : slots) {
+        *sl.ptr = sl.bytes ? reinterpret_cast<float *>(base) : nullptr;
+        base += align256(sl.bytes);
+    }
+    bw->fw.S0 = nullptr;
+    return GDN2_OK;
+}
+
+gdn2_status check_state_arg(const gdn2_layer *L, const gdn2_state *S, int64_t B, const char *what) {
+    if (S && (S->layer != L || S->batch != B))
+        return fail(GDN2_EINVAL, std::string("gdn2_layer_backward_f32: ") + what + " made for another layer or batch");
+    return GDN2_OK;
+}
+
+}  // namespace
+
+extern "C" void gdn2_layer_grads_destroy(gdn2_layer_grads *G) {
+    if (!G) return;
+    (void)hipDeviceSynchronize();
+    (void)hipFree(G->g_in);
+    for (float *p : G->p) (void)hipFree(p);
+    delete G;
+}
+
+extern "C" gdn2_status gdn2_layer_grads_create(const gdn2_layer *L, gdn2_layer_grads **out) {
+    if (!L || !out) return fail(GDN2_EINVAL, "gdn2_layer_grads_create: null argument");
+    *out = nullptr;
+    gdn2_layer_grads *G = new gdn2_layer_grads();
+    G->layer = L;
+    const size_t nin = sizeof(float) * L->d.D * L->ld_in;
+    bool ok = hipMalloc(&G->g_in, nin) == hipSuccess && hipMemset(G->g_in, 0, nin) == hipSuccess;
+    for (int id = 0; id < P_COUNT && ok; ++id) {
+        const int64_t n = param_shape(L->cfg, id, nullptr, nullptr);
+        if (n == 0 || L->col_offset(id) >= 0) continue;
+        ok = hipMalloc(&G->p[id], sizeof(float) * n) == hipSuccess &&
+             hipMemset(G->p[id], 0, sizeof(float) * n) == hipSuccess;
+    }
+    if (!ok) {
+        gdn2_layer_grads_destroy(G);
+        return fail(GDN2_EHIP, "gdn2_layer_grads_create: device allocation failed");
+    }
+    *out = G;
+    return GDN2_OK;
+}
+
+extern "C" gdn2_status gdn2_layer_grads_zero(gdn2_layer_grads *G, gdn2_stream_t stream) {
+    if (!G) return fail(GDN2_EINVAL, "gdn2_layer_grads_zero: null grads");
+    hipStream_t s = (hipStream_t)stream;
+    GDN2_HIP_CHECK(launch_fill_rows(G->g_in, 0, nullptr, 1, G->layer->d.D * G->layer->ld_in, s));
+    for (int id = 0; id < P_COUNT; ++id)
+        if (G->p[id])
+            GDN2_HIP_CHECK(launch_fill_rows(G->p[id], 0, nullptr, 1, param_shape(G->layer->cfg, id, nullptr, nullptr), s));
+    return GDN2_OK;
+}
+
+extern "C" gdn2_status gdn2_layer_grads_get(const gdn2_layer_grads *G, const char *name, float *host, int64_t numel) {
+    if (!G || !host) return fail(GDN2_EINVAL, "gdn2_layer_grads_get: null argument");
+    const gdn2_layer *L = G->layer;
+    const int id = param_id(name);
+    if (id < 0) return fail(GDN2_EINVAL, std::string("gdn2_layer_grads_get: unknown parameter ") + (name ? name : ""));
+    int64_t rows = 0, cols = 0;
+    const int64_t n = param_shape(L->cfg, id, &rows, &cols);
+    if (n == 0) return fail(GDN2_EINVAL, std::string("gdn2_layer_grads_get: ") + name + " is absent in this config");
+    if (n != numel)
+        return fail(GDN2_EINVAL, std::string("gdn2_layer_grads_get: ") + name + " has " + std::to_string(n) +
+                                     " elements, got " + std::to_string(numel));
+    GDN2_HIP_CHECK(hipDeviceSynchronize());
+    const int64_t off = L->col_offset(id);
+    if (off >= 0)
+        GDN2_HIP_CHECK(hipMemcpy2D(host, sizeof(float) * cols, G->g_in + off, sizeof(float) * L->ld_in,
+                                   sizeof(float) * cols, rows, hipMemcpyDeviceToHost));
+    else
+        GDN2_HIP_CHECK(hipMemcpy(host, G->p[id], sizeof(float) * n, hipMemcpyDeviceToHost));
+    return GDN2_OK;
+}
+
+extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, int64_t B, int64_t T,
+                                               const gdn2_state *state_in, const float *d_out,
+                                               const gdn2_state *d_state, float *dx, gdn2_state *d_state_in,
+                                               gdn2_layer_grads *G, int accumulate, gdn2_stream_t stream) {
+    const char *who = "gdn2_layer_backward_f32";
+    gdn2_status st = check_layer_call(L, x, B, T, d_out, who);
+    if (st != GDN2_OK) return st;
+    if (!G || G->layer != L) return fail(GDN2_EINVAL, "gdn2_layer_backward_f32: grads missing or made for another layer");
+    if ((st = check_state_arg(L, state_in, B, "state_in")) != GDN2_OK) return st;
+    if ((st = check_state_arg(L, d_state, B, "d_state")) != GDN2_OK) return st;
+    if ((st = check_state_arg(L, d_state_in, B, "d_state_in")) != GDN2_OK) return st;
+    if (d_state_in && (d_state_in == state_in || d_state_in == d_state))
+        return fail(GDN2_EINVAL, "gdn2_layer_backward_f32: d_state_in must be a state of its own");
+    const Dims &d = L->d;
+    if (!chunk_supported((int)d.K, (int)d.V))
+        return fail(GDN2_NOT_APPLICABLE, "gdn2_layer_backward_f32: needs head_dim in {64, 128} and head_v_dim in "
+                                         "{64, 128, 256} (the chunked backward's shapes)");
+    hipStream_t s = (hipStream_t)stream;
+    const bool sc = L->cfg.use_short_conv != 0, md = L->cfg.has_min_decay != 0;
+    const bool has_state = state_in && state_in->some, has_ds = d_state && d_state->some;
+    const float beta = accumulate ? 1.0f : 0.0f;
+    const int64_t M = B * T, nS = B * d.HV * d.K * d.V;
+    const int64_t ncache[3] = {B * 3 * d.kd, B * 3 * d.kd, B * 3 * d.vd};
+
+    // gradient of the caches on entry when they do not enter the conv: a pass-through
+    // without short conv (the forward leaves them unchanged), zero otherwise
+    auto pass_caches = [&](bool through) -> gdn2_status {
+        for (int i = 0; i < 3; ++i) {
+            float *dst = d_state_in->conv[d_state_in->cur][i];
+            if (through && has_ds)
+                GDN2_HIP_CHECK(hipMemcpyAsync(dst, d_state->conv[d_state->cur][i], sizeof(float) * ncache[i],
+                                              hipMemcpyDeviceToDevice, s));
+            else
+                GDN2_HIP_CHECK(launch_fill_rows(dst, 0, nullptr, 1, ncache[i], s));
+        }
+        return GDN2_OK;
+    };
+
+    if (T == 0) {  // forward is a no-op: the state's gradient passes through
+        if (!accumulate && (st = gdn2_layer_grads_zero(G, stream)) != GDN2_OK) return st;
+        if (d_state_in) {
+            if (has_ds)
+                GDN2_HIP_CHECK(hipMemcpyAsync(d_state_in->S, d_state->S, sizeof(float) * nS, hipMemcpyDeviceToDevice, s));
+            else
+                GDN2_HIP_CHECK(launch_fill_rows(d_state_in->S, 0, nullptr, 1, nS, s));
+            if ((st = pass_caches(true)) != GDN2_OK) return st;
+            d_state_in->some = true;
+        }
+        return GDN2_OK;
+    }
+
+    BwdWork bw{};
+    if ((st = bwd_workspace(*L, B, T, &bw)) != GDN2_OK) return st;
+    const Work &fw = bw.fw;
+    const float *conv_in[3] = {};
+    if (has_state)
+        for (int i = 0; i < 3; ++i) conv_in[i] = state_in->conv[state_in->cur][i];
+
+    // forward recomputation up to the recurrence output O
+    if ((st = input_gemms(*L, x, M, fw, s)) != GDN2_OK) return st;
+    if ((st = project_epilogue(*L, B, T, has_state ? conv_in : nullptr, fw, s)) != GDN2_OK) return st;
+    if (has_state)
+        GDN2_HIP_CHECK(hipMemcpyAsync(bw.S0, state_in->S, sizeof(float) * nS, hipMemcpyDeviceToDevice, s));
+    else
+        GDN2_HIP_CHECK(launch_fill_rows(bw.S0, 0, nullptr, 1, nS, s));
+    GDN2_HIP_CHECK(hipMemcpyAsync(bw.Sf, bw.S0, sizeof(float) * nS, hipMemcpyDeviceToDevice, s));
+    gdn2_chunk_args ca = chunk_args_for(*L, B, T, fw, bw.Sf);
+    ca.workspace = fw.chunk;
+    ca.workspace_bytes = fw.chunk_bytes;
+    if ((st = gdn2_chunk_fwd_f32(&ca, s)) != GDN2_OK) return st;
+
+    // o_proj and the gated RMSNorm
+    if ((st = gemm_t(L->blas, false, true, M, d.vd, d.D, d_out, d.D, L->p[P_O], d.D, bw.dy, d.vd, 0.0f)) != GDN2_OK)
+        return st;
+    NormBwdParams np{};
+    np.O = fw.O; np.G = fw.G; np.weight = L->p[P_O_NORM];
+    np.dy = bw.dy; np.y = bw.y; np.dO = bw.dO; np.dG = bw.dG;
+    np.rows = M * d.HV; np.V = (int)d.V; np.eps = (float)L->cfg.norm_eps;
+    GDN2_HIP_CHECK(launch_rmsnorm_gate_bwd(np, s));
+    if ((st = gemm_t(L->blas, true, false, d.vd, d.D, M, bw.y, d.vd, d_out, d.D, G->p[P_O], d.D, beta)) != GDN2_OK)
+        return st;
+    GDN2_HIP_CHECK(launch_colsum(bw.dy, M * d.HV, d.V, d.V, 1, G->p[P_O_NORM], accumulate, bw.part, kColParts, s));
+
+    // the recurrence
+    gdn2_chunk_bwd_args ba{};
+    ba.fwd = chunk_args_for(*L, B, T, fw, bw.S0);
+    ba.d_out = bw.dO;
+    ba.d_state_out = has_ds ? d_state->S : nullptr;
+    ba.dq = bw.dq; ba.dk = bw.dk; ba.dg = bw.dg; ba.db = bw.db; ba.dv = bw.dv; ba.dw = bw.dw;
+    ba.d_state0 = d_state_in ? d_state_in->S : bw.dS0;
+    ba.workspace = fw.chunk;
+    ba.workspace_bytes = fw.chunk_bytes;
+    if ((st = gdn2_chunk_bwd_f32(&ba, s)) != GDN2_OK) return st;
+
+    // projection epilogue and short conv
+    ProjectBwdParams pp{};
+    pp.Y = fw.Y; pp.ldY = L->ld_in;
+    pp.off_q = L->off_q; pp.off_k = L->off_k; pp.off_b = L->off_b; pp.off_v = L->off_v; pp.off_w = L->off_w;
+    pp.F = fw.F; pp.ldF = d.kd;
+    pp.conv_q_in = conv_in[0]; pp.conv_k_in = conv_in[1]; pp.conv_v_in = conv_in[2];
+    pp.q_conv_w = L->p[P_QCONV]; pp.k_conv_w = L->p[P_KCONV]; pp.v_conv_w = L->p[P_VCONV];
+    pp.a_log = L->p[P_A_LOG]; pp.dt_bias = L->p[P_DT_BIAS]; pp.decay_factors = md ? L->p[P_DECAY] : nullptr;
+    pp.dq = bw.dq; pp.dk = bw.dk; pp.dg = bw.dg; pp.db = bw.db; pp.dv = bw.dv; pp.dw = bw.dw;
+    pp.dY = bw.dY; pp.DU = sc ? bw.DU : nullptr; pp.dF = bw.dF; pp.PA = bw.PA; pp.PD = md ? bw.PD : nullptr;
+    pp.B = (int)B; pp.T = (int)T; pp.H = (int)d.H; pp.K = (int)d.K; pp.HV = (int)d.HV; pp.V = (int)d.V;
+    pp.use_short_conv = L->cfg.use_short_conv; pp.allow_neg_eigval = L->cfg.allow_neg_eigval;
+    pp.min_decay = (float)L->cfg.min_decay; pp.one_minus_min_decay = (float)(1.0 - L->cfg.min_decay);
+    GDN2_HIP_CHECK(launch_project_bwd(pp, s));
+    if (sc) {
+        ConvBwdParams cp{};
+        cp.Y = fw.Y; cp.ldY = L->ld_in; cp.off_q = L->off_q; cp.off_k = L->off_k; cp.off_v = L->off_v;
+        cp.DU = bw.DU;
+        cp.cache_q = conv_in[0]; cp.cache_k = conv_in[1]; cp.cache_v = conv_in[2];
+        if (has_ds) {
+            cp.d_out_q = d_state->conv[d_state->cur][0];
+            cp.d_out_k = d_state->conv[d_state->cur][1];
+            cp.d_out_v = d_state->conv[d_state->cur][2];
+        }
+        cp.q_conv_w = L->p[P_QCONV]; cp.k_conv_w = L->p[P_KCONV]; cp.v_conv_w = L->p[P_VCONV];
+        cp.dY = bw.dY;
+        if (d_state_in && has_state) {
+            cp.d_in_q = d_state_in->conv[d_state_in->cur][0];
+            cp.d_in_k = d_state_in->conv[d_state_in->cur][1];
+            cp.d_in_v = d_state_in->conv[d_state_in->cur][2];
+        }
+        cp.wpart = bw.wpart;
+        cp.B = (int)B; cp.T = (int)T; cp.kd = (int)d.kd; cp.vd = (int)d.vd; cp.tblock = kConvTBlock;
+        GDN2_HIP_CHECK(launch_conv_bwd(cp, s));
+        const int64_t parts = B * conv_bwd_blocks((int)T, kConvTBlock), ld = 4 * (2 * d.kd + d.vd);
+        GDN2_HIP_CHECK(launch_colsum(bw.wpart, parts, 4 * d.kd, ld, 1, G->p[P_QCONV], accumulate, bw.part, kColParts, s));
+        GDN2_HIP_CHECK(launch_colsum(bw.wpart + 4 * d.kd, parts, 4 * d.kd, ld, 1, G->p[P_KCONV], accumulate, bw.part,
+                                     kColParts, s));
+        GDN2_HIP_CHECK(launch_colsum(bw.wpart + 8 * d.kd, parts, 4 * d.vd, ld, 1, G->p[P_VCONV], accumulate, bw.part,
+                                     kColParts, s));
+        if (d_state_in && !has_state && (st = pass_caches(false)) != GDN2_OK) return st;
+    } else {
+        if (!accumulate)
+            for (int id : {P_QCONV, P_KCONV, P_VCONV})
+                GDN2_HIP_CHECK(launch_fill_rows(G->p[id], 0, nullptr, 1, param_shape(L->cfg, id, nullptr, nullptr), s));
+        if (d_state_in && (st = pass_caches(has_state)) != GDN2_OK) return st;
+    }
+    // columns of dY between the blocks stay zero, so that dW_in's padding does too
+    const int64_t blocks[7][2] = {{L->off_q, d.kd}, {L->off_k, d.kd}, {L->off_b, d.kd}, {L->off_v, d.vd},
+                                  {L->off_w, d.vd}, {L->off_f0, d.V}, {L->off_g0, d.V}};
+    for (int i = 0; i < 7; ++i) {
+        const int64_t end = blocks[i][0] + blocks[i][1], next = i < 6 ? blocks[i + 1][0] : L->ld_in;
+        if (next > end) GDN2_HIP_CHECK(launch_fill_rows(bw.dY + end, L->ld_in, nullptr, M, next - end, s));
+    }
+
+    // gates: f_proj_1, g_proj_1 (+ bias), dt_bias, A_log, decay_factors
+    const float *Yf0 = fw.Y + L->off_f0, *Yg0 = fw.Y + L->off_g0;
+    if ((st = gemm_t(L->blas, false, true, M, d.V, d.kd, bw.dF, d.kd, L->p[P_F1], d.kd, bw.dY + L->off_f0, L->ld_in,
+                     0.0f)) != GDN2_OK)
+        return st;
+    if ((st = gemm_t(L->blas, true, false, d.V, d.kd, M, Yf0, L->ld_in, bw.dF, d.kd, G->p[P_F1], d.kd, beta)) != GDN2_OK)
+        return st;
+    if ((st = gemm_t(L->blas, false, true, M, d.V, d.vd, bw.dG, d.vd, L->p[P_G1], d.vd, bw.dY + L->off_g0, L->ld_in,
+                     0.0f)) != GDN2_OK)
+        return st;
+    if ((st = gemm_t(L->blas, true, false, d.V, d.vd, M, Yg0, L->ld_in, bw.dG, d.vd, G->p[P_G1], d.vd, beta)) != GDN2_OK)
+        return st;
+    GDN2_HIP_CHECK(launch_colsum(bw.dG, M, d.vd, d.vd, 1, G->p[P_G1_BIAS], accumulate, bw.part, kColParts, s));
+    GDN2_HIP_CHECK(launch_colsum(bw.dF, M, d.kd, d.kd, 1, G->p[P_DT_BIAS], accumulate, bw.part, kColParts, s));
+    GDN2_HIP_CHECK(launch_colsum(bw.PA, M, d.kd, d.kd, (int)d.K, G->p[P_A_LOG], accumulate, bw.part, kColParts, s));
+    if (md) GDN2_HIP_CHECK(launch_colsum(bw.PD, M, d.kd, d.kd, 1, G->p[P_DECAY], accumulate, bw.part, kColParts, s));
+
+    // the input Linear layers
+    if ((st = gemm_t(L->blas, true, false, d.D, L->ld_in, M, x, d.D, bw.dY, L->ld_in, G->g_in, L->ld_in, beta)) !=
+        GDN2_OK)
+        return st;
+    if (dx && (st = gemm_t(L->blas, false, true, M, d.D, L->ld_in, bw.dY, L->ld_in, L->w_in, L->ld_in, dx, d.D,
+                           0.0f)) != GDN2_OK)
+        return st;
+    if (d_state_in) d_state_in->some = true;
     return GDN2_OK;
 }

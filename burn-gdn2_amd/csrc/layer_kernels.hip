@@ -13,6 +13,11 @@ __device__ __forceinline__ float sigmoid_(float x) { return 1.0f / (1.0f + __exp
 __device__ __forceinline__ float silu_(float x) { return x / (1.0f + __expf(-x)); }
 // burn's softplus(x, beta = 1) = ln(1 + e^x); above 20 the f32 value is x.
 __device__ __forceinline__ float softplus_(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+// d silu(x) / dx = s (1 + x (1 - s)), s = sigmoid(x)
+__device__ __forceinline__ float dsilu_(float x) {
+    const float sg = sigmoid_(x);
+    return sg * (1.0f + x * (1.0f - sg));
+}
 
 // Causal depthwise conv with four taps at token t of one sequence
 // (src/short_conv.rs:22-65): y = sum_i xpad[t + i] * w[c, i] with
@@ -162,6 +167,231 @@ __global__ __launch_bounds__(256) void fill_rows_kernel(float *y, int64_t ld, co
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Backward (the adjoints of the kernels above)
+// ---------------------------------------------------------------------------
+
+// Gated RMSNorm adjoint, one wave per (token, value head) row.  With
+// r = (mean O^2 + eps)^-1/2, n = O r, z = silu(G), y = n w z:
+//   dn = dy w z,  dO = r dn - O r^3 (sum dy w z O) / V,
+//   dG = dy n w silu'(G),  weight-gradient terms dy n z.
+__global__ __launch_bounds__(256) void rmsnorm_gate_bwd_kernel(NormBwdParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (row >= p.rows) return;
+    const int64_t o = row * p.V;
+    float s1 = 0.f, s2 = 0.f;
+    for (int i = lane; i < p.V; i += 64) {
+        const float x = p.O[o + i];
+        s1 += x * x;
+        s2 += p.dy[o + i] * p.weight[i] * silu_(p.G[o + i]) * x;
+    }
+    s1 = wave_sum(s1);
+    s2 = wave_sum(s2);
+    const float r = 1.0f / sqrtf(s1 / (float)p.V + p.eps);
+    const float c3 = r * r * r * s2 / (float)p.V;
+    for (int i = lane; i < p.V; i += 64) {
+        const float x = p.O[o + i], gt = p.G[o + i], dyv = p.dy[o + i], w = p.weight[i];
+        const float z = silu_(gt), n = x * r;
+        p.y[o + i] = n * w * z;
+        p.dO[o + i] = r * dyv * w * z - x * c3;
+        p.dG[o + i] = dyv * n * w * dsilu_(gt);
+        p.dy[o + i] = dyv * n * z;
+    }
+}
+
+// Projection epilogue adjoint, one workgroup per token m = b * T + t.
+__global__ __launch_bounds__(256) void project_bwd_kernel(ProjectBwdParams p) {
+    extern __shared__ float sm[];
+    const int kd = p.H * p.K, vd = p.HV * p.V;
+    float *s_uq = sm, *s_uk = sm + kd;
+    const int64_t m = blockIdx.x;
+    const int bi = (int)(m / p.T), t = (int)(m % p.T);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t m0 = (int64_t)bi * p.T;
+    const float *Y = p.Y + m * p.ldY;
+    const float *Y0 = p.Y + m0 * p.ldY;
+    float *dY = p.dY + m * p.ldY;
+    float *DU = p.DU ? p.DU + m * (int64_t)(2 * kd + vd) : nullptr;
+    const bool sc = p.use_short_conv != 0;
+
+    // pre-activations of q and k (conv output or raw projection)
+    for (int c = tid; c < kd; c += 256) {
+        if (sc) {
+            const int64_t cb = (int64_t)bi * 3 * kd + c;
+            s_uq[c] = conv4(Y0 + p.off_q + c, p.ldY, t, p.conv_q_in ? p.conv_q_in + cb : nullptr, kd, p.q_conv_w + 4 * c);
+            s_uk[c] = conv4(Y0 + p.off_k + c, p.ldY, t, p.conv_k_in ? p.conv_k_in + cb : nullptr, kd, p.k_conv_w + 4 * c);
+        } else {
+            s_uq[c] = Y[p.off_q + c];
+            s_uk[c] = Y[p.off_k + c];
+        }
+    }
+    // gates: g = -e^{A_log} softplus(f + dt_bias) (+ min_decay), b = sigmoid (x2)
+    for (int c = tid; c < kd; c += 256) {
+        const int64_t o = ((int64_t)bi * p.H + c / p.K) * p.T * p.K + (int64_t)t * p.K + c % p.K;
+        const float xg = p.F[m * p.ldF + c] + p.dt_bias[c];
+        const float A = expf(p.a_log[c / p.K]);
+        const float gp = -A * softplus_(xg);
+        float dgv = p.dg[o];
+        if (p.decay_factors) {
+            // g = ln(sd (1 - m) e^{gp} + m), sd = sigmoid(decay_factors)
+            const float sd = sigmoid_(p.decay_factors[c]);
+            const float eg = expf(gp);
+            const float e = sd * p.one_minus_min_decay * eg;
+            const float inv = 1.0f / (e + p.min_decay);
+            p.PD[m * kd + c] = dgv * eg * p.one_minus_min_decay * sd * (1.0f - sd) * inv;
+            dgv *= e * inv;
+        }
+        p.PA[m * kd + c] = dgv * gp;
+        p.dF[m * kd + c] = -dgv * A * sigmoid_(xg);
+        const float sb = sigmoid_(Y[p.off_b + c]);
+        dY[p.off_b + c] = p.db[o] * (p.allow_neg_eigval ? 2.0f : 1.0f) * sb * (1.0f - sb);
+    }
+    // v = silu(conv(v_raw)), w = sigmoid(w_raw)
+    for (int c = tid; c < vd; c += 256) {
+        const int64_t o = ((int64_t)bi * p.HV + c / p.V) * p.T * p.V + (int64_t)t * p.V + c % p.V;
+        float uv;
+        if (sc) {
+            const int64_t cb = (int64_t)bi * 3 * vd + c;
+            uv = conv4(Y0 + p.off_v + c, p.ldY, t, p.conv_v_in ? p.conv_v_in + cb : nullptr, vd, p.v_conv_w + 4 * c);
+        } else {
+            uv = Y[p.off_v + c];
+        }
+        const float duv = p.dv[o] * dsilu_(uv);
+        if (sc)
+            DU[2 * kd + c] = duv;
+        else
+            dY[p.off_v + c] = duv;
+        const float sw = sigmoid_(Y[p.off_w + c]);
+        dY[p.off_w + c] = p.dw[o] * sw * (1.0f - sw);
+    }
+    __syncthreads();
+    // L2 norm adjoint per key head (one wave per head): with a = silu(u),
+    // nrm = sqrt(sum a^2 + 1e-6), q = a / nrm:
+    //   da = (dq - a (sum dq a) / nrm^2) / nrm,  du = da silu'(u)
+    for (int h = wave; h < p.H; h += 4) {
+        const int64_t o = ((int64_t)bi * p.H + h) * p.T * p.K + (int64_t)t * p.K;
+        float sq = 0.f, sk = 0.f, dq_a = 0.f, dk_a = 0.f;
+        for (int i = lane; i < p.K; i += 64) {
+            const float aq = silu_(s_uq[h * p.K + i]), ak = silu_(s_uk[h * p.K + i]);
+            sq += aq * aq;
+            sk += ak * ak;
+            dq_a += p.dq[o + i] * aq;
+            dk_a += p.dk[o + i] * ak;
+        }
+        sq = wave_sum(sq);
+        sk = wave_sum(sk);
+        dq_a = wave_sum(dq_a);
+        dk_a = wave_sum(dk_a);
+        const float iq = 1.0f / sqrtf(sq + 1e-6f), ik = 1.0f / sqrtf(sk + 1e-6f);
+        const float cq = dq_a * iq * iq, ck = dk_a * ik * ik;
+        for (int i = lane; i < p.K; i += 64) {
+            const int c = h * p.K + i;
+            const float uq = s_uq[c], uk = s_uk[c];
+            const float duq = (p.dq[o + i] - silu_(uq) * cq) * iq * dsilu_(uq);
+            const float duk = (p.dk[o + i] - silu_(uk) * ck) * ik * dsilu_(uk);
+            if (sc) {
+                DU[c] = duq;
+                DU[kd + c] = duk;
+            } else {
+                dY[p.off_q + c] = duq;
+                dY[p.off_k + c] = duk;
+            }
+        }
+    }
+}
+
+// Short-conv adjoint.  One thread per (batch row, channel, block of tblock
+// tokens); channels [0, kd) are q, [kd, 2 kd) k, [2 kd, 2 kd + vd) v.  With
+// xpad = cat(cache or 3 copies of token 0, x) of length T + 3, u[t] =
+// sum_i xpad[t + i] w[i] and the new cache xpad[T .. T + 3):
+//   dxpad[j] = sum_{i, 0 <= j - i < T} du[j - i] w[i]  (+ d_cache_out[j - T] for j >= T)
+//   dx[s] = dxpad[s + 3]  (+ dxpad[0] + dxpad[1] + dxpad[2] at s = 0 without a cache)
+//   d_cache_in[j] = dxpad[j] (j < 3, with a cache),  dw[i] = sum_t du[t] xpad[t + i]
+__global__ __launch_bounds__(256) void conv_bwd_kernel(ConvBwdParams p) {
+    const int kd = p.kd, vd = p.vd, Ctot = 2 * kd + vd;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    const int blk = blockIdx.y, bi = blockIdx.z, nblk = gridDim.y;
+    if (c >= Ctot) return;
+    int cc;
+    int64_t col, n;
+    const float *wc, *cache, *dco;
+    float *dci;
+    if (c < kd) {
+        cc = c; n = kd; col = p.off_q + cc; wc = p.q_conv_w; cache = p.cache_q; dco = p.d_out_q; dci = p.d_in_q;
+    } else if (c < 2 * kd) {
+        cc = c - kd; n = kd; col = p.off_k + cc; wc = p.k_conv_w; cache = p.cache_k; dco = p.d_out_k; dci = p.d_in_k;
+    } else {
+        cc = c - 2 * kd; n = vd; col = p.off_v + cc; wc = p.v_conv_w; cache = p.cache_v; dco = p.d_out_v; dci = p.d_in_v;
+    }
+    const int64_t cb = (int64_t)bi * 3 * n + cc;  // [B, 3, n] offset of this channel
+    if (cache) cache += cb;
+    if (dco) dco += cb;
+    if (dci) dci += cb;
+    const float w[4] = {wc[4 * cc], wc[4 * cc + 1], wc[4 * cc + 2], wc[4 * cc + 3]};
+    const int T = p.T;
+    const int64_t ldu = Ctot;
+    const float *du = p.DU + (int64_t)bi * T * ldu + c;
+    const float *x = p.Y + (int64_t)bi * T * p.ldY + col;
+    float *dx = p.dY + (int64_t)bi * T * p.ldY + col;
+    auto xpad = [&](int j) -> float {
+        if (j >= 3) return x[(int64_t)(j - 3) * p.ldY];
+        return cache ? cache[(int64_t)j * n] : x[0];
+    };
+    auto dxpad = [&](int j) -> float {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int tt = j - i;
+            if (tt >= 0 && tt < T) acc += du[(int64_t)tt * ldu] * w[i];
+        }
+        if (dco && j >= T) acc += dco[(int64_t)(j - T) * n];
+        return acc;
+    };
+    const int t0 = blk * p.tblock, t1 = min(T, t0 + p.tblock);
+    float dw0 = 0.f, dw1 = 0.f, dw2 = 0.f, dw3 = 0.f;
+    for (int t = t0; t < t1; ++t) {
+        const float g = du[(int64_t)t * ldu];
+        dw0 += g * xpad(t);
+        dw1 += g * xpad(t + 1);
+        dw2 += g * xpad(t + 2);
+        dw3 += g * xpad(t + 3);
+        float d = dxpad(t + 3);
+        if (t == 0 && !cache) d += dxpad(0) + dxpad(1) + dxpad(2);
+        dx[(int64_t)t * p.ldY] = d;
+    }
+    if (blk == 0 && cache && dci)
+        for (int j = 0; j < 3; ++j) dci[(int64_t)j * n] = dxpad(j);
+    float *wp = p.wpart + ((int64_t)(bi * nblk + blk) * Ctot + c) * 4;
+    wp[0] = dw0;
+    wp[1] = dw1;
+    wp[2] = dw2;
+    wp[3] = dw3;
+}
+
+// Column sums in two deterministic steps: partial sums over `parts` row
+// ranges, then the sum of the parts (and of `group` adjacent columns).
+__global__ __launch_bounds__(256) void colsum_part_kernel(const float *A, int64_t rows, int64_t N, int64_t lda,
+                                                          int64_t rows_per, float *part) {
+    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= N) return;
+    const int64_t r0 = (int64_t)blockIdx.y * rows_per, r1 = min(rows, r0 + rows_per);
+    float acc = 0.f;
+    for (int64_t r = r0; r < r1; ++r) acc += A[r * lda + c];
+    part[(int64_t)blockIdx.y * N + c] = acc;
+}
+
+__global__ __launch_bounds__(256) void colsum_final_kernel(const float *part, int parts, int64_t N, int group,
+                                                           float *out, int accumulate) {
+    const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (j >= N / group) return;
+    float acc = 0.f;
+    for (int r = 0; r < parts; ++r)
+        for (int i = 0; i < group; ++i) acc += part[(int64_t)r * N + j * group + i];
+    out[j] = accumulate ? out[j] + acc : acc;
+}
+
 int grid_for(int64_t n) {
     const int64_t g = (n + 255) / 256;
     return (int)(g < 8192 ? (g > 0 ? g : 1) : 8192);
@@ -197,6 +427,49 @@ hipError_t launch_rmsnorm_gate(float *out, int64_t ld_out, const float *x, int64
 hipError_t launch_fill_rows(float *y, int64_t ld, const float *row, int64_t M, int64_t N, hipStream_t s) {
     if (M * N == 0) return hipSuccess;
     hipLaunchKernelGGL(fill_rows_kernel, dim3(grid_for(M * N)), dim3(256), 0, s, y, ld, row, M, N);
+    return hipGetLastError();
+}
+
+}  // namespace gdn2
+
+namespace gdn2 {
+
+hipError_t launch_rmsnorm_gate_bwd(const NormBwdParams &p, hipStream_t s) {
+    if (p.rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(rmsnorm_gate_bwd_kernel, dim3((unsigned)((p.rows + 3) / 4)), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_project_bwd(const ProjectBwdParams &p, hipStream_t s) {
+    const int64_t M = (int64_t)p.B * p.T;
+    if (M == 0) return hipSuccess;
+    hipLaunchKernelGGL(project_bwd_kernel, dim3((unsigned)M), dim3(256), project_lds_bytes(p.H * p.K), s, p);
+    return hipGetLastError();
+}
+
+int conv_bwd_blocks(int T, int tblock) { return (T + tblock - 1) / tblock; }
+
+hipError_t launch_conv_bwd(const ConvBwdParams &p, hipStream_t s) {
+    if (p.B == 0 || p.T == 0) return hipSuccess;
+    const int Ctot = 2 * p.kd + p.vd;
+    hipLaunchKernelGGL(conv_bwd_kernel, dim3((unsigned)((Ctot + 255) / 256), (unsigned)conv_bwd_blocks(p.T, p.tblock),
+                                             (unsigned)p.B),
+                       dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_colsum(const float *A, int64_t rows, int64_t N, int64_t lda, int group, float *out, bool accumulate,
+                         float *part, int parts, hipStream_t s) {
+    if (N == 0) return hipSuccess;
+    if (parts < 1) parts = 1;
+    const int64_t rows_per = rows > 0 ? (rows + parts - 1) / parts : 0;
+    hipLaunchKernelGGL(colsum_part_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)parts), dim3(256), 0, s, A,
+                       rows, N, lda, rows_per, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t nout = N / group;
+    hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((nout + 255) / 256)), dim3(256), 0, s, part, parts, N,
+                       group, out, accumulate ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -4,6 +4,8 @@ of include/gdn2_layer.h.
   Gdn2Config      src/config.rs:23-130 (fields, Default, validate)
   GatedDeltaNet2  src/module.rs:93-495 (new, forward, forward_train, project)
   Gdn2State       src/module.rs:30-63
+  Gdn2Grads       the parameter gradients that burn's autodiff returns
+                  (tests/autodiff.rs:153-205), from GatedDeltaNet2.backward
 
 Parameters live in device memory owned by the library; x and the outputs
 are float32 torch device tensors [B, T, hidden_size].  Every call runs the
@@ -223,6 +225,65 @@ class Gdn2State:
         return self.read(self.CONV_V)
 
 
+class Gdn2Grads:
+    """Gradients of every parameter of one layer, in device buffers owned by
+    the library (zero on creation).  `get(name)` returns a host copy in the
+    parameter's shape."""
+
+    def __init__(self, layer: "GatedDeltaNet2"):
+        self._layer = layer
+        h = ctypes.c_void_p()
+        C.check(C.lib().gdn2_layer_grads_create(layer._h, ctypes.byref(h)))
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            C.lib().gdn2_layer_grads_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def zero(self) -> None:
+        C.check(C.lib().gdn2_layer_grads_zero(self._h, _stream()))
+
+    def get(self, name: str) -> Optional[np.ndarray]:
+        shape = param_shape(self._layer.config, name)
+        if not shape:
+            return None
+        out = np.empty(shape, np.float32)
+        C.check(C.lib().gdn2_layer_grads_get(self._h, name.encode(), out.ctypes.data_as(ctypes.c_void_p), out.size))
+        return out
+
+    def as_dict(self) -> Dict[str, Optional[np.ndarray]]:
+        return {n: self.get(n) for n in param_names()}
+
+
+def _forward_train_fn():
+    import torch
+
+    class _ForwardTrain(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x, layer):
+            ctx.layer = layer
+            ctx.save_for_backward(x)
+            return layer.forward_train(x)
+
+        @staticmethod
+        def backward(ctx, d_out):
+            (x,) = ctx.saved_tensors
+            layer = ctx.layer
+            if layer.grads is None:
+                layer.grads = Gdn2Grads(layer)
+            dx, _, _ = layer.backward(x, d_out, grads=layer.grads, accumulate=True)
+            return dx, None
+
+    return _ForwardTrain
+
+
 class GatedDeltaNet2:
     """GatedDeltaNet2 (src/module.rs:93-495) on the current HIP device."""
 
@@ -232,8 +293,12 @@ class GatedDeltaNet2:
         h = ctypes.c_void_p()
         C.check(C.lib().gdn2_layer_create(ctypes.byref(cfg.to_c()), ctypes.c_uint64(seed), ctypes.byref(h)))
         self._h = h
+        self.grads: Optional[Gdn2Grads] = None  # filled by forward_train_autograd's backward
 
     def close(self):
+        if getattr(self, "grads", None) is not None:
+            self.grads.close()
+            self.grads = None
         if getattr(self, "_h", None):
             C.lib().gdn2_layer_destroy(self._h)
             self._h = None
@@ -320,3 +385,35 @@ class GatedDeltaNet2:
                                                *(o[n].data_ptr() for n in ("q", "k", "g", "b", "v", "w", "gate")),
                                                _stream()))
         return o
+
+    # -- backward -----------------------------------------------------------
+    def backward(self, x, d_out, state: Optional[Gdn2State] = None, d_state: Optional[Gdn2State] = None,
+                 grads: Optional[Gdn2Grads] = None, accumulate: bool = False, want_dx: bool = True,
+                 want_d_state: bool = False):
+        """Gradients of <d_out, out> + <d_state, state after the call> for
+        forward(x, state) (state None or empty: forward_train).  `state` is
+        the state BEFORE that call and is not modified.  Returns
+        (dx or None, grads, d_state_in or None); parameter gradients go into
+        `grads` (a new Gdn2Grads when None), added to it with accumulate."""
+        import torch
+
+        x = self._check_x(x)
+        if d_out.shape != x.shape or d_out.dtype != torch.float32 or not d_out.is_cuda:
+            raise TypeError("d_out must be a float32 device tensor shaped like x")
+        d_out = d_out.contiguous()
+        B, T = x.shape[:2]
+        if grads is None:
+            grads = Gdn2Grads(self)
+        dx = torch.empty_like(x) if want_dx else None
+        d_state_in = Gdn2State(self, B) if want_d_state else None
+        C.check(C.lib().gdn2_layer_backward_f32(
+            self._h, x.data_ptr(), B, T, state._h if state is not None else None, d_out.data_ptr(),
+            d_state._h if d_state is not None else None, dx.data_ptr() if dx is not None else None,
+            d_state_in._h if d_state_in is not None else None, grads._h, int(bool(accumulate)), _stream()))
+        return dx, grads, d_state_in
+
+    def forward_train_autograd(self, x):
+        """forward_train as a torch autograd node: `loss.backward()` adds the
+        parameter gradients to `self.grads` (created on first use, as burn's
+        Gradients) and propagates dx to x."""
+        return _forward_train_fn().apply(x, self)

@@ -140,6 +140,51 @@ GDN2_API gdn2_status gdn2_layer_project_f32(gdn2_layer *layer, const float *x, i
                                             float *v, float *w, float *gate, gdn2_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Training.  The reference trains the layer through burn's autodiff
+ * (tests/autodiff.rs:153-205: gradients of every parameter, through
+ * forward_train in both modes and through token-by-token forward calls with
+ * a state).  Here the backward is an explicit call that recomputes the
+ * forward from x and returns the same gradients.
+ * ---------------------------------------------------------------------- */
+typedef struct gdn2_layer_grads gdn2_layer_grads;
+
+/* One gradient buffer per parameter of `layer`, on its device, zeroed. */
+GDN2_API gdn2_status gdn2_layer_grads_create(const gdn2_layer *layer, gdn2_layer_grads **out);
+GDN2_API void gdn2_layer_grads_destroy(gdn2_layer_grads *grads);
+/* Zero every gradient (stream-ordered fill kernels). */
+GDN2_API gdn2_status gdn2_layer_grads_zero(gdn2_layer_grads *grads, gdn2_stream_t stream);
+/* Synchronous copy of one parameter's gradient to host memory, in the
+ * parameter's shape (gdn2_param_shape); an absent parameter is GDN2_EINVAL. */
+GDN2_API gdn2_status gdn2_layer_grads_get(const gdn2_layer_grads *grads, const char *name, float *host,
+                                          int64_t numel);
+
+/* The gradients of L = <d_out, out> + <d_state, state after the call> for
+ * gdn2_layer_forward_f32(x, state_in) -- and for forward_train when state_in
+ * is NULL or empty (Option::None: S0 = 0, the first token pads the conv).
+ *   x, d_out     [B, T, D]
+ *   state_in     the state before the call (read only), NULL or empty = None
+ *   d_state      NULL or empty = zero; else the gradient of the state after
+ *                the call (recurrent and conv caches)
+ *   dx           [B, T, D], or NULL
+ *   d_state_in   NULL, or a state (not state_in, not d_state) that receives
+ *                the gradient of the state before the call: recurrent = dS0
+ *                (also for None, whose S0 is zero); conv caches = their
+ *                gradient (zero for None with short conv; without short conv
+ *                the caches pass through the call, and so does d_state's).
+ *                It becomes non-empty.
+ *   grads        accumulate = 0: overwritten; 1: added to (gradient
+ *                accumulation, or a chain of calls run backwards, each with
+ *                d_state = the d_state_in of the call after it)
+ * The result does not depend on cfg->mode (both modes compute the same
+ * recurrence); the recurrence's adjoint is gdn2_chunk_bwd_f32.
+ * Limits (else GDN2_NOT_APPLICABLE): head_dim in {64, 128}, head_v_dim in
+ * {64, 128, 256}. */
+GDN2_API gdn2_status gdn2_layer_backward_f32(gdn2_layer *layer, const float *x, int64_t batch, int64_t seq_len,
+                                             const gdn2_state *state_in, const float *d_out,
+                                             const gdn2_state *d_state, float *dx, gdn2_state *d_state_in,
+                                             gdn2_layer_grads *grads, int accumulate, gdn2_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * State: Option<Gdn2State> (src/module.rs:30-63) for one layer and batch.
  * Tensors: 0 recurrent [B, HV, K, V], 1 conv_q [B, 3, kd], 2 conv_k
  * [B, 3, kd], 3 conv_v [B, 3, vd] (oldest cached token first).

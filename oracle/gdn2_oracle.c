@@ -156,8 +156,8 @@ GDN2O_EXPORT void gdn2o_recurrent_f64(const float *q, const float *k, const floa
 /* heads; with gdim / bdim = 1 they sum over channels.  d_ST may be NULL     */
 /* (zero).  dS0 receives the gradient of S0 (zero S0 when S0 is NULL).       */
 /* ------------------------------------------------------------------------ */
-GDN2O_EXPORT void gdn2o_recurrent_bwd_f64(const float *q, const float *k, const float *v, const float *g,
-                                          const float *b, const float *w, const double *S0, const double *d_out,
+static void rec_bwd_d(const double *q, const double *k, const double *v, const double *g,
+                                          const double *b, const double *w, const double *S0, const double *d_out,
                                           const double *d_ST, int B, int HV, int Hk, int T, int K, int V, int gdim,
                                           int bdim, double scale, double *dq, double *dk, double *dg, double *db,
                                           double *dv, double *dw, double *dS0) {
@@ -185,11 +185,11 @@ GDN2O_EXPORT void gdn2o_recurrent_bwd_f64(const float *q, const float *k, const 
             else
                 memset(Sall, 0, sizeof(double) * KV);
             for (int t = 0; t < T; ++t) {
-                const float *kt = k + idx4(bi, Hk, hk, T, t, K, 0);
-                const float *gt = g + idx4(bi, Hk, hk, T, t, gdim, 0);
-                const float *bt = b + idx4(bi, Hk, hk, T, t, bdim, 0);
-                const float *vt = v + idx4(bi, HV, hv, T, t, V, 0);
-                const float *wt = w + idx4(bi, HV, hv, T, t, V, 0);
+                const double *kt = k + idx4(bi, Hk, hk, T, t, K, 0);
+                const double *gt = g + idx4(bi, Hk, hk, T, t, gdim, 0);
+                const double *bt = b + idx4(bi, Hk, hk, T, t, bdim, 0);
+                const double *vt = v + idx4(bi, HV, hv, T, t, V, 0);
+                const double *wt = w + idx4(bi, HV, hv, T, t, V, 0);
                 const double *Sp = Sall + (size_t)t * KV;
                 double *Sn = Sall + (size_t)(t + 1) * KV;
                 for (int i = 0; i < K; ++i) {
@@ -210,12 +210,12 @@ GDN2O_EXPORT void gdn2o_recurrent_bwd_f64(const float *q, const float *k, const 
             else
                 memset(dS, 0, sizeof(double) * KV);
             for (int t = T - 1; t >= 0; --t) {
-                const float *qt = q + idx4(bi, Hk, hk, T, t, K, 0);
-                const float *kt = k + idx4(bi, Hk, hk, T, t, K, 0);
-                const float *gt = g + idx4(bi, Hk, hk, T, t, gdim, 0);
-                const float *bt = b + idx4(bi, Hk, hk, T, t, bdim, 0);
-                const float *vt = v + idx4(bi, HV, hv, T, t, V, 0);
-                const float *wt = w + idx4(bi, HV, hv, T, t, V, 0);
+                const double *qt = q + idx4(bi, Hk, hk, T, t, K, 0);
+                const double *kt = k + idx4(bi, Hk, hk, T, t, K, 0);
+                const double *gt = g + idx4(bi, Hk, hk, T, t, gdim, 0);
+                const double *bt = b + idx4(bi, Hk, hk, T, t, bdim, 0);
+                const double *vt = v + idx4(bi, HV, hv, T, t, V, 0);
+                const double *wt = w + idx4(bi, HV, hv, T, t, V, 0);
                 const double *dOt = d_out + idx4(bi, HV, hv, T, t, V, 0);
                 const double *Sp = Sall + (size_t)t * KV, *S2 = Sall + (size_t)(t + 1) * KV;
                 double *dqt = dq + idx4(bi, Hk, hk, T, t, K, 0), *dkt = dk + idx4(bi, Hk, hk, T, t, K, 0);
@@ -276,6 +276,35 @@ GDN2O_EXPORT void gdn2o_recurrent_bwd_f64(const float *q, const float *k, const 
         free(eg);
         free(kb);
     }
+}
+
+/* Inputs in double (the layer adjoint feeds its own double operands). */
+GDN2O_EXPORT void gdn2o_recurrent_bwd_d(const double *q, const double *k, const double *v, const double *g,
+                                        const double *b, const double *w, const double *S0, const double *d_out,
+                                        const double *d_ST, int B, int HV, int Hk, int T, int K, int V, int gdim,
+                                        int bdim, double scale, double *dq, double *dk, double *dg, double *db,
+                                        double *dv, double *dw, double *dS0) {
+    rec_bwd_d(q, k, v, g, b, w, S0, d_out, d_ST, B, HV, Hk, T, K, V, gdim, bdim, scale, dq, dk, dg, db, dv, dw,
+              dS0);
+}
+
+static double *widen(const float *x, size_t n) {
+    double *y = (double *)malloc(sizeof(double) * (n ? n : 1));
+    for (size_t i = 0; i < n; ++i) y[i] = (double)x[i];
+    return y;
+}
+
+GDN2O_EXPORT void gdn2o_recurrent_bwd_f64(const float *q, const float *k, const float *v, const float *g,
+                                          const float *b, const float *w, const double *S0, const double *d_out,
+                                          const double *d_ST, int B, int HV, int Hk, int T, int K, int V, int gdim,
+                                          int bdim, double scale, double *dq, double *dk, double *dg, double *db,
+                                          double *dv, double *dw, double *dS0) {
+    const size_t nk = (size_t)B * Hk * T, nv = (size_t)B * HV * T * V;
+    double *qd = widen(q, nk * K), *kd = widen(k, nk * K), *gd = widen(g, nk * gdim), *bd = widen(b, nk * bdim);
+    double *vd = widen(v, nv), *wd = widen(w, nv);
+    rec_bwd_d(qd, kd, vd, gd, bd, wd, S0, d_out, d_ST, B, HV, Hk, T, K, V, gdim, bdim, scale, dq, dk, dg, db, dv,
+              dw, dS0);
+    free(qd); free(kd); free(gd); free(bd); free(vd); free(wd);
 }
 
 /* Same scan in f32 with the reference's tensor-op order
@@ -655,6 +684,13 @@ static void scan_d(const double *q, const double *k, const double *v, const doub
         }
         free(vnew);
     }
+}
+
+/* scan_d for callers: S [B][HV][K][V] in/out, out [B][HV][T][V]. */
+GDN2O_EXPORT void gdn2o_scan_d(const double *q, const double *k, const double *v, const double *g, const double *b,
+                               const double *w, double *S, int B, int HV, int Hk, int T, int K, int V,
+                               double scale, double *out) {
+    scan_d(q, k, v, g, b, w, S, B, HV, Hk, T, K, V, scale, out);
 }
 
 /*

@@ -48,6 +48,8 @@ def lib():
         L.gdn2o_recurrent_f64.argtypes = [_vp] * 7 + [i] * 8 + [d, _vp, _vp]
         L.gdn2o_recurrent_f32.argtypes = [_vp] * 7 + [i] * 8 + [d, _vp, _vp]
         L.gdn2o_recurrent_bwd_f64.argtypes = [_vp] * 9 + [i] * 8 + [d] + [_vp] * 7
+        L.gdn2o_recurrent_bwd_d.argtypes = [_vp] * 9 + [i] * 8 + [d] + [_vp] * 7
+        L.gdn2o_scan_d.argtypes = [_vp] * 7 + [i] * 6 + [d, _vp]
         L.gdn2o_chunk_wy_f32.argtypes = [_vp] * 7 + [i] * 8 + [d, i, _vp, _vp]
         L.gdn2o_short_conv.argtypes = [_vp, _vp, _vp, i, i, i, _vp, _vp]
         L.gdn2o_l2norm_rows.argtypes = [_vp, ctypes.c_long, i, d]
@@ -303,3 +305,201 @@ def layer_from_raw(cfg, weights: dict, raw: dict, state: Optional[OracleState] =
                                _ptr(S), _ptr(cq), _ptr(ck), _ptr(cv), _ptr(on), _ptr(oc),
                                None, None, None, None, None, None)
     return on, oc, OracleState(S, cq, ck, cv)
+
+
+# ---------------------------------------------------------------------------
+# Layer adjoint (the gradients burn's autodiff takes through forward /
+# forward_train, tests/autodiff.rs:153-205), in double.
+# ---------------------------------------------------------------------------
+def _sig(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def _silu(x):
+    return x * _sig(x)
+
+
+def _dsilu(x):
+    s = _sig(x)
+    return s * (1.0 + x * (1.0 - s))
+
+
+def _softplus(x):
+    """ln(1 + e^x), evaluated without overflow (burn's softplus with beta = 1)."""
+    return np.maximum(x, 0.0) + np.log1p(np.exp(-np.abs(x)))
+
+
+def scan_d(q, k, v, g, b, w, S0, scale):
+    """The per-token scan on double operands (q, k, g, b [B,H,T,K] with true
+    head repeat for GVA).  Returns (out [B,HV,T,V], S_T)."""
+    q, k, v, g, b, w = (_c(a, np.float64) for a in (q, k, v, g, b, w))
+    B, Hk, T, K = q.shape
+    HV, V = v.shape[1], v.shape[3]
+    S = np.array(S0, np.float64, order="C", copy=True)
+    out = np.empty((B, HV, T, V), np.float64)
+    lib().gdn2o_scan_d(*(_ptr(a) for a in (q, k, v, g, b, w, S)), B, HV, Hk, T, K, V, float(scale), _ptr(out))
+    return out, S
+
+
+def recurrent_bwd_d(q, k, v, g, b, w, d_out, S0=None, d_ST=None, scale=1.0):
+    """recurrent_bwd_f64 on double operands (full-width g and b)."""
+    q, k, v, g, b, w = (_c(a, np.float64) for a in (q, k, v, g, b, w))
+    B, Hk, T, K = q.shape
+    HV, V = v.shape[1], v.shape[3]
+    S0 = None if S0 is None else _c(S0, np.float64)
+    d_out = _c(d_out, np.float64)
+    d_ST = None if d_ST is None else _c(d_ST, np.float64)
+    r = {"dq": np.empty(q.shape), "dk": np.empty(k.shape), "dg": np.empty(g.shape), "db": np.empty(b.shape),
+         "dv": np.empty(v.shape), "dw": np.empty(w.shape), "dS0": np.empty((B, HV, K, V))}
+    lib().gdn2o_recurrent_bwd_d(*(_ptr(a) for a in (q, k, v, g, b, w, S0, d_out, d_ST)), B, HV, Hk, T, K, V, K, K,
+                                float(scale), *(_ptr(r[n]) for n in ("dq", "dk", "dg", "db", "dv", "dw", "dS0")))
+    return r
+
+
+@dataclass
+class LayerGrads:
+    out: np.ndarray          # the forward's output [B, T, D] (recomputed)
+    dx: np.ndarray           # [B, T, D]
+    params: dict             # parameter name -> gradient (None for an absent parameter)
+    d_state: OracleState     # gradient of the state on entry (zeros for the conv caches of Option::None)
+
+
+def layer_backward_f64(cfg, weights: dict, x, d_out, state: Optional[OracleState] = None,
+                       d_state: Optional[OracleState] = None) -> LayerGrads:
+    """Gradients of L = <d_out, out> + <d_state, state after the call> for
+    GatedDeltaNet2::forward(x, &mut state, true) (src/module.rs:224-316;
+    state None = Option::None, which is forward_train, :326-375), true head
+    repeat for GVA.  Everything is recomputed from x in double: Linear layers
+    (y = x W), short conv with replicate padding or cache
+    (src/short_conv.rs:22-65), gates (src/module.rs:417-443), L2 norm
+    (src/l2norm.rs:13-16), the scan (gdn2o_scan_d / gdn2o_recurrent_bwd_d)
+    and the gated RMSNorm (src/module.rs:501-517).  Without short conv the
+    conv caches pass through unchanged, so their gradient passes through."""
+    H, K = cfg.num_heads, cfg.head_dim
+    HV = cfg.num_v_heads or H
+    V = int(K * cfg.expand_v)
+    kd, vd = H * K, HV * V
+    sc, neg, md = bool(cfg.use_short_conv), bool(cfg.allow_neg_eigval), cfg.min_decay
+    W = {n: (None if weights.get(n) is None else np.asarray(weights[n], np.float64)) for n in WEIGHT_NAMES}
+    x = np.asarray(x, np.float64)
+    B, T, D = x.shape
+    M = B * T
+    X = x.reshape(M, D)
+    dY = np.asarray(d_out, np.float64).reshape(M, D)
+    names = {"q": "q_proj", "k": "k_proj", "v": "v_proj", "b": "b_proj", "w": "w_proj"}
+    raw = {n: X @ W[p] for n, p in names.items()}
+    f0 = X @ W["f_proj_0"]
+    f_raw = f0 @ W["f_proj_1"]
+    g0 = X @ W["g_proj_0"]
+    gate = g0 @ W["g_proj_1"] + W["g_proj_1_bias"]
+    width = {"q": kd, "k": kd, "v": vd}
+    caches = None if state is None else {"q": state.conv_q, "k": state.conv_k, "v": state.conv_v}
+    xpad, u = {}, {}
+    for n, C in width.items():
+        r = raw[n].reshape(B, T, C)
+        if sc:
+            pad = np.repeat(r[:, :1], 3, axis=1) if caches is None else np.asarray(caches[n], np.float64)
+            xp = np.concatenate([pad, r], axis=1)
+            wc = W[n + "_conv_w"]
+            u[n] = sum(xp[:, i:i + T] * wc[:, i] for i in range(4))
+            xpad[n] = xp
+        else:
+            u[n] = r
+    A = np.repeat(np.exp(W["a_log"]), K)
+    xg = f_raw + W["dt_bias"]
+    g_pre = -A * _softplus(xg)
+    if md is not None:
+        sdf = _sig(W["decay_factors"].reshape(kd))
+        e = sdf * (1.0 - md) * np.exp(g_pre)
+        gg = np.log(e + md)
+    else:
+        gg = g_pre
+    bs, ws = _sig(raw["b"]), _sig(raw["w"])
+    bmul = 2.0 if neg else 1.0
+    qa = _silu(u["q"]).reshape(B, T, H, K)
+    ka = _silu(u["k"]).reshape(B, T, H, K)
+    nq = np.sqrt((qa * qa).sum(-1, keepdims=True) + 1e-6)
+    nk = np.sqrt((ka * ka).sum(-1, keepdims=True) + 1e-6)
+    qn, kn = qa / nq, ka / nk
+
+    def to4(a, n, d):
+        return np.ascontiguousarray(a.reshape(B, T, n, d).transpose(0, 2, 1, 3))
+
+    def back(a):
+        return a.transpose(0, 2, 1, 3).reshape(M, -1)
+
+    q4, k4, g4, b4 = to4(qn, H, K), to4(kn, H, K), to4(gg, H, K), to4(bs * bmul, H, K)
+    v4, w4 = to4(_silu(u["v"]), HV, V), to4(ws, HV, V)
+    S0 = np.zeros((B, HV, K, V)) if state is None else np.asarray(state.recurrent, np.float64)
+    scale = float(K) ** -0.5
+    O, _ = scan_d(q4, k4, v4, g4, b4, w4, S0, scale)
+    Ob = O.transpose(0, 2, 1, 3)
+    G4 = gate.reshape(B, T, HV, V)
+    rms = np.sqrt((Ob * Ob).mean(-1, keepdims=True) + cfg.norm_eps)
+    nrm, z, wn = Ob / rms, _silu(G4), W["o_norm_weight"]
+    y = (nrm * wn * z).reshape(M, vd)
+    out = (y @ W["o_proj"]).reshape(B, T, D)
+
+    g = {}
+    g["o_proj"] = y.T @ dY
+    dy = (dY @ W["o_proj"].T).reshape(B, T, HV, V)
+    dn = dy * wn * z
+    g["o_norm_weight"] = (dy * nrm * z).reshape(-1, V).sum(0)
+    dgate = (dy * nrm * wn * _dsilu(G4)).reshape(M, vd)
+    dOb = (dn - nrm * (dn * nrm).mean(-1, keepdims=True)) / rms
+    r = recurrent_bwd_d(q4, k4, v4, g4, b4, w4, dOb.transpose(0, 2, 1, 3), S0,
+                        None if d_state is None else d_state.recurrent, scale)
+    dqn, dkn = back(r["dq"]).reshape(B, T, H, K), back(r["dk"]).reshape(B, T, H, K)
+    dqa = (dqn - qn * (dqn * qn).sum(-1, keepdims=True)) / nq
+    dka = (dkn - kn * (dkn * kn).sum(-1, keepdims=True)) / nk
+    dgg, dbb, dva, dws = back(r["dg"]), back(r["db"]), back(r["dv"]), back(r["dw"])
+    if md is not None:
+        dg_pre = dgg * e / (e + md)
+        g["decay_factors"] = ((dgg * np.exp(g_pre) * (1.0 - md) * sdf * (1.0 - sdf) / (e + md)).sum(0)
+                              .reshape(np.shape(W["decay_factors"])))
+    else:
+        dg_pre = dgg
+        g["decay_factors"] = None
+    g["a_log"] = (dg_pre * g_pre).sum(0).reshape(H, K).sum(1)
+    dxg = dg_pre * (-A) * _sig(xg)
+    g["dt_bias"] = dxg.sum(0)
+    draw = {"b": dbb * bmul * bs * (1.0 - bs), "w": dws * ws * (1.0 - ws)}
+    du = {"q": dqa.reshape(B, T, kd) * _dsilu(u["q"]), "k": dka.reshape(B, T, kd) * _dsilu(u["k"]),
+          "v": dva.reshape(B, T, vd) * _dsilu(u["v"])}
+    dconv = {}
+    for n, C in width.items():
+        d_out_cache = None if d_state is None else np.asarray(getattr(d_state, "conv_" + n), np.float64)
+        if sc:
+            wc = W[n + "_conv_w"]
+            dxp = np.zeros((B, T + 3, C))
+            for i in range(4):
+                dxp[:, i:i + T] += du[n] * wc[:, i]
+            if d_out_cache is not None:
+                dxp[:, T:T + 3] += d_out_cache
+            g[n + "_conv_w"] = np.stack([(du[n] * xpad[n][:, i:i + T]).sum((0, 1)) for i in range(4)], axis=1)
+            dr = dxp[:, 3:].copy()
+            if caches is None:
+                dr[:, 0] += dxp[:, :3].sum(1)
+                dconv[n] = np.zeros((B, 3, C))
+            else:
+                dconv[n] = dxp[:, :3].copy()
+        else:
+            dr = du[n]
+            g[n + "_conv_w"] = np.zeros((C, 4))
+            dconv[n] = (d_out_cache.copy() if (d_out_cache is not None and state is not None)
+                        else np.zeros((B, 3, C)))
+        draw[n] = dr.reshape(M, C)
+    dX = np.zeros((M, D))
+    for n, p in names.items():
+        g[p] = X.T @ draw[n]
+        dX += draw[n] @ W[p].T
+    g["f_proj_1"] = f0.T @ dxg
+    df0 = dxg @ W["f_proj_1"].T
+    g["f_proj_0"] = X.T @ df0
+    dX += df0 @ W["f_proj_0"].T
+    g["g_proj_1"] = g0.T @ dgate
+    g["g_proj_1_bias"] = dgate.sum(0)
+    dg0 = dgate @ W["g_proj_1"].T
+    g["g_proj_0"] = X.T @ dg0
+    dX += dg0 @ W["g_proj_0"].T
+    return LayerGrads(out, dX.reshape(B, T, D), g, OracleState(r["dS0"], dconv["q"], dconv["k"], dconv["v"]))
