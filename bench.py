@@ -54,6 +54,10 @@ def parse():
     ap.add_argument("--layer-steps", type=int, default=5)
     ap.add_argument("--decode-prefill", type=int, default=2048)
     ap.add_argument("--no-backward", action="store_true", help="skip the chunked backward timing")
+    ap.add_argument("--train-only", action="store_true",
+                    help="time only the layer training step (forward_train with saved activations + backward)")
+    ap.add_argument("--train-summary", metavar="KERNEL_TRACE_CSV",
+                    help="per-kernel table of the last training step in a rocprofv3 kernel trace of --train-only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="end with a 1 GiB device-to-device copy (reference kernel for HBM counters)")
     ap.add_argument("--stats-summary", metavar="KERNEL_STATS_CSV",
@@ -146,11 +150,54 @@ def bench_prefill(torch, G, args, dev):
     lay = None
     if not args.no_layer:
         lay = time_layer(torch, lambda: layer.forward_train(x), args.layer_steps, tokens)
-        lay["gemm_tflop"] = 2 * tokens * cfg.hidden_size * (3 * cfg.kd + 2 * cfg.vd + 2 * V) / 1e12 + \
-            2 * tokens * V * (cfg.kd + cfg.vd) / 1e12 + 2 * tokens * cfg.vd * cfg.hidden_size / 1e12
+        lay["gemm_tflop"] = sum(layer_gemm_tflop(cfg, tokens))
+        lay.update(time_train_steps(torch, G, layer, x, gen, args, recompute=True))
     layer.close()
     return {"tokens": tokens, "ms_per_step": ms_per_step, "value": tokens / (ms_per_step / 1e3),
             "kernels": kernels, "roofline": roof, "host_sample": host, "scale": scale, "layer": lay}
+
+
+def layer_gemm_tflop(cfg, tokens):
+    """Input-side, gate and o_proj GEMM TFLOP of one forward over `tokens`."""
+    V = cfg.v_head
+    g_in = 2 * tokens * cfg.hidden_size * (3 * cfg.kd + 2 * cfg.vd + 2 * V) / 1e12
+    g_gate = 2 * tokens * V * (cfg.kd + cfg.vd) / 1e12
+    g_out = 2 * tokens * cfg.vd * cfg.hidden_size / 1e12
+    return g_in, g_gate, g_out
+
+
+def time_train_steps(torch, G, layer, x, gen, args, recompute):
+    """One training step: forward_train keeping its activations, then the
+    backward into persistent parameter gradients and dx (d_out ~ N(0,1));
+    with `recompute` also the variant whose backward recomputes the forward."""
+    B, T = x.shape[:2]
+    tokens = B * T
+    g_in, g_gate, g_out = layer_gemm_tflop(layer.config, tokens)
+    d_out = torch.randn(x.shape, generator=gen, device=x.device, dtype=torch.float32)
+    grads = G.Gdn2Grads(layer)
+    acts = G.Gdn2Saved(layer, B, T)
+
+    def train_step():
+        layer.forward_train(x, saved=acts)
+        layer.backward(x, d_out, grads=grads, saved=acts)
+
+    res = {}
+    tr = time_layer(torch, train_step, args.layer_steps, tokens)
+    tr["gemm_tflop"] = 3 * (g_in + g_gate + g_out)
+    tr["activations"] = "saved by forward_train"
+    res["train_step"] = tr
+    acts.close()
+    if recompute:
+        def train_step_recompute():
+            layer.forward_train(x)
+            layer.backward(x, d_out, grads=grads)
+
+        rc = time_layer(torch, train_step_recompute, args.layer_steps, tokens)
+        rc["gemm_tflop"] = 4 * (g_in + g_gate) + 3 * g_out
+        rc["activations"] = "recomputed by the backward"
+        res["train_step_recompute"] = rc
+    grads.close()
+    return res
 
 
 def time_layer(torch, fn, steps, tokens):
@@ -230,6 +277,7 @@ def bench_decode(torch, G, args, dev):
         layer = G.GatedDeltaNet2(cfg, seed=1337)
         xp = torch.randn((Bd, args.decode_prefill, cfg.hidden_size), generator=gen, device=dev)
         xs = torch.randn((steps, Bd, 1, cfg.hidden_size), generator=gen, device=dev)
+        layer.forward(xp)  # first call of this shape: workspace and GEMM plans
         torch.cuda.synchronize()
         e0.record()
         _, st = layer.forward(xp)
@@ -312,6 +360,34 @@ def stats_summary(path):
     for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:12]:
         print(f"| `{_short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
               f"{float(r['TotalDurationNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
+
+
+def train_summary(path):
+    """The kernels of the last training step of a --train-only trace: from the
+    forward's input GEMM (four launches before its project_kernel) to the end."""
+    import csv
+    import re
+
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    last = max(i for i, r in enumerate(rows) if "project_kernel" in r["Kernel_Name"])
+    step = rows[last - 4:]
+    t0 = int(step[0]["Start_Timestamp"])
+    print("| start us | duration us | kernel |")
+    print("|---|---|---|")
+    gemm = other = 0.0
+    for r in step:
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        name = r["Kernel_Name"]
+        if name.startswith("Cijk"):
+            m = re.search(r"MT\d+x\d+x\d+", name)
+            label = f"hipBLASLt {name[:14]} {m.group(0) if m else ''}"
+            gemm += d
+        else:
+            label = _short(name)
+            other += d
+        print(f"| {(int(r['Start_Timestamp']) - t0) / 1e3:.1f} | {d:.1f} | `{label}` |")
+    span = (int(step[-1]["End_Timestamp"]) - t0) / 1e3
+    print(f"\nspan {span:.1f} us; GEMM kernels {gemm:.1f} us, other kernels {other:.1f} us")
 
 
 def traffic_summary(fetch_csv, write_csv):
@@ -411,6 +487,9 @@ def main():
     if args.stats_summary:
         stats_summary(args.stats_summary)
         return
+    if args.train_summary:
+        train_summary(args.train_summary)
+        return
     if args.traffic_summary:
         traffic_summary(*args.traffic_summary)
         return
@@ -428,6 +507,16 @@ def main():
     dev = torch.device("cuda:0")
     if not G.hip_available():
         raise SystemExit("no gfx950 device: bench.py needs an MI355X")
+    if args.train_only:
+        cfg = G.Gdn2Config(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0, mode="chunk", chunk_size=64)
+        layer = G.GatedDeltaNet2(cfg, seed=1337)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(42)
+        x = torch.randn((args.batch, args.seq, cfg.hidden_size), generator=gen, device=dev, dtype=torch.float32)
+        res = time_train_steps(torch, G, layer, x, gen, args, recompute=False)
+        res["workload"] = f"GDN-2 layer training step, B={args.batch} T={args.seq} D=2048 H=16 K=V=128, f32"
+        print(json.dumps(res), flush=True)
+        return
     pre = bench_prefill(torch, G, args, dev)
     dec = None if args.no_decode else bench_decode(torch, G, args, dev)
     bwd = None if args.no_backward else bench_backward(torch, G, args, dev)

@@ -21,7 +21,7 @@ FLAGS = [
     "-fvisibility=hidden",
     "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc"),
 ]
-LIBS = ["-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
+LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
 
 
 def sources():

@@ -1,0 +1,173 @@
+// hipBLASLt plans for the layer's row-major GEMMs (see blas.hpp).
+//
+// Row-major C = op(A) op(B) is column-major C^T = op(B)^T op(A)^T, so the
+// library's first operand is B's memory and its second is A's; a row-major
+// [r, c] matrix with row stride ld is a column-major [c, r] one with leading
+// dimension ld.
+#include "blas.hpp"
+
+#include <algorithm>
+#include <string>
+
+namespace gdn2 {
+
+namespace {
+constexpr size_t kMaxWorkspace = size_t(64) << 20;
+constexpr int kCandidates = 8;  // heuristic results timed per shape
+}
+
+gdn2_status Gemm::ensure_ws(size_t bytes) {
+    if (bytes <= ws_bytes_) return GDN2_OK;
+    if (ws_) {
+        GDN2_HIP_CHECK(hipDeviceSynchronize());
+        GDN2_HIP_CHECK(hipFree(ws_));
+        ws_ = nullptr;
+        ws_bytes_ = 0;
+    }
+    GDN2_HIP_CHECK(hipMalloc(&ws_, bytes));
+    ws_bytes_ = bytes;
+    return GDN2_OK;
+}
+
+gdn2_status Gemm::init() {
+    if (hipblasLtCreate(&lt_) != HIPBLAS_STATUS_SUCCESS) return fail(GDN2_EHIP, "hipblasLtCreate failed");
+    if (rocblas_create_handle(&rb_) != rocblas_status_success) return fail(GDN2_EHIP, "rocblas_create_handle failed");
+    return GDN2_OK;
+}
+
+void Gemm::destroy() {
+    for (Plan &p : plans_) {
+        if (!p.ok) continue;
+        hipblasLtMatrixLayoutDestroy(p.la);
+        hipblasLtMatrixLayoutDestroy(p.lb);
+        hipblasLtMatrixLayoutDestroy(p.lc);
+        hipblasLtMatmulDescDestroy(p.desc);
+    }
+    plans_.clear();
+    if (ws_) (void)hipFree(ws_);
+    ws_ = nullptr;
+    ws_bytes_ = 0;
+    if (lt_) hipblasLtDestroy(lt_);
+    lt_ = nullptr;
+    if (rb_) rocblas_destroy_handle(rb_);
+    rb_ = nullptr;
+}
+
+gdn2_status Gemm::plan(bool ta, bool tb, int64_t M, int64_t N, int64_t Kd, const float *A, int64_t lda,
+                       const float *B, int64_t ldb, int64_t ldc, hipStream_t s, const Plan **out) {
+    for (const Plan &p : plans_)
+        if (p.ta == ta && p.tb == tb && p.M == M && p.N == N && p.Kd == Kd && p.lda == lda && p.ldb == ldb &&
+            p.ldc == ldc) {
+            *out = &p;
+            return GDN2_OK;
+        }
+    Plan p{};
+    p.ta = ta; p.tb = tb; p.M = M; p.N = N; p.Kd = Kd; p.lda = lda; p.ldb = ldb; p.ldc = ldc;
+    const hipblasOperation_t op1 = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N, op2 = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+    bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op1, sizeof op1) ==
+                   HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op2, sizeof op2) ==
+                   HIPBLAS_STATUS_SUCCESS;
+    // first operand: B's memory, column-major [N, Kd] (op N) or [Kd, N] (op T)
+    ok = ok && hipblasLtMatrixLayoutCreate(&p.la, HIP_R_32F, tb ? Kd : N, tb ? N : Kd, ldb) == HIPBLAS_STATUS_SUCCESS;
+    // second operand: A's memory, column-major [Kd, M] (op N) or [M, Kd] (op T)
+    ok = ok && hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_32F, ta ? M : Kd, ta ? Kd : M, lda) == HIPBLAS_STATUS_SUCCESS;
+    ok = ok && hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc) == HIPBLAS_STATUS_SUCCESS;
+    if (!ok) return fail(GDN2_EHIP, "hipBLASLt descriptor creation failed");
+    hipblasLtMatmulPreference_t pref;
+    if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS)
+        return fail(GDN2_EHIP, "hipblasLtMatmulPreferenceCreate failed");
+    const uint64_t maxws = kMaxWorkspace;
+    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &maxws, sizeof maxws);
+    hipblasLtMatmulHeuristicResult_t res[kCandidates];
+    int n = 0;
+    const hipblasStatus_t hs =
+        hipblasLtMatmulAlgoGetHeuristic(lt_, p.desc, p.la, p.lb, p.lc, p.lc, pref, kCandidates, res, &n);
+    hipblasLtMatmulPreferenceDestroy(pref);
+    int best = -1;
+    if (hs == HIPBLAS_STATUS_SUCCESS)
+        for (int i = 0; i < n && best < 0; ++i)
+            if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= kMaxWorkspace) best = i;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (best >= 0 && n > 1 && hipStreamIsCapturing(s, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone) {
+        // time the candidates on these operands, writing a scratch output
+        size_t wsmax = 0;
+        for (int i = 0; i < n; ++i)
+            if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= kMaxWorkspace)
+                wsmax = std::max(wsmax, res[i].workspaceSize);
+        gdn2_status st = ensure_ws(wsmax);
+        if (st != GDN2_OK) return st;
+        float *scratch = nullptr;
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        if (hipMalloc(&scratch, sizeof(float) * (size_t)ldc * M) == hipSuccess && hipEventCreate(&e0) == hipSuccess &&
+            hipEventCreate(&e1) == hipSuccess) {
+            const float alpha = 1.0f, beta = 0.0f;
+            float best_ms = 0.0f;
+            for (int i = 0; i < n; ++i) {
+                if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kMaxWorkspace) continue;
+                bool ok = true;
+                for (int r = 0; r < 3 && ok; ++r) {  // one warm-up, then two timed runs
+                    if (r == 1) ok = hipEventRecord(e0, s) == hipSuccess;
+                    ok = ok && hipblasLtMatmul(lt_, p.desc, &alpha, B, p.la, A, p.lb, &beta, scratch, p.lc, scratch,
+                                               p.lc, &res[i].algo, res[i].workspaceSize ? ws_ : nullptr,
+                                               res[i].workspaceSize, s) == HIPBLAS_STATUS_SUCCESS;
+                }
+                float ms = 0.0f;
+                ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+                     hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+                if (ok && (ms < best_ms || best_ms == 0.0f)) {
+                    best_ms = ms;
+                    best = i;
+                }
+            }
+        }
+        (void)hipGetLastError();  // a failed scratch allocation only skips the timing
+        if (e0) (void)hipEventDestroy(e0);
+        if (e1) (void)hipEventDestroy(e1);
+        if (scratch) {
+            (void)hipStreamSynchronize(s);
+            (void)hipFree(scratch);
+        }
+    }
+    p.ok = best >= 0;
+    if (p.ok) {
+        p.algo = res[best].algo;
+        p.ws = res[best].workspaceSize;
+    } else {
+        hipblasLtMatrixLayoutDestroy(p.la);
+        hipblasLtMatrixLayoutDestroy(p.lb);
+        hipblasLtMatrixLayoutDestroy(p.lc);
+        hipblasLtMatmulDescDestroy(p.desc);
+    }
+    plans_.push_back(p);
+    *out = &plans_.back();
+    return GDN2_OK;
+}
+
+gdn2_status Gemm::run(bool ta, bool tb, int64_t M, int64_t N, int64_t Kd, const float *A, int64_t lda, const float *B,
+                      int64_t ldb, float *C, int64_t ldc, float beta, hipStream_t s) {
+    if (M == 0 || N == 0) return GDN2_OK;
+    const float alpha = 1.0f;
+    const Plan *p = nullptr;
+    gdn2_status st = plan(ta, tb, M, N, Kd, A, lda, B, ldb, ldc, s, &p);
+    if (st != GDN2_OK) return st;
+    if (p->ok) {
+        if ((st = ensure_ws(p->ws)) != GDN2_OK) return st;
+        const hipblasStatus_t hs = hipblasLtMatmul(lt_, p->desc, &alpha, B, p->la, A, p->lb, &beta, C, p->lc, C,
+                                                   p->lc, &p->algo, p->ws ? ws_ : nullptr, p->ws, s);
+        if (hs != HIPBLAS_STATUS_SUCCESS)
+            return fail(GDN2_EHIP, "hipblasLtMatmul failed with status " + std::to_string((int)hs));
+        return GDN2_OK;
+    }
+    if (rocblas_set_stream(rb_, s) != rocblas_status_success) return fail(GDN2_EHIP, "rocblas_set_stream failed");
+    const rocblas_status rs =
+        rocblas_sgemm(rb_, tb ? rocblas_operation_transpose : rocblas_operation_none,
+                      ta ? rocblas_operation_transpose : rocblas_operation_none, (rocblas_int)N, (rocblas_int)M,
+                      (rocblas_int)Kd, &alpha, B, (rocblas_int)ldb, A, (rocblas_int)lda, &beta, C, (rocblas_int)ldc);
+    if (rs != rocblas_status_success)
+        return fail(GDN2_EHIP, std::string("rocblas_sgemm: ") + rocblas_status_to_string(rs));
+    return GDN2_OK;
+}
+
+}  // namespace gdn2

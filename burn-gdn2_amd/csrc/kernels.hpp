@@ -164,10 +164,11 @@ hipError_t launch_rmsnorm_gate_bwd(const NormBwdParams &p, hipStream_t s);
 hipError_t launch_project_bwd(const ProjectBwdParams &p, hipStream_t s);
 int conv_bwd_blocks(int T, int tblock);
 hipError_t launch_conv_bwd(const ConvBwdParams &p, hipStream_t s);
-// out[j] (+)= sum over rows of A[r, c] for c in [j * group, (j + 1) * group),
-// j < N / group; deterministic (fixed split over rows into `parts`).
-hipError_t launch_colsum(const float *A, int64_t rows, int64_t N, int64_t lda, int group, float *out, bool accumulate,
-                         float *part, int parts, hipStream_t s);
+// out[j] (+)= sum over rows r, f < fold and i < group of
+// A[r, f * (N / fold) + j * group + i], j < N / (group * fold); deterministic
+// (fixed split of the rows into `parts`; part holds parts * N floats).
+hipError_t launch_colsum(const float *A, int64_t rows, int64_t N, int64_t lda, int group, int fold, float *out,
+                         bool accumulate, float *part, int parts, hipStream_t s);
 
 hipError_t launch_scan(const ScanParams &p, hipStream_t s);
 hipError_t launch_decode(const DecodeParams &p, hipStream_t s);

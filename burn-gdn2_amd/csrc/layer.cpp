@@ -21,6 +21,7 @@
 #include <string>
 #include <vector>
 
+#include "blas.hpp"
 #include "common.hpp"
 #include "gdn2_layer.h"
 #include "kernels.hpp"
@@ -159,7 +160,7 @@ struct gdn2_layer {
     gdn2_config cfg;
     Dims d;
     int device = 0;
-    rocblas_handle blas = nullptr;
+    Gemm mm;  // the Linear layers' GEMMs
     // The input-side Linear weights share one [D, ld_in] matrix so that x is
     // read by a single GEMM; column offsets of each block:
     int64_t ld_in = 0, off_q = 0, off_k = 0, off_b = 0, off_v = 0, off_w = 0, off_f0 = 0, off_g0 = 0;
@@ -194,19 +195,6 @@ struct gdn2_state {
 };
 
 namespace {
-
-// Y[M, N] = X[M, Kd] W[Kd, N] (+ beta Y), row-major, through column-major rocBLAS.
-gdn2_status gemm(rocblas_handle h, int64_t M, int64_t N, int64_t Kd, const float *X, int64_t ldx, const float *W,
-                 int64_t ldw, float *Y, int64_t ldy, float beta) {
-    if (M == 0 || N == 0) return GDN2_OK;
-    const float alpha = 1.0f;
-    const rocblas_status st = rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_none, (rocblas_int)N,
-                                            (rocblas_int)M, (rocblas_int)Kd, &alpha, W, (rocblas_int)ldw, X,
-                                            (rocblas_int)ldx, &beta, Y, (rocblas_int)ldy);
-    if (st != rocblas_status_success)
-        return fail(GDN2_EHIP, std::string("rocblas_sgemm: ") + rocblas_status_to_string(st));
-    return GDN2_OK;
-}
 
 struct Work {
     float *Y, *F, *G, *q, *k, *g, *b, *v, *w, *O, *S0;
@@ -270,14 +258,14 @@ gdn2_status workspace(gdn2_layer &L, int64_t B, int64_t T, bool need_s0, Work *w
 // Linear layers of the input side: Y, F, G.
 gdn2_status input_gemms(gdn2_layer &L, const float *x, int64_t M, const Work &wk, hipStream_t s) {
     const Dims &d = L.d;
-    rocblas_status bs = rocblas_set_stream(L.blas, s);
-    if (bs != rocblas_status_success) return fail(GDN2_EHIP, "rocblas_set_stream failed");
     gdn2_status st;
-    if ((st = gemm(L.blas, M, L.ld_in, d.D, x, d.D, L.w_in, L.ld_in, wk.Y, L.ld_in, 0.0f)) != GDN2_OK) return st;
-    if ((st = gemm(L.blas, M, d.kd, d.V, wk.Y + L.off_f0, L.ld_in, L.p[P_F1], d.kd, wk.F, d.kd, 0.0f)) != GDN2_OK)
+    if ((st = L.mm.run(false, false, M, L.ld_in, d.D, x, d.D, L.w_in, L.ld_in, wk.Y, L.ld_in, 0.0f, s)) != GDN2_OK)
+        return st;
+    if ((st = L.mm.run(false, false, M, d.kd, d.V, wk.Y + L.off_f0, L.ld_in, L.p[P_F1], d.kd, wk.F, d.kd, 0.0f, s)) !=
+        GDN2_OK)
         return st;
     GDN2_HIP_CHECK(launch_fill_rows(wk.G, d.vd, L.p[P_G1_BIAS], M, d.vd, s));
-    return gemm(L.blas, M, d.vd, d.V, wk.Y + L.off_g0, L.ld_in, L.p[P_G1], d.vd, wk.G, d.vd, 1.0f);
+    return L.mm.run(false, false, M, d.vd, d.V, wk.Y + L.off_g0, L.ld_in, L.p[P_G1], d.vd, wk.G, d.vd, 1.0f, s);
 }
 
 gdn2_status project_epilogue(gdn2_layer &L, int64_t B, int64_t T, const float *const conv_in[3], const Work &wk,
@@ -322,13 +310,15 @@ gdn2_status recurrence(gdn2_layer &L, int64_t B, int64_t T, int mode, const Work
     return gdn2_recurrent_fwd_f32(&ra, s);
 }
 
-// Gated RMSNorm in place on O, then out = O W_o.
-gdn2_status output_side(gdn2_layer &L, int64_t M, bool norm, const Work &wk, float *out, hipStream_t s) {
+// Gated RMSNorm of wk.O into `normed` (wk.O itself when null), then out = normed W_o.
+gdn2_status output_side(gdn2_layer &L, int64_t M, bool norm, const Work &wk, float *out, hipStream_t s,
+                        float *normed = nullptr) {
     const Dims &d = L.d;
+    float *y = normed ? normed : wk.O;
     if (norm)
-        GDN2_HIP_CHECK(launch_rmsnorm_gate(wk.O, d.vd, wk.O, d.vd, wk.G, d.vd, L.p[P_O_NORM], M, (int)d.HV, (int)d.V,
+        GDN2_HIP_CHECK(launch_rmsnorm_gate(y, d.vd, wk.O, d.vd, wk.G, d.vd, L.p[P_O_NORM], M, (int)d.HV, (int)d.V,
                                            (float)L.cfg.norm_eps, s));
-    return gemm(L.blas, M, d.D, d.vd, wk.O, d.vd, L.p[P_O], d.D, out, d.D, 0.0f);
+    return L.mm.run(false, false, M, d.D, d.vd, y, d.vd, L.p[P_O], d.D, out, d.D, 0.0f, s);
 }
 
 gdn2_status check_layer_call(const gdn2_layer *L, const float *x, int64_t B, int64_t T, const void *out,
@@ -443,7 +433,7 @@ extern "C" void gdn2_layer_destroy(gdn2_layer *L) {
     (void)hipGetDevice(&prev);
     (void)hipSetDevice(L->device);
     (void)hipDeviceSynchronize();
-    if (L->blas) rocblas_destroy_handle(L->blas);
+    L->mm.destroy();
     (void)hipFree(L->w_in);
     for (float *p : L->p) (void)hipFree(p);
     (void)hipFree(L->ws);
@@ -520,8 +510,7 @@ extern "C" gdn2_status gdn2_layer_create(const gdn2_config *c, uint64_t seed, gd
         gdn2_layer_destroy(L);
         return s;
     };
-    if (rocblas_create_handle(&L->blas) != rocblas_status_success)
-        return cleanup(fail(GDN2_EHIP, "gdn2_layer_create: rocblas_create_handle failed"));
+    if ((st = L->mm.init()) != GDN2_OK) return cleanup(st);
     if (hipMalloc(&L->w_in, sizeof(float) * d.D * L->ld_in) != hipSuccess ||
         hipMemset(L->w_in, 0, sizeof(float) * d.D * L->ld_in) != hipSuccess)
         return cleanup(fail(GDN2_EHIP, "gdn2_layer_create: hipMalloc failed"));
@@ -977,25 +966,21 @@ struct gdn2_layer_grads {
     float *p[P_COUNT] = {};  // gradients of the standalone parameters
 };
 
+// What forward_train computes before the norm, kept for the backward instead
+// of recomputing it: Y, F, G, the kernel operands q .. w and the recurrence
+// output O (pre-norm).
+struct gdn2_layer_saved {
+    const gdn2_layer *layer = nullptr;
+    int64_t batch = 0, seq_len = 0;
+    bool filled = false;
+    void *buf = nullptr;
+    Work fw{};
+};
+
 namespace {
 
-constexpr int kColParts = 64;   // row split of the column sums
+constexpr int kColParts = 256;  // row split of the column sums
 constexpr int kConvTBlock = 64; // tokens per thread in the short-conv adjoint
-
-// Row-major C[M, N] = op(A) op(B) (+ beta C), op(A) [M, Kd], op(B) [Kd, N];
-// ta: A is stored [Kd, M]; tb: B is stored [N, Kd].
-gdn2_status gemm_t(rocblas_handle h, bool ta, bool tb, int64_t M, int64_t N, int64_t Kd, const float *A, int64_t lda,
-                   const float *B, int64_t ldb, float *C, int64_t ldc, float beta) {
-    if (M == 0 || N == 0) return GDN2_OK;
-    const float alpha = 1.0f;
-    const rocblas_status st =
-        rocblas_sgemm(h, tb ? rocblas_operation_transpose : rocblas_operation_none,
-                      ta ? rocblas_operation_transpose : rocblas_operation_none, (rocblas_int)N, (rocblas_int)M,
-                      (rocblas_int)Kd, &alpha, B, (rocblas_int)ldb, A, (rocblas_int)lda, &beta, C, (rocblas_int)ldc);
-    if (st != rocblas_status_success)
-        return fail(GDN2_EHIP, std::string("rocblas_sgemm: ") + rocblas_status_to_string(st));
-    return GDN2_OK;
-}
 
 struct BwdWork {
     Work fw;                      // the forward's buffers (Y, F, G, q .. w, O) and the chunk workspace
@@ -1011,7 +996,7 @@ struct BwdWork {
     float *part;                  // column-sum partials
 };
 
-gdn2_status bwd_workspace(gdn2_layer &L, int64_t B, int64_t T, BwdWork *bw) {
+gdn2_status bwd_workspace(gdn2_layer &L, int64_t B, int64_t T, bool recompute, BwdWork *bw) {
     const Dims &d = L.d;
     const int64_t M = B * T;
     const bool sc = L.cfg.use_short_conv != 0, md = L.cfg.has_min_decay != 0;
@@ -1023,14 +1008,15 @@ gdn2_status bwd_workspace(gdn2_layer &L, int64_t B, int64_t T, BwdWork *bw) {
     const size_t chunk_bytes = std::max(gdn2_chunk_workspace_bytes(&ca), gdn2_chunk_bwd_workspace_bytes(&ba));
     const size_t f = sizeof(float), nS = f * B * d.HV * d.K * d.V;
     const size_t nk = f * M * d.kd, nv = f * M * d.vd, nY = f * M * L.ld_in;
+    const size_t rk = recompute ? nk : 0, rv = recompute ? nv : 0;  // the forward's buffers, when recomputed
     const int64_t part_cols = std::max<int64_t>(std::max(d.kd, d.vd), 4 * ctot);
     struct Slot {
         float **ptr;
         size_t bytes;
     } slots[] = {
-        {&bw->fw.Y, nY}, {&bw->fw.F, nk}, {&bw->fw.G, nv}, {&bw->fw.q, nk}, {&bw->fw.k, nk}, {&bw->fw.g, nk},
-        {&bw->fw.b, nk}, {&bw->fw.v, nv}, {&bw->fw.w, nv}, {&bw->fw.O, nv},
-        {&bw->S0, nS}, {&bw->Sf, nS}, {&bw->dS0, nS},
+        {&bw->fw.Y, recompute ? nY : 0}, {&bw->fw.F, rk}, {&bw->fw.G, rv}, {&bw->fw.q, rk}, {&bw->fw.k, rk},
+        {&bw->fw.g, rk}, {&bw->fw.b, rk}, {&bw->fw.v, rv}, {&bw->fw.w, rv}, {&bw->fw.O, rv},
+        {&bw->S0, nS}, {&bw->Sf, recompute ? nS : 0}, {&bw->dS0, nS},
         {&bw->y, nv}, {&bw->dy, nv}, {&bw->dO, nv}, {&bw->dG, nv},
         {&bw->dq, nk}, {&bw->dk, nk}, {&bw->dg, nk}, {&bw->db, nk}, {&bw->dv, nv}, {&bw->dw, nv},
         {&bw->dY, nY}, {&bw->DU, sc ? f * M * ctot : 0}, {&bw->dF, nk}, {&bw->PA, nk}, {&bw->PD, md ? nk : 0},
@@ -1067,6 +1053,70 @@ gdn2_status check_state_arg(const gdn2_layer *L, const gdn2_state *S, int64_t B,
 }
 
 }  // namespace
+
+extern "C" void gdn2_layer_saved_destroy(gdn2_layer_saved *A) {
+    if (!A) return;
+    (void)hipDeviceSynchronize();
+    (void)hipFree(A->buf);
+    delete A;
+}
+
+extern "C" gdn2_status gdn2_layer_saved_create(const gdn2_layer *L, int64_t B, int64_t T, gdn2_layer_saved **out) {
+    if (!L || !out) return fail(GDN2_EINVAL, "gdn2_layer_saved_create: null argument");
+    *out = nullptr;
+    if (B <= 0 || T < 0 || B * T > INT32_MAX / 4)
+        return fail(GDN2_EINVAL, "gdn2_layer_saved_create: batch must be > 0, seq_len >= 0, batch * seq_len bounded");
+    const Dims &d = L->d;
+    const size_t M = (size_t)(B * T), f = sizeof(float);
+    const size_t sz[10] = {f * M * L->ld_in, f * M * d.kd, f * M * d.vd, f * M * d.kd, f * M * d.kd,
+                           f * M * d.kd,     f * M * d.kd, f * M * d.vd, f * M * d.vd, f * M * d.vd};
+    size_t total = 0;
+    for (size_t v : sz) total += align256(v);
+    gdn2_layer_saved *A = new gdn2_layer_saved();
+    A->layer = L;
+    A->batch = B;
+    A->seq_len = T;
+    if (total && hipMalloc(&A->buf, total) != hipSuccess) {
+        delete A;
+        return fail(GDN2_EHIP, "gdn2_layer_saved_create: device allocation failed");
+    }
+    char *base = static_cast<char *>(A->buf);
+    float **dst[10] = {&A->fw.Y, &A->fw.F, &A->fw.G, &A->fw.q, &A->fw.k, &A->fw.g, &A->fw.b, &A->fw.v, &A->fw.w, &A->fw.O};
+    for (int i = 0; i < 10; ++i) {
+        *dst[i] = reinterpret_cast<float *>(base);
+        base += align256(sz[i]);
+    }
+    *out = A;
+    return GDN2_OK;
+}
+
+extern "C" gdn2_status gdn2_layer_forward_train_saved_f32(gdn2_layer *L, const float *x, int64_t B, int64_t T,
+                                                          float *out, gdn2_layer_saved *A, gdn2_stream_t stream) {
+    gdn2_status st = check_layer_call(L, x, B, T, out, "gdn2_layer_forward_train_saved_f32");
+    if (st != GDN2_OK) return st;
+    if (!A || A->layer != L || A->batch != B || A->seq_len != T)
+        return fail(GDN2_EINVAL, "gdn2_layer_forward_train_saved_f32: saved missing or made for another layer or shape");
+    A->filled = false;
+    if (T == 0) {
+        A->filled = true;
+        return GDN2_OK;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    Work wk{};
+    if ((st = workspace(*L, B, T, true, &wk)) != GDN2_OK) return st;
+    Work sv = A->fw;
+    sv.chunk = wk.chunk;
+    sv.chunk_bytes = wk.chunk_bytes;
+    sv.S0 = wk.S0;
+    const int64_t M = B * T;
+    if ((st = input_gemms(*L, x, M, sv, s)) != GDN2_OK) return st;
+    if ((st = project_epilogue(*L, B, T, nullptr, sv, s)) != GDN2_OK) return st;
+    GDN2_HIP_CHECK(launch_fill_rows(wk.S0, 0, nullptr, 1, B * L->d.HV * L->d.K * L->d.V, s));
+    if ((st = recurrence(*L, B, T, L->cfg.mode, sv, wk.S0, s)) != GDN2_OK) return st;
+    if ((st = output_side(*L, M, true, sv, out, s, wk.O)) != GDN2_OK) return st;  // O stays pre-norm
+    A->filled = true;
+    return GDN2_OK;
+}
 
 extern "C" void gdn2_layer_grads_destroy(gdn2_layer_grads *G) {
     if (!G) return;
@@ -1129,7 +1179,8 @@ extern "C" gdn2_status gdn2_layer_grads_get(const gdn2_layer_grads *G, const cha
 }
 
 extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, int64_t B, int64_t T,
-                                               const gdn2_state *state_in, const float *d_out,
+                                               const gdn2_state *state_in, const gdn2_layer_saved *saved,
+                                               const float *d_out,
                                                const gdn2_state *d_state, float *dx, gdn2_state *d_state_in,
                                                gdn2_layer_grads *G, int accumulate, gdn2_stream_t stream) {
     const char *who = "gdn2_layer_backward_f32";
@@ -1141,6 +1192,10 @@ extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, in
     if ((st = check_state_arg(L, d_state_in, B, "d_state_in")) != GDN2_OK) return st;
     if (d_state_in && (d_state_in == state_in || d_state_in == d_state))
         return fail(GDN2_EINVAL, "gdn2_layer_backward_f32: d_state_in must be a state of its own");
+    if (saved && (saved->layer != L || saved->batch != B || saved->seq_len != T || !saved->filled))
+        return fail(GDN2_EINVAL, "gdn2_layer_backward_f32: saved made for another layer or shape, or never filled");
+    if (saved && state_in && state_in->some)
+        return fail(GDN2_EINVAL, "gdn2_layer_backward_f32: saved activations come from forward_train (no state_in)");
     const Dims &d = L->d;
     if (!chunk_supported((int)d.K, (int)d.V))
         return fail(GDN2_NOT_APPLICABLE, "gdn2_layer_backward_f32: needs head_dim in {64, 128} and head_v_dim in "
@@ -1180,36 +1235,44 @@ extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, in
     }
 
     BwdWork bw{};
-    if ((st = bwd_workspace(*L, B, T, &bw)) != GDN2_OK) return st;
+    if ((st = bwd_workspace(*L, B, T, saved == nullptr, &bw)) != GDN2_OK) return st;
+    if (saved) {  // the forward's buffers come from forward_train_saved
+        void *chunk = bw.fw.chunk;
+        const size_t chunk_bytes = bw.fw.chunk_bytes;
+        bw.fw = saved->fw;
+        bw.fw.chunk = chunk;
+        bw.fw.chunk_bytes = chunk_bytes;
+    }
     const Work &fw = bw.fw;
     const float *conv_in[3] = {};
     if (has_state)
         for (int i = 0; i < 3; ++i) conv_in[i] = state_in->conv[state_in->cur][i];
-
-    // forward recomputation up to the recurrence output O
-    if ((st = input_gemms(*L, x, M, fw, s)) != GDN2_OK) return st;
-    if ((st = project_epilogue(*L, B, T, has_state ? conv_in : nullptr, fw, s)) != GDN2_OK) return st;
     if (has_state)
         GDN2_HIP_CHECK(hipMemcpyAsync(bw.S0, state_in->S, sizeof(float) * nS, hipMemcpyDeviceToDevice, s));
     else
         GDN2_HIP_CHECK(launch_fill_rows(bw.S0, 0, nullptr, 1, nS, s));
-    GDN2_HIP_CHECK(hipMemcpyAsync(bw.Sf, bw.S0, sizeof(float) * nS, hipMemcpyDeviceToDevice, s));
-    gdn2_chunk_args ca = chunk_args_for(*L, B, T, fw, bw.Sf);
-    ca.workspace = fw.chunk;
-    ca.workspace_bytes = fw.chunk_bytes;
-    if ((st = gdn2_chunk_fwd_f32(&ca, s)) != GDN2_OK) return st;
+
+    if (!saved) {  // forward recomputation up to the recurrence output O
+        if ((st = input_gemms(*L, x, M, fw, s)) != GDN2_OK) return st;
+        if ((st = project_epilogue(*L, B, T, has_state ? conv_in : nullptr, fw, s)) != GDN2_OK) return st;
+        GDN2_HIP_CHECK(hipMemcpyAsync(bw.Sf, bw.S0, sizeof(float) * nS, hipMemcpyDeviceToDevice, s));
+        gdn2_chunk_args ca = chunk_args_for(*L, B, T, fw, bw.Sf);
+        ca.workspace = fw.chunk;
+        ca.workspace_bytes = fw.chunk_bytes;
+        if ((st = gdn2_chunk_fwd_f32(&ca, s)) != GDN2_OK) return st;
+    }
 
     // o_proj and the gated RMSNorm
-    if ((st = gemm_t(L->blas, false, true, M, d.vd, d.D, d_out, d.D, L->p[P_O], d.D, bw.dy, d.vd, 0.0f)) != GDN2_OK)
+    if ((st = L->mm.run(false, true, M, d.vd, d.D, d_out, d.D, L->p[P_O], d.D, bw.dy, d.vd, 0.0f, s)) != GDN2_OK)
         return st;
     NormBwdParams np{};
     np.O = fw.O; np.G = fw.G; np.weight = L->p[P_O_NORM];
     np.dy = bw.dy; np.y = bw.y; np.dO = bw.dO; np.dG = bw.dG;
     np.rows = M * d.HV; np.V = (int)d.V; np.eps = (float)L->cfg.norm_eps;
     GDN2_HIP_CHECK(launch_rmsnorm_gate_bwd(np, s));
-    if ((st = gemm_t(L->blas, true, false, d.vd, d.D, M, bw.y, d.vd, d_out, d.D, G->p[P_O], d.D, beta)) != GDN2_OK)
+    if ((st = L->mm.run(true, false, d.vd, d.D, M, bw.y, d.vd, d_out, d.D, G->p[P_O], d.D, beta, s)) != GDN2_OK)
         return st;
-    GDN2_HIP_CHECK(launch_colsum(bw.dy, M * d.HV, d.V, d.V, 1, G->p[P_O_NORM], accumulate, bw.part, kColParts, s));
+    GDN2_HIP_CHECK(launch_colsum(bw.dy, M, d.vd, d.vd, 1, (int)d.HV, G->p[P_O_NORM], accumulate, bw.part, kColParts, s));
 
     // the recurrence
     gdn2_chunk_bwd_args ba{};
@@ -1257,10 +1320,10 @@ extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, in
         cp.B = (int)B; cp.T = (int)T; cp.kd = (int)d.kd; cp.vd = (int)d.vd; cp.tblock = kConvTBlock;
         GDN2_HIP_CHECK(launch_conv_bwd(cp, s));
         const int64_t parts = B * conv_bwd_blocks((int)T, kConvTBlock), ld = 4 * (2 * d.kd + d.vd);
-        GDN2_HIP_CHECK(launch_colsum(bw.wpart, parts, 4 * d.kd, ld, 1, G->p[P_QCONV], accumulate, bw.part, kColParts, s));
-        GDN2_HIP_CHECK(launch_colsum(bw.wpart + 4 * d.kd, parts, 4 * d.kd, ld, 1, G->p[P_KCONV], accumulate, bw.part,
+        GDN2_HIP_CHECK(launch_colsum(bw.wpart, parts, 4 * d.kd, ld, 1, 1, G->p[P_QCONV], accumulate, bw.part, kColParts, s));
+        GDN2_HIP_CHECK(launch_colsum(bw.wpart + 4 * d.kd, parts, 4 * d.kd, ld, 1, 1, G->p[P_KCONV], accumulate, bw.part,
                                      kColParts, s));
-        GDN2_HIP_CHECK(launch_colsum(bw.wpart + 8 * d.kd, parts, 4 * d.vd, ld, 1, G->p[P_VCONV], accumulate, bw.part,
+        GDN2_HIP_CHECK(launch_colsum(bw.wpart + 8 * d.kd, parts, 4 * d.vd, ld, 1, 1, G->p[P_VCONV], accumulate, bw.part,
                                      kColParts, s));
         if (d_state_in && !has_state && (st = pass_caches(false)) != GDN2_OK) return st;
     } else {
@@ -1279,27 +1342,27 @@ extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, in
 
     // gates: f_proj_1, g_proj_1 (+ bias), dt_bias, A_log, decay_factors
     const float *Yf0 = fw.Y + L->off_f0, *Yg0 = fw.Y + L->off_g0;
-    if ((st = gemm_t(L->blas, false, true, M, d.V, d.kd, bw.dF, d.kd, L->p[P_F1], d.kd, bw.dY + L->off_f0, L->ld_in,
-                     0.0f)) != GDN2_OK)
+    if ((st = L->mm.run(false, true, M, d.V, d.kd, bw.dF, d.kd, L->p[P_F1], d.kd, bw.dY + L->off_f0, L->ld_in,
+                     0.0f, s)) != GDN2_OK)
         return st;
-    if ((st = gemm_t(L->blas, true, false, d.V, d.kd, M, Yf0, L->ld_in, bw.dF, d.kd, G->p[P_F1], d.kd, beta)) != GDN2_OK)
+    if ((st = L->mm.run(true, false, d.V, d.kd, M, Yf0, L->ld_in, bw.dF, d.kd, G->p[P_F1], d.kd, beta, s)) != GDN2_OK)
         return st;
-    if ((st = gemm_t(L->blas, false, true, M, d.V, d.vd, bw.dG, d.vd, L->p[P_G1], d.vd, bw.dY + L->off_g0, L->ld_in,
-                     0.0f)) != GDN2_OK)
+    if ((st = L->mm.run(false, true, M, d.V, d.vd, bw.dG, d.vd, L->p[P_G1], d.vd, bw.dY + L->off_g0, L->ld_in,
+                     0.0f, s)) != GDN2_OK)
         return st;
-    if ((st = gemm_t(L->blas, true, false, d.V, d.vd, M, Yg0, L->ld_in, bw.dG, d.vd, G->p[P_G1], d.vd, beta)) != GDN2_OK)
+    if ((st = L->mm.run(true, false, d.V, d.vd, M, Yg0, L->ld_in, bw.dG, d.vd, G->p[P_G1], d.vd, beta, s)) != GDN2_OK)
         return st;
-    GDN2_HIP_CHECK(launch_colsum(bw.dG, M, d.vd, d.vd, 1, G->p[P_G1_BIAS], accumulate, bw.part, kColParts, s));
-    GDN2_HIP_CHECK(launch_colsum(bw.dF, M, d.kd, d.kd, 1, G->p[P_DT_BIAS], accumulate, bw.part, kColParts, s));
-    GDN2_HIP_CHECK(launch_colsum(bw.PA, M, d.kd, d.kd, (int)d.K, G->p[P_A_LOG], accumulate, bw.part, kColParts, s));
-    if (md) GDN2_HIP_CHECK(launch_colsum(bw.PD, M, d.kd, d.kd, 1, G->p[P_DECAY], accumulate, bw.part, kColParts, s));
+    GDN2_HIP_CHECK(launch_colsum(bw.dG, M, d.vd, d.vd, 1, 1, G->p[P_G1_BIAS], accumulate, bw.part, kColParts, s));
+    GDN2_HIP_CHECK(launch_colsum(bw.dF, M, d.kd, d.kd, 1, 1, G->p[P_DT_BIAS], accumulate, bw.part, kColParts, s));
+    GDN2_HIP_CHECK(launch_colsum(bw.PA, M, d.kd, d.kd, (int)d.K, 1, G->p[P_A_LOG], accumulate, bw.part, kColParts, s));
+    if (md) GDN2_HIP_CHECK(launch_colsum(bw.PD, M, d.kd, d.kd, 1, 1, G->p[P_DECAY], accumulate, bw.part, kColParts, s));
 
     // the input Linear layers
-    if ((st = gemm_t(L->blas, true, false, d.D, L->ld_in, M, x, d.D, bw.dY, L->ld_in, G->g_in, L->ld_in, beta)) !=
+    if ((st = L->mm.run(true, false, d.D, L->ld_in, M, x, d.D, bw.dY, L->ld_in, G->g_in, L->ld_in, beta, s)) !=
         GDN2_OK)
         return st;
-    if (dx && (st = gemm_t(L->blas, false, true, M, d.D, L->ld_in, bw.dY, L->ld_in, L->w_in, L->ld_in, dx, d.D,
-                           0.0f)) != GDN2_OK)
+    if (dx && (st = L->mm.run(false, true, M, d.D, L->ld_in, bw.dY, L->ld_in, L->w_in, L->ld_in, dx, d.D,
+                           0.0f, s)) != GDN2_OK)
         return st;
     if (d_state_in) d_state_in->some = true;
     return GDN2_OK;

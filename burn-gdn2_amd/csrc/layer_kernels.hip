@@ -371,25 +371,43 @@ __global__ __launch_bounds__(256) void conv_bwd_kernel(ConvBwdParams p) {
 }
 
 // Column sums in two deterministic steps: partial sums over `parts` row
-// ranges, then the sum of the parts (and of `group` adjacent columns).
+// ranges (one thread per column), then one workgroup per output summing the
+// parts, `fold` strided column blocks and `group` adjacent columns.
 __global__ __launch_bounds__(256) void colsum_part_kernel(const float *A, int64_t rows, int64_t N, int64_t lda,
                                                           int64_t rows_per, float *part) {
     const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (c >= N) return;
     const int64_t r0 = (int64_t)blockIdx.y * rows_per, r1 = min(rows, r0 + rows_per);
-    float acc = 0.f;
-    for (int64_t r = r0; r < r1; ++r) acc += A[r * lda + c];
-    part[(int64_t)blockIdx.y * N + c] = acc;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    int64_t r = r0;
+    for (; r + 4 <= r1; r += 4) {
+        a0 += A[r * lda + c];
+        a1 += A[(r + 1) * lda + c];
+        a2 += A[(r + 2) * lda + c];
+        a3 += A[(r + 3) * lda + c];
+    }
+    for (; r < r1; ++r) a0 += A[r * lda + c];
+    part[(int64_t)blockIdx.y * N + c] = (a0 + a1) + (a2 + a3);
 }
 
 __global__ __launch_bounds__(256) void colsum_final_kernel(const float *part, int parts, int64_t N, int group,
-                                                           float *out, int accumulate) {
-    const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (j >= N / group) return;
+                                                           int fold, float *out, int accumulate) {
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t stride = N / fold, j = blockIdx.x;
+    const int64_t terms = (int64_t)parts * fold * group;
     float acc = 0.f;
-    for (int r = 0; r < parts; ++r)
-        for (int i = 0; i < group; ++i) acc += part[(int64_t)r * N + j * group + i];
-    out[j] = accumulate ? out[j] + acc : acc;
+    for (int64_t e = tid; e < terms; e += 256) {
+        const int64_t i = e % group, f = (e / group) % fold, r = e / ((int64_t)group * fold);
+        acc += part[r * N + f * stride + j * group + i];
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) red[wave] = acc;
+    __syncthreads();
+    if (tid == 0) {
+        const float t = (red[0] + red[1]) + (red[2] + red[3]);
+        out[j] = accumulate ? out[j] + t : t;
+    }
 }
 
 int grid_for(int64_t n) {
@@ -458,8 +476,8 @@ hipError_t launch_conv_bwd(const ConvBwdParams &p, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_colsum(const float *A, int64_t rows, int64_t N, int64_t lda, int group, float *out, bool accumulate,
-                         float *part, int parts, hipStream_t s) {
+hipError_t launch_colsum(const float *A, int64_t rows, int64_t N, int64_t lda, int group, int fold, float *out,
+                         bool accumulate, float *part, int parts, hipStream_t s) {
     if (N == 0) return hipSuccess;
     if (parts < 1) parts = 1;
     const int64_t rows_per = rows > 0 ? (rows + parts - 1) / parts : 0;
@@ -467,9 +485,9 @@ hipError_t launch_colsum(const float *A, int64_t rows, int64_t N, int64_t lda, i
                        rows, N, lda, rows_per, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int64_t nout = N / group;
-    hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((nout + 255) / 256)), dim3(256), 0, s, part, parts, N,
-                       group, out, accumulate ? 1 : 0);
+    const int64_t nout = N / ((int64_t)group * fold);
+    hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)nout), dim3(256), 0, s, part, parts, N, group, fold, out,
+                       accumulate ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -99,7 +99,8 @@ EXPORTS = ("gdn2_last_error", "gdn2_hip_available", "gdn2_recurrent_step_f32", "
            "gdn2_state_set_zeros", "gdn2_state_clear", "gdn2_state_is_some", "gdn2_state_batch",
            "gdn2_state_numel", "gdn2_state_tensor", "gdn2_state_read", "gdn2_state_write", "gdn2_state_serialize",
            "gdn2_state_deserialize", "gdn2_layer_grads_create", "gdn2_layer_grads_destroy",
-           "gdn2_layer_grads_zero", "gdn2_layer_grads_get", "gdn2_layer_backward_f32")
+           "gdn2_layer_grads_zero", "gdn2_layer_grads_get", "gdn2_layer_backward_f32",
+           "gdn2_layer_saved_create", "gdn2_layer_saved_destroy", "gdn2_layer_forward_train_saved_f32")
 
 _lib = None
 
@@ -171,7 +172,10 @@ def _declare_layer(L):
         "gdn2_layer_grads_destroy": (None, [vp]),
         "gdn2_layer_grads_zero": (i32, [vp, vp]),
         "gdn2_layer_grads_get": (i32, [vp, ctypes.c_char_p, fp, i64]),
-        "gdn2_layer_backward_f32": (i32, [vp, fp, i64, i64, vp, fp, vp, fp, vp, vp, i32, vp]),
+        "gdn2_layer_backward_f32": (i32, [vp, fp, i64, i64, vp, vp, fp, vp, fp, vp, vp, i32, vp]),
+        "gdn2_layer_saved_create": (i32, [vp, i64, i64, ctypes.POINTER(vp)]),
+        "gdn2_layer_saved_destroy": (None, [vp]),
+        "gdn2_layer_forward_train_saved_f32": (i32, [vp, fp, i64, i64, fp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

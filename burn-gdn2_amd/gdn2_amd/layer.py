@@ -262,6 +262,29 @@ class Gdn2Grads:
         return {n: self.get(n) for n in param_names()}
 
 
+class Gdn2Saved:
+    """Activations kept by forward_train for the backward (one object per
+    batch and sequence length; see GatedDeltaNet2.forward_train)."""
+
+    def __init__(self, layer: "GatedDeltaNet2", batch: int, seq_len: int):
+        self._layer = layer
+        h = ctypes.c_void_p()
+        C.check(C.lib().gdn2_layer_saved_create(layer._h, int(batch), int(seq_len), ctypes.byref(h)))
+        self._h = h
+        self.shape = (int(batch), int(seq_len))
+
+    def close(self):
+        if getattr(self, "_h", None):
+            C.lib().gdn2_layer_saved_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def _forward_train_fn():
     import torch
 
@@ -270,7 +293,8 @@ def _forward_train_fn():
         def forward(ctx, x, layer):
             ctx.layer = layer
             ctx.save_for_backward(x)
-            return layer.forward_train(x)
+            ctx.acts = Gdn2Saved(layer, x.shape[0], x.shape[1])
+            return layer.forward_train(x, saved=ctx.acts)
 
         @staticmethod
         def backward(ctx, d_out):
@@ -278,7 +302,8 @@ def _forward_train_fn():
             layer = ctx.layer
             if layer.grads is None:
                 layer.grads = Gdn2Grads(layer)
-            dx, _, _ = layer.backward(x, d_out, grads=layer.grads, accumulate=True)
+            dx, _, _ = layer.backward(x, d_out, saved=ctx.acts, grads=layer.grads, accumulate=True)
+            ctx.acts.close()
             return dx, None
 
     return _ForwardTrain
@@ -345,14 +370,20 @@ class GatedDeltaNet2:
                              f"but got {x.shape[2]}. Check that the model hidden_size matches your input.")
         return x.contiguous()
 
-    def forward_train(self, x):
-        """forward_train (src/module.rs:326-375): [B, T, D] -> [B, T, D]."""
+    def forward_train(self, x, saved: Optional["Gdn2Saved"] = None):
+        """forward_train (src/module.rs:326-375): [B, T, D] -> [B, T, D].
+        With `saved` (a Gdn2Saved of x's batch and length) the activations
+        the backward needs are kept in it."""
         import torch
 
         x = self._check_x(x)
         out = torch.empty_like(x)
-        C.check(C.lib().gdn2_layer_forward_train_f32(self._h, x.data_ptr(), x.shape[0], x.shape[1], out.data_ptr(),
-                                                     _stream()))
+        if saved is None:
+            C.check(C.lib().gdn2_layer_forward_train_f32(self._h, x.data_ptr(), x.shape[0], x.shape[1],
+                                                         out.data_ptr(), _stream()))
+        else:
+            C.check(C.lib().gdn2_layer_forward_train_saved_f32(self._h, x.data_ptr(), x.shape[0], x.shape[1],
+                                                               out.data_ptr(), saved._h, _stream()))
         return out
 
     def forward(self, x, state: Optional[Gdn2State] = None):
@@ -389,10 +420,11 @@ class GatedDeltaNet2:
     # -- backward -----------------------------------------------------------
     def backward(self, x, d_out, state: Optional[Gdn2State] = None, d_state: Optional[Gdn2State] = None,
                  grads: Optional[Gdn2Grads] = None, accumulate: bool = False, want_dx: bool = True,
-                 want_d_state: bool = False):
+                 want_d_state: bool = False, saved: Optional[Gdn2Saved] = None):
         """Gradients of <d_out, out> + <d_state, state after the call> for
         forward(x, state) (state None or empty: forward_train).  `state` is
-        the state BEFORE that call and is not modified.  Returns
+        the state BEFORE that call and is not modified; `saved`, filled by
+        forward_train(x, saved=...), replaces the recomputation.  Returns
         (dx or None, grads, d_state_in or None); parameter gradients go into
         `grads` (a new Gdn2Grads when None), added to it with accumulate."""
         import torch
@@ -407,7 +439,8 @@ class GatedDeltaNet2:
         dx = torch.empty_like(x) if want_dx else None
         d_state_in = Gdn2State(self, B) if want_d_state else None
         C.check(C.lib().gdn2_layer_backward_f32(
-            self._h, x.data_ptr(), B, T, state._h if state is not None else None, d_out.data_ptr(),
+            self._h, x.data_ptr(), B, T, state._h if state is not None else None,
+            saved._h if saved is not None else None, d_out.data_ptr(),
             d_state._h if d_state is not None else None, dx.data_ptr() if dx is not None else None,
             d_state_in._h if d_state_in is not None else None, grads._h, int(bool(accumulate)), _stream()))
         return dx, grads, d_state_in

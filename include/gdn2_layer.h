@@ -144,7 +144,8 @@ GDN2_API gdn2_status gdn2_layer_project_f32(gdn2_layer *layer, const float *x, i
  * (tests/autodiff.rs:153-205: gradients of every parameter, through
  * forward_train in both modes and through token-by-token forward calls with
  * a state).  Here the backward is an explicit call that recomputes the
- * forward from x and returns the same gradients.
+ * forward from x (or takes it from saved activations) and returns the same
+ * gradients.
  * ---------------------------------------------------------------------- */
 typedef struct gdn2_layer_grads gdn2_layer_grads;
 
@@ -158,11 +159,28 @@ GDN2_API gdn2_status gdn2_layer_grads_zero(gdn2_layer_grads *grads, gdn2_stream_
 GDN2_API gdn2_status gdn2_layer_grads_get(const gdn2_layer_grads *grads, const char *name, float *host,
                                           int64_t numel);
 
+/* Activations kept from forward_train for the backward (what the forward
+ * computes before the norm: the Linear outputs, the kernel operands and the
+ * recurrence output; about 4 * B * T * (D_in + 8 kd + 4 vd) bytes with
+ * D_in ~ 3 kd + 2 vd + 2 V), so that the backward need not recompute them.
+ * One object per (batch, seq_len); reusable. */
+typedef struct gdn2_layer_saved gdn2_layer_saved;
+GDN2_API gdn2_status gdn2_layer_saved_create(const gdn2_layer *layer, int64_t batch, int64_t seq_len,
+                                             gdn2_layer_saved **out);
+GDN2_API void gdn2_layer_saved_destroy(gdn2_layer_saved *saved);
+/* gdn2_layer_forward_train_f32 that also fills `saved`. */
+GDN2_API gdn2_status gdn2_layer_forward_train_saved_f32(gdn2_layer *layer, const float *x, int64_t batch,
+                                                        int64_t seq_len, float *out, gdn2_layer_saved *saved,
+                                                        gdn2_stream_t stream);
+
 /* The gradients of L = <d_out, out> + <d_state, state after the call> for
  * gdn2_layer_forward_f32(x, state_in) -- and for forward_train when state_in
  * is NULL or empty (Option::None: S0 = 0, the first token pads the conv).
  *   x, d_out     [B, T, D]
  *   state_in     the state before the call (read only), NULL or empty = None
+ *   saved        NULL: the forward is recomputed from x; else filled by
+ *                gdn2_layer_forward_train_saved_f32 on this x (state_in must
+ *                then be NULL or empty)
  *   d_state      NULL or empty = zero; else the gradient of the state after
  *                the call (recurrent and conv caches)
  *   dx           [B, T, D], or NULL
@@ -180,7 +198,8 @@ GDN2_API gdn2_status gdn2_layer_grads_get(const gdn2_layer_grads *grads, const c
  * Limits (else GDN2_NOT_APPLICABLE): head_dim in {64, 128}, head_v_dim in
  * {64, 128, 256}. */
 GDN2_API gdn2_status gdn2_layer_backward_f32(gdn2_layer *layer, const float *x, int64_t batch, int64_t seq_len,
-                                             const gdn2_state *state_in, const float *d_out,
+                                             const gdn2_state *state_in, const gdn2_layer_saved *saved,
+                                             const float *d_out,
                                              const gdn2_state *d_state, float *dx, gdn2_state *d_state_in,
                                              gdn2_layer_grads *grads, int accumulate, gdn2_stream_t stream);
 

@@ -177,3 +177,29 @@ def test_backward_rejects_unsupported_shapes(gpu):
     with pytest.raises(G._capi.Gdn2Error) as e:
         layer.backward(x, x)
     assert e.value.status == G._capi.GDN2_NOT_APPLICABLE
+
+
+def test_saved_activations_equal_recompute(gpu):
+    """forward_train with saved activations gives the same output as without,
+    and the backward from them equals the recomputing backward bit for bit
+    (both run the chunked kernels on the same operands)."""
+    import torch
+
+    G, cfg, layer, W = _setup(gpu, dict(SMALL, min_decay=0.9, allow_neg_eigval=True))
+    rng = np.random.default_rng(12)
+    B, T = 2, 130
+    x = torch.from_numpy(rng.standard_normal((B, T, cfg.hidden_size)).astype(np.float32)).to(gpu)
+    d = torch.from_numpy(rng.standard_normal((B, T, cfg.hidden_size)).astype(np.float32)).to(gpu)
+    saved = G.Gdn2Saved(layer, B, T)
+    out_s = layer.forward_train(x, saved=saved)
+    out_r = layer.forward_train(x)
+    assert torch.equal(out_s, out_r)
+    dx_s, g_s, _ = layer.backward(x, d, saved=saved)
+    dx_r, g_r, _ = layer.backward(x, d)
+    assert torch.equal(dx_s, dx_r)
+    for n in O.WEIGHT_NAMES:
+        a, b = g_s.get(n), g_r.get(n)
+        if b is not None:
+            np.testing.assert_array_equal(a, b, err_msg=n)
+    with pytest.raises(G._capi.Gdn2Error):  # shape mismatch
+        layer.backward(x[:, :64].contiguous(), d[:, :64].contiguous(), saved=saved)
