@@ -48,6 +48,34 @@ def _strides3(t: torch.Tensor):
     return t.stride(0), t.stride(1), t.stride(2)
 
 
+def _channels_contiguous(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(3) == 1 or t.shape[3] == 1 else t.contiguous()
+
+
+def _like(t: torch.Tensor, ref: torch.Tensor) -> torch.Tensor:
+    """t in ref's shape and layout: a last dim of 1 (per-head scalar g or b,
+    src/forward.rs:149,173,180-182) is broadcast over ref's channels, and a
+    different layout is copied on the device into ref's."""
+    if t.shape == ref.shape and t.stride() == ref.stride():
+        return t
+    out = torch.empty_strided(ref.shape, ref.stride(), device=ref.device, dtype=torch.float32)
+    out.copy_(t.expand(ref.shape))
+    return out
+
+
+def _operands(q, k, v, g, b, w):
+    """The kernels read q, k, g, b in one layout and v, w in another, each
+    with contiguous channels; other inputs are brought to that form."""
+    q, v = _channels_contiguous(q), _channels_contiguous(v)
+    return q, _like(k, q), v, _like(g, q), _like(b, q), _like(w, v)
+
+
+def _reduce_like(grad: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
+    """The gradient of an operand broadcast by _like: summed over the
+    broadcast channels."""
+    return grad.sum(dim=3, keepdim=True) if t.shape[3] == 1 and grad.shape[3] != 1 else grad
+
+
 def hip_available() -> bool:
     return bool(C.lib().gdn2_hip_available())
 
@@ -60,6 +88,7 @@ def fused_step(q, k, v, g, b, w, state, scale: float, out_state=None) -> Optiona
     HV, V = v.shape[1], v.shape[3]
     if T != 1:
         raise ValueError("fused_step takes one token")
+    q, k, v, g, b, w = _operands(q, k, v, g, b, w)
     state = state.contiguous()
     new_state = torch.empty_like(state) if out_state is None else out_state
     out = torch.empty((B, HV, 1, V), device=q.device, dtype=torch.float32)
@@ -77,8 +106,10 @@ def fused_step(q, k, v, g, b, w, state, scale: float, out_state=None) -> Optiona
 
 
 def fused_recurrent_forward(q, k, v, g, b, w, state, scale: float, out=None, in_place=False):
-    """Per-token scan over T tokens in one launch.  Returns (out, new_state)."""
+    """Per-token scan over T tokens in one launch.  Returns (out, new_state).
+    g and b may have a last dim of 1 (one value per head and token)."""
     _check_f32_cuda(q, k, v, g, b, w, state)
+    q, k, v, g, b, w = _operands(q, k, v, g, b, w)
     B, Hk, T, K = q.shape
     HV, V = v.shape[1], v.shape[3]
     state = state.contiguous()
@@ -123,8 +154,10 @@ def chunk_wy_forward(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64
                      in_place=False):
     """Chunked forward over the whole sequence.  Returns (out, new_state),
     or None when the chunk kernels do not apply (K, V or chunk size outside
-    their limits)."""
+    their limits).  g and b may have a last dim of 1 (one value per head and
+    token), as in the reference."""
     _check_f32_cuda(q, k, v, g, b, w, state)
+    q, k, v, g, b, w = _operands(q, k, v, g, b, w)
     B, Hk, T, K = q.shape
     HV, V = v.shape[1], v.shape[3]
     st = state.contiguous()
@@ -149,17 +182,22 @@ def chunk_wy_backward(q, k, v, g, b, w, state0, d_out, scale: float, chunk_size:
     src/kernel/chunk_adjoint_cube.rs:464-707): for
     L = <d_out, out> + <d_state, S_T> returns dict dq, dk, dg, db (shapes of
     q, k, g, b), dv, dw (shapes of v, w) and dS0, or None when the chunk
-    kernels do not apply.  Gradient tensors take the layouts of their inputs."""
+    kernels do not apply.  dq, dk, dg, db take q's layout and dv, dw v's; dg
+    and db of a g or b with a last dim of 1 are summed over the channels."""
     _check_f32_cuda(q, k, v, g, b, w, state0, d_out)
+    g_in, b_in = g, b
+    q, k, v, g, b, w = _operands(q, k, v, g, b, w)
+    d_out = _channels_contiguous(d_out)
     B, Hk, T, K = q.shape
     HV, V = v.shape[1], v.shape[3]
     st = state0.contiguous()
     grads = {n: torch.empty_strided(t.shape, t.stride(), device=t.device, dtype=torch.float32)
-             for n, t in (("dq", q), ("dk", k), ("dg", g), ("db", b), ("dv", v), ("dw", w))}
+             for n, t in (("dq", q), ("dk", q), ("dg", q), ("db", q), ("dv", v), ("dw", v))}
     grads["dS0"] = torch.empty((B, HV, K, V), device=q.device, dtype=torch.float32)
     ds = None if d_state is None else d_state.contiguous()
     if T == 0:  # no tokens: only the state gradient passes through
         grads["dS0"] = ds.clone() if ds is not None else torch.zeros_like(grads["dS0"])
+        grads["dg"], grads["db"] = _reduce_like(grads["dg"], g_in), _reduce_like(grads["db"], b_in)
         return grads
     fwd = chunk_args(q, k, v, g, b, w, st, d_out, scale, chunk_size)
     a = C.ChunkBwdArgs(fwd, _p(d_out), _p(ds), *(_p(grads[n]) for n in ("dq", "dk", "dg", "db", "dv", "dw", "dS0")),
@@ -170,6 +208,7 @@ def chunk_wy_backward(q, k, v, g, b, w, state0, d_out, scale: float, chunk_size:
     a.workspace, a.workspace_bytes = _p(workspace), workspace.numel() * workspace.element_size()
     if not C.check(C.lib().gdn2_chunk_bwd_f32(ctypes.byref(a), _stream()), allow_not_applicable=True):
         return None
+    grads["dg"], grads["db"] = _reduce_like(grads["dg"], g_in), _reduce_like(grads["db"], b_in)
     return grads
 
 

@@ -166,3 +166,28 @@ def test_chunk_empty_sequence_keeps_state(gpu):
     S0 = torch.randn((1, 1, 128, 128), device=gpu)
     o, S = gdn2_amd.chunk_wy_forward(*d, S0, 0.1)
     assert o.shape == (1, 1, 0, 128) and torch.equal(S, S0)
+
+
+@pytest.mark.parametrize("gdim,bdim", [(1, 1), (1, None), (None, 1)])
+def test_scalar_broadcast_gates_and_mixed_layouts(gpu, gdim, bdim):
+    """g and b with a last dim of 1 -- one value per head and token, the
+    Gated DeltaNet special case (src/forward.rs:149,173,180-182;
+    tests/stable_chunk.rs scalar-broadcast cases) -- through the chunk and
+    the scan operators, with k in a different layout from q."""
+    import gdn2_amd
+
+    B, Hk, HV, T, K, V = 2, 2, 4, 150, 128, 128
+    rng = np.random.default_rng(77)
+    q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=-0.5, g_hi=-0.01, b_hi=2.0, gdim=gdim, bdim=bdim)
+    q *= K ** -0.5 * 4
+    S0 = (rng.standard_normal((B, HV, K, V)) * 0.5).astype(np.float32)
+    scale = K ** -0.5
+    o_ref, S_ref = O.recurrent_f64(q, k, v, g, b, w, S0=S0, scale=scale)
+    dq, dk, dv, dg, db, dw, dS0 = _dev(gpu, q, k, v, g, b, w, S0)
+    dk = dk.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)  # [B, T, H, K] memory, another layout than q
+    for name, res in (("chunk", gdn2_amd.chunk_wy_forward(dq, dk, dv, dg, db, dw, dS0, scale, chunk_size=64)),
+                      ("scan", gdn2_amd.fused_recurrent_forward(dq, dk, dv, dg, db, dw, dS0, scale))):
+        o, S = res
+        eo, es = maxabs(o.cpu().numpy(), o_ref), maxabs(S.cpu().numpy(), S_ref)
+        print(f"{name}: max|out err|={eo:.2e} max|S err|={es:.2e}")
+        assert eo < TOL and es < TOL

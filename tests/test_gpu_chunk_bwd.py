@@ -108,3 +108,26 @@ def test_chunk_bwd_empty_sequence(gpu):
     dO = torch.empty((1, 1, 0, 128), device=gpu)
     got = gdn2_amd.chunk_wy_backward(*d, S0, dO, 0.1, d_state=dST)
     assert torch.equal(got["dS0"], dST)
+
+
+def test_chunk_bwd_scalar_broadcast_gates(gpu):
+    """g and b with a last dim of 1: dg and db come back in their shape,
+    summed over the channels they were broadcast to."""
+    import torch
+
+    import gdn2_amd
+
+    B, Hk, HV, T, K, V = 1, 2, 2, 140, 64, 128
+    rng = np.random.default_rng(31)
+    q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=-0.4, g_hi=-0.02, b_hi=1.0, gdim=1, bdim=1)
+    q *= K ** -0.5 * 4
+    S0 = (rng.standard_normal((B, HV, K, V)) * 0.5).astype(np.float32)
+    dO = rng.standard_normal((B, HV, T, V)).astype(np.float32)
+    dST = rng.standard_normal((B, HV, K, V)).astype(np.float32)
+    scale = K ** -0.5
+    ref = O.recurrent_bwd_f64(q, k, v, g, b, w, dO, S0=S0, d_ST=dST, scale=scale)
+    d = _dev(gpu, q, k, v, g, b, w, S0, dO, dST)
+    got = gdn2_amd.chunk_wy_backward(*d[:7], d[7], scale, 64, d_state=d[8])
+    torch.cuda.synchronize()
+    assert tuple(got["dg"].shape) == (B, Hk, T, 1) and tuple(got["db"].shape) == (B, Hk, T, 1)
+    _compare(got, ref, "broadcast g, b")
