@@ -130,6 +130,31 @@ def fused_recurrent_forward(q, k, v, g, b, w, state, scale: float, out=None, in_
     return out, new_state
 
 
+def fused_recurrent_gdn2(q, k, v, g, b, w, state=None, scale: float = 1.0, update_state: bool = True):
+    """The reference's recurrent dispatch (src/kernel/fused_recurrent.rs:65-108):
+    state None means zeros; with update_state a single token runs the fused
+    step and longer inputs the scan, returning (out [B, HV, T, V], new state).
+    With update_state False the state is only read: out = scale * q S, laid
+    out [B, T, HV, V] as the reference's read-only branch permutes it, and the
+    state comes back unchanged.  That branch runs the scan with k = 0 and
+    g = 0, which leaves S exactly as it is (decay e^0 = 1, update 0 * v_new)
+    while every token reads it."""
+    _check_f32_cuda(q, k, v, g, b, w, state)
+    B, Hk, T, K = q.shape
+    HV, V = v.shape[1], v.shape[3]
+    if state is None:
+        state = torch.zeros((B, HV, K, V), device=q.device, dtype=torch.float32)
+    if update_state:
+        if T == 1:
+            res = fused_step(q, k, v, g, b, w, state, scale)
+            if res is not None:
+                return res
+        return fused_recurrent_forward(q, k, v, g, b, w, state, scale)
+    zk = torch.zeros_like(q)
+    out, _ = fused_recurrent_forward(q, zk, v, zk, zk, w, state, scale)
+    return out.permute(0, 2, 1, 3), state
+
+
 def chunk_args(q, k, v, g, b, w, state, out, scale, chunk_size, workspace=None):
     B, Hk, T, K = q.shape
     HV, V = v.shape[1], v.shape[3]

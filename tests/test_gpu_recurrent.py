@@ -77,6 +77,35 @@ def test_scan_in_place_and_strided_layout(gpu):
     assert maxabs(S.cpu().numpy(), S_ref) < TOL
 
 
+@pytest.mark.parametrize("T,update", [(1, True), (40, True), (40, False), (1, False)])
+def test_fused_recurrent_gdn2_dispatch(gpu, T, update):
+    """fused_recurrent_gdn2 (src/kernel/fused_recurrent.rs:65-108): state
+    None = zeros, the fused step at T = 1, the scan otherwise; update_state
+    False reads the state only (out = scale q S, permuted to [B, T, HV, V])
+    and returns it unchanged."""
+    import gdn2_amd
+
+    B, Hk, HV, K, V = 2, 2, 4, 64, 128
+    rng = np.random.default_rng(300 + T)
+    q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V)
+    S0 = rng.standard_normal((B, HV, K, V)).astype(np.float32) * 0.5
+    dq, dk, dv, dg, db, dw, dS = _dev(gpu, q, k, v, g, b, w, S0)
+    o, S = gdn2_amd.fused_recurrent_gdn2(dq, dk, dv, dg, db, dw, dS, 0.3, update_state=update)
+    if update:
+        o_ref, S_ref = O.recurrent_f64(q, k, v, g, b, w, S0=S0, scale=0.3)
+        assert maxabs(o.cpu().numpy(), o_ref) < TOL and maxabs(S.cpu().numpy(), S_ref) < TOL
+        o0, S_zero = gdn2_amd.fused_recurrent_gdn2(dq, dk, dv, dg, db, dw, None, 0.3)  # None = zeros
+        r0, Sr0 = O.recurrent_f64(q, k, v, g, b, w, S0=None, scale=0.3)
+        assert maxabs(o0.cpu().numpy(), r0) < TOL and maxabs(S_zero.cpu().numpy(), Sr0) < TOL
+    else:
+        rep = HV // Hk
+        qf = np.repeat(q.astype(np.float64), rep, axis=1)                 # [B, HV, T, K]
+        ref = 0.3 * np.einsum("bhtk,bhkv->bhtv", qf, S0.astype(np.float64)).transpose(0, 2, 1, 3)
+        assert tuple(o.shape) == (B, T, HV, V)
+        assert maxabs(o.cpu().numpy(), ref) < TOL
+        np.testing.assert_array_equal(S.cpu().numpy(), S0)
+
+
 def _raw_from_layer(cfg, W, x):
     xd = x.astype(np.float64)
     return {"q_raw": xd @ W["q_proj"], "k_raw": xd @ W["k_proj"], "v_raw": xd @ W["v_proj"],
