@@ -561,30 +561,55 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     const size_t cid0 = (size_t)bh * p.NC;
     const size_t uvf4 = (size_t)C * V / 4;
 
+    // the operands go from global memory straight into LDS (lds_copy4):
+    // thread tid's float4 i lands at index i * 256 + tid, as a wave's 64 lanes
+    const int wv = 64 * wave;
     if (n1 > n0) {
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
-            sW[i * 256 + tid] = W4[(cid0 + n0) * OPF4 + i * 256 + tid];
-            if (OUT) sQ[i * 256 + tid] = Q4[(cid0 + n0) * OPF4 + i * 256 + tid];
+            lds_copy4(&W4[(cid0 + n0) * OPF4 + i * 256 + tid], &sW[i * 256 + wv]);
+            if (OUT) lds_copy4(&Q4[(cid0 + n0) * OPF4 + i * 256 + tid], &sQ[i * 256 + wv]);
         }
     }
 
     // row 4 lg of each 16-row tile; the rest of the row offset is wave-uniform
     float *ob = p.out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + col + (int64_t)(4 * lg) * p.sot;
+    // chunk nn's output rows from X2 (rows past T are not written)
+    auto store_out = [&](const floatx4 *o, int nn) {
+        if ((nn + 1) * C <= p.T) { // a full chunk (wave-uniform): unconditional stores
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ob[(int64_t)(nn * C + 16 * mt + i) * p.sot] = o[mt][i];
+        } else {
+            const int cv = p.T - nn * C;
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (16 * mt + 4 * lg + i < cv) ob[(int64_t)(nn * C + 16 * mt + i) * p.sot] = o[mt][i];
+        }
+    };
+    floatx4 X2[NT]; // chunk n's output, stored early in iteration n + 1
     for (int n = n0; n < n1; ++n) {
         const size_t cid = cid0 + n;
+        vm_wait0();      // this wave's copies of chunk n's W, q exp(G) have landed
         __syncthreads(); // sW, sQ hold chunk n; every wave is done with sKd, sA (n-1)
-        floatx4 kpre[PFO], apre[OUT ? APF : 1], u_cur[NT], g_cur = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < PFO; ++i) kpre[i] = K4[cid * OPF4 + i * 256 + tid];
+        for (int i = 0; i < PFO; ++i) lds_copy4(&K4[cid * OPF4 + i * 256 + tid], &sKd[i * 256 + wv]);
         if (OUT) {
 #pragma unroll
-            for (int i = 0; i < APF; ++i) apre[i] = A4[cid * AF4 + i * 256 + tid];
+            for (int i = 0; i < APF; ++i) lds_copy4(&A4[cid * AF4 + i * 256 + tid], &sA[i * 256 + wv]);
+            if (n > n0) store_out(X2, n - 1);
         }
+        floatx4 u_cur[NT], g_cur = floatx4{0.f, 0.f, 0.f, 0.f};
         if (tid < K / 4) g_cur = G4[cid * (K / 4) + tid];
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt)
             u_cur[mt] = pcol ? floatx4{0.f, 0.f, 0.f, 0.f} : U4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
+        // keep these loads here, a whole phase ahead of their use and of the
+        // vmcnt wait before the next barrier
+        __builtin_amdgcn_sched_barrier(0);
         if (STATES) { // the state entering chunk n
             float *Sn = p.ws_sn + cid * K * V;
 #pragma unroll
@@ -594,7 +619,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         }
 
         // A: X1 = W S, X2 = scale (q exp(G)) S
-        floatx4 X1[NT], X2[NT];
+        floatx4 X1[NT];
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) X1[mt] = X2[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -614,23 +639,17 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
                     if (OUT) X2[mt] = mfma16(ma[mt][st], S[kb][st], X2[mt]);
                 }
         }
-#pragma unroll
-        for (int i = 0; i < PFO; ++i) sKd[i * 256 + tid] = kpre[i];
-        if (OUT) {
-#pragma unroll
-            for (int i = 0; i < APF; ++i) sA[i * 256 + tid] = apre[i];
-        }
         if (tid < K / 4) sGam[tid] = g_cur;
-        __syncthreads(); // A done everywhere (sW, sQ free); sKd(n), sA(n) visible
+        vm_wait0();      // this wave's copies of chunk n's Kd, A_qk have landed
+        __syncthreads(); // A done everywhere (sW, sQ free); sKd(n), sA(n), sGam(n) visible
 
-        // W, q exp(G) of chunk n+1 (the last chunk re-fetches itself: harmless,
-        // and unconditional loads keep the staging registers out of scratch)
-        const size_t cnx = cid + (n + 1 < n1 ? 1 : 0);
-        floatx4 wpre[PFO], qpre[OUT ? PFO : 1];
+        // W, q exp(G) of chunk n+1
+        if (n + 1 < n1) {
 #pragma unroll
-        for (int i = 0; i < PFO; ++i) {
-            wpre[i] = W4[cnx * OPF4 + i * 256 + tid];
-            if (OUT) qpre[i] = Q4[cnx * OPF4 + i * 256 + tid];
+            for (int i = 0; i < PFO; ++i) {
+                lds_copy4(&W4[(cid + 1) * OPF4 + i * 256 + tid], &sW[i * 256 + wv]);
+                if (OUT) lds_copy4(&Q4[(cid + 1) * OPF4 + i * 256 + tid], &sQ[i * 256 + wv]);
+            }
         }
 
         // B: v_new = U - X1 (kept in X1)
@@ -644,23 +663,19 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
                 for (int i = 0; i < 4; ++i) Vn[(size_t)(16 * mt + 4 * lg + i) * V + col] = X1[mt][i];
         }
 
-        // D: out = X2 + A_qk v_new (A_qk is lower block-triangular)
+        // D: out = X2 + A_qk v_new (A_qk is lower block-triangular); the
+        // chains of the four time tiles interleave, and the stores wait until
+        // the next chunk so that no MFMA result is waited on early
         if (OUT) {
-            const int cv = min(C, p.T - n * C);
 #pragma unroll
-            for (int mt = 0; mt < NT; ++mt) {
-                floatx4 o = X2[mt];
+            for (int qt = 0; qt < NT; ++qt) {
+                floatx4 aa[NT];
 #pragma unroll
-                for (int qt = 0; qt <= mt; ++qt) {
-                    const floatx4 aa = sA[(mt * NT + qt) * 64 + lane];
-                    o = mfma16(aa[0], X1[qt][0], o);
-                    o = mfma16(aa[1], X1[qt][1], o);
-                    o = mfma16(aa[2], X1[qt][2], o);
-                    o = mfma16(aa[3], X1[qt][3], o);
-                }
+                for (int mt = qt; mt < NT; ++mt) aa[mt] = sA[(mt * NT + qt) * 64 + lane];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (16 * mt + 4 * lg + i < cv) ob[(int64_t)(n * C + 16 * mt + i) * p.sot] = o[i];
+                for (int st = 0; st < 4; ++st)
+#pragma unroll
+                    for (int mt = qt; mt < NT; ++mt) X2[mt] = mfma16(aa[mt][st], X1[qt][st], X2[mt]);
             }
         }
 
@@ -688,12 +703,8 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
 #pragma unroll
             for (int kb = 0; kb < NKT; ++kb) S[kb] = mfma16(ka[kb][3], X1[tt][3], S[kb]);
         }
-#pragma unroll
-        for (int i = 0; i < PFO; ++i) {
-            sW[i * 256 + tid] = wpre[i];
-            if (OUT) sQ[i * 256 + tid] = qpre[i];
-        }
     }
+    if (OUT && n1 > n0) store_out(X2, n1 - 1);
 
     // leaving state: the final state (last segment), Q_j or P_j (pass 1)
     float *Sout = nullptr;

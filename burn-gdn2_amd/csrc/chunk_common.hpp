@@ -72,6 +72,17 @@ __device__ __forceinline__ floatx4 exp2v(floatx4 x) {
 // that the V-slices of one sequence, which read the same W, M and Kd^T,
 // land on the same XCD and share its L2.  Identity when the sequence count
 // is not a multiple of 8.
+// Direct global -> LDS copy of one float4 per lane (global_load_lds_dwordx4):
+// lane l of the calling wave writes wave_base[l]; wave_base is wave-uniform.
+// The copy counts in vmcnt: wait with vm_wait0() before the barrier that
+// publishes it.
+__device__ __forceinline__ void lds_copy4(const floatx4 *src, floatx4 *wave_base) {
+    __builtin_amdgcn_global_load_lds(static_cast<const void *>(src),
+                                     (__attribute__((address_space(3))) void *)(wave_base), 16, 0, 0);
+}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt not waited on)
+__device__ __forceinline__ void vm_wait0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 __device__ __forceinline__ void inter_block(int blk, int nseq, int nvs, int *bh, int *vs) {
     if (nseq % 8 == 0) {
         const int x = blk % 8, j = blk / 8;
