@@ -352,14 +352,25 @@ def _short(name):
 
 
 def stats_summary(path):
+    """The library's kernels by total time; hipBLASLt's GEMM kernels (the
+    layer's Linear layers, many kernel names, including the candidates timed
+    on the first call of each shape) are summed into one row."""
     import csv
 
     rows = list(csv.DictReader(open(path)))
+    gemm = [r for r in rows if r["Name"].startswith("Cijk")]
+    own = [r for r in rows if not r["Name"].startswith("Cijk")]
     print("| kernel | calls | avg us | total us | % of GPU time |")
     print("|---|---|---|---|---|")
-    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:12]:
+    for r in sorted(own, key=lambda r: -float(r["TotalDurationNs"]))[:12]:
         print(f"| `{_short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
               f"{float(r['TotalDurationNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
+    if gemm:
+        calls = sum(int(r["Calls"]) for r in gemm)
+        tot = sum(float(r["TotalDurationNs"]) for r in gemm)
+        pct = sum(float(r["Percentage"]) for r in gemm)
+        print(f"| hipBLASLt GEMM kernels ({len(gemm)} names) | {calls} | {tot / calls / 1e3:.1f} | {tot / 1e3:.1f} | "
+              f"{pct:.1f} |")
 
 
 def train_summary(path):
