@@ -289,6 +289,20 @@ gdn2_status project_epilogue(gdn2_layer &L, int64_t B, int64_t T, const float *c
     return GDN2_OK;
 }
 
+// The scan's arguments for the same operands (state in place).
+gdn2_recurrent_args recurrent_args_for(const gdn2_chunk_args &ca) {
+    gdn2_recurrent_args ra{};
+    ra.q = ca.q; ra.k = ca.k; ra.g = ca.g; ra.b = ca.b; ra.v = ca.v; ra.w = ca.w;
+    ra.state_in = ca.state; ra.state_out = ca.state; ra.out = ca.out;
+    ra.batch = ca.batch; ra.num_heads = ca.num_heads; ra.num_v_heads = ca.num_v_heads; ra.seq_len = ca.seq_len;
+    ra.head_dim = ca.head_dim; ra.head_v_dim = ca.head_v_dim;
+    ra.stride_qk_b = ca.stride_qk_b; ra.stride_qk_h = ca.stride_qk_h; ra.stride_qk_t = ca.stride_qk_t;
+    ra.stride_vw_b = ca.stride_vw_b; ra.stride_vw_h = ca.stride_vw_h; ra.stride_vw_t = ca.stride_vw_t;
+    ra.stride_o_b = ca.stride_o_b; ra.stride_o_h = ca.stride_o_h; ra.stride_o_t = ca.stride_o_t;
+    ra.scale = ca.scale;
+    return ra;
+}
+
 // The recurrence over the projected inputs into O; S is updated in place.
 gdn2_status recurrence(gdn2_layer &L, int64_t B, int64_t T, int mode, const Work &wk, float *S, hipStream_t s) {
     gdn2_chunk_args ca = chunk_args_for(L, B, T, wk, S);
@@ -298,15 +312,7 @@ gdn2_status recurrence(gdn2_layer &L, int64_t B, int64_t T, int mode, const Work
         const gdn2_status st = gdn2_chunk_fwd_f32(&ca, s);
         if (st != GDN2_NOT_APPLICABLE) return st;
     }
-    gdn2_recurrent_args ra{};
-    ra.q = ca.q; ra.k = ca.k; ra.g = ca.g; ra.b = ca.b; ra.v = ca.v; ra.w = ca.w;
-    ra.state_in = S; ra.state_out = S; ra.out = ca.out;
-    ra.batch = B; ra.num_heads = ca.num_heads; ra.num_v_heads = ca.num_v_heads; ra.seq_len = T;
-    ra.head_dim = ca.head_dim; ra.head_v_dim = ca.head_v_dim;
-    ra.stride_qk_b = ca.stride_qk_b; ra.stride_qk_h = ca.stride_qk_h; ra.stride_qk_t = ca.stride_qk_t;
-    ra.stride_vw_b = ca.stride_vw_b; ra.stride_vw_h = ca.stride_vw_h; ra.stride_vw_t = ca.stride_vw_t;
-    ra.stride_o_b = ca.stride_o_b; ra.stride_o_h = ca.stride_o_h; ra.stride_o_t = ca.stride_o_t;
-    ra.scale = ca.scale;
+    gdn2_recurrent_args ra = recurrent_args_for(ca);
     return gdn2_recurrent_fwd_f32(&ra, s);
 }
 
@@ -1005,7 +1011,11 @@ gdn2_status bwd_workspace(gdn2_layer &L, int64_t B, int64_t T, bool recompute, B
     gdn2_chunk_args ca = chunk_args_for(L, B, T, tmp, nullptr);
     gdn2_chunk_bwd_args ba{};
     ba.fwd = ca;
-    const size_t chunk_bytes = std::max(gdn2_chunk_workspace_bytes(&ca), gdn2_chunk_bwd_workspace_bytes(&ba));
+    gdn2_recurrent_bwd_args ra{};
+    ra.fwd = recurrent_args_for(ca);
+    const size_t chunk_bytes = std::max({gdn2_chunk_workspace_bytes(&ca), gdn2_chunk_bwd_workspace_bytes(&ba),
+                                         chunk_supported((int)d.K, (int)d.V) ? size_t(0)
+                                                                             : gdn2_recurrent_bwd_workspace_bytes(&ra)});
     const size_t f = sizeof(float), nS = f * B * d.HV * d.K * d.V;
     const size_t nk = f * M * d.kd, nv = f * M * d.vd, nY = f * M * L.ld_in;
     const size_t rk = recompute ? nk : 0, rv = recompute ? nv : 0;  // the forward's buffers, when recomputed
@@ -1197,9 +1207,9 @@ extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, in
     if (saved && state_in && state_in->some)
         return fail(GDN2_EINVAL, "gdn2_layer_backward_f32: saved activations come from forward_train (no state_in)");
     const Dims &d = L->d;
-    if (!chunk_supported((int)d.K, (int)d.V))
-        return fail(GDN2_NOT_APPLICABLE, "gdn2_layer_backward_f32: needs head_dim in {64, 128} and head_v_dim in "
-                                         "{64, 128, 256} (the chunked backward's shapes)");
+    // the recurrence's adjoint: the chunked kernels where they apply, else the
+    // scan's (which returns GDN2_NOT_APPLICABLE for heads beyond its LDS)
+    const bool use_chunk = chunk_supported((int)d.K, (int)d.V);
     hipStream_t s = (hipStream_t)stream;
     const bool sc = L->cfg.use_short_conv != 0, md = L->cfg.has_min_decay != 0;
     const bool has_state = state_in && state_in->some, has_ds = d_state && d_state->some;
@@ -1256,10 +1266,9 @@ extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, in
         if ((st = input_gemms(*L, x, M, fw, s)) != GDN2_OK) return st;
         if ((st = project_epilogue(*L, B, T, has_state ? conv_in : nullptr, fw, s)) != GDN2_OK) return st;
         GDN2_HIP_CHECK(hipMemcpyAsync(bw.Sf, bw.S0, sizeof(float) * nS, hipMemcpyDeviceToDevice, s));
-        gdn2_chunk_args ca = chunk_args_for(*L, B, T, fw, bw.Sf);
-        ca.workspace = fw.chunk;
-        ca.workspace_bytes = fw.chunk_bytes;
-        if ((st = gdn2_chunk_fwd_f32(&ca, s)) != GDN2_OK) return st;
+        if ((st = recurrence(*L, B, T, use_chunk ? GDN2_MODE_CHUNK : GDN2_MODE_FUSED_RECURRENT, fw, bw.Sf, s)) !=
+            GDN2_OK)
+            return st;
     }
 
     // o_proj and the gated RMSNorm
@@ -1275,15 +1284,27 @@ extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, in
     GDN2_HIP_CHECK(launch_colsum(bw.dy, M, d.vd, d.vd, 1, (int)d.HV, G->p[P_O_NORM], accumulate, bw.part, kColParts, s));
 
     // the recurrence
-    gdn2_chunk_bwd_args ba{};
-    ba.fwd = chunk_args_for(*L, B, T, fw, bw.S0);
-    ba.d_out = bw.dO;
-    ba.d_state_out = has_ds ? d_state->S : nullptr;
-    ba.dq = bw.dq; ba.dk = bw.dk; ba.dg = bw.dg; ba.db = bw.db; ba.dv = bw.dv; ba.dw = bw.dw;
-    ba.d_state0 = d_state_in ? d_state_in->S : bw.dS0;
-    ba.workspace = fw.chunk;
-    ba.workspace_bytes = fw.chunk_bytes;
-    if ((st = gdn2_chunk_bwd_f32(&ba, s)) != GDN2_OK) return st;
+    if (use_chunk) {
+        gdn2_chunk_bwd_args ba{};
+        ba.fwd = chunk_args_for(*L, B, T, fw, bw.S0);
+        ba.d_out = bw.dO;
+        ba.d_state_out = has_ds ? d_state->S : nullptr;
+        ba.dq = bw.dq; ba.dk = bw.dk; ba.dg = bw.dg; ba.db = bw.db; ba.dv = bw.dv; ba.dw = bw.dw;
+        ba.d_state0 = d_state_in ? d_state_in->S : bw.dS0;
+        ba.workspace = fw.chunk;
+        ba.workspace_bytes = fw.chunk_bytes;
+        if ((st = gdn2_chunk_bwd_f32(&ba, s)) != GDN2_OK) return st;
+    } else {
+        gdn2_recurrent_bwd_args ra{};
+        ra.fwd = recurrent_args_for(chunk_args_for(*L, B, T, fw, bw.S0));
+        ra.d_out = bw.dO;
+        ra.d_state_out = has_ds ? d_state->S : nullptr;
+        ra.dq = bw.dq; ra.dk = bw.dk; ra.dg = bw.dg; ra.db = bw.db; ra.dv = bw.dv; ra.dw = bw.dw;
+        ra.d_state0 = d_state_in ? d_state_in->S : bw.dS0;
+        ra.workspace = fw.chunk;
+        ra.workspace_bytes = fw.chunk_bytes;
+        if ((st = gdn2_recurrent_bwd_f32(&ra, s)) != GDN2_OK) return st;
+    }
 
     // projection epilogue and short conv
     ProjectBwdParams pp{};

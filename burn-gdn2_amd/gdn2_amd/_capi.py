@@ -60,6 +60,12 @@ class ChunkBwdArgs(ctypes.Structure):
                 ("workspace", _fp), ("workspace_bytes", ctypes.c_size_t)]
 
 
+class RecurrentBwdArgs(ctypes.Structure):
+    _fields_ = [("fwd", RecurrentArgs), ("d_out", _fp), ("d_state_out", _fp),
+                ("dq", _fp), ("dk", _fp), ("dg", _fp), ("db", _fp), ("dv", _fp), ("dw", _fp), ("d_state0", _fp),
+                ("workspace", _fp), ("workspace_bytes", ctypes.c_size_t)]
+
+
 class LayerParams(ctypes.Structure):
     _fields_ = [("q_conv_w", _fp), ("k_conv_w", _fp), ("v_conv_w", _fp), ("a_log", _fp), ("dt_bias", _fp),
                 ("decay_factors", _fp), ("o_norm_weight", _fp), ("min_decay", _dbl), ("norm_eps", _dbl),
@@ -91,7 +97,8 @@ STATE_RECURRENT, STATE_CONV_Q, STATE_CONV_K, STATE_CONV_V = 0, 1, 2, 3
 # Every symbol include/*.h declares (checked by tests/test_capi_exports.py).
 EXPORTS = ("gdn2_last_error", "gdn2_hip_available", "gdn2_recurrent_step_f32", "gdn2_recurrent_fwd_f32",
            "gdn2_chunk_workspace_bytes", "gdn2_chunk_fwd_f32", "gdn2_chunk_intra_f32", "gdn2_chunk_inter_f32",
-           "gdn2_chunk_bwd_workspace_bytes", "gdn2_chunk_bwd_f32", "gdn2_decode_fused_f32",
+           "gdn2_chunk_bwd_workspace_bytes", "gdn2_chunk_bwd_f32", "gdn2_recurrent_bwd_workspace_bytes",
+           "gdn2_recurrent_bwd_f32", "gdn2_decode_fused_f32",
            "gdn2_config_default", "gdn2_config_validate", "gdn2_config_dims", "gdn2_param_count",
            "gdn2_param_name", "gdn2_param_shape", "gdn2_param_init", "gdn2_layer_create", "gdn2_layer_destroy",
            "gdn2_layer_config", "gdn2_layer_set_param", "gdn2_layer_get_param", "gdn2_layer_forward_train_f32",
@@ -124,7 +131,7 @@ def lib():
         for name, st in (("gdn2_recurrent_step_f32", StepArgs), ("gdn2_recurrent_fwd_f32", RecurrentArgs),
                          ("gdn2_chunk_fwd_f32", ChunkArgs), ("gdn2_chunk_intra_f32", ChunkArgs),
                          ("gdn2_chunk_inter_f32", ChunkArgs), ("gdn2_decode_fused_f32", DecodeArgs),
-                         ("gdn2_chunk_bwd_f32", ChunkBwdArgs)):
+                         ("gdn2_chunk_bwd_f32", ChunkBwdArgs), ("gdn2_recurrent_bwd_f32", RecurrentBwdArgs)):
             fn = getattr(L, name)
             fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
             fn.restype = ctypes.c_int
@@ -132,6 +139,8 @@ def lib():
         L.gdn2_chunk_workspace_bytes.restype = ctypes.c_size_t
         L.gdn2_chunk_bwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkBwdArgs)]
         L.gdn2_chunk_bwd_workspace_bytes.restype = ctypes.c_size_t
+        L.gdn2_recurrent_bwd_workspace_bytes.argtypes = [ctypes.POINTER(RecurrentBwdArgs)]
+        L.gdn2_recurrent_bwd_workspace_bytes.restype = ctypes.c_size_t
         _declare_layer(L)
         _lib = L
     return _lib

@@ -237,6 +237,41 @@ def chunk_wy_backward(q, k, v, g, b, w, state0, d_out, scale: float, chunk_size:
     return grads
 
 
+def fused_recurrent_backward(q, k, v, g, b, w, state0, d_out, scale: float, d_state=None, workspace=None):
+    """Gradients of the per-token scan (fused_recurrent_forward) for any (K, V)
+    the scan backward kernel takes: for L = <d_out, out> + <d_state, S_T>
+    returns dict dq, dk, dg, db, dv, dw, dS0 (layouts as chunk_wy_backward),
+    or None outside its limits.  state0 None means zeros."""
+    _check_f32_cuda(q, k, v, g, b, w, state0, d_out)
+    g_in, b_in = g, b
+    q, k, v, g, b, w = _operands(q, k, v, g, b, w)
+    d_out = _channels_contiguous(d_out)
+    B, Hk, T, K = q.shape
+    HV, V = v.shape[1], v.shape[3]
+    st = None if state0 is None else state0.contiguous()
+    grads = {n: torch.empty_strided(t.shape, t.stride(), device=t.device, dtype=torch.float32)
+             for n, t in (("dq", q), ("dk", q), ("dg", q), ("db", q), ("dv", v), ("dw", v))}
+    grads["dS0"] = torch.empty((B, HV, K, V), device=q.device, dtype=torch.float32)
+    ds = None if d_state is None else d_state.contiguous()
+    if T == 0:  # no tokens: only the state gradient passes through
+        grads["dS0"] = ds.clone() if ds is not None else torch.zeros_like(grads["dS0"])
+        grads["dg"], grads["db"] = _reduce_like(grads["dg"], g_in), _reduce_like(grads["db"], b_in)
+        return grads
+    sq, sv, so = _strides3(q), _strides3(v), _strides3(d_out)
+    fwd = C.RecurrentArgs(_p(q), _p(k), _p(g), _p(b), _p(v), _p(w), _p(st), None, None, B, Hk, HV, T, K, V,
+                          *sq, *sv, *so, float(scale))
+    a = C.RecurrentBwdArgs(fwd, _p(d_out), _p(ds), *(_p(grads[n]) for n in ("dq", "dk", "dg", "db", "dv", "dw", "dS0")),
+                           None, 0)
+    need = int(C.lib().gdn2_recurrent_bwd_workspace_bytes(ctypes.byref(a)))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    a.workspace, a.workspace_bytes = _p(workspace), workspace.numel() * workspace.element_size()
+    if not C.check(C.lib().gdn2_recurrent_bwd_f32(ctypes.byref(a), _stream()), allow_not_applicable=True):
+        return None
+    grads["dg"], grads["db"] = _reduce_like(grads["dg"], g_in), _reduce_like(grads["db"], b_in)
+    return grads
+
+
 def decode_args(raw: dict, params: dict, state, conv_in, conv_out, out, *, num_heads, num_v_heads, head_dim,
                 head_v_dim, scale, min_decay=None, norm_eps=1e-5, use_short_conv=True, allow_neg_eigval=False):
     """Build the gdn2_decode_args block (the LayerParams it points to is

@@ -193,6 +193,41 @@ GDN2_API size_t gdn2_chunk_bwd_workspace_bytes(const gdn2_chunk_bwd_args *args);
 GDN2_API gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *args, gdn2_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Backward of the per-token scan                 -- autodiff of the recurrence
+ * (src/kernel/fused_recurrent.rs:27-52, differentiated by burn's autodiff in
+ * the reference's training path, tests/autodiff.rs:153-206): the gradients
+ * of L = <d_out, out> + <d_state_out, S_T> for the scan of `fwd`, for any
+ * (K, V) whose working set fits one workgroup -- the shapes the chunked
+ * backward does not take.
+ *   fwd          the forward's arguments: q, k, g, b, v, w, state_in = S0
+ *                (read only; NULL = zeros), strides, scale; state_out, out unused
+ *   d_out        strided like out (fwd.stride_o_*)
+ *   d_state_out  [B, HV, K, V] contiguous, or NULL (zero)
+ *   dq, dk, dg, db  strided like q; with num_v_heads > num_heads the sum over
+ *                the value heads of each key head
+ *   dv, dw       strided like v
+ *   d_state0     [B, HV, K, V] contiguous
+ * workspace: gdn2_recurrent_bwd_workspace_bytes(args) bytes (the state every
+ * 64 tokens, and the states of one 64-token segment, per key head).
+ * Limits (else GDN2_NOT_APPLICABLE): 4 (2 K (V + 1) + 5 K + 3 V) bytes of LDS
+ * at most 160 KB (e.g. K = V = 128).  One workgroup per (batch row, key
+ * head), sequential over tokens: meant for small heads.
+ * ---------------------------------------------------------------------- */
+typedef struct gdn2_recurrent_bwd_args {
+    gdn2_recurrent_args fwd;
+    const float *d_out;
+    const float *d_state_out;
+    float *dq, *dk, *dg, *db;
+    float *dv, *dw;
+    float *d_state0;
+    void *workspace;
+    size_t workspace_bytes;
+} gdn2_recurrent_bwd_args;
+
+GDN2_API size_t gdn2_recurrent_bwd_workspace_bytes(const gdn2_recurrent_bwd_args *args);
+GDN2_API gdn2_status gdn2_recurrent_bwd_f32(const gdn2_recurrent_bwd_args *args, gdn2_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Fused decode of one token for every batch row           -- forward at T=1
  * Inputs are the raw projections of one token (outputs of the Linear
  * layers, src/module.rs:400-402,417-418,442-443,474-475):

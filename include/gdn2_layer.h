@@ -194,9 +194,10 @@ GDN2_API gdn2_status gdn2_layer_forward_train_saved_f32(gdn2_layer *layer, const
  *                accumulation, or a chain of calls run backwards, each with
  *                d_state = the d_state_in of the call after it)
  * The result does not depend on cfg->mode (both modes compute the same
- * recurrence); the recurrence's adjoint is gdn2_chunk_bwd_f32.
- * Limits (else GDN2_NOT_APPLICABLE): head_dim in {64, 128}, head_v_dim in
- * {64, 128, 256}. */
+ * recurrence).  The recurrence's adjoint is gdn2_chunk_bwd_f32 where it
+ * applies (head_dim in {64, 128}, head_v_dim in {64, 128, 256}), else
+ * gdn2_recurrent_bwd_f32, whose limit is the only one here (else
+ * GDN2_NOT_APPLICABLE). */
 GDN2_API gdn2_status gdn2_layer_backward_f32(gdn2_layer *layer, const float *x, int64_t batch, int64_t seq_len,
                                              const gdn2_state *state_in, const gdn2_layer_saved *saved,
                                              const float *d_out,

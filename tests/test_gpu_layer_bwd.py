@@ -167,13 +167,31 @@ def test_decode_chain_backward_equals_one_pass(gpu):
     _close(d_state.read(0), dsi_one.read(0), "dS0")
 
 
-def test_backward_rejects_unsupported_shapes(gpu):
+@pytest.mark.parametrize("mode", ["fused_recurrent", "chunk"])
+def test_small_heads_backward_matches_oracle(gpu, mode):
+    """The reference's gradient test configuration (tests/autodiff.rs:153-175:
+    hidden 32, 2 heads of 16, B = 2, T = 24, both modes): heads the chunked
+    backward does not take run the scan's adjoint."""
+    import torch
+
+    G, cfg, layer, W = _setup(gpu, dict(hidden_size=32, num_heads=2, head_dim=16, mode=mode))
+    rng = np.random.default_rng(21)
+    B, T = 2, 24
+    xh = rng.standard_normal((B, T, cfg.hidden_size)).astype(np.float32)
+    dh = rng.standard_normal((B, T, cfg.hidden_size)).astype(np.float32)
+    dx, grads, dsi = layer.backward(torch.from_numpy(xh).to(gpu), torch.from_numpy(dh).to(gpu), want_d_state=True)
+    ref = O.layer_backward_f64(cfg, W, xh, dh)
+    assert float(np.abs(grads.get("q_proj")).max()) > 0 and float(np.abs(grads.get("a_log")).max()) > 0
+    _compare(grads, dx, dsi, ref, O.WEIGHT_NAMES)
+
+
+def test_backward_rejects_oversized_heads(gpu):
     import torch
 
     G = pytest.importorskip("gdn2_amd")
-    cfg = G.Gdn2Config(hidden_size=32, num_heads=2, head_dim=16)
+    cfg = G.Gdn2Config(hidden_size=256, num_heads=1, head_dim=256)  # K = V = 256: neither backward kernel
     layer = G.GatedDeltaNet2(cfg)
-    x = torch.zeros((1, 4, 32), device=gpu)
+    x = torch.zeros((1, 4, 256), device=gpu)
     with pytest.raises(G._capi.Gdn2Error) as e:
         layer.backward(x, x)
     assert e.value.status == G._capi.GDN2_NOT_APPLICABLE
