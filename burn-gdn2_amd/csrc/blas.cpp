@@ -13,7 +13,7 @@ namespace gdn2 {
 
 namespace {
 constexpr size_t kMaxWorkspace = size_t(64) << 20;
-constexpr int kCandidates = 8;  // heuristic results timed per shape
+constexpr int kCandidates = 32;  // heuristic results timed per shape
 }
 
 gdn2_status Gemm::ensure_ws(size_t bytes) {

@@ -1,6 +1,6 @@
 // Row-major f32 GEMMs of the layer: C[M, N] = op(A) op(B) (+ beta C) through
 // hipBLASLt, with one plan (descriptors + algorithm) cached per shape.  The
-// algorithm is the fastest of the heuristic's first few candidates, timed on
+// algorithm is the fastest of the heuristic's first 32 candidates, timed on
 // the first call's operands into a scratch output (when the stream is not
 // being captured; otherwise the heuristic's first).  rocBLAS runs the shapes
 // hipBLASLt has no algorithm for.
