@@ -28,6 +28,9 @@
  *                         (src/module.rs:404-476, :244-312)
  *   gdn2o_layer_forward   GatedDeltaNet2::project + forward / forward_train
  *                         in double (src/module.rs:224-495)
+ *   gdn2o_scan_d, gdn2o_recurrent_bwd_d  the scan and its adjoint on double
+ *                         operands (the layer adjoint in oracle.py feeds them
+ *                         its own double values)
  *
  * Pinning (what checks each function against something other than itself):
  *   recurrent_f64/f32  closed forms (b=0,g=0 linear attention; T=1 rank-1
@@ -35,7 +38,11 @@
  *                      the reference's own torch model (tests/golden/)
  *   recurrent_bwd_f64  central finite differences of recurrent_f64 on
  *                      every input (tests/test_oracle_bwd.py); the
- *                      b=0, g=0 closed form
+ *                      b=0, g=0 closed form.  recurrent_bwd_d is the same
+ *                      code on double inputs; scan_d is the layer's scan
+ *   (layer adjoint)    oracle.py's layer_backward_f64: central finite
+ *                      differences of gdn2o_layer_forward on every parameter,
+ *                      the input and the state (tests/test_oracle_layer_bwd.py)
  *   chunk_wy_f32       chunk == recurrence invariant for C in {4..128},
  *                      ragged T, non-zero S0, broadcast g/b
  *   short_conv         brute-force convolution on tiny inputs + cache

@@ -11,6 +11,10 @@ Array conventions (numpy, C-contiguous):
   S           [B, HV, K, V]
   out         [B, HV, T, V]
 Value head hv reads key head hv // (HV // Hk).
+
+layer_backward_f64 (the layer's adjoint, in numpy on double values with the
+scan parts in C) is pinned by central finite differences of the C layer
+forward in tests/test_oracle_layer_bwd.py.
 """
 from __future__ import annotations
 
