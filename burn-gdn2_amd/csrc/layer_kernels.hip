@@ -41,72 +41,152 @@ __device__ __forceinline__ float conv4(const float *x, int64_t ldx, int t, const
     return acc;
 }
 
-// One workgroup per token m = b * T + t.
+// One workgroup per (batch row, block of kProjTB tokens, head), so that every
+// raw projection element is read once (plus three tokens of conv history per
+// thread's run of tokens) and every output is a contiguous head-major block.
+// Key heads (blockIdx.y < H) produce q, k, g, b of their head; the L2 norms
+// over K need the whole head, so q and k pass through LDS (heads up to 256
+// channels; wider heads keep them in the output rows instead).  Value heads
+// produce v and w.  A thread owns one channel and a run of kProjRun tokens,
+// sliding the four-tap window along it.
+constexpr int kProjTB = 64, kProjRun = 16, kProjLdsMaxK = 256;
+
+// xpad row of token tt (tt < 0: the cache, or token 0 replicated) in column c
+__device__ __forceinline__ float conv_row(const float *col, int64_t ld, int tt, const float *cache, int64_t n_ch) {
+    if (tt >= 0) return col[(int64_t)tt * ld];
+    return cache ? cache[(int64_t)(3 + tt) * n_ch] : col[0];
+}
+
 __global__ __launch_bounds__(256) void project_kernel(ProjectParams p) {
     extern __shared__ float sm[];
-    const int kd = p.H * p.K, vd = p.HV * p.V;
-    float *s_q = sm, *s_k = sm + kd;
-    const int64_t m = blockIdx.x;
-    const int bi = (int)(m / p.T), t = (int)(m % p.T);
+    const int nb = (p.T + kProjTB - 1) / kProjTB;
+    const int bi = blockIdx.x / nb, t0 = (blockIdx.x % nb) * kProjTB;
+    const int tn = min(kProjTB, p.T - t0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t m0 = (int64_t)bi * p.T;
-    const float *Y = p.Y + m * p.ldY;
-    const float *Y0 = p.Y + m0 * p.ldY;
     const bool sc = p.use_short_conv != 0;
-
-    // q, k: conv (or plain) + SiLU into LDS
-    for (int c = tid; c < kd; c += 256) {
-        float aq, ak;
-        if (sc) {
-            const int64_t cb = (int64_t)bi * 3 * kd + c;
-            aq = conv4(Y0 + p.off_q + c, p.ldY, t, p.conv_q_in ? p.conv_q_in + cb : nullptr, kd, p.q_conv_w + 4 * c);
-            ak = conv4(Y0 + p.off_k + c, p.ldY, t, p.conv_k_in ? p.conv_k_in + cb : nullptr, kd, p.k_conv_w + 4 * c);
-        } else {
-            aq = Y[p.off_q + c];
-            ak = Y[p.off_k + c];
+    const int kd = p.H * p.K, vd = p.HV * p.V;
+    const float *Y0 = p.Y + (int64_t)bi * p.T * p.ldY;  // token 0 of this sequence
+    constexpr int NRUN = kProjTB / kProjRun;
+    if ((int)blockIdx.y < p.H) {
+        const int h = blockIdx.y, K = p.K, K1 = K + 1;
+        const int64_t ob = ((int64_t)bi * p.H + h) * p.T * K;  // [B, H, T, K] row of token 0
+        // staging of the activated q, k of token t0 + tl, channel c
+        const bool lds = K <= kProjLdsMaxK;
+        float *sq = lds ? sm : p.q + ob + (int64_t)t0 * K, *sk = lds ? sm + kProjTB * K1 : p.k + ob + (int64_t)t0 * K;
+        const int ld = lds ? K1 : K;
+        for (int e = tid; e < K * NRUN; e += 256) {
+            const int c = e % K, run = e / K, gc = h * K + c;
+            const int ta = t0 + run * kProjRun, tb = min(t0 + tn, ta + kProjRun);
+            if (ta >= tb) continue;
+            const float *qc = Y0 + p.off_q + gc, *kc = Y0 + p.off_k + gc;
+            float wq[4] = {0.f, 0.f, 0.f, 0.f}, wk[4] = {0.f, 0.f, 0.f, 0.f};
+            float q1 = 0.f, q2 = 0.f, q3 = 0.f, k1 = 0.f, k2 = 0.f, k3 = 0.f;  // x(t-3), x(t-2), x(t-1)
+            if (sc) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    wq[i] = p.q_conv_w[4 * gc + i];
+                    wk[i] = p.k_conv_w[4 * gc + i];
+                }
+                const int64_t cb = (int64_t)bi * 3 * kd + gc;
+                const float *cq = p.conv_q_in ? p.conv_q_in + cb : nullptr;
+                const float *ck = p.conv_k_in ? p.conv_k_in + cb : nullptr;
+                q1 = conv_row(qc, p.ldY, ta - 3, cq, kd); q2 = conv_row(qc, p.ldY, ta - 2, cq, kd);
+                q3 = conv_row(qc, p.ldY, ta - 1, cq, kd);
+                k1 = conv_row(kc, p.ldY, ta - 3, ck, kd); k2 = conv_row(kc, p.ldY, ta - 2, ck, kd);
+                k3 = conv_row(kc, p.ldY, ta - 1, ck, kd);
+            }
+            const float dtb = p.dt_bias[gc], A = expf(p.a_log[h]);
+            const float dfs = p.decay_factors ? sigmoid_(p.decay_factors[gc]) * p.one_minus_min_decay : 0.f;
+            // the run's loads first, all in flight together (rows past the end read row ta)
+            float xqs[kProjRun], xks[kProjRun], fs[kProjRun], bs[kProjRun];
+#pragma unroll
+            for (int j = 0; j < kProjRun; ++j) {
+                const int t = ta + j < tb ? ta + j : ta;
+                const int64_t row = (int64_t)t * p.ldY;
+                xqs[j] = qc[row];
+                xks[j] = kc[row];
+                fs[j] = p.F[((int64_t)bi * p.T + t) * p.ldF + gc];
+                bs[j] = Y0[row + p.off_b + gc];
+            }
+#pragma unroll
+            for (int j = 0; j < kProjRun; ++j) {
+                const int t = ta + j;
+                if (t >= tb) continue;  // (only the tail of the last block)
+                const float xq = xqs[j], xk = xks[j];
+                float uq = xq, uk = xk;
+                if (sc) {
+                    uq = q1 * wq[0] + q2 * wq[1] + q3 * wq[2] + xq * wq[3];
+                    uk = k1 * wk[0] + k2 * wk[1] + k3 * wk[2] + xk * wk[3];
+                    q1 = q2; q2 = q3; q3 = xq;
+                    k1 = k2; k2 = k3; k3 = xk;
+                }
+                sq[(t - t0) * ld + c] = silu_(uq);
+                sk[(t - t0) * ld + c] = silu_(uk);
+                // g, b (src/module.rs:417-443, :470-472)
+                float gv = -A * softplus_(fs[j] + dtb);
+                if (p.decay_factors) gv = logf(dfs * expf(gv) + p.min_decay);
+                float bv = sigmoid_(bs[j]);
+                if (p.allow_neg_eigval) bv *= 2.0f;
+                p.g[ob + (int64_t)t * K + c] = gv;
+                p.b[ob + (int64_t)t * K + c] = bv;
+            }
         }
-        s_q[c] = silu_(aq);
-        s_k[c] = silu_(ak);
-    }
-    // g, b (src/module.rs:417-443, :470-472)
-    for (int c = tid; c < kd; c += 256) {
-        float gv = -expf(p.a_log[c / p.K]) * softplus_(p.F[m * p.ldF + c] + p.dt_bias[c]);
-        if (p.decay_factors) gv = logf(sigmoid_(p.decay_factors[c]) * p.one_minus_min_decay * expf(gv) + p.min_decay);
-        float bv = sigmoid_(Y[p.off_b + c]);
-        if (p.allow_neg_eigval) bv *= 2.0f;
-        const int64_t o = ((int64_t)bi * p.H + c / p.K) * p.T * p.K + (int64_t)t * p.K + c % p.K;
-        p.g[o] = gv;
-        p.b[o] = bv;
-    }
-    // v = SiLU(conv(v_raw)), w = sigmoid(w_raw)
-    for (int c = tid; c < vd; c += 256) {
-        float av;
-        if (sc) {
-            const int64_t cb = (int64_t)bi * 3 * vd + c;
-            av = conv4(Y0 + p.off_v + c, p.ldY, t, p.conv_v_in ? p.conv_v_in + cb : nullptr, vd, p.v_conv_w + 4 * c);
-        } else {
-            av = Y[p.off_v + c];
+        __syncthreads();
+        // L2 norm per token over the head's K channels (src/l2norm.rs:13-16): a wave per token
+        for (int tl = wave; tl < tn; tl += 4) {
+            float ssq = 0.f, ssk = 0.f;
+            for (int c = lane; c < K; c += 64) {
+                const float a = sq[tl * ld + c], bq = sk[tl * ld + c];
+                ssq += a * a;
+                ssk += bq * bq;
+            }
+            ssq = wave_sum(ssq);
+            ssk = wave_sum(ssk);
+            const float nq = 1.0f / sqrtf(ssq + 1e-6f), nk = 1.0f / sqrtf(ssk + 1e-6f);
+            const int64_t o = ob + (int64_t)(t0 + tl) * K;
+            for (int c = lane; c < K; c += 64) {
+                const float a = sq[tl * ld + c], bq = sk[tl * ld + c];
+                p.q[o + c] = a * nq;
+                p.k[o + c] = bq * nk;
+            }
         }
-        const int64_t o = ((int64_t)bi * p.HV + c / p.V) * p.T * p.V + (int64_t)t * p.V + c % p.V;
-        p.v[o] = silu_(av);
-        p.w[o] = sigmoid_(Y[p.off_w + c]);
-    }
-    __syncthreads();
-    // L2 norm per head over K channels (src/l2norm.rs:13-16): one wave per head.
-    for (int h = wave; h < p.H; h += 4) {
-        float sq = 0.f, sk = 0.f;
-        for (int i = lane; i < p.K; i += 64) {
-            const float a = s_q[h * p.K + i], b = s_k[h * p.K + i];
-            sq += a * a;
-            sk += b * b;
-        }
-        sq = wave_sum(sq);
-        sk = wave_sum(sk);
-        const float nq = sqrtf(sq + 1e-6f), nk = sqrtf(sk + 1e-6f);
-        const int64_t o = ((int64_t)bi * p.H + h) * p.T * p.K + (int64_t)t * p.K;
-        for (int i = lane; i < p.K; i += 64) {
-            p.q[o + i] = s_q[h * p.K + i] / nq;
-            p.k[o + i] = s_k[h * p.K + i] / nk;
+    } else {
+        const int hv = blockIdx.y - p.H, V = p.V;
+        const int64_t ob = ((int64_t)bi * p.HV + hv) * p.T * V;  // [B, HV, T, V] row of token 0
+        for (int e = tid; e < V * NRUN; e += 256) {
+            const int c = e % V, run = e / V, gc = hv * V + c;
+            const int ta = t0 + run * kProjRun, tb = min(t0 + tn, ta + kProjRun);
+            if (ta >= tb) continue;
+            const float *vc = Y0 + p.off_v + gc;
+            float wv[4] = {0.f, 0.f, 0.f, 0.f}, v1 = 0.f, v2 = 0.f, v3 = 0.f;
+            if (sc) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) wv[i] = p.v_conv_w[4 * gc + i];
+                const float *cv = p.conv_v_in ? p.conv_v_in + (int64_t)bi * 3 * vd + gc : nullptr;
+                v1 = conv_row(vc, p.ldY, ta - 3, cv, vd); v2 = conv_row(vc, p.ldY, ta - 2, cv, vd);
+                v3 = conv_row(vc, p.ldY, ta - 1, cv, vd);
+            }
+            float xvs[kProjRun], xws[kProjRun];
+#pragma unroll
+            for (int j = 0; j < kProjRun; ++j) {
+                const int t = ta + j < tb ? ta + j : ta;
+                const int64_t row = (int64_t)t * p.ldY;
+                xvs[j] = vc[row];
+                xws[j] = Y0[row + p.off_w + gc];
+            }
+#pragma unroll
+            for (int j = 0; j < kProjRun; ++j) {
+                const int t = ta + j;
+                if (t >= tb) continue;
+                const float xv = xvs[j];
+                float uv = xv;
+                if (sc) {
+                    uv = v1 * wv[0] + v2 * wv[1] + v3 * wv[2] + xv * wv[3];
+                    v1 = v2; v2 = v3; v3 = xv;
+                }
+                p.v[ob + (int64_t)t * V + c] = silu_(uv);
+                p.w[ob + (int64_t)t * V + c] = sigmoid_(xws[j]);
+            }
         }
     }
 }
@@ -419,10 +499,19 @@ int grid_for(int64_t n) {
 
 size_t project_lds_bytes(int kd) { return sizeof(float) * 2 * (size_t)kd; }
 
+size_t project_tile_lds_bytes(int K) { return K <= kProjLdsMaxK ? sizeof(float) * 2 * (size_t)kProjTB * (K + 1) : 0; }
+
 hipError_t launch_project(const ProjectParams &p, hipStream_t s) {
     const int64_t M = (int64_t)p.B * p.T;
     if (M == 0) return hipSuccess;
-    hipLaunchKernelGGL(project_kernel, dim3((unsigned)M), dim3(256), project_lds_bytes(p.H * p.K), s, p);
+    const size_t lds = project_tile_lds_bytes(p.K);
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&project_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    const int nb = (p.T + kProjTB - 1) / kProjTB;
+    hipLaunchKernelGGL(project_kernel, dim3((unsigned)(p.B * nb), (unsigned)(p.H + p.HV)), dim3(256), lds, s, p);
     return hipGetLastError();
 }
 
