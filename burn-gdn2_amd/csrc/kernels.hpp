@@ -25,6 +25,7 @@ struct ScanParams {
 struct DecodeParams {
     const float *q_raw, *k_raw, *f_raw, *b_raw; // [B, kd]
     const float *v_raw, *w_raw, *gate;          // [B, vd]
+    const float *gate_bias;                     // [vd] added to gate, or null (gate includes it)
     const float *conv_q_in, *conv_k_in, *conv_v_in;
     float *conv_q_out, *conv_k_out, *conv_v_out;
     const float *q_conv_w, *k_conv_w, *v_conv_w;
@@ -105,11 +106,12 @@ struct ConvCacheParams {
 // row contiguous).  y = O / rms * weight * silu(G) is recomputed on the way.
 struct NormBwdParams {
     const float *O, *G, *weight;
+    const float *gate_bias; // [HV * V] added to G (row r is value head r % HV), or null
     float *dy;     // in: gradient of y; out: dy * (O / rms) * silu(G) (weight-gradient terms)
     float *y;      // out: y (input of o_proj)
     float *dO, *dG;
     int64_t rows;
-    int V;
+    int V, HV;
     float eps;
 };
 
@@ -156,9 +158,10 @@ constexpr int kChunk = 64; // chunk length of the kernels (four 16-row tiles)
 size_t project_lds_bytes(int kd);
 hipError_t launch_project(const ProjectParams &p, hipStream_t s);
 hipError_t launch_conv_cache(const ConvCacheParams &p, hipStream_t s);
+// gate_bias [HV * V] (nullable) is added to the gate before its SiLU.
 hipError_t launch_rmsnorm_gate(float *out, int64_t ld_out, const float *x, int64_t ld_x, const float *gate,
-                               int64_t ld_gate, const float *weight, int64_t M, int HV, int V, float eps,
-                               hipStream_t s);
+                               int64_t ld_gate, const float *gate_bias, const float *weight, int64_t M, int HV, int V,
+                               float eps, hipStream_t s);
 hipError_t launch_fill_rows(float *y, int64_t ld, const float *row, int64_t M, int64_t N, hipStream_t s);
 hipError_t launch_rmsnorm_gate_bwd(const NormBwdParams &p, hipStream_t s);
 hipError_t launch_project_bwd(const ProjectBwdParams &p, hipStream_t s);

@@ -256,7 +256,10 @@ gdn2_status workspace(gdn2_layer &L, int64_t B, int64_t T, bool need_s0, Work *w
 }
 
 // Linear layers of the input side: Y, F, G.
-gdn2_status input_gemms(gdn2_layer &L, const float *x, int64_t M, const Work &wk, hipStream_t s) {
+// G holds the g_proj_1 bias only with_bias; the kernels that read G otherwise
+// add it themselves (one launch less per call).
+gdn2_status input_gemms(gdn2_layer &L, const float *x, int64_t M, const Work &wk, hipStream_t s,
+                        bool with_bias = false) {
     const Dims &d = L.d;
     gdn2_status st;
     if ((st = L.mm.run(false, false, M, L.ld_in, d.D, x, d.D, L.w_in, L.ld_in, wk.Y, L.ld_in, 0.0f, s)) != GDN2_OK)
@@ -264,8 +267,9 @@ gdn2_status input_gemms(gdn2_layer &L, const float *x, int64_t M, const Work &wk
     if ((st = L.mm.run(false, false, M, d.kd, d.V, wk.Y + L.off_f0, L.ld_in, L.p[P_F1], d.kd, wk.F, d.kd, 0.0f, s)) !=
         GDN2_OK)
         return st;
-    GDN2_HIP_CHECK(launch_fill_rows(wk.G, d.vd, L.p[P_G1_BIAS], M, d.vd, s));
-    return L.mm.run(false, false, M, d.vd, d.V, wk.Y + L.off_g0, L.ld_in, L.p[P_G1], d.vd, wk.G, d.vd, 1.0f, s);
+    if (with_bias) GDN2_HIP_CHECK(launch_fill_rows(wk.G, d.vd, L.p[P_G1_BIAS], M, d.vd, s));
+    return L.mm.run(false, false, M, d.vd, d.V, wk.Y + L.off_g0, L.ld_in, L.p[P_G1], d.vd, wk.G, d.vd,
+                    with_bias ? 1.0f : 0.0f, s);
 }
 
 gdn2_status project_epilogue(gdn2_layer &L, int64_t B, int64_t T, const float *const conv_in[3], const Work &wk,
@@ -322,7 +326,8 @@ gdn2_status output_side(gdn2_layer &L, int64_t M, bool norm, const Work &wk, flo
     const Dims &d = L.d;
     float *y = normed ? normed : wk.O;
     if (norm)
-        GDN2_HIP_CHECK(launch_rmsnorm_gate(y, d.vd, wk.O, d.vd, wk.G, d.vd, L.p[P_O_NORM], M, (int)d.HV, (int)d.V,
+        GDN2_HIP_CHECK(launch_rmsnorm_gate(y, d.vd, wk.O, d.vd, wk.G, d.vd, L.p[P_G1_BIAS], L.p[P_O_NORM], M, (int)d.HV,
+                                           (int)d.V,
                                            (float)L.cfg.norm_eps, s));
     return L.mm.run(false, false, M, d.D, d.vd, y, d.vd, L.p[P_O], d.D, out, d.D, 0.0f, s);
 }
@@ -589,6 +594,7 @@ extern "C" gdn2_status gdn2_layer_forward_f32(gdn2_layer *L, const float *x, int
         DecodeParams p{};
         p.q_raw = wk.Y + L->off_q; p.k_raw = wk.Y + L->off_k; p.b_raw = wk.Y + L->off_b;
         p.v_raw = wk.Y + L->off_v; p.w_raw = wk.Y + L->off_w; p.f_raw = wk.F; p.gate = wk.G;
+        p.gate_bias = L->p[P_G1_BIAS];
         p.ld_q = p.ld_k = p.ld_b = p.ld_v = p.ld_w = L->ld_in;
         p.ld_f = d.kd; p.ld_gate = d.vd; p.ld_out = d.vd;
         p.conv_q_in = has_cache ? conv_in[0] : nullptr;
@@ -640,7 +646,7 @@ extern "C" gdn2_status gdn2_layer_project_f32(gdn2_layer *L, const float *x, int
     Work wk{};
     if ((st = workspace(*L, B, T, false, &wk)) != GDN2_OK) return st;
     const int64_t M = B * T;
-    if ((st = input_gemms(*L, x, M, wk, s)) != GDN2_OK) return st;
+    if ((st = input_gemms(*L, x, M, wk, s, true)) != GDN2_OK) return st;  // gate out with its bias
     const float *conv_in[3] = {};
     const bool has_cache = S && S->some;
     if (has_cache)
@@ -1275,7 +1281,7 @@ extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, in
     if ((st = L->mm.run(false, true, M, d.vd, d.D, d_out, d.D, L->p[P_O], d.D, bw.dy, d.vd, 0.0f, s)) != GDN2_OK)
         return st;
     NormBwdParams np{};
-    np.O = fw.O; np.G = fw.G; np.weight = L->p[P_O_NORM];
+    np.O = fw.O; np.G = fw.G; np.weight = L->p[P_O_NORM]; np.gate_bias = L->p[P_G1_BIAS]; np.HV = (int)d.HV;
     np.dy = bw.dy; np.y = bw.y; np.dO = bw.dO; np.dG = bw.dG;
     np.rows = M * d.HV; np.V = (int)d.V; np.eps = (float)L->cfg.norm_eps;
     GDN2_HIP_CHECK(launch_rmsnorm_gate_bwd(np, s));

@@ -222,8 +222,8 @@ __global__ __launch_bounds__(256) void conv_cache_kernel(ConvCacheParams p) {
 
 // rms_norm_gate_per_head (src/module.rs:501-517): one wave per (token, value head).
 __global__ __launch_bounds__(256) void rmsnorm_gate_kernel(float *out, int64_t ld_out, const float *x, int64_t ld_x,
-                                                           const float *gate, int64_t ld_gate, const float *weight,
-                                                           int64_t rows, int HV, int V, float eps) {
+                                                           const float *gate, int64_t ld_gate, const float *gate_bias,
+                                                           const float *weight, int64_t rows, int HV, int V, float eps) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (row >= rows) return;
@@ -236,7 +236,8 @@ __global__ __launch_bounds__(256) void rmsnorm_gate_kernel(float *out, int64_t l
     for (int i = lane; i < V; i += 64) ss += xr[i] * xr[i];
     ss = wave_sum(ss);
     const float rms = sqrtf(ss / (float)V + eps);
-    for (int i = lane; i < V; i += 64) orow[i] = xr[i] / rms * weight[i] * silu_(gr[i]);
+    const float *br = gate_bias ? gate_bias + (int64_t)hv * V : nullptr;
+    for (int i = lane; i < V; i += 64) orow[i] = xr[i] / rms * weight[i] * silu_(gr[i] + (br ? br[i] : 0.f));
 }
 
 __global__ __launch_bounds__(256) void fill_rows_kernel(float *y, int64_t ld, const float *row, int64_t M, int64_t N) {
@@ -261,18 +262,20 @@ __global__ __launch_bounds__(256) void rmsnorm_gate_bwd_kernel(NormBwdParams p) 
     const int64_t row = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (row >= p.rows) return;
     const int64_t o = row * p.V;
+    // gate bias of this row's value head (row = token * HV + head)
+    const float *gb = p.gate_bias ? p.gate_bias + (row % p.HV) * p.V : nullptr;
     float s1 = 0.f, s2 = 0.f;
     for (int i = lane; i < p.V; i += 64) {
         const float x = p.O[o + i];
         s1 += x * x;
-        s2 += p.dy[o + i] * p.weight[i] * silu_(p.G[o + i]) * x;
+        s2 += p.dy[o + i] * p.weight[i] * silu_(p.G[o + i] + (gb ? gb[i] : 0.f)) * x;
     }
     s1 = wave_sum(s1);
     s2 = wave_sum(s2);
     const float r = 1.0f / sqrtf(s1 / (float)p.V + p.eps);
     const float c3 = r * r * r * s2 / (float)p.V;
     for (int i = lane; i < p.V; i += 64) {
-        const float x = p.O[o + i], gt = p.G[o + i], dyv = p.dy[o + i], w = p.weight[i];
+        const float x = p.O[o + i], gt = p.G[o + i] + (gb ? gb[i] : 0.f), dyv = p.dy[o + i], w = p.weight[i];
         const float z = silu_(gt), n = x * r;
         p.y[o + i] = n * w * z;
         p.dO[o + i] = r * dyv * w * z - x * c3;
@@ -522,12 +525,12 @@ hipError_t launch_conv_cache(const ConvCacheParams &p, hipStream_t s) {
 }
 
 hipError_t launch_rmsnorm_gate(float *out, int64_t ld_out, const float *x, int64_t ld_x, const float *gate,
-                               int64_t ld_gate, const float *weight, int64_t M, int HV, int V, float eps,
-                               hipStream_t s) {
+                               int64_t ld_gate, const float *gate_bias, const float *weight, int64_t M, int HV, int V,
+                               float eps, hipStream_t s) {
     const int64_t rows = M * HV;
     if (rows == 0) return hipSuccess;
     hipLaunchKernelGGL(rmsnorm_gate_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, out, ld_out, x, ld_x,
-                       gate, ld_gate, weight, rows, HV, V, eps);
+                       gate, ld_gate, gate_bias, weight, rows, HV, V, eps);
     return hipGetLastError();
 }
 

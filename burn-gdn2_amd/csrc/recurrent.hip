@@ -322,7 +322,8 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
     const int cvc = hv * V + col;
     const int64_t xv = (int64_t)bi * p.ld_v + cvc;
     const float vr = p.v_raw[xv], wr = p.w_raw[(int64_t)bi * p.ld_w + cvc];
-    const float gt = p.gate[(int64_t)bi * p.ld_gate + cvc], onw = p.o_norm_weight[col];
+    const float gt = p.gate[(int64_t)bi * p.ld_gate + cvc] + (p.gate_bias ? p.gate_bias[cvc] : 0.f),
+                onw = p.o_norm_weight[col];
     const int64_t vcb = (int64_t)bi * 3 * vd + cvc;
     const float *cvi = (sc && p.conv_v_in) ? p.conv_v_in + vcb : p.v_raw + xv;
     const int64_t vst = (sc && p.conv_v_in) ? vd : 0;
@@ -527,7 +528,8 @@ __global__ __launch_bounds__(256) void decode_fused_generic_kernel(DecodeParams 
     n = 0;
     for (int c = tid; c < V; c += 256, ++n) {
         const int64_t ch = (int64_t)hv * V + c;
-        p.out[bi * p.ld_out + ch] = ov[n] / rms * p.o_norm_weight[c] * siluf_(p.gate[bi * p.ld_gate + ch]);
+        const float gt = p.gate[bi * p.ld_gate + ch] + (p.gate_bias ? p.gate_bias[ch] : 0.f);
+        p.out[bi * p.ld_out + ch] = ov[n] / rms * p.o_norm_weight[c] * siluf_(gt);
     }
 }
 
