@@ -480,7 +480,7 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
 // Per chunk n:
 //   A: X1 = W S, X2 = scale (q exp(G)) S      (reads sW, sQ)
 //   B: v_new = U - X1
-//   C: S = exp(G_last) S + Kd^T v_new         (reads sKd, sGam)
+//   C: S = exp(G_last) S + Kd^T v_new         (reads sKd)
 //   D: out = X2 + A_qk v_new                  (reads sA; independent of C)
 // LDS holds one chunk of W, q exp(G) (2 C K floats), Kd^T (K C) and A_qk
 // (C C).  Each buffer is refilled while another phase runs: Kd^T(n) and
@@ -520,7 +520,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     constexpr int APF = AF4 / 256;
     __shared__ floatx4 sW[OPF4], sKd[OPF4];
     __shared__ floatx4 sQ[OUT ? OPF4 : 1], sA[OUT ? AF4 : 1];
-    __shared__ floatx4 sGam[K / 4];
+    __shared__ float sPf[256]; // destination of the L2 touches, never read
 
     const int V = p.V;
     const int nvv = V / 64;                   // value slices
@@ -564,13 +564,39 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     // the operands go from global memory straight into LDS (lds_copy4):
     // thread tid's float4 i lands at index i * 256 + tid, as a wave's 64 lanes
     const int wv = 64 * wave;
+    // Each chunk's operands are also pulled toward L2 one phase before their
+    // LDS copy (l2_touch, one 128-byte line per thread): W, q exp(G) of chunk
+    // n + 1 during A(n), Kd^T, A_qk, U of chunk n + 1 during B-D(n).  Every
+    // wave issues the same count (2, then 3) last before the vmcnt waits, which
+    // leave them in flight; past the last chunk the current one is touched.
+    float *pf_slot = &sPf[wv];
+    constexpr int LOP = OPF4 / 8, LA = AF4 / 8, LU = 4 * NT * 64 / 8; // lines per operand block
+    const int vsu = pcol ? 0 : vs; // the P slices of pass 1 read no U
+    auto touch_wq = [&](size_t c) { // 2 per wave
+        l2_touch(reinterpret_cast<const char *>(W4 + c * OPF4) + 128 * (tid % LOP), pf_slot);
+        l2_touch(reinterpret_cast<const char *>((OUT ? Q4 : K4) + c * OPF4) + 128 * (tid % LOP), pf_slot);
+    };
+    auto touch_kau = [&](size_t c) { // 3 per wave
+        l2_touch(reinterpret_cast<const char *>(K4 + c * OPF4) + 128 * (tid % LOP), pf_slot);
+        if (OUT)
+            l2_touch(reinterpret_cast<const char *>(A4 + c * AF4) + 128 * (tid % LA), pf_slot);
+        else
+            l2_touch(reinterpret_cast<const char *>(W4 + c * OPF4) + 128 * (tid % LOP), pf_slot);
+        l2_touch(reinterpret_cast<const char *>(U4 + c * uvf4 + (size_t)vsu * 4 * NT * 64) + 128 * (tid % LU), pf_slot);
+    };
     if (n1 > n0) {
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
             lds_copy4(&W4[(cid0 + n0) * OPF4 + i * 256 + tid], &sW[i * 256 + wv]);
             if (OUT) lds_copy4(&Q4[(cid0 + n0) * OPF4 + i * 256 + tid], &sQ[i * 256 + wv]);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        touch_kau(cid0 + n0);
+        __builtin_amdgcn_sched_barrier(0);
     }
+    // S and the first copies have landed: nothing from before the loop is
+    // left in flight for the compiler's own vmcnt waits inside it
+    vm_wait0();
 
     // row 4 lg of each 16-row tile; the rest of the row offset is wave-uniform
     float *ob = p.out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + col + (int64_t)(4 * lg) * p.sot;
@@ -593,8 +619,9 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     floatx4 X2[NT]; // chunk n's output, stored early in iteration n + 1
     for (int n = n0; n < n1; ++n) {
         const size_t cid = cid0 + n;
-        vm_wait0();      // this wave's copies of chunk n's W, q exp(G) have landed
-        __syncthreads(); // sW, sQ hold chunk n; every wave is done with sKd, sA (n-1)
+        const size_t cnext = n + 1 < n1 ? cid + 1 : cid;
+        vm_wait<3>();  // this wave's copies of chunk n's W, q exp(G) have landed (not the 3 touches after them)
+        lds_barrier(); // sW, sQ hold chunk n; every wave is done with sKd, sA (n-1)
 #pragma unroll
         for (int i = 0; i < PFO; ++i) lds_copy4(&K4[cid * OPF4 + i * 256 + tid], &sKd[i * 256 + wv]);
         if (OUT) {
@@ -602,14 +629,13 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
             for (int i = 0; i < APF; ++i) lds_copy4(&A4[cid * AF4 + i * 256 + tid], &sA[i * 256 + wv]);
             if (n > n0) store_out(X2, n - 1);
         }
-        floatx4 u_cur[NT], g_cur = floatx4{0.f, 0.f, 0.f, 0.f};
-        if (tid < K / 4) g_cur = G4[cid * (K / 4) + tid];
+        // exp(G_last) for this lane's rows 16 kb + 4 lg .. + 3 of S
+        floatx4 u_cur[NT], gam[NKT];
+#pragma unroll
+        for (int kb = 0; kb < NKT; ++kb) gam[kb] = G4[cid * (K / 4) + 4 * kb + lg];
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt)
             u_cur[mt] = pcol ? floatx4{0.f, 0.f, 0.f, 0.f} : U4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
-        // keep these loads here, a whole phase ahead of their use and of the
-        // vmcnt wait before the next barrier
-        __builtin_amdgcn_sched_barrier(0);
         if (STATES) { // the state entering chunk n
             float *Sn = p.ws_sn + cid * K * V;
 #pragma unroll
@@ -617,6 +643,11 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
 #pragma unroll
                 for (int i = 0; i < 4; ++i) Sn[(size_t)(16 * kb + 4 * lg + i) * V + col] = S[kb][i];
         }
+        // keep these loads here, a whole phase ahead of their use and of the
+        // vmcnt wait before the next barrier, and the touches last
+        __builtin_amdgcn_sched_barrier(0);
+        touch_wq(cnext);
+        __builtin_amdgcn_sched_barrier(0);
 
         // A: X1 = W S, X2 = scale (q exp(G)) S
         floatx4 X1[NT];
@@ -639,18 +670,8 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
                     if (OUT) X2[mt] = mfma16(ma[mt][st], S[kb][st], X2[mt]);
                 }
         }
-        if (tid < K / 4) sGam[tid] = g_cur;
-        vm_wait0();      // this wave's copies of chunk n's Kd, A_qk have landed
-        __syncthreads(); // A done everywhere (sW, sQ free); sKd(n), sA(n), sGam(n) visible
-
-        // W, q exp(G) of chunk n+1
-        if (n + 1 < n1) {
-#pragma unroll
-            for (int i = 0; i < PFO; ++i) {
-                lds_copy4(&W4[(cid + 1) * OPF4 + i * 256 + tid], &sW[i * 256 + wv]);
-                if (OUT) lds_copy4(&Q4[(cid + 1) * OPF4 + i * 256 + tid], &sQ[i * 256 + wv]);
-            }
-        }
+        vm_wait<2>();  // this wave's copies of chunk n's Kd, A_qk and its U, exp(G_last) have landed (not the 2 touches)
+        lds_barrier(); // A done everywhere (sW, sQ free); sKd(n), sA(n) visible
 
         // B: v_new = U - X1 (kept in X1)
 #pragma unroll
@@ -662,6 +683,19 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
 #pragma unroll
                 for (int i = 0; i < 4; ++i) Vn[(size_t)(16 * mt + 4 * lg + i) * V + col] = X1[mt][i];
         }
+
+        // W, q exp(G) of chunk n+1, then the touches of its Kd^T, A_qk, U
+        __builtin_amdgcn_sched_barrier(0);
+        if (n + 1 < n1) {
+#pragma unroll
+            for (int i = 0; i < PFO; ++i) {
+                lds_copy4(&W4[(cid + 1) * OPF4 + i * 256 + tid], &sW[i * 256 + wv]);
+                if (OUT) lds_copy4(&Q4[(cid + 1) * OPF4 + i * 256 + tid], &sQ[i * 256 + wv]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        touch_kau(cnext);
+        __builtin_amdgcn_sched_barrier(0);
 
         // D: out = X2 + A_qk v_new (A_qk is lower block-triangular); the
         // chains of the four time tiles interleave, and the stores wait until
@@ -682,11 +716,10 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         // C: S = exp(G_last) S + Kd^T v_new
 #pragma unroll
         for (int kb = 0; kb < NKT; ++kb) {
-            const floatx4 gm = sGam[4 * kb + lg];
-            S[kb][0] *= gm[0];
-            S[kb][1] *= gm[1];
-            S[kb][2] *= gm[2];
-            S[kb][3] *= gm[3];
+            S[kb][0] *= gam[kb][0];
+            S[kb][1] *= gam[kb][1];
+            S[kb][2] *= gam[kb][2];
+            S[kb][3] *= gam[kb][3];
         }
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt) {
@@ -704,6 +737,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
             for (int kb = 0; kb < NKT; ++kb) S[kb] = mfma16(ka[kb][3], X1[tt][3], S[kb]);
         }
     }
+    vm_wait0(); // the last touches have landed in sPf
     if (OUT && n1 > n0) store_out(X2, n1 - 1);
 
     // leaving state: the final state (last segment), Q_j or P_j (pass 1)

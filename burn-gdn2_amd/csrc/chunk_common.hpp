@@ -68,10 +68,6 @@ __device__ __forceinline__ floatx4 exp2v(floatx4 x) {
     return floatx4{fast_exp2(x[0]), fast_exp2(x[1]), fast_exp2(x[2]), fast_exp2(x[3])};
 }
 
-// Sequences are spread over the 8 XCDs (workgroup i runs on XCD i % 8) so
-// that the V-slices of one sequence, which read the same W, M and Kd^T,
-// land on the same XCD and share its L2.  Identity when the sequence count
-// is not a multiple of 8.
 // Direct global -> LDS copy of one float4 per lane (global_load_lds_dwordx4):
 // lane l of the calling wave writes wave_base[l]; wave_base is wave-uniform.
 // The copy counts in vmcnt: wait with vm_wait0() before the barrier that
@@ -80,9 +76,35 @@ __device__ __forceinline__ void lds_copy4(const floatx4 *src, floatx4 *wave_base
     __builtin_amdgcn_global_load_lds(static_cast<const void *>(src),
                                      (__attribute__((address_space(3))) void *)(wave_base), 16, 0, 0);
 }
-// s_waitcnt vmcnt(0) (expcnt and lgkmcnt not waited on)
-__device__ __forceinline__ void vm_wait0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// Pulls the 128-byte line holding `line` toward this XCD's L2: a 4-byte copy
+// into the calling lane's word of wave_slot (64 floats per wave, never read).
+// It counts in vmcnt like lds_copy4, so a wait that must not cover it leaves
+// it among the most recent operations (vm_wait<N>).
+__device__ __forceinline__ void l2_touch(const void *line, float *wave_slot) {
+    __builtin_amdgcn_global_load_lds(line, (__attribute__((address_space(3))) void *)(wave_slot), 4, 0, 0);
+}
+// s_waitcnt vmcnt(N): every vector memory operation of the wave but the N
+// most recent has completed (they complete in issue order); expcnt and
+// lgkmcnt are not waited on.
+template <int N> __device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void vm_wait0() { vm_wait<0>(); }
+// Workgroup barrier that leaves vmcnt alone (__syncthreads' fence would wait
+// for every copy and touch in flight): lgkmcnt(0) completes this wave's LDS
+// accesses, and the asm's memory clobber keeps the compiler from moving
+// memory accesses across it.  The caller's vm_wait<N>() decides which
+// global -> LDS copies have landed.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0); vmcnt(63) and expcnt(7) are no-ops
+    asm volatile("s_barrier" ::: "memory");
+}
 
+// Sequences are spread over the 8 XCDs (workgroup i runs on XCD i % 8) so
+// that the V-slices of one sequence, which read the same W, M and Kd^T,
+// land on the same XCD and share its L2.  Identity when the sequence count
+// is not a multiple of 8.
 __device__ __forceinline__ void inter_block(int blk, int nseq, int nvs, int *bh, int *vs) {
     if (nseq % 8 == 0) {
         const int x = blk % 8, j = blk / 8;
