@@ -625,8 +625,11 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
 #pragma unroll
         for (int i = 0; i < PFO; ++i) lds_copy4(&K4[cid * OPF4 + i * 256 + tid], &sKd[i * 256 + wv]);
         if (OUT) {
+            // A_qk is lower block-triangular: copy i brings tile (i, wave), so
+            // wave w copies only i >= w (10 of the 16 tiles)
 #pragma unroll
-            for (int i = 0; i < APF; ++i) lds_copy4(&A4[cid * AF4 + i * 256 + tid], &sA[i * 256 + wv]);
+            for (int i = 0; i < APF; ++i)
+                if (i >= wave) lds_copy4(&A4[cid * AF4 + i * 256 + tid], &sA[i * 256 + wv]);
             if (n > n0) store_out(X2, n - 1);
         }
         // exp(G_last) for this lane's rows 16 kb + 4 lg .. + 3 of S
