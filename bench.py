@@ -62,6 +62,10 @@ def parse():
                     help="end with a 1 GiB device-to-device copy (reference kernel for HBM counters)")
     ap.add_argument("--stats-summary", metavar="KERNEL_STATS_CSV",
                     help="host only: print a rocprofv3 --stats kernel table as markdown and exit")
+    ap.add_argument("--timed-summary", metavar="KERNEL_TRACE_CSV",
+                    help="host only: mean duration of the dispatches inside bench.py's timed regions (chunk-intra, "
+                         "chunk-inter, decode) in a rocprofv3 kernel trace of a default run with the same "
+                         "--warmup/--steps/--decode-steps")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="host only: per-launch HBM bytes from two rocprofv3 --pmc runs (FETCH_SIZE, "
                          "WRITE_SIZE) of this script with --copy-calibration; writes profiles/*_traffic.json")
@@ -373,6 +377,25 @@ def stats_summary(path):
               f"{pct:.1f} |")
 
 
+def timed_summary(path, warmup, steps, decode_steps):
+    """The timed dispatches of the prefill core (the first warmup + steps
+    launches of each kernel, warm-ups skipped) and of the decode kernel (eight
+    warm-up launches, then decode_steps), as the bench line's kernel times
+    see them."""
+    import csv
+
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    print("| kernel | timed dispatches | mean us | min us | max us |")
+    print("|---|---|---|---|---|")
+    for label, key, skip, take in (("chunk_intra", "chunk_intra_kernel<128, 128, false>", warmup, steps),
+                                   ("chunk_inter", "chunk_inter_kernel<128, 0>", warmup, steps),
+                                   ("decode", "decode_fused_kernel<128, 128>", 8, decode_steps)):
+        d = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows
+             if _short(r["Kernel_Name"]) == key][skip:skip + take]
+        if d:
+            print(f"| `{key}` ({label}) | {len(d)} | {sum(d) / len(d):.1f} | {min(d):.1f} | {max(d):.1f} |")
+
+
 def train_summary(path):
     """The kernels of the last training step of a --train-only trace: from the
     forward's input GEMM (four launches before its project_kernel) to the end."""
@@ -500,6 +523,9 @@ def main():
         return
     if args.train_summary:
         train_summary(args.train_summary)
+        return
+    if args.timed_summary:
+        timed_summary(args.timed_summary, args.warmup, args.steps, args.decode_steps)
         return
     if args.traffic_summary:
         traffic_summary(*args.traffic_summary)
