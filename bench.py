@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-batch", type=int, default=8)
+    ap.add_argument("--cpu-layer-tokens", type=int, default=4096,
+                    help="tokens of the one-sequence sample of the full-layer CPU baseline")
     ap.add_argument("--no-layer", action="store_true")
     ap.add_argument("--layer-steps", type=int, default=5)
     ap.add_argument("--decode-prefill", type=int, default=2048)
@@ -325,7 +327,30 @@ def cpu_baseline(pre, args):
     return {"value": n * T / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"{n} of 8 sequences x {T} tokens x 16 heads, f32 chunk_wy_forward restatement "
                       f"(oracle/gdn2_oracle.c), {cores} OpenMP threads, {dt:.2f} s",
-            "cpu_model": _cpu_model()}
+            "cpu_model": _cpu_model(), "layer": cpu_layer_baseline(args)}
+
+
+def cpu_layer_baseline(args):
+    """The whole layer's forward_train on the host cores, the way the
+    reference's CPU backend computes it (f32 Linear layers through BLAS sgemm,
+    the gates and norms, chunk_wy_forward as the core), on one sequence of
+    cpu_layer_tokens tokens of the benchmarked layer (D=2048, H=16, K=V=128)."""
+    import numpy as np
+
+    import gdn2_amd as G
+    from oracle import oracle as O
+
+    cfg = G.Gdn2Config(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0, mode="chunk", chunk_size=64)
+    W = G.init_params(cfg, seed=1337)
+    T = args.cpu_layer_tokens
+    x = np.random.default_rng(42).standard_normal((1, T, cfg.hidden_size)).astype(np.float32)
+    O.layer_forward_f32_host(cfg, W, x[:, :64])  # warm-up
+    t0 = time.perf_counter()
+    O.layer_forward_f32_host(cfg, W, x)
+    dt = time.perf_counter() - t0
+    return {"value": T / dt, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
+            "sample": f"1 sequence x {T} tokens of the D=2048 layer's forward_train: numpy f32 sgemm Linear layers "
+                      f"+ numpy f32 glue + f32 chunk_wy_forward restatement (oracle), {dt:.2f} s"}
 
 
 def _cpu_model():

@@ -311,6 +311,60 @@ def layer_from_raw(cfg, weights: dict, raw: dict, state: Optional[OracleState] =
     return on, oc, OracleState(S, cq, ck, cv)
 
 
+def layer_forward_f32_host(cfg, weights: dict, x):
+    """forward_train(x) from a zero state the way the reference's CPU backend
+    computes it, as f32 tensor operations: Linear layers through BLAS sgemm
+    (numpy), short conv as four shifted multiply-adds over the replicate-padded
+    input (src/short_conv.rs:22-65), the gates (src/module.rs:417-443), L2
+    norm (src/l2norm.rs:13-16), the f32 chunk_wy_forward restatement
+    (src/forward.rs:44-278) and gated RMSNorm (src/module.rs:501-517).  Used as
+    bench.py's full-layer CPU baseline; tests/test_oracle.py checks it against
+    layer_forward.  Short conv on; GVA, neg-eig and min_decay are not covered.
+    Returns out [B, T, D] (float32)."""
+    H, K = cfg.num_heads, cfg.head_dim
+    HV = cfg.num_v_heads or H
+    V = int(K * cfg.expand_v)
+    if HV != H or cfg.allow_neg_eigval or cfg.min_decay is not None or not cfg.use_short_conv:
+        raise ValueError("layer_forward_f32_host: short conv on, HV == H, no neg-eig, no min_decay only")
+    kd, vd = H * K, HV * V
+    W = {n: (None if a is None else np.asarray(a, np.float32)) for n, a in weights.items()}
+    x = _c(x, np.float32)
+    B, T, D = x.shape
+    x2 = x.reshape(B * T, D)
+
+    def silu(a):
+        return a / (np.float32(1) + np.exp(-a))
+
+    def conv(n_proj, n_w, n):
+        y = (x2 @ W[n_proj]).reshape(B, T, n)
+        pad = np.concatenate([np.repeat(y[:, :1], 3, axis=1), y], axis=1)
+        wc = W[n_w]
+        acc = pad[:, 0:T] * wc[:, 0]
+        for i in range(1, 4):
+            acc += pad[:, i:i + T] * wc[:, i]
+        return silu(acc)
+
+    def heads(a, n):  # [B, T, H * n] -> [B, H, T, n]
+        return np.ascontiguousarray(a.reshape(B, T, -1, n).transpose(0, 2, 1, 3), dtype=np.float32)
+
+    def l2n(a):
+        return a / np.sqrt(np.sum(a * a, axis=-1, keepdims=True) + np.float32(1e-6))
+
+    q = l2n(heads(conv("q_proj", "q_conv_w", kd), K))
+    k = l2n(heads(conv("k_proj", "k_conv_w", kd), K))
+    v = heads(conv("v_proj", "v_conv_w", vd), V)
+    f = ((x2 @ W["f_proj_0"]) @ W["f_proj_1"]).reshape(B, T, H, K) + W["dt_bias"].reshape(H, K)
+    g = -np.exp(W["a_log"])[:, None] * np.logaddexp(np.float32(0), f)
+    b = np.float32(1) / (np.float32(1) + np.exp(-(x2 @ W["b_proj"])))
+    w = np.float32(1) / (np.float32(1) + np.exp(-(x2 @ W["w_proj"])))
+    gate = ((x2 @ W["g_proj_0"]) @ W["g_proj_1"] + W["g_proj_1_bias"]).reshape(B, T, HV, V)
+    o, _ = chunk_wy_f32(q, k, v, heads(g.reshape(B, T, kd), K), heads(b, K), heads(w, V), scale=K ** -0.5,
+                        chunk_size=cfg.chunk_size)
+    o = o.transpose(0, 2, 1, 3)  # [B, T, HV, V]
+    y = o / np.sqrt(np.mean(o * o, axis=-1, keepdims=True) + np.float32(cfg.norm_eps)) * W["o_norm_weight"] * silu(gate)
+    return (y.reshape(B * T, vd) @ W["o_proj"]).reshape(B, T, D).astype(np.float32)
+
+
 # ---------------------------------------------------------------------------
 # Layer adjoint (the gradients burn's autodiff takes through forward /
 # forward_train, tests/autodiff.rs:153-205), in double.

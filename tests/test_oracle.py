@@ -279,6 +279,20 @@ def test_layer_from_raw_is_the_layer_after_its_linears():
     assert maxabs(oc, full.o_core) < 1e-12 and maxabs(st2.recurrent, st.recurrent) < 1e-12
 
 
+def test_layer_forward_f32_host_matches_layer_forward():
+    """The f32 host layer (BLAS Linear layers + chunk_wy_f32; bench.py's CPU
+    layer baseline) computes forward_train: ragged T, two batch rows."""
+    cfg = Cfg(hidden_size=64, num_heads=2, head_dim=32, mode="chunk")
+    W = init_weights(cfg, seed=6)
+    x = np.random.default_rng(17).standard_normal((2, 100, 64)).astype(np.float32)
+    full, _ = O.layer_forward(cfg, W, x)
+    host = O.layer_forward_f32_host(cfg, W, x)
+    assert host.dtype == np.float32 and host.shape == full.out.shape
+    assert maxabs(host, full.out) <= 1e-4 * np.abs(full.out).max()
+    with pytest.raises(ValueError):
+        O.layer_forward_f32_host(Cfg(hidden_size=64, num_heads=2, head_dim=32, allow_neg_eigval=True), W, x)
+
+
 def test_gva_reference_layout_scrambles_time():
     """The reference's unsqueeze/repeat/reshape (src/module.rs:459-463) maps
     value head h*rep+j at time t to key-side time (j*T + t) // rep: decode no
