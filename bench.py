@@ -130,16 +130,17 @@ def bench_prefill(torch, G, args, dev):
         e2.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    intra_ms = sum(e0.elapsed_time(e1) for e0, e1, _ in evs) / args.steps
-    inter_ms = sum(e1.elapsed_time(e2) for _, e1, e2 in evs) / args.steps
+    intra_all = [e0.elapsed_time(e1) for e0, e1, _ in evs]
+    inter_all = [e1.elapsed_time(e2) for _, e1, e2 in evs]
+    intra_ms, inter_ms = sum(intra_all) / args.steps, sum(inter_all) / args.steps
     ms_per_step = wall * 1e3 / args.steps
     tokens = B * T
     intra_gflop = B * H * T * 2 * C * (3 * K + V) / 1e9
     inter_gflop = B * H * T * (6 * K * V + 2 * C * V) / 1e9
     kernels = {
-        "chunk_intra": {"ms": intra_ms, "gflop": intra_gflop,
+        "chunk_intra": {"ms": intra_ms, "ms_median": _median(intra_all), "gflop": intra_gflop,
                         "tflops": intra_gflop / intra_ms, "frac_f32_mfma": intra_gflop / intra_ms / PEAK_F32_TFLOPS},
-        "chunk_inter": {"ms": inter_ms, "gflop": inter_gflop,
+        "chunk_inter": {"ms": inter_ms, "ms_median": _median(inter_all), "gflop": inter_gflop,
                         "tflops": inter_gflop / inter_ms, "frac_f32_mfma": inter_gflop / inter_ms / PEAK_F32_TFLOPS},
     }
     dom = "chunk_intra" if intra_ms >= inter_ms else "chunk_inter"
@@ -351,6 +352,12 @@ def cpu_layer_baseline(args):
     return {"value": T / dt, "unit": "tokens/s", "cores": O.num_threads(), "kind": "port",
             "sample": f"1 sequence x {T} tokens of the D=2048 layer's forward_train: numpy f32 sgemm Linear layers "
                       f"+ numpy f32 glue + f32 chunk_wy_forward restatement (oracle), {dt:.2f} s"}
+
+
+def _median(xs):
+    ys = sorted(xs)
+    n = len(ys)
+    return ys[n // 2] if n % 2 else 0.5 * (ys[n // 2 - 1] + ys[n // 2])
 
 
 def _cpu_model():
