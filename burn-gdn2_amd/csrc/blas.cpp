@@ -74,7 +74,13 @@ gdn2_status Gemm::plan(bool ta, bool tb, int64_t M, int64_t N, int64_t Kd, const
     // second operand: A's memory, column-major [Kd, M] (op N) or [M, Kd] (op T)
     ok = ok && hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_32F, ta ? M : Kd, ta ? Kd : M, lda) == HIPBLAS_STATUS_SUCCESS;
     ok = ok && hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc) == HIPBLAS_STATUS_SUCCESS;
-    if (!ok) return fail(GDN2_EHIP, "hipBLASLt descriptor creation failed");
+    if (!ok) {
+        if (p.la) hipblasLtMatrixLayoutDestroy(p.la);
+        if (p.lb) hipblasLtMatrixLayoutDestroy(p.lb);
+        if (p.lc) hipblasLtMatrixLayoutDestroy(p.lc);
+        if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+        return fail(GDN2_EHIP, "hipBLASLt descriptor creation failed");
+    }
     hipblasLtMatmulPreference_t pref;
     if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS)
         return fail(GDN2_EHIP, "hipblasLtMatmulPreferenceCreate failed");
