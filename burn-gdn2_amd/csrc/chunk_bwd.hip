@@ -69,10 +69,11 @@ __device__ __forceinline__ floatx4 mfma4x(floatx4 a, floatx4 b, floatx4 c) {
 // Per chunk n, last to first:
 //   1: dv_new = A_qk^T dO + Kd dS'         (reads sAT, sKd)
 //      dS' and dv_new go to the workspace for the per-chunk kernels
-//   2: dS' <- e^{G_last} dS' + QG^T dO - W^T dv_new   (reads sQT, sWT, sGam)
+//   2: dS' <- e^{G_last} dS' + QG^T dO - W^T dv_new   (reads sQT, sWT)
 // The operands are A-operand fragments written by the training forward, so
 // every product has the shape of the forward's chunk-inter products.  As
-// there, each LDS buffer is refilled while the other phase runs.
+// there, each LDS buffer is refilled by direct copies while the other phase
+// runs, behind fence-free barriers that wait only for those copies.
 //
 // Segmented form (NSEG > 1), the mirror of the forward's: over a segment the
 // map from the gradient leaving it to the gradient entering it is affine,
@@ -93,7 +94,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
     constexpr int OPF4 = NKT * NT * 64, PFO = OPF4 / 256;
     constexpr int AF4 = NT * NT * 64, APF = AF4 / 256;
     __shared__ floatx4 sKd[OPF4], sAT[AF4], sQT[OPF4], sWT[OPF4];
-    __shared__ floatx4 sGam[K / 4];
+    __shared__ float sPf[256]; // destination of the L2 touches, never read
 
     const int V = p.V, nvv = V / 64;
     int sq, vs;
@@ -125,34 +126,75 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
     const floatx4 *__restrict__ WT4 = reinterpret_cast<const floatx4 *>(p.ws_wt);
     const floatx4 *__restrict__ G4 = reinterpret_cast<const floatx4 *>(p.ws_gam);
     const size_t cid0 = (size_t)bh * p.NC;
+    const int wv = 64 * wave;
 
-    if (n1 > n0) {
-        const size_t cl = cid0 + n1 - 1;
+    // The operands go from global memory straight into LDS (lds_copy4: thread
+    // tid's float4 i lands at index i * 256 + tid).  Each is also pulled
+    // toward L2 ahead of its copy (l2_touch, one 128-byte line per thread):
+    // Kd, A_qk^T of chunk n - 2 during phase 1 of chunk n, QT, WT of chunk
+    // n - 1 during phase 2 of chunk n.  Each wave issues 2 touches last before
+    // every vmcnt wait, which leaves them in flight; outside the segment the
+    // chunk is clamped to it.
+    float *pf_slot = &sPf[wv];
+    constexpr int LOP = OPF4 / 8, LA = AF4 / 8; // 128-byte lines per operand block
+    auto clamp_c = [&](int n) { return cid0 + (size_t)max(n0, min(n1 - 1, n)); };
+    auto touch_ka = [&](size_t c) {
+        l2_touch(reinterpret_cast<const char *>(KD4 + c * OPF4) + 128 * (tid % LOP), pf_slot);
+        l2_touch(reinterpret_cast<const char *>(AT4 + c * AF4) + 128 * (tid % LA), pf_slot);
+    };
+    auto touch_qw = [&](size_t c) {
+        l2_touch(reinterpret_cast<const char *>(QT4 + c * OPF4) + 128 * (tid % LOP), pf_slot);
+        l2_touch(reinterpret_cast<const char *>(WT4 + c * OPF4) + 128 * (tid % LOP), pf_slot);
+    };
+    auto copy_ka = [&](size_t c) {
 #pragma unroll
-        for (int i = 0; i < PFO; ++i) sKd[i * 256 + tid] = KD4[cl * OPF4 + i * 256 + tid];
+        for (int i = 0; i < PFO; ++i) lds_copy4(&KD4[c * OPF4 + i * 256 + tid], &sKd[i * 256 + wv]);
 #pragma unroll
-        for (int i = 0; i < APF; ++i) sAT[i * 256 + tid] = AT4[cl * AF4 + i * 256 + tid];
-    }
+        for (int i = 0; i < APF; ++i) lds_copy4(&AT4[c * AF4 + i * 256 + tid], &sAT[i * 256 + wv]);
+    };
     // row 4 lg of each 16-row tile of d_out; the rest of the row offset is wave-uniform
     const float *dob = bp.d_out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + col + (int64_t)(4 * lg) * p.sot;
-
-    for (int n = n1 - 1; n >= n0; --n) {
-        const size_t cid = cid0 + n;
-        __syncthreads(); // sKd, sAT hold chunk n; every wave is done with sQT, sWT (n+1)
-        floatx4 qpre[PFO], wpre[PFO], g_cur = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < PFO; ++i) {
-            qpre[i] = QT4[cid * OPF4 + i * 256 + tid];
-            wpre[i] = WT4[cid * OPF4 + i * 256 + tid];
-        }
-        if (tid < K / 4) g_cur = G4[cid * (K / 4) + tid];
+    auto load_dO = [&](floatx4 *dO, int n) {
         const int cv = min(C, p.T - n * C);
-        floatx4 dO[NT];
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 dO[mt][i] = (16 * mt + 4 * lg + i < cv) ? dob[(int64_t)(n * C + 16 * mt + i) * p.sot] : 0.f;
+    };
+
+    floatx4 dO[NT]; // rows of d_out of the current chunk, loaded a phase ahead
+    if (n1 > n0) {
+        copy_ka(cid0 + n1 - 1);
+        load_dO(dO, n1 - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        touch_qw(cid0 + n1 - 1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // dS and the first copies have landed: nothing from before the loop is
+    // left in flight for the compiler's own vmcnt waits inside it
+    vm_wait0();
+
+    for (int n = n1 - 1; n >= n0; --n) {
+        const size_t cid = cid0 + n;
+        vm_wait<2>();  // this wave's copies of Kd, A_qk^T (n) and its dO rows have landed (not the 2 touches)
+        lds_barrier(); // sKd, sAT hold chunk n; every wave is done with sQT, sWT (n+1)
+#pragma unroll
+        for (int i = 0; i < PFO; ++i) {
+            lds_copy4(&QT4[cid * OPF4 + i * 256 + tid], &sQT[i * 256 + wv]);
+            lds_copy4(&WT4[cid * OPF4 + i * 256 + tid], &sWT[i * 256 + wv]);
+        }
+        if (!LOCAL) { // dL/d(state leaving chunk n)
+            float *Dsn = bp.ws_dsn + cid * K * V;
+#pragma unroll
+            for (int kb = 0; kb < NKT; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) Dsn[(size_t)(16 * kb + 4 * lg + i) * V + col] = dS[kb][i];
+        }
+        // e^{G_last} for this lane's rows 16 kb + 4 lg .. + 3 of dS'
+        floatx4 gam[NKT];
+#pragma unroll
+        for (int kb = 0; kb < NKT; ++kb) gam[kb] = G4[cid * (K / 4) + 4 * kb + lg];
 
         // 1: dv_new = Kd dS' + A_qk^T dO (A_qk^T is upper block-triangular)
         floatx4 dvn[NT];
@@ -172,13 +214,20 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
         for (int st = 0; st < NT; ++st)
 #pragma unroll
             for (int rt = st; rt < NT; ++rt) dvn[st] = mfma4x(sAT[(st * NT + rt) * 64 + lane], dO[rt], dvn[st]);
+        __builtin_amdgcn_sched_barrier(0);
+        touch_ka(clamp_c(n - 2));
+        __builtin_amdgcn_sched_barrier(0);
+        vm_wait<2>();  // this wave's copies of QT, WT (n) and its e^{G_last} have landed (not the 2 touches)
+        lds_barrier(); // phase 1 done everywhere (sKd, sAT free); sQT, sWT (n) visible
 
+        // Kd, A_qk^T and the dO rows of chunk n - 1; dv_new to the workspace
+        floatx4 dO_next[NT];
+        __builtin_amdgcn_sched_barrier(0);
+        if (n > n0) {
+            copy_ka(cid - 1);
+            load_dO(dO_next, n - 1);
+        }
         if (!LOCAL) {
-            float *Dsn = bp.ws_dsn + cid * K * V;
-#pragma unroll
-            for (int kb = 0; kb < NKT; ++kb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) Dsn[(size_t)(16 * kb + 4 * lg + i) * V + col] = dS[kb][i];
             float *Dvn = bp.ws_dvn + cid * C * V;
 #pragma unroll
             for (int st = 0; st < NT; ++st)
@@ -189,30 +238,17 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
 #pragma unroll
             for (int st = 0; st < NT; ++st) Dvf[(st * nvt + vt) * 64 + lane] = dvn[st];
         }
-#pragma unroll
-        for (int i = 0; i < PFO; ++i) {
-            sQT[i * 256 + tid] = qpre[i];
-            sWT[i * 256 + tid] = wpre[i];
-        }
-        if (tid < K / 4) sGam[tid] = g_cur;
-        __syncthreads(); // phase 1 done everywhere (sKd, sAT free); sQT, sWT, sGam (n) visible
-
-        // Kd, A_qk^T of chunk n-1 (the segment's first chunk re-fetches itself)
-        const size_t cpv = cid - (n > n0 ? 1 : 0);
-        floatx4 kpre[PFO], apre[APF];
-#pragma unroll
-        for (int i = 0; i < PFO; ++i) kpre[i] = KD4[cpv * OPF4 + i * 256 + tid];
-#pragma unroll
-        for (int i = 0; i < APF; ++i) apre[i] = AT4[cpv * AF4 + i * 256 + tid];
+        __builtin_amdgcn_sched_barrier(0);
+        touch_qw(clamp_c(n - 1));
+        __builtin_amdgcn_sched_barrier(0);
 
         // 2: dS' <- e^{G_last} dS' + QG^T dO - W^T dv_new
 #pragma unroll
         for (int kb = 0; kb < NKT; ++kb) {
-            const floatx4 gm = sGam[4 * kb + lg];
-            dS[kb][0] *= gm[0];
-            dS[kb][1] *= gm[1];
-            dS[kb][2] *= gm[2];
-            dS[kb][3] *= gm[3];
+            dS[kb][0] *= gam[kb][0];
+            dS[kb][1] *= gam[kb][1];
+            dS[kb][2] *= gam[kb][2];
+            dS[kb][3] *= gam[kb][3];
         }
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt) {
@@ -230,11 +266,12 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
                     dS[kb] = mfma16(-wa[kb][j], dvn[tt][j], dS[kb]);
                 }
         }
+        if (n > n0) {
 #pragma unroll
-        for (int i = 0; i < PFO; ++i) sKd[i * 256 + tid] = kpre[i];
-#pragma unroll
-        for (int i = 0; i < APF; ++i) sAT[i * 256 + tid] = apre[i];
+            for (int mt = 0; mt < NT; ++mt) dO[mt] = dO_next[mt];
+        }
     }
+    vm_wait0(); // the last touches have landed in sPf
     // the gradient entering the segment: dS0 (first segment) or R_j (pass 1)
     float *out = nullptr;
     if (!LOCAL) {
