@@ -415,9 +415,9 @@ __global__ __launch_bounds__(256) void conv_bwd_kernel(ConvBwdParams p) {
     const float w[4] = {wc[4 * cc], wc[4 * cc + 1], wc[4 * cc + 2], wc[4 * cc + 3]};
     const int T = p.T;
     const int64_t ldu = Ctot;
-    const float *du = p.DU + (int64_t)bi * T * ldu + c;
-    const float *x = p.Y + (int64_t)bi * T * p.ldY + col;
-    float *dx = p.dY + (int64_t)bi * T * p.ldY + col;
+    const float *__restrict__ du = p.DU + (int64_t)bi * T * ldu + c;
+    const float *__restrict__ x = p.Y + (int64_t)bi * T * p.ldY + col;
+    float *__restrict__ dx = p.dY + (int64_t)bi * T * p.ldY + col;
     auto xpad = [&](int j) -> float {
         if (j >= 3) return x[(int64_t)(j - 3) * p.ldY];
         return cache ? cache[(int64_t)j * n] : x[0];
@@ -434,15 +434,31 @@ __global__ __launch_bounds__(256) void conv_bwd_kernel(ConvBwdParams p) {
     };
     const int t0 = blk * p.tblock, t1 = min(T, t0 + p.tblock);
     float dw0 = 0.f, dw1 = 0.f, dw2 = 0.f, dw3 = 0.f;
+    // sliding windows, one new du and one new x per token:
+    //   xw_i = xpad[t + i],  g_i = du[t + i] (0 past T), so that
+    //   dw_i += g_0 xw_i  and  dxpad[t + 3] = g_3 w_0 + g_2 w_1 + g_1 w_2 + g_0 w_3
+    float xw0 = xpad(t0), xw1 = xpad(t0 + 1), xw2 = xpad(t0 + 2);
+    float g0 = t0 < T ? du[(int64_t)t0 * ldu] : 0.f;
+    float g1 = t0 + 1 < T ? du[(int64_t)(t0 + 1) * ldu] : 0.f;
+    float g2 = t0 + 2 < T ? du[(int64_t)(t0 + 2) * ldu] : 0.f;
+#pragma unroll 4
     for (int t = t0; t < t1; ++t) {
-        const float g = du[(int64_t)t * ldu];
-        dw0 += g * xpad(t);
-        dw1 += g * xpad(t + 1);
-        dw2 += g * xpad(t + 2);
-        dw3 += g * xpad(t + 3);
-        float d = dxpad(t + 3);
+        const float xw3 = x[(int64_t)t * p.ldY];
+        const float g3 = t + 3 < T ? du[(int64_t)(t + 3) * ldu] : 0.f;
+        dw0 += g0 * xw0;
+        dw1 += g0 * xw1;
+        dw2 += g0 * xw2;
+        dw3 += g0 * xw3;
+        float d = g3 * w[0] + g2 * w[1] + g1 * w[2] + g0 * w[3];
+        if (dco && t + 3 >= T) d += dco[(int64_t)(t + 3 - T) * n];
         if (t == 0 && !cache) d += dxpad(0) + dxpad(1) + dxpad(2);
         dx[(int64_t)t * p.ldY] = d;
+        xw0 = xw1;
+        xw1 = xw2;
+        xw2 = xw3;
+        g0 = g1;
+        g1 = g2;
+        g2 = g3;
     }
     if (blk == 0 && cache && dci)
         for (int j = 0; j < 3; ++j) dci[(int64_t)j * n] = dxpad(j);
