@@ -430,13 +430,26 @@ def timed_summary(path, warmup, steps, decode_steps):
 
 def train_summary(path):
     """The kernels of the last training step of a --train-only trace: from the
-    forward's input GEMM (four launches before its project_kernel) to the end."""
+    forward's input GEMM (the long GEMM before its project_kernel) to the end."""
     import csv
     import re
 
     rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
     last = max(i for i, r in enumerate(rows) if "project_kernel" in r["Kernel_Name"])
-    step = rows[last - 4:]
+    # the step starts at the input GEMM: walk back over the GEMM and fill
+    # launches before project_kernel up to the first long (> 1 ms) GEMM, which
+    # is x W_in; the one before it is the previous step's dx GEMM
+    start, big = last, 0
+    for i in range(last - 1, -1, -1):
+        name = rows[i]["Kernel_Name"]
+        if not (name.startswith("Cijk") or "fill_rows" in name):
+            break
+        if int(rows[i]["End_Timestamp"]) - int(rows[i]["Start_Timestamp"]) > 1_000_000:
+            big += 1
+            if big > 1:
+                break
+        start = i
+    step = rows[start:]
     t0 = int(step[0]["Start_Timestamp"])
     print("| start us | duration us | kernel |")
     print("|---|---|---|")
