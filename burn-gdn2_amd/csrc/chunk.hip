@@ -502,15 +502,17 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
 //     last segment writes the final state.
 // With NSEG = 1 pass 3 alone is the plain sequential kernel.
 //
-// MODE: kInterOut (pass 3), kInterLocal (pass 1) or kInterStates, pass 3 for
+// MODE: kInterOut (pass 3), kInterLocal (pass 1), kInterStates (pass 3 for
 // the backward: no output and no final state; instead the state entering
-// every chunk (ws_sn) and every chunk's v_new (ws_vn).
+// every chunk (ws_sn) and every chunk's v_new (ws_vn)) or kInterOutStates
+// (pass 3 with both, the reference's fused_chunk_forward tuple).
 // ---------------------------------------------------------------------------
-constexpr int kInterOut = 0, kInterLocal = 1, kInterStates = 2;
+constexpr int kInterOut = 0, kInterLocal = 1, kInterStates = 2, kInterOutStates = 3;
 
 template <int K, int MODE>
 __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int nseg_launch) {
-    constexpr bool OUT = MODE == kInterOut, LOCAL = MODE == kInterLocal, STATES = MODE == kInterStates;
+    constexpr bool OUT = MODE == kInterOut || MODE == kInterOutStates, LOCAL = MODE == kInterLocal;
+    constexpr bool STATES = MODE == kInterStates || MODE == kInterOutStates;
     constexpr int NKT = K / 16;
     constexpr int FR = NKT * NT;   // 16x16 fragments per operand per chunk
     constexpr int OPF4 = FR * 64;  // float4 per operand per chunk
@@ -828,7 +830,7 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    if (phases & 6) {
+    if (phases & 14) {
         const int seqs = p.B * p.HV;
         if (p.NSEG > 1) {
             // the training forward (phases & 4) also takes the last segment's P, which
@@ -842,7 +844,10 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
             e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
-        if (phases & 2)
+        if (phases & 8)
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOutStates>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0,
+                               s, p, p.NSEG);
+        else if (phases & 2)
             hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOut>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0, s,
                                p, p.NSEG);
         else
@@ -997,27 +1002,44 @@ void chunk_bind_ws(const gdn2_chunk_args *a, char *ws, ChunkParams *p) {
 }  // namespace gdn2
 
 // fused_chunk_forward (src/kernel/chunk_cube.rs:781-952) / chunk_wy_forward
-// (src/forward.rs:44-278).
-static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, int phases) {
+// (src/forward.rs:44-278).  phases: 1 intra, 2 inter, 8 inter that also
+// writes v_new and the per-chunk states.
+static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, int phases, const char *who,
+                              float *v_new = nullptr, float *states = nullptr) {
     ChunkParams p;
-    const gdn2_status st = chunk_setup(a, "gdn2_chunk_fwd_f32", true, &p);
+    const gdn2_status st = chunk_setup(a, who, true, &p);
     if (st != GDN2_OK) return st;
     if (a->seq_len == 0) return GDN2_OK;
     if (!a->workspace || a->workspace_bytes < chunk_fwd_ws_bytes(a) || (reinterpret_cast<uintptr_t>(a->workspace) & 255u))
-        return fail(GDN2_EINVAL, "gdn2_chunk_fwd_f32: workspace missing, too small or not 256-byte aligned");
+        return fail(GDN2_EINVAL, std::string(who) + ": workspace missing, too small or not 256-byte aligned");
     chunk_bind_ws(a, static_cast<char *>(a->workspace), &p);
+    p.ws_vn = v_new;
+    p.ws_sn = states;
     GDN2_HIP_CHECK(launch_chunk(p, (hipStream_t)stream, phases));
     return GDN2_OK;
 }
 
 extern "C" gdn2_status gdn2_chunk_fwd_f32(const gdn2_chunk_args *a, gdn2_stream_t stream) {
-    return chunk_call(a, stream, 3);
+    return chunk_call(a, stream, 3, "gdn2_chunk_fwd_f32");
 }
 
 extern "C" gdn2_status gdn2_chunk_intra_f32(const gdn2_chunk_args *a, gdn2_stream_t stream) {
-    return chunk_call(a, stream, 1);
+    return chunk_call(a, stream, 1, "gdn2_chunk_intra_f32");
 }
 
 extern "C" gdn2_status gdn2_chunk_inter_f32(const gdn2_chunk_args *a, gdn2_stream_t stream) {
-    return chunk_call(a, stream, 2);
+    return chunk_call(a, stream, 2, "gdn2_chunk_inter_f32");
+}
+
+// The whole tuple of fused_chunk_forward (src/kernel/chunk_cube.rs:781-952):
+// out and the state as gdn2_chunk_fwd_f32, plus v_new and the state entering
+// every chunk, which it returns for training.
+extern "C" gdn2_status gdn2_chunk_fwd_states_f32(const gdn2_chunk_args *a, float *v_new, float *states,
+                                                 gdn2_stream_t stream) {
+    const char *who = "gdn2_chunk_fwd_states_f32";
+    if (!a) return fail(GDN2_EINVAL, std::string(who) + ": null args");
+    if (a->seq_len > 0 && (!v_new || !states)) return fail(GDN2_EINVAL, std::string(who) + ": null v_new or states");
+    if (a->chunk_size != kChunk)
+        return fail(GDN2_NOT_APPLICABLE, std::string(who) + ": v_new and states come per 64-token chunk (chunk_size 64)");
+    return chunk_call(a, stream, 9, who, v_new, states);
 }

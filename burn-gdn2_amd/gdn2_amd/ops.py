@@ -176,11 +176,17 @@ def chunk_workspace_bytes(q, k, v, g, b, w, state, out, scale, chunk_size) -> in
 
 
 def chunk_wy_forward(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64, out=None, workspace=None,
-                     in_place=False):
+                     in_place=False, return_states=False):
     """Chunked forward over the whole sequence.  Returns (out, new_state),
     or None when the chunk kernels do not apply (K, V or chunk size outside
     their limits).  g and b may have a last dim of 1 (one value per head and
-    token), as in the reference."""
+    token), as in the reference.
+
+    return_states=True returns fused_chunk_forward's whole tuple
+    (src/kernel/chunk_cube.rs:781-952): (out, new_state, v_new, states) with
+    v_new [B*HV*NC, 64, V] (the delta-rule values of each 64-token chunk) and
+    states [B*HV*NC, K, V] (the state entering each chunk), NC = ceil(T/64);
+    chunk_size must then be 64."""
     _check_f32_cuda(q, k, v, g, b, w, state)
     q, k, v, g, b, w = _operands(q, k, v, g, b, w)
     B, Hk, T, K = q.shape
@@ -190,15 +196,23 @@ def chunk_wy_forward(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64
         st = st.clone()
     if out is None:
         out = torch.empty((B, HV, T, V), device=q.device, dtype=torch.float32)
+    nblk = B * HV * ((T + 63) // 64)
+    if return_states:
+        v_new = torch.empty((nblk, 64, V), device=q.device, dtype=torch.float32)
+        states = torch.empty((nblk, K, V), device=q.device, dtype=torch.float32)
     if T == 0:
-        return out, st
+        return (out, st, v_new, states) if return_states else (out, st)
     need = chunk_workspace_bytes(q, k, v, g, b, w, st, out, scale, chunk_size)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
     a = chunk_args(q, k, v, g, b, w, st, out, scale, chunk_size, workspace)
-    if not C.check(C.lib().gdn2_chunk_fwd_f32(ctypes.byref(a), _stream()), allow_not_applicable=True):
+    if return_states:
+        status = C.lib().gdn2_chunk_fwd_states_f32(ctypes.byref(a), v_new.data_ptr(), states.data_ptr(), _stream())
+    else:
+        status = C.lib().gdn2_chunk_fwd_f32(ctypes.byref(a), _stream())
+    if not C.check(status, allow_not_applicable=True):
         return None
-    return out, st
+    return (out, st, v_new, states) if return_states else (out, st)
 
 
 def chunk_wy_backward(q, k, v, g, b, w, state0, d_out, scale: float, chunk_size: int = 64, d_state=None,

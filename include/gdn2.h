@@ -8,6 +8,7 @@
  *   gdn2_chunk_fwd_f32       <- fused_chunk_forward   src/kernel/chunk_cube.rs:781-952
  *                               (and the tensor path chunk_wy_forward, src/forward.rs:44-278,
  *                                which is the only live chunk path in the reference)
+ *   gdn2_chunk_fwd_states_f32   the same, with fused_chunk_forward's v_new and states
  *   gdn2_chunk_bwd_f32       <- fused_chunk_backward  src/kernel/chunk_adjoint_cube.rs:464-707
  *                               (gradients of the chunked forward; the reference's training
  *                                path otherwise takes them through autodiff)
@@ -159,6 +160,20 @@ GDN2_API gdn2_status gdn2_chunk_fwd_f32(const gdn2_chunk_args *args, gdn2_stream
  * on one stream with the same args they equal gdn2_chunk_fwd_f32. */
 GDN2_API gdn2_status gdn2_chunk_intra_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
 GDN2_API gdn2_status gdn2_chunk_inter_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
+
+/* The full return of fused_chunk_forward (src/kernel/chunk_cube.rs:781-952),
+ * (out, state, v_new, states): gdn2_chunk_fwd_f32 plus
+ *   v_new   [B*HV*NC, 64, V] contiguous: chunk n's pseudo-values U - W S_n;
+ *           row r is the value the delta rule writes at token 64 n + r
+ *           (rows past T, in a ragged last chunk, are zero)
+ *   states  [B*HV*NC, K, V] contiguous: the state entering chunk n
+ * with NC = ceil(T / 64) and chunk id (b * HV + hv) * NC + n, the
+ * reference's [nblk, C, V] / [nblk, K, V] at C = 64.  The workspace is
+ * gdn2_chunk_workspace_bytes(args) as for gdn2_chunk_fwd_f32.
+ * Limits: those of gdn2_chunk_fwd_f32, and chunk_size == 64 (else
+ * GDN2_NOT_APPLICABLE: the states exist at 64-token boundaries only). */
+GDN2_API gdn2_status gdn2_chunk_fwd_states_f32(const gdn2_chunk_args *args, float *v_new, float *states,
+                                               gdn2_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Chunked backward                                     -- fused_chunk_backward
