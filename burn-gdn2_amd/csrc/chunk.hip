@@ -353,16 +353,16 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
     }
     __syncthreads();
 
-    // A_qk -> the sequential kernel as A-operand fragments (mt, qt), zero above the
-    // diagonal (the backward takes A_qk^T only).
+    // A_qk -> the sequential kernel as A-operand fragments (mt, qt), the lower
+    // block triangle qt <= mt only: chunk-inter reads no other tile (the
+    // backward takes A_qk^T only).
     {
         floatx4 *Af = reinterpret_cast<floatx4 *>(p.ws_aqk) + cid * (C * C / 4);
 #pragma unroll
         for (int j = 0; j < (TRAIN ? 0 : NT * NT / NW); ++j) {
             const int f = wave + NW * j, mt = f / NT, qt = f % NT;
-            floatx4 val = *reinterpret_cast<const floatx4 *>(&sAqk[16 * mt + lr][16 * qt + 4 * lg]);
-            if (qt > mt) val = floatx4{0.f, 0.f, 0.f, 0.f};
-            st_stream(Af + f * 64 + lane, val);
+            if (qt > mt) continue; // wave-uniform
+            st_stream(Af + f * 64 + lane, *reinterpret_cast<const floatx4 *>(&sAqk[16 * mt + lr][16 * qt + 4 * lg]));
         }
         if (TRAIN) {
             // A_qk^T fragments (st, rt): lane (g, r) holds A_qk[16 rt + 4 g + j][16 st + r]

@@ -55,7 +55,8 @@ struct ChunkParams {
     float *ws_w;   // C*K   W = (I + A_kk)^-1 (b*k*gamma), A-operand tiles (row tile, col tile)
     float *ws_qg;  // C*K   scale * (q * gamma), same order
     float *ws_u;   // C*V   U = (I + A_kk)^-1 (w*v), accumulator tiles (col tile, row tile)
-    float *ws_aqk; // C*C   A_qk (scale included, zero above the diagonal), A-operand tiles (row tile, col tile)
+    float *ws_aqk; // C*C   A_qk (scale included, zero above the diagonal), A-operand tiles (row tile, col tile);
+                   //       the tiles above the diagonal are left unwritten
     float *ws_kdt; // K*C   (k * exp(G_last - G))^T, A-operand tiles (key tile, time tile)
     float *ws_gam; // K     exp(G_last)
     // Segmented recurrence for few long sequences (NSEG > 1): the chunks of a
