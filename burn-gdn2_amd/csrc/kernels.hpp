@@ -164,6 +164,20 @@ hipError_t launch_rmsnorm_gate(float *out, int64_t ld_out, const float *x, int64
                                int64_t ld_gate, const float *gate_bias, const float *weight, int64_t M, int HV, int V,
                                float eps, hipStream_t s);
 hipError_t launch_fill_rows(float *y, int64_t ld, const float *row, int64_t M, int64_t N, hipStream_t s);
+
+// f_proj_1 and g_proj_1 for at most kLowRankMaxM rows and rank R in {64, 128,
+// 256} (lowrank_up_kernel).
+constexpr int kLowRankMaxM = 256;
+struct LowRankParams {
+    const float *Y;           // rows of the input GEMM's output, row stride ldY
+    int64_t ldY, off_f0, off_g0;
+    const float *F1, *G1;     // [R, kd], [R, vd] row-major
+    const float *g_bias;      // [vd] or null
+    float *F, *G;             // [M, kd], [M, vd] row-major
+    int M, R, kd, vd;
+};
+bool lowrank_up_supported(int R, int64_t M);
+hipError_t launch_lowrank_up(const LowRankParams &p, hipStream_t s);
 hipError_t launch_rmsnorm_gate_bwd(const NormBwdParams &p, hipStream_t s);
 hipError_t launch_project_bwd(const ProjectBwdParams &p, hipStream_t s);
 int conv_bwd_blocks(int T, int tblock);

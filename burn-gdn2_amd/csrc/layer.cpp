@@ -264,6 +264,15 @@ gdn2_status input_gemms(gdn2_layer &L, const float *x, int64_t M, const Work &wk
     gdn2_status st;
     if ((st = L.mm.run(false, false, M, L.ld_in, d.D, x, d.D, L.w_in, L.ld_in, wk.Y, L.ld_in, 0.0f, s)) != GDN2_OK)
         return st;
+    if (lowrank_up_supported((int)d.V, M)) { // a few rows (decode): one small launch for both
+        LowRankParams lp{};
+        lp.Y = wk.Y; lp.ldY = L.ld_in; lp.off_f0 = L.off_f0; lp.off_g0 = L.off_g0;
+        lp.F1 = L.p[P_F1]; lp.G1 = L.p[P_G1]; lp.g_bias = with_bias ? L.p[P_G1_BIAS] : nullptr;
+        lp.F = wk.F; lp.G = wk.G;
+        lp.M = (int)M; lp.R = (int)d.V; lp.kd = (int)d.kd; lp.vd = (int)d.vd;
+        GDN2_HIP_CHECK(launch_lowrank_up(lp, s));
+        return GDN2_OK;
+    }
     if ((st = L.mm.run(false, false, M, d.kd, d.V, wk.Y + L.off_f0, L.ld_in, L.p[P_F1], d.kd, wk.F, d.kd, 0.0f, s)) !=
         GDN2_OK)
         return st;

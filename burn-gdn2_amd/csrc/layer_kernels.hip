@@ -240,6 +240,67 @@ __global__ __launch_bounds__(256) void rmsnorm_gate_kernel(float *out, int64_t l
     for (int i = lane; i < V; i += 64) orow[i] = xr[i] / rms * weight[i] * silu_(gr[i] + (br ? br[i] : 0.f));
 }
 
+// The layer's two rank-R up-projections for a few rows (the decode step), in
+// one launch instead of two GEMM calls:
+//   F[m, n] = sum_j Y[m, off_f0 + j] F1[j, n]              n < kd
+//   G[m, n] = sum_j Y[m, off_g0 + j] G1[j, n] (+ bias[n])  n < vd
+// Workgroup = (64 columns of F or of G, 16 rows).  The 16 input rows and the
+// R x 64 weight tile go to LDS through registers, every load issued before
+// the first LDS write so that their latencies overlap; then thread (column,
+// row group) accumulates 4 rows over j in order.
+template <int R>
+__global__ __launch_bounds__(256) void lowrank_up_kernel(LowRankParams p) {
+    __shared__ float sA[16][R];
+    __shared__ float sB[R][64];
+    const int nft = (p.kd + 63) / 64;
+    const bool isf = (int)blockIdx.x < nft;
+    const int N = isf ? p.kd : p.vd;
+    const int c0 = 64 * (isf ? blockIdx.x : blockIdx.x - nft);
+    const int tid = threadIdx.x, tx = tid & 63, ty = tid >> 6, m0 = 16 * blockIdx.y;
+    const float *A = p.Y + (isf ? p.off_f0 : p.off_g0);
+    const float *Bm = isf ? p.F1 : p.G1;
+    constexpr int NA = 16 * R / 256, NB = 64 * R / 256; // elements per thread
+    float ra[NA], rb[NB];
+#pragma unroll
+    for (int u = 0; u < NA; ++u) {
+        const int i = tid + 256 * u, r = i / R, j = i % R;
+        ra[u] = m0 + r < p.M ? A[(int64_t)(m0 + r) * p.ldY + j] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+        const int i = tid + 256 * u, j = i >> 6, cc = i & 63;
+        rb[u] = c0 + cc < N ? Bm[(int64_t)j * N + c0 + cc] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < NA; ++u) {
+        const int i = tid + 256 * u;
+        sA[i / R][i % R] = ra[u];
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+        const int i = tid + 256 * u;
+        sB[i >> 6][i & 63] = rb[u];
+    }
+    __syncthreads();
+    const int c = c0 + tx;
+    if (c >= N) return;
+    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < R; ++j) {
+        const float bj = sB[j][tx];
+        acc0 += sA[4 * ty][j] * bj;
+        acc1 += sA[4 * ty + 1][j] * bj;
+        acc2 += sA[4 * ty + 2][j] * bj;
+        acc3 += sA[4 * ty + 3][j] * bj;
+    }
+    const float bias = (!isf && p.g_bias) ? p.g_bias[c] : 0.f;
+    float *O = (isf ? p.F : p.G) + c;
+    const float acc[4] = {acc0, acc1, acc2, acc3};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (m0 + 4 * ty + i < p.M) O[(int64_t)(m0 + 4 * ty + i) * N] = acc[i] + bias;
+}
+
 __global__ __launch_bounds__(256) void fill_rows_kernel(float *y, int64_t ld, const float *row, int64_t M, int64_t N) {
     const int64_t total = M * N;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
@@ -547,6 +608,21 @@ hipError_t launch_rmsnorm_gate(float *out, int64_t ld_out, const float *x, int64
     if (rows == 0) return hipSuccess;
     hipLaunchKernelGGL(rmsnorm_gate_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, out, ld_out, x, ld_x,
                        gate, ld_gate, gate_bias, weight, rows, HV, V, eps);
+    return hipGetLastError();
+}
+
+bool lowrank_up_supported(int R, int64_t M) { return M <= kLowRankMaxM && (R == 64 || R == 128 || R == 256); }
+
+hipError_t launch_lowrank_up(const LowRankParams &p, hipStream_t s) {
+    if (p.M == 0) return hipSuccess;
+    if (!lowrank_up_supported(p.R, p.M)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((p.kd + 63) / 64 + (p.vd + 63) / 64), (unsigned)((p.M + 15) / 16));
+    if (p.R == 64)
+        hipLaunchKernelGGL(lowrank_up_kernel<64>, grid, dim3(256), 0, s, p);
+    else if (p.R == 128)
+        hipLaunchKernelGGL(lowrank_up_kernel<128>, grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL(lowrank_up_kernel<256>, grid, dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
