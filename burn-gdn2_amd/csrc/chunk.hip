@@ -263,9 +263,11 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
                 }
             }
         }
-        // The solve's right-hand sides b k exp(G_r) (A_kk waves), from a second
-        // read of the b rows (recent, so served by the caches) rather than
-        // registers held across the products.
+        // The solve's right-hand sides b k exp(G_r) (A_kk waves), from the b
+        // rows still held in araw since the score products (128 VGPRs, no
+        // spill): a second read from global memory missed L2 about half the
+        // time.  The training variant, whose extra stores already spill a
+        // little, reads them again instead.
         floatx4 stg[2][NKH];
         if (mat == 1) {
             floatx4 ar2[2][NKH];
@@ -273,7 +275,8 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
             for (int pi = 0; pi < 2; ++pi) {
                 const int row = 16 * (pi ? (NT - 1 - half) : half) + lr;
 #pragma unroll
-                for (int m = 0; m < NKH; ++m) ar2[pi][m] = bld4(Rb, lr_q + (row - lr) * rq + 16 * (m0 + m) + 4 * lg);
+                for (int m = 0; m < NKH; ++m)
+                    ar2[pi][m] = TRAIN ? bld4(Rb, lr_q + (row - lr) * rq + 16 * (m0 + m) + 4 * lg) : araw[pi][m];
             }
 #pragma unroll
             for (int pi = 0; pi < 2; ++pi) {
