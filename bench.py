@@ -10,13 +10,16 @@ kernels) over all 8 x 16 x 4096 token-heads, inputs already resident in
 HBM.  The projected operands (q, k, g, b, v, w) come from the layer's own
 project() once, outside the timed region.
 
-Also reported: the whole layer (rocBLAS Linear layers + kernels) for the
+Also reported: the whole layer (hipBLASLt Linear layers + kernels) for the
 same prefill; B = 64 fused decode (short conv + gates + L2 norm + step +
 gated RMSNorm per token), the kernel alone over 256 tokens with 5 rotating
 state buffers (335 MB, larger than the 256 MB MALL; the kernel's time does
 not depend on the state values) and the whole layer over a 2048-token
-prefill then 256 single-token steps; and the CPU oracle on the same prefill
-workload.
+prefill then 256 single-token steps; the other benchmark configurations
+(C1 quick-start, C4 GVA + extensions, C5 long context: core per kernel,
+C5's segmented inter passes one by one, and the whole layer); a 1 GiB
+device-to-device copy as the measured practical HBM roof; and the CPU
+oracle on the same prefill workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -68,6 +71,18 @@ def parse():
                     help="host only: mean duration of the dispatches inside bench.py's timed regions (chunk-intra, "
                          "chunk-inter, decode) in a rocprofv3 kernel trace of a default run with the same "
                          "--warmup/--steps/--decode-steps")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other benchmark configurations (C1, C4, C5)")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="time only the other benchmark configurations (C1, C4, C5) and the copy roof")
+    ap.add_argument("--config-steps", type=int, default=10, help="timed core steps per other configuration")
+    ap.add_argument("--configs-summary", metavar="KERNEL_TRACE_CSV",
+                    help="host only: mean duration of the timed core dispatches of each configuration in a "
+                         "rocprofv3 kernel trace of --configs-only with the same --warmup/--config-steps")
+    ap.add_argument("--mfma-summary", metavar="COUNTER_CSV",
+                    help="host only: per kernel, the MFMA operations by data type and the shader clock from a "
+                         "rocprofv3 --pmc run with SQ_INSTS_VALU_MFMA_MOPS_F32 SQ_INSTS_VALU_MFMA_MOPS_BF16 "
+                         "SQ_INSTS_VALU_MFMA_MOPS_XF32 SQ_BUSY_CYCLES GRBM_GUI_ACTIVE")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="host only: per-launch HBM bytes from two rocprofv3 --pmc runs (FETCH_SIZE, "
                          "WRITE_SIZE) of this script with --copy-calibration; writes profiles/*_traffic.json")
@@ -162,6 +177,198 @@ def bench_prefill(torch, G, args, dev):
     layer.close()
     return {"tokens": tokens, "ms_per_step": ms_per_step, "value": tokens / (ms_per_step / 1e3),
             "kernels": kernels, "roofline": roof, "host_sample": host, "scale": scale, "layer": lay}
+
+
+# The other benchmark configurations: (layer config, batch, tokens, dt_bias
+# shift, x seed, description).  C3 (B = 64 decode) is bench_decode's.
+OTHER_CONFIGS = {
+    "C1": (dict(hidden_size=256, num_heads=4, head_dim=64, expand_v=1.0, mode="chunk", chunk_size=64), 1, 1024, 0.0,
+           41, "quick-start layer: hidden 256, 4 heads, head_dim 64, chunk 64, short conv, x [1, 1024, 256]"),
+    "C4": (dict(hidden_size=2048, num_heads=8, num_v_heads=16, head_dim=128, expand_v=2.0, allow_neg_eigval=True,
+                min_decay=0.9, mode="chunk", chunk_size=64), 4, 8192, 0.0, 44,
+           "GVA + extensions: hidden 2048, 8 key heads, 16 value heads, K 128, V 256, neg-eig, min_decay 0.9, "
+           "x [4, 8192, 2048] (value heads read key head hv / 2)"),
+    "C5": (dict(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0, mode="chunk", chunk_size=128), 1, 65536,
+           4.0, 45, "long context: hidden 2048, 16 heads, K = V = 128, chunk_size 128, dt_bias + 4, "
+                    "x [1, 65536, 2048]"),
+}
+
+
+def bench_other_config(torch, G, args, dev, name):
+    """One of the other benchmark configurations: the recurrence core on the
+    layer's own project() operands (chunk-intra, then chunk-inter; with more
+    than one segment its three passes timed one by one), then the whole layer
+    (forward_train).  The kernels always work on 64-token chunks (the result
+    does not depend on the chunk size beyond rounding), so the algorithmic
+    work is counted at C = 64."""
+    import ctypes
+
+    from gdn2_amd import _capi as CA
+    from gdn2_amd.ops import _stream, chunk_args
+
+    over, B, T, dt_shift, xseed, desc = OTHER_CONFIGS[name]
+    cfg = G.Gdn2Config(**over)
+    layer = G.GatedDeltaNet2(cfg, seed=1337)
+    if dt_shift:
+        layer.set_param("dt_bias", layer.param("dt_bias") + dt_shift)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(xseed)
+    x = torch.randn((B, T, cfg.hidden_size), generator=gen, device=dev, dtype=torch.float32)
+    P = layer.project(x)
+    q, k, g, b, v, w = (P[n] for n in ("q", "k", "g", "b", "v", "w"))
+    HV, K, V, C = cfg.hv, cfg.head_dim, cfg.v_head, 64
+    state = torch.zeros((B, HV, K, V), device=dev)
+    out = torch.empty((B, T, HV, V), device=dev).permute(0, 2, 1, 3)
+    scale = K ** -0.5
+    need = G.chunk_workspace_bytes(q, k, v, g, b, w, state, out, scale, C)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    cargs = chunk_args(q, k, v, g, b, w, state, out, scale, C, ws)
+    L, stream, pa = CA.lib(), _stream(), ctypes.byref(cargs)
+    nseg = int(L.gdn2_chunk_segments(pa))
+    passes = (1, 2, 3) if nseg > 1 else (3,)
+
+    def step(evs=None):
+        if evs:
+            evs[0].record()
+        CA.check(L.gdn2_chunk_intra_f32(pa, stream))
+        for i, ps in enumerate(passes):
+            if evs:
+                evs[1 + i].record()
+            CA.check(L.gdn2_chunk_inter_pass_f32(pa, ps, stream))
+        if evs:
+            evs[-1].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    reps = max(1, args.config_steps)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(passes) + 2)] for _ in range(reps)]
+    for e in evs:
+        step(e)
+    torch.cuda.synchronize()
+    intra = [e[0].elapsed_time(e[1]) for e in evs]
+    per_pass = [[e[1 + i].elapsed_time(e[2 + i]) for e in evs] for i in range(len(passes))]
+    inter = [sum(pp[r] for pp in per_pass) for r in range(reps)]
+    intra_ms, inter_ms = sum(intra) / reps, sum(inter) / reps
+    tokens = B * T
+    intra_gflop = B * HV * T * 2 * C * (3 * K + V) / 1e9
+    inter_gflop = B * HV * T * (6 * K * V + 2 * C * V) / 1e9
+    core_ms = intra_ms + inter_ms
+    res = {"workload": desc, "batch": B, "seq_len": T, "tokens": tokens, "kernel_chunk": C,
+           "core": {"ms_per_step": core_ms, "tokens_per_s": tokens / (core_ms / 1e3), "steps": reps,
+                    "chunk_intra": {"ms": intra_ms, "ms_median": _median(intra), "gflop": intra_gflop,
+                                    "tflops": intra_gflop / intra_ms,
+                                    "frac_f32_mfma": intra_gflop / intra_ms / PEAK_F32_TFLOPS},
+                    "chunk_inter": {"ms": inter_ms, "ms_median": _median(inter), "gflop": inter_gflop,
+                                    "tflops": inter_gflop / inter_ms,
+                                    "frac_f32_mfma": inter_gflop / inter_ms / PEAK_F32_TFLOPS,
+                                    "segments": nseg}}}
+    if nseg > 1:
+        names = ("segment_summaries", "chain", "output_pass")
+        res["core"]["chunk_inter"]["passes_ms"] = {n: sum(pp) / reps for n, pp in zip(names, per_pass)}
+    del P, q, k, g, b, v, w, ws, out, state
+    torch.cuda.empty_cache()
+    if not args.no_layer:
+        lay = time_layer(torch, lambda: layer.forward_train(x), max(1, min(args.layer_steps, 3)), tokens)
+        lay["gemm_tflop"] = sum(layer_gemm_tflop(cfg, tokens))
+        res["layer"] = lay
+    del x
+    layer.close()
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_copy_roof(torch, dev, reps=10):
+    """The practical HBM roof: a 1 GiB device-to-device copy (read + write
+    2 GiB per copy), timed with events."""
+    src = torch.ones(COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    gbs = 2 * COPY_BYTES / (ms / 1e3) / 1e9
+    return {"GBs": gbs, "ms": ms, "bytes_moved": 2 * COPY_BYTES, "frac_of_peak": gbs / PEAK_HBM_GBS,
+            "what": "1 GiB device-to-device copy (torch copy_), read + write"}
+
+
+def mfma_summary(path, n_se=32, n_xcc=8):
+    """MFMA operations (the MOPS counters count 512 flops each) by data type
+    and the clock per kernel, over dispatches longer than 100 us:
+    SQ_BUSY_CYCLES summed over the 32 shader engines and GRBM_GUI_ACTIVE
+    summed over the 8 XCDs, each divided by the dispatch duration.  hipBLASLt
+    kernels are labelled by their macro tile; only the timed shapes' dispatches
+    (the longest of each label) are kept, the candidates timed at plan
+    creation fall out as slower ones."""
+    import collections
+    import csv
+    import re
+
+    by = collections.defaultdict(dict)
+    for r in csv.DictReader(open(path)):
+        d = by[int(r["Dispatch_Id"])]
+        d["name"] = r["Kernel_Name"]
+        d["us"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    groups = collections.defaultdict(list)
+    for d in by.values():
+        if d["us"] < 100:
+            continue
+        n = d["name"]
+        if n.startswith("Cijk"):
+            m = re.search(r"MT\d+x\d+x\d+", n)
+            label = f"hipBLASLt {n[:18]} {m.group(0) if m else ''}"
+        else:
+            label = _short(n)
+        groups[(label, round(d.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0.0)))].append(d)
+    # per GEMM shape (its flop count), the algorithm the plan kept is the one run most often
+    best = {}
+    for (label, fl), ds in groups.items():
+        if label.startswith("hipBLASLt") and len(ds) > len(groups.get(best.get(fl), [])):
+            best[fl] = (label, fl)
+    groups = {k: v for k, v in groups.items() if not k[0].startswith("hipBLASLt") or best.get(k[1]) == k}
+    print("| kernel | dispatches | mean us | F32 MFMA GFLOP | BF16 | XF32 | F32 TFLOP/s | clock GHz "
+          "(SQ_BUSY_CYCLES / 32 SE) | clock GHz (GRBM_GUI_ACTIVE / 8 XCD) |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for (label, _), ds in sorted(groups.items(), key=lambda kv: -sum(d["us"] for d in kv[1]))[:16]:
+        us = sum(d["us"] for d in ds) / len(ds)
+        f32 = sum(d.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0.0) for d in ds) / len(ds) * 512 / 1e9
+        bf = sum(d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) for d in ds) / len(ds) * 512 / 1e9
+        xf = sum(d.get("SQ_INSTS_VALU_MFMA_MOPS_XF32", 0.0) for d in ds) / len(ds) * 512 / 1e9
+        sq = sum(d.get("SQ_BUSY_CYCLES", 0.0) for d in ds) / len(ds) / n_se / (us * 1e3)
+        gr = sum(d.get("GRBM_GUI_ACTIVE", 0.0) for d in ds) / len(ds) / n_xcc / (us * 1e3)
+        print(f"| `{label}` | {len(ds)} | {us:.1f} | {f32:.2f} | {bf:.2f} | {xf:.2f} | {f32 / us * 1e3:.1f} | "
+              f"{sq:.3f} | {gr:.3f} |")
+
+
+def configs_summary(path, warmup, steps):
+    """Per (kernel, grid size): the mean duration of the timed core dispatches
+    of each configuration in a kernel trace of --configs-only (the warm-up
+    launches skipped; the layer's own launches of the same shape come after
+    the timed ones and are not counted)."""
+    import csv
+
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    groups = {}
+    for r in rows:
+        key = (_short(r["Kernel_Name"]), int(r.get("Grid_Size", r.get("Grid_Size_X", 0)) or 0))
+        if not key[0].startswith(("chunk_intra", "chunk_inter", "chunk_chain")):
+            continue
+        groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print("| kernel | grid (work-items) | timed dispatches | mean us | min us | max us |")
+    print("|---|---|---|---|---|---|")
+    for (name, grid), d in groups.items():
+        d = d[warmup:warmup + steps]
+        if d:
+            print(f"| `{name}` | {grid} | {len(d)} | {sum(d) / len(d):.1f} | {min(d):.1f} | {max(d):.1f} |")
 
 
 def layer_gemm_tflop(cfg, tokens):
@@ -575,6 +782,12 @@ def main():
     if args.traffic_summary:
         traffic_summary(*args.traffic_summary)
         return
+    if args.mfma_summary:
+        mfma_summary(args.mfma_summary)
+        return
+    if args.configs_summary:
+        configs_summary(args.configs_summary, args.warmup, args.config_steps)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: the GDN-2 path shards over (batch, value head) with no "
@@ -599,9 +812,16 @@ def main():
         res["workload"] = f"GDN-2 layer training step, B={args.batch} T={args.seq} D=2048 H=16 K=V=128, f32"
         print(json.dumps(res), flush=True)
         return
+    if args.configs_only:
+        res = {n: bench_other_config(torch, G, args, dev, n) for n in OTHER_CONFIGS}
+        res["hbm_copy_roof"] = bench_copy_roof(torch, dev)
+        print(json.dumps(res), flush=True)
+        return
     pre = bench_prefill(torch, G, args, dev)
     dec = None if args.no_decode else bench_decode(torch, G, args, dev)
     bwd = None if args.no_backward else bench_backward(torch, G, args, dev)
+    others = None if args.no_configs else {n: bench_other_config(torch, G, args, dev, n) for n in OTHER_CONFIGS}
+    copy_roof = bench_copy_roof(torch, dev)
     cpu = None if args.no_cpu else cpu_baseline(pre, args)
     if args.copy_calibration:
         src = torch.empty(COPY_BYTES // 4, device=dev)
@@ -633,7 +853,17 @@ def main():
         "decode_tokens_per_s": None if dec is None else dec["tokens_per_s"],
         "layer": {"prefill": pre["layer"], "decode": None if dec is None else dec.get("layer")},
         "backward": bwd,
+        "configs": others,
+        "hbm_copy_roof": copy_roof,
     }
+    # fractions of the measured copy bandwidth (the practical HBM roof) beside the 8 TB/s peak
+    tr_intra = load_traffic("chunk_intra_b8_t4096_traffic.json") if (args.batch, args.seq) == (8, 4096) else None
+    if tr_intra:
+        gbs = tr_intra["hbm_bytes_per_launch"] / (pre["kernels"]["chunk_intra"]["ms"] / 1e3) / 1e9
+        pre["kernels"]["chunk_intra"].update({"hbm_GBs": gbs, "frac_hbm": gbs / PEAK_HBM_GBS,
+                                              "frac_copy_roof": gbs / copy_roof["GBs"]})
+    if dec is not None:
+        dec["frac_copy_roof"] = dec["achieved_GBs"] / copy_roof["GBs"]
     print(json.dumps(line), flush=True)
 
 

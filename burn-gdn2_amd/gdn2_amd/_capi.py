@@ -97,6 +97,7 @@ STATE_RECURRENT, STATE_CONV_Q, STATE_CONV_K, STATE_CONV_V = 0, 1, 2, 3
 # Every symbol include/*.h declares (checked by tests/test_capi_exports.py).
 EXPORTS = ("gdn2_last_error", "gdn2_hip_available", "gdn2_recurrent_step_f32", "gdn2_recurrent_fwd_f32",
            "gdn2_chunk_workspace_bytes", "gdn2_chunk_fwd_f32", "gdn2_chunk_intra_f32", "gdn2_chunk_inter_f32",
+           "gdn2_chunk_segments", "gdn2_chunk_inter_pass_f32",
            "gdn2_chunk_fwd_states_f32",
            "gdn2_chunk_bwd_workspace_bytes", "gdn2_chunk_bwd_f32", "gdn2_recurrent_bwd_workspace_bytes",
            "gdn2_recurrent_bwd_f32", "gdn2_decode_fused_f32",
@@ -139,6 +140,10 @@ def lib():
         L.gdn2_chunk_fwd_states_f32.argtypes = [ctypes.POINTER(ChunkArgs), ctypes.c_void_p, ctypes.c_void_p,
                                                 ctypes.c_void_p]
         L.gdn2_chunk_fwd_states_f32.restype = ctypes.c_int
+        L.gdn2_chunk_segments.argtypes = [ctypes.POINTER(ChunkArgs)]
+        L.gdn2_chunk_segments.restype = _i64
+        L.gdn2_chunk_inter_pass_f32.argtypes = [ctypes.POINTER(ChunkArgs), ctypes.c_int, ctypes.c_void_p]
+        L.gdn2_chunk_inter_pass_f32.restype = ctypes.c_int
         L.gdn2_chunk_workspace_bytes.argtypes = [ctypes.POINTER(ChunkArgs)]
         L.gdn2_chunk_workspace_bytes.restype = ctypes.c_size_t
         L.gdn2_chunk_bwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkBwdArgs)]

@@ -9,8 +9,8 @@ of include/gdn2_layer.h.
 
 Parameters live in device memory owned by the library; x and the outputs
 are float32 torch device tensors [B, T, hidden_size].  Every call runs the
-library's HIP kernels and rocBLAS GEMMs on torch's current stream; there is
-no CPU path.
+library's HIP kernels and hipBLASLt GEMMs (rocBLAS for any shape hipBLASLt
+has no algorithm for) on torch's current stream; there is no CPU path.
 """
 from __future__ import annotations
 

@@ -161,6 +161,18 @@ GDN2_API gdn2_status gdn2_chunk_fwd_f32(const gdn2_chunk_args *args, gdn2_stream
 GDN2_API gdn2_status gdn2_chunk_intra_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
 GDN2_API gdn2_status gdn2_chunk_inter_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
 
+/* The passes of gdn2_chunk_inter_f32 one at a time, for per-pass timing (the
+ * same diagnostic role).  Few long sequences split each sequence into
+ * gdn2_chunk_segments(args) segments so that the sequential walk spreads over
+ * the compute units: pass 1 runs every segment but the last from a zero state
+ * (its transition and offset), pass 2 chains the segments' entering states,
+ * pass 3 re-runs every segment from its entering state and writes out and the
+ * final state.  With one segment, passes 1 and 2 launch nothing.  Called
+ * 1, 2, 3 in order on one stream after gdn2_chunk_intra_f32 they equal
+ * gdn2_chunk_inter_f32.  Any other pass is GDN2_EINVAL. */
+GDN2_API int64_t gdn2_chunk_segments(const gdn2_chunk_args *args);
+GDN2_API gdn2_status gdn2_chunk_inter_pass_f32(const gdn2_chunk_args *args, int pass, gdn2_stream_t stream);
+
 /* The full return of fused_chunk_forward (src/kernel/chunk_cube.rs:781-952),
  * (out, state, v_new, states): gdn2_chunk_fwd_f32 plus
  *   v_new   [B*HV*NC, 64, V] contiguous: chunk n's pseudo-values U - W S_n;

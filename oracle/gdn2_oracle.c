@@ -606,17 +606,30 @@ GDN2O_EXPORT void gdn2o_rmsnorm_gate(const double *x, const double *gate, const 
     }
 }
 
-/* y[M][N] = x[M][Kd] W[Kd][N] (+ bias[N]); W in burn's [in, out] layout. */
+/* y[M][N] = x[M][Kd] W[Kd][N] (+ bias[N]); W in burn's [in, out] layout.
+ * Every element is bias + sum over kk = 0, 1, .. of x[m][kk] W[kk][n], added in
+ * that order.  Blocks of LIN_MB rows x LIN_NB columns keep their W rows in cache
+ * across the block's rows (one pass over W per LIN_MB rows, not per row), which
+ * keeps D = 2048 layers over thousands of tokens at seconds. */
+#define LIN_MB 8
+#define LIN_NB 256
 static void linear_d(const double *x, const float *W, const float *bias, long M, int Kd, int N, double *y) {
-#pragma omp parallel for schedule(static)
-    for (long m = 0; m < M; ++m) {
-        double *yr = y + m * N;
-        for (int n = 0; n < N; ++n) yr[n] = bias ? (double)bias[n] : 0.0;
+    const long nmb = (M + LIN_MB - 1) / LIN_MB, nnb = (N + LIN_NB - 1) / LIN_NB;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (long blk = 0; blk < nmb * nnb; ++blk) {
+        const long m0 = (blk / nnb) * LIN_MB, n0 = (blk % nnb) * LIN_NB;
+        const int mb = (int)(M - m0 < LIN_MB ? M - m0 : LIN_MB), nb = (int)(N - n0 < LIN_NB ? N - n0 : LIN_NB);
+        double acc[LIN_MB][LIN_NB];
+        for (int i = 0; i < mb; ++i)
+            for (int n = 0; n < nb; ++n) acc[i][n] = bias ? (double)bias[n0 + n] : 0.0;
         for (int kk = 0; kk < Kd; ++kk) {
-            const double a = x[m * Kd + kk];
-            const float *Wr = W + (size_t)kk * N;
-            for (int n = 0; n < N; ++n) yr[n] += a * (double)Wr[n];
+            const float *Wr = W + (size_t)kk * N + n0;
+            for (int i = 0; i < mb; ++i) {
+                const double a = x[(m0 + i) * Kd + kk];
+                for (int n = 0; n < nb; ++n) acc[i][n] += a * (double)Wr[n];
+            }
         }
+        for (int i = 0; i < mb; ++i) memcpy(y + (m0 + i) * N + n0, acc[i], sizeof(double) * nb);
     }
 }
 

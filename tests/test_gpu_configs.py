@@ -1,16 +1,24 @@
 """The benchmark configurations at their full sizes, on the GPU.
 
-At these sizes the oracle cannot run the whole layer in seconds, so each
+At these sizes the oracle cannot run the whole batch in seconds, so each
 configuration is held to size-independent properties plus oracle checks on
-sampled heads:
+sampled heads and sampled batch rows:
   * chunk == per-token recurrence on the layer's own projected inputs (the
     reference's invariant, tests/stable_chunk.rs:11-63), two independent
     kernels on identical operands;
   * the sampled (batch, value head) sequences against the double recurrence
     of the oracle (outputs and final state);
   * token-by-token decode after a prefill == one forward over the whole
-    sequence (src/module.rs:224-316; tests/autodiff.rs:31-104).
-Tolerance: max |error| <= 1e-4 (tests/test_chunk.rs:254-255)."""
+    sequence (src/module.rs:224-316; tests/autodiff.rs:31-104);
+  * the whole layer (hipBLASLt GEMMs at K = 2048, projection epilogue,
+    recurrence, gated norm, o_proj) against the double layer oracle on
+    causal prefixes of sampled batch rows, on whole sampled rows for the
+    decode configuration, and for the long-context configuration on its last
+    256 tokens from the layer's own state at that point.
+Tolerance: max |error| <= 1e-4 (tests/test_chunk.rs:254-255); layer outputs
+(about 2e-3 in size) also within 1e-4 of max |reference|.
+The GVA configuration is checked against true head repeat (value head hv
+reads key head hv / rep), not the reference's time-scrambling reshape."""
 import numpy as np
 import pytest
 
@@ -34,6 +42,29 @@ def _x(torch, gpu, seed, shape):
     gen = torch.Generator(device=gpu)
     gen.manual_seed(seed)
     return torch.randn(shape, generator=gen, device=gpu, dtype=torch.float32)
+
+
+def _vs_oracle(got, ref, what):
+    """max |got - ref| <= 1e-4 and <= 1e-4 max |ref|."""
+    got = np.asarray(got, np.float64)
+    err = maxabs(got, ref)
+    scale = float(np.abs(ref).max())
+    print(f"{what}: max|err| {err:.2e}  max|ref| {scale:.3e}  ratio {err / max(scale, 1e-30):.2e}", flush=True)
+    assert np.isfinite(got).all(), what
+    assert err <= TOL and err <= TOL * scale, (what, err, scale)
+
+
+def _layer_prefix_vs_oracle(cfg, layer, x, out, rows, T):
+    """out[rows, :T] (a causal prefix of forward_train / forward from no
+    state) against the double layer oracle on x[rows, :T] with the layer's
+    own weights."""
+    xr = x[rows, :T].contiguous().cpu().numpy()
+    ref, _ = O.layer_forward(cfg, layer.params(), xr)
+    _vs_oracle(out[rows, :T].cpu().numpy(), ref.out, f"layer rows {rows} tokens [0, {T}) vs oracle")
+
+
+def _oracle_state(st, rows):
+    return O.OracleState(st.recurrent[rows], st.conv_q[rows], st.conv_k[rows], st.conv_v[rows])
 
 
 def _core_views(P):
@@ -84,8 +115,11 @@ def test_config2_default_prefill_chunk(gpu):
     x = _x(torch, gpu, 42, (8, 4096, 2048))
     P = layer.project(x)
     _check_core(G, cfg, P, 64, sample=[(0, 0), (7, 15), (3, 9)])
+    del P
     out = layer.forward_train(x)
+    torch.cuda.synchronize()
     assert bool(torch.isfinite(out).all())
+    _layer_prefix_vs_oracle(cfg, layer, x, out, [0, 7], 512)
 
 
 def test_config3_decode_reproduces_full_forward(gpu):
@@ -114,6 +148,17 @@ def test_config3_decode_reproduces_full_forward(gpu):
     assert e_pre < TOL and e_dec < TOL and e_dec <= 1e-4 * scale and e_s < TOL
     for n in ("conv_q", "conv_k", "conv_v"):  # raw projections, up to the GEMMs' rounding at other M
         assert maxabs(getattr(st, n), getattr(st_full, n)) < 1e-5, n
+    # whole sampled batch rows against the double layer oracle: the prefill's
+    # outputs, the 256 decoded tokens, the final recurrent state and conv caches
+    rows = [0, 37]
+    ref, rst = O.layer_forward(cfg, layer.params(), x[rows].contiguous().cpu().numpy())
+    _vs_oracle(out_p[rows].cpu().numpy(), ref.out[:, :Tp], f"prefill rows {rows} vs oracle")
+    _vs_oracle(dec[rows].cpu().numpy(), ref.out[:, Tp:], f"decoded tokens rows {rows} vs oracle")
+    e_so = maxabs(st.recurrent[rows], rst.recurrent)
+    print(f"final S rows {rows} vs oracle: {e_so:.2e}", flush=True)
+    assert e_so < TOL
+    for n in ("conv_q", "conv_k", "conv_v"):
+        assert maxabs(getattr(st, n)[rows], getattr(rst, n)) < TOL, n
     # the core of the one-pass forward against the double oracle on sampled heads
     P = layer.project(x[:4, :512].contiguous())
     _check_core(G, cfg, P, 64, sample=[(0, 0), (3, 11)])
@@ -135,6 +180,8 @@ def test_config4_gva_negeig_mindecay_chunk_then_decode(gpu):
     _check_core(G, cfg, P, 64, sample=[(0, 0), (1, 7), (3, 15)])
     del P
     full, st_full = layer.forward(x)
+    torch.cuda.synchronize()
+    _layer_prefix_vs_oracle(cfg, layer, x, full, [0, 3], 512)
     _, st = layer.forward(x[:, :T].contiguous())
     outs = []
     for t in range(T, T + Td):
@@ -165,5 +212,24 @@ def test_config5_long_context_strong_decay(gpu):
     print(f"cumulative log-decay over one chunk reaches -{span:.1f}", flush=True)
     assert span > 88.0
     _check_core(G, cfg, P, 128, sample=[(0, 0), (0, 13)])
+    del P
     out = layer.forward_train(x)
+    torch.cuda.synchronize()
     assert bool(torch.isfinite(out).all())
+    _layer_prefix_vs_oracle(cfg, layer, x, out, [0], 512)
+    # the last 256 tokens: continued from the layer's own state after the first
+    # T - 256 tokens, against forward_train's tail and the double layer oracle
+    # started from that same state
+    T, t0 = x.shape[1], x.shape[1] - 256
+    _, st = layer.forward(x[:, :t0].contiguous())
+    st_t0 = _oracle_state(st, [0])  # forward() updates the state object in place
+    tail, st_end = layer.forward(x[:, t0:].contiguous(), st)
+    torch.cuda.synchronize()
+    e_cont = float((tail - out[:, t0:]).abs().max())
+    print(f"tail after a {t0}-token prefill vs forward_train: {e_cont:.2e}", flush=True)
+    assert e_cont < TOL and e_cont <= TOL * float(out[:, t0:].abs().max())
+    ref, rst = O.layer_forward(cfg, layer.params(), x[:, t0:].contiguous().cpu().numpy(), state=st_t0)
+    _vs_oracle(tail.cpu().numpy(), ref.out, f"last 256 tokens of {T} vs oracle from the same state")
+    e_s = maxabs(st_end.recurrent, rst.recurrent)
+    print(f"final S vs oracle: {e_s:.2e}", flush=True)
+    assert e_s < TOL
