@@ -187,6 +187,21 @@ GDN2_API gdn2_status gdn2_chunk_inter_pass_f32(const gdn2_chunk_args *args, int 
 GDN2_API gdn2_status gdn2_chunk_fwd_states_f32(const gdn2_chunk_args *args, float *v_new, float *states,
                                                gdn2_stream_t stream);
 
+/* gdn2_chunk_fwd_f32 without a workspace argument and without any device
+ * allocation.  No counterpart in the reference: it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The kernels and results are those of gdn2_chunk_fwd_f32;
+ * the workspace is a static device array of gdn2_chunk_noalloc_scratch_bytes()
+ * bytes (64 MiB) that each GPU holds until the process ends.  args->workspace
+ * and args->workspace_bytes are ignored.  A call whose
+ * gdn2_chunk_workspace_bytes(args) exceeds the array returns GDN2_EINVAL and
+ * launches nothing (at K = V = 128 the array holds about 450 chunks of 64
+ * tokens, counted over every (batch row, value head)).  All calls on one GPU
+ * share its array: calls that overlap in time on one GPU (two streams or two
+ * host threads) race and must be ordered by the caller. */
+GDN2_API size_t gdn2_chunk_noalloc_scratch_bytes(void);
+GDN2_API gdn2_status gdn2_chunk_fwd_noalloc_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Chunked backward                                     -- fused_chunk_backward
  * (src/kernel/chunk_adjoint_cube.rs:464-707; the reference's training path
