@@ -266,6 +266,9 @@ def bench_other_config(torch, G, args, dev, name):
     if nseg > 1:
         names = ("segment_summaries", "chain", "output_pass")
         res["core"]["chunk_inter"]["passes_ms"] = {n: sum(pp) / reps for n, pp in zip(names, per_pass)}
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_config_core(name, [t[:1].contiguous().cpu().numpy() for t in (q, k, v, g, b, w)],
+                                              scale)
     del P, q, k, g, b, v, w, ws, out, state
     torch.cuda.empty_cache()
     if not args.no_layer:
@@ -280,24 +283,45 @@ def bench_other_config(torch, G, args, dev, name):
 
 def bench_copy_roof(torch, dev, reps=10):
     """The practical HBM roof: a 1 GiB device-to-device copy (read + write
-    2 GiB per copy), timed with events."""
+    2 GiB per copy), timed with events: the library's streaming copy
+    (gdn2_stream_copy_f32) at a few grid sizes, the best kept, and torch's
+    copy_ beside it."""
+    import ctypes
+
+    from gdn2_amd import _capi as CA
+    from gdn2_amd.ops import _stream
+
     src = torch.ones(COPY_BYTES // 4, device=dev)
     dst = torch.empty_like(src)
-    for _ in range(2):
-        dst.copy_(src)
-    torch.cuda.synchronize()
+    L, stream = CA.lib(), _stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        dst.copy_(src)
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    per_grid = {}
+    for wg in (2048, 4096, 8192, 16384):
+        ms = timed(lambda: CA.check(L.gdn2_stream_copy_f32(ctypes.c_void_p(dst.data_ptr()),
+                                                            ctypes.c_void_p(src.data_ptr()), src.numel(), wg,
+                                                            stream)))
+        per_grid[wg] = 2 * COPY_BYTES / (ms / 1e3) / 1e9
+    torch_gbs = 2 * COPY_BYTES / (timed(lambda: dst.copy_(src)) / 1e3) / 1e9
+    ok = bool(torch.equal(dst, src))
     del src, dst
     torch.cuda.empty_cache()
-    gbs = 2 * COPY_BYTES / (ms / 1e3) / 1e9
-    return {"GBs": gbs, "ms": ms, "bytes_moved": 2 * COPY_BYTES, "frac_of_peak": gbs / PEAK_HBM_GBS,
-            "what": "1 GiB device-to-device copy (torch copy_), read + write"}
+    wg = max(per_grid, key=per_grid.get)
+    gbs = per_grid[wg]
+    return {"GBs": gbs, "bytes_moved": 2 * COPY_BYTES, "frac_of_peak": gbs / PEAK_HBM_GBS, "workgroups": wg,
+            "GBs_per_grid": per_grid, "torch_copy_GBs": torch_gbs, "copy_ok": ok,
+            "what": "1 GiB device-to-device copy (gdn2_stream_copy_f32, best grid), read + write"}
 
 
 def mfma_summary(path, n_se=32, n_xcc=8):
@@ -358,17 +382,22 @@ def configs_summary(path, warmup, steps):
 
     rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
     groups = {}
+    cur = None  # the configuration, known by the shape of its chunk-intra launch
     for r in rows:
         key = (_short(r["Kernel_Name"]), int(r.get("Grid_Size", r.get("Grid_Size_X", 0)) or 0))
         if not key[0].startswith(("chunk_intra", "chunk_inter", "chunk_chain")):
             continue
-        groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    print("| kernel | grid (work-items) | timed dispatches | mean us | min us | max us |")
-    print("|---|---|---|---|---|---|")
-    for (name, grid), d in groups.items():
+        if key[0].startswith("chunk_intra"):
+            cur = key
+        groups.setdefault((cur,) + key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print("| configuration (its chunk-intra launch) | kernel | grid (work-items) | timed dispatches | mean us | "
+          "min us | max us |")
+    print("|---|---|---|---|---|---|---|")
+    for (c, name, grid), d in groups.items():
         d = d[warmup:warmup + steps]
         if d:
-            print(f"| `{name}` | {grid} | {len(d)} | {sum(d) / len(d):.1f} | {min(d):.1f} | {max(d):.1f} |")
+            print(f"| `{c[0]}` x {c[1] // 512} | `{name}` | {grid} | {len(d)} | {sum(d) / len(d):.1f} | {min(d):.1f} | "
+                  f"{max(d):.1f} |")
 
 
 def layer_gemm_tflop(cfg, tokens):
@@ -535,7 +564,65 @@ def cpu_baseline(pre, args):
     return {"value": n * T / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"{n} of 8 sequences x {T} tokens x 16 heads, f32 chunk_wy_forward restatement "
                       f"(oracle/gdn2_oracle.c), {cores} OpenMP threads, {dt:.2f} s",
-            "cpu_model": _cpu_model(), "layer": cpu_layer_baseline(args)}
+            "cpu_model": _cpu_model(), "layer": cpu_layer_baseline(args), "decode_b64": cpu_decode_core(args)}
+
+
+def cpu_config_core(name, host, scale):
+    """The recurrence core of one batch row of a configuration on the host
+    cores: the oracle's f32 restatement of chunk_wy_forward (the Chunk-mode
+    tensor path), except for the long-context configuration, where the
+    reference's chunked tensor path overflows (its decay factor
+    k / exp(G_s - G_b) passes the f32 range once 16 |g| > 88), so its f32
+    per-token scan (fused_recurrent_forward) is timed instead."""
+    from oracle import oracle as O
+
+    q, k, v, g, b, w = host
+    T = q.shape[2]
+    short = [a[:, :, :min(T, 128)] for a in host]
+    if name == "C5":
+        fn, what = O.recurrent_f32, "f32 per-token scan restatement (fused_recurrent_forward)"
+        fn(*short, scale=scale)
+        t0 = time.perf_counter()
+        fn(q, k, v, g, b, w, scale=scale)
+    else:
+        fn, what = O.chunk_wy_f32, "f32 chunk_wy_forward restatement"
+        fn(*short, scale=scale, chunk_size=64)
+        t0 = time.perf_counter()
+        fn(q, k, v, g, b, w, scale=scale, chunk_size=64)
+    dt = time.perf_counter() - t0
+    cores = O.num_threads()
+    return {"value": T / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"1 batch row x {T} tokens x {v.shape[1]} value heads, {what} (oracle/gdn2_oracle.c), "
+                      f"{cores} OpenMP threads, {dt:.2f} s"}
+
+
+def cpu_decode_core(args):
+    """One B = 64 decode step of the recurrence core on the host cores: the
+    oracle's f32 per-token scan over one token for 64 x 16 heads (K = V =
+    128), averaged over 20 steps."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    rng = np.random.default_rng(7)
+    B, H, K, V = args.decode_batch, 16, 128, 128
+    q = rng.standard_normal((B, H, 1, K)).astype(np.float32)
+    kk = rng.standard_normal((B, H, 1, K))
+    k = (kk / np.linalg.norm(kk, axis=-1, keepdims=True)).astype(np.float32)
+    v, w = (rng.standard_normal((B, H, 1, V)).astype(np.float32) for _ in range(2))
+    g = rng.uniform(-0.3, -0.02, (B, H, 1, K)).astype(np.float32)
+    b = rng.uniform(0, 1, (B, H, 1, K)).astype(np.float32)
+    S = (rng.standard_normal((B, H, K, V)) * 0.05).astype(np.float32)
+    O.recurrent_f32(q, k, v, g, b, w, S0=S, scale=K ** -0.5)
+    n = 20
+    t0 = time.perf_counter()
+    for _ in range(n):
+        O.recurrent_f32(q, k, v, g, b, w, S0=S, scale=K ** -0.5)
+    dt = (time.perf_counter() - t0) / n
+    cores = O.num_threads()
+    return {"value": B / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"B={B} one-token steps x 16 heads, f32 per-token scan restatement (oracle), {cores} OpenMP "
+                      f"threads, {n} steps of {dt * 1e3:.2f} ms"}
 
 
 def cpu_layer_baseline(args):

@@ -645,7 +645,8 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         for (int mt = 0; mt < NT; ++mt)
             u_cur[mt] = pcol ? floatx4{0.f, 0.f, 0.f, 0.f} : U4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
         if (STATES) { // the state entering chunk n
-            float *Sn = p.ws_sn + cid * K * V;
+            const size_t slot = p.st_step ? (size_t)bh * p.st_chunks + (size_t)n * p.st_step : cid;
+            float *Sn = p.ws_sn + slot * K * V;
 #pragma unroll
             for (int kb = 0; kb < NKT; ++kb)
 #pragma unroll
@@ -685,11 +686,20 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) X1[mt] = u_cur[mt] - X1[mt];
         if (STATES) {
-            float *Vn = p.ws_vn + cid * C * V;
+            if (p.st_step) { // token rows [B * HV, T, V]; rows past T (ragged last chunk) are not written
+                float *Vn = p.ws_vn + ((size_t)bh * p.T + (size_t)n * C) * V;
 #pragma unroll
-            for (int mt = 0; mt < NT; ++mt)
+                for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) Vn[(size_t)(16 * mt + 4 * lg + i) * V + col] = X1[mt][i];
+                    for (int i = 0; i < 4; ++i)
+                        if (n * C + 16 * mt + 4 * lg + i < p.T) Vn[(size_t)(16 * mt + 4 * lg + i) * V + col] = X1[mt][i];
+            } else {
+                float *Vn = p.ws_vn + cid * C * V;
+#pragma unroll
+                for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) Vn[(size_t)(16 * mt + 4 * lg + i) * V + col] = X1[mt][i];
+            }
         }
 
         // W, q exp(G) of chunk n+1, then the touches of its Kd^T, A_qk, U
@@ -822,6 +832,61 @@ __global__ __launch_bounds__(256, 1) void chunk_chain_kernel(ChunkParams p) {
     }
 }
 
+// The states at the boundaries of caller chunks of Cc tokens (Cc dividing 64,
+// p.st_step = 64 / Cc > 1) that fall inside a 64-token chunk n, from the state
+// S_n entering it (already in its slot) and the chunk's own tokens:
+//   S(64 n + m) = diag(exp(G_m)) S_n + sum_{t < m} (k_t exp(G_m - G_{t+1}))^T v_new_t
+// with G_j = g_0 + .. + g_{j-1} per key channel from the chunk start, so that
+// every exponent is <= 0 (src/kernel/chunk_cube.rs:612-734 returns these
+// states for the reference's own chunk size).  One workgroup per (b, hv,
+// 64-token chunk, boundary m = Cc, 2 Cc, .., 64 - Cc, 64 value columns).
+template <int K>
+__global__ __launch_bounds__(256) void chunk_states_kernel(ChunkParams p) {
+    __shared__ float sA[C][K]; // k rows, then the decayed keys k_t exp(G_m - G_{t+1})
+    __shared__ float sB[C][K]; // g rows, then v_new rows (64 value columns)
+    __shared__ float sGam[K];
+    static_assert(K >= 64, "sB holds 64 value columns");
+    const int r = p.st_step, nvs = p.V / 64;
+    int blk = blockIdx.x;
+    const int vs = blk % nvs;
+    blk /= nvs;
+    const int m = (blk % (r - 1) + 1) * (C / r); // tokens of chunk n before the boundary
+    blk /= r - 1;
+    const int n = blk % p.NC, bh = blk / p.NC;
+    const int t0 = n * C;
+    if (t0 + m >= p.T) return; // no caller chunk starts there (T is a multiple of the caller's chunk size)
+    const int bi = bh / p.HV, hv = bh % p.HV, hk = hv / p.rep;
+    const int64_t kofs = (int64_t)bi * p.sqb + (int64_t)hk * p.sqh + (int64_t)t0 * p.sqt;
+    const int tid = threadIdx.x;
+    for (int i = tid; i < m * K; i += 256) {
+        const int t = i / K, c = i % K;
+        sA[t][c] = p.k[kofs + (int64_t)t * p.sqt + c];
+        sB[t][c] = p.g[kofs + (int64_t)t * p.sqt + c];
+    }
+    __syncthreads();
+    for (int c = tid; c < K; c += 256) { // a thread per key channel walks the m tokens backwards
+        float acc = 0.f;                 // g_{t+1} + .. + g_{m-1}
+        for (int t = m - 1; t >= 0; --t) {
+            sA[t][c] *= fast_exp2(acc * kLog2e);
+            acc += sB[t][c];
+        }
+        sGam[c] = fast_exp2(acc * kLog2e);
+    }
+    __syncthreads();
+    const float *vn = p.ws_vn + ((size_t)bh * p.T + t0) * p.V + vs * 64;
+    for (int i = tid; i < m * 64; i += 256) sB[i / 64][i % 64] = vn[(size_t)(i / 64) * p.V + i % 64];
+    __syncthreads();
+    const int v = tid & 63, cg = tid >> 6, col = vs * 64 + v;
+    const size_t slot = (size_t)bh * p.st_chunks + (size_t)n * r;
+    const float *Sn = p.ws_sn + slot * K * p.V;
+    float *So = p.ws_sn + (slot + m / (C / r)) * K * p.V;
+    for (int c = cg; c < K; c += 4) {
+        float acc = sGam[c] * Sn[(size_t)c * p.V + col];
+        for (int t = 0; t < m; ++t) acc += sA[t][c] * sB[t][v];
+        So[(size_t)c * p.V + col] = acc;
+    }
+}
+
 // phases: 1 intra; 2 inter with the output, 4 training (every segment's P), 8
 // output plus v_new and the per-chunk states (2, 4, 8 run every inter pass the
 // shape needs); one pass of the segmented inter alone (phase diagnostics):
@@ -881,6 +946,19 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
 
 bool chunk_supported(int K, int V) {
     return (K == 64 || K == 128) && (V == 64 || V == 128 || V == 256);
+}
+
+hipError_t launch_chunk_states(const ChunkParams &p, hipStream_t s) {
+    if (p.st_step <= 1) return hipSuccess;
+    const int64_t grid = (int64_t)p.B * p.HV * p.NC * (p.st_step - 1) * (p.V / 64);
+    if (grid <= 0) return hipSuccess;
+    if (p.K == 128)
+        hipLaunchKernelGGL(chunk_states_kernel<128>, dim3((unsigned)grid), dim3(256), 0, s, p);
+    else if (p.K == 64)
+        hipLaunchKernelGGL(chunk_states_kernel<64>, dim3((unsigned)grid), dim3(256), 0, s, p);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
 }
 
 hipError_t launch_chunk(const ChunkParams &p, hipStream_t s, int phases) {
@@ -1024,7 +1102,7 @@ void chunk_bind_ws(const gdn2_chunk_args *a, char *ws, ChunkParams *p) {
 // (src/forward.rs:44-278).  phases: 1 intra, 2 inter, 8 inter that also
 // writes v_new and the per-chunk states.
 static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, int phases, const char *who,
-                              float *v_new = nullptr, float *states = nullptr) {
+                              float *v_new = nullptr, float *states = nullptr, int st_step = 0) {
     ChunkParams p;
     const gdn2_status st = chunk_setup(a, who, true, &p);
     if (st != GDN2_OK) return st;
@@ -1034,7 +1112,12 @@ static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, in
     chunk_bind_ws(a, static_cast<char *>(a->workspace), &p);
     p.ws_vn = v_new;
     p.ws_sn = states;
+    if (st_step) {
+        p.st_step = st_step;
+        p.st_chunks = (int)(a->seq_len / (kChunk / st_step));
+    }
     GDN2_HIP_CHECK(launch_chunk(p, (hipStream_t)stream, phases));
+    if (st_step > 1) GDN2_HIP_CHECK(launch_chunk_states(p, (hipStream_t)stream));
     return GDN2_OK;
 }
 
@@ -1068,7 +1151,13 @@ extern "C" gdn2_status gdn2_chunk_fwd_states_f32(const gdn2_chunk_args *a, float
     const char *who = "gdn2_chunk_fwd_states_f32";
     if (!a) return fail(GDN2_EINVAL, std::string(who) + ": null args");
     if (a->seq_len > 0 && (!v_new || !states)) return fail(GDN2_EINVAL, std::string(who) + ": null v_new or states");
-    if (a->chunk_size != kChunk)
-        return fail(GDN2_NOT_APPLICABLE, std::string(who) + ": v_new and states come per 64-token chunk (chunk_size 64)");
-    return chunk_call(a, stream, 9, who, v_new, states);
+    if (a->chunk_size == kChunk) return chunk_call(a, stream, 9, who, v_new, states);
+    // smaller caller chunks: the reference's limits (chunk_size <= 64, T a
+    // multiple of it), and here a divisor of 64 so that every 64-token chunk
+    // starts a caller chunk
+    if (a->chunk_size <= 0 || a->chunk_size > kChunk || kChunk % a->chunk_size != 0)
+        return fail(GDN2_NOT_APPLICABLE, std::string(who) + ": chunk_size must divide 64");
+    if (a->seq_len % a->chunk_size != 0)
+        return fail(GDN2_NOT_APPLICABLE, std::string(who) + ": seq_len must be a multiple of chunk_size");
+    return chunk_call(a, stream, 9, who, v_new, states, (int)(kChunk / a->chunk_size));
 }

@@ -74,6 +74,12 @@ struct ChunkParams {
     float *ws_akk;  // C*C  (I + A_kk)^-1, accumulator-layout tiles (row tile, column tile)
     float *ws_sn;   // K*V  state entering each chunk (row-major)
     float *ws_vn;   // C*V  v_new of each chunk (row-major)
+    // Layout of ws_sn / ws_vn for a caller chunk size Cc dividing 64 (0: the
+    // 64-token chunk layout above).  st_step = 64 / Cc slots per 64-token
+    // chunk, st_chunks = T / Cc slots per (b, hv): the state entering 64-chunk
+    // n goes to slot (b * HV + hv) * st_chunks + n * st_step, and v_new is
+    // written as token rows [B * HV, T, V] (rows < T only).
+    int st_step, st_chunks;
 };
 
 // Projection epilogue: raw Linear outputs -> kernel inputs, one token per

@@ -184,9 +184,11 @@ def chunk_wy_forward(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64
 
     return_states=True returns fused_chunk_forward's whole tuple
     (src/kernel/chunk_cube.rs:781-952): (out, new_state, v_new, states) with
-    v_new [B*HV*NC, 64, V] (the delta-rule values of each 64-token chunk) and
-    states [B*HV*NC, K, V] (the state entering each chunk), NC = ceil(T/64);
-    chunk_size must then be 64."""
+    v_new [B*HV*NC, C, V] (the delta-rule values of each chunk of C =
+    chunk_size tokens) and states [B*HV*NC, K, V] (the state entering each
+    chunk).  chunk_size 64: NC = ceil(T/64) (rows past T are zero); a smaller
+    chunk_size must divide 64 and T (the reference's T % C == 0), NC = T/C;
+    other chunk sizes return None."""
     _check_f32_cuda(q, k, v, g, b, w, state)
     q, k, v, g, b, w = _operands(q, k, v, g, b, w)
     B, Hk, T, K = q.shape
@@ -196,9 +198,12 @@ def chunk_wy_forward(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64
         st = st.clone()
     if out is None:
         out = torch.empty((B, HV, T, V), device=q.device, dtype=torch.float32)
-    nblk = B * HV * ((T + 63) // 64)
+    Cs = 64 if (not return_states or chunk_size == 64) else int(chunk_size)
+    nblk = B * HV * ((T + 63) // 64 if Cs == 64 else (T // Cs if Cs > 0 else 0))
     if return_states:
-        v_new = torch.empty((nblk, 64, V), device=q.device, dtype=torch.float32)
+        if Cs <= 0 or 64 % Cs or (Cs < 64 and T % Cs):
+            return None  # the per-chunk tensors exist for chunk sizes dividing 64 (and T)
+        v_new = torch.empty((nblk, Cs, V), device=q.device, dtype=torch.float32)
         states = torch.empty((nblk, K, V), device=q.device, dtype=torch.float32)
     if T == 0:
         return (out, st, v_new, states) if return_states else (out, st)

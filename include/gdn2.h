@@ -174,16 +174,19 @@ GDN2_API int64_t gdn2_chunk_segments(const gdn2_chunk_args *args);
 GDN2_API gdn2_status gdn2_chunk_inter_pass_f32(const gdn2_chunk_args *args, int pass, gdn2_stream_t stream);
 
 /* The full return of fused_chunk_forward (src/kernel/chunk_cube.rs:781-952),
- * (out, state, v_new, states): gdn2_chunk_fwd_f32 plus
- *   v_new   [B*HV*NC, 64, V] contiguous: chunk n's pseudo-values U - W S_n;
- *           row r is the value the delta rule writes at token 64 n + r
- *           (rows past T, in a ragged last chunk, are zero)
+ * (out, state, v_new, states): gdn2_chunk_fwd_f32 plus, per chunk of
+ * C = chunk_size tokens,
+ *   v_new   [B*HV*NC, C, V] contiguous: row r of chunk n is the value the
+ *           delta rule writes at token C n + r (the pseudo-values U - W S)
  *   states  [B*HV*NC, K, V] contiguous: the state entering chunk n
- * with NC = ceil(T / 64) and chunk id (b * HV + hv) * NC + n, the
- * reference's [nblk, C, V] / [nblk, K, V] at C = 64.  The workspace is
- * gdn2_chunk_workspace_bytes(args) as for gdn2_chunk_fwd_f32.
- * Limits: those of gdn2_chunk_fwd_f32, and chunk_size == 64 (else
- * GDN2_NOT_APPLICABLE: the states exist at 64-token boundaries only). */
+ * with chunk id (b * HV + hv) * NC + n, the reference's [nblk, C, V] /
+ * [nblk, K, V].  C = 64: NC = ceil(T / 64), rows past T (a ragged last
+ * chunk) are zero.  C < 64: C must divide 64 and T (the reference's
+ * T % C == 0), NC = T / C; the states inside each 64-token chunk are derived
+ * from the state entering it by one more small kernel.  The workspace is
+ * gdn2_chunk_workspace_bytes(args) as for gdn2_chunk_fwd_f32.  Limits: those
+ * of gdn2_chunk_fwd_f32, and the chunk sizes above (else
+ * GDN2_NOT_APPLICABLE). */
 GDN2_API gdn2_status gdn2_chunk_fwd_states_f32(const gdn2_chunk_args *args, float *v_new, float *states,
                                                gdn2_stream_t stream);
 
@@ -199,6 +202,14 @@ GDN2_API gdn2_status gdn2_chunk_fwd_states_f32(const gdn2_chunk_args *args, floa
  * tokens, counted over every (batch row, value head)).  All calls on one GPU
  * share its array: calls that overlap in time on one GPU (two streams or two
  * host threads) race and must be ordered by the caller. */
+/* A streaming copy of n floats (dst, src 16-byte aligned, not overlapping)
+ * over `workgroups` workgroups of 256 threads (0 = 8 per compute unit), each
+ * looping over the array with 16-byte non-temporal loads and stores.  No
+ * reference counterpart: the benchmark's measurement of the practical HBM
+ * bandwidth (2 n x 4 bytes moved per call) beside the 8 TB/s peak. */
+GDN2_API gdn2_status gdn2_stream_copy_f32(float *dst, const float *src, int64_t n, int64_t workgroups,
+                                          gdn2_stream_t stream);
+
 GDN2_API size_t gdn2_chunk_noalloc_scratch_bytes(void);
 GDN2_API gdn2_status gdn2_chunk_fwd_noalloc_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
 

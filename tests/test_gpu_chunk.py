@@ -229,35 +229,42 @@ def test_chunk_repeat_is_bit_identical(gpu, shape):
 
 
 STATE_CASES = [
-    # B, Hk, HV, T, K, V
-    (1, 2, 2, 130, 64, 64),      # ragged last chunk
-    (2, 1, 2, 200, 128, 128),    # GVA rep 2
-    (1, 2, 2, 2100, 128, 256),   # segmented inter (few long sequences), V = 2K
+    # B, Hk, HV, T, K, V, chunk_size
+    (1, 2, 2, 130, 64, 64, 64),      # ragged last chunk
+    (2, 1, 2, 200, 128, 128, 64),    # GVA rep 2
+    (1, 2, 2, 2100, 128, 256, 64),   # segmented inter (few long sequences), V = 2K
+    (1, 2, 2, 160, 64, 64, 32),      # chunk_size 32, a ragged last 64-token chunk holding one boundary
+    (2, 1, 2, 208, 128, 128, 16),    # chunk_size 16, GVA rep 2
+    (1, 1, 1, 200, 64, 128, 8),      # chunk_size 8
+    (1, 2, 2, 2112, 128, 128, 32),   # chunk_size 32 with the segmented inter
 ]
 
 
-@pytest.mark.parametrize("case", STATE_CASES, ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}" for c in STATE_CASES])
+@pytest.mark.parametrize("case", STATE_CASES,
+                         ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}C{c[6]}" for c in STATE_CASES])
 def test_chunk_forward_returns_v_new_and_states(gpu, case):
-    """fused_chunk_forward's (out, state, v_new, states), src/kernel/chunk_cube.rs:781-952.
-    states[n] is the oracle recurrence's state after 64 n tokens; row r of
-    v_new[n] is the value the delta rule writes at token 64 n + r, which the
-    oracle's consecutive states give through S_t - diag(e^{g_t}) S_{t-1} =
-    k_t v_new_t^T (|k_t| = 1); rows past T are zero."""
+    """fused_chunk_forward's (out, state, v_new, states), src/kernel/chunk_cube.rs:781-952,
+    for chunk size C: states[j] is the oracle recurrence's state after C j
+    tokens; row r of v_new[j] is the value the delta rule writes at token
+    C j + r, which the oracle's consecutive states give through
+    S_t - diag(e^{g_t}) S_{t-1} = k_t v_new_t^T (|k_t| = 1).  C = 64 takes any
+    T (rows past T are zero); smaller C divide 64 and T, as the reference
+    requires T % C == 0."""
     import gdn2_amd
 
-    B, Hk, HV, T, K, V = case
+    B, Hk, HV, T, K, V, Cs = case
     rep = HV // Hk
-    rng = np.random.default_rng(5000 + T + K + V)
+    rng = np.random.default_rng(5000 + T + K + V + Cs)
     q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=-0.2, g_hi=-0.01, b_hi=1.0)
     q *= K ** -0.5 * 4
     S0 = (rng.standard_normal((B, HV, K, V)) * 0.5).astype(np.float32)
     scale = K ** -0.5
     d = _dev(gpu, q, k, v, g, b, w, S0)
-    res = gdn2_amd.chunk_wy_forward(*d, scale, chunk_size=64, return_states=True)
+    res = gdn2_amd.chunk_wy_forward(*d, scale, chunk_size=Cs, return_states=True)
     assert res is not None
     o, S, vn, st = (t.cpu().numpy() for t in res)
-    NC = (T + 63) // 64
-    assert vn.shape == (B * HV * NC, 64, V) and st.shape == (B * HV * NC, K, V)
+    NC = (T + Cs - 1) // Cs
+    assert vn.shape == (B * HV * NC, Cs, V) and st.shape == (B * HV * NC, K, V)
     o_ref, S_ref = O.recurrent_f64(q, k, v, g, b, w, S0=S0, scale=scale)
     assert maxabs(o, o_ref) < TOL and maxabs(S, S_ref) < TOL
     # the oracle's state after every token
@@ -265,14 +272,29 @@ def test_chunk_forward_returns_v_new_and_states(gpu, case):
     for t in range(T):
         sl = lambda a: a[:, :, t:t + 1]
         Ss.append(O.recurrent_f64(*(sl(a) for a in (q, k, v, g, b, w)), S0=Ss[-1], scale=scale)[1])
-    st_ref = np.stack([Ss[64 * n] for n in range(NC)], axis=2)  # [B, HV, NC, K, V]
-    assert maxabs(st.reshape(B, HV, NC, K, V), st_ref) < TOL
-    vn_ref = np.zeros((B, HV, NC * 64, V))
+    st_ref = np.stack([Ss[Cs * n] for n in range(NC)], axis=2)  # [B, HV, NC, K, V]
+    e_st = maxabs(st.reshape(B, HV, NC, K, V), st_ref)
+    vn_ref = np.zeros((B, HV, NC * Cs, V))
     for t in range(T):
         kt = k[:, :, t].astype(np.float64).repeat(rep, axis=1)             # [B, HV, K]
         gt = np.exp(g[:, :, t].astype(np.float64)).repeat(rep, axis=1)     # [B, HV, K]
         dS = Ss[t + 1] - gt[..., None] * Ss[t]
         vn_ref[:, :, t] = np.einsum("bhk,bhkv->bhv", kt, dS)
-    assert maxabs(vn.reshape(B, HV, NC * 64, V), vn_ref) < TOL
-    # chunk_size other than 64: the per-chunk tensors do not apply
-    assert gdn2_amd.chunk_wy_forward(*d, scale, chunk_size=32, return_states=True) is None
+    e_vn = maxabs(vn.reshape(B, HV, NC * Cs, V), vn_ref)
+    print(f"C={Cs}: states {e_st:.2e}  v_new {e_vn:.2e}", flush=True)
+    assert e_st < TOL and e_vn < TOL
+
+
+def test_chunk_states_refuse_other_chunk_sizes(gpu):
+    """Chunk sizes that do not divide 64, or T, have no per-chunk tensors here
+    (None, the caller's fallback)."""
+    import gdn2_amd
+
+    rng = np.random.default_rng(77)
+    q, k, v, g, b, w = rand_inputs(rng, 1, 1, 1, 96, 64, 64)
+    d = _dev(gpu, q, k, v, g, b, w, np.zeros((1, 1, 64, 64), np.float32))
+    assert gdn2_amd.chunk_wy_forward(*d, 0.125, chunk_size=48, return_states=True) is None
+    assert gdn2_amd.chunk_wy_forward(*d, 0.125, chunk_size=64 + 64, return_states=True) is None
+    assert gdn2_amd.chunk_wy_forward(*d, 0.125, chunk_size=64, return_states=True) is not None
+    d2 = _dev(gpu, *(a[:, :, :90] for a in (q, k, v, g, b, w)), np.zeros((1, 1, 64, 64), np.float32))
+    assert gdn2_amd.chunk_wy_forward(*d2, 0.125, chunk_size=32, return_states=True) is None  # 90 % 32 != 0
