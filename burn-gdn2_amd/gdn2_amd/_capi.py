@@ -99,7 +99,7 @@ EXPORTS = ("gdn2_last_error", "gdn2_hip_available", "gdn2_recurrent_step_f32", "
            "gdn2_chunk_workspace_bytes", "gdn2_chunk_fwd_f32", "gdn2_chunk_intra_f32", "gdn2_chunk_inter_f32",
            "gdn2_chunk_segments", "gdn2_chunk_inter_pass_f32",
            "gdn2_chunk_fwd_states_f32", "gdn2_chunk_noalloc_scratch_bytes", "gdn2_chunk_fwd_noalloc_f32",
-           "gdn2_stream_copy_f32",
+           "gdn2_stream_copy_f32", "gdn2_short_conv_f32", "gdn2_l2_normalize_f32", "gdn2_rms_norm_gate_f32",
            "gdn2_chunk_bwd_workspace_bytes", "gdn2_chunk_bwd_f32", "gdn2_recurrent_bwd_workspace_bytes",
            "gdn2_recurrent_bwd_f32", "gdn2_decode_fused_f32",
            "gdn2_config_default", "gdn2_config_validate", "gdn2_config_dims", "gdn2_param_count",
@@ -146,6 +146,12 @@ def lib():
         L.gdn2_chunk_segments.restype = _i64
         L.gdn2_chunk_inter_pass_f32.argtypes = [ctypes.POINTER(ChunkArgs), ctypes.c_int, ctypes.c_void_p]
         L.gdn2_chunk_inter_pass_f32.restype = ctypes.c_int
+        vp = ctypes.c_void_p
+        L.gdn2_short_conv_f32.argtypes = [vp, vp, vp, vp, vp, _i64, _i64, _i64, vp]
+        L.gdn2_l2_normalize_f32.argtypes = [vp, vp, _i64, _i64, _dbl, vp]
+        L.gdn2_rms_norm_gate_f32.argtypes = [vp, vp, vp, vp, _i64, _i64, _dbl, vp]
+        for n in ("gdn2_short_conv_f32", "gdn2_l2_normalize_f32", "gdn2_rms_norm_gate_f32"):
+            getattr(L, n).restype = ctypes.c_int
         L.gdn2_stream_copy_f32.argtypes = [ctypes.c_void_p, ctypes.c_void_p, _i64, _i64, ctypes.c_void_p]
         L.gdn2_stream_copy_f32.restype = ctypes.c_int
         L.gdn2_chunk_noalloc_scratch_bytes.argtypes = []

@@ -8,6 +8,9 @@ libgdn2_amd.so.
   chunk_wy_forward         src/forward.rs:44-278 (+ fused_chunk_forward,
                            src/kernel/chunk_cube.rs:781-952)
   decode_fused             forward() at T == 1, src/module.rs:224-316
+  short_conv_1d            src/short_conv.rs:22-65
+  l2_normalize(_4d)        src/l2norm.rs:4-16
+  rms_norm_gate_per_head   src/module.rs:501-517
 
 Tensor conventions follow the reference: q, k, g, b [B, Hk, T, K];
 v, w [B, HV, T, V]; state [B, HV, K, V]; out [B, HV, T, V].  Hk may be
@@ -327,3 +330,49 @@ def decode_fused(raw: dict, params: dict, state, conv_in, conv_out, *, num_heads
                     use_short_conv=use_short_conv, allow_neg_eigval=allow_neg_eigval)
     C.check(C.lib().gdn2_decode_fused_f32(ctypes.byref(a), _stream()))
     return out
+
+
+# -- the reference's standalone operators (src/lib.rs:58-62) -------------------
+
+def short_conv_1d(x, weight, cache=None):
+    """short_conv_1d (src/short_conv.rs:22-65): x [B, T, C], weight [C, 4],
+    cache [B, 3, C] or None (the first token repeated as padding).  Returns
+    (silu(causal conv of 4 taps) [B, T, C], new cache [B, 3, C])."""
+    _check_f32_cuda(x, weight, cache)
+    x, weight = x.contiguous(), weight.contiguous()
+    cache = None if cache is None else cache.contiguous()
+    B, T, Cn = x.shape
+    if tuple(weight.shape) != (Cn, 4) or (cache is not None and tuple(cache.shape) != (B, 3, Cn)):
+        raise ValueError("short_conv_1d: weight must be [C, 4] and cache [B, 3, C]")
+    out = torch.empty_like(x)
+    new_cache = torch.empty((B, 3, Cn), device=x.device, dtype=torch.float32)
+    C.check(C.lib().gdn2_short_conv_f32(_p(x), _p(weight), _p(cache), _p(out), _p(new_cache), B, T, Cn, _stream()))
+    return out, new_cache
+
+
+def l2_normalize(x, eps: float = 1e-6):
+    """l2_normalize / l2_normalize_4d (src/l2norm.rs:4-16): x / sqrt(sum x^2 +
+    eps) along the last dimension, any leading shape."""
+    _check_f32_cuda(x)
+    x = x.contiguous()
+    y = torch.empty_like(x)
+    n = x.shape[-1] if x.dim() else 1
+    C.check(C.lib().gdn2_l2_normalize_f32(_p(x), _p(y), x.numel() // max(n, 1), n, float(eps), _stream()))
+    return y
+
+
+l2_normalize_4d = l2_normalize
+
+
+def rms_norm_gate_per_head(x, gate, weight, eps: float):
+    """rms_norm_gate_per_head (src/module.rs:501-517): x, gate [B, T, HV, V],
+    weight [V]: x / sqrt(mean_V x^2 + eps) * weight * silu(gate)."""
+    _check_f32_cuda(x, gate, weight)
+    x, gate, weight = x.contiguous(), gate.contiguous(), weight.contiguous()
+    if gate.shape != x.shape or weight.numel() != x.shape[-1]:
+        raise ValueError("rms_norm_gate_per_head: gate must match x and weight must have x's last dim")
+    y = torch.empty_like(x)
+    V = x.shape[-1]
+    C.check(C.lib().gdn2_rms_norm_gate_f32(_p(x), _p(gate), _p(weight), _p(y), x.numel() // V, V, float(eps),
+                                           _stream()))
+    return y

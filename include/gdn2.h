@@ -16,6 +16,9 @@
  *                               o_proj: short conv (src/short_conv.rs:22-65), gates
  *                               (src/module.rs:417-443), L2 norm (src/l2norm.rs:13-16),
  *                               the step, rms_norm_gate_per_head (src/module.rs:501-517)
+ *   gdn2_short_conv_f32, gdn2_l2_normalize_f32, gdn2_rms_norm_gate_f32
+ *                            <- short_conv_1d, l2_normalize(_4d), rms_norm_gate_per_head
+ *                               (src/lib.rs:58-62)
  *   gdn2_hip_available       <- is_cuda / CudaBare TypeId gate
  *                               src/kernel/fused_recurrent_cube.rs:74-78
  *
@@ -202,6 +205,35 @@ GDN2_API gdn2_status gdn2_chunk_fwd_states_f32(const gdn2_chunk_args *args, floa
  * tokens, counted over every (batch row, value head)).  All calls on one GPU
  * share its array: calls that overlap in time on one GPU (two streams or two
  * host threads) race and must be ordered by the caller. */
+/* ------------------------------------------------------------------------
+ * Standalone operators, the reference's public functions (src/lib.rs:58-62),
+ * for a binding that calls them one by one (the layer fuses them into its
+ * own kernels).  Contiguous f32 device arrays; every status as above.
+ *
+ * short_conv_1d (src/short_conv.rs:22-65): causal depthwise conv of 4 taps +
+ * SiLU.  x [B, T, C], weight [C, 4], cache_in [B, 3, C] or NULL (Option::None:
+ * the first token is repeated 3 times as padding), out [B, T, C],
+ * cache_out [B, 3, C] = the last 3 rows of cat(cache or padding, x) along time.
+ *   out[b, t, c] = silu(sum_{i<4} xpad[b, t + i, c] weight[c, i])
+ * cache_out must not overlap x, out or cache_in.  T = 0 needs cache_in
+ * (cache_out = cache_in).
+ *
+ * l2_normalize / l2_normalize_4d (src/l2norm.rs:4-16): y = x / sqrt(sum x^2 +
+ * eps) over each of `rows` rows of n values (any leading shape flattened);
+ * y may be x.
+ *
+ * rms_norm_gate_per_head (src/module.rs:501-517):
+ *   y = x / sqrt(mean x^2 + eps) * weight * silu(gate)
+ * over each of `rows` rows of V values (x, gate [B, T, HV, V] flattened to
+ * rows = B T HV), weight [V]; y may be x.
+ * ---------------------------------------------------------------------- */
+GDN2_API gdn2_status gdn2_short_conv_f32(const float *x, const float *weight, const float *cache_in, float *out,
+                                         float *cache_out, int64_t B, int64_t T, int64_t C, gdn2_stream_t stream);
+GDN2_API gdn2_status gdn2_l2_normalize_f32(const float *x, float *y, int64_t rows, int64_t n, double eps,
+                                           gdn2_stream_t stream);
+GDN2_API gdn2_status gdn2_rms_norm_gate_f32(const float *x, const float *gate, const float *weight, float *y,
+                                            int64_t rows, int64_t V, double eps, gdn2_stream_t stream);
+
 /* A streaming copy of n floats (dst, src 16-byte aligned, not overlapping)
  * over `workgroups` workgroups of 256 threads (0 = 8 per compute unit), each
  * looping over the array with 16-byte non-temporal loads and stores.  No
