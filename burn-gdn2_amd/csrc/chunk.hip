@@ -48,13 +48,16 @@ constexpr float kSafeSpan = 96.0f; // log2 units
 // ---------------------------------------------------------------------------
 // TRAIN adds the backward's operands (ws_wt, ws_qgt, ws_kd, ws_aqkt, and
 // (I + A_kk)^-1 in ws_akk).
+// K = 256 needs 137 KiB of LDS: one workgroup per CU, two waves per SIMD,
+// and up to 256 VGPRs per wave.
 template <int K, int V, bool TRAIN>
-__global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
-    constexpr int NW = 8; // waves per workgroup; two workgroups per CU = four waves per SIMD
+__global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(ChunkParams p) {
+    constexpr int NW = 8; // waves per workgroup; two workgroups per CU = four waves per SIMD (K <= 128)
     constexpr int KP = K + 4, CP = C + 4;
     constexpr int NKT = K / 16, NVT = V / 16, NTOT = NKT + NVT;
-    static_assert(NKT % 2 == 0 && NKT <= NW, "K in {32, 64, 96, 128}");
+    static_assert(NKT % 2 == 0 && (NKT <= NW || NKT % NW == 0), "K in {32, 64, 96, 128, 256}");
     constexpr int NTW = (NTOT + NW - 1) / NW; // column tiles per wave in the solve (nt = wave + NW u)
+    constexpr int NKW = (NKT + NW - 1) / NW;  // key-column tiles per wave (nt = wave + NW u, u < NKW)
     constexpr int NKH = NKT / 2;              // 16-channel blocks per wave in the score products
     constexpr int NSEG = 512 / K, RPS = C / NSEG;
     static_assert(512 % K == 0 && C % NSEG == 0, "K");
@@ -174,7 +177,7 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
     //    blocks, over the channel half kh; the two halves are summed through
     //    LDS below.  The row operands, with exp(G) applied, are kept for the
     //    solve: q exp(G) (A_qk waves) and b k exp(G) (A_kk waves).
-    floatx4 stR[NT]; // the solve's key-column right-hand sides (staged below)
+    floatx4 stR[NKW][NT]; // the solve's key-column right-hand sides (staged below)
     floatx4 *QGf = reinterpret_cast<floatx4 *>(p.ws_qg) + cid * (C * K / 4);
     {
         const int mat = wave >> 2, half = (wave >> 1) & 1, kh = wave & 1;
@@ -317,15 +320,18 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
             }
         }
         __syncthreads();
-        // The solve's owner of key column tile nt = wave reads its columns in
-        // accumulator layout (rows 4 g + i, column r of each 16 x 16 tile);
-        // channel half 0 completes the score matrices.
-        if (wave < NKT) {
-            const int col = 16 * wave + lr;
+        // The solve's owner of key column tile nt = wave + NW u reads its
+        // columns in accumulator layout (rows 4 g + i, column r of each 16 x 16
+        // tile); channel half 0 completes the score matrices.
 #pragma unroll
-            for (int tp = 0; tp < NT; ++tp)
+        for (int u = 0; u < NKW; ++u) {
+            if (wave + NW * u < NKT) {
+                const int col = 16 * (wave + NW * u) + lr;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) stR[tp][i] = sBKG[16 * tp + 4 * lg + i][col];
+                for (int tp = 0; tp < NT; ++tp)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) stR[u][tp][i] = sBKG[16 * tp + 4 * lg + i][col];
+            }
         }
         if (kh == 0) {
 #pragma unroll
@@ -419,7 +425,7 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
 #pragma unroll
             for (int u = 0; u < NTW; ++u) {
                 const int nt = wave + NW * u;
-                const bool kcol = u == 0 && (NKT >= NW || wave < NKT);
+                const bool kcol = nt < NKT;
                 if (nt < NTOT && !kcol) {
                     const int c = 16 * (nt - NKT) + lr;
 #pragma unroll
@@ -436,9 +442,9 @@ __global__ __launch_bounds__(512, 4) void chunk_intra_kernel(ChunkParams p) {
 #pragma unroll
         for (int u = 0; u < NTW; ++u) {
             const int nt = wave + NW * u;
-            const bool kcol = u == 0 && (NKT >= NW || wave < NKT);
+            const bool kcol = nt < NKT; // then u < NKW
             if (nt >= NTOT) continue;
-            floatx4 R = kcol ? stR[tp] : r1[sl][u] * r2[sl][u];
+            floatx4 R = kcol ? stR[u < NKW ? u : 0][tp] : r1[sl][u] * r2[sl][u];
 #pragma unroll
             for (int q = 0; q < NT; ++q)
                 if (q < tp) R = mfma4n(*reinterpret_cast<const float4 *>(&sAkk[16 * tp + lr][16 * q + 4 * lg]), X[u][q], R);
@@ -524,7 +530,11 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     constexpr int AF4 = NT * NT * 64; // float4 of A_qk per chunk
     constexpr int APF = AF4 / 256;
     __shared__ floatx4 sW[OPF4], sKd[OPF4];
-    __shared__ floatx4 sQ[OUT ? OPF4 : 1], sA[OUT ? AF4 : 1];
+    // K = 256: W and Kd^T take 64 KiB each, so scale q exp(G), which feeds only
+    // the output (off the sequential chain), is read from L2 into registers in
+    // phase A instead of through a third LDS buffer (145 KiB in all).
+    constexpr bool QLDS = OUT && K <= 128;
+    __shared__ floatx4 sQ[QLDS ? OPF4 : 1], sA[OUT ? AF4 : 1];
     __shared__ float sPf[256]; // destination of the L2 touches, never read
 
     const int V = p.V;
@@ -593,7 +603,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
             lds_copy4(&W4[(cid0 + n0) * OPF4 + i * 256 + tid], &sW[i * 256 + wv]);
-            if (OUT) lds_copy4(&Q4[(cid0 + n0) * OPF4 + i * 256 + tid], &sQ[i * 256 + wv]);
+            if (QLDS) lds_copy4(&Q4[(cid0 + n0) * OPF4 + i * 256 + tid], &sQ[i * 256 + wv]);
         }
         __builtin_amdgcn_sched_barrier(0);
         touch_kau(cid0 + n0);
@@ -668,7 +678,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) {
                 wa[mt] = sW[(mt * NKT + kb) * 64 + lane];
-                if (OUT) ma[mt] = sQ[(mt * NKT + kb) * 64 + lane];
+                if (OUT) ma[mt] = QLDS ? sQ[(mt * NKT + kb) * 64 + lane] : Q4[cid * OPF4 + (mt * NKT + kb) * 64 + lane];
             }
             // eight (pass 1: four) independent accumulator chains per k-step
 #pragma unroll
@@ -708,7 +718,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
 #pragma unroll
             for (int i = 0; i < PFO; ++i) {
                 lds_copy4(&W4[(cid + 1) * OPF4 + i * 256 + tid], &sW[i * 256 + wv]);
-                if (OUT) lds_copy4(&Q4[(cid + 1) * OPF4 + i * 256 + tid], &sQ[i * 256 + wv]);
+                if (QLDS) lds_copy4(&Q4[(cid + 1) * OPF4 + i * 256 + tid], &sQ[i * 256 + wv]);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -907,9 +917,12 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
     }
     if (phases & 1) {
         const int nchunks = p.B * p.HV * p.NC;
-        if (p.ws_akk)
-            hipLaunchKernelGGL((chunk_intra_kernel<K, V, true>), dim3(nchunks), dim3(512), 0, s, p);
-        else
+        if (p.ws_akk) {
+            if constexpr (K <= 128)
+                hipLaunchKernelGGL((chunk_intra_kernel<K, V, true>), dim3(nchunks), dim3(512), 0, s, p);
+            else
+                return hipErrorInvalidValue; // the chunked backward takes K <= 128
+        } else
             hipLaunchKernelGGL((chunk_intra_kernel<K, V, false>), dim3(nchunks), dim3(512), 0, s, p);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -945,14 +958,18 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
 }  // namespace
 
 bool chunk_supported(int K, int V) {
-    return (K == 64 || K == 128) && (V == 64 || V == 128 || V == 256);
+    return ((K == 64 || K == 128) && (V == 64 || V == 128 || V == 256)) || (K == 256 && (V == 128 || V == 256));
 }
+
+bool chunk_bwd_supported(int K, int V) { return (K == 64 || K == 128) && (V == 64 || V == 128 || V == 256); }
 
 hipError_t launch_chunk_states(const ChunkParams &p, hipStream_t s) {
     if (p.st_step <= 1) return hipSuccess;
     const int64_t grid = (int64_t)p.B * p.HV * p.NC * (p.st_step - 1) * (p.V / 64);
     if (grid <= 0) return hipSuccess;
-    if (p.K == 128)
+    if (p.K == 256)
+        hipLaunchKernelGGL(chunk_states_kernel<256>, dim3((unsigned)grid), dim3(256), 0, s, p);
+    else if (p.K == 128)
         hipLaunchKernelGGL(chunk_states_kernel<128>, dim3((unsigned)grid), dim3(256), 0, s, p);
     else if (p.K == 64)
         hipLaunchKernelGGL(chunk_states_kernel<64>, dim3((unsigned)grid), dim3(256), 0, s, p);
@@ -963,6 +980,8 @@ hipError_t launch_chunk_states(const ChunkParams &p, hipStream_t s) {
 
 hipError_t launch_chunk(const ChunkParams &p, hipStream_t s, int phases) {
     if (p.K == 128 && p.V == 128) return launch_chunk_t<128, 128>(p, s, phases);
+    if (p.K == 256 && p.V == 256) return launch_chunk_t<256, 256>(p, s, phases);
+    if (p.K == 256 && p.V == 128) return launch_chunk_t<256, 128>(p, s, phases);
     if (p.K == 128 && p.V == 256) return launch_chunk_t<128, 256>(p, s, phases);
     if (p.K == 128 && p.V == 64) return launch_chunk_t<128, 64>(p, s, phases);
     if (p.K == 64 && p.V == 64) return launch_chunk_t<64, 64>(p, s, phases);

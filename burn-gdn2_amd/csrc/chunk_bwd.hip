@@ -951,6 +951,8 @@ extern "C" size_t gdn2_chunk_bwd_workspace_bytes(const gdn2_chunk_bwd_args *a) {
 extern "C" gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *a, gdn2_stream_t stream) {
     if (!a) return fail(GDN2_EINVAL, "gdn2_chunk_bwd_f32: null args");
     BwdParams bp{};
+    if (!chunk_bwd_supported((int)a->fwd.head_dim, (int)a->fwd.head_v_dim))
+        return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_bwd_f32: (K, V) outside the chunked backward's instances");
     gdn2_status st = chunk_setup(&a->fwd, "gdn2_chunk_bwd_f32", false, &bp.f);
     if (st != GDN2_OK) return st;
     if (!a->d_out || !a->dq || !a->dk || !a->dg || !a->db || !a->dv || !a->dw || !a->d_state0)

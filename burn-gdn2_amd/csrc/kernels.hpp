@@ -196,7 +196,8 @@ hipError_t launch_colsum(const float *A, int64_t rows, int64_t N, int64_t lda, i
 
 hipError_t launch_scan(const ScanParams &p, hipStream_t s);
 hipError_t launch_decode(const DecodeParams &p, hipStream_t s);
-bool chunk_supported(int K, int V);
+bool chunk_supported(int K, int V);     // the chunked forward's instances
+bool chunk_bwd_supported(int K, int V); // the chunked backward's
 // phases: bit 0 intra (with the training outputs when ws_akk is set), bit 1
 // inter with the output, bit 2 inter writing ws_sn / ws_vn instead of the
 // output and the final state.

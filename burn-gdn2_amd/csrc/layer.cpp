@@ -1033,7 +1033,7 @@ gdn2_status bwd_workspace(gdn2_layer &L, int64_t B, int64_t T, bool recompute, B
     gdn2_recurrent_bwd_args ra{};
     ra.fwd = recurrent_args_for(ca);
     const size_t chunk_bytes = std::max({gdn2_chunk_workspace_bytes(&ca), gdn2_chunk_bwd_workspace_bytes(&ba),
-                                         chunk_supported((int)d.K, (int)d.V) ? size_t(0)
+                                         chunk_bwd_supported((int)d.K, (int)d.V) ? size_t(0)
                                                                              : gdn2_recurrent_bwd_workspace_bytes(&ra)});
     const size_t f = sizeof(float), nS = f * B * d.HV * d.K * d.V;
     const size_t nk = f * M * d.kd, nv = f * M * d.vd, nY = f * M * L.ld_in;
@@ -1228,7 +1228,7 @@ extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, in
     const Dims &d = L->d;
     // the recurrence's adjoint: the chunked kernels where they apply, else the
     // scan's (which returns GDN2_NOT_APPLICABLE for heads beyond its LDS)
-    const bool use_chunk = chunk_supported((int)d.K, (int)d.V);
+    const bool use_chunk = chunk_bwd_supported((int)d.K, (int)d.V);
     hipStream_t s = (hipStream_t)stream;
     const bool sc = L->cfg.use_short_conv != 0, md = L->cfg.has_min_decay != 0;
     const bool has_state = state_in && state_in->some, has_ds = d_state && d_state->some;

@@ -132,8 +132,9 @@ GDN2_API gdn2_status gdn2_recurrent_fwd_f32(const gdn2_recurrent_args *args, gdn
  * the result does not depend on it beyond rounding, as in the reference.
  * workspace: device memory of at least gdn2_chunk_workspace_bytes(args)
  * bytes, 256-byte aligned.
- * Limits (else GDN2_NOT_APPLICABLE): K in {64, 128}, V in {64, 128, 256};
- * q, k, b rows 16-byte aligned (strides multiples of 4 elements); token
+ * Limits (else GDN2_NOT_APPLICABLE): K in {64, 128} with V in {64, 128, 256},
+ * or K = 256 with V in {128, 256} (the reference's K, V <= 256 at its head
+ * shapes); q, k, b rows 16-byte aligned (strides multiples of 4 elements); token
  * strides at least the row length (stride_qk_t >= K, stride_vw_t >= V) and
  * 63 token strides plus a row under 2 GiB.
  * ---------------------------------------------------------------------- */

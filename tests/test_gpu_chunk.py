@@ -32,6 +32,9 @@ CASES = [
     (2, 2, 2, 97, 64, 64, (-0.3, -0.02), 1.0, 0.5),       # K = V = 64 (config 1 shape)
     (1, 1, 1, 1, 128, 128, (-0.3, -0.02), 1.0, 1.0),      # T = 1
     (1, 1, 2, 63, 64, 128, (-1.0, -0.1), 2.0, 0.3),
+    (2, 2, 2, 150, 256, 256, (-0.3, -0.02), 1.0, 0.5),    # K = V = 256 (head_dim 256), ragged
+    (1, 1, 2, 200, 256, 128, (-0.4, -0.01), 2.0, 0.5),    # K = 256, V = 128, GVA, negative eigenvalues
+    (1, 2, 2, 128, 256, 256, (-31.0, -0.05), 1.0, 0.5),   # K = 256 with spans beyond the f32 exp range
 ]
 
 
@@ -73,6 +76,7 @@ SEG_CASES = [
     (1, 2, 2, 2530, 128, 128, (-0.003, -0.0005), 1.0, 1.0),  # 40 chunks, ragged end
     (1, 1, 2, 6400, 64, 128, (-0.002, 0.0), 2.0, 1.0),       # GVA, negative eigenvalues, 100 chunks
     (1, 2, 2, 2100, 128, 128, (-0.3, -0.02), 1.0, 0.5),
+    (1, 1, 2, 2530, 256, 256, (-0.003, -0.0005), 1.0, 1.0),  # K = V = 256, segmented
     (1, 2, 2, 2560, 128, 128, (-0.001, 0.0), 0.0, 1.0),      # b = 0: P = diag(exp(G)) ~ 0.3-1, S0 carried whole
     (1, 1, 1, 4100, 128, 256, (-5.0, -0.5), 1.0, 1.0),       # strong decay, V = 2K
 ]
@@ -237,6 +241,7 @@ STATE_CASES = [
     (2, 1, 2, 208, 128, 128, 16),    # chunk_size 16, GVA rep 2
     (1, 1, 1, 200, 64, 128, 8),      # chunk_size 8
     (1, 2, 2, 2112, 128, 128, 32),   # chunk_size 32 with the segmented inter
+    (1, 1, 2, 192, 256, 256, 16),    # K = V = 256, chunk_size 16
 ]
 
 

@@ -96,6 +96,20 @@ def test_chunk_bwd_strided_views(gpu):
     _compare(got, ref, "strided")
 
 
+def test_chunk_bwd_declines_k256(gpu):
+    """head_dim 256 runs the chunked forward but not the chunked backward:
+    the reference's `None` (the caller keeps its own path)."""
+    import torch
+
+    import gdn2_amd
+
+    rng = np.random.default_rng(12)
+    d = _dev(gpu, *rand_inputs(rng, 1, 1, 1, 64, 256, 256))
+    S0 = torch.zeros((1, 1, 256, 256), device=gpu)
+    assert gdn2_amd.chunk_wy_forward(*d, S0, 0.0625) is not None
+    assert gdn2_amd.chunk_wy_backward(*d, S0, torch.randn((1, 1, 64, 256), device=gpu), 0.0625) is None
+
+
 def test_chunk_bwd_empty_sequence(gpu):
     import torch
 

@@ -51,6 +51,9 @@ CASES = {
     "gva_negeig_mindecay": (dict(hidden_size=256, num_heads=2, num_v_heads=4, head_dim=64, expand_v=2.0,
                                  allow_neg_eigval=True, min_decay=0.9, mode="chunk"), 2, 200),
     "k128_chunk": (dict(hidden_size=512, num_heads=2, head_dim=128, mode="chunk"), 1, 300),
+    "k256_chunk": (dict(hidden_size=512, num_heads=2, head_dim=256, mode="chunk"), 2, 200),
+    "k256_v128_gva": (dict(hidden_size=512, num_heads=1, num_v_heads=2, head_dim=256, expand_v=0.5, mode="chunk"),
+                      1, 150),
 }
 
 
