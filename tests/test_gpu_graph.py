@@ -1,0 +1,117 @@
+"""The chunked forward under HIP graph capture (torch.cuda.CUDAGraph on the
+stream the C ABI receives): gdn2_chunk_fwd_f32 on a caller workspace and
+gdn2_chunk_fwd_noalloc_f32 on the library's static scratch, and the
+per-token scan.  Each graph is replayed several times with the program's
+own eager work in between (new inputs copied into the captured buffers, the
+state reset), and every replay must equal the eager call on the same inputs
+bit for bit: the entry points launch kernels only (fills by kernel, no
+hipMemsetAsync, no allocation), so a replay runs exactly the eager work."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import rand_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _capture(torch, fn):
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()  # first call outside the capture (static scratch address lookup, module load)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def _sets(rng, n, B, Hk, HV, T, K, V):
+    out = []
+    for _ in range(n):
+        q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=-0.4, g_hi=-0.01)
+        S0 = (rng.standard_normal((B, HV, K, V)) * 0.3).astype(np.float32)
+        out.append((q, k, v, g, b, w, S0))
+    return out
+
+
+@pytest.mark.parametrize("entry", ["gdn2_chunk_fwd_f32", "gdn2_chunk_fwd_noalloc_f32"])
+@pytest.mark.parametrize("shape", [(2, 2, 2, 200, 128, 128), (1, 1, 2, 2048, 128, 128)],
+                         ids=["B2T200", "B1T2048-segmented"])
+def test_chunk_forward_replays_in_a_graph(gpu, entry, shape):
+    import torch
+
+    import gdn2_amd as G
+    from gdn2_amd import _capi as C
+    from gdn2_amd import ops
+
+    B, Hk, HV, T, K, V = shape
+    sets = _sets(np.random.default_rng(hash(shape) % 1000 + len(entry)), 2, B, Hk, HV, T, K, V)
+    bufs = [torch.empty(a.shape, device=gpu) for a in sets[0][:6]]
+    S = torch.empty((B, HV, K, V), device=gpu)
+    out = torch.empty((B, HV, T, V), device=gpu)
+    need = G.chunk_workspace_bytes(*bufs, S, out, K ** -0.5, 64)
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu) if entry == "gdn2_chunk_fwd_f32" else None
+    a = ops.chunk_args(*bufs, S, out, K ** -0.5, 64, ws)
+    fn_c = getattr(C.lib(), entry)
+
+    def fn():
+        C.check(fn_c(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+
+    def load(i):
+        for buf, arr in zip(bufs, sets[i][:6]):
+            buf.copy_(torch.from_numpy(arr))
+        S.copy_(torch.from_numpy(sets[i][6]))
+
+    ref = []
+    for i in range(2):  # eager results
+        load(i)
+        fn()
+        torch.cuda.synchronize()
+        ref.append((out.clone(), S.clone()))
+    load(0)
+    graph = _capture(torch, fn)
+    for rep in range(5):
+        i = rep % 2
+        load(i)  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref[i][0]) and torch.equal(S, ref[i][1]), f"replay {rep}"
+
+
+def test_scan_replays_in_a_graph(gpu):
+    import torch
+
+    import gdn2_amd as G
+
+    B, Hk, HV, T, K, V = 2, 2, 2, 40, 128, 128
+    sets = _sets(np.random.default_rng(21), 2, B, Hk, HV, T, K, V)
+    bufs = [torch.empty(a.shape, device=gpu) for a in sets[0][:6]]
+    S = torch.empty((B, HV, K, V), device=gpu)
+    res = {}
+
+    def fn():
+        res["o"], res["S"] = G.fused_recurrent_forward(*bufs, S, K ** -0.5)
+
+    def load(i):
+        for buf, arr in zip(bufs, sets[i][:6]):
+            buf.copy_(torch.from_numpy(arr))
+        S.copy_(torch.from_numpy(sets[i][6]))
+
+    ref = []
+    for i in range(2):
+        load(i)
+        fn()
+        torch.cuda.synchronize()
+        ref.append((res["o"].clone(), res["S"].clone()))
+    load(0)
+    graph = _capture(torch, fn)
+    for rep in range(4):
+        i = rep % 2
+        load(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(res["o"], ref[i][0]) and torch.equal(res["S"], ref[i][1]), f"replay {rep}"
