@@ -6,6 +6,8 @@
 // dimension ld.
 #include "blas.hpp"
 
+#include "kernels.hpp"
+
 #include <algorithm>
 #include <string>
 
@@ -14,6 +16,14 @@ namespace gdn2 {
 namespace {
 constexpr size_t kMaxWorkspace = size_t(64) << 20;
 constexpr int kCandidates = 32;  // heuristic results timed per shape
+// Shapes of at most this many rows (a decode step) read mostly weights, which
+// the real call finds outside L2 (the step's other kernels stream far more
+// than the 8 x 4 MB of L2): each of their timed runs follows a read sweep
+// over kFlushBytes, twice the L2s together (reads, so that no write-back
+// overlaps the timed run), and a candidate's time is its best of three, so
+// that an algorithm that only wins on L2-resident weights is not picked.
+constexpr int64_t kColdTimingMaxM = 256;
+constexpr size_t kFlushBytes = size_t(64) << 20;
 }
 
 gdn2_status Gemm::ensure_ws(size_t bytes) {
@@ -104,8 +114,10 @@ gdn2_status Gemm::plan(bool ta, bool tb, int64_t M, int64_t N, int64_t Kd, const
                 wsmax = std::max(wsmax, res[i].workspaceSize);
         gdn2_status st = ensure_ws(wsmax);
         if (st != GDN2_OK) return st;
-        float *scratch = nullptr;
+        float *scratch = nullptr, *flush = nullptr;
         hipEvent_t e0 = nullptr, e1 = nullptr;
+        if (M <= kColdTimingMaxM && hipMalloc(&flush, kFlushBytes) != hipSuccess) flush = nullptr;
+        const int64_t nflush = (int64_t)(kFlushBytes / sizeof(float));
         if (hipMalloc(&scratch, sizeof(float) * (size_t)ldc * M) == hipSuccess && hipEventCreate(&e0) == hipSuccess &&
             hipEventCreate(&e1) == hipSuccess) {
             const float alpha = 1.0f, beta = 0.0f;
@@ -113,28 +125,32 @@ gdn2_status Gemm::plan(bool ta, bool tb, int64_t M, int64_t N, int64_t Kd, const
             for (int i = 0; i < n; ++i) {
                 if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kMaxWorkspace) continue;
                 bool ok = true;
-                for (int r = 0; r < 3 && ok; ++r) {  // one warm-up, then two timed runs
-                    if (r == 1) ok = hipEventRecord(e0, s) == hipSuccess;
+                float total = 0.0f;
+                for (int r = 0; r < 4 && ok; ++r) {  // one warm-up, then three timed runs
+                    if (flush) ok = launch_cache_sweep(flush, nflush, flush, s) == hipSuccess;
+                    if (r > 0) ok = ok && hipEventRecord(e0, s) == hipSuccess;
                     ok = ok && hipblasLtMatmul(lt_, p.desc, &alpha, B, p.la, A, p.lb, &beta, scratch, p.lc, scratch,
                                                p.lc, &res[i].algo, res[i].workspaceSize ? ws_ : nullptr,
                                                res[i].workspaceSize, s) == HIPBLAS_STATUS_SUCCESS;
+                    if (r > 0) {
+                        float ms = 0.0f;
+                        ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+                             hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+                        total = (r == 1 || ms < total) ? ms : total;
+                    }
                 }
-                float ms = 0.0f;
-                ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
-                     hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
-                if (ok && (ms < best_ms || best_ms == 0.0f)) {
-                    best_ms = ms;
+                if (ok && (total < best_ms || best_ms == 0.0f)) {
+                    best_ms = total;
                     best = i;
                 }
             }
         }
-        (void)hipGetLastError();  // a failed scratch allocation only skips the timing
+        (void)hipGetLastError();  // a failed scratch allocation only skips the timing (or the flush)
         if (e0) (void)hipEventDestroy(e0);
         if (e1) (void)hipEventDestroy(e1);
-        if (scratch) {
-            (void)hipStreamSynchronize(s);
-            (void)hipFree(scratch);
-        }
+        if (scratch || flush) (void)hipStreamSynchronize(s);
+        if (scratch) (void)hipFree(scratch);
+        if (flush) (void)hipFree(flush);
     }
     p.ok = best >= 0;
     if (p.ok) {

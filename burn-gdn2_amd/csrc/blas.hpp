@@ -2,7 +2,8 @@
 // hipBLASLt, with one plan (descriptors + algorithm) cached per shape.  The
 // algorithm is the fastest of the heuristic's first 32 candidates, timed on
 // the first call's operands into a scratch output (when the stream is not
-// being captured; otherwise the heuristic's first).  rocBLAS runs the shapes
+// being captured; otherwise the heuristic's first), with L2 flushed before
+// each timed run for shapes of at most 256 rows.  rocBLAS runs the shapes
 // hipBLASLt has no algorithm for.
 #pragma once
 

@@ -170,9 +170,13 @@ hipError_t launch_rmsnorm_gate(float *out, int64_t ld_out, const float *x, int64
                                int64_t ld_gate, const float *gate_bias, const float *weight, int64_t M, int HV, int V,
                                float eps, hipStream_t s);
 hipError_t launch_fill_rows(float *y, int64_t ld, const float *row, int64_t M, int64_t N, hipStream_t s);
+// Reads buf[0, n) (16-byte aligned) to push other data out of the caches; writes
+// nothing but, in theory, sink[0].
+hipError_t launch_cache_sweep(const float *buf, int64_t n, float *sink, hipStream_t s);
 
 // f_proj_1 and g_proj_1 for at most kLowRankMaxM rows and rank R in {64, 128,
-// 256} (lowrank_up_kernel).
+// 256} (lowrank_up_kernel), Y 16-byte aligned with ldY and the offsets
+// multiples of 4.
 constexpr int kLowRankMaxM = 256;
 struct LowRankParams {
     const float *Y;           // rows of the input GEMM's output, row stride ldY
@@ -182,7 +186,7 @@ struct LowRankParams {
     float *F, *G;             // [M, kd], [M, vd] row-major
     int M, R, kd, vd;
 };
-bool lowrank_up_supported(int R, int64_t M);
+bool lowrank_up_supported(int R, int64_t M, const float *Y, int64_t ldY, int64_t off_f0, int64_t off_g0);
 hipError_t launch_lowrank_up(const LowRankParams &p, hipStream_t s);
 hipError_t launch_rmsnorm_gate_bwd(const NormBwdParams &p, hipStream_t s);
 hipError_t launch_project_bwd(const ProjectBwdParams &p, hipStream_t s);

@@ -264,7 +264,7 @@ gdn2_status input_gemms(gdn2_layer &L, const float *x, int64_t M, const Work &wk
     gdn2_status st;
     if ((st = L.mm.run(false, false, M, L.ld_in, d.D, x, d.D, L.w_in, L.ld_in, wk.Y, L.ld_in, 0.0f, s)) != GDN2_OK)
         return st;
-    if (lowrank_up_supported((int)d.V, M)) { // a few rows (decode): one small launch for both
+    if (lowrank_up_supported((int)d.V, M, wk.Y, L.ld_in, L.off_f0, L.off_g0)) { // a few rows (decode): one small launch for both
         LowRankParams lp{};
         lp.Y = wk.Y; lp.ldY = L.ld_in; lp.off_f0 = L.off_f0; lp.off_g0 = L.off_g0;
         lp.F1 = L.p[P_F1]; lp.G1 = L.p[P_G1]; lp.g_bias = with_bias ? L.p[P_G1_BIAS] : nullptr;
