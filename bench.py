@@ -14,7 +14,8 @@ Also reported: the whole layer (hipBLASLt Linear layers + kernels) for the
 same prefill; B = 64 fused decode (short conv + gates + L2 norm + step +
 gated RMSNorm per token), the kernel alone over 256 tokens with 5 rotating
 state buffers (335 MB, larger than the 256 MB MALL; the kernel's time does
-not depend on the state values) and the whole layer over a 2048-token
+not depend on the state values) beside a streaming copy of the same bytes,
+and the whole layer over a 2048-token
 prefill then 256 single-token steps; the other benchmark configurations
 (C1 quick-start, C4 GVA + extensions, C5 long context: core per kernel,
 C5's segmented inter passes one by one, and the whole layer); a 1 GiB
@@ -83,6 +84,12 @@ def parse():
                     help="host only: per kernel, the MFMA operations by data type and the shader clock from a "
                          "rocprofv3 --pmc run with SQ_INSTS_VALU_MFMA_MOPS_F32 SQ_INSTS_VALU_MFMA_MOPS_BF16 "
                          "SQ_INSTS_VALU_MFMA_MOPS_XF32 SQ_BUSY_CYCLES GRBM_GUI_ACTIVE")
+    ap.add_argument("--mix-summary", nargs=2, metavar=("COUNTER_CSV_1", "COUNTER_CSV_2"),
+                    help="host only: per-wave instruction mix, MFMA busy and waiting share of the timed kernels "
+                         "from two rocprofv3 --pmc runs (SQ_WAVES SQ_BUSY_CYCLES SQ_WAVE_CYCLES SQ_INSTS_VALU "
+                         "SQ_INSTS_LDS SQ_INSTS_VMEM_RD SQ_INSTS_VMEM_WR SQ_INSTS_MFMA, then "
+                         "SQ_VALU_MFMA_BUSY_CYCLES SQ_WAIT_INST_ANY SQ_WAIT_ANY SQ_LDS_BANK_CONFLICT "
+                         "SQ_ACTIVE_INST_VMEM SQ_ACTIVE_INST_LDS SQ_INSTS_SALU GRBM_GUI_ACTIVE)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="host only: per-launch HBM bytes from two rocprofv3 --pmc runs (FETCH_SIZE, "
                          "WRITE_SIZE) of this script with --copy-calibration; writes profiles/*_traffic.json")
@@ -324,6 +331,43 @@ def bench_copy_roof(torch, dev, reps=10):
             "what": "1 GiB device-to-device copy (gdn2_stream_copy_f32, best grid), read + write"}
 
 
+def decode_copy_roof(torch, dev, bytes_step, steps, nrot):
+    """The decode step's bytes as a plain copy: gdn2_stream_copy_f32 reading
+    and writing bytes_step / 2 each, over nrot rotating buffer pairs like the
+    decode's states, best of a few grid sizes.  The decode kernel's time
+    against it is its distance from a streaming kernel of the same size."""
+    import ctypes
+
+    from gdn2_amd import _capi as CA
+    from gdn2_amd.ops import _stream
+
+    n = bytes_step // 8 // 4 * 4
+    src = [torch.ones(n, device=dev) for _ in range(nrot)]
+    dst = [torch.empty(n, device=dev) for _ in range(nrot)]
+    L, stream = CA.lib(), _stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    best = None
+    for wg in (512, 1024, 2048):
+        def one(t):
+            CA.check(L.gdn2_stream_copy_f32(ctypes.c_void_p(dst[t % nrot].data_ptr()),
+                                            ctypes.c_void_p(src[t % nrot].data_ptr()), n, wg, stream))
+        for t in range(8):
+            one(t)
+        torch.cuda.synchronize()
+        e0.record()
+        for t in range(steps):
+            one(t)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / steps * 1e3
+        if best is None or us < best["us"]:
+            best = {"us": us, "GBs": 8 * n / (us / 1e6) / 1e9, "workgroups": wg}
+    del src, dst
+    torch.cuda.empty_cache()
+    best["bytes"] = 8 * n
+    return best
+
+
 def mfma_summary(path, n_se=32, n_xcc=8):
     """MFMA operations (the MOPS counters count 512 flops each) by data type
     and the clock per kernel, over dispatches longer than 100 us:
@@ -509,12 +553,14 @@ def bench_decode(torch, G, args, dev):
     param_bytes = (4 * (2 * kd + vd) + H + kd + V) * 4
     bytes_step = state_bytes + io_bytes + param_bytes
     gbs = bytes_step / (ms / 1e3) / 1e9
+    copy_same = decode_copy_roof(torch, dev, bytes_step, steps, nrot)
     tr = load_traffic("decode_b64_traffic.json") if Bd == 64 else None
     res = {"batch": Bd, "tokens_per_s": Bd / (ms / 1e3), "ms_per_token_step": ms, "bytes_per_step": bytes_step,
            "traffic": None if tr is None else tr.get("hbm_bytes_per_launch"),
            "core_bytes_per_step": 2 * Bd * H * K * V * 4 + Bd * (4 * H * K + 3 * H * V) * 4,
            "achieved_GBs": gbs, "peak_GBs": PEAK_HBM_GBS, "frac_hbm": gbs / PEAK_HBM_GBS,
-           "rotating_state_buffers": nrot, "kernel": "gdn2_decode_fused_f32"}
+           "rotating_state_buffers": nrot, "kernel": "gdn2_decode_fused_f32",
+           "copy_same_bytes": copy_same, "frac_copy_same_bytes": copy_same["us"] / (ms * 1e3)}
     del blocks, states, conv, raw, x, W
     if not args.no_layer:
         layer = G.GatedDeltaNet2(cfg, seed=1337)
@@ -675,7 +721,7 @@ KERNELS = {"chunk_intra": "chunk_intra_kernel<128, 128, false>", "chunk_inter": 
 def _short(name):
     import re
 
-    m = re.search(r"gdn2::\(anonymous namespace\)::(\w+(<[^>]*>)?)", name)
+    m = re.search(r"(?:gdn2::)?\(anonymous namespace\)::(\w+(<[^>]*>)?)", name)
     if m:
         return m.group(1)
     return name.split("(")[0].replace("void ", "")[:70]
@@ -763,9 +809,44 @@ def train_summary(path):
     print(f"\nspan {span:.1f} us; GEMM kernels {gemm:.1f} us, other kernels {other:.1f} us")
 
 
+def mix_summary(csv1, csv2, n_xcc=8, n_simd=1024):
+    """Per dispatch of each timed kernel, counters summed over the chip, then
+    averaged over its dispatches: instructions per wave, MFMA busy =
+    SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / n_xcc x n_simd), waiting =
+    SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES."""
+    import csv
+
+    per = {}
+    for path in (csv1, csv2):
+        for r in csv.DictReader(open(path)):
+            for key, frag in KERNELS.items():
+                if frag in r["Kernel_Name"]:
+                    d = per.setdefault(key, {}).setdefault(r["Dispatch_Id"], {})
+                    d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+
+    def mean(key, name, scale=None):
+        vals = [d[name] / (d[scale] if scale else 1.0) for d in per[key].values() if name in d and (not scale or d.get(scale))]
+        return sum(vals) / len(vals) if vals else float("nan")
+
+    print("| kernel | waves | VALU | MFMA | SALU | LDS | VMEM rd / wr | MFMA busy (per SIMD) | wave cycles waiting |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for key in KERNELS:
+        if key not in per:
+            continue
+        waves = mean(key, "SQ_WAVES")
+        busy = [d["SQ_VALU_MFMA_BUSY_CYCLES"] / (d["GRBM_GUI_ACTIVE"] / n_xcc * n_simd)
+                for d in per[key].values() if d.get("GRBM_GUI_ACTIVE") and "SQ_VALU_MFMA_BUSY_CYCLES" in d]
+        busy_s = f"{100 * sum(busy) / len(busy):.1f} %" if busy and key != "decode" else "-"
+        wait = mean(key, "SQ_WAIT_INST_ANY") / mean(key, "SQ_WAVE_CYCLES")
+        pw = lambda n: mean(key, n) / waves
+        print(f"| {key} | {waves:.0f} | {pw('SQ_INSTS_VALU'):.0f} | {pw('SQ_INSTS_MFMA'):.0f} | {pw('SQ_INSTS_SALU'):.0f} | "
+              f"{pw('SQ_INSTS_LDS'):.0f} | {pw('SQ_INSTS_VMEM_RD'):.0f} / {pw('SQ_INSTS_VMEM_WR'):.0f} | {busy_s} | "
+              f"{100 * wait:.0f} % |")
+
+
 def traffic_summary(fetch_csv, write_csv):
     """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) per kernel, scaled so that
-    the 1 GiB copy reads and writes 1 GiB."""
+    the 1 GiB streaming copy (gdn2_stream_copy_f32) reads and writes 1 GiB."""
     import csv
 
     def per_kernel(path, counter):
@@ -779,10 +860,12 @@ def traffic_summary(fetch_csv, write_csv):
     fetch, write = per_kernel(fetch_csv, "FETCH_SIZE"), per_kernel(write_csv, "WRITE_SIZE")
 
     def copy_bytes(acc):
-        # the largest single dispatch of a copy kernel is the 1 GiB calibration copy
+        # the largest dispatch of the library's streaming copy is the 1 GiB
+        # copy of the measured roof (torch's own kernels of the run read other
+        # sizes, e.g. comparisons of two 1 GiB tensors)
         best = 0.0
         for name, vals in acc.items():
-            if "copy" in name.lower() or "elementwise" in name:
+            if "stream_copy_kernel" in name:
                 best = max(best, max(vals))
         return best
 
@@ -871,6 +954,9 @@ def main():
         return
     if args.mfma_summary:
         mfma_summary(args.mfma_summary)
+        return
+    if args.mix_summary:
+        mix_summary(*args.mix_summary)
         return
     if args.configs_summary:
         configs_summary(args.configs_summary, args.warmup, args.config_steps)
