@@ -829,10 +829,12 @@ struct Json {
         }
         return v;
     }
-    // skips any value (used for unknown metadata entries)
-    void skip() {
+    // skips any value (used for unknown metadata entries); nesting deeper
+    // than kMaxDepth is rejected rather than recursed into
+    static constexpr int kMaxDepth = 64;
+    void skip(int depth = 0) {
         ws();
-        if (p >= end) { ok = false; return; }
+        if (p >= end || depth > kMaxDepth) { ok = false; return; }
         if (*p == '"') { str(); return; }
         if (*p == '{' || *p == '[') {
             const char open = *p, close = open == '{' ? '}' : ']';
@@ -840,7 +842,7 @@ struct Json {
             if (eat(close)) return;
             do {
                 if (open == '{') { str(); if (!eat(':')) { ok = false; return; } }
-                skip();
+                skip(depth + 1);
                 if (!ok) return;
             } while (eat(','));
             if (!eat(close)) ok = false;

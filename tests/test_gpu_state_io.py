@@ -103,3 +103,47 @@ def test_deserialize_rejects_mismatches(gpu):
     with pytest.raises(Gdn2Error, match="truncated header|header length"):
         st.load_bytes(b"\x01\x02")
     assert not st.is_some  # nothing was loaded
+
+
+def _with_header(header: str, data: bytes) -> bytes:
+    h = header.encode()
+    h += b" " * ((8 - (8 + len(h)) % 8) % 8)
+    return len(h).to_bytes(8, "little") + h + data
+
+
+def test_deserialize_survives_malformed_bytes(gpu):
+    """Every truncation is refused; seeded byte flips in the header either
+    load (a flip that leaves a valid header) or raise Gdn2Error; metadata
+    nested 100000 deep is refused without recursing into it; a header length
+    beyond the buffer is refused.  The good bytes still load afterwards."""
+    from gdn2_amd._capi import Gdn2Error
+
+    G, layer, x = _setup(gpu)
+    _, st = layer.forward(x[:, :70])
+    good = st.to_bytes()
+    hn = int.from_bytes(good[:8], "little")
+    target = G.Gdn2State(layer, 2)
+    rng = np.random.default_rng(5)
+    cuts = set(rng.integers(0, len(good), 40).tolist()) | {0, 7, 8, 9, 8 + hn - 1, 8 + hn, len(good) - 1}
+    for cut in sorted(cuts):
+        with pytest.raises(Gdn2Error):
+            target.load_bytes(good[:cut])
+    for _ in range(300):
+        buf = bytearray(good)
+        for pos in rng.integers(8, 8 + hn, int(rng.integers(1, 4))):
+            buf[int(pos)] = int(rng.integers(0, 256))
+        try:
+            target.load_bytes(bytes(buf))
+        except Gdn2Error:
+            pass
+    header = good[8:8 + hn].decode().rstrip(" ")
+    deep = header.replace('"__metadata__":{', '"__metadata__":{"x":' + "[" * 100000 + "]" * 100000 + ",", 1)
+    with pytest.raises(Gdn2Error, match="malformed"):
+        target.load_bytes(_with_header(deep, good[8 + hn:]))
+    shallow = header.replace('"__metadata__":{', '"__metadata__":{"x":' + "[" * 8 + "]" * 8 + ",", 1)
+    target.load_bytes(_with_header(shallow, good[8 + hn:]))  # moderate nesting is fine
+    with pytest.raises(Gdn2Error, match="header length"):
+        target.load_bytes((2 ** 63).to_bytes(8, "little") + good[8:])
+    target.load_bytes(good)
+    for name in ("recurrent", "conv_q", "conv_k", "conv_v"):
+        assert np.array_equal(getattr(target, name), getattr(st, name)), name
