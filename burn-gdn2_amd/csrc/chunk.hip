@@ -103,6 +103,14 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
     const int lg_q = 4 * lg * rq;  // row 4 lg of a tile, q/k/g/b
     const int lg_v = 4 * lg * rv;  // row 4 lg of a tile, v/w
 
+    // Wave roles of the score products (phase 2): A_qk (mat 0) or A_kk (mat 1),
+    // row tiles {half, NT-1-half}, channel half kh.  Their row operands (q or
+    // b rows, araw) are requested in phase 1, right after its own loads, so
+    // that they arrive while phase 1 computes instead of after its barriers.
+    const int mat = wave >> 2, half = (wave >> 1) & 1, kh = wave & 1;
+    const int m0 = kh * NKH;
+    floatx4 araw[2][NKH];
+
     // 1. k -> sK; G = cumsum_t g per channel -> sG in log2 units.  Rows past
     //    the end of a ragged last chunk are zero (src/forward.rs:94-99).
     {
@@ -115,6 +123,14 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
         float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < RPS; ++i) vals[i] = bld1(Rg, c + (seg * RPS + i) * rq);
+#pragma unroll
+        for (int pi = 0; pi < 2; ++pi) {
+            const int row = 16 * (pi ? (NT - 1 - half) : half) + lr;
+#pragma unroll
+            for (int m = 0; m < NKH; ++m)
+                araw[pi][m] = bld4(mat == 0 ? Rq : Rb, lr_q + (row - lr) * rq + 16 * (m0 + m) + 4 * lg);
+        }
+        __builtin_amdgcn_sched_barrier(0); // the waits below leave araw in flight
 #pragma unroll
         for (int i = 0; i < RPS; ++i) {
             acc += vals[i];
@@ -177,19 +193,31 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
     //    blocks, over the channel half kh; the two halves are summed through
     //    LDS below.  The row operands, with exp(G) applied, are kept for the
     //    solve: q exp(G) (A_qk waves) and b k exp(G) (A_kk waves).
+    // The solve's value-column right-hand sides w, v of row tile pt, for the
+    // column tiles nt = wave + NW u past the key columns (slot sl of r1 / r2).
+    // With one value-column tile per wave every row tile gets its own slot
+    // (all requested at once); with more, two slots rotate.
+    constexpr bool ALLV = NTW - NKW <= 1;
+    constexpr int NSL = ALLV ? NT : 2;
+    floatx4 r1[NSL][NTW], r2[NSL][NTW];
+    auto load_vw = [&](int pt, int sl) {
+#pragma unroll
+        for (int u = 0; u < NTW; ++u) {
+            const int nt = wave + NW * u;
+            if (nt < NTOT && nt >= NKT) {
+                const int c = 16 * (nt - NKT) + lr;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * pt + 4 * lg + i;
+                    r1[sl][u][i] = bld1(Rw, lg_v + (t - 4 * lg) * rv + c);
+                    r2[sl][u][i] = bld1(Rv, lg_v + (t - 4 * lg) * rv + c);
+                }
+            }
+        }
+    };
     floatx4 stR[NKW][NT]; // the solve's key-column right-hand sides (staged below)
     floatx4 *QGf = reinterpret_cast<floatx4 *>(p.ws_qg) + cid * (C * K / 4);
     {
-        const int mat = wave >> 2, half = (wave >> 1) & 1, kh = wave & 1;
-        const int m0 = kh * NKH;
-        floatx4 araw[2][NKH];
-#pragma unroll
-        for (int pi = 0; pi < 2; ++pi) {
-            const int row = 16 * (pi ? (NT - 1 - half) : half) + lr;
-#pragma unroll
-            for (int m = 0; m < NKH; ++m)
-                araw[pi][m] = bld4(mat == 0 ? Rq : Rb, lr_q + (row - lr) * rq + 16 * (m0 + m) + 4 * lg);
-        }
         floatx4 acc[2][NT];
 #pragma unroll
         for (int pi = 0; pi < 2; ++pi) {
@@ -266,6 +294,9 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
                 }
             }
         }
+        // Row tile 0's value-column right-hand sides: requested now, so that
+        // they arrive during the reductions and the diagonal inverses.
+        load_vw(0, 0);
         // The solve's right-hand sides b k exp(G_r) (A_kk waves), from the b
         // rows still held in araw since the score products (128 VGPRs, no
         // spill): a second read from global memory missed L2 about half the
@@ -407,8 +438,10 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
     // 4. Blocked solve of (I + A_kk) [W | U] = [b k exp(G) | w v]; wave w owns
     //    column tiles w, w + 8, ... of [W | U]
     //    (key columns first, whose right-hand sides were staged above; the
-    //    value columns' w, v rows of tile p+1 are loaded while tile p is
-    //    solved).  Outputs go to the workspace in MFMA fragment order (one
+    //    value columns' w, v rows of tile 0 were requested after the score
+    //    products, those of the other tiles are requested here at once, or
+    //    one tile ahead when a wave owns several value-column tiles).
+    //    Outputs go to the workspace in MFMA fragment order (one
     //    1 KB block of 64 lanes x float4 per 16x16 tile) so that every store
     //    here and every load in chunk-inter is a contiguous 16-byte access per
     //    lane:
@@ -417,28 +450,14 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
     floatx4 *Wf = reinterpret_cast<floatx4 *>(p.ws_w) + cid * (C * K / 4);
     floatx4 *Uf = reinterpret_cast<floatx4 *>(p.ws_u) + cid * (C * V / 4);
     floatx4 X[NTW][NT];
-    floatx4 r1[2][NTW], r2[2][NTW];
+    if constexpr (ALLV) {
 #pragma unroll
-    for (int pt = 0; pt <= NT; ++pt) {
-        if (pt < NT) { // issue the value-column loads of row tile pt (consumed at iteration pt + 1)
-            const int sl = pt & 1;
+        for (int pt = 1; pt < NT; ++pt) load_vw(pt, pt); // the other row tiles' value columns, all at once
+    }
 #pragma unroll
-            for (int u = 0; u < NTW; ++u) {
-                const int nt = wave + NW * u;
-                const bool kcol = nt < NKT;
-                if (nt < NTOT && !kcol) {
-                    const int c = 16 * (nt - NKT) + lr;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int t = 16 * pt + 4 * lg + i;
-                        r1[sl][u][i] = bld1(Rw, lg_v + (t - 4 * lg) * rv + c);
-                        r2[sl][u][i] = bld1(Rv, lg_v + (t - 4 * lg) * rv + c);
-                    }
-                }
-            }
-        }
-        if (pt == 0) continue;
-        const int tp = pt - 1, sl = tp & 1; // the row tile solved in this iteration
+    for (int pt = 1; pt <= NT; ++pt) {
+        if (!ALLV && pt < NT) load_vw(pt, pt & 1); // row tile pt's value columns, consumed at iteration pt + 1
+        const int tp = pt - 1, sl = ALLV ? tp : tp & 1; // the row tile solved in this iteration
 #pragma unroll
         for (int u = 0; u < NTW; ++u) {
             const int nt = wave + NW * u;
