@@ -265,7 +265,13 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
             }
         }
         // Diagonal blocks, channels (of this half) outside the safe span: exact
-        // pairwise terms (after the products, so no row load is outstanding here).
+        // pairwise terms.  The row operand q or b of channel c and row 16 pt + r
+        // is already in this wave's registers: component c % 4 of
+        // araw[pi][c / 16 - m0] in lane 16 ((c % 16) / 4) + r.  It is gathered
+        // across lanes (ds_bpermute) rather than read again from memory, which
+        // costs one round trip per masked channel.  The training variant, whose
+        // registers are fuller, reads it from memory (keeping araw live here
+        // would spill 72 bytes per lane).
 #pragma unroll
         for (int pi = 0; pi < 2; ++pi) {
             const int pt = pi ? (NT - 1 - half) : half;
@@ -277,6 +283,16 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
                         while (mw) {
                             const int c = wd * 32 + __builtin_ctz(mw);
                             mw &= mw - 1u;
+                            const int cm = (c >> 4) - m0, cj = c & 3, cg = (c & 15) >> 2;
+                            float own = 0.f;
+                            if constexpr (!TRAIN) {
+#pragma unroll
+                                for (int m = 0; m < NKH; ++m)
+#pragma unroll
+                                    for (int j = 0; j < 4; ++j)
+                                        if (m == cm && j == cj) own = araw[pi][m][j];
+                            }
+                            const int owni = __builtin_bit_cast(int, own);
                             const int srow = 16 * pt + lr;
                             const float ks = sK[srow][c];
                             const float gs = sG[srow][c];
@@ -284,8 +300,10 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
                             for (int i = 0; i < 4; ++i) {
                                 const int r = 4 * lg + i;
                                 const int rrow = 16 * pt + r;
-                                const int ro = lg_q + (16 * pt + i) * rq + c; // row rrow
-                                const float xr = (mat == 0) ? bld1(Rq, ro) : bld1(Rb, ro) * sK[rrow][c];
+                                const float xg =
+                                    TRAIN ? bld1(mat == 0 ? Rq : Rb, lg_q + (16 * pt + i) * rq + c) // row rrow
+                                          : __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (16 * cg + r), owni));
+                                const float xr = (mat == 0) ? xg : xg * sK[rrow][c];
                                 const float e = (mat == 0 ? (r >= lr) : (r > lr)) ? fast_exp2(sG[rrow][c] - gs) : 0.f;
                                 acc[pi][q][i] += xr * ks * e;
                             }
