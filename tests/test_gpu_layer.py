@@ -54,6 +54,8 @@ CASES = {
     "k256_chunk": (dict(hidden_size=512, num_heads=2, head_dim=256, mode="chunk"), 2, 200),
     "k256_v128_gva": (dict(hidden_size=512, num_heads=1, num_v_heads=2, head_dim=256, expand_v=0.5, mode="chunk"),
                       1, 150),
+    # at most 256 rows: the rank-256 up-projections take the one-launch MFMA kernel
+    "k256_few_rows": (dict(hidden_size=512, num_heads=2, head_dim=256, mode="chunk"), 2, 100),
 }
 
 
