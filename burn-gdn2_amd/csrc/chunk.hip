@@ -1039,10 +1039,13 @@ struct WsLayout {
 
 // Segments per sequence for chunk-inter.  Few long sequences are split so
 // that the output pass runs about one workgroup per compute unit (an MI355X
-// has 256); a segment keeps at least 16 chunks, so that the two extra passes
-// stay small against the work they spread.
+// has 256); a segment keeps at least 4 chunks.  The split only binds where
+// the sequences leave most of the chip idle, so the extra passes' work (each
+// segment's transition, the chain) costs little beside the shorter walk: at
+// 4 value heads x 16 chunks (hidden 256, K = V = 64) chunk-inter takes 57 us
+// in 4 segments against 79 us in one.
 constexpr int64_t kInterWorkgroups = 256;
-constexpr int64_t kMinSegmentChunks = 16;
+constexpr int64_t kMinSegmentChunks = 4;
 
 struct Segments {
     int nseg, segl;

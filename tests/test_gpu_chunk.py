@@ -70,9 +70,9 @@ def _base_workspace_bytes(B, HV, T, K, V):
 
 
 SEG_CASES = [
-    # few long sequences: chunk-inter splits each sequence into segments.  Slow
-    # decays keep a segment's transition P far from 0 (exp(g * 1280) ~ 0.02-0.5
-    # over a 20-chunk segment), so that S0 and the chaining both reach the output.
+    # few long sequences: chunk-inter splits each sequence into segments (of at
+    # least 4 chunks).  Slow decays keep the transitions P far from 0 over a
+    # segment, so that S0 and the chaining both reach the output.
     (1, 2, 2, 2530, 128, 128, (-0.003, -0.0005), 1.0, 1.0),  # 40 chunks, ragged end
     (1, 1, 2, 6400, 64, 128, (-0.002, 0.0), 2.0, 1.0),       # GVA, negative eigenvalues, 100 chunks
     (1, 2, 2, 2100, 128, 128, (-0.3, -0.02), 1.0, 0.5),
