@@ -61,14 +61,15 @@ __global__ __launch_bounds__(256) void project_kernel(ProjectParams p) {
     extern __shared__ float sm[];
     const int nb = (p.T + kProjTB - 1) / kProjTB;
     const int bi = blockIdx.x / nb, t0 = (blockIdx.x % nb) * kProjTB;
+    const int head = blockIdx.y;
     const int tn = min(kProjTB, p.T - t0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool sc = p.use_short_conv != 0;
     const int kd = p.H * p.K, vd = p.HV * p.V;
     const float *Y0 = p.Y + (int64_t)bi * p.T * p.ldY;  // token 0 of this sequence
     constexpr int NRUN = kProjTB / kProjRun;
-    if ((int)blockIdx.y < p.H) {
-        const int h = blockIdx.y, K = p.K, K1 = K + 1;
+    if (head < p.H) {
+        const int h = head, K = p.K, K1 = K + 1;
         const int64_t ob = ((int64_t)bi * p.H + h) * p.T * K;  // [B, H, T, K] row of token 0
         // staging of the activated q, k of token t0 + tl, channel c
         const bool lds = K <= kProjLdsMaxK;
@@ -151,7 +152,7 @@ __global__ __launch_bounds__(256) void project_kernel(ProjectParams p) {
             }
         }
     } else {
-        const int hv = blockIdx.y - p.H, V = p.V;
+        const int hv = head - p.H, V = p.V;
         const int64_t ob = ((int64_t)bi * p.HV + hv) * p.T * V;  // [B, HV, T, V] row of token 0
         for (int e = tid; e < V * NRUN; e += 256) {
             const int c = e % V, run = e / V, gc = hv * V + c;
@@ -220,6 +221,8 @@ __global__ __launch_bounds__(256) void conv_cache_kernel(ConvCacheParams p) {
     }
 }
 
+constexpr int kNormHeld = 4; // row elements per lane held in registers (V <= 256)
+
 // rms_norm_gate_per_head (src/module.rs:501-517): one wave per (token, value head).
 __global__ __launch_bounds__(256) void rmsnorm_gate_kernel(float *out, int64_t ld_out, const float *x, int64_t ld_x,
                                                            const float *gate, int64_t ld_gate, const float *gate_bias,
@@ -232,11 +235,35 @@ __global__ __launch_bounds__(256) void rmsnorm_gate_kernel(float *out, int64_t l
     const float *xr = x + m * ld_x + (int64_t)hv * V;
     const float *gr = gate + m * ld_gate + (int64_t)hv * V;
     float *orow = out + m * ld_out + (int64_t)hv * V;
+    const float *br = gate_bias ? gate_bias + (int64_t)hv * V : nullptr;
+    if (V <= 64 * kNormHeld) {
+        // every operand of the row requested before the reduction: one memory
+        // round trip per row instead of two
+        float xv[kNormHeld], gv[kNormHeld], wv[kNormHeld];
+#pragma unroll
+        for (int u = 0; u < kNormHeld; ++u) {
+            const int i = lane + 64 * u;
+            const bool in = i < V;
+            xv[u] = in ? xr[i] : 0.f;
+            gv[u] = in ? gr[i] + (br ? br[i] : 0.f) : 0.f;
+            wv[u] = in ? weight[i] : 0.f;
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < kNormHeld; ++u) ss += xv[u] * xv[u];
+        ss = wave_sum(ss);
+        const float rms = sqrtf(ss / (float)V + eps);
+#pragma unroll
+        for (int u = 0; u < kNormHeld; ++u) {
+            const int i = lane + 64 * u;
+            if (i < V) orow[i] = xv[u] / rms * wv[u] * silu_(gv[u]);
+        }
+        return;
+    }
     float ss = 0.f;
     for (int i = lane; i < V; i += 64) ss += xr[i] * xr[i];
     ss = wave_sum(ss);
     const float rms = sqrtf(ss / (float)V + eps);
-    const float *br = gate_bias ? gate_bias + (int64_t)hv * V : nullptr;
     for (int i = lane; i < V; i += 64) orow[i] = xr[i] / rms * weight[i] * silu_(gr[i] + (br ? br[i] : 0.f));
 }
 
