@@ -35,6 +35,9 @@ CASES = [
     (2, 2, 2, 150, 256, 256, (-0.3, -0.02), 1.0, 0.5),    # K = V = 256 (head_dim 256), ragged
     (1, 1, 2, 200, 256, 128, (-0.4, -0.01), 2.0, 0.5),    # K = 256, V = 128, GVA, negative eigenvalues
     (1, 2, 2, 128, 256, 256, (-31.0, -0.05), 1.0, 0.5),   # K = 256 with spans beyond the f32 exp range
+    (1, 2, 2, 100, 128, 64, (-0.3, -0.02), 1.0, 0.5),     # K = 128, V = 64, ragged
+    (1, 2, 2, 96, 128, 64, (-31.0, -0.05), 1.0, 0.5),     # V = 64 with spans beyond the f32 exp range
+    (1, 1, 2, 130, 64, 256, (-31.0, -0.05), 2.0, 0.5),    # K = 64, V = 256, GVA, neg-eig, the exact diagonal path
 ]
 
 
