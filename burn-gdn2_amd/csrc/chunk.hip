@@ -528,6 +528,8 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
 //   B: v_new = U - X1
 //   C: S = exp(G_last) S + Kd^T v_new         (reads sKd)
 //   D: out = X2 + A_qk v_new                  (reads sA; independent of C)
+// D(n) runs at the top of iteration n + 1, before the wait for chunk n + 1's
+// copies, whose latency its MFMAs cover.
 // LDS holds one chunk of W, q exp(G) (2 C K floats), Kd^T (K C) and A_qk
 // (C C).  Each buffer is refilled while another phase runs: Kd^T(n) and
 // A_qk(n) are fetched during A(n) and stored after it; W, q exp(G)(n+1) are
@@ -668,10 +670,28 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
                     if (16 * mt + 4 * lg + i < cv) ob[(int64_t)(nn * C + 16 * mt + i) * p.sot] = o[mt][i];
         }
     };
-    floatx4 X2[NT]; // chunk n's output, stored early in iteration n + 1
+    floatx4 X1[NT], X2[NT]; // chunk n's v_new and output, both read again in iteration n + 1
+    // D: out = X2 + A_qk v_new (A_qk is lower block-triangular; the chains of
+    // the four time tiles interleave).  D(n) runs at the top of iteration
+    // n + 1, where its MFMAs cover this wave's wait for the next copies: sA
+    // still holds A_qk(n) there, as the next copy into it comes after the
+    // barrier that follows.
+    auto phase_d = [&]() {
+#pragma unroll
+        for (int qt = 0; qt < NT; ++qt) {
+            floatx4 aa[NT];
+#pragma unroll
+            for (int mt = qt; mt < NT; ++mt) aa[mt] = sA[(mt * NT + qt) * 64 + lane];
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int mt = qt; mt < NT; ++mt) X2[mt] = mfma16(aa[mt][st], X1[qt][st], X2[mt]);
+        }
+    };
     for (int n = n0; n < n1; ++n) {
         const size_t cid = cid0 + n;
         const size_t cnext = n + 1 < n1 ? cid + 1 : cid;
+        if (OUT && n > n0) phase_d(); // D(n - 1)
         vm_wait<3>();  // this wave's copies of chunk n's W, q exp(G) have landed (not the 3 touches after them)
         lds_barrier(); // sW, sQ hold chunk n; every wave is done with sKd, sA (n-1)
 #pragma unroll
@@ -706,7 +726,6 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         __builtin_amdgcn_sched_barrier(0);
 
         // A: X1 = W S, X2 = scale (q exp(G)) S
-        floatx4 X1[NT];
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) X1[mt] = X2[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -762,22 +781,6 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         touch_kau(cnext);
         __builtin_amdgcn_sched_barrier(0);
 
-        // D: out = X2 + A_qk v_new (A_qk is lower block-triangular); the
-        // chains of the four time tiles interleave, and the stores wait until
-        // the next chunk so that no MFMA result is waited on early
-        if (OUT) {
-#pragma unroll
-            for (int qt = 0; qt < NT; ++qt) {
-                floatx4 aa[NT];
-#pragma unroll
-                for (int mt = qt; mt < NT; ++mt) aa[mt] = sA[(mt * NT + qt) * 64 + lane];
-#pragma unroll
-                for (int st = 0; st < 4; ++st)
-#pragma unroll
-                    for (int mt = qt; mt < NT; ++mt) X2[mt] = mfma16(aa[mt][st], X1[qt][st], X2[mt]);
-            }
-        }
-
         // C: S = exp(G_last) S + Kd^T v_new
 #pragma unroll
         for (int kb = 0; kb < NKT; ++kb) {
@@ -803,7 +806,10 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         }
     }
     vm_wait0(); // the last touches have landed in sPf
-    if (OUT && n1 > n0) store_out(X2, n1 - 1);
+    if (OUT && n1 > n0) {
+        phase_d();
+        store_out(X2, n1 - 1);
+    }
 
     // leaving state: the final state (last segment), Q_j or P_j (pass 1)
     float *Sout = nullptr;
