@@ -575,6 +575,9 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     constexpr bool QLDS = OUT && K <= 128;
     __shared__ floatx4 sQ[QLDS ? OPF4 : 1], sA[OUT ? AF4 : 1];
     __shared__ float sPf[256]; // destination of the L2 touches, never read
+    // exp(G_last) of the chunk, copied with Kd^T: read just before phase C, so
+    // that it holds no registers through phases A and D
+    __shared__ floatx4 sGam[K / 4];
 
     const int V = p.V;
     const int nvv = V / 64;                   // value slices
@@ -704,10 +707,8 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
                 if (i >= wave) lds_copy4(&A4[cid * AF4 + i * 256 + tid], &sA[i * 256 + wv]);
             if (n > n0) store_out(X2, n - 1);
         }
-        // exp(G_last) for this lane's rows 16 kb + 4 lg .. + 3 of S
-        floatx4 u_cur[NT], gam[NKT];
-#pragma unroll
-        for (int kb = 0; kb < NKT; ++kb) gam[kb] = G4[cid * (K / 4) + 4 * kb + lg];
+        if (wave == 0 && lane < K / 4) lds_copy4(&G4[cid * (K / 4) + lane], sGam);
+        floatx4 u_cur[NT];
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt)
             u_cur[mt] = pcol ? floatx4{0.f, 0.f, 0.f, 0.f} : U4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
@@ -745,7 +746,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
                     if (OUT) X2[mt] = mfma16(ma[mt][st], S[kb][st], X2[mt]);
                 }
         }
-        vm_wait<2>();  // this wave's copies of chunk n's Kd, A_qk and its U, exp(G_last) have landed (not the 2 touches)
+        vm_wait<2>();  // this wave's copies of chunk n's Kd, A_qk, exp(G_last) and its U have landed (not the 2 touches)
         lds_barrier(); // A done everywhere (sW, sQ free); sKd(n), sA(n) visible
 
         // B: v_new = U - X1 (kept in X1)
@@ -784,10 +785,11 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         // C: S = exp(G_last) S + Kd^T v_new
 #pragma unroll
         for (int kb = 0; kb < NKT; ++kb) {
-            S[kb][0] *= gam[kb][0];
-            S[kb][1] *= gam[kb][1];
-            S[kb][2] *= gam[kb][2];
-            S[kb][3] *= gam[kb][3];
+            const floatx4 gk = sGam[4 * kb + lg]; // exp(G_last) of rows 16 kb + 4 lg .. + 3
+            S[kb][0] *= gk[0];
+            S[kb][1] *= gk[1];
+            S[kb][2] *= gk[2];
+            S[kb][3] *= gk[3];
         }
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt) {
