@@ -676,20 +676,23 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     floatx4 X1[NT], X2[NT]; // chunk n's v_new and output, both read again in iteration n + 1
     // D: out = X2 + A_qk v_new (A_qk is lower block-triangular; the chains of
     // the four time tiles interleave).  D(n) runs at the top of iteration
-    // n + 1, where its MFMAs cover this wave's wait for the next copies: sA
-    // still holds A_qk(n) there, as the next copy into it comes after the
-    // barrier that follows.
+    // n + 1, where its MFMAs cover this wave's wait for the next copies.  Its
+    // A_qk tiles are read from sA during the last time tile of C(n), so that
+    // D waits on no LDS read.
+    floatx4 aq[NT][NT]; // A_qk tiles (mt, qt), mt >= qt
+    auto load_aq = [&]() {
+#pragma unroll
+        for (int qt = 0; qt < NT; ++qt)
+#pragma unroll
+            for (int mt = qt; mt < NT; ++mt) aq[mt][qt] = sA[(mt * NT + qt) * 64 + lane];
+    };
     auto phase_d = [&]() {
 #pragma unroll
-        for (int qt = 0; qt < NT; ++qt) {
-            floatx4 aa[NT];
-#pragma unroll
-            for (int mt = qt; mt < NT; ++mt) aa[mt] = sA[(mt * NT + qt) * 64 + lane];
+        for (int qt = 0; qt < NT; ++qt)
 #pragma unroll
             for (int st = 0; st < 4; ++st)
 #pragma unroll
-                for (int mt = qt; mt < NT; ++mt) X2[mt] = mfma16(aa[mt][st], X1[qt][st], X2[mt]);
-        }
+                for (int mt = qt; mt < NT; ++mt) X2[mt] = mfma16(aq[mt][qt][st], X1[qt][st], X2[mt]);
     };
     for (int n = n0; n < n1; ++n) {
         const size_t cid = cid0 + n;
@@ -729,25 +732,48 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         // A: X1 = W S, X2 = scale (q exp(G)) S
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) X1[mt] = X2[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < NKT; ++kb) {
-            floatx4 wa[NT], ma[NT];
+        floatx4 wa[2][NT], ma[2][NT];
+        auto load_a = [&](int kb, int bf) {
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) {
-                wa[mt] = sW[(mt * NKT + kb) * 64 + lane];
-                if (OUT) ma[mt] = QLDS ? sQ[(mt * NKT + kb) * 64 + lane] : Q4[cid * OPF4 + (mt * NKT + kb) * 64 + lane];
+                wa[bf][mt] = sW[(mt * NKT + kb) * 64 + lane];
+                if (OUT) ma[bf][mt] = QLDS ? sQ[(mt * NKT + kb) * 64 + lane] : Q4[cid * OPF4 + (mt * NKT + kb) * 64 + lane];
             }
-            // eight (pass 1: four) independent accumulator chains per k-step
+        };
+        load_a(0, 0);
 #pragma unroll
-            for (int st = 0; st < 4; ++st)
+        for (int kb = 0; kb < NKT; ++kb) {
+            const int cb = kb & 1;
+            // eight (pass 1: four) independent accumulator chains per k-step;
+            // the next step's operands are requested after the first quarter
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
 #pragma unroll
                 for (int mt = 0; mt < NT; ++mt) {
-                    X1[mt] = mfma16(wa[mt][st], S[kb][st], X1[mt]);
-                    if (OUT) X2[mt] = mfma16(ma[mt][st], S[kb][st], X2[mt]);
+                    X1[mt] = mfma16(wa[cb][mt][st], S[kb][st], X1[mt]);
+                    if (OUT) X2[mt] = mfma16(ma[cb][mt][st], S[kb][st], X2[mt]);
                 }
+                if (st == 0) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (kb + 1 < NKT) load_a(kb + 1, cb ^ 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
         vm_wait<2>();  // this wave's copies of chunk n's Kd, A_qk, exp(G_last) and its U have landed (not the 2 touches)
         lds_barrier(); // A done everywhere (sW, sQ free); sKd(n), sA(n) visible
+        // exp(G_last) and phase C's first Kd^T tile, requested before the
+        // copies below so that their latency is spent on the copies' issue
+        floatx4 gk[NKT], ka[2][NKT];
+        auto load_c = [&](int tt, int bf) {
+#pragma unroll
+            for (int kb = 0; kb < NKT; ++kb) ka[bf][kb] = sKd[(kb * NT + tt) * 64 + lane];
+        };
+#pragma unroll
+        for (int kb = 0; kb < NKT; ++kb) gk[kb] = sGam[4 * kb + lg]; // rows 16 kb + 4 lg .. + 3
+        load_c(0, 0);
+        __builtin_amdgcn_sched_barrier(0);
 
         // B: v_new = U - X1 (kept in X1)
 #pragma unroll
@@ -785,26 +811,29 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         // C: S = exp(G_last) S + Kd^T v_new
 #pragma unroll
         for (int kb = 0; kb < NKT; ++kb) {
-            const floatx4 gk = sGam[4 * kb + lg]; // exp(G_last) of rows 16 kb + 4 lg .. + 3
-            S[kb][0] *= gk[0];
-            S[kb][1] *= gk[1];
-            S[kb][2] *= gk[2];
-            S[kb][3] *= gk[3];
+            S[kb][0] *= gk[kb][0];
+            S[kb][1] *= gk[kb][1];
+            S[kb][2] *= gk[kb][2];
+            S[kb][3] *= gk[kb][3];
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt) {
-            floatx4 ka[NKT];
+            const int cb = tt & 1;
+            // NKT independent accumulator chains per k-step; the next time
+            // tile's operands are requested after the first quarter
 #pragma unroll
-            for (int kb = 0; kb < NKT; ++kb) ka[kb] = sKd[(kb * NT + tt) * 64 + lane];
-            // NKT independent accumulator chains per k-step
+            for (int st = 0; st < 4; ++st) {
 #pragma unroll
-            for (int kb = 0; kb < NKT; ++kb) S[kb] = mfma16(ka[kb][0], X1[tt][0], S[kb]);
-#pragma unroll
-            for (int kb = 0; kb < NKT; ++kb) S[kb] = mfma16(ka[kb][1], X1[tt][1], S[kb]);
-#pragma unroll
-            for (int kb = 0; kb < NKT; ++kb) S[kb] = mfma16(ka[kb][2], X1[tt][2], S[kb]);
-#pragma unroll
-            for (int kb = 0; kb < NKT; ++kb) S[kb] = mfma16(ka[kb][3], X1[tt][3], S[kb]);
+                for (int kb = 0; kb < NKT; ++kb) S[kb] = mfma16(ka[cb][kb][st], X1[tt][st], S[kb]);
+                if (st == 0) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (tt + 1 < NT) load_c(tt + 1, cb ^ 1);
+                    else if (OUT) load_aq(); // for D(n), at the top of iteration n + 1
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     vm_wait0(); // the last touches have landed in sPf
