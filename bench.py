@@ -57,7 +57,13 @@ def parse():
     ap.add_argument("--cpu-layer-tokens", type=int, default=4096,
                     help="tokens of the one-sequence sample of the full-layer CPU baseline")
     ap.add_argument("--no-layer", action="store_true")
+    ap.add_argument("--settle-ms", type=float, default=150.0,
+                    help="untimed back-to-back calls of each timed workload before its warm-ups (the card's clock "
+                         "reaches its sustained value after 20-40 ms of continuous load)")
     ap.add_argument("--layer-steps", type=int, default=5)
+    ap.add_argument("--warmup-timeline", type=int, metavar="STEPS", default=0,
+                    help="only: STEPS back-to-back prefill core steps from an idle card, three times with a 1 s "
+                         "host pause between, printed as means over blocks of 20 steps (the clock's warm-up)")
     ap.add_argument("--decode-prefill", type=int, default=2048)
     ap.add_argument("--no-backward", action="store_true", help="skip the chunked backward timing")
     ap.add_argument("--train-only", action="store_true",
@@ -105,6 +111,89 @@ def load_traffic(name):
         return json.load(fh)
 
 
+_MARK = {}
+
+
+def mark(torch, settled):
+    """A one-workgroup launch of the library's streaming copy that the trace
+    summaries use to find the timed dispatches: 4 floats (stream_copy_kernel)
+    before a settle loop, 3 floats (tail_copy_kernel alone) after it."""
+    import ctypes
+
+    from gdn2_amd import _capi as CA
+    from gdn2_amd.ops import _stream
+
+    if "buf" not in _MARK:
+        _MARK["buf"] = torch.zeros(8, device="cuda")
+    buf = _MARK["buf"]
+    n = 3 if settled else 4
+    CA.check(CA.lib().gdn2_stream_copy_f32(ctypes.c_void_p(buf[4:].data_ptr()), ctypes.c_void_p(buf.data_ptr()), n, 1,
+                                           _stream()))
+
+
+def settle(torch, fn, ms):
+    """Calls fn back to back, untimed, for `ms` of wall time, between two
+    marker launches.  After an idle period (setup, host work) the card runs
+    the first 20-40 ms of continuous load at a lower clock than it sustains
+    afterwards (chunk-inter measured at 1.55-1.85 GHz there, 2.05-2.3 GHz
+    after); the warm-up and timed steps that follow see the sustained clock.
+    Returns the number of calls."""
+    mark(torch, False)
+    n = 0
+    t_end = time.perf_counter() + ms / 1e3
+    while ms > 0:
+        fn()
+        n += 1
+        if n % 4 == 0:
+            torch.cuda.synchronize()
+            if time.perf_counter() >= t_end:
+                break
+    torch.cuda.synchronize()
+    mark(torch, True)
+    return n
+
+
+def warmup_timeline(torch, G, args, dev):
+    """The prefill core (B = 8, T = 4096 operands from the layer's project())
+    timed step by step from an idle card: what the settle loops skip."""
+    import ctypes
+
+    from gdn2_amd import _capi as CA
+    from gdn2_amd.ops import _stream, chunk_args
+
+    cfg = G.Gdn2Config(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0, mode="chunk", chunk_size=64)
+    layer = G.GatedDeltaNet2(cfg, seed=1337)
+    B, T, H, K, V = args.batch, args.seq, cfg.num_heads, cfg.head_dim, cfg.v_head
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(42)
+    P = layer.project(torch.randn((B, T, cfg.hidden_size), generator=gen, device=dev, dtype=torch.float32))
+    state = torch.zeros((B, H, K, V), device=dev)
+    out = torch.empty((B, T, H, V), device=dev).permute(0, 2, 1, 3)
+    ops = [P[n] for n in ("q", "k", "v", "g", "b", "w")]
+    ws = torch.empty(G.chunk_workspace_bytes(*ops, state, out, K ** -0.5, 64), dtype=torch.uint8, device=dev)
+    cargs = chunk_args(*ops, state, out, K ** -0.5, 64, ws)
+    L, stream, pa = CA.lib(), _stream(), ctypes.byref(cargs)
+    n, res = max(20, args.warmup_timeline), []
+    for phase in range(3):
+        time.sleep(1.0)
+        torch.cuda.synchronize()
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n)]
+        for e in ev:
+            e[0].record()
+            CA.check(L.gdn2_chunk_intra_f32(pa, stream))
+            e[1].record()
+            CA.check(L.gdn2_chunk_inter_f32(pa, stream))
+            e[2].record()
+        torch.cuda.synchronize()
+        ti = [e[0].elapsed_time(e[1]) * 1e3 for e in ev]
+        te = [e[1].elapsed_time(e[2]) * 1e3 for e in ev]
+        for lo in range(0, n - n % 20, 20):
+            res.append({"after_idle_s": 1.0, "pass": phase, "steps": [lo, lo + 19],
+                        "intra_us": sum(ti[lo:lo + 20]) / 20, "inter_us": sum(te[lo:lo + 20]) / 20})
+    layer.close()
+    return res
+
+
 def bench_prefill(torch, G, args, dev):
     """The recurrence core on the layer's own operands: q, k, g, b
     [B, H, T, K] and v, w [B, HV, T, V] from GatedDeltaNet2.project, prepared
@@ -138,6 +227,7 @@ def bench_prefill(torch, G, args, dev):
         CA.check(L.gdn2_chunk_intra_f32(pa, stream))
         CA.check(L.gdn2_chunk_inter_f32(pa, stream))
 
+    settle(torch, step, args.settle_ms)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -178,7 +268,7 @@ def bench_prefill(torch, G, args, dev):
     del q, k, v, g, b, w, ws, P, out, state
     lay = None
     if not args.no_layer:
-        lay = time_layer(torch, lambda: layer.forward_train(x), args.layer_steps, tokens)
+        lay = time_layer(torch, lambda: layer.forward_train(x), args.layer_steps, tokens, args.settle_ms)
         lay["gemm_tflop"] = sum(layer_gemm_tflop(cfg, tokens))
         lay.update(time_train_steps(torch, G, layer, x, gen, args, recompute=True))
     layer.close()
@@ -245,6 +335,7 @@ def bench_other_config(torch, G, args, dev, name):
         if evs:
             evs[-1].record()
 
+    settle(torch, step, args.settle_ms)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -279,7 +370,8 @@ def bench_other_config(torch, G, args, dev, name):
     del P, q, k, g, b, v, w, ws, out, state
     torch.cuda.empty_cache()
     if not args.no_layer:
-        lay = time_layer(torch, lambda: layer.forward_train(x), max(1, min(args.layer_steps, 3)), tokens)
+        lay = time_layer(torch, lambda: layer.forward_train(x), max(1, min(args.layer_steps, 3)), tokens,
+                         args.settle_ms)
         lay["gemm_tflop"] = sum(layer_gemm_tflop(cfg, tokens))
         res["layer"] = lay
     del x
@@ -419,21 +511,26 @@ def mfma_summary(path, n_se=32, n_xcc=8):
 
 def configs_summary(path, warmup, steps):
     """Per (kernel, grid size): the mean duration of the timed core dispatches
-    of each configuration in a kernel trace of --configs-only (the warm-up
-    launches skipped; the layer's own launches of the same shape come after
-    the timed ones and are not counted)."""
+    of each configuration in a kernel trace of --configs-only: the first
+    section after a settle loop in which that configuration's chunk-intra
+    launch shape appears (the layer's own launches of the same shape come in
+    later sections and are not counted), warm-up launches skipped."""
     import csv
 
     rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
-    groups = {}
-    cur = None  # the configuration, known by the shape of its chunk-intra launch
-    for r in rows:
-        key = (_short(r["Kernel_Name"]), int(r.get("Grid_Size", r.get("Grid_Size_X", 0)) or 0))
-        if not key[0].startswith(("chunk_intra", "chunk_inter", "chunk_chain")):
-            continue
-        if key[0].startswith("chunk_intra"):
-            cur = key
-        groups.setdefault((cur,) + key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    groups, owner = {}, {}
+    for si, sec in enumerate(_timed_sections(rows)):
+        cur = None  # the configuration, known by the shape of its chunk-intra launch
+        for r in sec:
+            key = (_short(r["Kernel_Name"]), int(r.get("Grid_Size", r.get("Grid_Size_X", 0)) or 0))
+            if not key[0].startswith(("chunk_intra", "chunk_inter", "chunk_chain")):
+                continue
+            if key[0].startswith("chunk_intra"):
+                cur = key
+            g = (cur,) + key
+            if owner.setdefault(g, si) != si:
+                continue
+            groups.setdefault(g, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     print("| configuration (its chunk-intra launch) | kernel | grid (work-items) | timed dispatches | mean us | "
           "min us | max us |")
     print("|---|---|---|---|---|---|---|")
@@ -469,7 +566,7 @@ def time_train_steps(torch, G, layer, x, gen, args, recompute):
         layer.backward(x, d_out, grads=grads, saved=acts)
 
     res = {}
-    tr = time_layer(torch, train_step, args.layer_steps, tokens)
+    tr = time_layer(torch, train_step, args.layer_steps, tokens, args.settle_ms)
     tr["gemm_tflop"] = 3 * (g_in + g_gate + g_out)
     tr["activations"] = "saved by forward_train"
     res["train_step"] = tr
@@ -479,7 +576,7 @@ def time_train_steps(torch, G, layer, x, gen, args, recompute):
             layer.forward_train(x)
             layer.backward(x, d_out, grads=grads)
 
-        rc = time_layer(torch, train_step_recompute, args.layer_steps, tokens)
+        rc = time_layer(torch, train_step_recompute, args.layer_steps, tokens, args.settle_ms)
         rc["gemm_tflop"] = 4 * (g_in + g_gate) + 3 * g_out
         rc["activations"] = "recomputed by the backward"
         res["train_step_recompute"] = rc
@@ -487,8 +584,9 @@ def time_train_steps(torch, G, layer, x, gen, args, recompute):
     return res
 
 
-def time_layer(torch, fn, steps, tokens):
+def time_layer(torch, fn, steps, tokens, settle_ms):
     """Whole-layer forward calls (Linear GEMMs + kernels) timed with events."""
+    settle(torch, fn, settle_ms)
     fn()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -537,6 +635,13 @@ def bench_decode(torch, G, args, dev):
                           scale=K ** -0.5, norm_eps=cfg.norm_eps) for t in range(steps)]
     L, stream = CA.lib(), _stream()
     fn = L.gdn2_decode_fused_f32
+    it = [0]
+
+    def one_step():  # cycles through the prepared tokens and rotating buffers
+        CA.check(fn(ctypes.byref(blocks[it[0] % steps]), stream))
+        it[0] += 1
+
+    settle(torch, one_step, args.settle_ms)
     for t in range(min(8, steps)):
         CA.check(fn(ctypes.byref(blocks[t]), stream))
     torch.cuda.synchronize()
@@ -574,6 +679,14 @@ def bench_decode(torch, G, args, dev):
         torch.cuda.synchronize()
         pre_ms = e0.elapsed_time(e1)
         del xp
+        sd = [st, 0]
+
+        def one_token():  # the state keeps evolving; its values do not change the timing
+            sd[0] = layer.forward(xs[sd[1] % steps], sd[0])[1]
+            sd[1] += 1
+
+        settle(torch, one_token, args.settle_ms)
+        st = sd[0]
         for t in range(min(4, steps)):  # warm-up, then restart from the prefill state is not needed for timing
             _, st = layer.forward(xs[t], st)
         torch.cuda.synchronize()
@@ -749,23 +862,48 @@ def stats_summary(path):
               f"{pct:.1f} |")
 
 
+def _timed_sections(rows):
+    """Splits launch-ordered trace rows at the settle markers (see mark()):
+    a section starts at a tail_copy_kernel launch (end of a settle loop) and
+    ends at the next stream_copy_kernel or tail_copy_kernel launch; the rows
+    of each section are the warm-up and timed dispatches of one workload.
+    Returns a list of row lists."""
+    sections, cur = [], None
+    for r in rows:
+        name = _short(r["Kernel_Name"])
+        if name in ("stream_copy_kernel", "tail_copy_kernel"):
+            if cur is not None:
+                sections.append(cur)
+            cur = [] if name == "tail_copy_kernel" else None
+        elif cur is not None:
+            cur.append(r)
+    if cur is not None:
+        sections.append(cur)
+    return sections
+
+
 def timed_summary(path, warmup, steps, decode_steps):
-    """The timed dispatches of the prefill core (the first warmup + steps
-    launches of each kernel, warm-ups skipped) and of the decode kernel (eight
-    warm-up launches, then decode_steps), as the bench line's kernel times
-    see them."""
+    """The timed dispatches of the prefill core (in the first section after a
+    settle loop that launches each kernel: warmup launches skipped, then
+    steps) and of the decode kernel (eight warm-up launches, then
+    decode_steps), as the bench line's kernel times see them."""
     import csv
 
     rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    sections = _timed_sections(rows)
     print("| kernel | timed dispatches | mean us | min us | max us |")
     print("|---|---|---|---|---|")
     for label, key, skip, take in (("chunk_intra", "chunk_intra_kernel<128, 128, false>", warmup, steps),
                                    ("chunk_inter", "chunk_inter_kernel<128, 0>", warmup, steps),
                                    ("decode", "decode_fused_kernel<128, 128>", 8, decode_steps)):
-        d = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows
-             if _short(r["Kernel_Name"]) == key][skip:skip + take]
-        if d:
-            print(f"| `{key}` ({label}) | {len(d)} | {sum(d) / len(d):.1f} | {min(d):.1f} | {max(d):.1f} |")
+        for sec in sections:
+            d = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in sec
+                 if _short(r["Kernel_Name"]) == key]
+            if d:
+                d = d[skip:skip + take]
+                if d:
+                    print(f"| `{key}` ({label}) | {len(d)} | {sum(d) / len(d):.1f} | {min(d):.1f} | {max(d):.1f} |")
+                break
 
 
 def train_summary(path):
@@ -919,6 +1057,7 @@ def bench_backward(torch, G, args, dev):
     ws = torch.empty(need, dtype=torch.uint8, device=dev)
     a.workspace, a.workspace_bytes = _p(ws), need
     stream = _stream()
+    settle(torch, lambda: CA.check(L.gdn2_chunk_bwd_f32(ctypes.byref(a), stream)), args.settle_ms)
     for _ in range(args.warmup):
         CA.check(L.gdn2_chunk_bwd_f32(ctypes.byref(a), stream))
     torch.cuda.synchronize()
@@ -985,6 +1124,10 @@ def main():
         res["workload"] = f"GDN-2 layer training step, B={args.batch} T={args.seq} D=2048 H=16 K=V=128, f32"
         print(json.dumps(res), flush=True)
         return
+    if args.warmup_timeline:
+        for r in warmup_timeline(torch, G, args, dev):
+            print(json.dumps(r), flush=True)
+        return
     if args.configs_only:
         res = {n: bench_other_config(torch, G, args, dev, n) for n in OTHER_CONFIGS}
         res["hbm_copy_roof"] = bench_copy_roof(torch, dev)
@@ -1009,6 +1152,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": args.settle_ms,
         "ms_per_step": pre["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",

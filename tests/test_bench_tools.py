@@ -29,11 +29,15 @@ def test_timed_summary_skips_warmups_and_takes_steps(tmp_path, capsys):
     intra = f"void {NS}chunk_intra_kernel<128, 128, false>(gdn2::ChunkParams)"
     inter = f"void {NS}chunk_inter_kernel<128, 0>(gdn2::ChunkParams, int)"
     dec = f"void {NS}decode_fused_kernel<128, 128>(gdn2::DecodeParams)"
-    rows = []
+    pre = "void (anonymous namespace)::stream_copy_kernel(HIP_vector_type<float, 4u>*, long)"
+    post = "void (anonymous namespace)::tail_copy_kernel(float*, float const*, long)"
+    rows = [(pre, 1.0)] + [(intra, 700.0), (inter, 700.0)] * 4 + [(post, 1.0)]  # settle loop, then its marker
     for i in range(2 + 3):  # 2 warm-ups (long), then 3 timed steps
         rows += [(intra, 900.0 if i < 2 else 500.0), (inter, 900.0 if i < 2 else 600.0)]
+    rows += [(pre, 1.0)] + [(intra, 1.0), (inter, 1.0)] * 2 + [(post, 1.0)]  # the layer's settle loop
+    rows += [(intra, 2.0), (inter, 2.0)] * 6  # the layer's own calls: another section, not counted
+    rows += [(pre, 1.0)] + [(dec, 77.0)] * 5 + [(post, 1.0)]  # decode settle loop
     rows += [(dec, 99.0)] * 8 + [(dec, 28.0)] * 4 + [(dec, 99.0)]  # 8 warm-ups, 4 timed, 1 check
-    rows += [(intra, 1.0), (inter, 1.0)]  # later calls (the layer's) do not count
     p = tmp_path / "kt.csv"
     _trace(p, rows)
     bench.timed_summary(str(p), warmup=2, steps=3, decode_steps=4)
@@ -82,3 +86,30 @@ def test_median(xs, med):
     import bench
 
     assert bench._median(xs) == med
+
+
+def test_configs_summary_counts_the_first_settled_section_of_each_shape(tmp_path, capsys):
+    import bench
+
+    intra = f"void {NS}chunk_intra_kernel<128, 128, false>(gdn2::ChunkParams)"
+    inter = f"void {NS}chunk_inter_kernel<128, 0>(gdn2::ChunkParams, int)"
+    pre = "void (anonymous namespace)::stream_copy_kernel(HIP_vector_type<float, 4u>*, long)"
+    post = "void (anonymous namespace)::tail_copy_kernel(float*, float const*, long)"
+    g = 512 * 64  # 64 chunks
+    rows = [(pre, 1.0, 256)] + [(intra, 70.0, g), (inter, 70.0, 256)] * 3 + [(post, 1.0, 256)]
+    rows += [(intra, 90.0, g), (inter, 90.0, 256)]  # one warm-up
+    rows += [(intra, 15.0, g), (inter, 55.0, 256)] * 2  # two timed steps
+    rows += [(pre, 1.0, 256), (post, 1.0, 256)] + [(intra, 5.0, g), (inter, 5.0, 256)] * 3  # the layer's calls
+    p = tmp_path / "kt.csv"
+    t = 1_000_000
+    with open(p, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=["Kernel_Name", "Start_Timestamp", "End_Timestamp", "Grid_Size_X"])
+        w.writeheader()
+        for name, dur, grid in rows:
+            w.writerow({"Kernel_Name": name, "Start_Timestamp": t, "End_Timestamp": t + int(dur * 1000),
+                        "Grid_Size_X": grid})
+            t += int(dur * 1000) + 500
+    bench.configs_summary(str(p), warmup=1, steps=2)
+    out = capsys.readouterr().out
+    assert "| `chunk_intra_kernel<128, 128, false>` x 64 | `chunk_intra_kernel<128, 128, false>` | 32768 | 2 | 15.0 |" in out
+    assert "| `chunk_inter_kernel<128, 0>` | 256 | 2 | 55.0 |" in out
