@@ -269,14 +269,70 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
         // is already in this wave's registers: component c % 4 of
         // araw[pi][c / 16 - m0] in lane 16 ((c % 16) / 4) + r.  It is gathered
         // across lanes (ds_bpermute) rather than read again from memory, which
-        // costs one round trip per masked channel.  The training variant, whose
-        // registers are fuller, reads it from memory (keeping araw live here
-        // would spill 72 bytes per lane).
+        // costs one round trip per masked channel.  The channels are visited in
+        // register order (block m, component j, then the four lane groups cg
+        // holding channel 16 (m0 + m) + 4 cg + j), so that the register is
+        // known at compile time; the terms are summed in dacc and added to the
+        // diagonal block's accumulator once.  The training variant, whose
+        // registers are fuller, reads the row operand from memory (keeping araw
+        // live here would spill 72 bytes per lane).
+        if constexpr (!TRAIN) {
+#pragma unroll
+            for (int pi = 0; pi < 2; ++pi) {
+                const int pt = pi ? (NT - 1 - half) : half;
+                constexpr int NWD = K / 64; // mask words of one channel half
+                uint32_t mwh[NWD];
+                uint32_t anyw = 0u;
+#pragma unroll
+                for (int x = 0; x < NWD; ++x) {
+                    mwh[x] = __builtin_amdgcn_readfirstlane(sMask[pt][kh * NWD + x]);
+                    anyw |= mwh[x];
+                }
+                if (anyw == 0u) continue; // wave-uniform
+                floatx4 dacc = floatx4{0.f, 0.f, 0.f, 0.f};
+                const int srow = 16 * pt + lr;
+#pragma unroll
+                for (int m = 0; m < NKH; ++m) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        // bits of channels 16 m + 4 cg + j (cg = 0..3) within the half
+                        const uint32_t w = mwh[(16 * m) >> 5] >> ((16 * m) & 31);
+                        uint32_t cgs = ((w >> j) & 1u) | (((w >> (4 + j)) & 1u) << 1) | (((w >> (8 + j)) & 1u) << 2) |
+                                       (((w >> (12 + j)) & 1u) << 3);
+                        if (cgs == 0u) continue;
+                        // through a scalar: __builtin_bit_cast of a vector element lvalue
+                        // reads the vector's first element
+                        const float ownf = araw[pi][m][j];
+                        const int owni = __builtin_bit_cast(int, ownf);
+                        while (cgs) {
+                            const int cg = __builtin_ctz(cgs);
+                            cgs &= cgs - 1u;
+                            const int c = 16 * (m0 + m) + 4 * cg + j;
+                            const float ks = sK[srow][c];
+                            const float gs = sG[srow][c];
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const int r = 4 * lg + i;
+                                const int rrow = 16 * pt + r;
+                                const float xg =
+                                    __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (16 * cg + r), owni));
+                                const float xr = (mat == 0) ? xg : xg * sK[rrow][c];
+                                const float e = (mat == 0 ? (r >= lr) : (r > lr)) ? fast_exp2(sG[rrow][c] - gs) : 0.f;
+                                dacc[i] += xr * ks * e;
+                            }
+                        }
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < NT; ++q)
+                    if (q == pt) acc[pi][q] += dacc;
+            }
+        }
 #pragma unroll
         for (int pi = 0; pi < 2; ++pi) {
             const int pt = pi ? (NT - 1 - half) : half;
 #pragma unroll
-            for (int q = 0; q < NT; ++q) {
+            for (int q = 0; q < NT && TRAIN; ++q) {
                 if (q == pt && (pi == 1 || q < NT / 2)) {
                     for (int wd = kh * (K / 64); wd < (kh + 1) * (K / 64); ++wd) {
                         uint32_t mw = sMask[pt][wd];
