@@ -270,10 +270,12 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
         // araw[pi][c / 16 - m0] in lane 16 ((c % 16) / 4) + r.  It is gathered
         // across lanes (ds_bpermute) rather than read again from memory, which
         // costs one round trip per masked channel.  The channels are visited in
-        // register order (block m, component j, then the four lane groups cg
-        // holding channel 16 (m0 + m) + 4 cg + j), so that the register is
-        // known at compile time; the terms are summed in dacc and added to the
-        // diagonal block's accumulator once.  The training variant, whose
+        // register order (block m, then the four lane groups cg, each holding
+        // channels 16 (m0 + m) + 4 cg + j in component j), so that the registers
+        // are known at compile time; the terms are summed in dacc and added to
+        // the diagonal block's accumulator once.  (A vector element goes
+        // through a scalar before __builtin_bit_cast: the cast of a vector
+        // element lvalue reads the vector's first element.)  The training variant, whose
         // registers are fuller, reads the row operand from memory (keeping araw
         // live here would spill 72 bytes per lane).
         if constexpr (!TRAIN) {
@@ -291,34 +293,45 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
                 if (anyw == 0u) continue; // wave-uniform
                 floatx4 dacc = floatx4{0.f, 0.f, 0.f, 0.f};
                 const int srow = 16 * pt + lr;
+                // the row conditions of the lower triangle: r >= s (A_qk), r > s (A_kk)
+                bool rowok[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) rowok[i] = mat == 0 ? (4 * lg + i >= lr) : (4 * lg + i > lr);
+                // two channels c0, c0 + 1 (c0 = 16 (m0 + m) + 4 cg + 2 jh) per step: their
+                // G and k come in 8-byte LDS reads, their row operands are
+                // components 2 jh, 2 jh + 1 of araw[pi][m] in lane group cg
 #pragma unroll
                 for (int m = 0; m < NKH; ++m) {
+                    const uint32_t w16 = (mwh[(16 * m) >> 5] >> ((16 * m) & 31)) & 0xffffu;
+                    if (w16 == 0u) continue; // wave-uniform
+                    for (int cg = 0; cg < 4; ++cg) {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        // bits of channels 16 m + 4 cg + j (cg = 0..3) within the half
-                        const uint32_t w = mwh[(16 * m) >> 5] >> ((16 * m) & 31);
-                        uint32_t cgs = ((w >> j) & 1u) | (((w >> (4 + j)) & 1u) << 1) | (((w >> (8 + j)) & 1u) << 2) |
-                                       (((w >> (12 + j)) & 1u) << 3);
-                        if (cgs == 0u) continue;
-                        // through a scalar: __builtin_bit_cast of a vector element lvalue
-                        // reads the vector's first element
-                        const float ownf = araw[pi][m][j];
-                        const int owni = __builtin_bit_cast(int, ownf);
-                        while (cgs) {
-                            const int cg = __builtin_ctz(cgs);
-                            cgs &= cgs - 1u;
-                            const int c = 16 * (m0 + m) + 4 * cg + j;
-                            const float ks = sK[srow][c];
-                            const float gs = sG[srow][c];
+                        for (int jh = 0; jh < 2; ++jh) { // channel pairs c0 + 2 jh + {0, 1}
+                            const uint32_t bits = (w16 >> (4 * cg + 2 * jh)) & 0x3u;
+                            if (bits == 0u) continue; // wave-uniform
+                            const int c0 = 16 * (m0 + m) + 4 * cg + 2 * jh;
+                            const float2 gs = *reinterpret_cast<const float2 *>(&sG[srow][c0]);
+                            const float2 ks = *reinterpret_cast<const float2 *>(&sK[srow][c0]);
+                            const float o0 = araw[pi][m][2 * jh], o1 = araw[pi][m][2 * jh + 1]; // scalars (see above)
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
                                 const int r = 4 * lg + i;
                                 const int rrow = 16 * pt + r;
-                                const float xg =
-                                    __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (16 * cg + r), owni));
-                                const float xr = (mat == 0) ? xg : xg * sK[rrow][c];
-                                const float e = (mat == 0 ? (r >= lr) : (r > lr)) ? fast_exp2(sG[rrow][c] - gs) : 0.f;
-                                dacc[i] += xr * ks * e;
+                                const float2 gr = *reinterpret_cast<const float2 *>(&sG[rrow][c0]);
+                                float x0 = __builtin_bit_cast(
+                                    float, __builtin_amdgcn_ds_bpermute(4 * (16 * cg + r), __builtin_bit_cast(int, o0)));
+                                float x1 = __builtin_bit_cast(
+                                    float, __builtin_amdgcn_ds_bpermute(4 * (16 * cg + r), __builtin_bit_cast(int, o1)));
+                                if (mat == 1) {
+                                    const float2 kr = *reinterpret_cast<const float2 *>(&sK[rrow][c0]);
+                                    x0 *= kr.x;
+                                    x1 *= kr.y;
+                                }
+                                // branch-free: exp2(-inf) = 0 outside the triangle and for the
+                                // channels whose terms the MFMA product already holds
+                                const float d0 = (rowok[i] && (bits & 1u)) ? gr.x - gs.x : -__builtin_inff();
+                                const float d1 = (rowok[i] && (bits & 2u)) ? gr.y - gs.y : -__builtin_inff();
+                                dacc[i] += x0 * ks.x * fast_exp2(d0) + x1 * ks.y * fast_exp2(d1);
                             }
                         }
                     }
