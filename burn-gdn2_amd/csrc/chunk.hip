@@ -957,24 +957,46 @@ __global__ __launch_bounds__(256, 1) void chunk_chain_kernel(ChunkParams p) {
             S[kb][i] = S0[o];
             slot0[o] = S[kb][i];
         }
-    for (int j = 0; j + 1 < p.NSEG; ++j) {
-        const float *P = p.ws_pseg + ((size_t)bh * p.NSEG + j) * K * K;
-        float *Q = slot0 + (size_t)(j + 1) * K * V;
-        floatx4 N[NKT];
+    // Every operand is requested one step ahead of its products: the next
+    // k-block of P_j (two register buffers), the first k-block of P_{j+1} during
+    // the last one of P_j, and Q_{j+1} during the products of step j, so that
+    // a step waits on no memory round trip but its own first one.
+    const int nsteps = p.NSEG - 1;
+    auto P_of = [&](int j) { return p.ws_pseg + ((size_t)bh * p.NSEG + j) * K * K; };
+    auto load_pa = [&](floatx4 *pa, const float *P, int kb) {
+#pragma unroll
+        for (int it = 0; it < NKT; ++it)
+            pa[it] = *reinterpret_cast<const floatx4 *>(P + (size_t)(16 * it + lr) * K + 16 * kb + 4 * lg);
+    };
+    auto load_q = [&](floatx4 *q, int j) { // slot j + 1 holds Q_j from pass 1
+        const float *Q = slot0 + (size_t)(j + 1) * K * V;
 #pragma unroll
         for (int it = 0; it < NKT; ++it)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) N[it][i] = Q[(size_t)(16 * it + 4 * lg + i) * V + col];
+            for (int i = 0; i < 4; ++i) q[it][i] = Q[(size_t)(16 * it + 4 * lg + i) * V + col];
+    };
+    floatx4 pa[2][NKT], Nq[NKT];
+    if (nsteps > 0) {
+        load_q(Nq, 0);
+        load_pa(pa[0], P_of(0), 0);
+    }
+    for (int j = 0; j < nsteps; ++j) {
+        float *Q = slot0 + (size_t)(j + 1) * K * V;
+        floatx4 N[NKT];
+#pragma unroll
+        for (int it = 0; it < NKT; ++it) N[it] = Nq[it];
 #pragma unroll
         for (int kb = 0; kb < NKT; ++kb) {
-            floatx4 pa[NKT];
-#pragma unroll
-            for (int it = 0; it < NKT; ++it)
-                pa[it] = *reinterpret_cast<const floatx4 *>(P + (size_t)(16 * it + lr) * K + 16 * kb + 4 * lg);
+            const int cb = kb & 1;
+            if (kb + 1 < NKT)
+                load_pa(pa[cb ^ 1], P_of(j), kb + 1);
+            else if (j + 1 < nsteps)
+                load_pa(pa[cb ^ 1], P_of(j + 1), 0);
+            if (kb == 0 && j + 1 < nsteps) load_q(Nq, j + 1);
 #pragma unroll
             for (int st = 0; st < 4; ++st)
 #pragma unroll
-                for (int it = 0; it < NKT; ++it) N[it] = mfma16(pa[it][st], S[kb][st], N[it]);
+                for (int it = 0; it < NKT; ++it) N[it] = mfma16(pa[cb][it][st], S[kb][st], N[it]);
         }
 #pragma unroll
         for (int it = 0; it < NKT; ++it) {
