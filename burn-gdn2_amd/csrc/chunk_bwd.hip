@@ -20,8 +20,7 @@
 //   chunk_intra_kernel<K, V, true>       the forward operands plus W^T, QG^T, Kd, A_qk^T, (I + A_kk)^-1
 //   chunk_inter_kernel<K, kInterStates>  the state entering every chunk and v_new
 //   bwd_inter_kernel   the reverse recurrence (one workgroup per (b, hv, 64 columns))
-//   bwd_gemm_kernel    dQG, dW, dKd, dA_qk, dv_new U^T (MFMA) and dgam, per chunk
-//   bwd_solve_kernel   dRk, dRv -> dv, dw; dA_kk, per chunk
+//   bwd_vprod_kernel   dQG, dKd, dA_qk, dgam, then dRk, dRv -> dv, dw and dA_kk, per chunk
 //   bwd_decay_kernel   dq, dk, db, dg, per chunk
 //   bwd_gva_kernel     key-side gradients summed over the value heads of a key head
 #include "chunk_common.hpp"
@@ -43,9 +42,8 @@ struct BwdParams {
     float *ws_dsn;                    // K*V  dL/d(state leaving the chunk), row-major
     float *ws_dvn;                    // C*V  dL/dv_new, row-major
     float *ws_dvnf;                   // C*V  dL/dv_new, fragments
-    float *ws_dqg, *ws_dwm, *ws_dkd;  // C*K  dL/dQG, dL/dW, dL/dKd, fragments
+    float *ws_dqg, *ws_dkd;           // C*K  dL/dQG, dL/dKd, fragments
     float *ws_daqk;                   // C*C  dL/dA_qk (lower), row-major
-    float *ws_duu;                    // C*C  dv_new U^T (strictly lower), fragments
     float *ws_dgam;                   // K    dL/d e^{G_last}
     float *ws_drk;                    // C*K  dL/dRk, fragments
     float *ws_dakk;                   // C*C  dL/dA_kk (strictly lower), row-major
@@ -344,29 +342,62 @@ __global__ __launch_bounds__(256, 1) void bwd_chain_kernel(BwdParams bp) {
 }
 
 // ---------------------------------------------------------------------------
-// Per-chunk products over the value dimension (MFMA, four waves):
+// Per-chunk products over the value dimension, then the solve adjoint (MFMA,
+// four waves, one workgroup per chunk):
 //   dQG = dO S^T, dW = -dv_new S^T, dKd = v_new dS'^T       (C x K)
 //   dA_qk = tril(dO v_new^T), dUU = strict_tril(dv_new U^T)  (C x C)
-// and dgam = rowsum(dS' * S).  Wave w owns the 16 rows of time tile w of
-// every product: its A fragments (rows of dO, dv_new, v_new) come straight
-// from memory, and its accumulators stay in registers over the V loop.  The
-// B operands (16 columns of S, dS', v_new and U per step) are read once per
-// workgroup into a double-buffered LDS slice; the slice loads of step vb+1
-// are issued before step vb's products.
+//   dgam = rowsum(dS' * S)
+// and, with Ai = (I + A_kk)^-1 from the training forward (accumulator-layout
+// tiles, i.e. the A fragments of Ai^T):
+//   [dRk | dRv] = Ai^T [dW | dv_new]   (dv = dRv * w, dw = dRv * v)
+//   dA_kk = strict_tril(-(dRk W^T + Ai^T dUU))
+// Value loop: wave w owns the 16 rows of time tile w of every product; its A
+// fragments (rows of dO, dv_new, v_new) come straight from memory, and its
+// accumulators stay in registers over the V loop.  The B operands (16 columns
+// of S, dS', v_new and U per step) are read once per workgroup into a
+// double-buffered LDS slice; the slice loads of step vb+1 are issued before
+// step vb's products.
+// dW and dUU never leave the compute unit: after the loop they take the
+// staging buffers' place in LDS (dW row-major, dUU as fragments).  Wave w then
+// owns column tiles w, w + 4, ... of [dRk | dRv]: it reads a dW column tile
+// whole before writing dRk over it, as rows for dA_kk's A fragments.  Last,
+// wave w computes dA_kk tiles w, w + 4, ... (W's stored A fragments are the B
+// fragments of W^T).
 // ---------------------------------------------------------------------------
 template <int K, int V>
-__global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(BwdParams bp) {
+struct VprodSmem {
+    static constexpr int SP = 20;     // padded row of a 16-column slice
+    static constexpr int KP = K + 4;  // padded row of dW / dRk
+    // value loop: S, dS' slices [2][K][SP], v_new slice [2][C][SP], U fragments [2][NT * 64]
+    static constexpr size_t oS = 0, oD = oS + 4 * 2 * K * SP, oV = oD + 4 * 2 * K * SP, oU = oV + 4 * 2 * C * SP;
+    static constexpr size_t stage = oU + 16 * 2 * NT * 64;
+    // solve: dW, then dRk [C][KP]; dUU fragments [NT * NT * 64]
+    static constexpr size_t oR = 0, oUU = oR + 4 * C * KP;
+    static constexpr size_t solve = oUU + 16 * NT * NT * 64;
+    static constexpr size_t bytes = stage > solve ? stage : solve;
+    static_assert(oU % 16 == 0 && oUU % 16 == 0, "float4 alignment");
+};
+
+template <int K, int V>
+__global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
     const ChunkParams &p = bp.f;
-    constexpr int NKT = K / 16, NVB = V / 16;
-    constexpr int SP = 20;                            // padded row of a 16-column slice
+    using SM = VprodSmem<K, V>;
+    constexpr int NKT = K / 16, NVB = V / 16, NVT = V / 16, NCT = NKT + NVT;
+    constexpr int SP = SM::SP, KP = SM::KP;
     constexpr int SF4 = K * 4 / 256, VF4 = C * 4 / 256; // float4 per thread: S (and dS') slice, v_new slice
-    __shared__ __attribute__((aligned(16))) float sS[2][K][SP], sD[2][K][SP], sV[2][C][SP];
-    __shared__ __attribute__((aligned(16))) floatx4 sU[2][NT * 64]; // U's fragments of this column block
+    constexpr int NLT = NT * (NT + 1) / 2;              // lower tiles
+    __shared__ __attribute__((aligned(16))) char smem[SM::bytes];
+    float(*sS)[K][SP] = reinterpret_cast<float(*)[K][SP]>(smem + SM::oS);
+    float(*sD)[K][SP] = reinterpret_cast<float(*)[K][SP]>(smem + SM::oD);
+    float(*sV)[C][SP] = reinterpret_cast<float(*)[C][SP]>(smem + SM::oV);
+    floatx4(*sU)[NT * 64] = reinterpret_cast<floatx4(*)[NT * 64]>(smem + SM::oU);
+    float(*sR)[KP] = reinterpret_cast<float(*)[KP]>(smem + SM::oR);
+    floatx4 *sUU = reinterpret_cast<floatx4 *>(smem + SM::oUU);
     const int cid = blockIdx.x, bh = cid / p.NC, n = cid % p.NC;
     const int bi = bh / p.HV, hv = bh % p.HV;
     const int cv = min(C, p.T - n * C);
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // = the time tile
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // = the time tile of the value loop
     const int lr = lane & 15, lg = lane >> 4;
 
     const float *dO = bp.d_out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + (int64_t)(n * C) * p.sot;
@@ -456,28 +487,22 @@ __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(BwdParams bp) {
             __syncthreads();
         }
     }
+    // dQG, dKd (fragments), dA_qk (row-major) and dgam go to the decay kernel
     floatx4 *oQ = reinterpret_cast<floatx4 *>(bp.ws_dqg) + (size_t)cid * (C * K / 4);
-    floatx4 *oW = reinterpret_cast<floatx4 *>(bp.ws_dwm) + (size_t)cid * (C * K / 4);
     floatx4 *oK = reinterpret_cast<floatx4 *>(bp.ws_dkd) + (size_t)cid * (C * K / 4);
-    floatx4 *oU = reinterpret_cast<floatx4 *>(bp.ws_duu) + (size_t)cid * (C * C / 4);
     float *oA = bp.ws_daqk + (size_t)cid * C * C;
 #pragma unroll
     for (int t = 0; t < NKT; ++t) {
         oQ[(wave * NKT + t) * 64 + lane] = aQ[t];
-        oW[(wave * NKT + t) * 64 + lane] = -aW[t];
         oK[(wave * NKT + t) * 64 + lane] = aK[t];
     }
 #pragma unroll
-    for (int st = 0; st < NT; ++st) {
-        floatx4 u = aU[st];
+    for (int st = 0; st < NT; ++st)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 16 * wave + 4 * lg + i, sc = 16 * st + lr;
             oA[r * C + sc] = sc <= r ? aA[st][i] : 0.f;
-            u[i] = sc < r ? u[i] : 0.f;
         }
-        oU[(wave * NT + st) * 64 + lane] = u;
-    }
     // dgam: the four threads that staged a row's 16-column pieces are lanes 4m .. 4m + 3
 #pragma unroll
     for (int i = 0; i < SF4; ++i) {
@@ -486,32 +511,23 @@ __global__ __launch_bounds__(256, 2) void bwd_gemm_kernel(BwdParams bp) {
         g += __shfl_xor(g, 2, 64);
         if ((tid & 3) == 0) bp.ws_dgam[(size_t)cid * K + ((i * 256 + tid) >> 2)] = g;
     }
-}
+    __syncthreads(); // every wave is done with the last slice: the staging buffers are free
+    // dW = -(dv_new S^T) rows of time tile `wave` (lane (lg, lr): rows 4 lg + i of column lr)
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sR[16 * wave + 4 * lg + i][16 * t + lr] = -aW[t][i];
+    // dUU tiles (wave, st), zero on and above the diagonal
+#pragma unroll
+    for (int st = 0; st < NT; ++st) {
+        floatx4 u = aU[st];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) u[i] = 16 * st + lr < 16 * wave + 4 * lg + i ? u[i] : 0.f;
+        sUU[(wave * NT + st) * 64 + lane] = u;
+    }
+    __syncthreads();
 
-// ---------------------------------------------------------------------------
-// Per-chunk solve adjoint (four waves), with Ai = (I + A_kk)^-1 from the
-// training forward (accumulator-layout tiles, i.e. the A fragments of Ai^T):
-//   [dRk | dRv] = Ai^T [dW | dv_new]   (MFMA; dv = dRv * w, dw = dRv * v)
-//   dA_kk = strict_tril(-(dRk W^T + Ai^T dUU))   (MFMA)
-// W's stored A fragments are the B fragments of W^T; dRk goes through LDS
-// (rows as A fragments) for the second product.
-// ---------------------------------------------------------------------------
-template <int K, int V>
-__global__ __launch_bounds__(256) void bwd_solve_kernel(BwdParams bp) {
-    const ChunkParams &p = bp.f;
-    constexpr int NW = 4;
-    constexpr int NKT = K / 16, NVT = V / 16, NCT = NKT + NVT;
-    constexpr int NLT = NT * (NT + 1) / 2; // lower tiles
-    constexpr int KP = K + 4;
-    __shared__ __attribute__((aligned(16))) float sR[C][KP]; // dRk
-    const int cid = blockIdx.x, bh = cid / p.NC, n = cid % p.NC;
-    const int bi = bh / p.HV, hv = bh % p.HV;
-    const int cv = min(C, p.T - n * C);
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lr = lane & 15, lg = lane >> 4;
-
-    // Ai^T A fragments (rt, st), st >= rt: Ai's tile (st, rt)
+    // [dRk | dRv] = Ai^T [dW | dv_new].  Ai^T A fragments (rt, st), st >= rt: Ai's tile (st, rt)
     const floatx4 *Aif = reinterpret_cast<const floatx4 *>(p.ws_akk) + (size_t)cid * (C * C / 4);
     floatx4 ai[NLT];
 #pragma unroll
@@ -521,22 +537,24 @@ __global__ __launch_bounds__(256) void bwd_solve_kernel(BwdParams bp) {
     auto aiT = [&](int rt, int st) -> floatx4 { // index of (rt, st) in the list above
         return ai[rt * NT - rt * (rt - 1) / 2 + (st - rt)];
     };
-
-    const floatx4 *dWf = reinterpret_cast<const floatx4 *>(bp.ws_dwm) + (size_t)cid * (C * K / 4);
     const floatx4 *dVf = reinterpret_cast<const floatx4 *>(bp.ws_dvnf) + (size_t)cid * (C * V / 4);
     floatx4 *drk = reinterpret_cast<floatx4 *>(bp.ws_drk) + (size_t)cid * (C * K / 4);
     const int64_t vo = (int64_t)bi * p.svb + (int64_t)hv * p.svh + (int64_t)(n * C) * p.svt;
     const int rv = (int)p.svt;
     const __amdgpu_buffer_rsrc_t Rv = rows_rsrc(p.v + vo, rv, cv, V), Rw = rows_rsrc(p.w + vo, rv, cv, V);
 #pragma unroll 1
-    for (int ct = wave; ct < NCT; ct += NW) {
+    for (int ct = wave; ct < NCT; ct += 4) {
         const bool kcol = ct < NKT;
         floatx4 xb[NT]; // B fragments X[16 st + 4 g + j][column lr]
-#pragma unroll
-        for (int st = 0; st < NT; ++st)
-            xb[st] = kcol ? dWf[(st * NKT + ct) * 64 + lane] : dVf[(st * NVT + ct - NKT) * 64 + lane];
         float vv[NT][4], ww[NT][4];
-        if (!kcol) {
+        if (kcol) {
+#pragma unroll
+            for (int st = 0; st < NT; ++st)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xb[st][j] = sR[16 * st + 4 * lg + j][16 * ct + lr];
+        } else {
+#pragma unroll
+            for (int st = 0; st < NT; ++st) xb[st] = dVf[(st * NVT + ct - NKT) * 64 + lane];
 #pragma unroll
             for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
@@ -552,6 +570,7 @@ __global__ __launch_bounds__(256) void bwd_solve_kernel(BwdParams bp) {
 #pragma unroll
             for (int st = rt; st < NT; ++st) acc = mfma4x(aiT(rt, st), xb[st], acc);
             if (kcol) {
+                // this lane read these four elements of dW above (rows 16 st + 4 lg + j, column lr)
                 drk[(rt * NKT + ct) * 64 + lane] = acc;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) sR[16 * rt + 4 * lg + i][16 * ct + lr] = acc[i];
@@ -568,14 +587,13 @@ __global__ __launch_bounds__(256) void bwd_solve_kernel(BwdParams bp) {
             }
         }
     }
-    __syncthreads();
+    __syncthreads(); // sR holds dRk
 
     // dA_kk tiles (rt, st): -(dRk W^T + Ai^T dUU) on the lower tiles, zero above
     const floatx4 *Wf = reinterpret_cast<const floatx4 *>(p.ws_w) + (size_t)cid * (C * K / 4);
-    const floatx4 *duu = reinterpret_cast<const floatx4 *>(bp.ws_duu) + (size_t)cid * (C * C / 4);
     float *dakk = bp.ws_dakk + (size_t)cid * C * C;
 #pragma unroll 1
-    for (int tl = wave; tl < NT * NT; tl += NW) {
+    for (int tl = wave; tl < NT * NT; tl += 4) {
         const int rt = tl / NT, st = tl % NT;
         floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
         if (st <= rt) {
@@ -584,7 +602,7 @@ __global__ __launch_bounds__(256) void bwd_solve_kernel(BwdParams bp) {
             for (int kt = 0; kt < NKT; ++kt) wb[kt] = Wf[(st * NKT + kt) * 64 + lane];
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) {
-                ub[mt] = mt >= rt ? duu[(mt * NT + st) * 64 + lane] : floatx4{0.f, 0.f, 0.f, 0.f};
+                ub[mt] = mt >= rt ? sUU[(mt * NT + st) * 64 + lane] : floatx4{0.f, 0.f, 0.f, 0.f};
                 ab[mt] = mt >= rt ? Aif[(mt * NT + rt) * 64 + lane] : floatx4{0.f, 0.f, 0.f, 0.f}; // Ai^T (rt, mt)
             }
 #pragma unroll
@@ -863,9 +881,7 @@ hipError_t launch_bwd_t(const BwdParams &bp, hipStream_t s) {
     hipLaunchKernelGGL((bwd_inter_kernel<K, kRevOut>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0, s, bp, 0,
                        p.NSEG);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_gemm_kernel<K, V>), dim3(nch), dim3(256), 0, s, bp);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL((bwd_solve_kernel<K, V>), dim3(nch), dim3(256), 0, s, bp);
+    hipLaunchKernelGGL((bwd_vprod_kernel<K, V>), dim3(nch), dim3(256), 0, s, bp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_decay_kernel<K, V>), dim3(nch), dim3(K * 4), 0, s, bp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -894,7 +910,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // The backward's workspace after the forward's: the training operands of the
 // forward, then the backward's per-chunk arrays.
 struct BwdLayout {
-    size_t fwd, wt, qgt, kd, aqkt, akk, sn, vn, dsn, dvn, dvnf, dqg, rseg, dwm, dkd, daqk, duu, dgam, drk, dakk, kgrad, total;
+    size_t fwd, wt, qgt, kd, aqkt, akk, sn, vn, dsn, dvn, dvnf, dqg, rseg, dkd, daqk, dgam, drk, dakk, kgrad, total;
 };
 
 BwdLayout bwd_layout(const gdn2_chunk_args *a) {
@@ -915,10 +931,8 @@ BwdLayout bwd_layout(const gdn2_chunk_args *a) {
     L.dvn = take(Cs * V);
     L.dvnf = take(Cs * V);
     L.dqg = take(Cs * K);
-    L.dwm = take(Cs * K);
     L.dkd = take(Cs * K);
     L.daqk = take(Cs * Cs);
-    L.duu = take(Cs * Cs);
     L.dgam = take(K);
     L.drk = take(Cs * K);
     L.dakk = take(Cs * Cs);
@@ -988,10 +1002,8 @@ extern "C" gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *a, gdn2_str
     bp.ws_dvn = reinterpret_cast<float *>(ws + L.dvn);
     bp.ws_dvnf = reinterpret_cast<float *>(ws + L.dvnf);
     bp.ws_dqg = reinterpret_cast<float *>(ws + L.dqg);
-    bp.ws_dwm = reinterpret_cast<float *>(ws + L.dwm);
     bp.ws_dkd = reinterpret_cast<float *>(ws + L.dkd);
     bp.ws_daqk = reinterpret_cast<float *>(ws + L.daqk);
-    bp.ws_duu = reinterpret_cast<float *>(ws + L.duu);
     bp.ws_dgam = reinterpret_cast<float *>(ws + L.dgam);
     bp.ws_drk = reinterpret_cast<float *>(ws + L.drk);
     bp.ws_dakk = reinterpret_cast<float *>(ws + L.dakk);
