@@ -41,7 +41,6 @@ struct BwdParams {
     // 4 g .. 4 g + 3 of column c), so that every access is one 16-byte load.
     float *ws_dsn;                    // K*V  dL/d(state leaving the chunk), row-major
     float *ws_dvn;                    // C*V  dL/dv_new, row-major
-    float *ws_dvnf;                   // C*V  dL/dv_new, fragments
     float *ws_dqg, *ws_dkd;           // C*K  dL/dQG, dL/dKd, fragments
     float *ws_daqk;                   // C*C  dL/dA_qk (lower), row-major
     float *ws_dgam;                   // K    dL/d e^{G_last}
@@ -231,10 +230,6 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
             for (int st = 0; st < NT; ++st)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) Dvn[(size_t)(16 * st + 4 * lg + i) * V + col] = dvn[st][i];
-            floatx4 *Dvf = reinterpret_cast<floatx4 *>(bp.ws_dvnf) + cid * (C * V / 4);
-            const int vt = vs * 4 + wave, nvt = V / 16;
-#pragma unroll
-            for (int st = 0; st < NT; ++st) Dvf[(st * nvt + vt) * 64 + lane] = dvn[st];
         }
         __builtin_amdgcn_sched_barrier(0);
         touch_qw(clamp_c(n - 1));
@@ -360,7 +355,8 @@ __global__ __launch_bounds__(256, 1) void bwd_chain_kernel(BwdParams bp) {
 // dW and dUU never leave the compute unit: after the loop they take the
 // staging buffers' place in LDS (dW row-major, dUU as fragments).  Wave w then
 // owns column tiles w, w + 4, ... of [dRk | dRv]: it reads a dW column tile
-// whole before writing dRk over it, as rows for dA_kk's A fragments.  Last,
+// whole before writing dRk over it, as rows for dA_kk's A fragments, and
+// gathers dv_new's column tiles from its rows in memory.  Last,
 // wave w computes dA_kk tiles w, w + 4, ... (W's stored A fragments are the B
 // fragments of W^T).
 // ---------------------------------------------------------------------------
@@ -537,7 +533,6 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
     auto aiT = [&](int rt, int st) -> floatx4 { // index of (rt, st) in the list above
         return ai[rt * NT - rt * (rt - 1) / 2 + (st - rt)];
     };
-    const floatx4 *dVf = reinterpret_cast<const floatx4 *>(bp.ws_dvnf) + (size_t)cid * (C * V / 4);
     floatx4 *drk = reinterpret_cast<floatx4 *>(bp.ws_drk) + (size_t)cid * (C * K / 4);
     const int64_t vo = (int64_t)bi * p.svb + (int64_t)hv * p.svh + (int64_t)(n * C) * p.svt;
     const int rv = (int)p.svt;
@@ -554,7 +549,9 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
                 for (int j = 0; j < 4; ++j) xb[st][j] = sR[16 * st + 4 * lg + j][16 * ct + lr];
         } else {
 #pragma unroll
-            for (int st = 0; st < NT; ++st) xb[st] = dVf[(st * NVT + ct - NKT) * 64 + lane];
+            for (int st = 0; st < NT; ++st) // from dv_new's rows (the value loop's A operand)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xb[st][j] = dvn[(16 * st + 4 * lg + j) * V + 16 * (ct - NKT) + lr];
 #pragma unroll
             for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
@@ -910,7 +907,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 // The backward's workspace after the forward's: the training operands of the
 // forward, then the backward's per-chunk arrays.
 struct BwdLayout {
-    size_t fwd, wt, qgt, kd, aqkt, akk, sn, vn, dsn, dvn, dvnf, dqg, rseg, dkd, daqk, dgam, drk, dakk, kgrad, total;
+    size_t fwd, wt, qgt, kd, aqkt, akk, sn, vn, dsn, dvn, dqg, rseg, dkd, daqk, dgam, drk, dakk, kgrad, total;
 };
 
 BwdLayout bwd_layout(const gdn2_chunk_args *a) {
@@ -929,7 +926,6 @@ BwdLayout bwd_layout(const gdn2_chunk_args *a) {
     L.vn = take(Cs * V);
     L.dsn = take(K * V);
     L.dvn = take(Cs * V);
-    L.dvnf = take(Cs * V);
     L.dqg = take(Cs * K);
     L.dkd = take(Cs * K);
     L.daqk = take(Cs * Cs);
@@ -1000,7 +996,6 @@ extern "C" gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *a, gdn2_str
     bp.d_state0 = a->d_state0;
     bp.ws_dsn = reinterpret_cast<float *>(ws + L.dsn);
     bp.ws_dvn = reinterpret_cast<float *>(ws + L.dvn);
-    bp.ws_dvnf = reinterpret_cast<float *>(ws + L.dvnf);
     bp.ws_dqg = reinterpret_cast<float *>(ws + L.dqg);
     bp.ws_dkd = reinterpret_cast<float *>(ws + L.dkd);
     bp.ws_daqk = reinterpret_cast<float *>(ws + L.daqk);
