@@ -35,12 +35,15 @@ struct BwdParams {
     float *dq, *dk, *dg, *db;         // strided like q (f.sqb, f.sqh, f.sqt)
     float *dv, *dw;                   // strided like v (f.svb, f.svh, f.svt)
     float *d_state0;                  // [B, HV, K, V]
-    // per chunk (chunk id = (b * HV + hv) * NC + n).  "Row-major" or
-    // "fragments": 16 x 16 tiles (row tile, column tile) in row-major tile order,
-    // each 64 lanes x float4 in accumulator layout (lane (g, c) holds rows
-    // 4 g .. 4 g + 3 of column c), so that every access is one 16-byte load.
-    float *ws_dsn;                    // K*V  dL/d(state leaving the chunk), row-major
-    float *ws_dvn;                    // C*V  dL/dv_new, row-major
+    // per chunk (chunk id = (b * HV + hv) * NC + n).  "Row-major",
+    // "slice-major" (an R x V matrix as V / 16 row-major R x 16 blocks: element
+    // (r, c) at ((c / 16) R + r) 16 + c % 16, so that a 16-column slice is one
+    // contiguous block) or "fragments": 16 x 16 tiles (row tile, column tile)
+    // in row-major tile order, each 64 lanes x float4 in accumulator layout
+    // (lane (g, c) holds rows 4 g .. 4 g + 3 of column c), so that every access
+    // is one 16-byte load.
+    float *ws_dsn;                    // K*V  dL/d(state leaving the chunk), slice-major
+    float *ws_dvn;                    // C*V  dL/dv_new, slice-major
     float *ws_dqg, *ws_dkd;           // C*K  dL/dQG, dL/dKd, fragments
     float *ws_daqk;                   // C*C  dL/dA_qk (lower), row-major
     float *ws_dgam;                   // K    dL/d e^{G_last}
@@ -186,7 +189,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
 #pragma unroll
             for (int kb = 0; kb < NKT; ++kb)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) Dsn[(size_t)(16 * kb + 4 * lg + i) * V + col] = dS[kb][i];
+                for (int i = 0; i < 4; ++i) Dsn[((size_t)(col >> 4) * K + 16 * kb + 4 * lg + i) * 16 + lr] = dS[kb][i];
         }
         // e^{G_last} for this lane's rows 16 kb + 4 lg .. + 3 of dS'
         floatx4 gam[NKT];
@@ -229,7 +232,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
 #pragma unroll
             for (int st = 0; st < NT; ++st)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) Dvn[(size_t)(16 * st + 4 * lg + i) * V + col] = dvn[st][i];
+                for (int i = 0; i < 4; ++i) Dvn[((size_t)(col >> 4) * C + 16 * st + 4 * lg + i) * 16 + lr] = dvn[st][i];
         }
         __builtin_amdgcn_sched_barrier(0);
         touch_qw(clamp_c(n - 1));
@@ -399,8 +402,12 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
     const float *dO = bp.d_out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + (int64_t)(n * C) * p.sot;
     const int ro = (int)p.sot;
     const __amdgpu_buffer_rsrc_t RdO = rows_rsrc(dO, ro, cv, V);
-    const float *Sn = p.ws_sn + (size_t)cid * K * V, *dSn = bp.ws_dsn + (size_t)cid * K * V;
-    const float *vn = p.ws_vn + (size_t)cid * C * V, *dvn = bp.ws_dvn + (size_t)cid * C * V;
+    // S, dS', v_new and dv_new of the chunk, slice-major: slice vb is one contiguous block
+    const floatx4 *Sn = reinterpret_cast<const floatx4 *>(p.ws_sn + (size_t)cid * K * V);
+    const floatx4 *dSn = reinterpret_cast<const floatx4 *>(bp.ws_dsn + (size_t)cid * K * V);
+    const floatx4 *vn = reinterpret_cast<const floatx4 *>(p.ws_vn + (size_t)cid * C * V);
+    const float *dvn = bp.ws_dvn + (size_t)cid * C * V;
+    const floatx4 *dvn4 = reinterpret_cast<const floatx4 *>(dvn);
     const floatx4 *Uf = reinterpret_cast<const floatx4 *>(p.ws_u + (size_t)cid * C * V);
     const int arow = 16 * wave + lr;
 
@@ -416,16 +423,12 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
     floatx4 ls[SF4], ld_[SF4], lv[VF4], lu;
     auto load_slice = [&](int vb) {
 #pragma unroll
-        for (int i = 0; i < SF4; ++i) {
-            const int f = i * 256 + tid, r = f >> 2, c4 = f & 3;
-            ls[i] = *reinterpret_cast<const floatx4 *>(Sn + r * V + 16 * vb + 4 * c4);
-            ld_[i] = *reinterpret_cast<const floatx4 *>(dSn + r * V + 16 * vb + 4 * c4);
+        for (int i = 0; i < SF4; ++i) { // row (i * 256 + tid) / 4, columns 16 vb + 4 (tid % 4) ..
+            ls[i] = Sn[vb * K * 4 + i * 256 + tid];
+            ld_[i] = dSn[vb * K * 4 + i * 256 + tid];
         }
 #pragma unroll
-        for (int i = 0; i < VF4; ++i) {
-            const int f = i * 256 + tid, r = f >> 2, c4 = f & 3;
-            lv[i] = *reinterpret_cast<const floatx4 *>(vn + r * V + 16 * vb + 4 * c4);
-        }
+        for (int i = 0; i < VF4; ++i) lv[i] = vn[vb * C * 4 + i * 256 + tid];
         lu = Uf[vb * NT * 64 + tid]; // tiles (vb, 0 .. NT-1): NT * 64 float4 = 256
     };
     auto store_slice = [&](int buf) {
@@ -455,8 +458,8 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
         if (vb + 1 < NVB) load_slice(vb + 1);
         const int c0 = 16 * vb + 4 * lg;
         const floatx4 fO = bld4(RdO, arow * ro + c0);
-        const floatx4 fD = *reinterpret_cast<const floatx4 *>(dvn + arow * V + c0);
-        const floatx4 fV = *reinterpret_cast<const floatx4 *>(vn + arow * V + c0);
+        const floatx4 fD = dvn4[(vb * C + arow) * 4 + lg];
+        const floatx4 fV = vn[(vb * C + arow) * 4 + lg];
 #pragma unroll
         for (int t = 0; t < NKT; ++t) {
             const floatx4 bS = *reinterpret_cast<const floatx4 *>(&sS[buf][16 * t + lr][4 * lg]);
@@ -551,7 +554,7 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
 #pragma unroll
             for (int st = 0; st < NT; ++st) // from dv_new's rows (the value loop's A operand)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) xb[st][j] = dvn[(16 * st + 4 * lg + j) * V + 16 * (ct - NKT) + lr];
+                for (int j = 0; j < 4; ++j) xb[st][j] = dvn[((ct - NKT) * C + 16 * st + 4 * lg + j) * 16 + lr];
 #pragma unroll
             for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
@@ -692,11 +695,6 @@ __global__ __launch_bounds__(K * 4, K / 32) void bwd_decay_kernel(BwdParams bp) 
         for (int i = 0; i < RPS; ++i) sG[seg * RPS + i][c] = (vals[i] + off) * kLog2e;
         __syncthreads();
     }
-    float gv[NT][4];
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) gv[t][j] = sG[16 * t + 4 * lg + j][ch];
     const float gl = sG[C - 1][ch];
     float gb[NT]; // Gb_t: G at the end of tile t-1
     bool msk[NT]; // diagonal block of tile t beyond the safe span
@@ -725,90 +723,92 @@ __global__ __launch_bounds__(K * 4, K / 32) void bwd_decay_kernel(BwdParams bp) 
     constexpr int NKT = K / 16;
     float kt_sum = 0.f;
 
-    // Tile by tile: the row sums of row tile t (rows 16 t + 4 lg + i, column =
-    // channel), the column sums of column tile t, then tile t's elementwise
-    // terms, whose dG overwrites tile t's rows of G (only this wave reads
-    // this channel's G, and every later use of tile t's G is from registers).
+    // Tiles from the last to the first.  Step t forms the column operands of
+    // row tile t (scale q and b k, decay-weighted, rows 16 t + 4 lg + j) once
+    // and adds their products to the column sums of every column tile <= t;
+    // column tile t then has all its terms (they come from row tiles >= t), so
+    // the step finishes it with the row sums of row tile t and tile t's
+    // elementwise terms.  Those overwrite tile t's rows of G with dG: only this
+    // wave reads this channel's G, every later use of tile t's G is from
+    // registers, and the pairwise terms that read G from LDS (row and column
+    // sums of tile t's diagonal block) come before in the same step.
+    floatx4 ckt[NT]; // column sums of column tiles 0 .. t
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        floatx4 rq, rkb, ck;
+    for (int t = 0; t < NT; ++t) ckt[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = NT - 1; t >= 0; --t) {
+        float gt[4]; // G at this lane's rows of tile t
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gt[j] = sG[16 * t + 4 * lg + j][ch];
+        floatx4 bq, bb; // column operands of row tile t
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float e = fast_exp2(gt[j] - gb[t]);
+            const int o = (16 * t + 4 * lg + j) * rq_ + ch;
+            bq[j] = scale * bld1(Rq, o) * e;
+            bb[j] = bld1(Rb, o) * kv[t][j] * e;
+        }
+        floatx4 rq, rkb;
         {
             floatx4 aq = floatx4{0.f, 0.f, 0.f, 0.f}, ab = aq;
 #pragma unroll
-            for (int qt = 0; qt <= t; ++qt) {
-                floatx4 kt;
+            for (int ct = 0; ct <= t; ++ct) {
+                // e^{Gb_t - G_s} at rows s = 16 ct + 4 lg + j: the weight of k_s in row tile t's
+                // row sums and of row tile t's products in column tile ct's sums
+                floatx4 wd, kt, a1, a2;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float e = fast_exp2(gb[t] - gv[qt][j]);
-                    kt[j] = (qt == t && msk[t]) ? 0.f : kv[qt][j] * e;
+                    wd[j] = (ct == t && msk[t]) ? 0.f : fast_exp2(gb[t] - sG[16 * ct + 4 * lg + j][ch]);
+                    kt[j] = kv[ct][j] * wd[j];
+                    a1[j] = sDA[16 * t + 4 * lg + j][16 * ct + lr];
+                    a2[j] = sDK[16 * t + 4 * lg + j][16 * ct + lr];
                 }
-                aq = mfma4x(*reinterpret_cast<const floatx4 *>(&sDA[16 * t + lr][16 * qt + 4 * lg]), kt, aq);
-                ab = mfma4x(*reinterpret_cast<const floatx4 *>(&sDK[16 * t + lr][16 * qt + 4 * lg]), kt, ab);
+                aq = mfma4x(*reinterpret_cast<const floatx4 *>(&sDA[16 * t + lr][16 * ct + 4 * lg]), kt, aq);
+                ab = mfma4x(*reinterpret_cast<const floatx4 *>(&sDK[16 * t + lr][16 * ct + 4 * lg]), kt, ab);
+                floatx4 tmp = mfma4x(a1, bq, floatx4{0.f, 0.f, 0.f, 0.f});
+                tmp = mfma4x(a2, bb, tmp);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ckt[ct][i] += tmp[i] * wd[i];
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float e = fast_exp2(gv[t][i] - gb[t]);
+                const float e = fast_exp2(gt[i] - gb[t]);
                 rq[i] = aq[i] * e;
                 rkb[i] = ab[i] * e;
             }
-            if (msk[t]) { // exact diagonal-block terms of this channel
+            if (msk[t]) { // exact diagonal-block terms of this channel: row sums, then column sums
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int r = 16 * t + 4 * lg + i;
                     float sq = 0.f, sb = 0.f;
                     for (int s2 = 16 * t; s2 <= r; ++s2) {
-                        const float e = fast_exp2(gv[t][i] - sG[s2][ch]) * bld1(Rk, s2 * rq_ + ch);
+                        const float e = fast_exp2(gt[i] - sG[s2][ch]) * bld1(Rk, s2 * rq_ + ch);
                         sq += sDA[r][s2] * e;
                         sb += sDK[r][s2] * e;
                     }
                     rq[i] += sq;
                     rkb[i] += sb;
                 }
-            }
-        }
-        {
-            floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int pt = t; pt < NT; ++pt) {
-                floatx4 bq, bb, a1, a2;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float e = fast_exp2(gv[pt][j] - gb[pt]);
-                    const int o = (16 * pt + 4 * lg + j) * rq_ + ch;
-                    bq[j] = scale * bld1(Rq, o) * e;
-                    bb[j] = bld1(Rb, o) * kv[pt][j] * e;
-                    a1[j] = sDA[16 * pt + 4 * lg + j][16 * t + lr];
-                    a2[j] = sDK[16 * pt + 4 * lg + j][16 * t + lr];
-                }
-                floatx4 tmp = mfma4x(a1, bq, floatx4{0.f, 0.f, 0.f, 0.f});
-                tmp = mfma4x(a2, bb, tmp);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float e = (pt == t && msk[t]) ? 0.f : fast_exp2(gb[pt] - gv[t][i]);
-                    acc[i] += tmp[i] * e;
-                }
-            }
-            if (msk[t]) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int s2 = 16 * t + 4 * lg + i;
                     float sc = 0.f;
                     for (int r = s2; r < 16 * t + 16; ++r) {
-                        const float e = fast_exp2(sG[r][ch] - gv[t][i]);
+                        const float e = fast_exp2(sG[r][ch] - gt[i]);
                         const int o = r * rq_ + ch;
                         sc += (scale * sDA[r][s2] * bld1(Rq, o) + sDK[r][s2] * bld1(Rb, o) * bld1(Rk, o)) * e;
                     }
-                    acc[i] += sc;
+                    ckt[t][i] += sc;
                 }
             }
-            ck = acc;
         }
+        const floatx4 ck = ckt[t];
         const floatx4 fqg = dqg[(t * NKT + wave) * 64 + lane], fkd = dkd[(t * NKT + wave) * 64 + lane];
         const floatx4 frk = drk[(t * NKT + wave) * 64 + lane];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 16 * t + 4 * lg + i;
-            const float eG = fast_exp2(gv[t][i]), eKd = fast_exp2(gl - gv[t][i]);
+            const float eG = fast_exp2(gt[i]), eKd = fast_exp2(gl - gt[i]);
             const float vqg = fqg[i], vkd = fkd[i], vrk = frk[i];
             const int o = r * rq_ + ch;
             const float qr = bld1(Rq, o), kr = kv[t][i], br = bld1(Rb, o);
@@ -821,8 +821,6 @@ __global__ __launch_bounds__(K * 4, K / 32) void bwd_decay_kernel(BwdParams bp) 
             }
             kt_sum += vkd * kd;
             const float dG = scale * qr * (eG * vqg + rq[i]) + br * kr * dkb - vkd * kd - kr * ck[i];
-            // tile t's G rows are read by this lane's column-pass pairwise terms of
-            // tile t only (done above), so they can be overwritten now
             sG[r][ch] = dG;
         }
     }
