@@ -367,9 +367,9 @@ template <int K, int V>
 struct VprodSmem {
     static constexpr int SP = 20;     // padded row of a 16-column slice
     static constexpr int KP = K + 4;  // padded row of dW / dRk
-    // value loop: S, dS' slices [2][K][SP], v_new slice [2][C][SP], U fragments [2][NT * 64]
+    // value loop: S, dS' slices [2][K][SP], v_new and U slices [2][C][SP]
     static constexpr size_t oS = 0, oD = oS + 4 * 2 * K * SP, oV = oD + 4 * 2 * K * SP, oU = oV + 4 * 2 * C * SP;
-    static constexpr size_t stage = oU + 16 * 2 * NT * 64;
+    static constexpr size_t stage = oU + 4 * 2 * C * SP;
     // solve: dW, then dRk [C][KP]; dUU fragments [NT * NT * 64]
     static constexpr size_t oR = 0, oUU = oR + 4 * C * KP;
     static constexpr size_t solve = oUU + 16 * NT * NT * 64;
@@ -389,7 +389,7 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
     float(*sS)[K][SP] = reinterpret_cast<float(*)[K][SP]>(smem + SM::oS);
     float(*sD)[K][SP] = reinterpret_cast<float(*)[K][SP]>(smem + SM::oD);
     float(*sV)[C][SP] = reinterpret_cast<float(*)[C][SP]>(smem + SM::oV);
-    floatx4(*sU)[NT * 64] = reinterpret_cast<floatx4(*)[NT * 64]>(smem + SM::oU);
+    float(*sU)[C][SP] = reinterpret_cast<float(*)[C][SP]>(smem + SM::oU);
     float(*sR)[KP] = reinterpret_cast<float(*)[KP]>(smem + SM::oR);
     floatx4 *sUU = reinterpret_cast<floatx4 *>(smem + SM::oUU);
     const int cid = blockIdx.x, bh = cid / p.NC, n = cid % p.NC;
@@ -445,7 +445,10 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
             const int f = i * 256 + tid, r = f >> 2, c4 = f & 3;
             *reinterpret_cast<floatx4 *>(&sV[buf][r][4 * c4]) = lv[i];
         }
-        sU[buf][tid] = lu;
+        // U's fragment (vb, tid / 64), lane (g, c) = tid % 64: rows 16 (tid / 64) + 4 g + i, column c
+        const int ur = 16 * (tid >> 6) + 4 * ((tid >> 4) & 3), uc = tid & 15;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sU[buf][ur + i][uc] = lu[i];
     };
     static_assert(NT * 64 == 256, "one U fragment per thread");
 
@@ -472,11 +475,7 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
         for (int st = 0; st < NT; ++st) {
             if (st <= wave) {
                 const floatx4 bV = *reinterpret_cast<const floatx4 *>(&sV[buf][16 * st + lr][4 * lg]);
-                // U[16 st + lr][16 vb + 4 lg + j]: fragment st, lane (lr / 4, 4 lg + j), component lr % 4
-                const float *uf = reinterpret_cast<const float *>(&sU[buf][st * 64]);
-                floatx4 bU;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) bU[j] = uf[((lr >> 2) * 16 + 4 * lg + j) * 4 + (lr & 3)];
+                const floatx4 bU = *reinterpret_cast<const floatx4 *>(&sU[buf][16 * st + lr][4 * lg]);
                 aA[st] = mfma4x(fO, bV, aA[st]);
                 aU[st] = mfma4x(fD, bU, aU[st]);
             }
