@@ -621,8 +621,9 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
 //
 // MODE: kInterOut (pass 3), kInterLocal (pass 1), kInterStates (pass 3 for
 // the backward: no output and no final state; instead the state entering
-// every chunk (ws_sn) and every chunk's v_new (ws_vn), both slice-major: V / 16
-// row-major blocks of 16 columns) or kInterOutStates
+// every chunk (ws_sn) and every chunk's v_new (ws_vn), both as accumulator
+// fragments in (value tile, row tile) order, so that each 16-column slice is
+// one contiguous block) or kInterOutStates
 // (pass 3 with both, the reference's fused_chunk_forward tuple).
 // ---------------------------------------------------------------------------
 constexpr int kInterOut = 0, kInterLocal = 1, kInterStates = 2, kInterOutStates = 3;
@@ -790,14 +791,11 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
             float *Sn = p.ws_sn + slot * K * V;
 #pragma unroll
             for (int kb = 0; kb < NKT; ++kb)
+                if (MODE == kInterStates) // the backward's fragment layout: tile (value tile, key tile)
+                    reinterpret_cast<floatx4 *>(Sn)[(vt * NKT + kb) * 64 + lane] = S[kb];
+                else
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int row = 16 * kb + 4 * lg + i;
-                    if (MODE == kInterStates) // the backward's slice-major layout (16-column blocks)
-                        Sn[((size_t)vt * K + row) * 16 + lr] = S[kb][i];
-                    else
-                        Sn[(size_t)row * V + col] = S[kb][i];
-                }
+                    for (int i = 0; i < 4; ++i) Sn[(size_t)(16 * kb + 4 * lg + i) * V + col] = S[kb][i];
         }
         // keep these loads here, a whole phase ahead of their use and of the
         // vmcnt wait before the next barrier, and the touches last
@@ -866,14 +864,11 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
                 float *Vn = p.ws_vn + cid * C * V;
 #pragma unroll
                 for (int mt = 0; mt < NT; ++mt)
+                    if (MODE == kInterStates) // tile (value tile, time tile)
+                        reinterpret_cast<floatx4 *>(Vn)[(vt * NT + mt) * 64 + lane] = X1[mt];
+                    else
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int row = 16 * mt + 4 * lg + i;
-                        if (MODE == kInterStates)
-                            Vn[((size_t)vt * C + row) * 16 + lr] = X1[mt][i];
-                        else
-                            Vn[(size_t)row * V + col] = X1[mt][i];
-                    }
+                        for (int i = 0; i < 4; ++i) Vn[(size_t)(16 * mt + 4 * lg + i) * V + col] = X1[mt][i];
             }
         }
 

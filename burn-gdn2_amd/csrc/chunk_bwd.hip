@@ -36,14 +36,13 @@ struct BwdParams {
     float *dv, *dw;                   // strided like v (f.svb, f.svh, f.svt)
     float *d_state0;                  // [B, HV, K, V]
     // per chunk (chunk id = (b * HV + hv) * NC + n).  "Row-major",
-    // "slice-major" (an R x V matrix as V / 16 row-major R x 16 blocks: element
-    // (r, c) at ((c / 16) R + r) 16 + c % 16, so that a 16-column slice is one
-    // contiguous block) or "fragments": 16 x 16 tiles (row tile, column tile)
-    // in row-major tile order, each 64 lanes x float4 in accumulator layout
-    // (lane (g, c) holds rows 4 g .. 4 g + 3 of column c), so that every access
-    // is one 16-byte load.
-    float *ws_dsn;                    // K*V  dL/d(state leaving the chunk), slice-major
-    float *ws_dvn;                    // C*V  dL/dv_new, slice-major
+    // "fragments": 16 x 16 tiles (row tile, column tile) in row-major tile
+    // order, each 64 lanes x float4 in accumulator layout (lane (g, c) holds
+    // rows 4 g .. 4 g + 3 of column c), so that every access is one 16-byte
+    // load, or "column fragments": the same tiles in (column tile, row tile)
+    // order, so that each 16-column slice of an R x V matrix is one block.
+    float *ws_dsn;                    // K*V  dL/d(state leaving the chunk), column fragments
+    float *ws_dvn;                    // C*V  dL/dv_new, column fragments
     float *ws_dqg, *ws_dkd;           // C*K  dL/dQG, dL/dKd, fragments
     float *ws_daqk;                   // C*C  dL/dA_qk (lower), row-major
     float *ws_dgam;                   // K    dL/d e^{G_last}
@@ -188,8 +187,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
             float *Dsn = bp.ws_dsn + cid * K * V;
 #pragma unroll
             for (int kb = 0; kb < NKT; ++kb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) Dsn[((size_t)(col >> 4) * K + 16 * kb + 4 * lg + i) * 16 + lr] = dS[kb][i];
+                reinterpret_cast<floatx4 *>(Dsn)[((col >> 4) * NKT + kb) * 64 + lane] = dS[kb];
         }
         // e^{G_last} for this lane's rows 16 kb + 4 lg .. + 3 of dS'
         floatx4 gam[NKT];
@@ -231,8 +229,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
             float *Dvn = bp.ws_dvn + cid * C * V;
 #pragma unroll
             for (int st = 0; st < NT; ++st)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) Dvn[((size_t)(col >> 4) * C + 16 * st + 4 * lg + i) * 16 + lr] = dvn[st][i];
+                reinterpret_cast<floatx4 *>(Dvn)[((col >> 4) * NT + st) * 64 + lane] = dvn[st];
         }
         __builtin_amdgcn_sched_barrier(0);
         touch_qw(clamp_c(n - 1));
@@ -359,7 +356,7 @@ __global__ __launch_bounds__(256, 1) void bwd_chain_kernel(BwdParams bp) {
 // staging buffers' place in LDS (dW row-major, dUU as fragments).  Wave w then
 // owns column tiles w, w + 4, ... of [dRk | dRv]: it reads a dW column tile
 // whole before writing dRk over it, as rows for dA_kk's A fragments, and
-// gathers dv_new's column tiles from its rows in memory.  Last,
+// reads dv_new's column tiles from memory.  Last,
 // wave w computes dA_kk tiles w, w + 4, ... (W's stored A fragments are the B
 // fragments of W^T).
 // ---------------------------------------------------------------------------
@@ -367,9 +364,9 @@ template <int K, int V>
 struct VprodSmem {
     static constexpr int SP = 20;     // padded row of a 16-column slice
     static constexpr int KP = K + 4;  // padded row of dW / dRk
-    // value loop: S, dS' slices [2][K][SP], v_new and U slices [2][C][SP]
-    static constexpr size_t oS = 0, oD = oS + 4 * 2 * K * SP, oV = oD + 4 * 2 * K * SP, oU = oV + 4 * 2 * C * SP;
-    static constexpr size_t stage = oU + 4 * 2 * C * SP;
+    // value loop: S, dS' slices [2][K][SP]; v_new, dv_new and U slices [2][C][SP]
+    static constexpr size_t oS = 0, oD = oS + 4 * 2 * K * SP, oV = oD + 4 * 2 * K * SP, oDV = oV + 4 * 2 * C * SP;
+    static constexpr size_t oU = oDV + 4 * 2 * C * SP, stage = oU + 4 * 2 * C * SP;
     // solve: dW, then dRk [C][KP]; dUU fragments [NT * NT * 64]
     static constexpr size_t oR = 0, oUU = oR + 4 * C * KP;
     static constexpr size_t solve = oUU + 16 * NT * NT * 64;
@@ -389,6 +386,7 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
     float(*sS)[K][SP] = reinterpret_cast<float(*)[K][SP]>(smem + SM::oS);
     float(*sD)[K][SP] = reinterpret_cast<float(*)[K][SP]>(smem + SM::oD);
     float(*sV)[C][SP] = reinterpret_cast<float(*)[C][SP]>(smem + SM::oV);
+    float(*sDV)[C][SP] = reinterpret_cast<float(*)[C][SP]>(smem + SM::oDV);
     float(*sU)[C][SP] = reinterpret_cast<float(*)[C][SP]>(smem + SM::oU);
     float(*sR)[KP] = reinterpret_cast<float(*)[KP]>(smem + SM::oR);
     floatx4 *sUU = reinterpret_cast<floatx4 *>(smem + SM::oUU);
@@ -402,12 +400,13 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
     const float *dO = bp.d_out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + (int64_t)(n * C) * p.sot;
     const int ro = (int)p.sot;
     const __amdgpu_buffer_rsrc_t RdO = rows_rsrc(dO, ro, cv, V);
-    // S, dS', v_new and dv_new of the chunk, slice-major: slice vb is one contiguous block
+    // S, dS', v_new, dv_new and U of the chunk as accumulator fragments in
+    // (value tile, row tile) order: slice vb is one contiguous block, and
+    // thread tid's float4 i of it is lane tid % 64 of row tile 4 i + tid / 64
     const floatx4 *Sn = reinterpret_cast<const floatx4 *>(p.ws_sn + (size_t)cid * K * V);
     const floatx4 *dSn = reinterpret_cast<const floatx4 *>(bp.ws_dsn + (size_t)cid * K * V);
     const floatx4 *vn = reinterpret_cast<const floatx4 *>(p.ws_vn + (size_t)cid * C * V);
-    const float *dvn = bp.ws_dvn + (size_t)cid * C * V;
-    const floatx4 *dvn4 = reinterpret_cast<const floatx4 *>(dvn);
+    const floatx4 *dvn = reinterpret_cast<const floatx4 *>(bp.ws_dvn + (size_t)cid * C * V);
     const floatx4 *Uf = reinterpret_cast<const floatx4 *>(p.ws_u + (size_t)cid * C * V);
     const int arow = 16 * wave + lr;
 
@@ -416,39 +415,50 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
     for (int t = 0; t < NKT; ++t) aQ[t] = aW[t] = aK[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < NT; ++t) aA[t] = aU[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float gam[SF4]; // dS' * S partial sums of the rows this thread stages
+    // this thread's fragment lane: rows 4 g .. 4 g + 3 (of its row tiles) of column c
+    const int g4 = 4 * ((tid >> 4) & 3), fc = tid & 15;
+    floatx4 gam[SF4]; // dS' * S partial sums of those rows, over this thread's columns
 #pragma unroll
-    for (int i = 0; i < SF4; ++i) gam[i] = 0.f;
+    for (int i = 0; i < SF4; ++i) gam[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    floatx4 ls[SF4], ld_[SF4], lv[VF4], lu;
+    floatx4 ls[SF4], ld_[SF4], lv[VF4], ldv[VF4], lu;
     auto load_slice = [&](int vb) {
 #pragma unroll
-        for (int i = 0; i < SF4; ++i) { // row (i * 256 + tid) / 4, columns 16 vb + 4 (tid % 4) ..
+        for (int i = 0; i < SF4; ++i) {
             ls[i] = Sn[vb * K * 4 + i * 256 + tid];
             ld_[i] = dSn[vb * K * 4 + i * 256 + tid];
         }
 #pragma unroll
-        for (int i = 0; i < VF4; ++i) lv[i] = vn[vb * C * 4 + i * 256 + tid];
+        for (int i = 0; i < VF4; ++i) {
+            lv[i] = vn[vb * C * 4 + i * 256 + tid];
+            ldv[i] = dvn[vb * C * 4 + i * 256 + tid];
+        }
         lu = Uf[vb * NT * 64 + tid]; // tiles (vb, 0 .. NT-1): NT * 64 float4 = 256
     };
+    // the fragments go to LDS as row-major slices (row, 16 columns)
     auto store_slice = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < SF4; ++i) {
-            const int f = i * 256 + tid, r = f >> 2, c4 = f & 3;
-            *reinterpret_cast<floatx4 *>(&sS[buf][r][4 * c4]) = ls[i];
-            *reinterpret_cast<floatx4 *>(&sD[buf][r][4 * c4]) = ld_[i];
-            const floatx4 pr = ls[i] * ld_[i];
-            gam[i] += pr[0] + pr[1] + pr[2] + pr[3];
+            const int r0 = 16 * (4 * i + (tid >> 6)) + g4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                sS[buf][r0 + j][fc] = ls[i][j];
+                sD[buf][r0 + j][fc] = ld_[i][j];
+            }
+            gam[i] += ls[i] * ld_[i];
         }
 #pragma unroll
         for (int i = 0; i < VF4; ++i) {
-            const int f = i * 256 + tid, r = f >> 2, c4 = f & 3;
-            *reinterpret_cast<floatx4 *>(&sV[buf][r][4 * c4]) = lv[i];
-        }
-        // U's fragment (vb, tid / 64), lane (g, c) = tid % 64: rows 16 (tid / 64) + 4 g + i, column c
-        const int ur = 16 * (tid >> 6) + 4 * ((tid >> 4) & 3), uc = tid & 15;
+            const int r0 = 16 * (4 * i + (tid >> 6)) + g4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sU[buf][ur + i][uc] = lu[i];
+            for (int j = 0; j < 4; ++j) {
+                sV[buf][r0 + j][fc] = lv[i][j];
+                sDV[buf][r0 + j][fc] = ldv[i][j];
+            }
+        }
+        const int ur = 16 * (tid >> 6) + g4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sU[buf][ur + j][fc] = lu[j];
     };
     static_assert(NT * 64 == 256, "one U fragment per thread");
 
@@ -461,8 +471,8 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
         if (vb + 1 < NVB) load_slice(vb + 1);
         const int c0 = 16 * vb + 4 * lg;
         const floatx4 fO = bld4(RdO, arow * ro + c0);
-        const floatx4 fD = dvn4[(vb * C + arow) * 4 + lg];
-        const floatx4 fV = vn[(vb * C + arow) * 4 + lg];
+        const floatx4 fD = *reinterpret_cast<const floatx4 *>(&sDV[buf][arow][4 * lg]);
+        const floatx4 fV = *reinterpret_cast<const floatx4 *>(&sV[buf][arow][4 * lg]);
 #pragma unroll
         for (int t = 0; t < NKT; ++t) {
             const floatx4 bS = *reinterpret_cast<const floatx4 *>(&sS[buf][16 * t + lr][4 * lg]);
@@ -501,13 +511,17 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
             const int r = 16 * wave + 4 * lg + i, sc = 16 * st + lr;
             oA[r * C + sc] = sc <= r ? aA[st][i] : 0.f;
         }
-    // dgam: the four threads that staged a row's 16-column pieces are lanes 4m .. 4m + 3
+    // dgam: a row's 16 columns of every slice were staged by the 16 lanes 16 g .. 16 g + 15
 #pragma unroll
     for (int i = 0; i < SF4; ++i) {
-        float g = gam[i];
-        g += __shfl_xor(g, 1, 64);
-        g += __shfl_xor(g, 2, 64);
-        if ((tid & 3) == 0) bp.ws_dgam[(size_t)cid * K + ((i * 256 + tid) >> 2)] = g;
+        floatx4 g = gam[i];
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) g[j] += __shfl_xor(g[j], m, 64);
+        if (fc == 0)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bp.ws_dgam[(size_t)cid * K + 16 * (4 * i + (tid >> 6)) + g4 + j] = g[j];
     }
     __syncthreads(); // every wave is done with the last slice: the staging buffers are free
     // dW = -(dv_new S^T) rows of time tile `wave` (lane (lg, lr): rows 4 lg + i of column lr)
@@ -551,9 +565,7 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
                 for (int j = 0; j < 4; ++j) xb[st][j] = sR[16 * st + 4 * lg + j][16 * ct + lr];
         } else {
 #pragma unroll
-            for (int st = 0; st < NT; ++st) // from dv_new's rows (the value loop's A operand)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) xb[st][j] = dvn[((ct - NKT) * C + 16 * st + 4 * lg + j) * 16 + lr];
+            for (int st = 0; st < NT; ++st) xb[st] = dvn[((ct - NKT) * NT + st) * 64 + lane];
 #pragma unroll
             for (int rt = 0; rt < NT; ++rt)
 #pragma unroll

@@ -72,9 +72,10 @@ struct ChunkParams {
     float *ws_kd;   // C*K  Kd as A-operand tiles (time tile, key tile)
     float *ws_aqkt; // C*C  A_qk^T as A-operand tiles (column tile, row tile)
     float *ws_akk;  // C*C  (I + A_kk)^-1, accumulator-layout tiles (row tile, column tile)
-    float *ws_sn;   // K*V  state entering each chunk (row-major; for the backward, V / 16
-                    //      row-major K x 16 blocks, one per 16 value columns)
-    float *ws_vn;   // C*V  v_new of each chunk (row-major; for the backward, V / 16 C x 16 blocks)
+    float *ws_sn;   // K*V  state entering each chunk (row-major; for the backward, 16 x 16
+                    //      accumulator fragments in (value tile, key tile) order)
+    float *ws_vn;   // C*V  v_new of each chunk (row-major; for the backward, fragments in
+                    //      (value tile, time tile) order)
     // Layout of ws_sn / ws_vn for a caller chunk size Cc dividing 64 (0: the
     // 64-token chunk layout above).  st_step = 64 / Cc slots per 64-token
     // chunk, st_chunks = T / Cc slots per (b, hv): the state entering 64-chunk
