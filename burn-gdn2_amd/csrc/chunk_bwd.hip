@@ -194,24 +194,47 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
 #pragma unroll
         for (int kb = 0; kb < NKT; ++kb) gam[kb] = G4[cid * (K / 4) + 4 * kb + lg];
 
-        // 1: dv_new = Kd dS' + A_qk^T dO (A_qk^T is upper block-triangular)
+        // 1: dv_new = Kd dS' + A_qk^T dO (A_qk^T is upper block-triangular).
+        // Each k-step's Kd fragments are requested after the first quarter of
+        // the previous step's products, the A_qk^T tiles during the last step.
         floatx4 dvn[NT];
 #pragma unroll
         for (int st = 0; st < NT; ++st) dvn[st] = floatx4{0.f, 0.f, 0.f, 0.f};
+        {
+            floatx4 ka[2][NT], at[NT][NT]; // at[st][rt], rt >= st
+            auto load_k = [&](int kb, int bf) {
 #pragma unroll
-        for (int kb = 0; kb < NKT; ++kb) {
-            floatx4 ka[NT];
+                for (int st = 0; st < NT; ++st) ka[bf][st] = sKd[(st * NKT + kb) * 64 + lane];
+            };
+            load_k(0, 0);
 #pragma unroll
-            for (int st = 0; st < NT; ++st) ka[st] = sKd[(st * NKT + kb) * 64 + lane];
+            for (int kb = 0; kb < NKT; ++kb) {
+                const int cb = kb & 1;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                    for (int st = 0; st < NT; ++st) dvn[st] = mfma16(ka[cb][st][j], dS[kb][j], dvn[st]);
+                    if (j == 0) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (kb + 1 < NKT)
+                            load_k(kb + 1, cb ^ 1);
+                        else
+#pragma unroll
+                            for (int st = 0; st < NT; ++st)
+#pragma unroll
+                                for (int rt = st; rt < NT; ++rt) at[st][rt] = sAT[(st * NT + rt) * 64 + lane];
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int st = 0; st < NT; ++st) dvn[st] = mfma16(ka[st][j], dS[kb][j], dvn[st]);
+                for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+                    for (int st = 0; st <= rt; ++st) dvn[st] = mfma16(at[st][rt][j], dO[rt][j], dvn[st]);
         }
-#pragma unroll
-        for (int st = 0; st < NT; ++st)
-#pragma unroll
-            for (int rt = st; rt < NT; ++rt) dvn[st] = mfma4x(sAT[(st * NT + rt) * 64 + lane], dO[rt], dvn[st]);
         __builtin_amdgcn_sched_barrier(0);
         touch_ka(clamp_c(n - 2));
         __builtin_amdgcn_sched_barrier(0);
@@ -243,21 +266,36 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
             dS[kb][2] *= gam[kb][2];
             dS[kb][3] *= gam[kb][3];
         }
-#pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
-            floatx4 qa[NKT], wa[NKT];
-#pragma unroll
-            for (int kb = 0; kb < NKT; ++kb) {
-                qa[kb] = sQT[(kb * NT + tt) * 64 + lane];
-                wa[kb] = sWT[(kb * NT + tt) * 64 + lane];
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
+        // each time tile's QG^T and W^T fragments are requested after the first
+        // quarter of the previous tile's products
+        {
+            floatx4 qa[2][NKT], wa[2][NKT];
+            auto load_qw = [&](int tt, int bf) {
 #pragma unroll
                 for (int kb = 0; kb < NKT; ++kb) {
-                    dS[kb] = mfma16(qa[kb][j], dO[tt][j], dS[kb]);
-                    dS[kb] = mfma16(-wa[kb][j], dvn[tt][j], dS[kb]);
+                    qa[bf][kb] = sQT[(kb * NT + tt) * 64 + lane];
+                    wa[bf][kb] = sWT[(kb * NT + tt) * 64 + lane];
                 }
+            };
+            load_qw(0, 0);
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt) {
+                const int cb = tt & 1;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                    for (int kb = 0; kb < NKT; ++kb) {
+                        dS[kb] = mfma16(qa[cb][kb][j], dO[tt][j], dS[kb]);
+                        dS[kb] = mfma16(-wa[cb][kb][j], dvn[tt][j], dS[kb]);
+                    }
+                    if (j == 0) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (tt + 1 < NT) load_qw(tt + 1, cb ^ 1);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
         if (n > n0) {
 #pragma unroll
