@@ -829,6 +829,8 @@ COPY_BYTES = 1 << 30
 # variants, chunk_intra_kernel<..., true> and chunk_inter_kernel<128, 2>, are others)
 KERNELS = {"chunk_intra": "chunk_intra_kernel<128, 128, false>", "chunk_inter": "chunk_inter_kernel<128, 0>",
            "decode": "decode_fused_kernel<128, 128>"}
+BWD_KERNELS = ("chunk_intra_kernel<128, 128, true>", "chunk_inter_kernel<128, 2>", "bwd_inter_kernel<128, 0>",
+               "bwd_vprod_kernel<128, 128>", "bwd_decay_kernel<128, 128>")
 
 
 def _short(name):
@@ -1025,6 +1027,13 @@ def traffic_summary(fetch_csv, write_csv):
         suffix = "b64" if key == "decode" else "b8_t4096"
         with open(os.path.join(ROOT, "profiles", f"{key}_{suffix}_traffic.json"), "w") as fh:
             json.dump(out[key], fh, indent=1)
+    # the chunked backward's kernels (bench.py's backward entry), printed only
+    for frag in BWD_KERNELS:
+        fv = [v for n, vals in fetch.items() if frag in n for v in vals]
+        wv = [v for n, vals in write.items() if frag in n for v in vals]
+        if fv and wv:
+            rd, wr = sum(fv) / len(fv) * f_fac, sum(wv) / len(wv) * w_fac
+            print(f"| `{frag}` | {len(fv)} | {rd / 1e9:.3f} | {wr / 1e9:.3f} | {(rd + wr) / 1e9:.3f} |")
     return out
 
 
