@@ -43,6 +43,8 @@ CASES = [
     (1, 2, 2, 200, 128, 128, (-5.0, -0.5), 1.0, 0.5, True),     # strong decay
     (1, 1, 1, 1, 128, 128, (-0.3, -0.02), 1.0, 1.0, True),      # T = 1
     (1, 1, 2, 63, 64, 128, (-1.0, -0.1), 2.0, 0.3, True),
+    (1, 1, 1, 100, 128, 64, (-0.3, -0.02), 1.0, 0.5, True),     # V = K / 2: four value slices
+    (1, 1, 1, 90, 64, 256, (-0.5, -0.05), 1.0, 0.5, True),      # V = 4 K: sixteen value slices
     (1, 2, 2, 2100, 128, 128, (-0.003, -0.0005), 1.0, 1.0, True),  # slow decay; seven segments of 5 chunks
     (1, 2, 2, 2560, 128, 128, (-0.001, 0.0), 0.0, 1.0, True),       # b = 0: S0 and d_state carried through
     (1, 1, 2, 6400, 64, 128, (-0.002, 0.0), 2.0, 1.0, True),        # 25 segments, GVA, negative eigenvalues
