@@ -267,8 +267,13 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
             dS[kb][3] *= gam[kb][3];
         }
         // each time tile's QG^T and W^T fragments are requested after the first
-        // quarter of the previous tile's products
+        // quarter of the previous tile's products.  -W^T dv_new = W^T (-dv_new):
+        // the MFMA takes no sign on an f32 operand, so the 16 values of -dv_new are
+        // formed once rather than the 128 of -W^T
         {
+            floatx4 ndv[NT];
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt) ndv[tt] = -dvn[tt];
             floatx4 qa[2][NKT], wa[2][NKT];
             auto load_qw = [&](int tt, int bf) {
 #pragma unroll
@@ -286,7 +291,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
 #pragma unroll
                     for (int kb = 0; kb < NKT; ++kb) {
                         dS[kb] = mfma16(qa[cb][kb][j], dO[tt][j], dS[kb]);
-                        dS[kb] = mfma16(-wa[cb][kb][j], dvn[tt][j], dS[kb]);
+                        dS[kb] = mfma16(wa[cb][kb][j], ndv[tt][j], dS[kb]);
                     }
                     if (j == 0) {
                         __builtin_amdgcn_sched_barrier(0);
