@@ -151,15 +151,17 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
 #pragma unroll
         for (int i = 0; i < APF; ++i) lds_copy4(&AT4[c * AF4 + i * 256 + tid], &sAT[i * 256 + wv]);
     };
-    // row 4 lg of each 16-row tile of d_out; the rest of the row offset is wave-uniform
-    const float *dob = bp.d_out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + col + (int64_t)(4 * lg) * p.sot;
+    // chunk n's rows of d_out through a buffer resource over its valid rows
+    // (rows past T read 0); row 4 lg of each 16-row tile, the rest of the row
+    // offset wave-uniform
+    const float *dob = bp.d_out + (int64_t)bi * p.sob + (int64_t)hv * p.soh;
+    const int ro = (int)p.sot, dol = 4 * lg * ro + col;
     auto load_dO = [&](floatx4 *dO, int n) {
-        const int cv = min(C, p.T - n * C);
+        const __amdgpu_buffer_rsrc_t R = rows_rsrc(dob + (int64_t)n * C * p.sot, ro, min(C, p.T - n * C), V);
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                dO[mt][i] = (16 * mt + 4 * lg + i < cv) ? dob[(int64_t)(n * C + 16 * mt + i) * p.sot] : 0.f;
+            for (int i = 0; i < 4; ++i) dO[mt][i] = bld1(R, dol + (16 * mt + i) * ro);
     };
 
     floatx4 dO[NT]; // rows of d_out of the current chunk, loaded a phase ahead
