@@ -288,6 +288,8 @@ OTHER_CONFIGS = {
     "C5": (dict(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0, mode="chunk", chunk_size=128), 1, 65536,
            4.0, 45, "long context: hidden 2048, 16 heads, K = V = 128, chunk_size 128, dt_bias + 4, "
                     "x [1, 65536, 2048]"),
+    "D256": (dict(hidden_size=2048, num_heads=8, head_dim=256, expand_v=1.0, mode="chunk", chunk_size=64), 8, 4096,
+             0.0, 46, "head_dim 256: hidden 2048, 8 heads, K = V = 256, chunk 64, x [8, 4096, 2048]"),
 }
 
 
@@ -599,45 +601,110 @@ def time_layer(torch, fn, steps, tokens, settle_ms):
     return {"ms_per_step": ms, "tokens_per_s": tokens / (ms / 1e3), "steps": steps}
 
 
-def bench_decode(torch, G, args, dev):
-    """Config 3: the default layer (FusedRecurrent, short conv) at B = 64.
-    (a) The fused decode kernel alone over 256 tokens whose raw projections
-    are prepared up front, with rotating state buffers (larger than the
-    256 MB MALL; the kernel's time does not depend on the state values).
-    (b) The whole layer: forward() over a 2048-token prefill, then 256
-    single-token forward() calls carrying the Gdn2State."""
-    cfg = G.Gdn2Config(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0)
-    Bd, H, K, V = args.decode_batch, cfg.num_heads, cfg.head_dim, cfg.v_head
-    kd, vd = cfg.kd, cfg.vd
-    Wn = G.init_params(cfg, seed=1337)
-    W = {n: torch.from_numpy(a).to(dev) for n, a in Wn.items() if a is not None}
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(43)
-    steps = args.decode_steps
-    x = torch.randn((steps, Bd, cfg.hidden_size), generator=gen, device=dev)
-    with torch.no_grad():
-        raw = {"q_raw": x @ W["q_proj"], "k_raw": x @ W["k_proj"], "v_raw": x @ W["v_proj"],
-               "f_raw": (x @ W["f_proj_0"]) @ W["f_proj_1"], "b_raw": x @ W["b_proj"], "w_raw": x @ W["w_proj"],
-               "gate": (x @ W["g_proj_0"]) @ W["g_proj_1"] + W["g_proj_1_bias"]}
-    nrot = max(1, args.decode_rotate)
-    states = [torch.randn((Bd, H, K, V), generator=gen, device=dev) * 0.05 for _ in range(nrot)]
-    conv = [tuple(torch.randn((Bd, 3, n), generator=gen, device=dev) for n in (kd, kd, vd)) for _ in range(2)]
-    out = torch.empty((Bd, vd), device=dev)
-    params = {n: W[n] for n in ("q_conv_w", "k_conv_w", "v_conv_w", "a_log", "dt_bias", "o_norm_weight")}
-
+def time_decode_kernel(torch, G, dev, cfg, Bd, steps, nrot, settle_ms, seed=43):
+    """The fused decode kernel (gdn2_decode_fused_f32) alone for layer config
+    cfg at batch Bd: `steps` tokens whose raw projections are prepared up
+    front, nrot rotating state buffers (the kernel's time does not depend on
+    the state values), timed with events on the launch stream after a settle
+    loop; beside it a streaming copy of the same bytes.  Bytes per step: the
+    state read and written, the raw projections and gate in, the conv caches
+    read and written, the output, the per-channel parameters."""
     import ctypes
 
     from gdn2_amd import _capi as CA
     from gdn2_amd.ops import _stream, decode_args
 
+    H, HV, K, V = cfg.num_heads, cfg.hv, cfg.head_dim, cfg.v_head
+    kd, vd = cfg.kd, cfg.vd
+    Wn = G.init_params(cfg, seed=1337)
+    W = {n: torch.from_numpy(a).to(dev) for n, a in Wn.items() if a is not None}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    x = torch.randn((steps, Bd, cfg.hidden_size), generator=gen, device=dev)
+    with torch.no_grad():
+        raw = {"q_raw": x @ W["q_proj"], "k_raw": x @ W["k_proj"], "v_raw": x @ W["v_proj"],
+               "f_raw": (x @ W["f_proj_0"]) @ W["f_proj_1"], "b_raw": x @ W["b_proj"], "w_raw": x @ W["w_proj"],
+               "gate": (x @ W["g_proj_0"]) @ W["g_proj_1"] + W["g_proj_1_bias"]}
+    states = [torch.randn((Bd, HV, K, V), generator=gen, device=dev) * 0.05 for _ in range(nrot)]
+    conv = [tuple(torch.randn((Bd, 3, n), generator=gen, device=dev) for n in (kd, kd, vd)) for _ in range(2)]
+    out = torch.empty((Bd, vd), device=dev)
+    pnames = ("q_conv_w", "k_conv_w", "v_conv_w", "a_log", "dt_bias", "o_norm_weight") + \
+        (("decay_factors",) if cfg.min_decay is not None else ())
+    params = {n: W[n] for n in pnames}
     blocks = [decode_args({n: a[t] for n, a in raw.items()}, params, states[t % nrot], conv[t % 2],
-                          conv[(t + 1) % 2], out, num_heads=H, num_v_heads=H, head_dim=K, head_v_dim=V,
-                          scale=K ** -0.5, norm_eps=cfg.norm_eps) for t in range(steps)]
+                          conv[(t + 1) % 2], out, num_heads=H, num_v_heads=HV, head_dim=K, head_v_dim=V,
+                          scale=K ** -0.5, min_decay=cfg.min_decay, norm_eps=cfg.norm_eps,
+                          allow_neg_eigval=cfg.allow_neg_eigval) for t in range(steps)]
     L, stream = CA.lib(), _stream()
     fn = L.gdn2_decode_fused_f32
     it = [0]
 
     def one_step():  # cycles through the prepared tokens and rotating buffers
+        CA.check(fn(ctypes.byref(blocks[it[0] % steps]), stream))
+        it[0] += 1
+
+    settle(torch, one_step, settle_ms)
+    for t in range(min(8, steps)):
+        CA.check(fn(ctypes.byref(blocks[t]), stream))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for t in range(steps):
+        fn(ctypes.byref(blocks[t]), stream)
+    e1.record()
+    torch.cuda.synchronize()
+    CA.check(fn(ctypes.byref(blocks[0]), stream))  # surfaces any launch error of the timed loop
+    ms = e0.elapsed_time(e1) / steps
+    state_bytes = 2 * Bd * HV * K * V * 4
+    io_bytes = Bd * (4 * kd + 3 * vd) * 4 + 2 * Bd * 3 * (2 * kd + vd) * 4 + Bd * vd * 4
+    param_bytes = (4 * (2 * kd + vd) + H + kd + V + (kd if cfg.min_decay is not None else 0)) * 4
+    bytes_step = state_bytes + io_bytes + param_bytes
+    gbs = bytes_step / (ms / 1e3) / 1e9
+    copy_same = decode_copy_roof(torch, dev, bytes_step, steps, nrot)
+    del blocks, states, conv, raw, x, W
+    torch.cuda.empty_cache()
+    return {"batch": Bd, "tokens_per_s": Bd / (ms / 1e3), "ms_per_token_step": ms, "bytes_per_step": bytes_step,
+            "core_bytes_per_step": 2 * Bd * HV * K * V * 4 + Bd * (4 * HV * K + 3 * HV * V) * 4,
+            "achieved_GBs": gbs, "peak_GBs": PEAK_HBM_GBS, "frac_hbm": gbs / PEAK_HBM_GBS,
+            "rotating_state_buffers": nrot, "kernel": "gdn2_decode_fused_f32",
+            "copy_same_bytes": copy_same, "frac_copy_same_bytes": copy_same["us"] / (ms * 1e3)}
+
+
+def bench_step(torch, G, args, dev):
+    """The bare one-token step (gdn2_recurrent_step_f32, the reference's
+    fused_step) at B = 64, 16 heads, K = V = 128: `decode_steps` tokens of
+    q, k, g, b [B, H, K] and v, w [B, H, V] prepared up front (L2-normalised
+    k, g in [-0.3, -0.02]), the state updated in place in `decode_rotate`
+    rotating buffers, timed with events on the launch stream; beside it a
+    streaming copy of the same bytes.  Bytes per step: the state read and
+    written plus q, k, g, b, v, w in and the output (2 B HV K V 4 +
+    B (4 HV K + 3 HV V) 4)."""
+    import ctypes
+
+    from gdn2_amd import _capi as CA
+    from gdn2_amd.ops import _stream
+
+    B, H, K, V = args.decode_batch, 16, 128, 128
+    steps, nrot = args.decode_steps, max(1, args.decode_rotate)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(47)
+    q = torch.randn((steps, B, H, K), generator=gen, device=dev) * K ** -0.5
+    k = torch.nn.functional.normalize(torch.randn((steps, B, H, K), generator=gen, device=dev), dim=-1)
+    g = torch.rand((steps, B, H, K), generator=gen, device=dev) * -0.28 - 0.02
+    b = torch.rand((steps, B, H, K), generator=gen, device=dev)
+    v = torch.randn((steps, B, H, V), generator=gen, device=dev)
+    w = torch.randn((steps, B, H, V), generator=gen, device=dev)
+    states = [torch.randn((B, H, K, V), generator=gen, device=dev) * 0.05 for _ in range(nrot)]
+    out = torch.empty((B, H, V), device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    blocks = [CA.StepArgs(P(q[t]), P(k[t]), P(g[t]), P(b[t]), P(v[t]), P(w[t]), P(states[t % nrot]),
+                          P(states[t % nrot]), P(out), B, H, H, K, V, H * K, K, H * V, V, H * V, V, K ** -0.5)
+              for t in range(steps)]
+    L, stream = CA.lib(), _stream()
+    fn = L.gdn2_recurrent_step_f32
+    it = [0]
+
+    def one_step():
         CA.check(fn(ctypes.byref(blocks[it[0] % steps]), stream))
         it[0] += 1
 
@@ -651,22 +718,47 @@ def bench_decode(torch, G, args, dev):
         fn(ctypes.byref(blocks[t]), stream)
     e1.record()
     torch.cuda.synchronize()
-    CA.check(fn(ctypes.byref(blocks[0]), stream))  # surfaces any launch error of the timed loop
+    CA.check(fn(ctypes.byref(blocks[0]), stream))
     ms = e0.elapsed_time(e1) / steps
-    state_bytes = 2 * Bd * H * K * V * 4
-    io_bytes = Bd * (4 * kd + 3 * vd) * 4 + 2 * Bd * 3 * (2 * kd + vd) * 4 + Bd * vd * 4
-    param_bytes = (4 * (2 * kd + vd) + H + kd + V) * 4
-    bytes_step = state_bytes + io_bytes + param_bytes
+    bytes_step = 2 * B * H * K * V * 4 + B * (4 * H * K + 3 * H * V) * 4
     gbs = bytes_step / (ms / 1e3) / 1e9
     copy_same = decode_copy_roof(torch, dev, bytes_step, steps, nrot)
+    del blocks, states, q, k, g, b, v, w, out
+    torch.cuda.empty_cache()
+    return {"workload": f"bare one-token step (fused_step), B={B} H=16 K=V=128, state in place",
+            "kernel": "gdn2_recurrent_step_f32", "batch": B, "tokens_per_s": B / (ms / 1e3),
+            "ms_per_token_step": ms, "bytes_per_step": bytes_step, "achieved_GBs": gbs, "peak_GBs": PEAK_HBM_GBS,
+            "frac_hbm": gbs / PEAK_HBM_GBS, "rotating_state_buffers": nrot, "copy_same_bytes": copy_same,
+            "frac_copy_same_bytes": copy_same["us"] / (ms * 1e3)}
+
+
+def bench_decode(torch, G, args, dev):
+    """Config 3: the default layer (FusedRecurrent, short conv) at B = 64.
+    (a) The fused decode kernel alone over 256 tokens whose raw projections
+    are prepared up front, with rotating state buffers (larger than the
+    256 MB MALL; the kernel's time does not depend on the state values).
+    (b) The whole layer: forward() over a 2048-token prefill, then 256
+    single-token forward() calls carrying the Gdn2State.
+    (c) The fused decode kernel at the GVA + extensions configuration (C4:
+    8 key heads, 16 value heads, K 128, V 256, neg-eig, min_decay) at its
+    batch of 4."""
+    cfg = G.Gdn2Config(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0)
+    Bd = args.decode_batch
+    steps = args.decode_steps
+    nrot = max(1, args.decode_rotate)
+    res = time_decode_kernel(torch, G, dev, cfg, Bd, steps, nrot, args.settle_ms)
     tr = load_traffic("decode_b64_traffic.json") if Bd == 64 else None
-    res = {"batch": Bd, "tokens_per_s": Bd / (ms / 1e3), "ms_per_token_step": ms, "bytes_per_step": bytes_step,
-           "traffic": None if tr is None else tr.get("hbm_bytes_per_launch"),
-           "core_bytes_per_step": 2 * Bd * H * K * V * 4 + Bd * (4 * H * K + 3 * H * V) * 4,
-           "achieved_GBs": gbs, "peak_GBs": PEAK_HBM_GBS, "frac_hbm": gbs / PEAK_HBM_GBS,
-           "rotating_state_buffers": nrot, "kernel": "gdn2_decode_fused_f32",
-           "copy_same_bytes": copy_same, "frac_copy_same_bytes": copy_same["us"] / (ms * 1e3)}
-    del blocks, states, conv, raw, x, W
+    res["traffic"] = None if tr is None else tr.get("hbm_bytes_per_launch")
+    over, B4 = OTHER_CONFIGS["C4"][0], OTHER_CONFIGS["C4"][1]
+    cfg4 = G.Gdn2Config(**dict(over, mode="fused_recurrent"))
+    # as many rotating states as the B = 64 leg's bytes (more than the 256 MB MALL)
+    nrot4 = max(nrot, -(-nrot * Bd * cfg.hv * cfg.head_dim * cfg.v_head // (B4 * cfg4.hv * cfg4.head_dim * cfg4.v_head)))
+    c4 = time_decode_kernel(torch, G, dev, cfg4, B4, steps, nrot4, args.settle_ms, seed=48)
+    c4["workload"] = "C4 decode: " + OTHER_CONFIGS["C4"][5]
+    res["c4_decode"] = c4
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(49)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if not args.no_layer:
         layer = G.GatedDeltaNet2(cfg, seed=1337)
         xp = torch.randn((Bd, args.decode_prefill, cfg.hidden_size), generator=gen, device=dev)
@@ -699,7 +791,7 @@ def bench_decode(torch, G, args, dev):
         res["layer"] = {"prefill_tokens": Bd * args.decode_prefill, "prefill_ms": pre_ms,
                         "prefill_tokens_per_s": Bd * args.decode_prefill / (pre_ms / 1e3),
                         "decode_ms_per_token_step": lms, "decode_tokens_per_s": Bd / (lms / 1e3),
-                        "weight_bytes_per_step": sum(a.nbytes for a in Wn.values() if a is not None)}
+                        "weight_bytes_per_step": sum(a.nbytes for a in layer.params().values() if a is not None)}
         del st
         layer.close()
     return res
@@ -897,7 +989,9 @@ def timed_summary(path, warmup, steps, decode_steps):
     print("|---|---|---|---|---|")
     for label, key, skip, take in (("chunk_intra", "chunk_intra_kernel<128, 128, false>", warmup, steps),
                                    ("chunk_inter", "chunk_inter_kernel<128, 0>", warmup, steps),
-                                   ("decode", "decode_fused_kernel<128, 128>", 8, decode_steps)):
+                                   ("decode", "decode_fused_kernel<128, 128>", 8, decode_steps),
+                                   ("decode C4", "decode_fused_kernel<128, 256>", 8, decode_steps),
+                                   ("bare step", "step_kernel<128, 128>", 8, decode_steps)):
         for sec in sections:
             d = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in sec
                  if _short(r["Kernel_Name"]) == key]
@@ -1144,6 +1238,7 @@ def main():
         return
     pre = bench_prefill(torch, G, args, dev)
     dec = None if args.no_decode else bench_decode(torch, G, args, dev)
+    step = None if args.no_decode else bench_step(torch, G, args, dev)
     bwd = None if args.no_backward else bench_backward(torch, G, args, dev)
     others = None if args.no_configs else {n: bench_other_config(torch, G, args, dev, n) for n in OTHER_CONFIGS}
     copy_roof = bench_copy_roof(torch, dev)
@@ -1177,6 +1272,7 @@ def main():
         "kernels": pre["kernels"],
         "decode": dec,
         "decode_tokens_per_s": None if dec is None else dec["tokens_per_s"],
+        "step": step,
         "layer": {"prefill": pre["layer"], "decode": None if dec is None else dec.get("layer")},
         "backward": bwd,
         "configs": others,
@@ -1190,6 +1286,8 @@ def main():
                                               "frac_copy_roof": gbs / copy_roof["GBs"]})
     if dec is not None:
         dec["frac_copy_roof"] = dec["achieved_GBs"] / copy_roof["GBs"]
+    if step is not None:
+        step["frac_copy_roof"] = step["achieved_GBs"] / copy_roof["GBs"]
     print(json.dumps(line), flush=True)
 
 

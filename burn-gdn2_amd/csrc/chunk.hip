@@ -341,40 +341,33 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
                     if (q == pt) acc[pi][q] += dacc;
             }
         }
+        // The training variant: one masked channel at a time, the row operand
+        // read again from memory (row 4 lg + i of the tile).
+        if constexpr (TRAIN) {
 #pragma unroll
-        for (int pi = 0; pi < 2; ++pi) {
-            const int pt = pi ? (NT - 1 - half) : half;
+            for (int pi = 0; pi < 2; ++pi) {
+                const int pt = pi ? (NT - 1 - half) : half;
 #pragma unroll
-            for (int q = 0; q < NT && TRAIN; ++q) {
-                if (q == pt && (pi == 1 || q < NT / 2)) {
-                    for (int wd = kh * (K / 64); wd < (kh + 1) * (K / 64); ++wd) {
-                        uint32_t mw = sMask[pt][wd];
-                        while (mw) {
-                            const int c = wd * 32 + __builtin_ctz(mw);
-                            mw &= mw - 1u;
-                            const int cm = (c >> 4) - m0, cj = c & 3, cg = (c & 15) >> 2;
-                            float own = 0.f;
-                            if constexpr (!TRAIN) {
+                for (int q = 0; q < NT; ++q) {
+                    if (q == pt && (pi == 1 || q < NT / 2)) {
+                        for (int wd = kh * (K / 64); wd < (kh + 1) * (K / 64); ++wd) {
+                            uint32_t mw = sMask[pt][wd];
+                            while (mw) {
+                                const int c = wd * 32 + __builtin_ctz(mw);
+                                mw &= mw - 1u;
+                                const int srow = 16 * pt + lr;
+                                const float ks = sK[srow][c];
+                                const float gs = sG[srow][c];
 #pragma unroll
-                                for (int m = 0; m < NKH; ++m)
-#pragma unroll
-                                    for (int j = 0; j < 4; ++j)
-                                        if (m == cm && j == cj) own = araw[pi][m][j];
-                            }
-                            const int owni = __builtin_bit_cast(int, own);
-                            const int srow = 16 * pt + lr;
-                            const float ks = sK[srow][c];
-                            const float gs = sG[srow][c];
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                const int r = 4 * lg + i;
-                                const int rrow = 16 * pt + r;
-                                const float xg =
-                                    TRAIN ? bld1(mat == 0 ? Rq : Rb, lg_q + (16 * pt + i) * rq + c) // row rrow
-                                          : __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(4 * (16 * cg + r), owni));
-                                const float xr = (mat == 0) ? xg : xg * sK[rrow][c];
-                                const float e = (mat == 0 ? (r >= lr) : (r > lr)) ? fast_exp2(sG[rrow][c] - gs) : 0.f;
-                                acc[pi][q][i] += xr * ks * e;
+                                for (int i = 0; i < 4; ++i) {
+                                    const int r = 4 * lg + i;
+                                    const int rrow = 16 * pt + r;
+                                    const float xg = bld1(mat == 0 ? Rq : Rb, lg_q + (16 * pt + i) * rq + c);
+                                    const float xr = (mat == 0) ? xg : xg * sK[rrow][c];
+                                    const float e =
+                                        (mat == 0 ? (r >= lr) : (r > lr)) ? fast_exp2(sG[rrow][c] - gs) : 0.f;
+                                    acc[pi][q][i] += xr * ks * e;
+                                }
                             }
                         }
                     }
@@ -1234,7 +1227,7 @@ extern "C" size_t gdn2_chunk_workspace_bytes(const gdn2_chunk_args *a) {
 namespace gdn2 {
 
 // Checks shared by the chunked forward and backward; fills p's shapes and
-// strides.  Limits: K in {64, 128}, V in {64, 128, 256}, 16-byte aligned q,
+// strides.  Limits: the (K, V) pairs of chunk_supported, 16-byte aligned q,
 // k, b with strides that are multiples of 4 elements, token strides within
 // the range-checked row loads.
 gdn2_status chunk_setup(const gdn2_chunk_args *a, const char *who, bool need_out, ChunkParams *p) {

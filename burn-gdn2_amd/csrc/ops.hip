@@ -88,6 +88,11 @@ extern "C" gdn2_status gdn2_short_conv_f32(const float *x, const float *weight, 
     if ((cache_in && overlaps(cache_in, nc, cache_out, nc)) || overlaps(x, sizeof(float) * B * T * C, cache_out, nc) ||
         overlaps(out, sizeof(float) * B * T * C, cache_out, nc))
         return fail(GDN2_EINVAL, who + "cache_out must not overlap x, out or cache_in");
+    // Each tile reads the three rows before it and the cache reads the last
+    // three rows of x, while other tiles write their outputs: out must not
+    // overlap x (no in-place use).
+    if (T > 0 && overlaps(x, sizeof(float) * B * T * C, out, sizeof(float) * B * T * C))
+        return fail(GDN2_EINVAL, who + "out must not overlap x");
     if (B > 65535 || (T + kConvTile - 1) / kConvTile > 65535) return fail(GDN2_NOT_APPLICABLE, who + "grid limits");
     const int64_t tiles = T > 0 ? (T + kConvTile - 1) / kConvTile : 1;
     hipLaunchKernelGGL(short_conv_kernel, dim3((unsigned)((C + 255) / 256), (unsigned)B, (unsigned)tiles), dim3(256),

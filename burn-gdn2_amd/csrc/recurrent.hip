@@ -475,6 +475,108 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
     }
 }
 
+// The bare single-token step (src/kernel/fused_recurrent_cube.rs:14-57) at
+// the decode kernel's head shapes: one workgroup per (b, hv) owns all V
+// columns.  Its q, k, g, b (lane r < K) and v, w (lane c < V) are requested
+// before the state, since the memory counter is in order and anything loaded
+// after the state would wait for the whole slice; the state is then streamed
+// once each way with 16-byte non-temporal accesses, in NH parts so that part
+// 0's update and write-back overlap part 1's loads.  state_out may equal
+// state_in: every element is read and written by the same lane.
+template <int K, int V>
+__global__ __launch_bounds__(256) void step_kernel(ScanParams p) {
+    constexpr int NH = V >= 128 ? 2 : 1, VP = V / NH;
+    constexpr int TPR = VP / 4, RPP = 256 / TPR, NP = K / RPP;
+    static_assert(VP % 4 == 0 && TPR <= 64 && 64 % TPR == 0, "V");
+    static_assert(K % RPP == 0 && K <= 256 && V <= 256, "K, V");
+    const int bh = blockIdx.x;
+    const int bi = bh / p.HV, hv = bh % p.HV, hk = hv / p.rep;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cg = tid % TPR, r0 = tid / TPR;
+
+    __shared__ float s_eg[K], s_a1[K], s_a2[K], s_k[K];
+    __shared__ float s_red[2][4][VP];
+    __shared__ float s_vn[V];
+    __shared__ float red[4];
+
+    const int r = tid % K; // key channel (lanes >= K duplicate)
+    const int64_t ko = (int64_t)bi * p.sqb + (int64_t)hk * p.sqh + r;
+    const float qq = p.q[ko], kk = p.k[ko], gg = p.g[ko], bb = p.b[ko];
+    const int col = tid % V; // value column (lanes >= V duplicate)
+    const int64_t vo = (int64_t)bi * p.svb + (int64_t)hv * p.svh + col;
+    const float vv = p.v[vo], ww = p.w[vo];
+
+    floatx4 S[NH][NP];
+    const size_t sb = (size_t)bh * K * V + cg * 4;
+    const float *Si = p.state_in + sb;
+    float *So = p.state_out + sb;
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int i = 0; i < NP; ++i)
+            S[h][i] = __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(Si + (size_t)(r0 + i * RPP) * V + h * VP));
+
+    const bool klane = tid < K;
+    float kq = 0.f;
+    if (klane) {
+        const float eg = expf(gg);
+        s_eg[r] = eg;
+        s_a1[r] = eg * (bb * kk);
+        s_a2[r] = eg * qq;
+        s_k[r] = kk;
+        kq = kk * qq;
+    }
+    kq = wave_sum(kq);
+    if (lane == 0) red[wave] = kq;
+    __syncthreads();
+    const float kqs = red[0] + red[1] + red[2] + red[3];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        float e1[4] = {0.f, 0.f, 0.f, 0.f}, e2[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int rr = r0 + i * RPP;
+            const float a1 = s_a1[rr], a2 = s_a2[rr];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                e1[j] += S[h][i][j] * a1;
+                e2[j] += S[h][i][j] * a2;
+            }
+        }
+#pragma unroll
+        for (int off = TPR; off < 64; off <<= 1)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                e1[j] += __shfl_xor(e1[j], off, 64);
+                e2[j] += __shfl_xor(e2[j], off, 64);
+            }
+        if (lane < TPR)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                s_red[0][wave][cg * 4 + j] = e1[j];
+                s_red[1][wave][cg * 4 + j] = e2[j];
+            }
+        __syncthreads();
+        if (tid >= h * VP && tid < (h + 1) * VP) {
+            const int pc = tid - h * VP;
+            const float E1 = s_red[0][0][pc] + s_red[0][1][pc] + s_red[0][2][pc] + s_red[0][3][pc];
+            const float E2 = s_red[1][0][pc] + s_red[1][1][pc] + s_red[1][2][pc] + s_red[1][3][pc];
+            const float vn = ww * vv - E1;
+            p.out[(int64_t)bi * p.sob + (int64_t)hv * p.soh + col] = p.scale * (E2 + vn * kqs);
+            s_vn[tid] = vn;
+        }
+        __syncthreads();
+        const floatx4 vn4 = *reinterpret_cast<const floatx4 *>(&s_vn[h * VP + cg * 4]);
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int rr = r0 + i * RPP;
+            const float eg = s_eg[rr], k2 = s_k[rr];
+            __builtin_nontemporal_store(S[h][i] * eg + k2 * vn4,
+                                        reinterpret_cast<floatx4 *>(So + (size_t)rr * V + h * VP));
+        }
+    }
+}
+
 // Any K <= 256, V <= 1024: state in global memory, one column per lane.
 __global__ __launch_bounds__(256) void decode_fused_generic_kernel(DecodeParams p) {
     extern __shared__ float sm[];
@@ -548,7 +650,20 @@ hipError_t launch_decode_t(const DecodeParams &p, hipStream_t s) {
 
 }  // namespace
 
+template <int K, int V>
+hipError_t launch_step_t(const ScanParams &p, hipStream_t s) {
+    hipLaunchKernelGGL((step_kernel<K, V>), dim3(p.B * p.HV), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
 hipError_t launch_scan(const ScanParams &p, hipStream_t s) {
+    // One token at the decode kernel's head shapes: the streaming step kernel.
+    if (p.T == 1) {
+        if (p.K == 128 && p.V == 128) return launch_step_t<128, 128>(p, s);
+        if (p.K == 128 && p.V == 256) return launch_step_t<128, 256>(p, s);
+        if (p.K == 64 && p.V == 64) return launch_step_t<64, 64>(p, s);
+        if (p.K == 64 && p.V == 128) return launch_step_t<64, 128>(p, s);
+    }
     // Register kernels: VS columns per workgroup.  VS = 64 splits each head's
     // V = 128 columns over two workgroups, which doubles the number of
     // workgroups for small batch x head counts.

@@ -205,7 +205,13 @@ GDN2_API gdn2_status gdn2_chunk_fwd_states_f32(const gdn2_chunk_args *args, floa
  * launches nothing (at K = V = 128 the array holds about 450 chunks of 64
  * tokens, counted over every (batch row, value head)).  All calls on one GPU
  * share its array: calls that overlap in time on one GPU (two streams or two
- * host threads) race and must be ordered by the caller. */
+ * host threads) race and must be ordered by the caller.  The first call on a
+ * device looks up that device's copy of the array (hipGetSymbolAddress),
+ * which may load the code object: make that first call eagerly, before any
+ * graph capture on that device. */
+GDN2_API size_t gdn2_chunk_noalloc_scratch_bytes(void);
+GDN2_API gdn2_status gdn2_chunk_fwd_noalloc_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Standalone operators, the reference's public functions (src/lib.rs:58-62),
  * for a binding that calls them one by one (the layer fuses them into its
@@ -216,8 +222,8 @@ GDN2_API gdn2_status gdn2_chunk_fwd_states_f32(const gdn2_chunk_args *args, floa
  * the first token is repeated 3 times as padding), out [B, T, C],
  * cache_out [B, 3, C] = the last 3 rows of cat(cache or padding, x) along time.
  *   out[b, t, c] = silu(sum_{i<4} xpad[b, t + i, c] weight[c, i])
- * cache_out must not overlap x, out or cache_in.  T = 0 needs cache_in
- * (cache_out = cache_in).
+ * out must not overlap x (no in-place use), and cache_out must not overlap
+ * x, out or cache_in.  T = 0 needs cache_in (cache_out = cache_in).
  *
  * l2_normalize / l2_normalize_4d (src/l2norm.rs:4-16): y = x / sqrt(sum x^2 +
  * eps) over each of `rows` rows of n values (any leading shape flattened);
@@ -242,9 +248,6 @@ GDN2_API gdn2_status gdn2_rms_norm_gate_f32(const float *x, const float *gate, c
  * bandwidth (2 n x 4 bytes moved per call) beside the 8 TB/s peak. */
 GDN2_API gdn2_status gdn2_stream_copy_f32(float *dst, const float *src, int64_t n, int64_t workgroups,
                                           gdn2_stream_t stream);
-
-GDN2_API size_t gdn2_chunk_noalloc_scratch_bytes(void);
-GDN2_API gdn2_status gdn2_chunk_fwd_noalloc_f32(const gdn2_chunk_args *args, gdn2_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Chunked backward                                     -- fused_chunk_backward

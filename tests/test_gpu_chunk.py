@@ -306,3 +306,48 @@ def test_chunk_states_refuse_other_chunk_sizes(gpu):
     assert gdn2_amd.chunk_wy_forward(*d, 0.125, chunk_size=64, return_states=True) is not None
     d2 = _dev(gpu, *(a[:, :, :90] for a in (q, k, v, g, b, w)), np.zeros((1, 1, 64, 64), np.float32))
     assert gdn2_amd.chunk_wy_forward(*d2, 0.125, chunk_size=32, return_states=True) is None  # 90 % 32 != 0
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 2, 2048, 128, 128), (2, 2, 2, 300, 128, 128)],
+                         ids=["segmented", "one_segment"])
+def test_inter_passes_equal_inter(gpu, shape):
+    """gdn2_chunk_inter_pass_f32 1, 2, 3 after gdn2_chunk_intra_f32 equal
+    gdn2_chunk_inter_f32 bit for bit (the phase bits of the passes, and pass 3
+    alone being the whole inter phase when there is one segment);
+    gdn2_chunk_segments names the split; other pass numbers are refused."""
+    import ctypes
+
+    import torch
+
+    import gdn2_amd
+    from gdn2_amd import _capi as C
+    from gdn2_amd.ops import _stream, chunk_args
+
+    B, Hk, HV, T, K, V = shape
+    rng = np.random.default_rng(77 + T)
+    q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=-0.01, g_hi=-0.001)
+    S0 = rng.standard_normal((B, HV, K, V)).astype(np.float32)
+    d = _dev(gpu, q, k, v, g, b, w)
+    scale = K ** -0.5
+    L, stream = C.lib(), _stream()
+    results = []
+    for by_pass in (False, True):
+        st = _dev(gpu, S0)[0]
+        out = torch.empty((B, HV, T, V), device=gpu)
+        ws = torch.empty(gdn2_amd.chunk_workspace_bytes(*d, st, out, scale, 64), dtype=torch.uint8, device=gpu)
+        a = chunk_args(*d, st, out, scale, 64, ws)
+        nseg = int(L.gdn2_chunk_segments(ctypes.byref(a)))
+        assert (nseg > 1) == (shape[3] == 2048), nseg
+        C.check(L.gdn2_chunk_intra_f32(ctypes.byref(a), stream))
+        if by_pass:
+            for ps in (1, 2, 3):
+                C.check(L.gdn2_chunk_inter_pass_f32(ctypes.byref(a), ps, stream))
+            for bad in (0, 4):
+                assert L.gdn2_chunk_inter_pass_f32(ctypes.byref(a), bad, stream) == C.GDN2_EINVAL
+        else:
+            C.check(L.gdn2_chunk_inter_f32(ctypes.byref(a), stream))
+        torch.cuda.synchronize()
+        results.append((out.cpu(), st.cpu()))
+    assert torch.equal(results[0][0], results[1][0]) and torch.equal(results[0][1], results[1][1])
+    o_ref, S_ref = O.recurrent_f64(q, k, v, g, b, w, S0=S0, scale=scale)
+    assert maxabs(results[1][0].numpy(), o_ref) < TOL and maxabs(results[1][1].numpy(), S_ref) < TOL

@@ -51,10 +51,35 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}g{c[6][0]}" for c in CASES])
-def test_chunk_bwd_matches_adjoint(gpu, case):
-    """Sequences of 2048+ tokens at one or two sequences x heads run the
-    segmented forward and reverse recurrences (per-segment transitions)."""
+# Decays whose 16-token span passes the kernels' safe span of 2^96 (in the
+# forward's chunk-intra and the backward's decay pass): those channels of a
+# diagonal 16 x 16 block leave the MFMA product and are added exactly, pair by
+# pair.  |g| up to 31 per token (the long-context configuration's decays) puts
+# nearly every channel there; U(-6, -2) mixes masked and unmasked channels.
+STRONG_CASES = [
+    (1, 1, 1, 200, 128, 128, (-31.0, -0.05), 1.0, 0.5, True),
+    (1, 2, 2, 130, 64, 64, (-31.0, -0.05), 1.0, 0.5, True),     # K = 64, ragged last chunk
+    (1, 1, 2, 150, 128, 256, (-31.0, -0.05), 2.0, 0.5, True),   # GVA rep 2, V = 2K, negative eigenvalues
+    (1, 1, 2, 100, 64, 256, (-31.0, -0.05), 1.0, 0.5, True),    # GVA, V = 4K
+    (2, 2, 2, 190, 128, 128, (-6.0, -2.0), 1.0, 0.5, True),     # masked and unmasked channels mixed
+    (1, 1, 1, 2100, 128, 128, (-6.0, -2.0), 2.0, 1.0, True),    # segmented, negative eigenvalues
+]
+
+SAFE_SPAN_LOG2 = 96.0
+
+
+def masked_tiles(g, T):
+    """Number of (16-token tile, channel) pairs whose decay span over the tile,
+    -sum(g) log2(e), exceeds the kernels' safe span (tiles start at multiples
+    of 16, since the 64-token chunks do)."""
+    gt = np.asarray(g, np.float64)
+    pad = (-T) % 16
+    gt = np.pad(gt, [(0, 0), (0, 0), (0, pad), (0, 0)])
+    span = -gt.reshape(gt.shape[0], gt.shape[1], -1, 16, gt.shape[3]).sum(3) * np.log2(np.e)
+    return int((span > SAFE_SPAN_LOG2).sum()), int(span.size)
+
+
+def _run_case(gpu, case):
     import torch
 
     import gdn2_amd
@@ -74,6 +99,27 @@ def test_chunk_bwd_matches_adjoint(gpu, case):
     assert got is not None
     torch.cuda.synchronize()
     _compare(got, ref, str(case[:6]))
+    return g
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}g{c[6][0]}" for c in CASES])
+def test_chunk_bwd_matches_adjoint(gpu, case):
+    """Sequences of 2048+ tokens at one or two sequences x heads run the
+    segmented forward and reverse recurrences (per-segment transitions)."""
+    _run_case(gpu, case)
+
+
+@pytest.mark.parametrize("case", STRONG_CASES,
+                         ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}g{c[6][0]}" for c in STRONG_CASES])
+def test_chunk_bwd_strong_decay(gpu, case):
+    """The exact pairwise diagonal terms of the training forward's chunk-intra
+    and of the backward's decay pass: every case has masked channels."""
+    g = _run_case(gpu, case)
+    n, tot = masked_tiles(g, case[3])
+    print(f"masked (tile, channel) pairs: {n} of {tot}")
+    assert n > 0
+    if case[6][0] > -10:  # the mixed range also keeps channels in the MFMA product
+        assert n < tot
 
 
 def test_chunk_bwd_strided_views(gpu):

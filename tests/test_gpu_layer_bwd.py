@@ -221,3 +221,29 @@ def test_saved_activations_equal_recompute(gpu):
             np.testing.assert_array_equal(a, b, err_msg=n)
     with pytest.raises(G._capi.Gdn2Error):  # shape mismatch
         layer.backward(x[:, :64].contiguous(), d[:, :64].contiguous(), saved=saved)
+
+
+def test_strong_decay_layer_backward(gpu):
+    """The long-context configuration's decays (dt_bias + 4: per-token |g| of
+    tens) on a small layer in chunk mode: the training forward's and the
+    backward's exact diagonal terms for channels whose 16-token decay span
+    passes 2^96 are reached (asserted on the layer's own g) and every
+    gradient matches the double adjoint."""
+    import torch
+
+    G, cfg, layer, W = _setup(gpu, dict(SMALL, hidden_size=256, num_heads=2, head_dim=128))
+    layer.set_param("dt_bias", W["dt_bias"] + 4.0)
+    W = layer.params()
+    rng = np.random.default_rng(15)
+    B, T = 2, 100
+    xh = rng.standard_normal((B, T, cfg.hidden_size)).astype(np.float32)
+    dh = rng.standard_normal((B, T, cfg.hidden_size)).astype(np.float32)
+    x = torch.from_numpy(xh).to(gpu)
+    g = layer.project(x)["g"].cpu().numpy()
+    gt = np.pad(g.astype(np.float64), [(0, 0), (0, 0), (0, (-T) % 16), (0, 0)])
+    span = -gt.reshape(B, cfg.num_heads, -1, 16, cfg.head_dim).sum(3) * np.log2(np.e)
+    print(f"tiles x channels over the safe span: {int((span > 96).sum())} of {span.size}")
+    assert (span > 96).any()
+    dx, grads, dsi = layer.backward(x, torch.from_numpy(dh).to(gpu), want_d_state=True)
+    ref = O.layer_backward_f64(cfg, W, xh, dh)
+    _compare(grads, dx, dsi, ref, O.WEIGHT_NAMES)

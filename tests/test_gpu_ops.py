@@ -95,3 +95,14 @@ def test_ops_refuse_bad_arguments(gpu):
         G.short_conv_1d(x, w)  # no tokens and no cache
     with pytest.raises(ValueError):
         G.short_conv_1d(torch.zeros((1, 4, 8), device=gpu), torch.zeros((8, 3), device=gpu))
+    # in-place use: the conv's tiles read rows that other tiles overwrite
+    xs = torch.zeros((2, 100, 8), device=gpu)
+    cache = torch.zeros((2, 3, 8), device=gpu)
+    lib = C.lib()
+    st = lib.gdn2_short_conv_f32(xs.data_ptr(), w.data_ptr(), None, xs.data_ptr(), cache.data_ptr(), 2, 100, 8, None)
+    assert st == C.GDN2_EINVAL and "overlap" in lib.gdn2_last_error().decode()
+    # a disjoint out is accepted
+    out = torch.empty_like(xs)
+    assert lib.gdn2_short_conv_f32(xs.data_ptr(), w.data_ptr(), None, out.data_ptr(), cache.data_ptr(), 2, 100, 8,
+                                   None) == C.GDN2_OK
+    torch.cuda.synchronize()
