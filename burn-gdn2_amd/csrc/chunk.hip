@@ -780,15 +780,23 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         for (int mt = 0; mt < NT; ++mt)
             u_cur[mt] = pcol ? floatx4{0.f, 0.f, 0.f, 0.f} : U4[cid * uvf4 + (size_t)(vt * NT + mt) * 64 + lane];
         if (STATES) { // the state entering chunk n
-            const size_t slot = p.st_step ? (size_t)bh * p.st_chunks + (size_t)n * p.st_step : cid;
+            size_t slot = cid;
+            bool keep = true;
+            if (p.st_cc) { // the first caller chunk starting inside chunk n (wave-uniform)
+                const int j0 = (n * C + p.st_cc - 1) / p.st_cc;
+                keep = j0 < p.st_chunks;
+                slot = (size_t)bh * p.st_chunks + j0;
+            }
             float *Sn = p.ws_sn + slot * K * V;
+            if (keep) {
 #pragma unroll
-            for (int kb = 0; kb < NKT; ++kb)
-                if (MODE == kInterStates) // the backward's fragment layout: tile (value tile, key tile)
-                    reinterpret_cast<floatx4 *>(Sn)[(vt * NKT + kb) * 64 + lane] = S[kb];
-                else
+                for (int kb = 0; kb < NKT; ++kb)
+                    if (MODE == kInterStates) // the backward's fragment layout: tile (value tile, key tile)
+                        reinterpret_cast<floatx4 *>(Sn)[(vt * NKT + kb) * 64 + lane] = S[kb];
+                    else
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) Sn[(size_t)(16 * kb + 4 * lg + i) * V + col] = S[kb][i];
+                        for (int i = 0; i < 4; ++i) Sn[(size_t)(16 * kb + 4 * lg + i) * V + col] = S[kb][i];
+            }
         }
         // keep these loads here, a whole phase ahead of their use and of the
         // vmcnt wait before the next barrier, and the touches last
@@ -846,7 +854,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) X1[mt] = u_cur[mt] - X1[mt];
         if (STATES) {
-            if (p.st_step) { // token rows [B * HV, T, V]; rows past T (ragged last chunk) are not written
+            if (p.st_cc) { // token rows [B * HV, T, V]; rows past T (ragged last chunk) are not written
                 float *Vn = p.ws_vn + ((size_t)bh * p.T + (size_t)n * C) * V;
 #pragma unroll
                 for (int mt = 0; mt < NT; ++mt)
@@ -1008,29 +1016,43 @@ __global__ __launch_bounds__(256, 1) void chunk_chain_kernel(ChunkParams p) {
     }
 }
 
-// The states at the boundaries of caller chunks of Cc tokens (Cc dividing 64,
-// p.st_step = 64 / Cc > 1) that fall inside a 64-token chunk n, from the state
-// S_n entering it (already in its slot) and the chunk's own tokens:
+// The states at the boundaries of caller chunks of Cc = p.st_cc tokens (Cc <
+// 64, T a multiple of Cc) from the state S_n entering the 64-token chunk n
+// that holds the boundary (stored by chunk-inter in slot j0(n), the first
+// caller chunk starting inside chunk n) and the chunk's own tokens: with m
+// the boundary's offset in chunk n,
 //   S(64 n + m) = diag(exp(G_m)) S_n + sum_{t < m} (k_t exp(G_m - G_{t+1}))^T v_new_t
 // with G_j = g_0 + .. + g_{j-1} per key channel from the chunk start, so that
 // every exponent is <= 0 (src/kernel/chunk_cube.rs:612-734 returns these
 // states for the reference's own chunk size).  One workgroup per (b, hv,
-// 64-token chunk, boundary m = Cc, 2 Cc, .., 64 - Cc, 64 value columns).
-template <int K>
+// caller chunk j, 64 value columns).  INPLACE = false: every caller chunk but
+// j0(n) (read-only access to slot j0(n)); INPLACE = true, launched after:
+// slot j0(n) itself where its boundary is not 64 n (Cc not dividing 64),
+// every element read and written by the same thread.
+template <int K, bool INPLACE>
 __global__ __launch_bounds__(256) void chunk_states_kernel(ChunkParams p) {
     __shared__ float sA[C][K]; // k rows, then the decayed keys k_t exp(G_m - G_{t+1})
     __shared__ float sB[C][K]; // g rows, then v_new rows (64 value columns)
     __shared__ float sGam[K];
     static_assert(K >= 64, "sB holds 64 value columns");
-    const int r = p.st_step, nvs = p.V / 64;
+    const int cc = p.st_cc, nvs = p.V / 64;
     int blk = blockIdx.x;
     const int vs = blk % nvs;
     blk /= nvs;
-    const int m = (blk % (r - 1) + 1) * (C / r); // tokens of chunk n before the boundary
-    blk /= r - 1;
-    const int n = blk % p.NC, bh = blk / p.NC;
-    const int t0 = n * C;
-    if (t0 + m >= p.T) return; // no caller chunk starts there (T is a multiple of the caller's chunk size)
+    int j, n, bh;
+    if (INPLACE) { // one workgroup per (b, hv, 64-token chunk)
+        n = blk % p.NC;
+        bh = blk / p.NC;
+        j = (n * C + cc - 1) / cc;
+        if (j >= p.st_chunks) return;
+    } else {
+        j = blk % p.st_chunks;
+        bh = blk / p.st_chunks;
+        n = j * cc / C;
+        if (j == (n * C + cc - 1) / cc) return; // slot j0(n): chunk-inter's (or the in-place pass's)
+    }
+    const int t0 = n * C, m = j * cc - t0; // tokens of chunk n before the boundary
+    if (m == 0) return;                    // (INPLACE: the boundary is the chunk start, already exact)
     const int bi = bh / p.HV, hv = bh % p.HV, hk = hv / p.rep;
     const int64_t kofs = (int64_t)bi * p.sqb + (int64_t)hk * p.sqh + (int64_t)t0 * p.sqt;
     const int tid = threadIdx.x;
@@ -1053,9 +1075,9 @@ __global__ __launch_bounds__(256) void chunk_states_kernel(ChunkParams p) {
     for (int i = tid; i < m * 64; i += 256) sB[i / 64][i % 64] = vn[(size_t)(i / 64) * p.V + i % 64];
     __syncthreads();
     const int v = tid & 63, cg = tid >> 6, col = vs * 64 + v;
-    const size_t slot = (size_t)bh * p.st_chunks + (size_t)n * r;
-    const float *Sn = p.ws_sn + slot * K * p.V;
-    float *So = p.ws_sn + (slot + m / (C / r)) * K * p.V;
+    const size_t slot0 = (size_t)bh * p.st_chunks + (t0 + cc - 1) / cc; // j0(n)
+    const float *Sn = p.ws_sn + slot0 * K * p.V;
+    float *So = p.ws_sn + ((size_t)bh * p.st_chunks + j) * K * p.V;
     for (int c = cg; c < K; c += 4) {
         float acc = sGam[c] * Sn[(size_t)c * p.V + col];
         for (int t = 0; t < m; ++t) acc += sA[t][c] * sB[t][v];
@@ -1129,19 +1151,24 @@ bool chunk_supported(int K, int V) {
 
 bool chunk_bwd_supported(int K, int V) { return (K == 64 || K == 128) && (V == 64 || V == 128 || V == 256); }
 
-hipError_t launch_chunk_states(const ChunkParams &p, hipStream_t s) {
-    if (p.st_step <= 1) return hipSuccess;
-    const int64_t grid = (int64_t)p.B * p.HV * p.NC * (p.st_step - 1) * (p.V / 64);
+template <int K>
+hipError_t launch_chunk_states_t(const ChunkParams &p, hipStream_t s) {
+    const int64_t grid = (int64_t)p.B * p.HV * p.st_chunks * (p.V / 64);
     if (grid <= 0) return hipSuccess;
-    if (p.K == 256)
-        hipLaunchKernelGGL(chunk_states_kernel<256>, dim3((unsigned)grid), dim3(256), 0, s, p);
-    else if (p.K == 128)
-        hipLaunchKernelGGL(chunk_states_kernel<128>, dim3((unsigned)grid), dim3(256), 0, s, p);
-    else if (p.K == 64)
-        hipLaunchKernelGGL(chunk_states_kernel<64>, dim3((unsigned)grid), dim3(256), 0, s, p);
-    else
-        return hipErrorInvalidValue;
+    hipLaunchKernelGGL((chunk_states_kernel<K, false>), dim3((unsigned)grid), dim3(256), 0, s, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || C % p.st_cc == 0) return e; // every j0(n) starts its chunk: nothing in place
+    hipLaunchKernelGGL((chunk_states_kernel<K, true>), dim3((unsigned)(p.B * p.HV * p.NC * (p.V / 64))), dim3(256),
+                       0, s, p);
     return hipGetLastError();
+}
+
+hipError_t launch_chunk_states(const ChunkParams &p, hipStream_t s) {
+    if (p.st_cc <= 0) return hipSuccess;
+    if (p.K == 256) return launch_chunk_states_t<256>(p, s);
+    if (p.K == 128) return launch_chunk_states_t<128>(p, s);
+    if (p.K == 64) return launch_chunk_states_t<64>(p, s);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_chunk(const ChunkParams &p, hipStream_t s, int phases) {
@@ -1290,7 +1317,7 @@ void chunk_bind_ws(const gdn2_chunk_args *a, char *ws, ChunkParams *p) {
 // (src/forward.rs:44-278).  phases: 1 intra, 2 inter, 8 inter that also
 // writes v_new and the per-chunk states.
 static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, int phases, const char *who,
-                              float *v_new = nullptr, float *states = nullptr, int st_step = 0) {
+                              float *v_new = nullptr, float *states = nullptr, int st_cc = 0) {
     ChunkParams p;
     const gdn2_status st = chunk_setup(a, who, true, &p);
     if (st != GDN2_OK) return st;
@@ -1300,12 +1327,12 @@ static gdn2_status chunk_call(const gdn2_chunk_args *a, gdn2_stream_t stream, in
     chunk_bind_ws(a, static_cast<char *>(a->workspace), &p);
     p.ws_vn = v_new;
     p.ws_sn = states;
-    if (st_step) {
-        p.st_step = st_step;
-        p.st_chunks = (int)(a->seq_len / (kChunk / st_step));
+    if (st_cc) {
+        p.st_cc = st_cc;
+        p.st_chunks = (int)(a->seq_len / st_cc);
     }
     GDN2_HIP_CHECK(launch_chunk(p, (hipStream_t)stream, phases));
-    if (st_step > 1) GDN2_HIP_CHECK(launch_chunk_states(p, (hipStream_t)stream));
+    if (st_cc) GDN2_HIP_CHECK(launch_chunk_states(p, (hipStream_t)stream));
     return GDN2_OK;
 }
 
@@ -1341,11 +1368,10 @@ extern "C" gdn2_status gdn2_chunk_fwd_states_f32(const gdn2_chunk_args *a, float
     if (a->seq_len > 0 && (!v_new || !states)) return fail(GDN2_EINVAL, std::string(who) + ": null v_new or states");
     if (a->chunk_size == kChunk) return chunk_call(a, stream, 9, who, v_new, states);
     // smaller caller chunks: the reference's limits (chunk_size <= 64, T a
-    // multiple of it), and here a divisor of 64 so that every 64-token chunk
-    // starts a caller chunk
-    if (a->chunk_size <= 0 || a->chunk_size > kChunk || kChunk % a->chunk_size != 0)
-        return fail(GDN2_NOT_APPLICABLE, std::string(who) + ": chunk_size must divide 64");
+    // multiple of it, src/kernel/chunk_cube.rs:795-800)
+    if (a->chunk_size <= 0 || a->chunk_size > kChunk)
+        return fail(GDN2_NOT_APPLICABLE, std::string(who) + ": chunk_size must be in [1, 64]");
     if (a->seq_len % a->chunk_size != 0)
         return fail(GDN2_NOT_APPLICABLE, std::string(who) + ": seq_len must be a multiple of chunk_size");
-    return chunk_call(a, stream, 9, who, v_new, states, (int)(kChunk / a->chunk_size));
+    return chunk_call(a, stream, 9, who, v_new, states, (int)a->chunk_size);
 }

@@ -76,12 +76,14 @@ struct ChunkParams {
                     //      accumulator fragments in (value tile, key tile) order)
     float *ws_vn;   // C*V  v_new of each chunk (row-major; for the backward, fragments in
                     //      (value tile, time tile) order)
-    // Layout of ws_sn / ws_vn for a caller chunk size Cc dividing 64 (0: the
-    // 64-token chunk layout above).  st_step = 64 / Cc slots per 64-token
-    // chunk, st_chunks = T / Cc slots per (b, hv): the state entering 64-chunk
-    // n goes to slot (b * HV + hv) * st_chunks + n * st_step, and v_new is
-    // written as token rows [B * HV, T, V] (rows < T only).
-    int st_step, st_chunks;
+    // Layout of ws_sn / ws_vn for a caller chunk size st_cc < 64 with T a
+    // multiple of it (0: the 64-token chunk layout above).  st_chunks = T /
+    // st_cc slots per (b, hv), slot j holding the state after st_cc j tokens;
+    // v_new is written as token rows [B * HV, T, V] (rows < T only).  The
+    // state entering 64-token chunk n goes to slot j0(n) = ceil(64 n / st_cc),
+    // the first caller chunk that starts inside it (none when j0(n) >=
+    // st_chunks); chunk_states_kernel derives the other slots from it.
+    int st_cc, st_chunks;
 };
 
 // Projection epilogue: raw Linear outputs -> kernel inputs, one token per

@@ -190,8 +190,8 @@ def chunk_wy_forward(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64
     v_new [B*HV*NC, C, V] (the delta-rule values of each chunk of C =
     chunk_size tokens) and states [B*HV*NC, K, V] (the state entering each
     chunk).  chunk_size 64: NC = ceil(T/64) (rows past T are zero); a smaller
-    chunk_size must divide 64 and T (the reference's T % C == 0), NC = T/C;
-    other chunk sizes return None."""
+    chunk_size must divide T (the reference's C <= 64 and T % C == 0), NC =
+    T/C; other chunk sizes return None."""
     _check_f32_cuda(q, k, v, g, b, w, state)
     q, k, v, g, b, w = _operands(q, k, v, g, b, w)
     B, Hk, T, K = q.shape
@@ -204,8 +204,8 @@ def chunk_wy_forward(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64
     Cs = 64 if (not return_states or chunk_size == 64) else int(chunk_size)
     nblk = B * HV * ((T + 63) // 64 if Cs == 64 else (T // Cs if Cs > 0 else 0))
     if return_states:
-        if Cs <= 0 or 64 % Cs or (Cs < 64 and T % Cs):
-            return None  # the per-chunk tensors exist for chunk sizes dividing 64 (and T)
+        if Cs <= 0 or Cs > 64 or (Cs < 64 and T % Cs):
+            return None  # the per-chunk tensors exist for chunk sizes up to 64 that divide T
         v_new = torch.empty((nblk, Cs, V), device=q.device, dtype=torch.float32)
         states = torch.empty((nblk, K, V), device=q.device, dtype=torch.float32)
     if T == 0:

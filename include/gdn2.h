@@ -185,9 +185,10 @@ GDN2_API gdn2_status gdn2_chunk_inter_pass_f32(const gdn2_chunk_args *args, int 
  *   states  [B*HV*NC, K, V] contiguous: the state entering chunk n
  * with chunk id (b * HV + hv) * NC + n, the reference's [nblk, C, V] /
  * [nblk, K, V].  C = 64: NC = ceil(T / 64), rows past T (a ragged last
- * chunk) are zero.  C < 64: C must divide 64 and T (the reference's
- * T % C == 0), NC = T / C; the states inside each 64-token chunk are derived
- * from the state entering it by one more small kernel.  The workspace is
+ * chunk) are zero.  C < 64: C must divide T (the reference's C <= 64 and
+ * T % C == 0, src/kernel/chunk_cube.rs:795-800), NC = T / C; the states at
+ * boundaries inside a 64-token chunk are derived from the state entering it
+ * by one or two more small kernels.  The workspace is
  * gdn2_chunk_workspace_bytes(args) as for gdn2_chunk_fwd_f32.  Limits: those
  * of gdn2_chunk_fwd_f32, and the chunk sizes above (else
  * GDN2_NOT_APPLICABLE). */

@@ -245,6 +245,11 @@ STATE_CASES = [
     (1, 1, 1, 200, 64, 128, 8),      # chunk_size 8
     (1, 2, 2, 2112, 128, 128, 32),   # chunk_size 32 with the segmented inter
     (1, 1, 2, 192, 256, 256, 16),    # K = V = 256, chunk_size 16
+    (1, 2, 2, 240, 128, 128, 48),    # chunk_size 48: boundaries at offsets 48, 32, 16 of the 64-token chunks
+    (2, 1, 2, 168, 64, 128, 24),     # chunk_size 24, GVA rep 2, a ragged last 64-token chunk
+    (1, 1, 1, 96, 64, 64, 48),       # chunk_size 48: the last 64-token chunk starts no caller chunk
+    (1, 2, 2, 2112, 128, 128, 33),   # chunk_size 33 with the segmented inter
+    (1, 1, 2, 180, 256, 128, 36),    # K = 256, chunk_size 36
 ]
 
 
@@ -294,14 +299,16 @@ def test_chunk_forward_returns_v_new_and_states(gpu, case):
 
 
 def test_chunk_states_refuse_other_chunk_sizes(gpu):
-    """Chunk sizes that do not divide 64, or T, have no per-chunk tensors here
-    (None, the caller's fallback)."""
+    """Chunk sizes above 64, or that do not divide T, have no per-chunk
+    tensors (None, the caller's fallback), as in the reference
+    (src/kernel/chunk_cube.rs:795-800)."""
     import gdn2_amd
 
     rng = np.random.default_rng(77)
     q, k, v, g, b, w = rand_inputs(rng, 1, 1, 1, 96, 64, 64)
     d = _dev(gpu, q, k, v, g, b, w, np.zeros((1, 1, 64, 64), np.float32))
-    assert gdn2_amd.chunk_wy_forward(*d, 0.125, chunk_size=48, return_states=True) is None
+    assert gdn2_amd.chunk_wy_forward(*d, 0.125, chunk_size=48, return_states=True) is not None
+    assert gdn2_amd.chunk_wy_forward(*d, 0.125, chunk_size=36, return_states=True) is None  # 96 % 36 != 0
     assert gdn2_amd.chunk_wy_forward(*d, 0.125, chunk_size=64 + 64, return_states=True) is None
     assert gdn2_amd.chunk_wy_forward(*d, 0.125, chunk_size=64, return_states=True) is not None
     d2 = _dev(gpu, *(a[:, :, :90] for a in (q, k, v, g, b, w)), np.zeros((1, 1, 64, 64), np.float32))
