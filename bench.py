@@ -290,7 +290,13 @@ OTHER_CONFIGS = {
                     "x [1, 65536, 2048]"),
     "D256": (dict(hidden_size=2048, num_heads=8, head_dim=256, expand_v=1.0, mode="chunk", chunk_size=64), 8, 4096,
              0.0, 46, "head_dim 256: hidden 2048, 8 heads, K = V = 256, chunk 64, x [8, 4096, 2048]"),
+    "V96": (dict(hidden_size=256, num_heads=4, head_dim=64, expand_v=1.5, mode="chunk", chunk_size=64), 8, 4096,
+            0.0, 47, "the reference's CPU-benchmark layer (tests/bit_exact.rs:224-235): hidden 256, 4 heads, K 64, "
+                     "expand_v 1.5 (V 96), x [8, 4096, 256]"),
 }
+# configurations whose core is also timed on the per-token scan (gdn2_recurrent_fwd_f32,
+# the path their head shapes took before the chunk kernels covered them)
+SCAN_COMPARE = ("V96",)
 
 
 def bench_other_config(torch, G, args, dev, name):
@@ -366,6 +372,25 @@ def bench_other_config(torch, G, args, dev, name):
     if nseg > 1:
         names = ("segment_summaries", "chain", "output_pass")
         res["core"]["chunk_inter"]["passes_ms"] = {n: sum(pp) / reps for n, pp in zip(names, per_pass)}
+    if name in SCAN_COMPARE:
+        from gdn2_amd.ops import _p, _strides3
+
+        ra = CA.RecurrentArgs(_p(q), _p(k), _p(g), _p(b), _p(v), _p(w), _p(state), _p(state), _p(out), B,
+                              cfg.num_heads, HV, T, K, V, *_strides3(q), *_strides3(v), *_strides3(out), scale)
+        rp = ctypes.byref(ra)
+        scan = lambda: CA.check(L.gdn2_recurrent_fwd_f32(rp, stream))
+        settle(torch, scan, args.settle_ms)
+        scan()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            scan()
+        e1.record()
+        torch.cuda.synchronize()
+        scan_ms = e0.elapsed_time(e1) / reps
+        res["core"]["scan"] = {"ms_per_step": scan_ms, "tokens_per_s": tokens / (scan_ms / 1e3),
+                               "chunk_speedup": scan_ms / core_ms, "kernel": "gdn2_recurrent_fwd_f32"}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_config_core(name, [t[:1].contiguous().cpu().numpy() for t in (q, k, v, g, b, w)],
                                               scale)

@@ -118,7 +118,7 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
 #pragma unroll
         for (int i = 0; i < KF4; ++i) // 512 % (K / 4) == 0: row = i 512 / (K / 4) + tid / (K / 4)
             kreg[i] = bld4(Rk, (tid / (K / 4)) * rq + 4 * (tid % (K / 4)) + i * (512 / (K / 4)) * rq);
-        const int c = tid % K, seg = wave * 64 / K; // tid / K, wave-uniform
+        const int c = tid % K, seg = K >= 64 ? wave * 64 / K : tid / K; // tid / K (wave-uniform for K >= 64)
         float vals[RPS];
         float acc = 0.f;
 #pragma unroll
@@ -282,13 +282,16 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
 #pragma unroll
             for (int pi = 0; pi < 2; ++pi) {
                 const int pt = pi ? (NT - 1 - half) : half;
-                constexpr int NWD = K / 64; // mask words of one channel half
+                // mask words of one channel half (K = 32: the half's 16 bits of word 0)
+                constexpr int NWD = K >= 64 ? K / 64 : 1;
                 uint32_t mwh[NWD];
                 uint32_t anyw = 0u;
 #pragma unroll
                 for (int x = 0; x < NWD; ++x) {
-                    mwh[x] = __builtin_amdgcn_readfirstlane(sMask[pt][kh * NWD + x]);
-                    anyw |= mwh[x];
+                    uint32_t wd = __builtin_amdgcn_readfirstlane(sMask[pt][K >= 64 ? kh * NWD + x : 0]);
+                    if (K < 64) wd = (wd >> (16 * kh)) & 0xffffu;
+                    mwh[x] = wd;
+                    anyw |= wd;
                 }
                 if (anyw == 0u) continue; // wave-uniform
                 floatx4 dacc = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -621,31 +624,35 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
 // ---------------------------------------------------------------------------
 constexpr int kInterOut = 0, kInterLocal = 1, kInterStates = 2, kInterOutStates = 3;
 
-template <int K, int MODE>
-__global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int nseg_launch) {
+// NWV waves per workgroup (NWV = 4: 64 value columns; NWV = 2: 32, for value
+// dimensions that are not a multiple of 64 and for K = 32).
+template <int K, int MODE, int NWV>
+__global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p, int nseg_launch) {
     constexpr bool OUT = MODE == kInterOut || MODE == kInterOutStates, LOCAL = MODE == kInterLocal;
     constexpr bool STATES = MODE == kInterStates || MODE == kInterOutStates;
+    constexpr int NTH = 64 * NWV;  // threads per workgroup
+    constexpr int VSW = 16 * NWV;  // value columns per workgroup
     constexpr int NKT = K / 16;
     constexpr int FR = NKT * NT;   // 16x16 fragments per operand per chunk
     constexpr int OPF4 = FR * 64;  // float4 per operand per chunk
-    constexpr int PFO = OPF4 / 256; // float4 per lane per operand
-    static_assert(OPF4 % 256 == 0, "K");
+    constexpr int PFO = OPF4 / NTH; // float4 per lane per operand
+    static_assert(OPF4 % NTH == 0 && K % VSW == 0, "K");
     constexpr int AF4 = NT * NT * 64; // float4 of A_qk per chunk
-    constexpr int APF = AF4 / 256;
+    constexpr int APF = AF4 / NTH;
     __shared__ floatx4 sW[OPF4], sKd[OPF4];
     // K = 256: W and Kd^T take 64 KiB each, so scale q exp(G), which feeds only
     // the output (off the sequential chain), is read from L2 into registers in
     // phase A instead of through a third LDS buffer (145 KiB in all).
     constexpr bool QLDS = OUT && K <= 128;
     __shared__ floatx4 sQ[QLDS ? OPF4 : 1], sA[OUT ? AF4 : 1];
-    __shared__ float sPf[256]; // destination of the L2 touches, never read
+    __shared__ float sPf[NTH]; // destination of the L2 touches, never read
     // exp(G_last) of the chunk, copied with Kd^T: read just before phase C, so
     // that it holds no registers through phases A and D
     __shared__ floatx4 sGam[K / 4];
 
     const int V = p.V;
-    const int nvv = V / 64;                   // value slices
-    const int nvs = LOCAL ? nvv + K / 64 : nvv; // pass 1 adds the slices of P
+    const int nvv = V / VSW;                    // value slices
+    const int nvs = LOCAL ? nvv + K / VSW : nvv; // pass 1 adds the slices of P
     int sq, vs;
     inter_block(blockIdx.x, p.B * p.HV * nseg_launch, nvs, &sq, &vs);
     const int bh = sq / nseg_launch, seg = sq % nseg_launch;
@@ -654,7 +661,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (scalar)
     const int lr = lane & 15, lg = lane >> 4;
     const bool pcol = LOCAL && vs >= nvv;          // a slice of P (wave-uniform)
-    const int vt = (pcol ? vs - nvv : vs) * 4 + wave; // this wave's 16-column tile
+    const int vt = (pcol ? vs - nvv : vs) * NWV + wave; // this wave's 16-column tile
     const int col = 16 * vt + lr;
     const int n0 = seg * p.SEGL;
     const int n1 = min(p.NC, n0 + p.SEGL);
@@ -683,7 +690,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     const size_t uvf4 = (size_t)C * V / 4;
 
     // the operands go from global memory straight into LDS (lds_copy4):
-    // thread tid's float4 i lands at index i * 256 + tid, as a wave's 64 lanes
+    // thread tid's float4 i lands at index i * NTH + tid, as a wave's 64 lanes
     const int wv = 64 * wave;
     // Each chunk's operands are also pulled toward L2 one phase before their
     // LDS copy (l2_touch, one 128-byte line per thread): W, q exp(G) of chunk
@@ -691,7 +698,7 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
     // wave issues the same count (2, then 3) last before the vmcnt waits, which
     // leave them in flight; past the last chunk the current one is touched.
     float *pf_slot = &sPf[wv];
-    constexpr int LOP = OPF4 / 8, LA = AF4 / 8, LU = 4 * NT * 64 / 8; // lines per operand block
+    constexpr int LOP = OPF4 / 8, LA = AF4 / 8, LU = NWV * NT * 64 / 8; // lines per operand block
     const int vsu = pcol ? 0 : vs; // the P slices of pass 1 read no U
     auto touch_wq = [&](size_t c) { // 2 per wave
         l2_touch(reinterpret_cast<const char *>(W4 + c * OPF4) + 128 * (tid % LOP), pf_slot);
@@ -703,13 +710,13 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
             l2_touch(reinterpret_cast<const char *>(A4 + c * AF4) + 128 * (tid % LA), pf_slot);
         else
             l2_touch(reinterpret_cast<const char *>(W4 + c * OPF4) + 128 * (tid % LOP), pf_slot);
-        l2_touch(reinterpret_cast<const char *>(U4 + c * uvf4 + (size_t)vsu * 4 * NT * 64) + 128 * (tid % LU), pf_slot);
+        l2_touch(reinterpret_cast<const char *>(U4 + c * uvf4 + (size_t)vsu * NWV * NT * 64) + 128 * (tid % LU), pf_slot);
     };
     if (n1 > n0) {
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
-            lds_copy4(&W4[(cid0 + n0) * OPF4 + i * 256 + tid], &sW[i * 256 + wv]);
-            if (QLDS) lds_copy4(&Q4[(cid0 + n0) * OPF4 + i * 256 + tid], &sQ[i * 256 + wv]);
+            lds_copy4(&W4[(cid0 + n0) * OPF4 + i * NTH + tid], &sW[i * NTH + wv]);
+            if (QLDS) lds_copy4(&Q4[(cid0 + n0) * OPF4 + i * NTH + tid], &sQ[i * NTH + wv]);
         }
         __builtin_amdgcn_sched_barrier(0);
         touch_kau(cid0 + n0);
@@ -765,13 +772,16 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         vm_wait<3>();  // this wave's copies of chunk n's W, q exp(G) have landed (not the 3 touches after them)
         lds_barrier(); // sW, sQ hold chunk n; every wave is done with sKd, sA (n-1)
 #pragma unroll
-        for (int i = 0; i < PFO; ++i) lds_copy4(&K4[cid * OPF4 + i * 256 + tid], &sKd[i * 256 + wv]);
+        for (int i = 0; i < PFO; ++i) lds_copy4(&K4[cid * OPF4 + i * NTH + tid], &sKd[i * NTH + wv]);
         if (OUT) {
-            // A_qk is lower block-triangular: copy i brings tile (i, wave), so
-            // wave w copies only i >= w (10 of the 16 tiles)
+            // A_qk is lower block-triangular: copy i of wave w brings tile
+            // f = NWV i + w = (f / NT, f % NT), copied only on or below the
+            // diagonal (10 of the 16 tiles)
 #pragma unroll
-            for (int i = 0; i < APF; ++i)
-                if (i >= wave) lds_copy4(&A4[cid * AF4 + i * 256 + tid], &sA[i * 256 + wv]);
+            for (int i = 0; i < APF; ++i) {
+                const int f = NWV * i + wave;
+                if (f % NT <= f / NT) lds_copy4(&A4[cid * AF4 + i * NTH + tid], &sA[i * NTH + wv]);
+            }
             if (n > n0) store_out(X2, n - 1);
         }
         if (wave == 0 && lane < K / 4) lds_copy4(&G4[cid * (K / 4) + lane], sGam);
@@ -878,8 +888,8 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
         if (n + 1 < n1) {
 #pragma unroll
             for (int i = 0; i < PFO; ++i) {
-                lds_copy4(&W4[(cid + 1) * OPF4 + i * 256 + tid], &sW[i * 256 + wv]);
-                if (QLDS) lds_copy4(&Q4[(cid + 1) * OPF4 + i * 256 + tid], &sQ[i * 256 + wv]);
+                lds_copy4(&W4[(cid + 1) * OPF4 + i * NTH + tid], &sW[i * NTH + wv]);
+                if (QLDS) lds_copy4(&Q4[(cid + 1) * OPF4 + i * NTH + tid], &sQ[i * NTH + wv]);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -944,16 +954,16 @@ __global__ __launch_bounds__(256, 1) void chunk_inter_kernel(ChunkParams p, int 
 // P_j S_in(j) + Q_j for j = 0 .. NSEG - 2.  One workgroup per (b, hv, 64 value
 // columns); S in MFMA accumulators, P_j read as A-operand fragments
 // (lane (g, r): row r of a 16-row tile, columns 4g .. 4g + 3) from L2.
-template <int K>
-__global__ __launch_bounds__(256, 1) void chunk_chain_kernel(ChunkParams p) {
+template <int K, int NWV>
+__global__ __launch_bounds__(64 * NWV, 1) void chunk_chain_kernel(ChunkParams p) {
     constexpr int NKT = K / 16;
-    const int V = p.V, nvv = V / 64;
+    const int V = p.V, nvv = V / (16 * NWV);
     int bh, vs;
     inter_block(blockIdx.x, p.B * p.HV, nvv, &bh, &vs);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lr = lane & 15, lg = lane >> 4;
-    const int col = 16 * (vs * 4 + wave) + lr;
+    const int col = 16 * (vs * NWV + wave) + lr;
 
     const float *S0 = p.state + (size_t)bh * K * V;
     float *slot0 = p.ws_qseg + (size_t)bh * p.NSEG * K * V;
@@ -1031,11 +1041,11 @@ __global__ __launch_bounds__(256, 1) void chunk_chain_kernel(ChunkParams p) {
 // every element read and written by the same thread.
 template <int K, bool INPLACE>
 __global__ __launch_bounds__(256) void chunk_states_kernel(ChunkParams p) {
-    __shared__ float sA[C][K]; // k rows, then the decayed keys k_t exp(G_m - G_{t+1})
-    __shared__ float sB[C][K]; // g rows, then v_new rows (64 value columns)
+    constexpr int KB = K > 64 ? K : 64;
+    __shared__ float sA[C][K];  // k rows, then the decayed keys k_t exp(G_m - G_{t+1})
+    __shared__ float sB[C][KB]; // g rows, then v_new rows (64 value columns; those past V are zero)
     __shared__ float sGam[K];
-    static_assert(K >= 64, "sB holds 64 value columns");
-    const int cc = p.st_cc, nvs = p.V / 64;
+    const int cc = p.st_cc, nvs = (p.V + 63) / 64;
     int blk = blockIdx.x;
     const int vs = blk % nvs;
     blk /= nvs;
@@ -1072,9 +1082,11 @@ __global__ __launch_bounds__(256) void chunk_states_kernel(ChunkParams p) {
     }
     __syncthreads();
     const float *vn = p.ws_vn + ((size_t)bh * p.T + t0) * p.V + vs * 64;
-    for (int i = tid; i < m * 64; i += 256) sB[i / 64][i % 64] = vn[(size_t)(i / 64) * p.V + i % 64];
+    const int vw = min(64, p.V - vs * 64); // value columns of this slice
+    for (int i = tid; i < m * 64; i += 256) sB[i / 64][i % 64] = (i % 64) < vw ? vn[(size_t)(i / 64) * p.V + i % 64] : 0.f;
     __syncthreads();
     const int v = tid & 63, cg = tid >> 6, col = vs * 64 + v;
+    if (v >= vw) return; // (no barrier below)
     const size_t slot0 = (size_t)bh * p.st_chunks + (t0 + cc - 1) / cc; // j0(n)
     const float *Sn = p.ws_sn + slot0 * K * p.V;
     float *So = p.ws_sn + ((size_t)bh * p.st_chunks + j) * K * p.V;
@@ -1091,53 +1103,54 @@ __global__ __launch_bounds__(256) void chunk_states_kernel(ChunkParams p) {
 // 16 segment summaries, 32 chain, 64 output pass.
 template <int K, int V>
 hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
+    constexpr int NWV = inter_nwv(K, V), VSW = 16 * NWV; // waves and value columns per sequential workgroup
+    const dim3 blk(64 * NWV);
+    const int seqs = p.B * p.HV;
     if (phases & 112) {
-        const int seqs = p.B * p.HV;
         if ((phases & 16) && p.NSEG > 1)
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal>), dim3(seqs * (p.NSEG - 1) * ((V + K) / 64)),
-                               dim3(256), 0, s, p, p.NSEG - 1);
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal, NWV>), dim3(seqs * (p.NSEG - 1) * ((V + K) / VSW)),
+                               blk, 0, s, p, p.NSEG - 1);
         if ((phases & 32) && p.NSEG > 1)
-            hipLaunchKernelGGL((chunk_chain_kernel<K>), dim3(seqs * (V / 64)), dim3(256), 0, s, p);
+            hipLaunchKernelGGL((chunk_chain_kernel<K, NWV>), dim3(seqs * (V / VSW)), blk, 0, s, p);
         if (phases & 64)
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOut>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0, s,
-                               p, p.NSEG);
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOut, NWV>), dim3(seqs * p.NSEG * (V / VSW)), blk, 0, s, p,
+                               p.NSEG);
         return hipGetLastError();
     }
     if (phases & 1) {
         const int nchunks = p.B * p.HV * p.NC;
         if (p.ws_akk) {
-            if constexpr (K <= 128)
+            if constexpr (K >= 64 && K <= 128)
                 hipLaunchKernelGGL((chunk_intra_kernel<K, V, true>), dim3(nchunks), dim3(512), 0, s, p);
             else
-                return hipErrorInvalidValue; // the chunked backward takes K <= 128
+                return hipErrorInvalidValue; // the chunked backward takes K in {64, 128}
         } else
             hipLaunchKernelGGL((chunk_intra_kernel<K, V, false>), dim3(nchunks), dim3(512), 0, s, p);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     if (phases & 14) {
-        const int seqs = p.B * p.HV;
         if (p.NSEG > 1) {
             // the training forward (phases & 4) also takes the last segment's P, which
             // the backward's reverse chain uses
             const int nl = (phases & 4) ? p.NSEG : p.NSEG - 1;
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal>), dim3(seqs * nl * ((V + K) / 64)), dim3(256), 0,
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal, NWV>), dim3(seqs * nl * ((V + K) / VSW)), blk, 0,
                                s, p, nl);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((chunk_chain_kernel<K>), dim3(seqs * (V / 64)), dim3(256), 0, s, p);
+            hipLaunchKernelGGL((chunk_chain_kernel<K, NWV>), dim3(seqs * (V / VSW)), blk, 0, s, p);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
+        const dim3 grid(seqs * p.NSEG * (V / VSW));
         if (phases & 8)
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOutStates>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0,
-                               s, p, p.NSEG);
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOutStates, NWV>), grid, blk, 0, s, p, p.NSEG);
         else if (phases & 2)
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOut>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0, s,
-                               p, p.NSEG);
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOut, NWV>), grid, blk, 0, s, p, p.NSEG);
+        else if constexpr (NWV == 4) // the backward's states pass (its shapes take four waves)
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterStates, NWV>), grid, blk, 0, s, p, p.NSEG);
         else
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterStates>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0,
-                               s, p, p.NSEG);
+            return hipErrorInvalidValue;
         return hipGetLastError();
     }
     return hipSuccess;
@@ -1146,19 +1159,21 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
 }  // namespace
 
 bool chunk_supported(int K, int V) {
-    return ((K == 64 || K == 128) && (V == 64 || V == 128 || V == 256)) || (K == 256 && (V == 128 || V == 256));
+    return (K == 32 && (V == 32 || V == 64)) || (K == 64 && (V == 64 || V == 96 || V == 128 || V == 256)) ||
+           (K == 128 && (V == 64 || V == 128 || V == 192 || V == 256)) || (K == 256 && (V == 128 || V == 256));
 }
 
 bool chunk_bwd_supported(int K, int V) { return (K == 64 || K == 128) && (V == 64 || V == 128 || V == 256); }
 
 template <int K>
 hipError_t launch_chunk_states_t(const ChunkParams &p, hipStream_t s) {
-    const int64_t grid = (int64_t)p.B * p.HV * p.st_chunks * (p.V / 64);
+    const int nvs = (p.V + 63) / 64;
+    const int64_t grid = (int64_t)p.B * p.HV * p.st_chunks * nvs;
     if (grid <= 0) return hipSuccess;
     hipLaunchKernelGGL((chunk_states_kernel<K, false>), dim3((unsigned)grid), dim3(256), 0, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || C % p.st_cc == 0) return e; // every j0(n) starts its chunk: nothing in place
-    hipLaunchKernelGGL((chunk_states_kernel<K, true>), dim3((unsigned)(p.B * p.HV * p.NC * (p.V / 64))), dim3(256),
+    hipLaunchKernelGGL((chunk_states_kernel<K, true>), dim3((unsigned)(p.B * p.HV * p.NC * nvs)), dim3(256),
                        0, s, p);
     return hipGetLastError();
 }
@@ -1168,11 +1183,16 @@ hipError_t launch_chunk_states(const ChunkParams &p, hipStream_t s) {
     if (p.K == 256) return launch_chunk_states_t<256>(p, s);
     if (p.K == 128) return launch_chunk_states_t<128>(p, s);
     if (p.K == 64) return launch_chunk_states_t<64>(p, s);
+    if (p.K == 32) return launch_chunk_states_t<32>(p, s);
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_chunk(const ChunkParams &p, hipStream_t s, int phases) {
     if (p.K == 128 && p.V == 128) return launch_chunk_t<128, 128>(p, s, phases);
+    if (p.K == 128 && p.V == 192) return launch_chunk_t<128, 192>(p, s, phases);
+    if (p.K == 64 && p.V == 96) return launch_chunk_t<64, 96>(p, s, phases);
+    if (p.K == 32 && p.V == 32) return launch_chunk_t<32, 32>(p, s, phases);
+    if (p.K == 32 && p.V == 64) return launch_chunk_t<32, 64>(p, s, phases);
     if (p.K == 256 && p.V == 256) return launch_chunk_t<256, 256>(p, s, phases);
     if (p.K == 256 && p.V == 128) return launch_chunk_t<256, 128>(p, s, phases);
     if (p.K == 128 && p.V == 256) return launch_chunk_t<128, 256>(p, s, phases);
@@ -1207,8 +1227,8 @@ struct Segments {
     int nseg, segl;
 };
 
-Segments inter_segments(int64_t B, int64_t HV, int64_t V, int64_t NC) {
-    const int64_t w = B * HV * (V / 64);
+Segments inter_segments(int64_t B, int64_t HV, int64_t K, int64_t V, int64_t NC) {
+    const int64_t w = (K > 0 && V > 0) ? B * HV * (V / (16 * inter_nwv((int)K, (int)V))) : 0;
     if (w <= 0 || NC <= 0) return {1, (int)NC}; // (K, V) outside the chunk kernels, or no tokens
     int64_t n = kInterWorkgroups / w;
     if (n > NC / kMinSegmentChunks) n = NC / kMinSegmentChunks;
@@ -1221,7 +1241,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 WsLayout ws_layout(int64_t seqs, int64_t NC, int64_t K, int64_t V) {
     const int64_t nchunks = seqs * NC;
-    const int64_t nseg = inter_segments(seqs, 1, V, NC).nseg;
+    const int64_t nseg = inter_segments(seqs, 1, K, V, NC).nseg;
     const int64_t np = nseg > 1 ? seqs * nseg : 0, nq = np;
     WsLayout L;
     size_t off = 0;
@@ -1289,7 +1309,7 @@ gdn2_status chunk_setup(const gdn2_chunk_args *a, const char *who, bool need_out
     p->svb = a->stride_vw_b; p->svh = a->stride_vw_h; p->svt = a->stride_vw_t;
     p->sob = a->stride_o_b; p->soh = a->stride_o_h; p->sot = a->stride_o_t;
     p->scale = (float)a->scale;
-    const Segments sg = inter_segments(p->B * p->HV, 1, p->V, p->NC);
+    const Segments sg = inter_segments(p->B * p->HV, 1, p->K, p->V, p->NC);
     p->NSEG = sg.nseg;
     p->SEGL = sg.segl;
     return GDN2_OK;
@@ -1297,7 +1317,7 @@ gdn2_status chunk_setup(const gdn2_chunk_args *a, const char *who, bool need_out
 
 size_t chunk_fwd_ws_bytes(const gdn2_chunk_args *a) { return ws_layout(a).total; }
 
-int chunk_segments(int64_t seqs, int64_t V, int64_t NC) { return inter_segments(seqs, 1, V, NC).nseg; }
+int chunk_segments(int64_t seqs, int64_t K, int64_t V, int64_t NC) { return inter_segments(seqs, 1, K, V, NC).nseg; }
 
 void chunk_bind_ws(const gdn2_chunk_args *a, char *ws, ChunkParams *p) {
     const WsLayout L = ws_layout(a);
@@ -1349,8 +1369,9 @@ extern "C" gdn2_status gdn2_chunk_inter_f32(const gdn2_chunk_args *a, gdn2_strea
 }
 
 extern "C" int64_t gdn2_chunk_segments(const gdn2_chunk_args *a) {
-    if (!a || a->batch <= 0 || a->num_v_heads <= 0 || a->seq_len <= 0 || a->head_v_dim <= 0) return 0;
-    return chunk_segments(a->batch * a->num_v_heads, a->head_v_dim, (a->seq_len + kChunk - 1) / kChunk);
+    if (!a || a->batch <= 0 || a->num_v_heads <= 0 || a->seq_len <= 0 || a->head_dim <= 0 || a->head_v_dim <= 0)
+        return 0;
+    return chunk_segments(a->batch * a->num_v_heads, a->head_dim, a->head_v_dim, (a->seq_len + kChunk - 1) / kChunk);
 }
 
 extern "C" gdn2_status gdn2_chunk_inter_pass_f32(const gdn2_chunk_args *a, int pass, gdn2_stream_t stream) {

@@ -989,7 +989,7 @@ BwdLayout bwd_layout(const gdn2_chunk_args *a) {
     L.kgrad = take(a->num_v_heads != a->num_heads ? 4 * Cs * K : 0);
     { // segment buffers of the reverse recurrence, per sequence (not per chunk)
         const size_t seqs = (size_t)a->batch * a->num_v_heads, NC = (a->seq_len + kChunk - 1) / kChunk;
-        const size_t nseg = (size_t)chunk_segments(seqs, V, NC);
+        const size_t nseg = (size_t)chunk_segments(seqs, K, V, NC);
         const size_t ns = nseg > 1 ? seqs * nseg : 0;
         L.rseg = off; off = align256(off + f * ns * K * V);
     }

@@ -11,6 +11,11 @@ namespace gdn2 {
 constexpr int C = kChunk;   // chunk length of the kernels
 constexpr int NT = C / 16;  // 16-row tiles per chunk
 
+// Waves per workgroup of the sequential kernels (each wave owns 16 value
+// columns): four when V and K are multiples of 64, else two (V = 32, 96 and
+// K = 32, whose segment transitions P have 32 columns).
+constexpr int inter_nwv(int K, int V) { return (V % 64 == 0 && K % 64 == 0) ? 4 : 2; }
+
 // Rows [0, valid) of a row-strided f32 matrix (row stride rs, rowlen
 // elements used per row) as a buffer resource.  The hardware's range check
 // returns 0 for every load past the last valid row, which is the zero padding
@@ -120,7 +125,7 @@ __device__ __forceinline__ void inter_block(int blk, int nseq, int nvs, int *bh,
 gdn2_status chunk_setup(const gdn2_chunk_args *a, const char *who, bool need_out, ChunkParams *p);
 size_t chunk_fwd_ws_bytes(const gdn2_chunk_args *a);
 // Segments per sequence of the sequential kernels (1 = unsegmented).
-int chunk_segments(int64_t seqs, int64_t V, int64_t NC);
+int chunk_segments(int64_t seqs, int64_t K, int64_t V, int64_t NC);
 void chunk_bind_ws(const gdn2_chunk_args *a, char *ws, ChunkParams *p);
 
 }  // namespace gdn2

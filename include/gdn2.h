@@ -132,9 +132,11 @@ GDN2_API gdn2_status gdn2_recurrent_fwd_f32(const gdn2_recurrent_args *args, gdn
  * the result does not depend on it beyond rounding, as in the reference.
  * workspace: device memory of at least gdn2_chunk_workspace_bytes(args)
  * bytes, 256-byte aligned.
- * Limits (else GDN2_NOT_APPLICABLE): K in {64, 128} with V in {64, 128, 256},
- * or K = 256 with V in {128, 256} (the reference's K, V <= 256 at its head
- * shapes); q, k, b rows 16-byte aligned (strides multiples of 4 elements); token
+ * Limits (else GDN2_NOT_APPLICABLE): (K, V) with K = 32 and V in {32, 64},
+ * K = 64 and V in {64, 96, 128, 256}, K = 128 and V in {64, 128, 192, 256},
+ * or K = 256 and V in {128, 256} (the reference takes K, V <= 256; these are
+ * its own benchmark and test head shapes and expand_v 0.5, 1, 1.5, 2, 4);
+ * q, k, b rows 16-byte aligned (strides multiples of 4 elements); token
  * strides at least the row length (stride_qk_t >= K, stride_vw_t >= V) and
  * 63 token strides plus a row under 2 GiB.
  * ---------------------------------------------------------------------- */
@@ -266,7 +268,8 @@ GDN2_API gdn2_status gdn2_stream_copy_f32(float *dst, const float *src, int64_t 
  * It recomputes the forward's per-chunk quantities (the reference's
  * FusedBackwardInputs) in its own workspace of
  * gdn2_chunk_bwd_workspace_bytes(args) bytes, 256-byte aligned.
- * Limits as gdn2_chunk_fwd_f32 (else GDN2_NOT_APPLICABLE).
+ * Limits (else GDN2_NOT_APPLICABLE): those of gdn2_chunk_fwd_f32, with K in
+ * {64, 128} and V in {64, 128, 256} (other heads: gdn2_recurrent_bwd_f32).
  * ---------------------------------------------------------------------- */
 typedef struct gdn2_chunk_bwd_args {
     gdn2_chunk_args fwd;

@@ -38,6 +38,15 @@ CASES = [
     (1, 2, 2, 100, 128, 64, (-0.3, -0.02), 1.0, 0.5),     # K = 128, V = 64, ragged
     (1, 2, 2, 96, 128, 64, (-31.0, -0.05), 1.0, 0.5),     # V = 64 with spans beyond the f32 exp range
     (1, 1, 2, 130, 64, 256, (-31.0, -0.05), 2.0, 0.5),    # K = 64, V = 256, GVA, neg-eig, the exact diagonal path
+    # head shapes of the reference's own benchmarks (tests/bench_cuda.rs:71-72: K = V = 32;
+    # tests/bit_exact.rs:224-235: K = 64 with expand_v 1.5, V = 96) and expand_v 1.5 at K = 128
+    (2, 2, 2, 150, 32, 32, (-0.3, -0.02), 1.0, 0.5),      # K = V = 32, ragged: two-wave sequential workgroups
+    (1, 2, 4, 200, 32, 64, (-0.4, -0.01), 2.0, 0.5),      # K = 32, V = 64, GVA, negative eigenvalues
+    (1, 2, 2, 130, 32, 32, (-31.0, -0.05), 1.0, 0.5),     # K = 32 with the exact diagonal path
+    (2, 2, 2, 140, 64, 96, (-0.3, -0.02), 1.0, 0.5),      # K = 64, V = 96: three 32-column slices
+    (1, 1, 2, 97, 64, 96, (-31.0, -0.05), 2.0, 0.5),      # V = 96, GVA, neg-eig, the exact diagonal path
+    (1, 2, 2, 150, 128, 192, (-0.3, -0.02), 1.0, 0.5),    # K = 128, V = 192: three 64-column slices
+    (1, 1, 2, 100, 128, 192, (-31.0, -0.05), 2.0, 0.5),   # V = 192, GVA, neg-eig, spans beyond the f32 exp range
 ]
 
 
@@ -82,6 +91,9 @@ SEG_CASES = [
     (1, 1, 2, 2530, 256, 256, (-0.003, -0.0005), 1.0, 1.0),  # K = V = 256, segmented
     (1, 2, 2, 2560, 128, 128, (-0.001, 0.0), 0.0, 1.0),      # b = 0: P = diag(exp(G)) ~ 0.3-1, S0 carried whole
     (1, 1, 1, 4100, 128, 256, (-5.0, -0.5), 1.0, 1.0),       # strong decay, V = 2K
+    (1, 2, 2, 2530, 32, 32, (-0.003, -0.0005), 1.0, 1.0),    # K = V = 32: 32-column slices of P
+    (1, 1, 2, 2600, 64, 96, (-0.002, 0.0), 2.0, 1.0),        # V = 96, GVA, negative eigenvalues
+    (1, 1, 1, 2400, 128, 192, (-0.003, -0.0005), 1.0, 1.0),  # V = 192
 ]
 
 
@@ -250,6 +262,8 @@ STATE_CASES = [
     (1, 1, 1, 96, 64, 64, 48),       # chunk_size 48: the last 64-token chunk starts no caller chunk
     (1, 2, 2, 2112, 128, 128, 33),   # chunk_size 33 with the segmented inter
     (1, 1, 2, 180, 256, 128, 36),    # K = 256, chunk_size 36
+    (1, 2, 2, 192, 64, 96, 48),      # V = 96: the states of a 32-column slice
+    (1, 1, 1, 160, 32, 32, 32),      # K = V = 32
 ]
 
 

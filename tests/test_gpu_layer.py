@@ -56,6 +56,15 @@ CASES = {
                       1, 150),
     # at most 256 rows: the rank-256 up-projections take the one-launch MFMA kernel
     "k256_few_rows": (dict(hidden_size=512, num_heads=2, head_dim=256, mode="chunk"), 2, 100),
+    # the reference's CPU benchmark model (tests/bit_exact.rs:224-235: D 256, 4 heads, K 64,
+    # expand_v 1.5, both modes): V = 96 on the chunk kernels' three 32-column slices
+    "bench_v96_chunk": (dict(hidden_size=256, num_heads=4, head_dim=64, expand_v=1.5, mode="chunk"), 2, 300),
+    "bench_v96_recurrent": (dict(hidden_size=256, num_heads=4, head_dim=64, expand_v=1.5,
+                                 mode="fused_recurrent"), 1, 256),
+    # the reference's "tiny" and "small" CUDA benchmark layers (tests/bench_cuda.rs:71-72: K = V = 32)
+    "bench_tiny": (dict(hidden_size=64, num_heads=2, head_dim=32, mode="chunk"), 1, 200),
+    "bench_small": (dict(hidden_size=128, num_heads=4, head_dim=32, mode="chunk"), 2, 256),
+    "k128_v192": (dict(hidden_size=512, num_heads=2, head_dim=128, expand_v=1.5, mode="chunk"), 1, 200),
 }
 
 
