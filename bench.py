@@ -1200,7 +1200,35 @@ def bench_backward(torch, G, args, dev):
     res = {"workload": f"chunked backward (gradients of q, k, g, b, v, w, S0), B={B} T={T} H=16 K=V=128",
            "ms_per_step": ms, "tokens_per_s": B * T / (ms / 1e3), "workspace_bytes": need,
            "kernel": "gdn2_chunk_bwd_f32"}
-    del P, q, k, g, b, v, w, S0, dO, grads, ws
+
+    # the training forward (output + final state, keeping the backward's inputs
+    # in the workspace), then the backward from them
+    St = torch.zeros_like(S0)
+    out = torch.empty((B, T, H, V), device=dev).permute(0, 2, 1, 3)
+    at = CA.ChunkBwdArgs(chunk_args(q, k, v, g, b, w, St, out, K ** -0.5, 64), _p(dO), None,
+                         *(_p(t) for t in grads), _p(ws), need)
+    pt = ctypes.byref(at)
+
+    def timed(fn, n):
+        settle(torch, fn, args.settle_ms)
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    fwd_ms = timed(lambda: CA.check(L.gdn2_chunk_fwd_train_f32(pt, stream)), args.steps)
+    saved_ms = timed(lambda: CA.check(L.gdn2_chunk_bwd_saved_f32(pt, stream)), args.steps)
+    res["from_saved_forward"] = {
+        "kernel": "gdn2_chunk_bwd_saved_f32", "ms_per_step": saved_ms, "tokens_per_s": B * T / (saved_ms / 1e3),
+        "training_forward": {"kernel": "gdn2_chunk_fwd_train_f32", "ms_per_step": fwd_ms,
+                             "tokens_per_s": B * T / (fwd_ms / 1e3)},
+        "what": "the backward reading the training forward's per-chunk quantities instead of recomputing them"}
+    del P, q, k, g, b, v, w, S0, dO, grads, ws, St, out
     torch.cuda.empty_cache()
     return res
 

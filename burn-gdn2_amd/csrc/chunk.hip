@@ -238,7 +238,8 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
                 // scale q exp(G_r): the sequential kernel's A operand, fragment (pt, m0 + m)
                 if (mat == 0) {
                     const floatx4 qg = a * exp2v(gb) * p.scale;
-                    if (!TRAIN) st_stream(QGf + (pt * NKT + m0 + m) * 64 + lane, qg); // the backward takes QG^T only
+                    // (the backward takes QG^T only; its training forward, fwd_out, both)
+                    if (!TRAIN || p.fwd_out) st_stream(QGf + (pt * NKT + m0 + m) * 64 + lane, qg);
                     if (TRAIN) // (q exp(G))^T fragment (m0 + m, pt)
                         st_stream(reinterpret_cast<floatx4 *>(p.ws_qgt) + cid * (C * K / 4) +
                                       ((m0 + m) * NT + pt) * 64 + lane,
@@ -277,8 +278,9 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
         // through a scalar before __builtin_bit_cast: the cast of a vector
         // element lvalue reads the vector's first element.)  The training variant, whose
         // registers are fuller, reads the row operand from memory (keeping araw
-        // live here would spill 72 bytes per lane).
-        if constexpr (!TRAIN) {
+        // live here would spill 72 bytes per lane); its arithmetic and order are
+        // the same, so that both variants give bit-identical scores.
+        {
 #pragma unroll
             for (int pi = 0; pi < 2; ++pi) {
                 const int pt = pi ? (NT - 1 - half) : half;
@@ -315,16 +317,26 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
                             const int c0 = 16 * (m0 + m) + 4 * cg + 2 * jh;
                             const float2 gs = *reinterpret_cast<const float2 *>(&sG[srow][c0]);
                             const float2 ks = *reinterpret_cast<const float2 *>(&sK[srow][c0]);
-                            const float o0 = araw[pi][m][2 * jh], o1 = araw[pi][m][2 * jh + 1]; // scalars (see above)
+                            float o0 = 0.f, o1 = 0.f;
+                            if constexpr (!TRAIN) {
+                                o0 = araw[pi][m][2 * jh]; // scalars (see above)
+                                o1 = araw[pi][m][2 * jh + 1];
+                            }
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
                                 const int r = 4 * lg + i;
                                 const int rrow = 16 * pt + r;
                                 const float2 gr = *reinterpret_cast<const float2 *>(&sG[rrow][c0]);
-                                float x0 = __builtin_bit_cast(
-                                    float, __builtin_amdgcn_ds_bpermute(4 * (16 * cg + r), __builtin_bit_cast(int, o0)));
-                                float x1 = __builtin_bit_cast(
-                                    float, __builtin_amdgcn_ds_bpermute(4 * (16 * cg + r), __builtin_bit_cast(int, o1)));
+                                float x0, x1;
+                                if constexpr (TRAIN) { // row rrow of q or b, channels c0, c0 + 1
+                                    x0 = bld1(mat == 0 ? Rq : Rb, lg_q + (16 * pt + i) * rq + c0);
+                                    x1 = bld1(mat == 0 ? Rq : Rb, lg_q + (16 * pt + i) * rq + c0 + 1);
+                                } else {
+                                    x0 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                                       4 * (16 * cg + r), __builtin_bit_cast(int, o0)));
+                                    x1 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                                       4 * (16 * cg + r), __builtin_bit_cast(int, o1)));
+                                }
                                 if (mat == 1) {
                                     const float2 kr = *reinterpret_cast<const float2 *>(&sK[rrow][c0]);
                                     x0 *= kr.x;
@@ -342,39 +354,6 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
 #pragma unroll
                 for (int q = 0; q < NT; ++q)
                     if (q == pt) acc[pi][q] += dacc;
-            }
-        }
-        // The training variant: one masked channel at a time, the row operand
-        // read again from memory (row 4 lg + i of the tile).
-        if constexpr (TRAIN) {
-#pragma unroll
-            for (int pi = 0; pi < 2; ++pi) {
-                const int pt = pi ? (NT - 1 - half) : half;
-#pragma unroll
-                for (int q = 0; q < NT; ++q) {
-                    if (q == pt && (pi == 1 || q < NT / 2)) {
-                        for (int wd = kh * (K / 64); wd < (kh + 1) * (K / 64); ++wd) {
-                            uint32_t mw = sMask[pt][wd];
-                            while (mw) {
-                                const int c = wd * 32 + __builtin_ctz(mw);
-                                mw &= mw - 1u;
-                                const int srow = 16 * pt + lr;
-                                const float ks = sK[srow][c];
-                                const float gs = sG[srow][c];
-#pragma unroll
-                                for (int i = 0; i < 4; ++i) {
-                                    const int r = 4 * lg + i;
-                                    const int rrow = 16 * pt + r;
-                                    const float xg = bld1(mat == 0 ? Rq : Rb, lg_q + (16 * pt + i) * rq + c);
-                                    const float xr = (mat == 0) ? xg : xg * sK[rrow][c];
-                                    const float e =
-                                        (mat == 0 ? (r >= lr) : (r > lr)) ? fast_exp2(sG[rrow][c] - gs) : 0.f;
-                                    acc[pi][q][i] += xr * ks * e;
-                                }
-                            }
-                        }
-                    }
-                }
             }
         }
         // Row tile 0's value-column right-hand sides: requested now, so that
@@ -478,14 +457,17 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
 
     // A_qk -> the sequential kernel as A-operand fragments (mt, qt), the lower
     // block triangle qt <= mt only: chunk-inter reads no other tile (the
-    // backward takes A_qk^T only).
+    // backward takes A_qk^T only; its training forward, fwd_out, both).
     {
         floatx4 *Af = reinterpret_cast<floatx4 *>(p.ws_aqk) + cid * (C * C / 4);
+        if (!TRAIN || p.fwd_out) {
 #pragma unroll
-        for (int j = 0; j < (TRAIN ? 0 : NT * NT / NW); ++j) {
-            const int f = wave + NW * j, mt = f / NT, qt = f % NT;
-            if (qt > mt) continue; // wave-uniform
-            st_stream(Af + f * 64 + lane, *reinterpret_cast<const floatx4 *>(&sAqk[16 * mt + lr][16 * qt + 4 * lg]));
+            for (int j = 0; j < NT * NT / NW; ++j) {
+                const int f = wave + NW * j, mt = f / NT, qt = f % NT;
+                if (qt > mt) continue; // wave-uniform
+                st_stream(Af + f * 64 + lane,
+                          *reinterpret_cast<const floatx4 *>(&sAqk[16 * mt + lr][16 * qt + 4 * lg]));
+            }
         }
         if (TRAIN) {
             // A_qk^T fragments (st, rt): lane (g, r) holds A_qk[16 rt + 4 g + j][16 st + r]
@@ -619,17 +601,21 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
 // the backward: no output and no final state; instead the state entering
 // every chunk (ws_sn) and every chunk's v_new (ws_vn), both as accumulator
 // fragments in (value tile, row tile) order, so that each 16-column slice is
-// one contiguous block) or kInterOutStates
-// (pass 3 with both, the reference's fused_chunk_forward tuple).
+// one contiguous block), kInterOutStates (pass 3 with both, the reference's
+// fused_chunk_forward tuple) or kInterOutTrain (pass 3 with the output and
+// the final state, and the per-chunk states and v_new in the backward's
+// fragment layout: the training forward whose quantities the backward keeps).
 // ---------------------------------------------------------------------------
-constexpr int kInterOut = 0, kInterLocal = 1, kInterStates = 2, kInterOutStates = 3;
+constexpr int kInterOut = 0, kInterLocal = 1, kInterStates = 2, kInterOutStates = 3, kInterOutTrain = 4;
 
 // NWV waves per workgroup (NWV = 4: 64 value columns; NWV = 2: 32, for value
 // dimensions that are not a multiple of 64 and for K = 32).
 template <int K, int MODE, int NWV>
 __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p, int nseg_launch) {
-    constexpr bool OUT = MODE == kInterOut || MODE == kInterOutStates, LOCAL = MODE == kInterLocal;
-    constexpr bool STATES = MODE == kInterStates || MODE == kInterOutStates;
+    constexpr bool OUT = MODE == kInterOut || MODE == kInterOutStates || MODE == kInterOutTrain;
+    constexpr bool LOCAL = MODE == kInterLocal;
+    constexpr bool STATES = MODE == kInterStates || MODE == kInterOutStates || MODE == kInterOutTrain;
+    constexpr bool FRAG = MODE == kInterStates || MODE == kInterOutTrain; // the backward's layouts
     constexpr int NTH = 64 * NWV;  // threads per workgroup
     constexpr int VSW = 16 * NWV;  // value columns per workgroup
     constexpr int NKT = K / 16;
@@ -801,7 +787,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p,
             if (keep) {
 #pragma unroll
                 for (int kb = 0; kb < NKT; ++kb)
-                    if (MODE == kInterStates) // the backward's fragment layout: tile (value tile, key tile)
+                    if (FRAG) // the backward's fragment layout: tile (value tile, key tile)
                         reinterpret_cast<floatx4 *>(Sn)[(vt * NKT + kb) * 64 + lane] = S[kb];
                     else
 #pragma unroll
@@ -875,7 +861,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p,
                 float *Vn = p.ws_vn + cid * C * V;
 #pragma unroll
                 for (int mt = 0; mt < NT; ++mt)
-                    if (MODE == kInterStates) // tile (value tile, time tile)
+                    if (FRAG) // tile (value tile, time tile)
                         reinterpret_cast<floatx4 *>(Vn)[(vt * NT + mt) * 64 + lane] = X1[mt];
                     else
 #pragma unroll
@@ -1097,7 +1083,8 @@ __global__ __launch_bounds__(256) void chunk_states_kernel(ChunkParams p) {
     }
 }
 
-// phases: 1 intra; 2 inter with the output, 4 training (every segment's P), 8
+// phases: 1 intra; 2 inter with the output, 4 training (every segment's P and
+// the backward's per-chunk states and v_new; with 2 also the output), 8
 // output plus v_new and the per-chunk states (2, 4, 8 run every inter pass the
 // shape needs); one pass of the segmented inter alone (phase diagnostics):
 // 16 segment summaries, 32 chain, 64 output pass.
@@ -1145,7 +1132,12 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
         const dim3 grid(seqs * p.NSEG * (V / VSW));
         if (phases & 8)
             hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOutStates, NWV>), grid, blk, 0, s, p, p.NSEG);
-        else if (phases & 2)
+        else if ((phases & 6) == 6) {
+            if constexpr (NWV == 4) // the backward's shapes
+                hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOutTrain, NWV>), grid, blk, 0, s, p, p.NSEG);
+            else
+                return hipErrorInvalidValue;
+        } else if (phases & 2)
             hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOut, NWV>), grid, blk, 0, s, p, p.NSEG);
         else if constexpr (NWV == 4) // the backward's states pass (its shapes take four waves)
             hipLaunchKernelGGL((chunk_inter_kernel<K, kInterStates, NWV>), grid, blk, 0, s, p, p.NSEG);

@@ -1011,29 +1011,38 @@ extern "C" size_t gdn2_chunk_bwd_workspace_bytes(const gdn2_chunk_bwd_args *a) {
     return bwd_layout(&a->fwd).total;
 }
 
-// fused_chunk_backward (src/kernel/chunk_adjoint_cube.rs:464-707).
-extern "C" gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *a, gdn2_stream_t stream) {
-    if (!a) return fail(GDN2_EINVAL, "gdn2_chunk_bwd_f32: null args");
+namespace {
+
+// The three entry points below share this: checks, the workspace binding, and
+// by `what` the launches -- 1 the training forward (output, final state and the
+// backward's inputs), 2 the backward from those inputs, 3 both forward
+// quantities (recomputed, without the output) and the backward.
+gdn2_status chunk_bwd_call(const gdn2_chunk_bwd_args *a, gdn2_stream_t stream, int what, const char *who) {
+    const std::string w = std::string(who) + ": ";
+    if (!a) return fail(GDN2_EINVAL, w + "null args");
     BwdParams bp{};
     if (!chunk_bwd_supported((int)a->fwd.head_dim, (int)a->fwd.head_v_dim))
-        return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_bwd_f32: (K, V) outside the chunked backward's instances");
-    gdn2_status st = chunk_setup(&a->fwd, "gdn2_chunk_bwd_f32", false, &bp.f);
+        return fail(GDN2_NOT_APPLICABLE, w + "(K, V) outside the chunked backward's instances");
+    gdn2_status st = chunk_setup(&a->fwd, who, what == 1, &bp.f);
     if (st != GDN2_OK) return st;
-    if (!a->d_out || !a->dq || !a->dk || !a->dg || !a->db || !a->dv || !a->dw || !a->d_state0)
-        return fail(GDN2_EINVAL, "gdn2_chunk_bwd_f32: null gradient pointer");
     const gdn2_chunk_args &f = a->fwd;
-    if (!aligned16b(a->d_out) || (f.stride_o_b % 4) || (f.stride_o_h % 4) || (f.stride_o_t % 4) ||
-        f.stride_o_t < f.head_v_dim || ((kChunk - 1) * f.stride_o_t + f.head_v_dim) * 4 >= (int64_t(1) << 31))
-        return fail(GDN2_NOT_APPLICABLE, "gdn2_chunk_bwd_f32: d_out needs 16-byte aligned rows within the row loads' range");
+    if (what != 1) {
+        if (!a->d_out || !a->dq || !a->dk || !a->dg || !a->db || !a->dv || !a->dw || !a->d_state0)
+            return fail(GDN2_EINVAL, w + "null gradient pointer");
+        if (!aligned16b(a->d_out) || (f.stride_o_b % 4) || (f.stride_o_h % 4) || (f.stride_o_t % 4) ||
+            f.stride_o_t < f.head_v_dim || ((kChunk - 1) * f.stride_o_t + f.head_v_dim) * 4 >= (int64_t(1) << 31))
+            return fail(GDN2_NOT_APPLICABLE, w + "d_out needs 16-byte aligned rows within the row loads' range");
+    }
     hipStream_t s = (hipStream_t)stream;
     const size_t sbytes = sizeof(float) * (size_t)f.batch * f.num_v_heads * f.head_dim * f.head_v_dim;
     if (f.seq_len == 0) { // no tokens: dS0 = d_state_out (or 0), by the fill kernel (a copy when a row is given)
-        GDN2_HIP_CHECK(launch_fill_rows(a->d_state0, 0, a->d_state_out, 1, (int64_t)(sbytes / sizeof(float)), s));
+        if (what != 1)
+            GDN2_HIP_CHECK(launch_fill_rows(a->d_state0, 0, a->d_state_out, 1, (int64_t)(sbytes / sizeof(float)), s));
         return GDN2_OK;
     }
     const BwdLayout L = bwd_layout(&f);
     if (!a->workspace || a->workspace_bytes < L.total || (reinterpret_cast<uintptr_t>(a->workspace) & 255u))
-        return fail(GDN2_EINVAL, "gdn2_chunk_bwd_f32: workspace missing, too small or not 256-byte aligned");
+        return fail(GDN2_EINVAL, w + "workspace missing, too small or not 256-byte aligned");
     char *ws = static_cast<char *>(a->workspace);
     chunk_bind_ws(&f, ws, &bp.f);
     ChunkParams &p = bp.f;
@@ -1058,8 +1067,35 @@ extern "C" gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *a, gdn2_str
     bp.ws_dakk = reinterpret_cast<float *>(ws + L.dakk);
     bp.ws_kgrad = p.rep > 1 ? reinterpret_cast<float *>(ws + L.kgrad) : nullptr;
     bp.ws_rseg = reinterpret_cast<float *>(ws + L.rseg);
+    if (what == 1) { // the forward with its output, keeping the backward's inputs
+        p.fwd_out = 1;
+        GDN2_HIP_CHECK(launch_chunk(p, s, 1 | 2 | 4));
+        return GDN2_OK;
+    }
     // forward: per-chunk operands (training outputs), then the state entering every chunk
-    GDN2_HIP_CHECK(launch_chunk(p, s, 1 | 4));
+    if (what == 3) GDN2_HIP_CHECK(launch_chunk(p, s, 1 | 4));
     GDN2_HIP_CHECK(launch_bwd(bp, s));
     return GDN2_OK;
+}
+
+}  // namespace
+
+// fused_chunk_backward (src/kernel/chunk_adjoint_cube.rs:464-707), recomputing
+// the forward's per-chunk quantities.
+extern "C" gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *a, gdn2_stream_t stream) {
+    return chunk_bwd_call(a, stream, 3, "gdn2_chunk_bwd_f32");
+}
+
+// The training forward: gdn2_chunk_fwd_f32's output and final state, and in
+// the backward's workspace the quantities the reference exports as
+// FusedBackwardInputs (src/kernel/chunk_adjoint_cube.rs:426-447).
+extern "C" gdn2_status gdn2_chunk_fwd_train_f32(const gdn2_chunk_bwd_args *a, gdn2_stream_t stream) {
+    return chunk_bwd_call(a, stream, 1, "gdn2_chunk_fwd_train_f32");
+}
+
+// fused_chunk_backward from the training forward's saved quantities
+// (fused_chunk_backward(fwd: &FusedBackwardInputs, ..),
+// src/kernel/chunk_adjoint_cube.rs:464-520).
+extern "C" gdn2_status gdn2_chunk_bwd_saved_f32(const gdn2_chunk_bwd_args *a, gdn2_stream_t stream) {
+    return chunk_bwd_call(a, stream, 2, "gdn2_chunk_bwd_saved_f32");
 }

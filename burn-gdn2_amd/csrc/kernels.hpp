@@ -84,6 +84,9 @@ struct ChunkParams {
     // the first caller chunk that starts inside it (none when j0(n) >=
     // st_chunks); chunk_states_kernel derives the other slots from it.
     int st_cc, st_chunks;
+    // Training forward with the output (the backward's saved inputs): the
+    // training chunk-intra also writes scale q exp(G) and A_qk for the output.
+    int fwd_out;
 };
 
 // Projection epilogue: raw Linear outputs -> kernel inputs, one token per
@@ -207,8 +210,8 @@ hipError_t launch_decode(const DecodeParams &p, hipStream_t s);
 bool chunk_supported(int K, int V);     // the chunked forward's instances
 bool chunk_bwd_supported(int K, int V); // the chunked backward's
 // phases: bit 0 intra (with the training outputs when ws_akk is set), bit 1
-// inter with the output, bit 2 inter writing ws_sn / ws_vn instead of the
-// output and the final state.
+// inter with the output, bit 2 inter writing ws_sn / ws_vn in the backward's
+// layouts (with bit 1: the output and the final state as well; without: neither).
 hipError_t launch_chunk(const ChunkParams &p, hipStream_t s, int phases);
 
 }  // namespace gdn2

@@ -995,13 +995,18 @@ struct gdn2_layer_grads {
 
 // What forward_train computes before the norm, kept for the backward instead
 // of recomputing it: Y, F, G, the kernel operands q .. w and the recurrence
-// output O (pre-norm).
+// output O (pre-norm); for heads the chunked backward takes, also the
+// recurrence's per-chunk quantities (the chunked backward's workspace as
+// gdn2_chunk_fwd_train_f32 leaves it, the reference's FusedBackwardInputs).
 struct gdn2_layer_saved {
     const gdn2_layer *layer = nullptr;
     int64_t batch = 0, seq_len = 0;
     bool filled = false;
     void *buf = nullptr;
     Work fw{};
+    void *chunk = nullptr;    // the chunked backward's workspace (inside buf), or null
+    size_t chunk_bytes = 0;
+    bool chunk_filled = false; // the last forward_train_saved ran the training forward into it
 };
 
 namespace {
@@ -1099,8 +1104,15 @@ extern "C" gdn2_status gdn2_layer_saved_create(const gdn2_layer *L, int64_t B, i
         return fail(GDN2_EINVAL, "gdn2_layer_saved_create: batch must be > 0, seq_len >= 0, batch * seq_len bounded");
     const Dims &d = L->d;
     const size_t M = (size_t)(B * T), f = sizeof(float);
-    const size_t sz[10] = {f * M * L->ld_in, f * M * d.kd, f * M * d.vd, f * M * d.kd, f * M * d.kd,
-                           f * M * d.kd,     f * M * d.kd, f * M * d.vd, f * M * d.vd, f * M * d.vd};
+    size_t cbytes = 0;
+    if (T > 0 && chunk_bwd_supported((int)d.K, (int)d.V)) {
+        Work tmp{};
+        gdn2_chunk_bwd_args ba{};
+        ba.fwd = chunk_args_for(*L, B, T, tmp, nullptr);
+        cbytes = gdn2_chunk_bwd_workspace_bytes(&ba);
+    }
+    const size_t sz[11] = {f * M * L->ld_in, f * M * d.kd, f * M * d.vd, f * M * d.kd, f * M * d.kd, f * M * d.kd,
+                           f * M * d.kd,     f * M * d.vd, f * M * d.vd, f * M * d.vd, cbytes};
     size_t total = 0;
     for (size_t v : sz) total += align256(v);
     gdn2_layer_saved *A = new gdn2_layer_saved();
@@ -1117,6 +1129,8 @@ extern "C" gdn2_status gdn2_layer_saved_create(const gdn2_layer *L, int64_t B, i
         *dst[i] = reinterpret_cast<float *>(base);
         base += align256(sz[i]);
     }
+    A->chunk = cbytes ? base : nullptr;
+    A->chunk_bytes = cbytes;
     *out = A;
     return GDN2_OK;
 }
@@ -1128,6 +1142,7 @@ extern "C" gdn2_status gdn2_layer_forward_train_saved_f32(gdn2_layer *L, const f
     if (!A || A->layer != L || A->batch != B || A->seq_len != T)
         return fail(GDN2_EINVAL, "gdn2_layer_forward_train_saved_f32: saved missing or made for another layer or shape");
     A->filled = false;
+    A->chunk_filled = false;
     if (T == 0) {
         A->filled = true;
         return GDN2_OK;
@@ -1143,7 +1158,19 @@ extern "C" gdn2_status gdn2_layer_forward_train_saved_f32(gdn2_layer *L, const f
     if ((st = input_gemms(*L, x, M, sv, s)) != GDN2_OK) return st;
     if ((st = project_epilogue(*L, B, T, nullptr, sv, s)) != GDN2_OK) return st;
     GDN2_HIP_CHECK(launch_fill_rows(wk.S0, 0, nullptr, 1, B * L->d.HV * L->d.K * L->d.V, s));
-    if ((st = recurrence(*L, B, T, L->cfg.mode, sv, wk.S0, s)) != GDN2_OK) return st;
+    st = GDN2_NOT_APPLICABLE;
+    // where the recurrence runs the chunk kernels, the training forward keeps
+    // their per-chunk quantities for the backward
+    if (A->chunk && (L->cfg.mode == GDN2_MODE_CHUNK || T > kFusedRecurrentMaxSeq)) {
+        gdn2_chunk_bwd_args ba{};
+        ba.fwd = chunk_args_for(*L, B, T, sv, wk.S0);
+        ba.workspace = A->chunk;
+        ba.workspace_bytes = A->chunk_bytes;
+        st = gdn2_chunk_fwd_train_f32(&ba, s);
+        if (st != GDN2_OK && st != GDN2_NOT_APPLICABLE) return st;
+        A->chunk_filled = st == GDN2_OK;
+    }
+    if (st == GDN2_NOT_APPLICABLE && (st = recurrence(*L, B, T, L->cfg.mode, sv, wk.S0, s)) != GDN2_OK) return st;
     if ((st = output_side(*L, M, true, sv, out, s, wk.O)) != GDN2_OK) return st;  // O stays pre-norm
     A->filled = true;
     return GDN2_OK;
@@ -1312,9 +1339,15 @@ extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, in
         ba.d_state_out = has_ds ? d_state->S : nullptr;
         ba.dq = bw.dq; ba.dk = bw.dk; ba.dg = bw.dg; ba.db = bw.db; ba.dv = bw.dv; ba.dw = bw.dw;
         ba.d_state0 = d_state_in ? d_state_in->S : bw.dS0;
-        ba.workspace = fw.chunk;
-        ba.workspace_bytes = fw.chunk_bytes;
-        if ((st = gdn2_chunk_bwd_f32(&ba, s)) != GDN2_OK) return st;
+        if (saved && saved->chunk_filled) { // the forward's per-chunk quantities are kept
+            ba.workspace = saved->chunk;
+            ba.workspace_bytes = saved->chunk_bytes;
+            if ((st = gdn2_chunk_bwd_saved_f32(&ba, s)) != GDN2_OK) return st;
+        } else {
+            ba.workspace = fw.chunk;
+            ba.workspace_bytes = fw.chunk_bytes;
+            if ((st = gdn2_chunk_bwd_f32(&ba, s)) != GDN2_OK) return st;
+        }
     } else {
         gdn2_recurrent_bwd_args ra{};
         ra.fwd = recurrent_args_for(chunk_args_for(*L, B, T, fw, bw.S0));

@@ -100,7 +100,8 @@ EXPORTS = ("gdn2_last_error", "gdn2_hip_available", "gdn2_recurrent_step_f32", "
            "gdn2_chunk_segments", "gdn2_chunk_inter_pass_f32",
            "gdn2_chunk_fwd_states_f32", "gdn2_chunk_noalloc_scratch_bytes", "gdn2_chunk_fwd_noalloc_f32",
            "gdn2_stream_copy_f32", "gdn2_short_conv_f32", "gdn2_l2_normalize_f32", "gdn2_rms_norm_gate_f32",
-           "gdn2_chunk_bwd_workspace_bytes", "gdn2_chunk_bwd_f32", "gdn2_recurrent_bwd_workspace_bytes",
+           "gdn2_chunk_bwd_workspace_bytes", "gdn2_chunk_bwd_f32", "gdn2_chunk_fwd_train_f32",
+           "gdn2_chunk_bwd_saved_f32", "gdn2_recurrent_bwd_workspace_bytes",
            "gdn2_recurrent_bwd_f32", "gdn2_decode_fused_f32",
            "gdn2_config_default", "gdn2_config_validate", "gdn2_config_dims", "gdn2_param_count",
            "gdn2_param_name", "gdn2_param_shape", "gdn2_param_init", "gdn2_layer_create", "gdn2_layer_destroy",
@@ -135,7 +136,8 @@ def lib():
                          ("gdn2_chunk_fwd_f32", ChunkArgs), ("gdn2_chunk_intra_f32", ChunkArgs),
                          ("gdn2_chunk_fwd_noalloc_f32", ChunkArgs),
                          ("gdn2_chunk_inter_f32", ChunkArgs), ("gdn2_decode_fused_f32", DecodeArgs),
-                         ("gdn2_chunk_bwd_f32", ChunkBwdArgs), ("gdn2_recurrent_bwd_f32", RecurrentBwdArgs)):
+                         ("gdn2_chunk_bwd_f32", ChunkBwdArgs), ("gdn2_chunk_fwd_train_f32", ChunkBwdArgs),
+                         ("gdn2_chunk_bwd_saved_f32", ChunkBwdArgs), ("gdn2_recurrent_bwd_f32", RecurrentBwdArgs)):
             fn = getattr(L, name)
             fn.argtypes = [ctypes.POINTER(st), ctypes.c_void_p]
             fn.restype = ctypes.c_int

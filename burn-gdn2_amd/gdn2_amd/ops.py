@@ -223,14 +223,42 @@ def chunk_wy_forward(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64
     return (out, st, v_new, states) if return_states else (out, st)
 
 
+def chunk_wy_forward_train(q, k, v, g, b, w, state, scale: float, chunk_size: int = 64, out=None, workspace=None):
+    """The training forward: (out, new_state, saved), the output and final
+    state of chunk_wy_forward plus `saved`, a device buffer holding the
+    quantities the backward takes (the reference's FusedBackwardInputs,
+    src/kernel/chunk_adjoint_cube.rs:426-447), for chunk_wy_backward(...,
+    saved=saved) on the same operands.  None when the chunked backward does
+    not take these heads."""
+    _check_f32_cuda(q, k, v, g, b, w, state)
+    q, k, v, g, b, w = _operands(q, k, v, g, b, w)
+    B, Hk, T, K = q.shape
+    HV, V = v.shape[1], v.shape[3]
+    st = state.contiguous().clone()
+    if out is None:
+        out = torch.empty((B, HV, T, V), device=q.device, dtype=torch.float32)
+    fwd = chunk_args(q, k, v, g, b, w, st, out, scale, chunk_size)
+    a = C.ChunkBwdArgs(fwd, None, None, None, None, None, None, None, None, None, None, 0)
+    need = int(C.lib().gdn2_chunk_bwd_workspace_bytes(ctypes.byref(a)))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    a.workspace, a.workspace_bytes = _p(workspace), workspace.numel() * workspace.element_size()
+    if not C.check(C.lib().gdn2_chunk_fwd_train_f32(ctypes.byref(a), _stream()), allow_not_applicable=True):
+        return None
+    return out, st, workspace
+
+
 def chunk_wy_backward(q, k, v, g, b, w, state0, d_out, scale: float, chunk_size: int = 64, d_state=None,
-                      workspace=None):
+                      workspace=None, saved=None):
     """Gradients of the chunked forward (fused_chunk_backward,
     src/kernel/chunk_adjoint_cube.rs:464-707): for
     L = <d_out, out> + <d_state, S_T> returns dict dq, dk, dg, db (shapes of
     q, k, g, b), dv, dw (shapes of v, w) and dS0, or None when the chunk
     kernels do not apply.  dq, dk, dg, db take q's layout and dv, dw v's; dg
-    and db of a g or b with a last dim of 1 are summed over the channels."""
+    and db of a g or b with a last dim of 1 are summed over the channels.
+    With `saved` (from chunk_wy_forward_train on the same operands) the
+    forward's per-chunk quantities are taken from it instead of recomputed
+    (state0 is then not read)."""
     _check_f32_cuda(q, k, v, g, b, w, state0, d_out)
     g_in, b_in = g, b
     q, k, v, g, b, w = _operands(q, k, v, g, b, w)
@@ -249,11 +277,16 @@ def chunk_wy_backward(q, k, v, g, b, w, state0, d_out, scale: float, chunk_size:
     fwd = chunk_args(q, k, v, g, b, w, st, d_out, scale, chunk_size)
     a = C.ChunkBwdArgs(fwd, _p(d_out), _p(ds), *(_p(grads[n]) for n in ("dq", "dk", "dg", "db", "dv", "dw", "dS0")),
                        None, 0)
+    if saved is not None:
+        workspace = saved
     need = int(C.lib().gdn2_chunk_bwd_workspace_bytes(ctypes.byref(a)))
     if workspace is None or workspace.numel() * workspace.element_size() < need:
+        if saved is not None:
+            raise ValueError("saved holds fewer bytes than this backward's workspace: not from these operands")
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
     a.workspace, a.workspace_bytes = _p(workspace), workspace.numel() * workspace.element_size()
-    if not C.check(C.lib().gdn2_chunk_bwd_f32(ctypes.byref(a), _stream()), allow_not_applicable=True):
+    fn = C.lib().gdn2_chunk_bwd_saved_f32 if saved is not None else C.lib().gdn2_chunk_bwd_f32
+    if not C.check(fn(ctypes.byref(a), _stream()), allow_not_applicable=True):
         return None
     grads["dg"], grads["db"] = _reduce_like(grads["dg"], g_in), _reduce_like(grads["db"], b_in)
     return grads

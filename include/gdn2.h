@@ -285,6 +285,25 @@ typedef struct gdn2_chunk_bwd_args {
 GDN2_API size_t gdn2_chunk_bwd_workspace_bytes(const gdn2_chunk_bwd_args *args);
 GDN2_API gdn2_status gdn2_chunk_bwd_f32(const gdn2_chunk_bwd_args *args, gdn2_stream_t stream);
 
+/* The training forward and the backward from its saved quantities, the
+ * reference's pair fused_chunk_forward -> FusedBackwardInputs ->
+ * fused_chunk_backward(fwd: &FusedBackwardInputs, ..)
+ * (src/kernel/chunk_adjoint_cube.rs:426-520):
+ *   gdn2_chunk_fwd_train_f32  the forward of args->fwd exactly as
+ *       gdn2_chunk_fwd_f32 (out written, state updated in place to S_T), that
+ *       also leaves in args->workspace (gdn2_chunk_bwd_workspace_bytes(args)
+ *       bytes, 256-byte aligned) every per-chunk quantity the backward reads:
+ *       the WY operands (W, U, Kd, e^{G_last}, A_qk, scale q e^G, (I + A_kk)^-1),
+ *       the state entering every chunk and v_new.  The gradient pointers are
+ *       not read.
+ *   gdn2_chunk_bwd_saved_f32  gdn2_chunk_bwd_f32 on that workspace, untouched
+ *       since, for the same q, k, g, b, v, w, shapes and strides: the forward's
+ *       quantities are read instead of recomputed (args->fwd.state is not read).
+ *       The gradients are bit-identical to gdn2_chunk_bwd_f32's.
+ * Limits: those of gdn2_chunk_bwd_f32. */
+GDN2_API gdn2_status gdn2_chunk_fwd_train_f32(const gdn2_chunk_bwd_args *args, gdn2_stream_t stream);
+GDN2_API gdn2_status gdn2_chunk_bwd_saved_f32(const gdn2_chunk_bwd_args *args, gdn2_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Backward of the per-token scan                 -- autodiff of the recurrence
  * (src/kernel/fused_recurrent.rs:27-52, differentiated by burn's autodiff in

@@ -163,7 +163,13 @@ GDN2_API gdn2_status gdn2_layer_grads_get(const gdn2_layer_grads *grads, const c
  * computes before the norm: the Linear outputs, the kernel operands and the
  * recurrence output; about 4 * B * T * (D_in + 8 kd + 4 vd) bytes with
  * D_in ~ 3 kd + 2 vd + 2 V), so that the backward need not recompute them.
- * One object per (batch, seq_len); reusable. */
+ * For heads the chunked backward takes it also holds that backward's
+ * workspace (gdn2_chunk_bwd_workspace_bytes), which the forward fills with
+ * the recurrence's per-chunk quantities through gdn2_chunk_fwd_train_f32
+ * wherever the recurrence runs the chunk kernels (mode chunk, or T > 64), and
+ * the backward reads through gdn2_chunk_bwd_saved_f32 (about 5 GB more at
+ * B = 8, T = 4096, 16 heads of 128).  One object per (batch, seq_len);
+ * reusable. */
 typedef struct gdn2_layer_saved gdn2_layer_saved;
 GDN2_API gdn2_status gdn2_layer_saved_create(const gdn2_layer *layer, int64_t batch, int64_t seq_len,
                                              gdn2_layer_saved **out);

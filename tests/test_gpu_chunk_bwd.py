@@ -193,3 +193,48 @@ def test_chunk_bwd_scalar_broadcast_gates(gpu):
     torch.cuda.synchronize()
     assert tuple(got["dg"].shape) == (B, Hk, T, 1) and tuple(got["db"].shape) == (B, Hk, T, 1)
     _compare(got, ref, "broadcast g, b")
+
+
+SAVED_CASES = [
+    (2, 2, 2, 130, 128, 128, (-0.3, -0.02)),     # ragged last chunk
+    (1, 1, 2, 150, 128, 256, (-31.0, -0.05)),    # GVA, V = 2K, masked diagonal channels
+    (1, 2, 2, 2100, 128, 128, (-0.003, -0.0005)),  # segmented: every segment's transition kept
+    (2, 2, 2, 97, 64, 64, (-0.3, -0.02)),
+]
+
+
+@pytest.mark.parametrize("case", SAVED_CASES, ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}" for c in SAVED_CASES])
+def test_chunk_bwd_from_saved_forward(gpu, case):
+    """gdn2_chunk_fwd_train_f32 (the forward keeping the backward's inputs,
+    the reference's FusedBackwardInputs) then gdn2_chunk_bwd_saved_f32: the
+    forward's output and final state match the double recurrence, and the
+    gradients are bit-identical to gdn2_chunk_bwd_f32's (which recomputes
+    those quantities) and match the double adjoint."""
+    import torch
+
+    import gdn2_amd
+
+    B, Hk, HV, T, K, V, (glo, ghi) = case
+    rng = np.random.default_rng(4000 + T + K + V)
+    q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=glo, g_hi=ghi, b_hi=2.0)
+    q *= K ** -0.5 * 4
+    S0 = (rng.standard_normal((B, HV, K, V)) * 0.5).astype(np.float32)
+    dO = rng.standard_normal((B, HV, T, V)).astype(np.float32)
+    dST = rng.standard_normal((B, HV, K, V)).astype(np.float32)
+    scale = K ** -0.5
+    d = _dev(gpu, q, k, v, g, b, w, S0, dO, dST)
+    res = gdn2_amd.chunk_wy_forward_train(*d[:7], scale)
+    assert res is not None
+    out, ST, saved = res
+    o_ref, S_ref = O.recurrent_f64(q, k, v, g, b, w, S0=S0, scale=scale)
+    eo = float(np.abs(out.cpu().numpy() - o_ref).max())
+    es = float(np.abs(ST.cpu().numpy() - S_ref).max())
+    print(f"training forward: max|out err|={eo:.2e} max|S err|={es:.2e}")
+    assert eo < 1e-4 and es < 1e-4
+    got = gdn2_amd.chunk_wy_backward(*d[:7], d[7], scale, 64, d_state=d[8], saved=saved)
+    rec = gdn2_amd.chunk_wy_backward(*d[:7], d[7], scale, 64, d_state=d[8])
+    torch.cuda.synchronize()
+    for n in NAMES:
+        assert torch.equal(got[n], rec[n]), n
+    ref = O.recurrent_bwd_f64(q, k, v, g, b, w, dO, S0=S0, d_ST=dST, scale=scale)
+    _compare(got, ref, "saved " + str(case[:6]))

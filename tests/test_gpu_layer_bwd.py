@@ -197,17 +197,29 @@ def test_backward_rejects_oversized_heads(gpu):
     assert e.value.status == G._capi.GDN2_NOT_APPLICABLE
 
 
-def test_saved_activations_equal_recompute(gpu):
-    """forward_train with saved activations gives the same output as without,
-    and the backward from them equals the recomputing backward bit for bit
-    (both run the chunked kernels on the same operands)."""
+@pytest.mark.parametrize("strong", [False, True], ids=["min_decay", "dt_bias_plus_4"])
+def test_saved_activations_equal_recompute(gpu, strong):
+    """forward_train with saved activations (which also keeps the chunked
+    recurrence's per-chunk quantities: gdn2_chunk_fwd_train_f32) gives the
+    same output as without, and the backward from them
+    (gdn2_chunk_bwd_saved_f32) equals the recomputing backward bit for bit;
+    also with decays strong enough that diagonal-block channels take the
+    exact pairwise path."""
     import torch
 
-    G, cfg, layer, W = _setup(gpu, dict(SMALL, min_decay=0.9, allow_neg_eigval=True))
+    over = dict(SMALL, hidden_size=256, num_heads=2, head_dim=128) if strong else \
+        dict(SMALL, min_decay=0.9, allow_neg_eigval=True)
+    G, cfg, layer, W = _setup(gpu, over)
+    if strong:
+        layer.set_param("dt_bias", W["dt_bias"] + 4.0)
     rng = np.random.default_rng(12)
     B, T = 2, 130
     x = torch.from_numpy(rng.standard_normal((B, T, cfg.hidden_size)).astype(np.float32)).to(gpu)
     d = torch.from_numpy(rng.standard_normal((B, T, cfg.hidden_size)).astype(np.float32)).to(gpu)
+    if strong:  # the case reaches the masked channels
+        gt = layer.project(x)["g"].cpu().numpy().astype(np.float64)
+        gt = np.pad(gt, [(0, 0), (0, 0), (0, (-T) % 16), (0, 0)])
+        assert (-gt.reshape(B, cfg.num_heads, -1, 16, cfg.head_dim).sum(3) * np.log2(np.e) > 96).any()
     saved = G.Gdn2Saved(layer, B, T)
     out_s = layer.forward_train(x, saved=saved)
     out_r = layer.forward_train(x)
