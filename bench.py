@@ -294,6 +294,8 @@ OTHER_CONFIGS = {
             0.0, 47, "the reference's CPU-benchmark layer (tests/bit_exact.rs:224-235): hidden 256, 4 heads, K 64, "
                      "expand_v 1.5 (V 96), x [8, 4096, 256]"),
 }
+# configurations whose chunked backward is timed too (head_dim 256)
+BWD_CONFIGS = ("D256",)
 # configurations whose core is also timed on the per-token scan (gdn2_recurrent_fwd_f32,
 # the path their head shapes took before the chunk kernels covered them)
 SCAN_COMPARE = ("V96",)
@@ -372,6 +374,8 @@ def bench_other_config(torch, G, args, dev, name):
     if nseg > 1:
         names = ("segment_summaries", "chain", "output_pass")
         res["core"]["chunk_inter"]["passes_ms"] = {n: sum(pp) / reps for n, pp in zip(names, per_pass)}
+    if name in BWD_CONFIGS and not args.no_backward:
+        res["backward"] = time_chunk_backward(torch, args, dev, q, k, g, b, v, w, desc)
     if name in SCAN_COMPARE:
         from gdn2_amd.ops import _p, _strides3
 
@@ -1156,25 +1160,21 @@ def traffic_summary(fetch_csv, write_csv):
     return out
 
 
-def bench_backward(torch, G, args, dev):
-    """gdn2_chunk_bwd_f32 on the prefill workload's operands (the layer's own
-    project() outputs, d_out ~ N(0,1)): the gradients of q, k, g, b, v, w and
-    S0, recomputing the forward's per-chunk quantities.  Outputs and the
-    workspace are allocated before the timed region."""
+def time_chunk_backward(torch, args, dev, q, k, g, b, v, w, label):
+    """gdn2_chunk_bwd_f32 on the given operands (d_out ~ N(0,1)): the
+    gradients of q, k, g, b, v, w and S0, recomputing the forward's per-chunk
+    quantities; then gdn2_chunk_fwd_train_f32 (the forward keeping them) and
+    gdn2_chunk_bwd_saved_f32 (the backward reading them).  Outputs and the
+    workspace are allocated before the timed regions."""
     import ctypes
 
     from gdn2_amd import _capi as CA
     from gdn2_amd.ops import _p, _stream, chunk_args
 
-    cfg = G.Gdn2Config(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0, mode="chunk", chunk_size=64)
-    layer = G.GatedDeltaNet2(cfg, seed=1337)
-    B, T, H, K, V = args.batch, args.seq, cfg.num_heads, cfg.head_dim, cfg.v_head
+    B, H, T, K = q.shape
+    V = v.shape[3]
     gen = torch.Generator(device=dev)
-    gen.manual_seed(42)
-    x = torch.randn((B, T, cfg.hidden_size), generator=gen, device=dev, dtype=torch.float32)
-    P = layer.project(x)
-    del x, layer
-    q, k, g, b, v, w = (P[n] for n in ("q", "k", "g", "b", "v", "w"))
+    gen.manual_seed(44)
     S0 = torch.zeros((B, H, K, V), device=dev)
     dO = torch.randn((B, H, T, V), generator=gen, device=dev)
     grads = [torch.empty_like(t) for t in (q, k, g, b, v, w)] + [torch.empty_like(S0)]
@@ -1185,29 +1185,7 @@ def bench_backward(torch, G, args, dev):
     ws = torch.empty(need, dtype=torch.uint8, device=dev)
     a.workspace, a.workspace_bytes = _p(ws), need
     stream = _stream()
-    settle(torch, lambda: CA.check(L.gdn2_chunk_bwd_f32(ctypes.byref(a), stream)), args.settle_ms)
-    for _ in range(args.warmup):
-        CA.check(L.gdn2_chunk_bwd_f32(ctypes.byref(a), stream))
-    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.steps):
-        L.gdn2_chunk_bwd_f32(ctypes.byref(a), stream)
-    e1.record()
-    torch.cuda.synchronize()
-    CA.check(L.gdn2_chunk_bwd_f32(ctypes.byref(a), stream))
-    ms = e0.elapsed_time(e1) / args.steps
-    res = {"workload": f"chunked backward (gradients of q, k, g, b, v, w, S0), B={B} T={T} H=16 K=V=128",
-           "ms_per_step": ms, "tokens_per_s": B * T / (ms / 1e3), "workspace_bytes": need,
-           "kernel": "gdn2_chunk_bwd_f32"}
-
-    # the training forward (output + final state, keeping the backward's inputs
-    # in the workspace), then the backward from them
-    St = torch.zeros_like(S0)
-    out = torch.empty((B, T, H, V), device=dev).permute(0, 2, 1, 3)
-    at = CA.ChunkBwdArgs(chunk_args(q, k, v, g, b, w, St, out, K ** -0.5, 64), _p(dO), None,
-                         *(_p(t) for t in grads), _p(ws), need)
-    pt = ctypes.byref(at)
 
     def timed(fn, n):
         settle(torch, fn, args.settle_ms)
@@ -1221,6 +1199,19 @@ def bench_backward(torch, G, args, dev):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n
 
+    pa = ctypes.byref(a)
+    ms = timed(lambda: CA.check(L.gdn2_chunk_bwd_f32(pa, stream)), args.steps)
+    res = {"workload": f"chunked backward (gradients of q, k, g, b, v, w, S0), {label}",
+           "ms_per_step": ms, "tokens_per_s": B * T / (ms / 1e3), "workspace_bytes": need,
+           "kernel": "gdn2_chunk_bwd_f32"}
+
+    # the training forward (output + final state, keeping the backward's inputs
+    # in the workspace), then the backward from them
+    St = torch.zeros_like(S0)
+    out = torch.empty((B, T, H, V), device=dev).permute(0, 2, 1, 3)
+    at = CA.ChunkBwdArgs(chunk_args(q, k, v, g, b, w, St, out, K ** -0.5, 64), _p(dO), None,
+                         *(_p(t) for t in grads), _p(ws), need)
+    pt = ctypes.byref(at)
     fwd_ms = timed(lambda: CA.check(L.gdn2_chunk_fwd_train_f32(pt, stream)), args.steps)
     saved_ms = timed(lambda: CA.check(L.gdn2_chunk_bwd_saved_f32(pt, stream)), args.steps)
     res["from_saved_forward"] = {
@@ -1228,7 +1219,25 @@ def bench_backward(torch, G, args, dev):
         "training_forward": {"kernel": "gdn2_chunk_fwd_train_f32", "ms_per_step": fwd_ms,
                              "tokens_per_s": B * T / (fwd_ms / 1e3)},
         "what": "the backward reading the training forward's per-chunk quantities instead of recomputing them"}
-    del P, q, k, g, b, v, w, S0, dO, grads, ws, St, out
+    del S0, dO, grads, ws, St, out
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_backward(torch, G, args, dev):
+    """The chunked backward on the prefill workload's operands (the layer's
+    own project() outputs)."""
+    cfg = G.Gdn2Config(hidden_size=2048, num_heads=16, head_dim=128, expand_v=1.0, mode="chunk", chunk_size=64)
+    layer = G.GatedDeltaNet2(cfg, seed=1337)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(42)
+    x = torch.randn((args.batch, args.seq, cfg.hidden_size), generator=gen, device=dev, dtype=torch.float32)
+    P = layer.project(x)
+    del x
+    layer.close()
+    res = time_chunk_backward(torch, args, dev, *(P[n] for n in ("q", "k", "g", "b", "v", "w")),
+                              f"B={args.batch} T={args.seq} H=16 K=V=128")
+    del P
     torch.cuda.empty_cache()
     return res
 

@@ -1107,10 +1107,10 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
     if (phases & 1) {
         const int nchunks = p.B * p.HV * p.NC;
         if (p.ws_akk) {
-            if constexpr (K >= 64 && K <= 128)
+            if constexpr (K >= 64 && (K <= 128 || V >= 128))
                 hipLaunchKernelGGL((chunk_intra_kernel<K, V, true>), dim3(nchunks), dim3(512), 0, s, p);
             else
-                return hipErrorInvalidValue; // the chunked backward takes K in {64, 128}
+                return hipErrorInvalidValue; // the chunked backward's shapes
         } else
             hipLaunchKernelGGL((chunk_intra_kernel<K, V, false>), dim3(nchunks), dim3(512), 0, s, p);
         hipError_t e = hipGetLastError();
@@ -1155,7 +1155,9 @@ bool chunk_supported(int K, int V) {
            (K == 128 && (V == 64 || V == 128 || V == 192 || V == 256)) || (K == 256 && (V == 128 || V == 256));
 }
 
-bool chunk_bwd_supported(int K, int V) { return (K == 64 || K == 128) && (V == 64 || V == 128 || V == 256); }
+bool chunk_bwd_supported(int K, int V) {
+    return ((K == 64 || K == 128) && (V == 64 || V == 128 || V == 256)) || (K == 256 && (V == 128 || V == 256));
+}
 
 template <int K>
 hipError_t launch_chunk_states_t(const ChunkParams &p, hipStream_t s) {

@@ -92,7 +92,11 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
     constexpr int NKT = K / 16;
     constexpr int OPF4 = NKT * NT * 64, PFO = OPF4 / 256;
     constexpr int AF4 = NT * NT * 64, APF = AF4 / 256;
-    __shared__ floatx4 sKd[OPF4], sAT[AF4], sQT[OPF4], sWT[OPF4];
+    // K = 256: Kd and W^T take 64 KiB of LDS each, so (scale q e^G)^T, whose
+    // product QG^T dO feeds only dS (not the dS -> dv_new chain), is read from
+    // L2 into registers in phase 2 instead of through a third LDS buffer.
+    constexpr bool QLDS = K <= 128;
+    __shared__ floatx4 sKd[OPF4], sAT[AF4], sQT[QLDS ? OPF4 : 1], sWT[OPF4];
     __shared__ float sPf[256]; // destination of the L2 touches, never read
 
     const int V = p.V, nvv = V / 64;
@@ -182,7 +186,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
         lds_barrier(); // sKd, sAT hold chunk n; every wave is done with sQT, sWT (n+1)
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
-            lds_copy4(&QT4[cid * OPF4 + i * 256 + tid], &sQT[i * 256 + wv]);
+            if (QLDS) lds_copy4(&QT4[cid * OPF4 + i * 256 + tid], &sQT[i * 256 + wv]);
             lds_copy4(&WT4[cid * OPF4 + i * 256 + tid], &sWT[i * 256 + wv]);
         }
         if (!LOCAL) { // dL/d(state leaving chunk n)
@@ -280,7 +284,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
             auto load_qw = [&](int tt, int bf) {
 #pragma unroll
                 for (int kb = 0; kb < NKT; ++kb) {
-                    qa[bf][kb] = sQT[(kb * NT + tt) * 64 + lane];
+                    qa[bf][kb] = QLDS ? sQT[(kb * NT + tt) * 64 + lane] : QT4[cid * OPF4 + (kb * NT + tt) * 64 + lane];
                     wa[bf][kb] = sWT[(kb * NT + tt) * 64 + lane];
                 }
             };
@@ -420,7 +424,7 @@ struct VprodSmem {
 };
 
 template <int K, int V>
-__global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
+__global__ __launch_bounds__(256, K >= 256 ? 1 : 2) void bwd_vprod_kernel(BwdParams bp) {
     const ChunkParams &p = bp.f;
     using SM = VprodSmem<K, V>;
     constexpr int NKT = K / 16, NVB = V / 16, NVT = V / 16, NCT = NKT + NVT;
@@ -697,7 +701,7 @@ __global__ __launch_bounds__(256, 2) void bwd_vprod_kernel(BwdParams bp) {
 // the rows of its B fragments, accumulator rows and elementwise terms.
 // ---------------------------------------------------------------------------
 template <int K, int V>
-__global__ __launch_bounds__(K * 4, K / 32) void bwd_decay_kernel(BwdParams bp) {
+__global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel(BwdParams bp) {
     const ChunkParams &p = bp.f;
     constexpr int NTH = K * 4, NSEG = NTH / K, RPS = C / NSEG; // cumsum: NSEG row segments per channel
     constexpr int KP = K + 4, CP = C + 4;
@@ -953,6 +957,8 @@ hipError_t launch_bwd(const BwdParams &bp, hipStream_t s) {
     if (K == 64 && V == 64) return launch_bwd_t<64, 64>(bp, s);
     if (K == 64 && V == 128) return launch_bwd_t<64, 128>(bp, s);
     if (K == 64 && V == 256) return launch_bwd_t<64, 256>(bp, s);
+    if (K == 256 && V == 256) return launch_bwd_t<256, 256>(bp, s);
+    if (K == 256 && V == 128) return launch_bwd_t<256, 128>(bp, s);
     return hipErrorInvalidValue;
 }
 

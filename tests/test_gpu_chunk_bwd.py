@@ -144,18 +144,42 @@ def test_chunk_bwd_strided_views(gpu):
     _compare(got, ref, "strided")
 
 
-def test_chunk_bwd_declines_k256(gpu):
-    """head_dim 256 runs the chunked forward but not the chunked backward:
-    the reference's `None` (the caller keeps its own path)."""
+K256_CASES = [
+    # head_dim 256 (the reference's fused backward host has no K cap,
+    # src/kernel/chunk_adjoint_cube.rs:464-520)
+    (1, 2, 2, 150, 256, 256, (-0.3, -0.02), 1.0, 0.5, True),     # ragged last chunk
+    (1, 1, 2, 130, 256, 128, (-0.4, -0.01), 2.0, 0.5, True),     # V = 128 (expand_v 0.5), GVA, neg-eig
+    (1, 1, 1, 100, 256, 256, (-31.0, -0.05), 1.0, 0.5, True),    # masked diagonal channels
+    (1, 1, 2, 2100, 256, 256, (-0.003, -0.0005), 1.0, 1.0, True),  # segmented forward and reverse recurrences
+]
+
+
+@pytest.mark.parametrize("case", K256_CASES, ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}g{c[6][0]}"
+                                                  for c in K256_CASES])
+def test_chunk_bwd_head_dim_256(gpu, case):
+    """The chunked backward at K = 256: every gradient against the double
+    adjoint, and the backward from a saved training forward bit-identical to
+    the recomputing one."""
     import torch
 
     import gdn2_amd
 
-    rng = np.random.default_rng(12)
-    d = _dev(gpu, *rand_inputs(rng, 1, 1, 1, 64, 256, 256))
-    S0 = torch.zeros((1, 1, 256, 256), device=gpu)
-    assert gdn2_amd.chunk_wy_forward(*d, S0, 0.0625) is not None
-    assert gdn2_amd.chunk_wy_backward(*d, S0, torch.randn((1, 1, 64, 256), device=gpu), 0.0625) is None
+    g = _run_case(gpu, case)
+    if case[6][0] < -10:
+        assert masked_tiles(g, case[3])[0] > 0
+    B, Hk, HV, T, K, V, (glo, ghi), bhi, s0, dst = case
+    rng = np.random.default_rng(3000 + T + K + V)
+    q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=glo, g_hi=ghi, b_hi=bhi)
+    q *= K ** -0.5 * 4
+    S0 = (rng.standard_normal((B, HV, K, V)) * s0).astype(np.float32)
+    dO = rng.standard_normal((B, HV, T, V)).astype(np.float32)
+    d = _dev(gpu, q, k, v, g, b, w, S0, dO)
+    out, ST, saved = gdn2_amd.chunk_wy_forward_train(*d[:7], K ** -0.5)
+    got = gdn2_amd.chunk_wy_backward(*d[:7], d[7], K ** -0.5, 64, saved=saved)
+    rec = gdn2_amd.chunk_wy_backward(*d[:7], d[7], K ** -0.5, 64)
+    torch.cuda.synchronize()
+    for n in NAMES:
+        assert torch.equal(got[n], rec[n]), n
 
 
 def test_chunk_bwd_empty_sequence(gpu):

@@ -185,13 +185,28 @@ def test_small_heads_backward_matches_oracle(gpu, mode):
     _compare(grads, dx, dsi, ref, O.WEIGHT_NAMES)
 
 
+def test_head_dim_256_backward_matches_oracle(gpu):
+    """head_dim 256 (K = V = 256, two heads): the chunked backward's K = 256
+    kernels, every gradient against the double adjoint."""
+    import torch
+
+    G, cfg, layer, W = _setup(gpu, dict(hidden_size=512, num_heads=2, head_dim=256, mode="chunk"))
+    rng = np.random.default_rng(17)
+    B, T = 1, 150
+    xh = rng.standard_normal((B, T, cfg.hidden_size)).astype(np.float32)
+    dh = rng.standard_normal((B, T, cfg.hidden_size)).astype(np.float32)
+    dx, grads, dsi = layer.backward(torch.from_numpy(xh).to(gpu), torch.from_numpy(dh).to(gpu), want_d_state=True)
+    ref = O.layer_backward_f64(cfg, W, xh, dh)
+    _compare(grads, dx, dsi, ref, O.WEIGHT_NAMES)
+
+
 def test_backward_rejects_oversized_heads(gpu):
     import torch
 
     G = pytest.importorskip("gdn2_amd")
-    cfg = G.Gdn2Config(hidden_size=256, num_heads=1, head_dim=256)  # K = V = 256: neither backward kernel
+    cfg = G.Gdn2Config(hidden_size=512, num_heads=1, head_dim=512)  # K = V = 512: neither backward kernel
     layer = G.GatedDeltaNet2(cfg)
-    x = torch.zeros((1, 4, 256), device=gpu)
+    x = torch.zeros((1, 4, 512), device=gpu)
     with pytest.raises(G._capi.Gdn2Error) as e:
         layer.backward(x, x)
     assert e.value.status == G._capi.GDN2_NOT_APPLICABLE
