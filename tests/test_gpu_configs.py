@@ -193,6 +193,17 @@ def test_config4_gva_negeig_mindecay_chunk_then_decode(gpu):
     e_s = maxabs(st.recurrent, st_full.recurrent)
     print(f"decode {e_dec:.2e} (max|out| {float(full.abs().max()):.3e})  S {e_s:.2e}", flush=True)
     assert e_dec < TOL and e_s < TOL
+    # the 32 decoded tokens of rows 0 and 3 against the double layer oracle
+    # started from the layer's own state after the 8192-token prefill (S and
+    # the conv caches), token by token like the decode calls
+    _, st_p = layer.forward(x[:, :T].contiguous())
+    rows = [0, 3]
+    ost = _oracle_state(st_p, rows)
+    ref, rst = O.layer_forward(cfg, layer.params(), x[rows, T:].contiguous().cpu().numpy(), state=ost)
+    _vs_oracle(dec[rows].cpu().numpy(), ref.out, f"32 decoded tokens rows {rows} vs oracle from the prefill state")
+    e_so = maxabs(st.recurrent[rows], rst.recurrent)
+    print(f"final S rows {rows} vs oracle: {e_so:.2e}", flush=True)
+    assert e_so < TOL
 
 
 def test_config5_long_context_strong_decay(gpu):

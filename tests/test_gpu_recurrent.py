@@ -42,6 +42,30 @@ def test_step_matches_recurrence(gpu, B, Hk, HV, K, V):
     assert maxabs(state.cpu().numpy(), S_ref) < TOL
 
 
+def test_step_batch64_matches_oracle(gpu):
+    """The bare step at the decode benchmark's shape (B = 64, 16 heads,
+    K = V = 128, the streaming step kernel), three tokens in place on one
+    state, against the double recurrence."""
+    import gdn2_amd
+
+    rng = np.random.default_rng(64)
+    B, H, K, V, T = 64, 16, 128, 128, 3
+    q, k, v, g, b, w = rand_inputs(rng, B, H, H, T, K, V, b_hi=1.0)
+    q *= K ** -0.5 * 4
+    S0 = rng.standard_normal((B, H, K, V)).astype(np.float32) * 0.3
+    o_ref, S_ref = O.recurrent_f64(q, k, v, g, b, w, S0=S0, scale=K ** -0.5)
+    dq, dk, dv, dg, db, dw, state = _dev(gpu, q, k, v, g, b, w, S0)
+    for t in range(T):
+        sl = lambda x: x[:, :, t:t + 1]
+        o, state = gdn2_amd.fused_step(sl(dq), sl(dk), sl(dv), sl(dg), sl(db), sl(dw), state, K ** -0.5,
+                                       out_state=state)
+        e = maxabs(o.cpu().numpy()[:, :, 0], o_ref[:, :, t])
+        assert e < TOL, (t, e)
+    e_s = maxabs(state.cpu().numpy(), S_ref)
+    print(f"B=64 step: final S err {e_s:.2e}")
+    assert e_s < TOL
+
+
 @pytest.mark.parametrize("B,Hk,HV,T,K,V", [(2, 4, 4, 64, 128, 128), (1, 2, 4, 37, 64, 128), (2, 2, 2, 20, 16, 24),
                                            (1, 1, 1, 300, 128, 128)])
 def test_scan_matches_recurrence(gpu, B, Hk, HV, T, K, V):
