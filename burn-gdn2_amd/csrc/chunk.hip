@@ -676,7 +676,9 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p,
     const size_t uvf4 = (size_t)C * V / 4;
 
     // the operands go from global memory straight into LDS (lds_copy4):
-    // thread tid's float4 i lands at index i * NTH + tid, as a wave's 64 lanes
+    // thread tid's float4 i lands at index i * NTH + tid, as a wave's 64 lanes.
+    // (The buffer-resource form of these copies, buffer_load_dwordx4 ... lds
+    // with 32-bit offsets, needs fewer registers but measured 1.8 % slower.)
     const int wv = 64 * wave;
     // Each chunk's operands are also pulled toward L2 one phase before their
     // LDS copy (l2_touch, one 128-byte line per thread): W, q exp(G) of chunk
@@ -712,23 +714,23 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p,
     // left in flight for the compiler's own vmcnt waits inside it
     vm_wait0();
 
-    // row 4 lg of each 16-row tile; the rest of the row offset is wave-uniform
-    float *ob = p.out + (int64_t)bi * p.sob + (int64_t)hv * p.soh + col + (int64_t)(4 * lg) * p.sot;
-    // chunk nn's output rows from X2 (rows past T are not written)
+    // chunk nn's output rows from X2 through a buffer resource over its valid
+    // rows: rows past T fall outside its range and the hardware drops those
+    // stores, and each store's offset is a per-lane term (row 4 lg of each
+    // 16-row tile, column col) plus a wave-uniform row term, both 32-bit, in
+    // place of 64-bit row addresses.  Needs sot >= V and 63 sot + V < 2^29
+    // (checked on the host).
+    float *obh = p.out + (int64_t)bi * p.sob + (int64_t)hv * p.soh;
+    const int sot = (int)p.sot, olane = 4 * (4 * lg * sot + col);
     auto store_out = [&](const floatx4 *o, int nn) {
-        if ((nn + 1) * C <= p.T) { // a full chunk (wave-uniform): unconditional stores
+        const __amdgpu_buffer_rsrc_t R = rows_rsrc(obh + (int64_t)nn * C * p.sot, sot, min(C, p.T - nn * C), V);
 #pragma unroll
-            for (int mt = 0; mt < NT; ++mt)
+        for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) ob[(int64_t)(nn * C + 16 * mt + i) * p.sot] = o[mt][i];
-        } else {
-            const int cv = p.T - nn * C;
-#pragma unroll
-            for (int mt = 0; mt < NT; ++mt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (16 * mt + 4 * lg + i < cv) ob[(int64_t)(nn * C + 16 * mt + i) * p.sot] = o[mt][i];
-        }
+            for (int i = 0; i < 4; ++i) {
+                const float val = o[mt][i]; // through a scalar: a bit_cast of the element lvalue reads element 0
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, val), R, olane, 4 * (16 * mt + i) * sot, 0);
+            }
     };
     floatx4 X1[NT], X2[NT]; // chunk n's v_new and output, both read again in iteration n + 1
     // D: out = X2 + A_qk v_new (A_qk is lower block-triangular; the chains of
@@ -785,13 +787,19 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p,
             }
             float *Sn = p.ws_sn + slot * K * V;
             if (keep) {
+                // row-major: 32-bit offsets in a buffer resource over the slot
+                const __amdgpu_buffer_rsrc_t R = __builtin_amdgcn_make_buffer_rsrc(Sn, (short)0, K * V * 4, 0x00020000);
 #pragma unroll
                 for (int kb = 0; kb < NKT; ++kb)
                     if (FRAG) // the backward's fragment layout: tile (value tile, key tile)
                         reinterpret_cast<floatx4 *>(Sn)[(vt * NKT + kb) * 64 + lane] = S[kb];
                     else
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) Sn[(size_t)(16 * kb + 4 * lg + i) * V + col] = S[kb][i];
+                        for (int i = 0; i < 4; ++i) {
+                            const float val = S[kb][i]; // (through a scalar, see store_out)
+                            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, val), R, 4 * (4 * lg * V + col),
+                                                                  4 * (16 * kb + i) * V, 0);
+                        }
             }
         }
         // keep these loads here, a whole phase ahead of their use and of the
@@ -808,7 +816,8 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p,
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) {
                 wa[bf][mt] = sW[(mt * NKT + kb) * 64 + lane];
-                if (OUT) ma[bf][mt] = QLDS ? sQ[(mt * NKT + kb) * 64 + lane] : Q4[cid * OPF4 + (mt * NKT + kb) * 64 + lane];
+                if (OUT)
+                    ma[bf][mt] = QLDS ? sQ[(mt * NKT + kb) * 64 + lane] : Q4[cid * OPF4 + (mt * NKT + kb) * 64 + lane];
             }
         };
         load_a(0, 0);
@@ -850,22 +859,24 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p,
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) X1[mt] = u_cur[mt] - X1[mt];
         if (STATES) {
-            if (p.st_cc) { // token rows [B * HV, T, V]; rows past T (ragged last chunk) are not written
-                float *Vn = p.ws_vn + ((size_t)bh * p.T + (size_t)n * C) * V;
+            // row-major rows through a buffer resource over the chunk's rows:
+            // token rows [B * HV, T, V] (the resource ends at row T, so rows past T
+            // of a ragged last chunk are dropped) or the chunk's [C, V] block
+            if (p.st_cc || !FRAG) {
+                float *Vn = p.st_cc ? p.ws_vn + ((size_t)bh * p.T + (size_t)n * C) * V : p.ws_vn + cid * C * V;
+                const __amdgpu_buffer_rsrc_t R = rows_rsrc(Vn, V, p.st_cc ? min(C, p.T - n * C) : C, V);
 #pragma unroll
                 for (int mt = 0; mt < NT; ++mt)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (n * C + 16 * mt + 4 * lg + i < p.T) Vn[(size_t)(16 * mt + 4 * lg + i) * V + col] = X1[mt][i];
-            } else {
+                    for (int i = 0; i < 4; ++i) {
+                        const float val = X1[mt][i]; // (through a scalar, see store_out)
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, val), R, 4 * (4 * lg * V + col),
+                                                              4 * (16 * mt + i) * V, 0);
+                    }
+            } else { // tile (value tile, time tile)
                 float *Vn = p.ws_vn + cid * C * V;
 #pragma unroll
-                for (int mt = 0; mt < NT; ++mt)
-                    if (FRAG) // tile (value tile, time tile)
-                        reinterpret_cast<floatx4 *>(Vn)[(vt * NT + mt) * 64 + lane] = X1[mt];
-                    else
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) Vn[(size_t)(16 * mt + 4 * lg + i) * V + col] = X1[mt][i];
+                for (int mt = 0; mt < NT; ++mt) reinterpret_cast<floatx4 *>(Vn)[(vt * NT + mt) * 64 + lane] = X1[mt];
             }
         }
 
@@ -1293,6 +1304,10 @@ gdn2_status chunk_setup(const gdn2_chunk_args *a, const char *who, bool need_out
         ((kChunk - 1) * a->stride_qk_t + a->head_dim) * 4 >= (int64_t(1) << 31) ||
         ((kChunk - 1) * a->stride_vw_t + a->head_v_dim) * 4 >= (int64_t(1) << 31))
         return fail(GDN2_NOT_APPLICABLE, w + "token strides outside the chunk kernels' range");
+    // The output rows of a chunk go through a range-checked buffer resource too.
+    if (need_out && (a->stride_o_t < a->head_v_dim ||
+                     ((kChunk - 1) * a->stride_o_t + a->head_v_dim) * 4 >= (int64_t(1) << 31)))
+        return fail(GDN2_NOT_APPLICABLE, w + "output token stride outside the chunk kernels' range");
     *p = ChunkParams{};
     p->q = a->q; p->k = a->k; p->g = a->g; p->b = a->b; p->v = a->v; p->w = a->w;
     p->state = a->state; p->out = a->out;

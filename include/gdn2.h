@@ -137,8 +137,8 @@ GDN2_API gdn2_status gdn2_recurrent_fwd_f32(const gdn2_recurrent_args *args, gdn
  * or K = 256 and V in {128, 256} (the reference takes K, V <= 256; these are
  * its own benchmark and test head shapes and expand_v 0.5, 1, 1.5, 2, 4);
  * q, k, b rows 16-byte aligned (strides multiples of 4 elements); token
- * strides at least the row length (stride_qk_t >= K, stride_vw_t >= V) and
- * 63 token strides plus a row under 2 GiB.
+ * strides at least the row length (stride_qk_t >= K, stride_vw_t >= V,
+ * stride_o_t >= V) and 63 token strides plus a row under 2 GiB.
  * ---------------------------------------------------------------------- */
 typedef struct gdn2_chunk_args {
     const float *q, *k, *g, *b;
