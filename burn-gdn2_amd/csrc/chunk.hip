@@ -17,9 +17,13 @@
 //    last row of tile p-1; both factors <= 1.  One MFMA product per block.
 //  * diagonal blocks: the same split, whose column factor exp(Gb_p - G_s)
 //    is >= 1 but bounded by exp(span) with span = Gb_p - G at the tile end.
-//    Channels with span <= 96 (log2 units) keep the MFMA product; channels
-//    above that (e.g. |g| ~ 30 per token) are zeroed in the MFMA operand
-//    and added exactly with pairwise exp2(G_r - G_s), r >= s.
+//    Channels with span <= 96 (log2 units) keep that MFMA product. Channels
+//    with 96 < span <= 192 move the reference (for their whole row tile) to
+//    the middle of the tile's range, Gb_p - span / 2, so that both diagonal
+//    factors lie in [2^-96, 2^96] (the bounds of the split above): still one
+//    MFMA product, whose discarded upper triangle may overflow. Channels above 192 (e.g. |g| ~ 30
+//    per token) are zeroed in the MFMA operand and added exactly with
+//    pairwise exp2(G_r - G_s), r >= s.
 //  * WY solve per 16-row tile (src/forward.rs:192-261): the 16x16 diagonal
 //    blocks of I + A_kk are inverted by forward substitution and the tiles
 //    are eliminated in order, never as one 64x64 solve.
@@ -36,7 +40,8 @@ namespace gdn2 {
 namespace {
 
 static_assert(NT == 4, "the diagonal-block inverse maps 4 tiles x 16 columns onto one wave");
-constexpr float kSafeSpan = 96.0f; // log2 units
+constexpr float kSafeSpan = 96.0f;      // log2 units: reference at the tile start
+constexpr float kSafeSpanMid = 192.0f;  // reference in the middle of the tile's range
 
 // ---------------------------------------------------------------------------
 // chunk-intra: one workgroup (8 waves) per (b, hv, chunk).
@@ -48,7 +53,7 @@ constexpr float kSafeSpan = 96.0f; // log2 units
 // ---------------------------------------------------------------------------
 // TRAIN adds the backward's operands (ws_wt, ws_qgt, ws_kd, ws_aqkt, and
 // (I + A_kk)^-1 in ws_akk).
-// K = 256 needs 137 KiB of LDS: one workgroup per CU, two waves per SIMD,
+// K = 256 needs 141 KiB of LDS: one workgroup per CU, two waves per SIMD,
 // and up to 256 VGPRs per wave.
 template <int K, int V, bool TRAIN>
 __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(ChunkParams p) {
@@ -70,7 +75,8 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
     __shared__ __attribute__((aligned(16))) float sR[RSZ];
     __shared__ __attribute__((aligned(16))) float sAinv[NT][16][20];
     __shared__ float sTot[NSEG][K];
-    __shared__ uint32_t sMask[NT][K / 32];
+    __shared__ uint32_t sMask[NT][K / 32]; // diagonal-tile channels with span > kSafeSpanMid
+    __shared__ float sRef[NT][K];          // the score products' reference G per row tile
     float(*sK)[KP] = reinterpret_cast<float(*)[KP]>(sR);
     float(*sQG)[KP] = reinterpret_cast<float(*)[KP]>(sR);
     float(*sBKG)[KP] = sG;
@@ -181,10 +187,18 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
             }
         }
     }
+    // The score products' reference per (row tile, channel): Gb = G at the end
+    // of the previous tile (0 for the first); for a mid-range span the middle
+    // of the tile's range, (Gb + G_end) / 2, for the whole row tile. Its
+    // diagonal factors then lie in [2^-96, 2^96]; in the off-diagonal blocks
+    // the row factor is at most 2^96 and the column factor at most 1, and a
+    // column factor that underflows drops a term below 2^-30 |row operand k|.
     for (int idx = tid; idx < NT * K; idx += 512) {
         const int pt = idx / K, c = idx % K;
-        const float gb = pt ? sG[16 * pt - 1][c] : 0.f;
-        if (gb - sG[16 * pt + 15][c] > kSafeSpan) atomicOr(&sMask[pt][c >> 5], 1u << (c & 31));
+        const float gb = pt ? sG[16 * pt - 1][c] : 0.f, ge = sG[16 * pt + 15][c];
+        const float span = gb - ge;
+        if (span > kSafeSpanMid) atomicOr(&sMask[pt][c >> 5], 1u << (c & 31));
+        sRef[pt][c] = (span > kSafeSpan && span <= kSafeSpanMid) ? 0.5f * (gb + ge) : gb;
     }
     __syncthreads();
 
@@ -223,15 +237,13 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
         for (int pi = 0; pi < 2; ++pi) {
             const int pt = pi ? (NT - 1 - half) : half;
             const int row = 16 * pt + lr;
-            const int brow = pt > 0 ? 16 * pt - 1 : 0;    // G at the end of tile pt-1
-            const float bmul = pt > 0 ? 1.f : 0.f;         // (Gb = 0 for the first tile)
 #pragma unroll
             for (int q = 0; q < NT; ++q) acc[pi][q] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int m = 0; m < NKH; ++m) {
                 const int c0 = 16 * (m0 + m) + 4 * lg;
                 const floatx4 gr = *reinterpret_cast<const floatx4 *>(&sG[row][c0]);
-                const floatx4 gb = *reinterpret_cast<const floatx4 *>(&sG[brow][c0]) * bmul;
+                const floatx4 gb = *reinterpret_cast<const floatx4 *>(&sRef[pt][c0]);
                 const floatx4 kr = *reinterpret_cast<const floatx4 *>(&sK[row][c0]);
                 floatx4 a = araw[pi][m] * (mat == 1 ? kr : floatx4{1.f, 1.f, 1.f, 1.f});
                 a *= exp2v(gr - gb);

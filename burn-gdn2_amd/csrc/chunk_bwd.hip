@@ -690,7 +690,8 @@ __global__ __launch_bounds__(256, K >= 256 ? 1 : 2) void bwd_vprod_kernel(BwdPar
 // row tile's reference Gb_p (G at the end of tile p-1):
 //   E_rs = exp(G_r - Gb_p) exp(Gb_p - G_s),
 // both factors <= 1 off the diagonal block; on it the second is bounded by
-// the tile's decay span, and channels whose span exceeds 96 take the exact
+// the tile's decay span. Channels whose span lies in (96, 192] move Gb_p to
+// the middle of the tile's range, and channels above 192 take the exact
 // pairwise terms instead.  Then, per (row r, channel c):
 //   dq = scale (e^G dQG + rq),  dkb = e^G dRk + rkb,  db = dkb k
 //   dk = e^{G_last - G} dKd + ck + dkb b
@@ -756,12 +757,18 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
         __syncthreads();
     }
     const float gl = sG[C - 1][ch];
-    float gb[NT]; // Gb_t: G at the end of tile t-1
-    bool msk[NT]; // diagonal block of tile t beyond the safe span
+    // Gb_t: G at the end of tile t-1, or, for a span in (96, 192], the middle
+    // of tile t's range, (Gb_t + G_end) / 2, as in the forward: the diagonal
+    // factors then lie in [2^-96, 2^96] and the off-diagonal column factors
+    // stay <= 1 (one that underflows drops a term below 2^-30 of its operands)
+    float gb[NT];
+    bool msk[NT]; // diagonal block of tile t beyond 192: exact pairwise terms
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        gb[t] = t ? sG[16 * t - 1][ch] : 0.f;
-        msk[t] = gb[t] - sG[16 * t + 15][ch] > 96.f;
+        const float b0 = t ? sG[16 * t - 1][ch] : 0.f, ge = sG[16 * t + 15][ch];
+        const float span = b0 - ge;
+        msk[t] = span > 192.f;
+        gb[t] = (span > 96.f && span <= 192.f) ? 0.5f * (b0 + ge) : b0;
     }
 
     float *oq, *okk, *og, *ob;

@@ -50,8 +50,31 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}g{c[6][0]}" for c in CASES])
-def test_chunk_matches_recurrence(gpu, case):
+# Decays whose 16-token spans fall mostly in (96, 192] log2 units: the diagonal
+# score blocks' mid-tile reference (the ranges around them reach both other
+# regimes, the boundary reference below 96 and the exact pairwise path above 192)
+MID_CASES = [
+    (1, 2, 2, 200, 128, 128, (-9.0, -3.0), 1.0, 0.5),
+    (1, 2, 2, 256, 128, 128, (-14.0, -0.05), 1.0, 0.5),
+    (1, 1, 2, 150, 64, 64, (-9.0, -3.0), 2.0, 0.5),       # GVA, negative eigenvalues
+    (1, 2, 2, 130, 256, 256, (-9.0, -3.0), 1.0, 0.5),
+    (1, 2, 2, 97, 32, 64, (-14.0, -0.05), 1.0, 0.5),
+    (1, 1, 2, 140, 64, 96, (-9.0, -3.0), 2.0, 0.5),
+    (1, 2, 2, 130, 128, 192, (-14.0, -0.05), 1.0, 0.5),
+]
+
+
+def span_regimes(g, T):
+    """(tile, channel) pairs whose decay span over the 16-token tile,
+    -sum(g) log2(e), is at most 96, in (96, 192] and above 192 (tiles start
+    at multiples of 16, since the 64-token chunks do)."""
+    gt = np.asarray(g, np.float64)
+    gt = np.pad(gt, [(0, 0), (0, 0), (0, (-T) % 16), (0, 0)])
+    span = -gt.reshape(gt.shape[0], gt.shape[1], -1, 16, gt.shape[3]).sum(3) * np.log2(np.e)
+    return int((span <= 96).sum()), int(((span > 96) & (span <= 192)).sum()), int((span > 192).sum())
+
+
+def _check_case(gpu, case):
     import gdn2_amd
 
     B, Hk, HV, T, K, V, (glo, ghi), bhi, s0 = case
@@ -72,6 +95,25 @@ def test_chunk_matches_recurrence(gpu, case):
     o32, S32 = O.chunk_wy_f32(q, k, v, g, b, w, S0=S0, scale=scale, chunk_size=64)
     if np.all(np.isfinite(o32)) and np.all(np.isfinite(S32)):
         assert maxabs(o.cpu().numpy(), o32) < TOL and maxabs(S.cpu().numpy(), S32) < TOL
+    return g
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}g{c[6][0]}" for c in CASES])
+def test_chunk_matches_recurrence(gpu, case):
+    _check_case(gpu, case)
+
+
+@pytest.mark.parametrize("case", MID_CASES,
+                         ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}g{c[6][0]}" for c in MID_CASES])
+def test_chunk_mid_span_diagonal(gpu, case):
+    """Diagonal score blocks whose decay spans lie between the boundary
+    reference's bound (96) and the exact pairwise path (above 192)."""
+    g = _check_case(gpu, case)
+    lo, mid, hi = span_regimes(g, case[3])
+    print(f"(tile, channel) spans <= 96: {lo}, (96, 192]: {mid}, > 192: {hi}")
+    assert mid > (lo + mid + hi) // 2
+    if case[6][0] < -10:  # the wide range reaches the other two regimes as well
+        assert lo > 0 and hi > 0
 
 
 def _base_workspace_bytes(B, HV, T, K, V):

@@ -51,11 +51,13 @@ CASES = [
 ]
 
 
-# Decays whose 16-token span passes the kernels' safe span of 2^96 (in the
-# forward's chunk-intra and the backward's decay pass): those channels of a
-# diagonal 16 x 16 block leave the MFMA product and are added exactly, pair by
-# pair.  |g| up to 31 per token (the long-context configuration's decays) puts
-# nearly every channel there; U(-6, -2) mixes masked and unmasked channels.
+# Decays whose 16-token spans leave the diagonal score blocks' boundary
+# reference (spans above 96 in log2 units, in the forward's chunk-intra and the
+# backward's decay pass): spans in (96, 192] move the reference to the middle
+# of the tile's range, larger ones leave the MFMA product and are added
+# exactly, pair by pair.  |g| up to 31 per token (the long-context
+# configuration's decays) puts most channels in the pairwise path; U(-6, -2)
+# mixes the two references; U(-14, -0.05) reaches all three regimes.
 STRONG_CASES = [
     (1, 1, 1, 200, 128, 128, (-31.0, -0.05), 1.0, 0.5, True),
     (1, 2, 2, 130, 64, 64, (-31.0, -0.05), 1.0, 0.5, True),     # K = 64, ragged last chunk
@@ -63,20 +65,19 @@ STRONG_CASES = [
     (1, 1, 2, 100, 64, 256, (-31.0, -0.05), 1.0, 0.5, True),    # GVA, V = 4K
     (2, 2, 2, 190, 128, 128, (-6.0, -2.0), 1.0, 0.5, True),     # masked and unmasked channels mixed
     (1, 1, 1, 2100, 128, 128, (-6.0, -2.0), 2.0, 1.0, True),    # segmented, negative eigenvalues
+    (1, 2, 2, 150, 128, 128, (-14.0, -0.05), 1.0, 0.5, True),   # all three regimes
+    (1, 1, 2, 130, 64, 256, (-14.0, -0.05), 2.0, 0.5, True),    # all three, GVA, negative eigenvalues
 ]
 
-SAFE_SPAN_LOG2 = 96.0
-
-
-def masked_tiles(g, T):
-    """Number of (16-token tile, channel) pairs whose decay span over the tile,
-    -sum(g) log2(e), exceeds the kernels' safe span (tiles start at multiples
-    of 16, since the 64-token chunks do)."""
+def span_regimes(g, T):
+    """(tile, channel) pairs whose decay span over the 16-token tile,
+    -sum(g) log2(e), is at most 96 (boundary reference), in (96, 192] (mid-tile
+    reference) and above 192 (exact pairwise terms); tiles start at multiples
+    of 16, since the 64-token chunks do."""
     gt = np.asarray(g, np.float64)
-    pad = (-T) % 16
-    gt = np.pad(gt, [(0, 0), (0, 0), (0, pad), (0, 0)])
+    gt = np.pad(gt, [(0, 0), (0, 0), (0, (-T) % 16), (0, 0)])
     span = -gt.reshape(gt.shape[0], gt.shape[1], -1, 16, gt.shape[3]).sum(3) * np.log2(np.e)
-    return int((span > SAFE_SPAN_LOG2).sum()), int(span.size)
+    return int((span <= 96).sum()), int(((span > 96) & (span <= 192)).sum()), int((span > 192).sum())
 
 
 def _run_case(gpu, case):
@@ -112,14 +113,19 @@ def test_chunk_bwd_matches_adjoint(gpu, case):
 @pytest.mark.parametrize("case", STRONG_CASES,
                          ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}g{c[6][0]}" for c in STRONG_CASES])
 def test_chunk_bwd_strong_decay(gpu, case):
-    """The exact pairwise diagonal terms of the training forward's chunk-intra
-    and of the backward's decay pass: every case has masked channels."""
+    """The diagonal blocks' mid-tile reference and exact pairwise terms of the
+    training forward's chunk-intra and of the backward's decay pass: each
+    case reaches the regimes its decay range is chosen for."""
     g = _run_case(gpu, case)
-    n, tot = masked_tiles(g, case[3])
-    print(f"masked (tile, channel) pairs: {n} of {tot}")
-    assert n > 0
-    if case[6][0] > -10:  # the mixed range also keeps channels in the MFMA product
-        assert n < tot
+    lo, mid, hi = span_regimes(g, case[3])
+    print(f"(tile, channel) spans <= 96: {lo}, (96, 192]: {mid}, > 192: {hi}")
+    glo = case[6][0]
+    if glo < -10:
+        assert hi > 0
+    if glo > -20:
+        assert mid > 0
+    if glo > -10:
+        assert lo > 0
 
 
 def test_chunk_bwd_strided_views(gpu):
@@ -166,7 +172,7 @@ def test_chunk_bwd_head_dim_256(gpu, case):
 
     g = _run_case(gpu, case)
     if case[6][0] < -10:
-        assert masked_tiles(g, case[3])[0] > 0
+        assert span_regimes(g, case[3])[2] > 0
     B, Hk, HV, T, K, V, (glo, ghi), bhi, s0, dst = case
     rng = np.random.default_rng(3000 + T + K + V)
     q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=glo, g_hi=ghi, b_hi=bhi)
