@@ -754,7 +754,9 @@ def bench_step(torch, G, args, dev):
     copy_same = decode_copy_roof(torch, dev, bytes_step, steps, nrot)
     del blocks, states, q, k, g, b, v, w, out
     torch.cuda.empty_cache()
+    tr = load_traffic("step_b64_traffic.json") if B == 64 else None
     return {"workload": f"bare one-token step (fused_step), B={B} H=16 K=V=128, state in place",
+            "traffic": None if tr is None else tr.get("hbm_bytes_per_launch"),
             "kernel": "gdn2_recurrent_step_f32", "batch": B, "tokens_per_s": B / (ms / 1e3),
             "ms_per_token_step": ms, "bytes_per_step": bytes_step, "achieved_GBs": gbs, "peak_GBs": PEAK_HBM_GBS,
             "frac_hbm": gbs / PEAK_HBM_GBS, "rotating_state_buffers": nrot, "copy_same_bytes": copy_same,
@@ -946,12 +948,12 @@ def _cpu_model():
 
 
 COPY_BYTES = 1 << 30
-# the inference instances at the benchmarked shape (the backward's training
-# variants, chunk_intra_kernel<..., true> and chunk_inter_kernel<128, 2>, are others)
-KERNELS = {"chunk_intra": "chunk_intra_kernel<128, 128, false>", "chunk_inter": "chunk_inter_kernel<128, 0>",
-           "decode": "decode_fused_kernel<128, 128>"}
-BWD_KERNELS = ("chunk_intra_kernel<128, 128, true>", "chunk_inter_kernel<128, 2>", "bwd_inter_kernel<128, 0>",
-               "bwd_vprod_kernel<128, 128>", "bwd_decay_kernel<128, 128>")
+# the inference instances at the benchmarked shape (the training variants,
+# chunk_intra_kernel<..., true> and chunk_inter_kernel<128, 2 or 4, 4>, are others)
+KERNELS = {"chunk_intra": "chunk_intra_kernel<128, 128, false>", "chunk_inter": "chunk_inter_kernel<128, 0, 4>",
+           "decode": "decode_fused_kernel<128, 128>", "step": "step_kernel<128, 128>"}
+BWD_KERNELS = ("chunk_intra_kernel<128, 128, true>", "chunk_inter_kernel<128, 2, 4>", "chunk_inter_kernel<128, 4, 4>",
+               "bwd_inter_kernel<128, 0>", "bwd_vprod_kernel<128, 128>", "bwd_decay_kernel<128, 128>")
 
 
 def _short(name):
@@ -1017,7 +1019,7 @@ def timed_summary(path, warmup, steps, decode_steps):
     print("| kernel | timed dispatches | mean us | min us | max us |")
     print("|---|---|---|---|---|")
     for label, key, skip, take in (("chunk_intra", "chunk_intra_kernel<128, 128, false>", warmup, steps),
-                                   ("chunk_inter", "chunk_inter_kernel<128, 0>", warmup, steps),
+                                   ("chunk_inter", "chunk_inter_kernel<128, 0, 4>", warmup, steps),
                                    ("decode", "decode_fused_kernel<128, 128>", 8, decode_steps),
                                    ("decode C4", "decode_fused_kernel<128, 256>", 8, decode_steps),
                                    ("bare step", "step_kernel<128, 128>", 8, decode_steps)):
@@ -1099,7 +1101,7 @@ def mix_summary(csv1, csv2, n_xcc=8, n_simd=1024):
         waves = mean(key, "SQ_WAVES")
         busy = [d["SQ_VALU_MFMA_BUSY_CYCLES"] / (d["GRBM_GUI_ACTIVE"] / n_xcc * n_simd)
                 for d in per[key].values() if d.get("GRBM_GUI_ACTIVE") and "SQ_VALU_MFMA_BUSY_CYCLES" in d]
-        busy_s = f"{100 * sum(busy) / len(busy):.1f} %" if busy and key != "decode" else "-"
+        busy_s = f"{100 * sum(busy) / len(busy):.1f} %" if busy and key not in ("decode", "step") else "-"
         wait = mean(key, "SQ_WAIT_INST_ANY") / mean(key, "SQ_WAVE_CYCLES")
         pw = lambda n: mean(key, n) / waves
         print(f"| {key} | {waves:.0f} | {pw('SQ_INSTS_VALU'):.0f} | {pw('SQ_INSTS_MFMA'):.0f} | {pw('SQ_INSTS_SALU'):.0f} | "
@@ -1147,7 +1149,7 @@ def traffic_summary(fetch_csv, write_csv):
         out[key] = {"hbm_bytes_per_launch": rd + wr, "read_bytes": rd, "write_bytes": wr,
                     "dispatches": len(fv), "fetch_factor": f_fac, "write_factor": w_fac}
         print(f"| `{key}` | {len(fv)} | {rd / 1e9:.3f} | {wr / 1e9:.3f} | {(rd + wr) / 1e9:.3f} |")
-        suffix = "b64" if key == "decode" else "b8_t4096"
+        suffix = "b64" if key in ("decode", "step") else "b8_t4096"
         with open(os.path.join(ROOT, "profiles", f"{key}_{suffix}_traffic.json"), "w") as fh:
             json.dump(out[key], fh, indent=1)
     # the chunked backward's kernels (bench.py's backward entry), printed only
