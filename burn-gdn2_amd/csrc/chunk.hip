@@ -21,9 +21,12 @@
 //    with 96 < span <= 192 move the reference (for their whole row tile) to
 //    the middle of the tile's range, Gb_p - span / 2, so that both diagonal
 //    factors lie in [2^-96, 2^96] (the bounds of the split above): still one
-//    MFMA product, whose discarded upper triangle may overflow. Channels above 192 (e.g. |g| ~ 30
-//    per token) are zeroed in the MFMA operand and added exactly with
-//    pairwise exp2(G_r - G_s), r >= s.
+//    MFMA product, whose discarded upper triangle may overflow.  Channels
+//    above 192 (e.g. |g| ~ 30 per token) are zeroed in that product.  Where
+//    both 8-token halves of the tile span at most 192 they are formed from
+//    half-block products (each half's own mid reference for its diagonal
+//    8x8 blocks, G at row 7 for rows 8-15 x columns 0-7); otherwise they are
+//    added exactly with pairwise exp2(G_r - G_s), r >= s.
 //  * WY solve per 16-row tile (src/forward.rs:192-261): the 16x16 diagonal
 //    blocks of I + A_kk are inverted by forward substitution and the tiles
 //    are eliminated in order, never as one 64x64 solve.
@@ -76,6 +79,7 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
     __shared__ __attribute__((aligned(16))) float sAinv[NT][16][20];
     __shared__ float sTot[NSEG][K];
     __shared__ uint32_t sMask[NT][K / 32]; // diagonal-tile channels with span > kSafeSpanMid
+    __shared__ uint32_t sPair[NT][K / 32]; // those of them with a half-tile span > kSafeSpanMid
     __shared__ float sRef[NT][K];          // the score products' reference G per row tile
     float(*sK)[KP] = reinterpret_cast<float(*)[KP]>(sR);
     float(*sQG)[KP] = reinterpret_cast<float(*)[KP]>(sR);
@@ -143,7 +147,7 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
             vals[i] = acc;
         }
         sTot[seg][c] = acc;
-        if (tid < NT * (K / 32)) (&sMask[0][0])[tid] = 0u;
+        if (tid < NT * (K / 32)) (&sMask[0][0])[tid] = (&sPair[0][0])[tid] = 0u;
 #pragma unroll
         for (int i = 0; i < KF4; ++i) {
             const int f = i * 512 + tid, row = f / (K / 4), c4 = f % (K / 4);
@@ -193,11 +197,17 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
     // diagonal factors then lie in [2^-96, 2^96]; in the off-diagonal blocks
     // the row factor is at most 2^96 and the column factor at most 1, and a
     // column factor that underflows drops a term below 2^-30 |row operand k|.
+    // Spans above kSafeSpanMid leave the diagonal block's MFMA product (sMask):
+    // if both 8-token halves span at most kSafeSpanMid, the block is formed from
+    // three half-block products (below); else from exact pairwise terms (sPair).
     for (int idx = tid; idx < NT * K; idx += 512) {
         const int pt = idx / K, c = idx % K;
-        const float gb = pt ? sG[16 * pt - 1][c] : 0.f, ge = sG[16 * pt + 15][c];
+        const float gb = pt ? sG[16 * pt - 1][c] : 0.f, g7 = sG[16 * pt + 7][c], ge = sG[16 * pt + 15][c];
         const float span = gb - ge;
-        if (span > kSafeSpanMid) atomicOr(&sMask[pt][c >> 5], 1u << (c & 31));
+        if (span > kSafeSpanMid) {
+            atomicOr(&sMask[pt][c >> 5], 1u << (c & 31));
+            if (gb - g7 > kSafeSpanMid || g7 - ge > kSafeSpanMid) atomicOr(&sPair[pt][c >> 5], 1u << (c & 31));
+        }
         sRef[pt][c] = (span > kSafeSpan && span <= kSafeSpanMid) ? 0.5f * (gb + ge) : gb;
     }
     __syncthreads();
@@ -239,6 +249,45 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
             const int row = 16 * pt + lr;
 #pragma unroll
             for (int q = 0; q < NT; ++q) acc[pi][q] = floatx4{0.f, 0.f, 0.f, 0.f};
+            // Diagonal block, channels split into 8-token halves: rows and columns
+            // 0-7 and 8-15 each with the middle of their half's range as reference
+            // (one product, whose cross-half terms are discarded), rows 8-15 x
+            // columns 0-7 with G at row 7 (both factors <= 1).  A lane's row and
+            // column are the same token, 16 pt + lr.  These terms start the
+            // diagonal block's accumulator; the products below leave the
+            // channels out.
+            {
+                floatx4 dsp = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int m = 0; m < NKH; ++m) {
+                    const int wix = (16 * (m0 + m)) >> 5, wsh = (16 * (m0 + m)) & 31;
+                    const uint32_t w16s = ((__builtin_amdgcn_readfirstlane(sMask[pt][wix]) &
+                                            ~__builtin_amdgcn_readfirstlane(sPair[pt][wix])) >> wsh) & 0xffffu;
+                    if (w16s == 0u) continue; // wave-uniform
+                    const int c0 = 16 * (m0 + m) + 4 * lg;
+                    const uint32_t sl = ((sMask[pt][c0 >> 5] & ~sPair[pt][c0 >> 5]) >> (c0 & 31)) & 0xfu;
+                    floatx4 aac = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if (((w16s >> j) & 0x1111u) == 0u) continue; // none of channels 16 (m0 + m) + 4 g + j
+                        const int c = c0 + j;
+                        const float gr = sG[row][c], kr = sK[row][c], g7 = sG[16 * pt + 7][c];
+                        const float ref = lr < 8 ? 0.5f * (sRef[pt][c] + g7) : 0.5f * (g7 + sG[16 * pt + 15][c]);
+                        const float raw = mat == 1 ? araw[pi][m][j] * kr : araw[pi][m][j];
+                        const bool sp = (sl >> j) & 1u;
+                        const float a1 = sp ? raw * fast_exp2(gr - ref) : 0.f;
+                        const float b1 = sp ? kr * fast_exp2(ref - gr) : 0.f;
+                        const float a2 = (sp && lr >= 8) ? raw * fast_exp2(gr - g7) : 0.f;
+                        const float b2 = (sp && lr < 8) ? kr * fast_exp2(g7 - gr) : 0.f;
+                        aac = mfma16(a1, b1, aac);
+                        dsp = mfma16(a2, b2, dsp); // exactly zero outside rows 8-15 x columns 0-7
+                    }
+                    if ((lg < 2) == (lr < 8)) dsp += aac; // rows 4 lg + i and column lr in one half
+                }
+#pragma unroll
+                for (int q = 0; q < NT; ++q)
+                    if (q == pt) acc[pi][q] = dsp;
+            }
 #pragma unroll
             for (int m = 0; m < NKH; ++m) {
                 const int c0 = 16 * (m0 + m) + 4 * lg;
@@ -277,7 +326,8 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
                 }
             }
         }
-        // Diagonal blocks, channels (of this half) outside the safe span: exact
+        // Diagonal blocks, channels (of this half) outside the mid-tile reference's
+        // span: half-block products where both halves allow it, else exact
         // pairwise terms.  The row operand q or b of channel c and row 16 pt + r
         // is already in this wave's registers: component c % 4 of
         // araw[pi][c / 16 - m0] in lane 16 ((c % 16) / 4) + r.  It is gathered
@@ -296,16 +346,16 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
 #pragma unroll
             for (int pi = 0; pi < 2; ++pi) {
                 const int pt = pi ? (NT - 1 - half) : half;
-                // mask words of one channel half (K = 32: the half's 16 bits of word 0)
+                // pairwise mask words of one channel half (K = 32: the half's 16 bits of word 0)
                 constexpr int NWD = K >= 64 ? K / 64 : 1;
-                uint32_t mwh[NWD];
+                uint32_t pwh[NWD];
                 uint32_t anyw = 0u;
 #pragma unroll
                 for (int x = 0; x < NWD; ++x) {
-                    uint32_t wd = __builtin_amdgcn_readfirstlane(sMask[pt][K >= 64 ? kh * NWD + x : 0]);
-                    if (K < 64) wd = (wd >> (16 * kh)) & 0xffffu;
-                    mwh[x] = wd;
-                    anyw |= wd;
+                    uint32_t wp = __builtin_amdgcn_readfirstlane(sPair[pt][K >= 64 ? kh * NWD + x : 0]);
+                    if (K < 64) wp = (wp >> (16 * kh)) & 0xffffu;
+                    pwh[x] = wp;
+                    anyw |= wp;
                 }
                 if (anyw == 0u) continue; // wave-uniform
                 floatx4 dacc = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -314,12 +364,13 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
                 bool rowok[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) rowok[i] = mat == 0 ? (4 * lg + i >= lr) : (4 * lg + i > lr);
-                // two channels c0, c0 + 1 (c0 = 16 (m0 + m) + 4 cg + 2 jh) per step: their
-                // G and k come in 8-byte LDS reads, their row operands are
-                // components 2 jh, 2 jh + 1 of araw[pi][m] in lane group cg
+                // two channels c0, c0 + 1 (c0 = 16 (m0 + m) + 4 cg + 2 jh) per step when
+                // both are masked (their G and k in 8-byte LDS reads), else the one
+                // that is; their row operands are components 2 jh, 2 jh + 1 of
+                // araw[pi][m] in lane group cg
 #pragma unroll
                 for (int m = 0; m < NKH; ++m) {
-                    const uint32_t w16 = (mwh[(16 * m) >> 5] >> ((16 * m) & 31)) & 0xffffu;
+                    const uint32_t w16 = (pwh[(16 * m) >> 5] >> ((16 * m) & 31)) & 0xffffu;
                     if (w16 == 0u) continue; // wave-uniform
                     for (int cg = 0; cg < 4; ++cg) {
 #pragma unroll
@@ -327,6 +378,41 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
                             const uint32_t bits = (w16 >> (4 * cg + 2 * jh)) & 0x3u;
                             if (bits == 0u) continue; // wave-uniform
                             const int c0 = 16 * (m0 + m) + 4 * cg + 2 * jh;
+                            // All of a step's loads are issued first and pinned (the
+                            // compiler would otherwise sink a load used only in a
+                            // lane-selected term into a divergent branch with its
+                            // own wait), then the terms are formed.
+                            if (bits != 0x3u) { // one channel of the pair (wave-uniform): it alone
+                                const int jj = bits >> 1, c = c0 + jj;
+                                const float gs1 = sG[srow][c], ks1 = sK[srow][c];
+                                float o = 0.f;
+                                if constexpr (!TRAIN) o = jj ? araw[pi][m][2 * jh + 1] : araw[pi][m][2 * jh];
+                                float x[4], kx[4], gx[4];
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) {
+                                    const int r = 4 * lg + i;
+                                    const int rrow = 16 * pt + r;
+                                    if constexpr (TRAIN)
+                                        x[i] = bld1(mat == 0 ? Rq : Rb, lg_q + (16 * pt + i) * rq + c);
+                                    else
+                                        x[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                                             4 * (16 * cg + r), __builtin_bit_cast(int, o)));
+                                    kx[i] = sK[rrow][c];
+                                    gx[i] = sG[rrow][c];
+                                }
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) {
+                                    kx[i] = pin(kx[i]);
+                                    gx[i] = pin(gx[i]);
+                                }
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) {
+                                    const float xi = mat == 1 ? x[i] * kx[i] : x[i];
+                                    const float d = rowok[i] ? gx[i] - gs1 : -__builtin_inff();
+                                    dacc[i] += xi * ks1 * fast_exp2(d);
+                                }
+                                continue;
+                            }
                             const float2 gs = *reinterpret_cast<const float2 *>(&sG[srow][c0]);
                             const float2 ks = *reinterpret_cast<const float2 *>(&sK[srow][c0]);
                             float o0 = 0.f, o1 = 0.f;
@@ -334,31 +420,37 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
                                 o0 = araw[pi][m][2 * jh]; // scalars (see above)
                                 o1 = araw[pi][m][2 * jh + 1];
                             }
+                            float x0[4], x1[4];
+                            float2 gr[4], kr[4];
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
                                 const int r = 4 * lg + i;
                                 const int rrow = 16 * pt + r;
-                                const float2 gr = *reinterpret_cast<const float2 *>(&sG[rrow][c0]);
-                                float x0, x1;
                                 if constexpr (TRAIN) { // row rrow of q or b, channels c0, c0 + 1
-                                    x0 = bld1(mat == 0 ? Rq : Rb, lg_q + (16 * pt + i) * rq + c0);
-                                    x1 = bld1(mat == 0 ? Rq : Rb, lg_q + (16 * pt + i) * rq + c0 + 1);
+                                    x0[i] = bld1(mat == 0 ? Rq : Rb, lg_q + (16 * pt + i) * rq + c0);
+                                    x1[i] = bld1(mat == 0 ? Rq : Rb, lg_q + (16 * pt + i) * rq + c0 + 1);
                                 } else {
-                                    x0 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
-                                                                       4 * (16 * cg + r), __builtin_bit_cast(int, o0)));
-                                    x1 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
-                                                                       4 * (16 * cg + r), __builtin_bit_cast(int, o1)));
+                                    x0[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                                          4 * (16 * cg + r), __builtin_bit_cast(int, o0)));
+                                    x1[i] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                                          4 * (16 * cg + r), __builtin_bit_cast(int, o1)));
                                 }
-                                if (mat == 1) {
-                                    const float2 kr = *reinterpret_cast<const float2 *>(&sK[rrow][c0]);
-                                    x0 *= kr.x;
-                                    x1 *= kr.y;
-                                }
-                                // branch-free: exp2(-inf) = 0 outside the triangle and for the
-                                // channels whose terms the MFMA product already holds
-                                const float d0 = (rowok[i] && (bits & 1u)) ? gr.x - gs.x : -__builtin_inff();
-                                const float d1 = (rowok[i] && (bits & 2u)) ? gr.y - gs.y : -__builtin_inff();
-                                dacc[i] += x0 * ks.x * fast_exp2(d0) + x1 * ks.y * fast_exp2(d1);
+                                gr[i] = *reinterpret_cast<const float2 *>(&sG[rrow][c0]);
+                                kr[i] = *reinterpret_cast<const float2 *>(&sK[rrow][c0]);
+                            }
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                gr[i] = pin(gr[i]);
+                                kr[i] = pin(kr[i]);
+                            }
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const float xa = mat == 1 ? x0[i] * kr[i].x : x0[i];
+                                const float xb = mat == 1 ? x1[i] * kr[i].y : x1[i];
+                                // branch-free: exp2(-inf) = 0 outside the triangle
+                                const float d0 = rowok[i] ? gr[i].x - gs.x : -__builtin_inff();
+                                const float d1 = rowok[i] ? gr[i].y - gs.y : -__builtin_inff();
+                                dacc[i] += xa * ks.x * fast_exp2(d0) + xb * ks.y * fast_exp2(d1);
                             }
                         }
                     }

@@ -69,6 +69,18 @@ __device__ __forceinline__ floatx4 mfma4n(float4 a, floatx4 b, floatx4 c) {
 // reads more than once.
 __device__ __forceinline__ void st_stream(floatx4 *dst, floatx4 v) { __builtin_nontemporal_store(v, dst); }
 
+// Pins a loaded value in a register where it is loaded: the compiler would
+// otherwise sink a load used only under a lane condition into a divergent
+// branch with its own wait, serialising the loads of an unrolled loop.
+__device__ __forceinline__ float pin(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+__device__ __forceinline__ float2 pin(float2 x) {
+    asm volatile("" : "+v"(x.x), "+v"(x.y));
+    return x;
+}
+
 __device__ __forceinline__ floatx4 exp2v(floatx4 x) {
     return floatx4{fast_exp2(x[0]), fast_exp2(x[1]), fast_exp2(x[2]), fast_exp2(x[3])};
 }

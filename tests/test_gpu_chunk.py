@@ -51,8 +51,8 @@ CASES = [
 
 
 # Decays whose 16-token spans fall mostly in (96, 192] log2 units: the diagonal
-# score blocks' mid-tile reference (the ranges around them reach both other
-# regimes, the boundary reference below 96 and the exact pairwise path above 192)
+# score blocks' mid-tile reference (the wider ranges also reach the boundary
+# reference below 96 and the half-block products above 192)
 MID_CASES = [
     (1, 2, 2, 200, 128, 128, (-9.0, -3.0), 1.0, 0.5),
     (1, 2, 2, 256, 128, 128, (-14.0, -0.05), 1.0, 0.5),
@@ -65,13 +65,17 @@ MID_CASES = [
 
 
 def span_regimes(g, T):
-    """(tile, channel) pairs whose decay span over the 16-token tile,
-    -sum(g) log2(e), is at most 96, in (96, 192] and above 192 (tiles start
-    at multiples of 16, since the 64-token chunks do)."""
+    """(tile, channel) pairs by the decay span of the 16-token tile,
+    -sum(g) log2(e): at most 96 (boundary reference), in (96, 192] (mid-tile
+    reference), above 192 with both 8-token halves at most 192 (half-block
+    products) and the rest (exact pairwise terms).  Tiles start at multiples
+    of 16, since the 64-token chunks do."""
     gt = np.asarray(g, np.float64)
     gt = np.pad(gt, [(0, 0), (0, 0), (0, (-T) % 16), (0, 0)])
-    span = -gt.reshape(gt.shape[0], gt.shape[1], -1, 16, gt.shape[3]).sum(3) * np.log2(np.e)
-    return int((span <= 96).sum()), int(((span > 96) & (span <= 192)).sum()), int((span > 192).sum())
+    half = -gt.reshape(gt.shape[0], gt.shape[1], -1, 2, 8, gt.shape[3]).sum(4) * np.log2(np.e)
+    span, hmax = half.sum(3), half.max(3)
+    return (int((span <= 96).sum()), int(((span > 96) & (span <= 192)).sum()),
+            int(((span > 192) & (hmax <= 192)).sum()), int(((span > 192) & (hmax > 192)).sum()))
 
 
 def _check_case(gpu, case):
@@ -100,7 +104,11 @@ def _check_case(gpu, case):
 
 @pytest.mark.parametrize("case", CASES, ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}g{c[6][0]}" for c in CASES])
 def test_chunk_matches_recurrence(gpu, case):
-    _check_case(gpu, case)
+    g = _check_case(gpu, case)
+    if case[6][0] < -20:  # |g| up to 31: half-block products and exact pairwise terms
+        lo, mid, split, pair = span_regimes(g, case[3])
+        print(f"(tile, channel) half-block: {split}, pairwise: {pair}")
+        assert split > 0 and pair > 0
 
 
 @pytest.mark.parametrize("case", MID_CASES,
@@ -109,11 +117,11 @@ def test_chunk_mid_span_diagonal(gpu, case):
     """Diagonal score blocks whose decay spans lie between the boundary
     reference's bound (96) and the exact pairwise path (above 192)."""
     g = _check_case(gpu, case)
-    lo, mid, hi = span_regimes(g, case[3])
-    print(f"(tile, channel) spans <= 96: {lo}, (96, 192]: {mid}, > 192: {hi}")
-    assert mid > (lo + mid + hi) // 2
-    if case[6][0] < -10:  # the wide range reaches the other two regimes as well
-        assert lo > 0 and hi > 0
+    lo, mid, split, pair = span_regimes(g, case[3])
+    print(f"(tile, channel) spans <= 96: {lo}, (96, 192]: {mid}, half-block: {split}, pairwise: {pair}")
+    assert mid > (lo + mid + split + pair) // 2
+    if case[6][0] < -10:  # the wide range reaches the boundary reference and the half-block products
+        assert lo > 0 and split > 0
 
 
 def _base_workspace_bytes(B, HV, T, K, V):

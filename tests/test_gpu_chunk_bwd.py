@@ -54,10 +54,11 @@ CASES = [
 # Decays whose 16-token spans leave the diagonal score blocks' boundary
 # reference (spans above 96 in log2 units, in the forward's chunk-intra and the
 # backward's decay pass): spans in (96, 192] move the reference to the middle
-# of the tile's range, larger ones leave the MFMA product and are added
-# exactly, pair by pair.  |g| up to 31 per token (the long-context
-# configuration's decays) puts most channels in the pairwise path; U(-6, -2)
-# mixes the two references; U(-14, -0.05) reaches all three regimes.
+# of the tile's range; larger ones leave the MFMA product, and the forward
+# forms them from half-block products where both 8-token halves span at most
+# 192, else (and the backward always) exactly, pair by pair.  |g| up to 31 per
+# token (the long-context configuration's decays) reaches both of those;
+# U(-6, -2) mixes the two references; U(-14, -0.05) reaches all but the last.
 STRONG_CASES = [
     (1, 1, 1, 200, 128, 128, (-31.0, -0.05), 1.0, 0.5, True),
     (1, 2, 2, 130, 64, 64, (-31.0, -0.05), 1.0, 0.5, True),     # K = 64, ragged last chunk
@@ -70,14 +71,18 @@ STRONG_CASES = [
 ]
 
 def span_regimes(g, T):
-    """(tile, channel) pairs whose decay span over the 16-token tile,
-    -sum(g) log2(e), is at most 96 (boundary reference), in (96, 192] (mid-tile
-    reference) and above 192 (exact pairwise terms); tiles start at multiples
-    of 16, since the 64-token chunks do."""
+    """(tile, channel) pairs by the decay span of the 16-token tile,
+    -sum(g) log2(e): at most 96 (boundary reference), in (96, 192] (mid-tile
+    reference), above 192 with both 8-token halves at most 192 (half-block
+    products) and the rest (exact pairwise terms; the backward's decay pass
+    takes every span above 192 pairwise).  Tiles start at multiples of 16,
+    since the 64-token chunks do."""
     gt = np.asarray(g, np.float64)
     gt = np.pad(gt, [(0, 0), (0, 0), (0, (-T) % 16), (0, 0)])
-    span = -gt.reshape(gt.shape[0], gt.shape[1], -1, 16, gt.shape[3]).sum(3) * np.log2(np.e)
-    return int((span <= 96).sum()), int(((span > 96) & (span <= 192)).sum()), int((span > 192).sum())
+    half = -gt.reshape(gt.shape[0], gt.shape[1], -1, 2, 8, gt.shape[3]).sum(4) * np.log2(np.e)
+    span, hmax = half.sum(3), half.max(3)
+    return (int((span <= 96).sum()), int(((span > 96) & (span <= 192)).sum()),
+            int(((span > 192) & (hmax <= 192)).sum()), int(((span > 192) & (hmax > 192)).sum()))
 
 
 def _run_case(gpu, case):
@@ -117,11 +122,13 @@ def test_chunk_bwd_strong_decay(gpu, case):
     training forward's chunk-intra and of the backward's decay pass: each
     case reaches the regimes its decay range is chosen for."""
     g = _run_case(gpu, case)
-    lo, mid, hi = span_regimes(g, case[3])
-    print(f"(tile, channel) spans <= 96: {lo}, (96, 192]: {mid}, > 192: {hi}")
+    lo, mid, split, pair = span_regimes(g, case[3])
+    print(f"(tile, channel) spans <= 96: {lo}, (96, 192]: {mid}, half-block: {split}, pairwise: {pair}")
     glo = case[6][0]
+    if glo < -20:
+        assert split > 0 and pair > 0
     if glo < -10:
-        assert hi > 0
+        assert split > 0
     if glo > -20:
         assert mid > 0
     if glo > -10:
@@ -172,7 +179,8 @@ def test_chunk_bwd_head_dim_256(gpu, case):
 
     g = _run_case(gpu, case)
     if case[6][0] < -10:
-        assert span_regimes(g, case[3])[2] > 0
+        _, _, split, pair = span_regimes(g, case[3])
+        assert split > 0 and pair > 0
     B, Hk, HV, T, K, V, (glo, ghi), bhi, s0, dst = case
     rng = np.random.default_rng(3000 + T + K + V)
     q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=glo, g_hi=ghi, b_hi=bhi)

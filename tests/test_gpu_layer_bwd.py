@@ -25,11 +25,11 @@ ABS = 1e-7
 pytestmark = pytest.mark.gpu
 
 
-def _close(got, ref, what):
+def _close(got, ref, what, rel=REL):
     e = maxabs(got, ref)
     scale = float(np.abs(ref).max()) if np.size(ref) else 0.0
     print(f"  {what:16s} max|err|={e:.2e} max|ref|={scale:.3e}")
-    assert e <= REL * scale + ABS, what
+    assert e <= rel * scale + ABS, what
 
 
 def _setup(gpu, over, seed=11):
@@ -56,13 +56,14 @@ def _rand_state(G, layer, rng, B, cfg):
     return st, O.OracleState(*(a.astype(np.float64) for a in arrs))
 
 
-def _compare(grads, dx, d_state_in, ref, names):
+def _compare(grads, dx, d_state_in, ref, names, rel=None):
+    """rel: per-parameter relative bounds that replace REL."""
     for n in names:
         g, r = grads.get(n), ref.params[n]
         if r is None:
             assert g is None, n
             continue
-        _close(g, r, n)
+        _close(g, r, n, (rel or {}).get(n, REL))
     if dx is not None:
         _close(dx.cpu().numpy(), ref.dx, "dx")
     if d_state_in is not None:
@@ -254,9 +255,9 @@ def test_strong_decay_layer_backward(gpu):
     """The long-context configuration's decays (dt_bias + 4: per-token |g| of
     tens) on a small layer in chunk mode: the training forward's and the
     backward's diagonal blocks with 16-token decay spans in (96, 192] (the
-    mid-tile reference) and above 192 (exact pairwise terms) are reached
-    (asserted on the layer's own g) and every gradient matches the double
-    adjoint."""
+    mid-tile reference) and above 192 (half-block products and exact pairwise
+    terms) are reached (asserted on the layer's own g) and every gradient
+    matches the double adjoint."""
     import torch
 
     G, cfg, layer, W = _setup(gpu, dict(SMALL, hidden_size=256, num_heads=2, head_dim=128))
@@ -269,10 +270,16 @@ def test_strong_decay_layer_backward(gpu):
     x = torch.from_numpy(xh).to(gpu)
     g = layer.project(x)["g"].cpu().numpy()
     gt = np.pad(g.astype(np.float64), [(0, 0), (0, 0), (0, (-T) % 16), (0, 0)])
-    span = -gt.reshape(B, cfg.num_heads, -1, 16, cfg.head_dim).sum(3) * np.log2(np.e)
-    mid, hi = int(((span > 96) & (span <= 192)).sum()), int((span > 192).sum())
-    print(f"tiles x channels with spans in (96, 192]: {mid}, above 192: {hi}, of {span.size}")
-    assert mid > 0 and hi > 0
+    half = -gt.reshape(B, cfg.num_heads, -1, 2, 8, cfg.head_dim).sum(4) * np.log2(np.e)
+    span, hmax = half.sum(3), half.max(3)
+    mid = int(((span > 96) & (span <= 192)).sum())
+    split, pair = int(((span > 192) & (hmax <= 192)).sum()), int(((span > 192) & (hmax > 192)).sum())
+    print(f"tiles x channels with spans in (96, 192]: {mid}, above 192 in halves of at most 192: {split}, "
+          f"other: {pair}, of {span.size}")
+    assert mid > 0 and split > 0 and pair > 0
     dx, grads, dsi = layer.backward(x, torch.from_numpy(dh).to(gpu), want_d_state=True)
     ref = O.layer_backward_f64(cfg, W, xh, dh)
-    _compare(grads, dx, dsi, ref, O.WEIGHT_NAMES)
+    # A_log's gradient is sum(dg g) with per-token |g| up to ~28 here: the f32
+    # rounding of dg (seen at ~2e-5 relative in dt_bias's gradient, sum(dg dg/d dt_bias)
+    # with |dg/d dt_bias| <= e^A_log) comes back scaled by |g|, ~1e-4 relative
+    _compare(grads, dx, dsi, ref, O.WEIGHT_NAMES, rel={"a_log": 2.5e-4})
