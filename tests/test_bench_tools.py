@@ -27,7 +27,7 @@ def test_timed_summary_skips_warmups_and_takes_steps(tmp_path, capsys):
     import bench
 
     intra = f"void {NS}chunk_intra_kernel<128, 128, false>(gdn2::ChunkParams)"
-    inter = f"void {NS}chunk_inter_kernel<128, 0>(gdn2::ChunkParams, int)"
+    inter = f"void {NS}chunk_inter_kernel<128, 0, 4>(gdn2::ChunkParams, int)"
     dec = f"void {NS}decode_fused_kernel<128, 128>(gdn2::DecodeParams)"
     pre = "void (anonymous namespace)::stream_copy_kernel(HIP_vector_type<float, 4u>*, long)"
     post = "void (anonymous namespace)::tail_copy_kernel(float*, float const*, long)"
@@ -70,14 +70,14 @@ def test_stats_summary_folds_gemm_kernels(tmp_path, capsys):
     with open(p, "w", newline="") as fh:
         w = csv.DictWriter(fh, fieldnames=["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage"])
         w.writeheader()
-        w.writerow({"Name": f"void {NS}chunk_inter_kernel<128, 0>(gdn2::ChunkParams, int)", "Calls": 2,
+        w.writerow({"Name": f"void {NS}chunk_inter_kernel<128, 0, 4>(gdn2::ChunkParams, int)", "Calls": 2,
                     "TotalDurationNs": 1_200_000, "AverageNs": 600_000, "Percentage": 10.0})
         for i in range(3):
             w.writerow({"Name": f"Cijk_Alik_Bljk_S_B_MT{i}", "Calls": 1, "TotalDurationNs": 3_000_000,
                         "AverageNs": 3_000_000, "Percentage": 30.0})
     bench.stats_summary(str(p))
     out = capsys.readouterr().out
-    assert "| `chunk_inter_kernel<128, 0>` | 2 | 600.0 | 1200.0 | 10.0 |" in out
+    assert "| `chunk_inter_kernel<128, 0, 4>` | 2 | 600.0 | 1200.0 | 10.0 |" in out
     assert "| hipBLASLt GEMM kernels (3 names) | 3 | 3000.0 | 9000.0 | 90.0 |" in out
 
 
@@ -92,7 +92,7 @@ def test_configs_summary_counts_the_first_settled_section_of_each_shape(tmp_path
     import bench
 
     intra = f"void {NS}chunk_intra_kernel<128, 128, false>(gdn2::ChunkParams)"
-    inter = f"void {NS}chunk_inter_kernel<128, 0>(gdn2::ChunkParams, int)"
+    inter = f"void {NS}chunk_inter_kernel<128, 0, 4>(gdn2::ChunkParams, int)"
     pre = "void (anonymous namespace)::stream_copy_kernel(HIP_vector_type<float, 4u>*, long)"
     post = "void (anonymous namespace)::tail_copy_kernel(float*, float const*, long)"
     g = 512 * 64  # 64 chunks
@@ -112,4 +112,4 @@ def test_configs_summary_counts_the_first_settled_section_of_each_shape(tmp_path
     bench.configs_summary(str(p), warmup=1, steps=2)
     out = capsys.readouterr().out
     assert "| `chunk_intra_kernel<128, 128, false>` x 64 | `chunk_intra_kernel<128, 128, false>` | 32768 | 2 | 15.0 |" in out
-    assert "| `chunk_inter_kernel<128, 0>` | 256 | 2 | 55.0 |" in out
+    assert "| `chunk_inter_kernel<128, 0, 4>` | 256 | 2 | 55.0 |" in out
