@@ -177,6 +177,21 @@ hipError_t launch_rmsnorm_gate(float *out, int64_t ld_out, const float *x, int64
                                int64_t ld_gate, const float *gate_bias, const float *weight, int64_t M, int HV, int V,
                                float eps, hipStream_t s);
 hipError_t launch_fill_rows(float *y, int64_t ld, const float *row, int64_t M, int64_t N, hipStream_t s);
+
+// The reference's GVA layout of the key-side operands (src/module.rs:456-468:
+// unsqueeze at 3, repeat rep times, reshape to [B, H rep, T, K]): value head
+// h rep + a at time t reads key head h at time (a T + t) / rep.  Four tensors
+// (q, k, g, b) at once.
+struct GvaParams {
+    const float *src[4];
+    float *dst[4];
+    int64_t B, H, T, K;
+    int rep;
+};
+// dst [B, H rep, T, K] <- src [B, H, T, K] in that layout
+hipError_t launch_gva_expand(const GvaParams &p, hipStream_t s);
+// the adjoint: dst [B, H, T, K] = sum over the rep places each element went to in src [B, H rep, T, K]
+hipError_t launch_gva_fold(const GvaParams &p, hipStream_t s);
 // Reads buf[0, n) (16-byte aligned) to push other data out of the caches; writes
 // nothing but, in theory, sink[0].
 hipError_t launch_cache_sweep(const float *buf, int64_t n, float *sink, hipStream_t s);

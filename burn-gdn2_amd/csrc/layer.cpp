@@ -43,6 +43,9 @@ enum ParamId {
 
 struct Dims {
     int64_t D, H, K, HV, V, kd, vd;
+    // key-side heads of the recurrence's q, k, g, b: H, or HV when they are
+    // laid out as the reference's GVA repeat (GDN2_GVA_REFERENCE, HV > H)
+    int64_t Hq, kq;
 };
 
 Dims dims_of(const gdn2_config &c) {
@@ -54,6 +57,8 @@ Dims dims_of(const gdn2_config &c) {
     d.V = (int64_t)((float)c.head_dim * c.expand_v);
     d.kd = d.H * d.K;
     d.vd = d.HV * d.V;
+    d.Hq = (c.gva_layout == GDN2_GVA_REFERENCE && d.HV > d.H) ? d.HV : d.H;
+    d.kq = d.Hq * d.K;
     return d;
 }
 
@@ -198,19 +203,47 @@ namespace {
 
 struct Work {
     float *Y, *F, *G, *q, *k, *g, *b, *v, *w, *O, *S0;
+    // the recurrence's key-side operands: q, k, g, b themselves, or their
+    // expansion to the reference's GVA layout [B, HV, T, K] (GDN2_GVA_REFERENCE)
+    float *xq, *xk, *xg, *xb;
     void *chunk;
     size_t chunk_bytes;
 };
 
+// Points the recurrence's key-side operands at q, k, g, b (head repeat) or
+// at the four expansion buffers that follow in `base` (reference layout),
+// and returns the bytes those take.
+size_t carve_expanded(const Dims &d, int64_t M, char *base, Work *wk) {
+    if (d.Hq == d.H) {
+        wk->xq = wk->q; wk->xk = wk->k; wk->xg = wk->g; wk->xb = wk->b;
+        return 0;
+    }
+    const size_t n = align256(sizeof(float) * M * d.kq);
+    float **dst[4] = {&wk->xq, &wk->xk, &wk->xg, &wk->xb};
+    for (int i = 0; i < 4; ++i) *dst[i] = base ? reinterpret_cast<float *>(base + i * n) : nullptr;
+    return 4 * n;
+}
+
+// The reference's GVA layout of q, k, g, b (nothing under head repeat).
+gdn2_status expand_keys(const Dims &d, int64_t B, int64_t T, const Work &wk, hipStream_t s) {
+    if (d.Hq == d.H) return GDN2_OK;
+    GvaParams gp{};
+    gp.src[0] = wk.q; gp.src[1] = wk.k; gp.src[2] = wk.g; gp.src[3] = wk.b;
+    gp.dst[0] = wk.xq; gp.dst[1] = wk.xk; gp.dst[2] = wk.xg; gp.dst[3] = wk.xb;
+    gp.B = B; gp.H = d.H; gp.T = T; gp.K = d.K; gp.rep = (int)(d.HV / d.H);
+    GDN2_HIP_CHECK(launch_gva_expand(gp, s));
+    return GDN2_OK;
+}
+
 gdn2_chunk_args chunk_args_for(const gdn2_layer &L, int64_t B, int64_t T, const Work &wk, float *S) {
     const Dims &d = L.d;
     gdn2_chunk_args a{};
-    a.q = wk.q; a.k = wk.k; a.g = wk.g; a.b = wk.b; a.v = wk.v; a.w = wk.w;
+    a.q = wk.xq; a.k = wk.xk; a.g = wk.xg; a.b = wk.xb; a.v = wk.v; a.w = wk.w;
     a.state = S; a.out = wk.O;
-    a.batch = B; a.num_heads = d.H; a.num_v_heads = d.HV; a.seq_len = T; a.head_dim = d.K; a.head_v_dim = d.V;
-    // q, k, g, b [B, H, T, K] and v, w [B, HV, T, V] (head-major, so that a
+    a.batch = B; a.num_heads = d.Hq; a.num_v_heads = d.HV; a.seq_len = T; a.head_dim = d.K; a.head_v_dim = d.V;
+    // q, k, g, b [B, Hq, T, K] and v, w [B, HV, T, V] (head-major, so that a
     // chunk's rows are one contiguous block); out [B, T, HV, V] for the norm
-    a.stride_qk_b = d.H * T * d.K; a.stride_qk_h = T * d.K; a.stride_qk_t = d.K;
+    a.stride_qk_b = d.Hq * T * d.K; a.stride_qk_h = T * d.K; a.stride_qk_t = d.K;
     a.stride_vw_b = d.HV * T * d.V; a.stride_vw_h = T * d.V; a.stride_vw_t = d.V;
     a.stride_o_b = T * d.vd; a.stride_o_h = d.V; a.stride_o_t = d.vd;
     a.scale = std::pow((double)d.K, -0.5);
@@ -231,6 +264,7 @@ gdn2_status workspace(gdn2_layer &L, int64_t B, int64_t T, bool need_s0, Work *w
                      need_s0 ? f * B * d.HV * d.K * d.V : 0};
     size_t total = 0;
     for (size_t s : sz) total += align256(s);
+    total += carve_expanded(d, M, nullptr, wk);
     total += align256(chunk_bytes);
     if (total > L.ws_bytes) {
         if (L.ws) {
@@ -250,6 +284,7 @@ gdn2_status workspace(gdn2_layer &L, int64_t B, int64_t T, bool need_s0, Work *w
     }
     wk->S0 = need_s0 ? reinterpret_cast<float *>(base) : nullptr;
     base += align256(sz[10]);
+    base += carve_expanded(d, M, base, wk);
     wk->chunk = base;
     wk->chunk_bytes = chunk_bytes;
     return GDN2_OK;
@@ -299,7 +334,7 @@ gdn2_status project_epilogue(gdn2_layer &L, int64_t B, int64_t T, const float *c
     p.use_short_conv = L.cfg.use_short_conv; p.allow_neg_eigval = L.cfg.allow_neg_eigval;
     p.min_decay = (float)L.cfg.min_decay; p.one_minus_min_decay = (float)(1.0 - L.cfg.min_decay);
     GDN2_HIP_CHECK(launch_project(p, s));
-    return GDN2_OK;
+    return expand_keys(d, B, T, wk, s);
 }
 
 // The scan's arguments for the same operands (state in place).
@@ -378,6 +413,7 @@ extern "C" void gdn2_config_default(gdn2_config *c) {
     c->chunk_size = 64;
     c->has_min_decay = 0;
     c->min_decay = 0.0;
+    c->gva_layout = GDN2_GVA_HEAD_REPEAT;
 }
 
 // Gdn2Config::validate (src/config.rs:71-111): same checks, same order, same messages.
@@ -408,6 +444,8 @@ extern "C" gdn2_status gdn2_config_validate(const gdn2_config *c) {
     if (!(c->norm_eps > 0.0)) return fail(GDN2_EINVAL, "norm_eps must be > 0, got " + fmt_f(c->norm_eps));
     if (c->mode != GDN2_MODE_FUSED_RECURRENT && c->mode != GDN2_MODE_CHUNK)
         return fail(GDN2_EINVAL, "mode must be GDN2_MODE_FUSED_RECURRENT or GDN2_MODE_CHUNK");
+    if (c->gva_layout != GDN2_GVA_HEAD_REPEAT && c->gva_layout != GDN2_GVA_REFERENCE)
+        return fail(GDN2_EINVAL, "gva_layout must be GDN2_GVA_HEAD_REPEAT or GDN2_GVA_REFERENCE");
     return GDN2_OK;
 }
 
@@ -665,11 +703,13 @@ extern "C" gdn2_status gdn2_layer_project_f32(gdn2_layer *L, const float *x, int
     if (has_cache)
         for (int i = 0; i < 3; ++i) conv_in[i] = S->conv[S->cur][i];
     if ((st = project_epilogue(*L, B, T, has_cache ? conv_in : nullptr, wk, s)) != GDN2_OK) return st;
-    const size_t nk = sizeof(float) * M * d.kd, nv = sizeof(float) * M * d.vd;
-    GDN2_HIP_CHECK(hipMemcpyAsync(q, wk.q, nk, hipMemcpyDeviceToDevice, s));
-    GDN2_HIP_CHECK(hipMemcpyAsync(k, wk.k, nk, hipMemcpyDeviceToDevice, s));
-    GDN2_HIP_CHECK(hipMemcpyAsync(g, wk.g, nk, hipMemcpyDeviceToDevice, s));
-    GDN2_HIP_CHECK(hipMemcpyAsync(b, wk.b, nk, hipMemcpyDeviceToDevice, s));
+    // q, k, g, b as the recurrence takes them: [B, H, T, K], or [B, HV, T, K]
+    // in the reference's GVA layout (which is what its project returns)
+    const size_t nk = sizeof(float) * M * d.kq, nv = sizeof(float) * M * d.vd;
+    GDN2_HIP_CHECK(hipMemcpyAsync(q, wk.xq, nk, hipMemcpyDeviceToDevice, s));
+    GDN2_HIP_CHECK(hipMemcpyAsync(k, wk.xk, nk, hipMemcpyDeviceToDevice, s));
+    GDN2_HIP_CHECK(hipMemcpyAsync(g, wk.xg, nk, hipMemcpyDeviceToDevice, s));
+    GDN2_HIP_CHECK(hipMemcpyAsync(b, wk.xb, nk, hipMemcpyDeviceToDevice, s));
     GDN2_HIP_CHECK(hipMemcpyAsync(v, wk.v, nv, hipMemcpyDeviceToDevice, s));
     GDN2_HIP_CHECK(hipMemcpyAsync(w, wk.w, nv, hipMemcpyDeviceToDevice, s));
     GDN2_HIP_CHECK(hipMemcpyAsync(gate, wk.G, nv, hipMemcpyDeviceToDevice, s));
@@ -1019,6 +1059,7 @@ struct BwdWork {
     float *S0, *Sf;               // state entering the call; the forward's working copy
     float *y, *dy, *dO, *dG;      // [M, vd]
     float *dq, *dk, *dg, *db;     // [B, H, T, K]
+    float *dxq, *dxk, *dxg, *dxb; // the recurrence's: dq .. db, or [B, HV, T, K] in the reference's GVA layout
     float *dv, *dw;               // [B, HV, T, V]
     float *dY;                    // [M, ld_in]
     float *DU;                    // [M, 2 kd + vd], short conv only
@@ -1045,6 +1086,7 @@ gdn2_status bwd_workspace(gdn2_layer &L, int64_t B, int64_t T, bool recompute, B
     const size_t f = sizeof(float), nS = f * B * d.HV * d.K * d.V;
     const size_t nk = f * M * d.kd, nv = f * M * d.vd, nY = f * M * L.ld_in;
     const size_t rk = recompute ? nk : 0, rv = recompute ? nv : 0;  // the forward's buffers, when recomputed
+    const size_t nx = d.Hq == d.H ? 0 : f * M * d.kq;               // the reference's GVA layout
     const int64_t part_cols = std::max<int64_t>(std::max(d.kd, d.vd), 4 * ctot);
     struct Slot {
         float **ptr;
@@ -1055,6 +1097,9 @@ gdn2_status bwd_workspace(gdn2_layer &L, int64_t B, int64_t T, bool recompute, B
         {&bw->S0, nS}, {&bw->Sf, recompute ? nS : 0}, {&bw->dS0, nS},
         {&bw->y, nv}, {&bw->dy, nv}, {&bw->dO, nv}, {&bw->dG, nv},
         {&bw->dq, nk}, {&bw->dk, nk}, {&bw->dg, nk}, {&bw->db, nk}, {&bw->dv, nv}, {&bw->dw, nv},
+        {&bw->dxq, nx}, {&bw->dxk, nx}, {&bw->dxg, nx}, {&bw->dxb, nx},
+        {&bw->fw.xq, recompute ? nx : 0}, {&bw->fw.xk, recompute ? nx : 0}, {&bw->fw.xg, recompute ? nx : 0},
+        {&bw->fw.xb, recompute ? nx : 0},
         {&bw->dY, nY}, {&bw->DU, sc ? f * M * ctot : 0}, {&bw->dF, nk}, {&bw->PA, nk}, {&bw->PD, md ? nk : 0},
         {&bw->wpart, sc ? f * B * nblk * 4 * ctot : 0}, {&bw->part, f * kColParts * part_cols},
     };
@@ -1079,6 +1124,10 @@ gdn2_status bwd_workspace(gdn2_layer &L, int64_t B, int64_t T, bool recompute, B
         base += align256(sl.bytes);
     }
     bw->fw.S0 = nullptr;
+    if (d.Hq == d.H) { // head repeat: the recurrence works on q .. b themselves
+        bw->dxq = bw->dq; bw->dxk = bw->dk; bw->dxg = bw->dg; bw->dxb = bw->db;
+        bw->fw.xq = bw->fw.q; bw->fw.xk = bw->fw.k; bw->fw.xg = bw->fw.g; bw->fw.xb = bw->fw.b;
+    }
     return GDN2_OK;
 }
 
@@ -1115,6 +1164,8 @@ extern "C" gdn2_status gdn2_layer_saved_create(const gdn2_layer *L, int64_t B, i
                            f * M * d.kd,     f * M * d.vd, f * M * d.vd, f * M * d.vd, cbytes};
     size_t total = 0;
     for (size_t v : sz) total += align256(v);
+    Work probe{};
+    total += carve_expanded(d, (int64_t)M, nullptr, &probe);
     gdn2_layer_saved *A = new gdn2_layer_saved();
     A->layer = L;
     A->batch = B;
@@ -1131,6 +1182,8 @@ extern "C" gdn2_status gdn2_layer_saved_create(const gdn2_layer *L, int64_t B, i
     }
     A->chunk = cbytes ? base : nullptr;
     A->chunk_bytes = cbytes;
+    base += align256(cbytes);
+    carve_expanded(d, (int64_t)M, base, &A->fw);
     *out = A;
     return GDN2_OK;
 }
@@ -1337,7 +1390,7 @@ extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, in
         ba.fwd = chunk_args_for(*L, B, T, fw, bw.S0);
         ba.d_out = bw.dO;
         ba.d_state_out = has_ds ? d_state->S : nullptr;
-        ba.dq = bw.dq; ba.dk = bw.dk; ba.dg = bw.dg; ba.db = bw.db; ba.dv = bw.dv; ba.dw = bw.dw;
+        ba.dq = bw.dxq; ba.dk = bw.dxk; ba.dg = bw.dxg; ba.db = bw.dxb; ba.dv = bw.dv; ba.dw = bw.dw;
         ba.d_state0 = d_state_in ? d_state_in->S : bw.dS0;
         if (saved && saved->chunk_filled) { // the forward's per-chunk quantities are kept
             ba.workspace = saved->chunk;
@@ -1353,11 +1406,18 @@ extern "C" gdn2_status gdn2_layer_backward_f32(gdn2_layer *L, const float *x, in
         ra.fwd = recurrent_args_for(chunk_args_for(*L, B, T, fw, bw.S0));
         ra.d_out = bw.dO;
         ra.d_state_out = has_ds ? d_state->S : nullptr;
-        ra.dq = bw.dq; ra.dk = bw.dk; ra.dg = bw.dg; ra.db = bw.db; ra.dv = bw.dv; ra.dw = bw.dw;
+        ra.dq = bw.dxq; ra.dk = bw.dxk; ra.dg = bw.dxg; ra.db = bw.dxb; ra.dv = bw.dv; ra.dw = bw.dw;
         ra.d_state0 = d_state_in ? d_state_in->S : bw.dS0;
         ra.workspace = fw.chunk;
         ra.workspace_bytes = fw.chunk_bytes;
         if ((st = gdn2_recurrent_bwd_f32(&ra, s)) != GDN2_OK) return st;
+    }
+    if (d.Hq != d.H) { // the reference's GVA layout back to the key heads
+        GvaParams gp{};
+        gp.src[0] = bw.dxq; gp.src[1] = bw.dxk; gp.src[2] = bw.dxg; gp.src[3] = bw.dxb;
+        gp.dst[0] = bw.dq; gp.dst[1] = bw.dk; gp.dst[2] = bw.dg; gp.dst[3] = bw.db;
+        gp.B = B; gp.H = d.H; gp.T = T; gp.K = d.K; gp.rep = (int)(d.HV / d.H);
+        GDN2_HIP_CHECK(launch_gva_fold(gp, s));
     }
 
     // projection epilogue and short conv

@@ -195,6 +195,40 @@ __global__ __launch_bounds__(256) void project_kernel(ProjectParams p) {
     }
 }
 
+// The reference's GVA layout: a [B, H, T, rep, K] repeat read as
+// [B, H rep, T, K].  Destination (b, hv, t2, c), hv = h rep + a, reads source
+// (b, h, (a T + t2) / rep, c); one thread per destination element of the four
+// tensors.
+__global__ __launch_bounds__(256) void gva_expand_kernel(GvaParams p) {
+    const int64_t n = p.B * p.H * p.rep * p.T * p.K;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < 4 * n; i += (int64_t)gridDim.x * 256) {
+        const int which = (int)(i / n);
+        const int64_t e = i % n;
+        const int64_t c = e % p.K, t2 = (e / p.K) % p.T, hv = (e / (p.K * p.T)) % (p.H * p.rep);
+        const int64_t bi = e / (p.K * p.T * p.H * p.rep);
+        const int64_t h = hv / p.rep, a = hv % p.rep, t = (a * p.T + t2) / p.rep;
+        p.dst[which][e] = p.src[which][((bi * p.H + h) * p.T + t) * p.K + c];
+    }
+}
+
+// Adjoint of gva_expand_kernel: key element (b, h, t, c) went to the places
+// f = t rep + j (j < rep) of the [T rep] run of head h, i.e. value head
+// h rep + f / T at time f % T; their gradients are summed in j order.
+__global__ __launch_bounds__(256) void gva_fold_kernel(GvaParams p) {
+    const int64_t n = p.B * p.H * p.T * p.K;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < 4 * n; i += (int64_t)gridDim.x * 256) {
+        const int which = (int)(i / n);
+        const int64_t e = i % n;
+        const int64_t c = e % p.K, t = (e / p.K) % p.T, h = (e / (p.K * p.T)) % p.H, bi = e / (p.K * p.T * p.H);
+        float acc = 0.f;
+        for (int j = 0; j < p.rep; ++j) {
+            const int64_t f = t * p.rep + j, hv = h * p.rep + f / p.T, t2 = f % p.T;
+            acc += p.src[which][((bi * p.H * p.rep + hv) * p.T + t2) * p.K + c];
+        }
+        p.dst[which][e] = acc;
+    }
+}
+
 // New conv caches: xpad[T .. T + 3) = the last three pre-conv tokens.
 __global__ __launch_bounds__(256) void conv_cache_kernel(ConvCacheParams p) {
     const int64_t nq = (int64_t)p.B * 3 * p.kd, nv = (int64_t)p.B * 3 * p.vd;
@@ -617,6 +651,20 @@ hipError_t launch_project(const ProjectParams &p, hipStream_t s) {
     }
     const int nb = (p.T + kProjTB - 1) / kProjTB;
     hipLaunchKernelGGL(project_kernel, dim3((unsigned)(p.B * nb), (unsigned)(p.H + p.HV)), dim3(256), lds, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_gva_expand(const GvaParams &p, hipStream_t s) {
+    const int64_t n = 4 * p.B * p.H * p.rep * p.T * p.K;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(gva_expand_kernel, dim3(grid_for(n)), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_gva_fold(const GvaParams &p, hipStream_t s) {
+    const int64_t n = 4 * p.B * p.H * p.T * p.K;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(gva_fold_kernel, dim3(grid_for(n)), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 

@@ -87,11 +87,13 @@ class Config(ctypes.Structure):
     _fields_ = [("hidden_size", _i64), ("num_heads", _i64), ("head_dim", _i64), ("expand_v", ctypes.c_float),
                 ("num_v_heads", _i64), ("use_short_conv", ctypes.c_int32), ("allow_neg_eigval", ctypes.c_int32),
                 ("norm_eps", _dbl), ("mode", ctypes.c_int32), ("chunk_size", _i64),
-                ("has_min_decay", ctypes.c_int32), ("min_decay", _dbl)]
+                ("has_min_decay", ctypes.c_int32), ("min_decay", _dbl), ("gva_layout", ctypes.c_int32)]
 
 
 MODE_FUSED_RECURRENT = 0
 MODE_CHUNK = 1
+GVA_HEAD_REPEAT = 0
+GVA_REFERENCE = 1
 STATE_RECURRENT, STATE_CONV_Q, STATE_CONV_K, STATE_CONV_V = 0, 1, 2, 3
 
 # Every symbol include/*.h declares (checked by tests/test_capi_exports.py).

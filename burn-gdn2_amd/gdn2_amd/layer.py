@@ -23,6 +23,7 @@ import numpy as np
 from . import _capi as C
 
 _MODES = {"fused_recurrent": C.MODE_FUSED_RECURRENT, "chunk": C.MODE_CHUNK}
+_GVA_LAYOUTS = {"head_repeat": C.GVA_HEAD_REPEAT, "reference": C.GVA_REFERENCE}
 
 
 def _stream():
@@ -37,7 +38,12 @@ def _msg() -> str:
 
 @dataclass
 class Gdn2Config:
-    """Gdn2Config (src/config.rs:23-58); `mode` is "fused_recurrent" or "chunk"."""
+    """Gdn2Config (src/config.rs:23-58); `mode` is "fused_recurrent" or "chunk".
+    `gva_layout` (not a Gdn2Config field) is "head_repeat" (value head hv
+    reads key head hv / rep at every time, so decode reproduces prefill) or
+    "reference" (the reference tensor path's unsqueeze/repeat/reshape,
+    src/module.rs:456-468: value head h rep + a at time t reads key head h at
+    time (a T + t) / rep of the same call)."""
     hidden_size: int = 2048
     num_heads: int = 16
     head_dim: int = 128
@@ -49,14 +55,18 @@ class Gdn2Config:
     mode: str = "fused_recurrent"
     chunk_size: int = 64
     min_decay: Optional[float] = None
+    gva_layout: str = "head_repeat"
 
     def to_c(self) -> C.Config:
         if self.mode not in _MODES:
             raise ValueError(f"mode must be one of {sorted(_MODES)}, got {self.mode!r}")
+        if self.gva_layout not in _GVA_LAYOUTS:
+            raise ValueError(f"gva_layout must be one of {sorted(_GVA_LAYOUTS)}, got {self.gva_layout!r}")
         return C.Config(int(self.hidden_size), int(self.num_heads), int(self.head_dim), float(self.expand_v),
                         0 if self.num_v_heads is None else int(self.num_v_heads), int(bool(self.use_short_conv)),
                         int(bool(self.allow_neg_eigval)), float(self.norm_eps), _MODES[self.mode],
-                        int(self.chunk_size), int(self.min_decay is not None), float(self.min_decay or 0.0))
+                        int(self.chunk_size), int(self.min_decay is not None), float(self.min_decay or 0.0),
+                        _GVA_LAYOUTS[self.gva_layout])
 
     def validate(self) -> None:
         """Gdn2Config::validate (src/config.rs:71-111): raises ValueError with
@@ -77,6 +87,12 @@ class Gdn2Config:
     @property
     def kd(self) -> int:
         return self.num_heads * self.head_dim
+
+    @property
+    def hq(self) -> int:
+        """Key-side heads of the recurrence's q, k, g, b: num_heads, or the
+        value heads in the reference's GVA layout."""
+        return self.hv if self.gva_layout == "reference" else self.num_heads
 
     @property
     def vd(self) -> int:
@@ -401,15 +417,16 @@ class GatedDeltaNet2:
         return out, state
 
     def project(self, x, state: Optional[Gdn2State] = None) -> Dict[str, "torch.Tensor"]:
-        """project (src/module.rs:381-495) without the GVA repeat: q, k, g, b
-        [B, H, T, K], v, w [B, HV, T, V] (the reference's layouts) and gate
-        [B, T, HV, V]."""
+        """project (src/module.rs:381-495): q, k, g, b as the recurrence takes
+        them, [B, H, T, K] under head repeat (the key heads, not repeated) or
+        [B, HV, T, K] in the reference's GVA layout (what its project
+        returns); v, w [B, HV, T, V] and gate [B, T, HV, V]."""
         import torch
 
         x = self._check_x(x)
         cfg = self.config
         B, T = x.shape[:2]
-        o = {n: torch.empty((B, cfg.num_heads, T, cfg.head_dim), device=x.device) for n in ("q", "k", "g", "b")}
+        o = {n: torch.empty((B, cfg.hq, T, cfg.head_dim), device=x.device) for n in ("q", "k", "g", "b")}
         o.update({n: torch.empty((B, cfg.hv, T, cfg.v_head), device=x.device) for n in ("v", "w")})
         o["gate"] = torch.empty((B, T, cfg.hv, cfg.v_head), device=x.device)
         C.check(C.lib().gdn2_layer_project_f32(self._h, x.data_ptr(), B, T, state._h if state is not None else None,

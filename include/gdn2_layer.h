@@ -38,8 +38,23 @@ typedef enum gdn2_mode {
     GDN2_MODE_CHUNK = 1,           /* Gdn2Mode::Chunk */
 } gdn2_mode;
 
+/* How the key-side heads (q, k, g, b) reach the value heads under GVA
+ * (num_v_heads > num_heads, rep = num_v_heads / num_heads).  Not a
+ * Gdn2Config field: the reference has one layout, its tensor path's
+ * unsqueeze/repeat/reshape (src/module.rs:456-468), which reads value head
+ * h * rep + a at time t from key head h at time (a * T + t) / rep of the same
+ * call, so that a T-token call differs from T one-token calls.
+ * GDN2_GVA_HEAD_REPEAT (the default) gives value head hv key head hv / rep at
+ * every time, so decode reproduces prefill; GDN2_GVA_REFERENCE reproduces the
+ * reference's layout (the two coincide at T = 1). */
+typedef enum gdn2_gva_layout {
+    GDN2_GVA_HEAD_REPEAT = 0,
+    GDN2_GVA_REFERENCE = 1,
+} gdn2_gva_layout;
+
 /* Gdn2Config (src/config.rs:23-58).  Option fields: num_v_heads = 0 is
- * None; has_min_decay = 0 is None. */
+ * None; has_min_decay = 0 is None.  gva_layout (gdn2_gva_layout) is this
+ * library's own field, 0 in gdn2_config_default. */
 typedef struct gdn2_config {
     int64_t hidden_size;
     int64_t num_heads;
@@ -53,6 +68,7 @@ typedef struct gdn2_config {
     int64_t chunk_size;
     int32_t has_min_decay;
     double min_decay;
+    int32_t gva_layout;
 } gdn2_config;
 
 /* Gdn2Config::default() (src/config.rs:114-130). */
@@ -129,12 +145,13 @@ GDN2_API gdn2_status gdn2_layer_forward_train_f32(gdn2_layer *layer, const float
 GDN2_API gdn2_status gdn2_layer_forward_f32(gdn2_layer *layer, const float *x, int64_t batch, int64_t seq_len,
                                             gdn2_state *state, float *out, gdn2_stream_t stream);
 
-/* project (src/module.rs:381-495) without the GVA repeat: writes the
- * kernel inputs q, k, g, b [B, H, T, K], v, w [B, HV, T, V] and the gate
- * signal [B, T, HV, V] (each contiguous, caller-owned).  `state` (nullable,
- * not modified) supplies the conv caches when non-empty.  The reference's
- * [B, HV, T, K] key-side tensors are these with each head repeated
- * num_v_heads / num_heads times. */
+/* project (src/module.rs:381-495): writes the recurrence's inputs q, k,
+ * g, b, v, w [B, HV, T, V] and the gate signal [B, T, HV, V] (each
+ * contiguous, caller-owned).  q, k, g, b are [B, H, T, K] under
+ * GDN2_GVA_HEAD_REPEAT (the key heads, not repeated: value head hv reads key
+ * head hv / rep) and [B, HV, T, K] under GDN2_GVA_REFERENCE (the reference's
+ * repeated layout, what its project returns).  `state` (nullable, not
+ * modified) supplies the conv caches when non-empty. */
 GDN2_API gdn2_status gdn2_layer_project_f32(gdn2_layer *layer, const float *x, int64_t batch, int64_t seq_len,
                                             const gdn2_state *state, float *q, float *k, float *g, float *b,
                                             float *v, float *w, float *gate, gdn2_stream_t stream);

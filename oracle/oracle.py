@@ -423,7 +423,7 @@ class LayerGrads:
 
 
 def layer_backward_f64(cfg, weights: dict, x, d_out, state: Optional[OracleState] = None,
-                       d_state: Optional[OracleState] = None) -> LayerGrads:
+                       d_state: Optional[OracleState] = None, gva_scrambled=False) -> LayerGrads:
     """Gradients of L = <d_out, out> + <d_state, state after the call> for
     GatedDeltaNet2::forward(x, &mut state, true) (src/module.rs:224-316;
     state None = Option::None, which is forward_train, :326-375), true head
@@ -432,7 +432,10 @@ def layer_backward_f64(cfg, weights: dict, x, d_out, state: Optional[OracleState
     (src/short_conv.rs:22-65), gates (src/module.rs:417-443), L2 norm
     (src/l2norm.rs:13-16), the scan (gdn2o_scan_d / gdn2o_recurrent_bwd_d)
     and the gated RMSNorm (src/module.rs:501-517).  Without short conv the
-    conv caches pass through unchanged, so their gradient passes through."""
+    conv caches pass through unchanged, so their gradient passes through.
+    gva_scrambled: the reference's GVA layout (src/module.rs:456-468,
+    unsqueeze at 3, repeat, reshape to [B, HV, T, K]) instead of head repeat;
+    its adjoint sums each key element's rep copies."""
     H, K = cfg.num_heads, cfg.head_dim
     HV = cfg.num_v_heads or H
     V = int(K * cfg.expand_v)
@@ -488,6 +491,11 @@ def layer_backward_f64(cfg, weights: dict, x, d_out, state: Optional[OracleState
 
     q4, k4, g4, b4 = to4(qn, H, K), to4(kn, H, K), to4(gg, H, K), to4(bs * bmul, H, K)
     v4, w4 = to4(_silu(u["v"]), HV, V), to4(ws, HV, V)
+    rep = HV // H
+    scr = gva_scrambled and rep > 1
+    if scr:  # [B, H, T, K] -> [B, H, T, rep, K] -> [B, HV, T, K] (src/module.rs:459-463)
+        q4, k4, g4, b4 = (np.repeat(a[:, :, :, None, :], rep, axis=3).reshape(B, HV, T, K)
+                          for a in (q4, k4, g4, b4))
     S0 = np.zeros((B, HV, K, V)) if state is None else np.asarray(state.recurrent, np.float64)
     scale = float(K) ** -0.5
     O, _ = scan_d(q4, k4, v4, g4, b4, w4, S0, scale)
@@ -507,6 +515,9 @@ def layer_backward_f64(cfg, weights: dict, x, d_out, state: Optional[OracleState
     dOb = (dn - nrm * (dn * nrm).mean(-1, keepdims=True)) / rms
     r = recurrent_bwd_d(q4, k4, v4, g4, b4, w4, dOb.transpose(0, 2, 1, 3), S0,
                         None if d_state is None else d_state.recurrent, scale)
+    if scr:  # adjoint of the repeat + reshape: each key element's rep copies summed
+        for n in ("dq", "dk", "dg", "db"):
+            r[n] = r[n].reshape(B, H, T, rep, K).sum(3)
     dqn, dkn = back(r["dq"]).reshape(B, T, H, K), back(r["dk"]).reshape(B, T, H, K)
     dqa = (dqn - qn * (dqn * qn).sum(-1, keepdims=True)) / nq
     dka = (dkn - kn * (dkn * kn).sum(-1, keepdims=True)) / nk

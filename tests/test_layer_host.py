@@ -26,7 +26,29 @@ def test_default_matches_reference():
     assert (d.hidden_size, d.num_heads, d.head_dim, d.expand_v, d.num_v_heads) == (2048, 16, 128, 1.0, 0)
     assert (d.use_short_conv, d.allow_neg_eigval, d.norm_eps, d.mode, d.chunk_size, d.has_min_decay) == (
         1, 0, 1e-5, C.MODE_FUSED_RECURRENT, 64, 0)
+    assert d.gva_layout == C.GVA_HEAD_REPEAT
     assert c.to_c().hidden_size == d.hidden_size and c.to_c().mode == d.mode
+    assert c.to_c().gva_layout == d.gva_layout
+
+
+def test_gva_layout_is_checked_after_the_reference_checks():
+    """gva_layout is this library's field: the C check runs after the
+    reference's (an invalid config reports the reference's message first),
+    and the Python mirror refuses unknown names."""
+    import ctypes
+
+    from gdn2_amd import _capi as C
+
+    d = G.Gdn2Config(num_heads=8, num_v_heads=16, gva_layout="reference").to_c()
+    assert C.lib().gdn2_config_validate(ctypes.byref(d)) == C.GDN2_OK
+    d.gva_layout = 2
+    assert C.lib().gdn2_config_validate(ctypes.byref(d)) == C.GDN2_EINVAL
+    assert "gva_layout" in C.lib().gdn2_last_error().decode()
+    d.hidden_size = 0
+    assert C.lib().gdn2_config_validate(ctypes.byref(d)) == C.GDN2_EINVAL
+    assert C.lib().gdn2_last_error().decode().startswith("hidden_size must be > 0")
+    with pytest.raises(ValueError):
+        G.Gdn2Config(gva_layout="scrambled").to_c()
 
 
 # (overrides, the reference's panic message) in the order validate checks them

@@ -2,8 +2,9 @@
 central finite differences of the oracle's layer forward (gdn2o_layer_forward,
 a separate C implementation pinned by the reference's golden vectors in
 test_oracle.py): every parameter, the input and every part of the state, on
-configurations with and without short conv, with GVA, negative eigenvalues,
-min_decay, a carried state, fewer than three tokens and a single token.
+configurations with and without short conv, with GVA (head repeat and the
+reference's layout), negative eigenvalues, min_decay, a carried state, fewer
+than three tokens and a single token.
 The loss is L = <d_out, out> + <d_state, state after the call>.  CPU only."""
 import copy
 
@@ -14,9 +15,9 @@ from gdn2_testutil import Cfg, init_weights
 from oracle import oracle as O
 
 
-def _loss(cfg, W, x, state, d_out, d_state):
+def _loss(cfg, W, x, state, d_out, d_state, scrambled=False):
     st = None if state is None else copy.deepcopy(state)
-    res, new = O.layer_forward(cfg, W, x, st)
+    res, new = O.layer_forward(cfg, W, x, st, gva_scrambled=scrambled)
     L = float((res.out * d_out).sum())
     if d_state is not None:
         for f in ("recurrent", "conv_q", "conv_k", "conv_v"):
@@ -37,12 +38,16 @@ CASES = [
                                        allow_neg_eigval=True, min_decay=0.9), 2, 2, True, True),
     ("noconv_state", dict(hidden_size=6, num_heads=2, head_dim=3, use_short_conv=False), 1, 6, True, True),
     ("conv_T1", dict(hidden_size=8, num_heads=2, head_dim=4), 2, 1, False, True),
+    # the reference's GVA layout (value head h rep + a at time t reads key time (a T + t) / rep)
+    ("gva_reference_layout_state", dict(hidden_size=8, num_heads=1, head_dim=4, num_v_heads=3,
+                                        allow_neg_eigval=True), 2, 5, True, True, True),
 ]
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_layer_adjoint_matches_finite_differences(case):
-    _, kw, B, T, carried, with_ds = case
+    _, kw, B, T, carried, with_ds = case[:6]
+    scr = len(case) > 6 and case[6]
     cfg = Cfg(**kw)
     rng = np.random.default_rng(7)
     W = init_weights(cfg, seed=11)
@@ -58,8 +63,8 @@ def test_layer_adjoint_matches_finite_differences(case):
     d_out = rng.normal(0, 1, (B, T, cfg.hidden_size))
     d_state = _rand_state(rng, B, cfg) if with_ds else None
 
-    G = O.layer_backward_f64(cfg, W, x, d_out, state, d_state)
-    _, out = _loss(cfg, W, x, state, d_out, d_state)
+    G = O.layer_backward_f64(cfg, W, x, d_out, state, d_state, gva_scrambled=scr)
+    _, out = _loss(cfg, W, x, state, d_out, d_state, scr)
     assert np.max(np.abs(G.out - out)) <= 1e-12 * max(1.0, np.max(np.abs(out)))
 
     worst = 0.0
@@ -83,9 +88,9 @@ def test_layer_adjoint_matches_finite_differences(case):
             h = np.float32(2.0 ** -14) * max(np.float32(1.0), abs(x0))
             xp, xm = np.float32(x0 + h), np.float32(x0 - h)
             flat[e] = xp
-            lp, _ = _loss(cfg, W, x, state, d_out, d_state)
+            lp, _ = _loss(cfg, W, x, state, d_out, d_state, scr)
             flat[e] = xm
-            lm, _ = _loss(cfg, W, x, state, d_out, d_state)
+            lm, _ = _loss(cfg, W, x, state, d_out, d_state, scr)
             flat[e] = x0
             check(name, gflat[e], (lp - lm) / (float(xp) - float(xm)))
     # double state entries
@@ -95,9 +100,9 @@ def test_layer_adjoint_matches_finite_differences(case):
             for e in rng.choice(flat.size, size=min(5, flat.size), replace=False):
                 x0 = flat[e]
                 flat[e] = x0 + 1e-5
-                lp, _ = _loss(cfg, W, x, state, d_out, d_state)
+                lp, _ = _loss(cfg, W, x, state, d_out, d_state, scr)
                 flat[e] = x0 - 1e-5
-                lm, _ = _loss(cfg, W, x, state, d_out, d_state)
+                lm, _ = _loss(cfg, W, x, state, d_out, d_state, scr)
                 flat[e] = x0
                 check(f, gflat[e], (lp - lm) / 2e-5)
     else:
