@@ -713,7 +713,8 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
 constexpr int kInterOut = 0, kInterLocal = 1, kInterStates = 2, kInterOutStates = 3, kInterOutTrain = 4;
 
 // NWV waves per workgroup (NWV = 4: 64 value columns; NWV = 2: 32, for value
-// dimensions that are not a multiple of 64 and for K = 32).
+// dimensions that are not a multiple of 64 and for K = 32; NWV = 8: 128, pass 1
+// at K = 128).
 template <int K, int MODE, int NWV>
 __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p, int nseg_launch) {
     constexpr bool OUT = MODE == kInterOut || MODE == kInterOutStates || MODE == kInterOutTrain;
@@ -1206,12 +1207,17 @@ __global__ __launch_bounds__(256) void chunk_states_kernel(ChunkParams p) {
 template <int K, int V>
 hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
     constexpr int NWV = inter_nwv(K, V), VSW = 16 * NWV; // waves and value columns per sequential workgroup
-    const dim3 blk(64 * NWV);
+    // Pass 1 (segment summaries: no output, so no q exp(G) or A_qk in LDS) at
+    // K = 128 takes 128 columns (V or P) per workgroup of eight waves: the
+    // chunk's W and Kd^T are copied once for twice the columns, and two waves
+    // per SIMD still fit its registers.
+    constexpr int NWL = (K == 128 && V % 128 == 0) ? 8 : NWV, VSWL = 16 * NWL;
+    const dim3 blk(64 * NWV), blkl(64 * NWL);
     const int seqs = p.B * p.HV;
     if (phases & 112) {
         if ((phases & 16) && p.NSEG > 1)
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal, NWV>), dim3(seqs * (p.NSEG - 1) * ((V + K) / VSW)),
-                               blk, 0, s, p, p.NSEG - 1);
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal, NWL>), dim3(seqs * (p.NSEG - 1) * ((V + K) / VSWL)),
+                               blkl, 0, s, p, p.NSEG - 1);
         if ((phases & 32) && p.NSEG > 1)
             hipLaunchKernelGGL((chunk_chain_kernel<K, NWV>), dim3(seqs * (V / VSW)), blk, 0, s, p);
         if (phases & 64)
@@ -1236,7 +1242,7 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
             // the training forward (phases & 4) also takes the last segment's P, which
             // the backward's reverse chain uses
             const int nl = (phases & 4) ? p.NSEG : p.NSEG - 1;
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal, NWV>), dim3(seqs * nl * ((V + K) / VSW)), blk, 0,
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal, NWL>), dim3(seqs * nl * ((V + K) / VSWL)), blkl, 0,
                                s, p, nl);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
