@@ -783,6 +783,12 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
         ot = K;
         obase = (int64_t)cid * C * K;
     }
+    // The four gradients go through buffer resources over the chunk's valid
+    // rows: the hardware drops the stores past the last one, and the offsets
+    // are 32-bit (a chunk's rows span less than 2 GiB, checked on the host).
+    const int ot_ = (int)ot;
+    const __amdgpu_buffer_rsrc_t Oq = rows_rsrc(oq + obase, ot_, cv, K), Ok = rows_rsrc(okk + obase, ot_, cv, K);
+    const __amdgpu_buffer_rsrc_t Og = rows_rsrc(og + obase, ot_, cv, K), Ob = rows_rsrc(ob + obase, ot_, cv, K);
     // dQG, dKd, dRk tiles (t, wave): lane (lg, lr) holds rows 16 t + 4 lg + i of channel ch
     const floatx4 *dqg = reinterpret_cast<const floatx4 *>(bp.ws_dqg) + (size_t)cid * (C * K / 4);
     const floatx4 *dkd = reinterpret_cast<const floatx4 *>(bp.ws_dkd) + (size_t)cid * (C * K / 4);
@@ -843,30 +849,45 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
                 rq[i] = aq[i] * e;
                 rkb[i] = ab[i] * e;
             }
-            if (msk[t]) { // exact diagonal-block terms of this channel: row sums, then column sums
+            if (__ballot(msk[t])) {
+                // Exact diagonal-block terms, wave-uniform so that lanes can
+                // exchange operands: each E_rs of the lane's rows r = 16 t + 4 lg + i
+                // and the tile's rows s <= r is formed once and feeds the row
+                // sum of r and the lane's part of the column sum of s; k_s
+                // comes from lane (s / 4, n), G_s from LDS.  Lanes of channels
+                // at or below 192 (their diagonal block is in the products)
+                // take E = 0: every lane of a column shares its channel.
+                const bool on = msk[t];
+                float sq[4], sbk[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int r = 16 * t + 4 * lg + i;
-                    float sq = 0.f, sb = 0.f;
-                    for (int s2 = 16 * t; s2 <= r; ++s2) {
-                        const float e = fast_exp2(gt[i] - sG[s2][ch]) * bld1(Rk, s2 * rq_ + ch);
-                        sq += sDA[r][s2] * e;
-                        sb += sDK[r][s2] * e;
-                    }
-                    rq[i] += sq;
-                    rkb[i] += sb;
+                    const int o = (16 * t + 4 * lg + i) * rq_ + ch;
+                    sq[i] = scale * bld1(Rq, o);
+                    sbk[i] = bld1(Rb, o) * kv[t][i];
                 }
+#pragma unroll 1
+                for (int sg = 0; sg < 4; ++sg) // rows s = 16 t + 4 sg + u
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int s2 = 16 * t + 4 * lg + i;
-                    float sc = 0.f;
-                    for (int r = s2; r < 16 * t + 16; ++r) {
-                        const float e = fast_exp2(sG[r][ch] - gt[i]);
-                        const int o = r * rq_ + ch;
-                        sc += (scale * sDA[r][s2] * bld1(Rq, o) + sDK[r][s2] * bld1(Rb, o) * bld1(Rk, o)) * e;
+                    for (int u = 0; u < 4; ++u) {
+                        const int s = 4 * sg + u;
+                        const float gs = sG[16 * t + s][ch];
+                        const float ks = __shfl(kv[t][u], 16 * sg + lr, 64);
+                        float cs = 0.f;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int r = 16 * t + 4 * lg + i;
+                            const float e = on && s <= 4 * lg + i ? fast_exp2(gt[i] - gs) : 0.f;
+                            const float da = sDA[r][16 * t + s], dk = sDK[r][16 * t + s];
+                            const float ke = ks * e;
+                            rq[i] += da * ke;
+                            rkb[i] += dk * ke;
+                            cs += (sq[i] * da + sbk[i] * dk) * e;
+                        }
+                        // the column sum of s over the four lanes (lg, n), kept at lane (sg, n)
+                        cs += __shfl_xor(cs, 16, 64);
+                        cs += __shfl_xor(cs, 32, 64);
+                        if (lg == sg) ckt[t][u] += cs;
                     }
-                    ckt[t][i] += sc;
-                }
             }
         }
         const floatx4 ck = ckt[t];
@@ -881,11 +902,10 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
             const float qr = bld1(Rq, o), kr = kv[t][i], br = bld1(Rb, o);
             const float dkb = eG * vrk + rkb[i];
             const float kd = kr * eKd;
-            if (r < cv) {
-                oq[obase + r * ot + ch] = scale * (eG * vqg + rq[i]);
-                okk[obase + r * ot + ch] = eKd * vkd + ck[i] + dkb * br;
-                ob[obase + r * ot + ch] = dkb * kr;
-            }
+            const int oo = r * ot_ + ch;
+            bst1(Oq, oo, scale * (eG * vqg + rq[i]));
+            bst1(Ok, oo, eKd * vkd + ck[i] + dkb * br);
+            bst1(Ob, oo, dkb * kr);
             kt_sum += vkd * kd;
             const float dG = scale * qr * (eG * vqg + rq[i]) + br * kr * dkb - vkd * kd - kr * ck[i];
             sG[r][ch] = dG;
@@ -893,13 +913,23 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
     }
     kt_sum += __shfl_xor(kt_sum, 16, 64);
     kt_sum += __shfl_xor(kt_sum, 32, 64);
-    if (lg == 0) { // dG_last, then dg = reverse cumulative sum of dG (this lane's channel)
-        float run = kt_sum + bp.ws_dgam[(size_t)cid * K + ch] * fast_exp2(gl);
-        for (int r = C - 1; r >= 0; --r) {
-            run += sG[r][ch];
-            if (r < cv) og[obase + r * ot + ch] = run;
-        }
+    // dg = the dG_last terms + the reverse cumulative sum of dG over the
+    // chunk's rows.  Lane (lg, n) sums rows 16 lg .. 16 lg + 15 of channel ch
+    // from the last up and adds the totals of the blocks after its own.
+    float part[16], tot = 0.f;
+#pragma unroll
+    for (int m = 15; m >= 0; --m) {
+        tot += sG[16 * lg + m][ch];
+        part[m] = tot;
     }
+    float after = kt_sum + bp.ws_dgam[(size_t)cid * K + ch] * fast_exp2(gl);
+#pragma unroll
+    for (int j = 1; j < 4; ++j) {
+        const float tj = __shfl(tot, 16 * j + lr, 64);
+        after += j > lg ? tj : 0.f;
+    }
+#pragma unroll
+    for (int m = 0; m < 16; ++m) bst1(Og, (16 * lg + m) * ot_ + ch, after + part[m]);
 }
 
 // Key-side gradients of a key head: the sum over its rep value heads.

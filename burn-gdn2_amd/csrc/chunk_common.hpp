@@ -31,6 +31,11 @@ __device__ __forceinline__ float bld1(__amdgpu_buffer_rsrc_t r, int idx) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, idx * 4, 0, 0));
 }
 
+// A store through a rows_rsrc resource: dropped past its last valid row.
+__device__ __forceinline__ void bst1(__amdgpu_buffer_rsrc_t r, int idx, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, v), r, idx * 4, 0, 0);
+}
+
 __device__ __forceinline__ floatx4 bld4(__amdgpu_buffer_rsrc_t r, int idx) {
     return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, idx * 4, 0, 0));
 }
