@@ -1228,10 +1228,7 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
     if (phases & 1) {
         const int nchunks = p.B * p.HV * p.NC;
         if (p.ws_akk) {
-            if constexpr (K >= 64 && (K <= 128 || V >= 128))
-                hipLaunchKernelGGL((chunk_intra_kernel<K, V, true>), dim3(nchunks), dim3(512), 0, s, p);
-            else
-                return hipErrorInvalidValue; // the chunked backward's shapes
+            hipLaunchKernelGGL((chunk_intra_kernel<K, V, true>), dim3(nchunks), dim3(512), 0, s, p);
         } else
             hipLaunchKernelGGL((chunk_intra_kernel<K, V, false>), dim3(nchunks), dim3(512), 0, s, p);
         hipError_t e = hipGetLastError();
@@ -1253,17 +1250,12 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
         const dim3 grid(seqs * p.NSEG * (V / VSW));
         if (phases & 8)
             hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOutStates, NWV>), grid, blk, 0, s, p, p.NSEG);
-        else if ((phases & 6) == 6) {
-            if constexpr (NWV == 4) // the backward's shapes
-                hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOutTrain, NWV>), grid, blk, 0, s, p, p.NSEG);
-            else
-                return hipErrorInvalidValue;
-        } else if (phases & 2)
+        else if ((phases & 6) == 6) // the training forward
+            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOutTrain, NWV>), grid, blk, 0, s, p, p.NSEG);
+        else if (phases & 2)
             hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOut, NWV>), grid, blk, 0, s, p, p.NSEG);
-        else if constexpr (NWV == 4) // the backward's states pass (its shapes take four waves)
+        else // the backward's states pass
             hipLaunchKernelGGL((chunk_inter_kernel<K, kInterStates, NWV>), grid, blk, 0, s, p, p.NSEG);
-        else
-            return hipErrorInvalidValue;
         return hipGetLastError();
     }
     return hipSuccess;
@@ -1276,9 +1268,7 @@ bool chunk_supported(int K, int V) {
            (K == 128 && (V == 64 || V == 128 || V == 192 || V == 256)) || (K == 256 && (V == 128 || V == 256));
 }
 
-bool chunk_bwd_supported(int K, int V) {
-    return ((K == 64 || K == 128) && (V == 64 || V == 128 || V == 256)) || (K == 256 && (V == 128 || V == 256));
-}
+bool chunk_bwd_supported(int K, int V) { return chunk_supported(K, V); }
 
 template <int K>
 hipError_t launch_chunk_states_t(const ChunkParams &p, hipStream_t s) {

@@ -63,8 +63,10 @@ __device__ __forceinline__ floatx4 mfma4x(floatx4 a, floatx4 b, floatx4 c) {
 }
 
 // ---------------------------------------------------------------------------
-// Reverse recurrence.  One workgroup per (b, hv, 64 value columns), wave w
+// Reverse recurrence.  One workgroup per (b, hv, 16 NW value columns), wave w
 // owns 16 columns; dS' stays in MFMA accumulators (key rows x 16 columns).
+// NW = 4, or 2 where V is not a multiple of 64 (V = 32, 96) and for K = 32,
+// as in the forward's chunk-inter.
 // Per chunk n, last to first:
 //   1: dv_new = A_qk^T dO + Kd dS'         (reads sAT, sKd)
 //      dS' and dv_new go to the workspace for the per-chunk kernels
@@ -85,13 +87,14 @@ __device__ __forceinline__ floatx4 mfma4x(floatx4 a, floatx4 b, floatx4 c) {
 // ---------------------------------------------------------------------------
 constexpr int kRevOut = 0, kRevLocal = 1;
 
-template <int K, int MODE>
-__global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg0, int nseg_launch) {
+template <int K, int MODE, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int seg0, int nseg_launch) {
     const ChunkParams &p = bp.f;
     constexpr bool LOCAL = MODE == kRevLocal;
-    constexpr int NKT = K / 16;
-    constexpr int OPF4 = NKT * NT * 64, PFO = OPF4 / 256;
-    constexpr int AF4 = NT * NT * 64, APF = AF4 / 256;
+    constexpr int NTH = 64 * NW, NKT = K / 16;
+    constexpr int OPF4 = NKT * NT * 64, PFO = OPF4 / NTH;
+    constexpr int AF4 = NT * NT * 64, APF = AF4 / NTH;
+    static_assert(OPF4 % NTH == 0 && AF4 % NTH == 0, "K");
     // K = 256: Kd and W^T take 64 KiB of LDS each, so (scale q e^G)^T, whose
     // product QG^T dO feeds only dS (not the dS -> dv_new chain), is read from
     // L2 into registers in phase 2 instead of through a third LDS buffer.
@@ -99,7 +102,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
     __shared__ floatx4 sKd[OPF4], sAT[AF4], sQT[QLDS ? OPF4 : 1], sWT[OPF4];
     __shared__ float sPf[256]; // destination of the L2 touches, never read
 
-    const int V = p.V, nvv = V / 64;
+    const int V = p.V, nvv = V / (16 * NW);
     int sq, vs;
     inter_block(blockIdx.x, p.B * p.HV * nseg_launch, nvv, &sq, &vs);
     const int bh = sq / nseg_launch, seg = seg0 + sq % nseg_launch;
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, lg = lane >> 4;
-    const int col = 16 * (vs * 4 + wave) + lr;
+    const int col = 16 * (vs * NW + wave) + lr;
     const int n0 = seg * p.SEGL, n1 = min(p.NC, n0 + p.SEGL);
 
     // the gradient leaving the segment: d_state_out (one segment), the chained
@@ -132,7 +135,7 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
     const int wv = 64 * wave;
 
     // The operands go from global memory straight into LDS (lds_copy4: thread
-    // tid's float4 i lands at index i * 256 + tid).  Each is also pulled
+    // tid's float4 i lands at index i * NTH + tid).  Each is also pulled
     // toward L2 ahead of its copy (l2_touch, one 128-byte line per thread):
     // Kd, A_qk^T of chunk n - 2 during phase 1 of chunk n, QT, WT of chunk
     // n - 1 during phase 2 of chunk n.  Each wave issues 2 touches last before
@@ -151,9 +154,9 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
     };
     auto copy_ka = [&](size_t c) {
 #pragma unroll
-        for (int i = 0; i < PFO; ++i) lds_copy4(&KD4[c * OPF4 + i * 256 + tid], &sKd[i * 256 + wv]);
+        for (int i = 0; i < PFO; ++i) lds_copy4(&KD4[c * OPF4 + i * NTH + tid], &sKd[i * NTH + wv]);
 #pragma unroll
-        for (int i = 0; i < APF; ++i) lds_copy4(&AT4[c * AF4 + i * 256 + tid], &sAT[i * 256 + wv]);
+        for (int i = 0; i < APF; ++i) lds_copy4(&AT4[c * AF4 + i * NTH + tid], &sAT[i * NTH + wv]);
     };
     // chunk n's rows of d_out through a buffer resource over its valid rows
     // (rows past T read 0); row 4 lg of each 16-row tile, the rest of the row
@@ -186,8 +189,8 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
         lds_barrier(); // sKd, sAT hold chunk n; every wave is done with sQT, sWT (n+1)
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
-            if (QLDS) lds_copy4(&QT4[cid * OPF4 + i * 256 + tid], &sQT[i * 256 + wv]);
-            lds_copy4(&WT4[cid * OPF4 + i * 256 + tid], &sWT[i * 256 + wv]);
+            if (QLDS) lds_copy4(&QT4[cid * OPF4 + i * NTH + tid], &sQT[i * NTH + wv]);
+            lds_copy4(&WT4[cid * OPF4 + i * NTH + tid], &sWT[i * NTH + wv]);
         }
         if (!LOCAL) { // dL/d(state leaving chunk n)
             float *Dsn = bp.ws_dsn + cid * K * V;
@@ -334,17 +337,17 @@ __global__ __launch_bounds__(256, 1) void bwd_inter_kernel(BwdParams bp, int seg
 // from pass 1) <- P_j^T slot j + R_j for j = NSEG-1 .. 1: the gradient leaving
 // every segment.  Same MFMA layout as the forward's chunk_chain_kernel, with
 // P_j^T's A fragments gathered from the forward's row-major P_j.
-template <int K>
-__global__ __launch_bounds__(256, 1) void bwd_chain_kernel(BwdParams bp) {
+template <int K, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void bwd_chain_kernel(BwdParams bp) {
     const ChunkParams &p = bp.f;
     constexpr int NKT = K / 16;
-    const int V = p.V, nvv = V / 64;
+    const int V = p.V, nvv = V / (16 * NW);
     int bh, vs;
     inter_block(blockIdx.x, p.B * p.HV, nvv, &bh, &vs);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lr = lane & 15, lg = lane >> 4;
-    const int col = 16 * (vs * 4 + wave) + lr;
+    const int col = 16 * (vs * NW + wave) + lr;
     float *slot0 = bp.ws_rseg + (size_t)bh * p.NSEG * K * V;
     float *last = slot0 + (size_t)(p.NSEG - 1) * K * V;
     floatx4 S[NKT];
@@ -429,7 +432,10 @@ __global__ __launch_bounds__(256, K >= 256 ? 1 : 2) void bwd_vprod_kernel(BwdPar
     using SM = VprodSmem<K, V>;
     constexpr int NKT = K / 16, NVB = V / 16, NVT = V / 16, NCT = NKT + NVT;
     constexpr int SP = SM::SP, KP = SM::KP;
-    constexpr int SF4 = K * 4 / 256, VF4 = C * 4 / 256; // float4 per thread: S (and dS') slice, v_new slice
+    // float4 per thread of an S (and dS') slice and of a v_new slice; at K = 32
+    // an S slice is 128 float4, taken by threads 0 .. 127
+    constexpr int SF4 = (K * 4 + 255) / 256, VF4 = C * 4 / 256;
+    constexpr bool SPART = K * 4 < 256;
     constexpr int NLT = NT * (NT + 1) / 2;              // lower tiles
     __shared__ __attribute__((aligned(16))) char smem[SM::bytes];
     float(*sS)[K][SP] = reinterpret_cast<float(*)[K][SP]>(smem + SM::oS);
@@ -473,10 +479,11 @@ __global__ __launch_bounds__(256, K >= 256 ? 1 : 2) void bwd_vprod_kernel(BwdPar
     floatx4 ls[SF4], ld_[SF4], lv[VF4], ldv[VF4], lu;
     auto load_slice = [&](int vb) {
 #pragma unroll
-        for (int i = 0; i < SF4; ++i) {
-            ls[i] = Sn[vb * K * 4 + i * 256 + tid];
-            ld_[i] = dSn[vb * K * 4 + i * 256 + tid];
-        }
+        for (int i = 0; i < SF4; ++i)
+            if (!SPART || tid < K * 4) {
+                ls[i] = Sn[vb * K * 4 + i * 256 + tid];
+                ld_[i] = dSn[vb * K * 4 + i * 256 + tid];
+            }
 #pragma unroll
         for (int i = 0; i < VF4; ++i) {
             lv[i] = vn[vb * C * 4 + i * 256 + tid];
@@ -487,15 +494,16 @@ __global__ __launch_bounds__(256, K >= 256 ? 1 : 2) void bwd_vprod_kernel(BwdPar
     // the fragments go to LDS as row-major slices (row, 16 columns)
     auto store_slice = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < SF4; ++i) {
-            const int r0 = 16 * (4 * i + (tid >> 6)) + g4;
+        for (int i = 0; i < SF4; ++i)
+            if (!SPART || tid < K * 4) {
+                const int r0 = 16 * (4 * i + (tid >> 6)) + g4;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                sS[buf][r0 + j][fc] = ls[i][j];
-                sD[buf][r0 + j][fc] = ld_[i][j];
+                for (int j = 0; j < 4; ++j) {
+                    sS[buf][r0 + j][fc] = ls[i][j];
+                    sD[buf][r0 + j][fc] = ld_[i][j];
+                }
+                gam[i] += ls[i] * ld_[i];
             }
-            gam[i] += ls[i] * ld_[i];
-        }
 #pragma unroll
         for (int i = 0; i < VF4; ++i) {
             const int r0 = 16 * (4 * i + (tid >> 6)) + g4;
@@ -568,7 +576,7 @@ __global__ __launch_bounds__(256, K >= 256 ? 1 : 2) void bwd_vprod_kernel(BwdPar
         for (int m = 1; m < 16; m <<= 1)
 #pragma unroll
             for (int j = 0; j < 4; ++j) g[j] += __shfl_xor(g[j], m, 64);
-        if (fc == 0)
+        if (fc == 0 && (!SPART || tid < K * 4))
 #pragma unroll
             for (int j = 0; j < 4; ++j) bp.ws_dgam[(size_t)cid * K + 16 * (4 * i + (tid >> 6)) + g4 + j] = g[j];
     }
@@ -961,17 +969,19 @@ __global__ __launch_bounds__(256) void bwd_gva_kernel(BwdParams bp) {
 template <int K, int V>
 hipError_t launch_bwd_t(const BwdParams &bp, hipStream_t s) {
     const ChunkParams &p = bp.f;
+    constexpr int NW = inter_nwv(K, V), VSW = 16 * NW; // waves and value columns per reverse-recurrence workgroup
+    static_assert(V % VSW == 0, "V");
     const int seqs = p.B * p.HV, nch = seqs * p.NC;
     hipError_t e;
     if (p.NSEG > 1) {
-        hipLaunchKernelGGL((bwd_inter_kernel<K, kRevLocal>), dim3(seqs * (p.NSEG - 1) * (V / 64)), dim3(256), 0, s, bp,
-                           1, p.NSEG - 1);
+        hipLaunchKernelGGL((bwd_inter_kernel<K, kRevLocal, NW>), dim3(seqs * (p.NSEG - 1) * (V / VSW)), dim3(64 * NW),
+                           0, s, bp, 1, p.NSEG - 1);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-        hipLaunchKernelGGL((bwd_chain_kernel<K>), dim3(seqs * (V / 64)), dim3(256), 0, s, bp);
+        hipLaunchKernelGGL((bwd_chain_kernel<K, NW>), dim3(seqs * (V / VSW)), dim3(64 * NW), 0, s, bp);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((bwd_inter_kernel<K, kRevOut>), dim3(seqs * p.NSEG * (V / 64)), dim3(256), 0, s, bp, 0,
-                       p.NSEG);
+    hipLaunchKernelGGL((bwd_inter_kernel<K, kRevOut, NW>), dim3(seqs * p.NSEG * (V / VSW)), dim3(64 * NW), 0, s, bp,
+                       0, p.NSEG);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_vprod_kernel<K, V>), dim3(nch), dim3(256), 0, s, bp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -996,6 +1006,10 @@ hipError_t launch_bwd(const BwdParams &bp, hipStream_t s) {
     if (K == 64 && V == 256) return launch_bwd_t<64, 256>(bp, s);
     if (K == 256 && V == 256) return launch_bwd_t<256, 256>(bp, s);
     if (K == 256 && V == 128) return launch_bwd_t<256, 128>(bp, s);
+    if (K == 128 && V == 192) return launch_bwd_t<128, 192>(bp, s);
+    if (K == 64 && V == 96) return launch_bwd_t<64, 96>(bp, s);
+    if (K == 32 && V == 32) return launch_bwd_t<32, 32>(bp, s);
+    if (K == 32 && V == 64) return launch_bwd_t<32, 64>(bp, s);
     return hipErrorInvalidValue;
 }
 

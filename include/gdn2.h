@@ -268,9 +268,8 @@ GDN2_API gdn2_status gdn2_stream_copy_f32(float *dst, const float *src, int64_t 
  * It recomputes the forward's per-chunk quantities (the reference's
  * FusedBackwardInputs) in its own workspace of
  * gdn2_chunk_bwd_workspace_bytes(args) bytes, 256-byte aligned.
- * Limits (else GDN2_NOT_APPLICABLE): those of gdn2_chunk_fwd_f32, with K in
- * {64, 128} and V in {64, 128, 256}, or K = 256 and V in {128, 256} (other
- * heads: gdn2_recurrent_bwd_f32).
+ * Limits (else GDN2_NOT_APPLICABLE): those of gdn2_chunk_fwd_f32, the same
+ * (K, V) pairs (other heads: gdn2_recurrent_bwd_f32).
  * ---------------------------------------------------------------------- */
 typedef struct gdn2_chunk_bwd_args {
     gdn2_chunk_args fwd;

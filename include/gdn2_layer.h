@@ -218,8 +218,7 @@ GDN2_API gdn2_status gdn2_layer_forward_train_saved_f32(gdn2_layer *layer, const
  *                d_state = the d_state_in of the call after it)
  * The result does not depend on cfg->mode (both modes compute the same
  * recurrence).  The recurrence's adjoint is gdn2_chunk_bwd_f32 where it
- * applies (head_dim in {64, 128} with head_v_dim in {64, 128, 256}, or
- * head_dim 256 with head_v_dim in {128, 256}), else
+ * applies (the (head_dim, head_v_dim) pairs of gdn2_chunk_fwd_f32), else
  * gdn2_recurrent_bwd_f32, whose limit is the only one here (else
  * GDN2_NOT_APPLICABLE). */
 GDN2_API gdn2_status gdn2_layer_backward_f32(gdn2_layer *layer, const float *x, int64_t batch, int64_t seq_len,

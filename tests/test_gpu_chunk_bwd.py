@@ -48,6 +48,13 @@ CASES = [
     (1, 2, 2, 2100, 128, 128, (-0.003, -0.0005), 1.0, 1.0, True),  # slow decay; seven segments of 5 chunks
     (1, 2, 2, 2560, 128, 128, (-0.001, 0.0), 0.0, 1.0, True),       # b = 0: S0 and d_state carried through
     (1, 1, 2, 6400, 64, 128, (-0.002, 0.0), 2.0, 1.0, True),        # 25 segments, GVA, negative eigenvalues
+    # the forward's other head shapes: two-wave reverse-recurrence workgroups (32 value columns)
+    (2, 2, 2, 130, 32, 32, (-0.3, -0.02), 1.0, 0.5, True),      # K = V = 32, ragged last chunk
+    (1, 1, 2, 150, 32, 64, (-0.5, -0.05), 2.0, 0.5, True),      # K = 32, V = 64, GVA, negative eigenvalues
+    (2, 1, 1, 97, 64, 96, (-0.3, -0.02), 1.0, 0.5, True),       # V = 96 (expand_v 1.5)
+    (1, 1, 1, 100, 128, 192, (-0.4, -0.01), 1.0, 0.5, False),   # V = 192
+    (1, 1, 1, 2100, 64, 96, (-0.003, -0.0005), 1.0, 1.0, True),   # segmented, V = 96
+    (1, 1, 2, 3000, 32, 32, (-0.002, 0.0), 2.0, 1.0, True),       # segmented, K = 32, GVA, negative eigenvalues
 ]
 
 
@@ -68,6 +75,8 @@ STRONG_CASES = [
     (1, 1, 1, 2100, 128, 128, (-6.0, -2.0), 2.0, 1.0, True),    # segmented, negative eigenvalues
     (1, 2, 2, 150, 128, 128, (-14.0, -0.05), 1.0, 0.5, True),   # all three regimes
     (1, 1, 2, 130, 64, 256, (-14.0, -0.05), 2.0, 0.5, True),    # all three, GVA, negative eigenvalues
+    (1, 1, 1, 200, 32, 32, (-31.0, -0.05), 1.0, 0.5, True),     # K = 32
+    (1, 2, 2, 150, 64, 96, (-31.0, -0.05), 2.0, 0.5, True),     # V = 96, negative eigenvalues
 ]
 
 def span_regimes(g, T):
@@ -238,6 +247,8 @@ SAVED_CASES = [
     (1, 1, 2, 150, 128, 256, (-31.0, -0.05)),    # GVA, V = 2K, masked diagonal channels
     (1, 2, 2, 2100, 128, 128, (-0.003, -0.0005)),  # segmented: every segment's transition kept
     (2, 2, 2, 97, 64, 64, (-0.3, -0.02)),
+    (1, 2, 2, 150, 64, 96, (-0.5, -0.05)),       # V = 96: two-wave workgroups
+    (1, 1, 2, 2100, 32, 64, (-0.003, -0.0005)),  # K = 32, segmented, GVA
 ]
 
 

@@ -80,6 +80,9 @@ CASES = {
                                        allow_neg_eigval=True, min_decay=0.9, mode="chunk"), 2, 100, True, True),
     "k128": (dict(hidden_size=512, num_heads=2, head_dim=128, mode="fused_recurrent"), 1, 300, False, False),
     "T2_state": (SMALL, 2, 2, True, True),
+    # the reference's CPU-benchmark layer (tests/bit_exact.rs:224-235): V = 96
+    "v96": (dict(SMALL, expand_v=1.5), 2, 130, False, True),
+    "k32": (dict(hidden_size=128, num_heads=4, head_dim=32, mode="chunk"), 1, 200, True, False),
 }
 
 
