@@ -294,8 +294,10 @@ OTHER_CONFIGS = {
             0.0, 47, "the reference's CPU-benchmark layer (tests/bit_exact.rs:224-235): hidden 256, 4 heads, K 64, "
                      "expand_v 1.5 (V 96), x [8, 4096, 256]"),
 }
-# configurations whose chunked backward is timed too (head_dim 256)
-BWD_CONFIGS = ("D256",)
+# configurations whose chunked backward is timed too: head_dim 256, V = 96 (two-wave
+# reverse-recurrence workgroups) and the long context's strong decays (the exact
+# diagonal terms of the decay pass, the segmented reverse recurrence)
+BWD_CONFIGS = ("C5", "D256", "V96")
 # configurations whose core is also timed on the per-token scan (gdn2_recurrent_fwd_f32,
 # the path their head shapes took before the chunk kernels covered them)
 SCAN_COMPARE = ("V96",)
@@ -375,7 +377,7 @@ def bench_other_config(torch, G, args, dev, name):
         names = ("segment_summaries", "chain", "output_pass")
         res["core"]["chunk_inter"]["passes_ms"] = {n: sum(pp) / reps for n, pp in zip(names, per_pass)}
     if name in BWD_CONFIGS and not args.no_backward:
-        res["backward"] = time_chunk_backward(torch, args, dev, q, k, g, b, v, w, desc)
+        res["backward"] = time_chunk_backward(torch, args, dev, q, k, g, b, v, w, desc, scan=name in SCAN_COMPARE)
     if name in SCAN_COMPARE:
         from gdn2_amd.ops import _p, _strides3
 
@@ -953,7 +955,7 @@ COPY_BYTES = 1 << 30
 KERNELS = {"chunk_intra": "chunk_intra_kernel<128, 128, false>", "chunk_inter": "chunk_inter_kernel<128, 0, 4>",
            "decode": "decode_fused_kernel<128, 128>", "step": "step_kernel<128, 128>"}
 BWD_KERNELS = ("chunk_intra_kernel<128, 128, true>", "chunk_inter_kernel<128, 2, 4>", "chunk_inter_kernel<128, 4, 4>",
-               "bwd_inter_kernel<128, 0>", "bwd_vprod_kernel<128, 128>", "bwd_decay_kernel<128, 128>")
+               "bwd_inter_kernel<128, 0, 4>", "bwd_vprod_kernel<128, 128>", "bwd_decay_kernel<128, 128>")
 
 
 def _short(name):
@@ -1109,17 +1111,32 @@ def mix_summary(csv1, csv2, n_xcc=8, n_simd=1024):
               f"{100 * wait:.0f} % |")
 
 
+def _tagged(name, frag):
+    """frag in the kernel name; a frag ending in a " (tag)" also needs the tag."""
+    if frag.endswith(")"):
+        base, tag = frag.rsplit(" (", 1)
+        return base in name and name.endswith(" (" + tag)
+    return frag in name
+
+
 def traffic_summary(fetch_csv, write_csv):
     """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) per kernel, scaled so that
     the 1 GiB streaming copy (gdn2_stream_copy_f32) reads and writes 1 GiB."""
     import csv
 
     def per_kernel(path, counter):
+        # the training chunk-intra serves the recomputing backward (followed by
+        # the states pass) and the training forward (followed by its output
+        # pass): its dispatches are named by the kernel that follows them
+        rows = sorted((r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter),
+                      key=lambda r: int(r["Dispatch_Id"]))
         acc = {}
-        for r in csv.DictReader(open(path)):
-            if r["Counter_Name"] != counter:
-                continue
-            acc.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]) * 1024.0)
+        for i, r in enumerate(rows):
+            name = r["Kernel_Name"]
+            if BWD_KERNELS[0] in _short(name) and i + 1 < len(rows):
+                nxt = _short(rows[i + 1]["Kernel_Name"])
+                name += " (recompute)" if BWD_KERNELS[1] in nxt else " (training forward)" if BWD_KERNELS[2] in nxt else ""
+            acc.setdefault(name, []).append(float(r["Counter_Value"]) * 1024.0)
         return acc
 
     fetch, write = per_kernel(fetch_csv, "FETCH_SIZE"), per_kernel(write_csv, "WRITE_SIZE")
@@ -1153,21 +1170,23 @@ def traffic_summary(fetch_csv, write_csv):
         with open(os.path.join(ROOT, "profiles", f"{key}_{suffix}_traffic.json"), "w") as fh:
             json.dump(out[key], fh, indent=1)
     # the chunked backward's kernels (bench.py's backward entry), printed only
-    for frag in BWD_KERNELS:
-        fv = [v for n, vals in fetch.items() if frag in n for v in vals]
-        wv = [v for n, vals in write.items() if frag in n for v in vals]
+    bwd = [BWD_KERNELS[0] + " (recompute)", BWD_KERNELS[1], BWD_KERNELS[0] + " (training forward)"] + list(BWD_KERNELS[2:])
+    for frag in bwd:
+        fv = [v for n, vals in fetch.items() if _tagged(n, frag) for v in vals]
+        wv = [v for n, vals in write.items() if _tagged(n, frag) for v in vals]
         if fv and wv:
             rd, wr = sum(fv) / len(fv) * f_fac, sum(wv) / len(wv) * w_fac
             print(f"| `{frag}` | {len(fv)} | {rd / 1e9:.3f} | {wr / 1e9:.3f} | {(rd + wr) / 1e9:.3f} |")
     return out
 
 
-def time_chunk_backward(torch, args, dev, q, k, g, b, v, w, label):
+def time_chunk_backward(torch, args, dev, q, k, g, b, v, w, label, scan=False):
     """gdn2_chunk_bwd_f32 on the given operands (d_out ~ N(0,1)): the
     gradients of q, k, g, b, v, w and S0, recomputing the forward's per-chunk
     quantities; then gdn2_chunk_fwd_train_f32 (the forward keeping them) and
-    gdn2_chunk_bwd_saved_f32 (the backward reading them).  Outputs and the
-    workspace are allocated before the timed regions."""
+    gdn2_chunk_bwd_saved_f32 (the backward reading them).  scan: also the
+    per-token scan's adjoint (gdn2_recurrent_bwd_f32) on the same operands.
+    Outputs and the workspaces are allocated before the timed regions."""
     import ctypes
 
     from gdn2_amd import _capi as CA
@@ -1221,6 +1240,20 @@ def time_chunk_backward(torch, args, dev, q, k, g, b, v, w, label):
         "training_forward": {"kernel": "gdn2_chunk_fwd_train_f32", "ms_per_step": fwd_ms,
                              "tokens_per_s": B * T / (fwd_ms / 1e3)},
         "what": "the backward reading the training forward's per-chunk quantities instead of recomputing them"}
+    if scan:
+        from gdn2_amd.ops import _strides3
+
+        rf = CA.RecurrentArgs(_p(q), _p(k), _p(g), _p(b), _p(v), _p(w), _p(S0), None, None, B, q.shape[1], v.shape[1], T, K,
+                              V, *_strides3(q), *_strides3(v), *_strides3(dO), K ** -0.5)
+        rb = CA.RecurrentBwdArgs(rf, _p(dO), None, *(_p(t) for t in grads), None, 0)
+        rneed = int(L.gdn2_recurrent_bwd_workspace_bytes(ctypes.byref(rb)))
+        rws = torch.empty(max(rneed, 1), dtype=torch.uint8, device=dev)
+        rb.workspace, rb.workspace_bytes = _p(rws), rneed
+        prb = ctypes.byref(rb)
+        scan_ms = timed(lambda: CA.check(L.gdn2_recurrent_bwd_f32(prb, stream)), max(1, min(args.steps, 5)))
+        res["scan"] = {"kernel": "gdn2_recurrent_bwd_f32", "ms_per_step": scan_ms,
+                       "tokens_per_s": B * T / (scan_ms / 1e3), "chunk_speedup": scan_ms / ms}
+        del rws
     del S0, dO, grads, ws, St, out
     torch.cuda.empty_cache()
     return res
