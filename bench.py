@@ -78,6 +78,10 @@ def parse():
                     help="host only: mean duration of the dispatches inside bench.py's timed regions (chunk-intra, "
                          "chunk-inter, decode) in a rocprofv3 kernel trace of a default run with the same "
                          "--warmup/--steps/--decode-steps")
+    ap.add_argument("--backward-summary", metavar="KERNEL_TRACE_CSV",
+                    help="host only: per timed section of a default run's rocprofv3 kernel trace that launches the "
+                         "chunked backward or the training forward, the mean duration of each chunk and backward "
+                         "kernel over the section's dispatches (warm-up and timed)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other benchmark configurations (C1, C4, C5)")
     ap.add_argument("--configs-only", action="store_true",
@@ -1035,6 +1039,36 @@ def timed_summary(path, warmup, steps, decode_steps):
                 break
 
 
+def backward_summary(path):
+    """The sections (see _timed_sections) of the backward entries: the
+    recomputing backward, the training forward and the saved backward of each
+    configuration timed with its backward, in launch order.  One line per
+    section: each chunk / backward kernel's mean duration and dispatch count,
+    and their sum (one call)."""
+    import csv
+
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    kinds = ("bwd_", "chunk_intra_kernel<", "chunk_inter_kernel<", "chunk_chain_kernel<")
+    for si, sec in enumerate(_timed_sections(rows)):
+        names = [_short(r["Kernel_Name"]) for r in sec]
+        # the backward's sections: a backward kernel, or the training variants of the forward;
+        # sections with GEMMs are the layer's
+        train = any(n.startswith("bwd_") or (n.startswith("chunk_intra_kernel<") and n.endswith("true>"))
+                    for n in names)
+        if not train or any(n.startswith("Cijk") for n in names):
+            continue
+        acc, order = {}, []
+        for r, n in zip(sec, names):
+            if not n.startswith(kinds):
+                continue
+            if n not in acc:
+                order.append(n)
+            acc.setdefault(n, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        tot = sum(sum(d) / len(d) for d in acc.values())
+        print(f"section {si}: " + ", ".join(f"`{n}` {sum(acc[n]) / len(acc[n]):.1f} (x{len(acc[n])})" for n in order)
+              + f"; sum {tot:.1f} us")
+
+
 def train_summary(path):
     """The kernels of the last training step of a --train-only trace: from the
     forward's input GEMM (the long GEMM before its project_kernel) to the end."""
@@ -1287,6 +1321,9 @@ def main():
         return
     if args.timed_summary:
         timed_summary(args.timed_summary, args.warmup, args.steps, args.decode_steps)
+        return
+    if args.backward_summary:
+        backward_summary(args.backward_summary)
         return
     if args.traffic_summary:
         traffic_summary(*args.traffic_summary)
