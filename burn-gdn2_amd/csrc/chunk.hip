@@ -74,7 +74,7 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
 
     // Region A: G (phases 1-2), then b k exp(G) (staging for the solve).
     __shared__ __attribute__((aligned(16))) float sG[C][KP];
-    // Region B: k (phases 1-2), then q exp(G) (staging), then A_qk | A_kk (phases 3-4).
+    // Region B: k (phases 1-2), then A_qk | A_kk (phases 3-4).
     __shared__ __attribute__((aligned(16))) float sR[RSZ];
     __shared__ __attribute__((aligned(16))) float sAinv[NT][16][20];
     __shared__ float sTot[NSEG][K];
@@ -82,7 +82,6 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
     __shared__ uint32_t sPair[NT][K / 32]; // those of them with a half-tile span > kSafeSpanMid
     __shared__ float sRef[NT][K];          // the score products' reference G per row tile
     float(*sK)[KP] = reinterpret_cast<float(*)[KP]>(sR);
-    float(*sQG)[KP] = reinterpret_cast<float(*)[KP]>(sR);
     float(*sBKG)[KP] = sG;
     float(*sAqk)[CP] = reinterpret_cast<float(*)[CP]>(sR);
     float(*sAkk)[CP] = reinterpret_cast<float(*)[CP]>(sR + C * CP);

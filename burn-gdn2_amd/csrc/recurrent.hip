@@ -290,7 +290,7 @@ __global__ __launch_bounds__(256) void decode_fused_kernel(DecodeParams p) {
     const int kd = p.H * K, vd = p.HV * V;
     const bool sc = p.use_short_conv != 0;
 
-    __shared__ float s_q[K], s_k[K], s_eg[K], s_a1[K], s_a2[K];
+    __shared__ float s_k[K], s_eg[K], s_a1[K], s_a2[K];
     __shared__ float s_red[2][4][VP];
     __shared__ float s_vn[V];
     __shared__ float red[3][4], red_o2[4];
