@@ -1,7 +1,8 @@
-"""The chunked forward under HIP graph capture (torch.cuda.CUDAGraph on the
-stream the C ABI receives): gdn2_chunk_fwd_f32 on a caller workspace and
-gdn2_chunk_fwd_noalloc_f32 on the library's static scratch, and the
-per-token scan.  Each graph is replayed several times with the program's
+"""The chunked forward and backward under HIP graph capture
+(torch.cuda.CUDAGraph on the stream the C ABI receives): gdn2_chunk_fwd_f32
+on a caller workspace, gdn2_chunk_fwd_noalloc_f32 on the library's static
+scratch, the per-token scan, gdn2_chunk_bwd_f32 and the training pair
+gdn2_chunk_fwd_train_f32 + gdn2_chunk_bwd_saved_f32.  Each graph is replayed several times with the program's
 own eager work in between (new inputs copied into the captured buffers, the
 state reset), and every replay must equal the eager call on the same inputs
 bit for bit: the entry points launch kernels only (fills by kernel, no
@@ -115,3 +116,63 @@ def test_scan_replays_in_a_graph(gpu):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(res["o"], ref[i][0]) and torch.equal(res["S"], ref[i][1]), f"replay {rep}"
+
+
+@pytest.mark.parametrize("shape", [(2, 2, 2, 200, 128, 128), (1, 1, 2, 2100, 64, 96)],
+                         ids=["B2T200", "B1T2100-segmented-V96"])
+def test_chunk_backward_replays_in_a_graph(gpu, shape):
+    """gdn2_chunk_bwd_f32 (recomputing the forward's per-chunk quantities),
+    and the pair gdn2_chunk_fwd_train_f32 + gdn2_chunk_bwd_saved_f32, each
+    captured once: every replay, with new operands and gradients of the
+    output and the final state copied in between, equals the eager call on
+    the same inputs bit for bit (the segmented shape takes the two-wave
+    reverse-recurrence workgroups and their chain)."""
+    import torch
+
+    import gdn2_amd as G
+
+    B, Hk, HV, T, K, V = shape
+    rng = np.random.default_rng(sum(shape))
+    sets = _sets(rng, 2, B, Hk, HV, T, K, V)
+    douts = [(rng.standard_normal((B, HV, T, V)).astype(np.float32),
+              rng.standard_normal((B, HV, K, V)).astype(np.float32)) for _ in range(2)]
+    bufs = [torch.empty(a.shape, device=gpu) for a in sets[0][:6]]
+    S0 = torch.empty((B, HV, K, V), device=gpu)
+    dO = torch.empty((B, HV, T, V), device=gpu)
+    dST = torch.empty((B, HV, K, V), device=gpu)
+    names = ("dq", "dk", "dg", "db", "dv", "dw", "dS0")
+    res = {}
+
+    def recompute():
+        res["g"] = G.chunk_wy_backward(*bufs, S0, dO, K ** -0.5, 64, d_state=dST)
+
+    def pair():
+        out, st, saved = G.chunk_wy_forward_train(*bufs, S0, K ** -0.5)
+        res["f"] = (out, st)
+        res["g"] = G.chunk_wy_backward(*bufs, S0, dO, K ** -0.5, 64, d_state=dST, saved=saved)
+
+    def load(i):
+        for buf, arr in zip(bufs, sets[i][:6]):
+            buf.copy_(torch.from_numpy(arr))
+        S0.copy_(torch.from_numpy(sets[i][6]))
+        dO.copy_(torch.from_numpy(douts[i][0]))
+        dST.copy_(torch.from_numpy(douts[i][1]))
+
+    for fn in (recompute, pair):
+        ref = []
+        for i in range(2):  # eager results
+            load(i)
+            fn()
+            torch.cuda.synchronize()
+            ref.append([res["g"][n].clone() for n in names] + [t.clone() for t in res.get("f", ())])
+        load(0)
+        graph = _capture(torch, fn)
+        for rep in range(4):
+            i = rep % 2
+            load(i)  # eager work between replays
+            graph.replay()
+            torch.cuda.synchronize()
+            got = [res["g"][n] for n in names] + list(res.get("f", ()))
+            for n, a, r in zip(names + ("out", "state"), got, ref[i]):
+                assert torch.equal(a, r), f"{fn.__name__} replay {rep}: {n}"
+        res.clear()
