@@ -1117,10 +1117,11 @@ def mix_summary(csv1, csv2, n_xcc=8, n_simd=1024):
     SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES."""
     import csv
 
+    kernels = dict(KERNELS, bwd_inter=BWD_KERNELS[3], bwd_vprod=BWD_KERNELS[4], bwd_decay=BWD_KERNELS[5])
     per = {}
     for path in (csv1, csv2):
         for r in csv.DictReader(open(path)):
-            for key, frag in KERNELS.items():
+            for key, frag in kernels.items():
                 if frag in r["Kernel_Name"]:
                     d = per.setdefault(key, {}).setdefault(r["Dispatch_Id"], {})
                     d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
@@ -1131,7 +1132,7 @@ def mix_summary(csv1, csv2, n_xcc=8, n_simd=1024):
 
     print("| kernel | waves | VALU | MFMA | SALU | LDS | VMEM rd / wr | MFMA busy (per SIMD) | wave cycles waiting |")
     print("|---|---|---|---|---|---|---|---|---|")
-    for key in KERNELS:
+    for key in kernels:
         if key not in per:
             continue
         waves = mean(key, "SQ_WAVES")
