@@ -101,6 +101,9 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
     constexpr bool QLDS = K <= 128;
     __shared__ floatx4 sKd[OPF4], sAT[AF4], sQT[QLDS ? OPF4 : 1], sWT[OPF4];
     __shared__ float sPf[256]; // destination of the L2 touches, never read
+    // e^{G_last} of the chunk, copied with the Q^T / W^T operands and read
+    // in phase 2: one copy for the workgroup instead of every wave's loads
+    __shared__ floatx4 sGam[K / 4];
 
     const int V = p.V, nvv = V / (16 * NW);
     int sq, vs;
@@ -156,7 +159,10 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
 #pragma unroll
         for (int i = 0; i < PFO; ++i) lds_copy4(&KD4[c * OPF4 + i * NTH + tid], &sKd[i * NTH + wv]);
 #pragma unroll
-        for (int i = 0; i < APF; ++i) lds_copy4(&AT4[c * AF4 + i * NTH + tid], &sAT[i * NTH + wv]);
+        for (int i = 0; i < APF; ++i) { // this wave's tile (st, rt) of the copy: A_qk^T needs rt >= st only
+            const int f = i * NW + wave;
+            if (f % NT >= f / NT) lds_copy4(&AT4[c * AF4 + i * NTH + tid], &sAT[i * NTH + wv]);
+        }
     };
     // chunk n's rows of d_out through a buffer resource over its valid rows
     // (rows past T read 0); row 4 lg of each 16-row tile, the rest of the row
@@ -198,10 +204,7 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
             for (int kb = 0; kb < NKT; ++kb)
                 reinterpret_cast<floatx4 *>(Dsn)[((col >> 4) * NKT + kb) * 64 + lane] = dS[kb];
         }
-        // e^{G_last} for this lane's rows 16 kb + 4 lg .. + 3 of dS'
-        floatx4 gam[NKT];
-#pragma unroll
-        for (int kb = 0; kb < NKT; ++kb) gam[kb] = G4[cid * (K / 4) + 4 * kb + lg];
+        if (wave == 0 && lane < K / 4) lds_copy4(&G4[cid * (K / 4) + lane], sGam);
 
         // 1: dv_new = Kd dS' + A_qk^T dO (A_qk^T is upper block-triangular).
         // Each k-step's Kd fragments are requested after the first quarter of
@@ -270,10 +273,11 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
         // 2: dS' <- e^{G_last} dS' + QG^T dO - W^T dv_new
 #pragma unroll
         for (int kb = 0; kb < NKT; ++kb) {
-            dS[kb][0] *= gam[kb][0];
-            dS[kb][1] *= gam[kb][1];
-            dS[kb][2] *= gam[kb][2];
-            dS[kb][3] *= gam[kb][3];
+            const floatx4 gam = sGam[4 * kb + lg]; // rows 16 kb + 4 lg .. + 3 of dS'
+            dS[kb][0] *= gam[0];
+            dS[kb][1] *= gam[1];
+            dS[kb][2] *= gam[2];
+            dS[kb][3] *= gam[3];
         }
         // each time tile's QG^T and W^T fragments are requested after the first
         // quarter of the previous tile's products.  -W^T dv_new = W^T (-dv_new):
