@@ -104,6 +104,15 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
     // e^{G_last} of the chunk, copied with the Q^T / W^T operands and read
     // in phase 2: one copy for the workgroup instead of every wave's loads
     __shared__ floatx4 sGam[K / 4];
+    // K = 128: the chunk's d_out rows of the workgroup's 16 NW columns,
+    // double-buffered, copied with Kd and A_qk^T (16-byte copies, a quarter of
+    // the vector memory instructions of per-lane row loads), in the LDS left
+    // beside its one workgroup per CU.  K = 256 has none left, and at K <= 64
+    // they would cost a second workgroup per CU: those load them into registers.
+    constexpr bool DOLDS = K == 128;
+    constexpr int VSW = 16 * NW, DOF4 = C * VSW / 4, DOPF = DOF4 / NTH;
+    static_assert(DOF4 % NTH == 0, "d_out block");
+    __shared__ floatx4 sDO[DOLDS ? 2 : 1][DOLDS ? DOF4 : 1];
 
     const int V = p.V, nvv = V / (16 * NW);
     int sq, vs;
@@ -165,8 +174,9 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
         }
     };
     // chunk n's rows of d_out through a buffer resource over its valid rows
-    // (rows past T read 0); row 4 lg of each 16-row tile, the rest of the row
-    // offset wave-uniform
+    // (rows past T read 0).  Registers: row 4 lg of each 16-row tile, the rest
+    // of the row offset wave-uniform.  LDS: the block [C][VSW] row-major in
+    // buffer n & 1, thread tid's float4 i at index i * NTH + tid.
     const float *dob = bp.d_out + (int64_t)bi * p.sob + (int64_t)hv * p.soh;
     const int ro = (int)p.sot, dol = 4 * lg * ro + col;
     auto load_dO = [&](floatx4 *dO, int n) {
@@ -176,11 +186,30 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
 #pragma unroll
             for (int i = 0; i < 4; ++i) dO[mt][i] = bld1(R, dol + (16 * mt + i) * ro);
     };
+    const int col0 = 16 * vs * NW; // the workgroup's first column
+    auto copy_dO = [&](int n) {
+        const __amdgpu_buffer_rsrc_t R = rows_rsrc(dob + (int64_t)n * C * p.sot, ro, min(C, p.T - n * C), V);
+#pragma unroll
+        for (int i = 0; i < DOPF; ++i) {
+            const int f = i * NTH + tid, row = f / (VSW / 4), c4 = f % (VSW / 4);
+            lds_copy4_rsrc(R, 4 * (row * ro + col0 + 4 * c4), &sDO[n & 1][i * NTH + wv]);
+        }
+    };
+    auto read_dO = [&](floatx4 *dO, int n) { // this lane's B-fragment values from the block
+        const float *blk = reinterpret_cast<const float *>(sDO[n & 1]);
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dO[mt][i] = blk[(16 * mt + 4 * lg + i) * VSW + 16 * wave + lr];
+    };
 
     floatx4 dO[NT]; // rows of d_out of the current chunk, loaded a phase ahead
     if (n1 > n0) {
         copy_ka(cid0 + n1 - 1);
-        load_dO(dO, n1 - 1);
+        if constexpr (DOLDS)
+            copy_dO(n1 - 1);
+        else
+            load_dO(dO, n1 - 1);
         __builtin_amdgcn_sched_barrier(0);
         touch_qw(cid0 + n1 - 1);
         __builtin_amdgcn_sched_barrier(0);
@@ -193,6 +222,7 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
         const size_t cid = cid0 + n;
         vm_wait<2>();  // this wave's copies of Kd, A_qk^T (n) and its dO rows have landed (not the 2 touches)
         lds_barrier(); // sKd, sAT hold chunk n; every wave is done with sQT, sWT (n+1)
+        if constexpr (DOLDS) read_dO(dO, n); // used from the end of phase 1 on
 #pragma unroll
         for (int i = 0; i < PFO; ++i) {
             if (QLDS) lds_copy4(&QT4[cid * OPF4 + i * NTH + tid], &sQT[i * NTH + wv]);
@@ -258,7 +288,10 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
         __builtin_amdgcn_sched_barrier(0);
         if (n > n0) {
             copy_ka(cid - 1);
-            load_dO(dO_next, n - 1);
+            if constexpr (DOLDS)
+                copy_dO(n - 1); // into the other buffer: every wave read this one after the last barrier
+            else
+                load_dO(dO_next, n - 1);
         }
         if (!LOCAL) {
             float *Dvn = bp.ws_dvn + cid * C * V;
@@ -315,7 +348,7 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        if (n > n0) {
+        if (!DOLDS && n > n0) {
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) dO[mt] = dO_next[mt];
         }

@@ -98,6 +98,12 @@ __device__ __forceinline__ void lds_copy4(const floatx4 *src, floatx4 *wave_base
     __builtin_amdgcn_global_load_lds(static_cast<const void *>(src),
                                      (__attribute__((address_space(3))) void *)(wave_base), 16, 0, 0);
 }
+// The same copy through a buffer resource (buffer_load_dwordx4 ... lds): the
+// range check zero-fills the lanes whose 16 bytes at byte offset `off` lie
+// past the resource, e.g. the rows past T of a rows_rsrc.
+__device__ __forceinline__ void lds_copy4_rsrc(__amdgpu_buffer_rsrc_t r, int off, floatx4 *wave_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(wave_base), 16, off, 0, 0, 0);
+}
 // Pulls the 128-byte line holding `line` toward this XCD's L2: a 4-byte copy
 // into the calling lane's word of wave_slot (64 floats per wave, never read).
 // It counts in vmcnt like lds_copy4, so a wait that must not cover it leaves
