@@ -149,10 +149,9 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
     // The operands go from global memory straight into LDS (lds_copy4: thread
     // tid's float4 i lands at index i * NTH + tid).  Each is also pulled
     // toward L2 ahead of its copy (l2_touch, one 128-byte line per thread):
-    // Kd, A_qk^T of chunk n - 2 during phase 1 of chunk n, QT, WT of chunk
-    // n - 1 during phase 2 of chunk n.  Each wave issues 2 touches last before
-    // every vmcnt wait, which leaves them in flight; outside the segment the
-    // chunk is clamped to it.
+    // Kd, A_qk^T of chunk n - 2 and QT, WT of chunk n - 1, both issued after
+    // the copies that follow chunk n's second barrier, so that they land during
+    // its phase 2; outside the segment the chunk is clamped to it.
     float *pf_slot = &sPf[wv];
     constexpr int LOP = OPF4 / 8, LA = AF4 / 8; // 128-byte lines per operand block
     auto clamp_c = [&](int n) { return cid0 + (size_t)max(n0, min(n1 - 1, n)); };
@@ -220,7 +219,7 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
 
     for (int n = n1 - 1; n >= n0; --n) {
         const size_t cid = cid0 + n;
-        vm_wait<2>();  // this wave's copies of Kd, A_qk^T (n) and its dO rows have landed (not the 2 touches)
+        vm_wait<2>();  // this wave's copies of Kd, A_qk^T (n) and its dO rows have landed (not the last 2 touches)
         lds_barrier(); // sKd, sAT hold chunk n; every wave is done with sQT, sWT (n+1)
         if constexpr (DOLDS) read_dO(dO, n); // used from the end of phase 1 on
 #pragma unroll
@@ -277,10 +276,7 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
 #pragma unroll
                     for (int st = 0; st <= rt; ++st) dvn[st] = mfma16(at[st][rt][j], dO[rt][j], dvn[st]);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        touch_ka(clamp_c(n - 2));
-        __builtin_amdgcn_sched_barrier(0);
-        vm_wait<2>();  // this wave's copies of QT, WT (n) and its e^{G_last} have landed (not the 2 touches)
+        vm_wait0();    // this wave's copies of QT, WT (n) and its e^{G_last} have landed
         lds_barrier(); // phase 1 done everywhere (sKd, sAT free); sQT, sWT (n) visible
 
         // Kd, A_qk^T and the dO rows of chunk n - 1; dv_new to the workspace
@@ -299,8 +295,13 @@ __global__ __launch_bounds__(64 * NW, 1) void bwd_inter_kernel(BwdParams bp, int
             for (int st = 0; st < NT; ++st)
                 reinterpret_cast<floatx4 *>(Dvn)[((col >> 4) * NT + st) * 64 + lane] = dvn[st];
         }
+        // the touches last, after this barrier's copies: issued before the
+        // barrier they would occupy the memory pipeline's outstanding line
+        // requests (64 lines per touch instruction, from HBM) while the copies
+        // above queue behind them
         __builtin_amdgcn_sched_barrier(0);
         touch_qw(clamp_c(n - 1));
+        touch_ka(clamp_c(n - 2));
         __builtin_amdgcn_sched_barrier(0);
 
         // 2: dS' <- e^{G_last} dS' + QG^T dO - W^T dv_new
