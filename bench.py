@@ -1051,16 +1051,17 @@ def backward_summary(path):
     kinds = ("bwd_", "chunk_intra_kernel<", "chunk_inter_kernel<", "chunk_chain_kernel<")
     for si, sec in enumerate(_timed_sections(rows)):
         names = [_short(r["Kernel_Name"]) for r in sec]
-        # the backward's sections: a backward kernel, or the training variants of the forward;
-        # sections with GEMMs are the layer's
+        # the backward's sections: a backward kernel, or the training variants of the forward,
+        # from the section's first dispatch on (the layer's sections start with its GEMMs;
+        # the next workload's set-up can follow in the same section)
         train = any(n.startswith("bwd_") or (n.startswith("chunk_intra_kernel<") and n.endswith("true>"))
                     for n in names)
-        if not train or any(n.startswith("Cijk") for n in names):
+        if not train or not names or not names[0].startswith(kinds):
             continue
         acc, order = {}, []
         for r, n in zip(sec, names):
             if not n.startswith(kinds):
-                continue
+                break  # the end of the backward entry's dispatches
             if n not in acc:
                 order.append(n)
             acc.setdefault(n, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
