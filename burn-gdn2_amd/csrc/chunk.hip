@@ -38,6 +38,8 @@
 // state S and v_new therefore never leave registers.
 #include "chunk_common.hpp"
 
+#include <mutex>
+
 namespace gdn2 {
 
 namespace {
@@ -714,8 +716,20 @@ constexpr int kInterOut = 0, kInterLocal = 1, kInterStates = 2, kInterOutStates 
 // NWV waves per workgroup (NWV = 4: 64 value columns; NWV = 2: 32, for value
 // dimensions that are not a multiple of 64 and for K = 32; NWV = 8: 128, pass 1
 // at K = 128).
+// Chunks [*n0, *n1) of segment seg (uniform runs of SEGL, or the inference
+// split's first segment of SEG0 then runs of SEGL), and the slot of segment
+// j's entering state in ws_qseg (its transition's in ws_pseg), per (b, hv).
+__device__ __forceinline__ void seg_range(const ChunkParams &p, int seg, int *n0, int *n1) {
+    const int a = p.SLOT0 ? (seg == 0 ? 0 : p.SEG0 + (seg - 1) * p.SEGL) : seg * p.SEGL;
+    *n0 = a;
+    *n1 = min(p.NC, p.SLOT0 && seg == 0 ? p.SEG0 : a + p.SEGL);
+}
+__device__ __forceinline__ size_t seg_slot(const ChunkParams &p, int bh, int j) {
+    return (size_t)bh * p.NSLOT + (j - p.SLOT0);
+}
+
 template <int K, int MODE, int NWV>
-__global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p, int nseg_launch) {
+__global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p, int nseg_launch, int seg_base) {
     constexpr bool OUT = MODE == kInterOut || MODE == kInterOutStates || MODE == kInterOutTrain;
     constexpr bool LOCAL = MODE == kInterLocal;
     constexpr bool STATES = MODE == kInterStates || MODE == kInterOutStates || MODE == kInterOutTrain;
@@ -745,7 +759,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p,
     const int nvs = LOCAL ? nvv + K / VSW : nvv; // pass 1 adds the slices of P
     int sq, vs;
     inter_block(blockIdx.x, p.B * p.HV * nseg_launch, nvs, &sq, &vs);
-    const int bh = sq / nseg_launch, seg = sq % nseg_launch;
+    const int bh = sq / nseg_launch, seg = seg_base + sq % nseg_launch;
     const int bi = bh / p.HV, hv = bh % p.HV;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (scalar)
@@ -753,14 +767,17 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p,
     const bool pcol = LOCAL && vs >= nvv;          // a slice of P (wave-uniform)
     const int vt = (pcol ? vs - nvv : vs) * NWV + wave; // this wave's 16-column tile
     const int col = 16 * vt + lr;
-    const int n0 = seg * p.SEGL;
-    const int n1 = min(p.NC, n0 + p.SEGL);
+    int n0, n1;
+    seg_range(p, seg, &n0, &n1);
 
-    // entering state: S0 (one segment), the chained state (pass 3; slot 0 is a
-    // copy of S0, so that no workgroup reads the state that the last segment
-    // overwrites), 0 (pass 1 value columns) or the identity (pass 1, P columns)
+    // entering state: S0 (one segment, or the split's segment 0), the chained
+    // state (pass 3; in uniform runs slot 0 is a copy of S0, so that no
+    // workgroup reads the state that the last segment overwrites), 0 (pass 1
+    // value columns) or the identity (pass 1, P columns)
     const float *Sin = nullptr;
-    if (!LOCAL) Sin = p.NSEG == 1 ? p.state + (size_t)bh * K * V : p.ws_qseg + ((size_t)bh * p.NSEG + seg) * K * V;
+    if (!LOCAL)
+        Sin = p.NSEG == 1 || (p.SLOT0 && seg == 0) ? p.state + (size_t)bh * K * V
+                                                   : p.ws_qseg + seg_slot(p, bh, seg) * K * V;
     floatx4 S[NKT];
 #pragma unroll
     for (int kb = 0; kb < NKT; ++kb)
@@ -1031,16 +1048,20 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p,
         store_out(X2, n1 - 1);
     }
 
-    // leaving state: the final state (last segment), Q_j or P_j (pass 1)
+    // leaving state: the final state (last segment), the state entering
+    // segment 1 (the split's segment 0), Q_j or P_j (pass 1)
     float *Sout = nullptr;
     int ld = V;
     if (OUT) {
-        if (seg == p.NSEG - 1) Sout = p.state + (size_t)bh * K * V;
+        if (seg == p.NSEG - 1)
+            Sout = p.state + (size_t)bh * K * V;
+        else if (MODE == kInterOut && p.SLOT0 && seg == 0)
+            Sout = p.ws_qseg + seg_slot(p, bh, 1) * K * V;
     } else if (LOCAL && pcol) {
-        Sout = p.ws_pseg + ((size_t)bh * p.NSEG + seg) * K * K;
+        Sout = p.ws_pseg + seg_slot(p, bh, seg) * K * K;
         ld = K;
     } else if (LOCAL && seg + 1 < p.NSEG) { // (the last segment runs for its P only: training)
-        Sout = p.ws_qseg + ((size_t)bh * p.NSEG + seg + 1) * K * V;
+        Sout = p.ws_qseg + seg_slot(p, bh, seg + 1) * K * V;
     }
     if (Sout) {
 #pragma unroll
@@ -1050,11 +1071,13 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_inter_kernel(ChunkParams p,
     }
 }
 
-// Pass 2 of the segmented form.  ws_qseg holds NSEG slots of K x V per
-// (b, hv): slot 0 <- S0, then slot j + 1 (Q_j from pass 1) <- S_in(j + 1) =
-// P_j S_in(j) + Q_j for j = 0 .. NSEG - 2.  One workgroup per (b, hv, 64 value
-// columns); S in MFMA accumulators, P_j read as A-operand fragments
-// (lane (g, r): row r of a 16-row tile, columns 4g .. 4g + 3) from L2.
+// Pass 2 of the segmented form.  Per (b, hv), the slot of segment j + 1
+// (Q_j from pass 1) <- S_in(j + 1) = P_j S_in(j) + Q_j for j = j0 .. NSEG - 2:
+// in uniform runs j0 = 0 and slot 0 <- S0 first; in the split j0 = 1 and
+// S_in(1) is already in its slot (segment 0's walk left it there).  One
+// workgroup per (b, hv, 64 value columns); S in MFMA accumulators, P_j read
+// as A-operand fragments (lane (g, r): row r of a 16-row tile, columns 4g ..
+// 4g + 3) from L2.
 template <int K, int NWV>
 __global__ __launch_bounds__(64 * NWV, 1) void chunk_chain_kernel(ChunkParams p) {
     constexpr int NKT = K / 16;
@@ -1066,8 +1089,9 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_chain_kernel(ChunkParams p)
     const int lr = lane & 15, lg = lane >> 4;
     const int col = 16 * (vs * NWV + wave) + lr;
 
-    const float *S0 = p.state + (size_t)bh * K * V;
-    float *slot0 = p.ws_qseg + (size_t)bh * p.NSEG * K * V;
+    const int j0 = p.SLOT0;
+    const float *S0 = j0 ? p.ws_qseg + seg_slot(p, bh, 1) * K * V : p.state + (size_t)bh * K * V;
+    float *slot0 = p.ws_qseg + seg_slot(p, bh, j0) * K * V; // the slot of segment j0
     floatx4 S[NKT];
 #pragma unroll
     for (int kb = 0; kb < NKT; ++kb)
@@ -1075,20 +1099,20 @@ __global__ __launch_bounds__(64 * NWV, 1) void chunk_chain_kernel(ChunkParams p)
         for (int i = 0; i < 4; ++i) {
             const size_t o = (size_t)(16 * kb + 4 * lg + i) * V + col;
             S[kb][i] = S0[o];
-            slot0[o] = S[kb][i];
+            if (!j0) slot0[o] = S[kb][i];
         }
     // Every operand is requested one step ahead of its products: the next
     // k-block of P_j (two register buffers), the first k-block of P_{j+1} during
     // the last one of P_j, and Q_{j+1} during the products of step j, so that
     // a step waits on no memory round trip but its own first one.
-    const int nsteps = p.NSEG - 1;
-    auto P_of = [&](int j) { return p.ws_pseg + ((size_t)bh * p.NSEG + j) * K * K; };
+    const int nsteps = p.NSEG - 1 - j0; // step i chains segment j0 + i
+    auto P_of = [&](int i) { return p.ws_pseg + seg_slot(p, bh, j0 + i) * K * K; };
     auto load_pa = [&](floatx4 *pa, const float *P, int kb) {
 #pragma unroll
         for (int it = 0; it < NKT; ++it)
             pa[it] = *reinterpret_cast<const floatx4 *>(P + (size_t)(16 * it + lr) * K + 16 * kb + 4 * lg);
     };
-    auto load_q = [&](floatx4 *q, int j) { // slot j + 1 holds Q_j from pass 1
+    auto load_q = [&](floatx4 *q, int j) { // slot j + 1 (from segment j0's) holds Q_{j0 + j} from pass 1
         const float *Q = slot0 + (size_t)(j + 1) * K * V;
 #pragma unroll
         for (int it = 0; it < NKT; ++it)
@@ -1198,13 +1222,136 @@ __global__ __launch_bounds__(256) void chunk_states_kernel(ChunkParams p) {
     }
 }
 
+// The inference output split.  A uniform run of n = NSEG segments (n >= 2)
+// walks every segment twice: pass 1 (its local state and transition from 0)
+// and pass 3 (with the output).  Segment 0 needs no pass 1, its entering state
+// being S0: the split walks it once, with the output, while pass 1 summarises
+// segments 1 .. n - 1, then pass 3 walks segments 1 .. n.  With n + 1
+// segments in all, pass 3's workgroups stay those of the uniform run's n, and
+// segment 0's walk takes one value slice per sequence beside pass 1's.
+// Segment 0 gets L0 = r NC / (n + r) chunks and the others L = ceil((NC - L0)
+// / n), so that its walk and pass 1 end together: r = 1.1 where pass 1 runs
+// eight waves over 128 columns, two per SIMD (the fastest of r = 0.5 .. 1.8
+// at B = 1, T = 65536, 16 heads, K = V = 128), else 0.8 (pass 1 cheaper per
+// chunk than the walk; the fastest of 0.6 .. 1.6 at B = 8, T = 4096, 4
+// heads, K = 64, V = 96).  Only where every segment keeps at least
+// kMinSplitChunks chunks; else the uniform run.
+constexpr int kMinSplitChunks = 16;
+
+bool split_segments(const ChunkParams &p, bool wide_pass1, ChunkParams *q) {
+    if (p.NSEG < 2) return false;
+    const int n = p.NSEG, NC = p.NC;
+    const double r = wide_pass1 ? 1.1 : 0.8;
+    const int L0 = (int)(r * NC / (n + r));
+    const int L = (NC - L0 + n - 1) / n;
+    const int last = NC - L0 - (n - 1) * L;
+    if (L0 < kMinSplitChunks || L < kMinSplitChunks || last < 1) return false;
+    *q = p;
+    q->NSEG = n + 1;
+    q->SEG0 = L0;
+    q->SEGL = L;
+    q->SLOT0 = 1; // segments 1 .. n in slots 0 .. n - 1 of the uniform run's n
+    return true;
+}
+
+// A second stream per device (default priority, non-blocking) with a fork
+// and a join event, for the split's segment-0 walk beside pass 1.  Created on
+// first use, never while the caller's stream is capturing (then, and if
+// creation fails, the two launches run in order on the caller's stream: the
+// same kernels and results).  One mutex keeps each record/wait/launch/record/
+// wait sequence whole when several host threads launch.
+struct AuxStream {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    bool tried = false;
+};
+constexpr int kMaxDevices = 64;
+std::mutex g_aux_mu;
+AuxStream g_aux[kMaxDevices];
+
+AuxStream *aux_stream(hipStream_t s) { // called with g_aux_mu held
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    AuxStream &a = g_aux[dev];
+    if (a.s) return &a;
+    if (a.tried) return nullptr;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
+    a.tried = true;
+    if (hipStreamCreateWithFlags(&a.s, hipStreamNonBlocking) != hipSuccess) {
+        a.s = nullptr;
+        return nullptr;
+    }
+    if (hipEventCreateWithFlags(&a.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&a.join, hipEventDisableTiming) != hipSuccess) {
+        if (a.fork) (void)hipEventDestroy(a.fork);
+        (void)hipStreamDestroy(a.s);
+        a = AuxStream{};
+        a.tried = true;
+        return nullptr;
+    }
+    return &a;
+}
+
+// on_aux(stream) after the work queued on s so far, beside on_s(s); s then
+// waits for both.
+template <class FA, class FS>
+hipError_t fork_join(hipStream_t s, FA on_aux, FS on_s) {
+    std::lock_guard<std::mutex> lock(g_aux_mu);
+    AuxStream *a = aux_stream(s);
+    if (!a) {
+        on_aux(s);
+        on_s(s);
+        return hipGetLastError();
+    }
+    hipError_t e = hipEventRecord(a->fork, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(a->s, a->fork, 0);
+    if (e != hipSuccess) return e;
+    on_aux(a->s);
+    const hipError_t el = hipGetLastError();
+    on_s(s);
+    const hipError_t el2 = hipGetLastError();
+    e = hipEventRecord(a->join, a->s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(s, a->join, 0);
+    return e != hipSuccess ? e : el != hipSuccess ? el : el2;
+}
+
+// Dynamic LDS that brings a workgroup of chunk_inter_kernel<K, MODE, NW> to
+// more than half of a compute unit's 160 KiB, so that no two share one: the
+// split's concurrent pair then spreads one workgroup per compute unit instead
+// of packing small workgroups of both kernels onto the same ones (two-wave
+// workgroups at K = 64 ran 40-60 % slower per chunk packed so).
+template <int K, int MODE, int NW>
+size_t half_cu_pad() {
+    static const size_t pad = [] {
+        hipFuncAttributes a{};
+        if (hipFuncGetAttributes(&a, reinterpret_cast<const void *>(&chunk_inter_kernel<K, MODE, NW>)) != hipSuccess)
+            return size_t(0);
+        constexpr size_t half = 80 * 1024 + 256;
+        return a.sharedSizeBytes >= half ? size_t(0) : half - a.sharedSizeBytes;
+    }();
+    return pad;
+}
+
+// Pass 3 (or the only pass) of chunk-inter in mode MODE over segments
+// seg_base .. seg_base + nseg - 1, with lds bytes of dynamic LDS.
+template <int K, int V, int MODE>
+void launch_inter(const ChunkParams &p, hipStream_t s, int nseg, int seg_base, size_t lds = 0) {
+    constexpr int NWV = inter_nwv(K, V), VSW = 16 * NWV;
+    hipLaunchKernelGGL((chunk_inter_kernel<K, MODE, NWV>), dim3(p.B * p.HV * nseg * (V / VSW)), dim3(64 * NWV), lds,
+                       s, p, nseg, seg_base);
+}
+
 // phases: 1 intra; 2 inter with the output, 4 training (every segment's P and
 // the backward's per-chunk states and v_new; with 2 also the output), 8
 // output plus v_new and the per-chunk states (2, 4, 8 run every inter pass the
 // shape needs); one pass of the segmented inter alone (phase diagnostics):
-// 16 segment summaries, 32 chain, 64 output pass.
+// 16 segment summaries (with the split, beside segment 0's walk), 32 chain,
+// 64 output pass.  The inference output (2 alone, or 16 / 32 / 64) takes the
+// split where split_segments allows it; the training and states runs keep
+// uniform segments, whose transitions the backward reuses.
 template <int K, int V>
-hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
+hipError_t launch_chunk_t(const ChunkParams &p0, hipStream_t s, int phases) {
     constexpr int NWV = inter_nwv(K, V), VSW = 16 * NWV; // waves and value columns per sequential workgroup
     // Pass 1 (segment summaries: no output, so no q exp(G) or A_qk in LDS) at
     // K = 128 takes 128 columns (V or P) per workgroup of eight waves: the
@@ -1212,17 +1359,43 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
     // per SIMD still fit its registers.
     constexpr int NWL = (K == 128 && V % 128 == 0) ? 8 : NWV, VSWL = 16 * NWL;
     const dim3 blk(64 * NWV), blkl(64 * NWL);
-    const int seqs = p.B * p.HV;
-    if (phases & 112) {
-        if ((phases & 16) && p.NSEG > 1)
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal, NWL>), dim3(seqs * (p.NSEG - 1) * ((V + K) / VSWL)),
-                               blkl, 0, s, p, p.NSEG - 1);
-        if ((phases & 32) && p.NSEG > 1)
-            hipLaunchKernelGGL((chunk_chain_kernel<K, NWV>), dim3(seqs * (V / VSW)), blk, 0, s, p);
-        if (phases & 64)
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOut, NWV>), dim3(seqs * p.NSEG * (V / VSW)), blk, 0, s, p,
-                               p.NSEG);
+    const int seqs = p0.B * p0.HV;
+    const bool infer = (phases & 112) || (phases & 14) == 2;
+    ChunkParams ps;
+    const bool split = infer && split_segments(p0, NWL == 8, &ps);
+    const ChunkParams &p = split ? ps : p0;
+    auto summaries = [&](int nl) -> hipError_t { // pass 1 over segments 0 .. nl - 1 (uniform)
+        hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal, NWL>), dim3(seqs * nl * ((V + K) / VSWL)), blkl, 0, s,
+                           p, nl, 0);
         return hipGetLastError();
+    };
+    auto first_pass = [&]() -> hipError_t { // pass 1, or the split's segment 0 beside it
+        if (!split) return p.NSEG > 1 ? summaries(p.NSEG - 1) : hipSuccess;
+        return fork_join(
+            s, [&](hipStream_t sa) { launch_inter<K, V, kInterOut>(p, sa, 1, 0, half_cu_pad<K, kInterOut, NWV>()); },
+            [&](hipStream_t sm) {
+                const size_t lds = half_cu_pad<K, kInterLocal, NWL>();
+                hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal, NWL>),
+                                   dim3(seqs * (p.NSEG - 2) * ((V + K) / VSWL)), blkl, lds, sm, p, p.NSEG - 2, 1);
+            });
+    };
+    auto chain = [&]() -> hipError_t {
+        hipLaunchKernelGGL((chunk_chain_kernel<K, NWV>), dim3(seqs * (V / VSW)), blk, 0, s, p);
+        return hipGetLastError();
+    };
+    auto output_pass = [&]() -> hipError_t { // pass 3 (split: segments 1 .. NSEG - 1)
+        if (split)
+            launch_inter<K, V, kInterOut>(p, s, p.NSEG - 1, 1);
+        else
+            launch_inter<K, V, kInterOut>(p, s, p.NSEG, 0);
+        return hipGetLastError();
+    };
+    hipError_t e = hipSuccess;
+    if (phases & 112) {
+        if ((phases & 16) && p.NSEG > 1 && (e = first_pass()) != hipSuccess) return e;
+        if ((phases & 32) && p.NSEG > 1 && (e = chain()) != hipSuccess) return e;
+        if (phases & 64) return output_pass();
+        return hipSuccess;
     }
     if (phases & 1) {
         const int nchunks = p.B * p.HV * p.NC;
@@ -1230,31 +1403,28 @@ hipError_t launch_chunk_t(const ChunkParams &p, hipStream_t s, int phases) {
             hipLaunchKernelGGL((chunk_intra_kernel<K, V, true>), dim3(nchunks), dim3(512), 0, s, p);
         } else
             hipLaunchKernelGGL((chunk_intra_kernel<K, V, false>), dim3(nchunks), dim3(512), 0, s, p);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+        if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     if (phases & 14) {
+        if (infer) {
+            if (p.NSEG > 1) {
+                if ((e = first_pass()) != hipSuccess) return e;
+                if ((e = chain()) != hipSuccess) return e;
+            }
+            return output_pass();
+        }
         if (p.NSEG > 1) {
             // the training forward (phases & 4) also takes the last segment's P, which
             // the backward's reverse chain uses
-            const int nl = (phases & 4) ? p.NSEG : p.NSEG - 1;
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterLocal, NWL>), dim3(seqs * nl * ((V + K) / VSWL)), blkl, 0,
-                               s, p, nl);
-            hipError_t e = hipGetLastError();
-            if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((chunk_chain_kernel<K, NWV>), dim3(seqs * (V / VSW)), blk, 0, s, p);
-            e = hipGetLastError();
-            if (e != hipSuccess) return e;
+            if ((e = summaries((phases & 4) ? p.NSEG : p.NSEG - 1)) != hipSuccess) return e;
+            if ((e = chain()) != hipSuccess) return e;
         }
-        const dim3 grid(seqs * p.NSEG * (V / VSW));
         if (phases & 8)
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOutStates, NWV>), grid, blk, 0, s, p, p.NSEG);
+            launch_inter<K, V, kInterOutStates>(p, s, p.NSEG, 0);
         else if ((phases & 6) == 6) // the training forward
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOutTrain, NWV>), grid, blk, 0, s, p, p.NSEG);
-        else if (phases & 2)
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterOut, NWV>), grid, blk, 0, s, p, p.NSEG);
+            launch_inter<K, V, kInterOutTrain>(p, s, p.NSEG, 0);
         else // the backward's states pass
-            hipLaunchKernelGGL((chunk_inter_kernel<K, kInterStates, NWV>), grid, blk, 0, s, p, p.NSEG);
+            launch_inter<K, V, kInterStates>(p, s, p.NSEG, 0);
         return hipGetLastError();
     }
     return hipSuccess;
@@ -1420,6 +1590,8 @@ gdn2_status chunk_setup(const gdn2_chunk_args *a, const char *who, bool need_out
     const Segments sg = inter_segments(p->B * p->HV, 1, p->K, p->V, p->NC);
     p->NSEG = sg.nseg;
     p->SEGL = sg.segl;
+    p->NSLOT = sg.nseg; // uniform runs; the inference split keeps these slots
+    p->SEG0 = p->SLOT0 = 0;
     return GDN2_OK;
 }
 

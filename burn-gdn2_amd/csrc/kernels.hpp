@@ -66,6 +66,12 @@ struct ChunkParams {
     float *ws_qseg; // NSEG x K*V      state entering each segment (slot j + 1 first
                     //                 holds segment j's state from S = 0)
     int NSEG, SEGL;
+    // Inference output split (SLOT0 = 1): segment 0 has SEG0 chunks and is
+    // walked with the output from S0 beside pass 1, segment j >= 1 starts at
+    // chunk SEG0 + (j - 1) SEGL and its slots are j - 1; pass 1 covers
+    // segments 1 .. NSEG - 2.  Uniform runs: SEG0 = SLOT0 = 0.  NSLOT is the
+    // slots per (b, hv) of ws_pseg / ws_qseg (the uniform run's NSEG).
+    int SEG0, NSLOT, SLOT0;
     // Training forward (null in inference): the operands of the backward.
     float *ws_wt;   // C*K  W^T as A-operand tiles (key tile, time tile)
     float *ws_qgt;  // C*K  (scale q exp(G))^T, same order

@@ -172,6 +172,65 @@ def test_chunk_segmented_matches_recurrence(gpu, case):
     assert eo < TOL and es < TOL
 
 
+def split_plan(B, HV, T, K, V):
+    """The inference forward's chunk-inter plan for a shape, restated from
+    chunk.hip (inter_segments, split_segments) so that a case can assert which
+    form it reaches: (uniform segment count n, None) or (n, (L0, L)) where the
+    split walks segment 0 (L0 chunks) beside pass 1 and the other n segments
+    have L chunks (the last fewer)."""
+    nwv = 4 if (V % 64 == 0 and K % 64 == 0) else 2
+    NC = (T + 63) // 64
+    w = B * HV * (V // (16 * nwv))
+    n = min(256 // w, NC // 4)
+    if n < 2:
+        return 1, None
+    L = -(-NC // n)
+    n = -(-NC // L)
+    if n < 2:
+        return n, None
+    r = 1.1 if (K == 128 and V % 128 == 0) else 0.8
+    L0 = int(r * NC / (n + r))
+    Ls = -(-(NC - L0) // n)
+    if L0 < 16 or Ls < 16 or NC - L0 - (n - 1) * Ls < 1:
+        return n, None
+    return n, (L0, Ls)
+
+
+SPLIT_CASES = [
+    # few long sequences whose uniform run has at most 8 segments of >= 16
+    # chunks: segment 0 is walked with the output from S0 beside pass 1 of the
+    # others, whose chain then starts from the state segment 0 left
+    (1, 8, 16, 10000, 128, 128, (-0.01, -0.001), 1.0, 1.0),  # the long-context class, GVA, ragged end
+    (2, 16, 16, 12000, 64, 64, (-0.3, -0.02), 1.0, 0.5),
+    (1, 16, 16, 11000, 64, 96, (-0.002, 0.0), 2.0, 1.0),     # V = 96 (two-wave slices), negative eigenvalues
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES,
+                         ids=[f"B{c[0]}H{c[1]}HV{c[2]}T{c[3]}K{c[4]}V{c[5]}" for c in SPLIT_CASES])
+def test_chunk_split_first_segment_matches_recurrence(gpu, case):
+    """The inference forward's split (segment 0 walked once, with the output,
+    beside the other segments' summaries; the chain and output pass over the
+    rest) == the per-token recurrence, with nonzero S0."""
+    import gdn2_amd
+
+    B, Hk, HV, T, K, V, (glo, ghi), bhi, s0 = case
+    n, plan = split_plan(B, HV, T, K, V)
+    assert plan is not None, (n, plan)
+    print(f"case {case}: uniform segments {n}, split (L0, L) = {plan}", flush=True)
+    rng = np.random.default_rng(3000 + T + K + V)
+    q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=glo, g_hi=ghi, b_hi=bhi)
+    q *= K ** -0.5 * 4
+    S0 = (rng.standard_normal((B, HV, K, V)) * s0).astype(np.float32)
+    scale = K ** -0.5
+    d = _dev(gpu, q, k, v, g, b, w, S0)
+    o, S = gdn2_amd.chunk_wy_forward(*d, scale, chunk_size=64)
+    o_ref, S_ref = O.recurrent_f64(q, k, v, g, b, w, S0=S0, scale=scale)
+    eo, es = maxabs(o.cpu().numpy(), o_ref), maxabs(S.cpu().numpy(), S_ref)
+    print(f"  max|out err|={eo:.2e} max|S err|={es:.2e}")
+    assert eo < TOL and es < TOL
+
+
 def test_chunk_strided_views_and_in_place_state(gpu):
     """q/k/g/b/v/w as [B, H, T, D] views of [B, T, H, D] storage and out
     written straight into [B, T, HV, V] (no permute copies)."""
@@ -379,13 +438,14 @@ def test_chunk_states_refuse_other_chunk_sizes(gpu):
     assert gdn2_amd.chunk_wy_forward(*d2, 0.125, chunk_size=32, return_states=True) is None  # 90 % 32 != 0
 
 
-@pytest.mark.parametrize("shape", [(1, 2, 2, 2048, 128, 128), (2, 2, 2, 300, 128, 128)],
-                         ids=["segmented", "one_segment"])
+@pytest.mark.parametrize("shape", [(1, 2, 2, 2048, 128, 128), (1, 8, 16, 9000, 128, 128), (2, 2, 2, 300, 128, 128)],
+                         ids=["segmented", "split", "one_segment"])
 def test_inter_passes_equal_inter(gpu, shape):
     """gdn2_chunk_inter_pass_f32 1, 2, 3 after gdn2_chunk_intra_f32 equal
-    gdn2_chunk_inter_f32 bit for bit (the phase bits of the passes, and pass 3
-    alone being the whole inter phase when there is one segment);
-    gdn2_chunk_segments names the split; other pass numbers are refused."""
+    gdn2_chunk_inter_f32 bit for bit (the phase bits of the passes, pass 1
+    with the split's segment-0 walk beside it, and pass 3 alone being the
+    whole inter phase when there is one segment); gdn2_chunk_segments names
+    the uniform segment count; other pass numbers are refused."""
     import ctypes
 
     import torch
@@ -395,6 +455,7 @@ def test_inter_passes_equal_inter(gpu, shape):
     from gdn2_amd.ops import _stream, chunk_args
 
     B, Hk, HV, T, K, V = shape
+    assert (split_plan(B, HV, T, K, V)[1] is not None) == (T == 9000)
     rng = np.random.default_rng(77 + T)
     q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=-0.01, g_hi=-0.001)
     S0 = rng.standard_normal((B, HV, K, V)).astype(np.float32)
@@ -408,7 +469,8 @@ def test_inter_passes_equal_inter(gpu, shape):
         ws = torch.empty(gdn2_amd.chunk_workspace_bytes(*d, st, out, scale, 64), dtype=torch.uint8, device=gpu)
         a = chunk_args(*d, st, out, scale, 64, ws)
         nseg = int(L.gdn2_chunk_segments(ctypes.byref(a)))
-        assert (nseg > 1) == (shape[3] == 2048), nseg
+        assert (nseg > 1) == (shape[3] >= 2048), nseg
+        assert nseg == split_plan(B, HV, T, K, V)[0]
         C.check(L.gdn2_chunk_intra_f32(ctypes.byref(a), stream))
         if by_pass:
             for ps in (1, 2, 3):

@@ -39,9 +39,16 @@ def _sets(rng, n, B, Hk, HV, T, K, V):
     return out
 
 
-@pytest.mark.parametrize("entry", ["gdn2_chunk_fwd_f32", "gdn2_chunk_fwd_noalloc_f32"])
-@pytest.mark.parametrize("shape", [(2, 2, 2, 200, 128, 128), (1, 1, 2, 2048, 128, 128)],
-                         ids=["B2T200", "B1T2048-segmented"])
+FWD_GRAPH_CASES = [(e, s) for e in ("gdn2_chunk_fwd_f32", "gdn2_chunk_fwd_noalloc_f32")
+                   for s in ((2, 2, 2, 200, 128, 128), (1, 1, 2, 2048, 128, 128))]
+# the inference split (segment 0 walked on a second stream, forked and joined
+# by events, beside pass 1): too large for the no-alloc scratch
+FWD_GRAPH_CASES.append(("gdn2_chunk_fwd_f32", (1, 8, 16, 9000, 128, 128)))
+
+
+@pytest.mark.parametrize("entry,shape", FWD_GRAPH_CASES,
+                         ids=[f"{e}-B{s[0]}T{s[3]}" + ("-segmented" if s[3] == 2048 else "-split" if s[3] == 9000 else "")
+                              for e, s in FWD_GRAPH_CASES])
 def test_chunk_forward_replays_in_a_graph(gpu, entry, shape):
     import torch
 
