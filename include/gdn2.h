@@ -173,9 +173,13 @@ GDN2_API gdn2_status gdn2_chunk_inter_f32(const gdn2_chunk_args *args, gdn2_stre
  * the compute units: pass 1 runs every segment but the last from a zero state
  * (its transition and offset), pass 2 chains the segments' entering states,
  * pass 3 re-runs every segment from its entering state and writes out and the
- * final state.  With one segment, passes 1 and 2 launch nothing.  Called
- * 1, 2, 3 in order on one stream after gdn2_chunk_intra_f32 they equal
- * gdn2_chunk_inter_f32.  Any other pass is GDN2_EINVAL. */
+ * final state.  Where those segments are long (16 chunks and more), one more
+ * segment is cut and segment 0, whose entering state is S0, is walked once
+ * with the output during pass 1 (on a second stream the library forks from
+ * and joins back to `stream`); passes 2 and 3 then cover the rest.  With one
+ * segment, passes 1 and 2 launch nothing.  Called 1, 2, 3 in order on one
+ * stream after gdn2_chunk_intra_f32 they equal gdn2_chunk_inter_f32.  Any
+ * other pass is GDN2_EINVAL. */
 GDN2_API int64_t gdn2_chunk_segments(const gdn2_chunk_args *args);
 GDN2_API gdn2_status gdn2_chunk_inter_pass_f32(const gdn2_chunk_args *args, int pass, gdn2_stream_t stream);
 
