@@ -44,10 +44,10 @@ struct BwdParams {
     float *ws_dsn;                    // K*V  dL/d(state leaving the chunk), column fragments
     float *ws_dvn;                    // C*V  dL/dv_new, column fragments
     float *ws_dqg, *ws_dkd;           // C*K  dL/dQG, dL/dKd, fragments
-    float *ws_daqk;                   // C*C  dL/dA_qk (lower), row-major
+    float *ws_daqk;                   // C*C  dL/dA_qk, fragments (the lower block triangle only)
     float *ws_dgam;                   // K    dL/d e^{G_last}
     float *ws_drk;                    // C*K  dL/dRk, fragments
-    float *ws_dakk;                   // C*C  dL/dA_kk (strictly lower), row-major
+    float *ws_dakk;                   // C*C  dL/dA_kk, fragments (the lower block triangle only)
     float *ws_kgrad;                  // rep > 1: 4 x (C*K per chunk): dq, dk, dg, db per value head
     // segmented reverse recurrence (NSEG > 1), per (b, hv):
     float *ws_rseg;                   // NSEG x K*V  the gradient leaving each segment (slot j - 1
@@ -457,11 +457,13 @@ struct VprodSmem {
     // value loop: S, dS' slices [2][K][SP]; v_new, dv_new and U slices [2][C][SP]
     static constexpr size_t oS = 0, oD = oS + 4 * 2 * K * SP, oV = oD + 4 * 2 * K * SP, oDV = oV + 4 * 2 * C * SP;
     static constexpr size_t oU = oDV + 4 * 2 * C * SP, stage = oU + 4 * 2 * C * SP;
-    // solve: dW, then dRk [C][KP]; dUU fragments [NT * NT * 64]
-    static constexpr size_t oR = 0, oUU = oR + 4 * C * KP;
-    static constexpr size_t solve = oUU + 16 * NT * NT * 64;
+    // solve: dW, then dRk [C][KP]; dUU fragments [NT * NT * 64]; per wave a
+    // [C][SP] tile of v, w, dv or dw rows (the transpose between 16-byte rows
+    // and accumulator fragments)
+    static constexpr size_t oR = 0, oUU = oR + 4 * C * KP, oX = oUU + 16 * NT * NT * 64;
+    static constexpr size_t solve = oX + 4 * 4 * C * SP;
     static constexpr size_t bytes = stage > solve ? stage : solve;
-    static_assert(oU % 16 == 0 && oUU % 16 == 0, "float4 alignment");
+    static_assert(oU % 16 == 0 && oUU % 16 == 0 && oX % 16 == 0, "float4 alignment");
 };
 
 template <int K, int V>
@@ -590,10 +592,11 @@ __global__ __launch_bounds__(256, K >= 256 ? 1 : 2) void bwd_vprod_kernel(BwdPar
             __syncthreads();
         }
     }
-    // dQG, dKd (fragments), dA_qk (row-major) and dgam go to the decay kernel
+    // dQG, dKd, dA_qk (fragments; tiles (wave, st <= wave) only, the decay kernel
+    // reads no other) and dgam go to the decay kernel
     floatx4 *oQ = reinterpret_cast<floatx4 *>(bp.ws_dqg) + (size_t)cid * (C * K / 4);
     floatx4 *oK = reinterpret_cast<floatx4 *>(bp.ws_dkd) + (size_t)cid * (C * K / 4);
-    float *oA = bp.ws_daqk + (size_t)cid * C * C;
+    floatx4 *oA = reinterpret_cast<floatx4 *>(bp.ws_daqk) + (size_t)cid * (C * C / 4);
 #pragma unroll
     for (int t = 0; t < NKT; ++t) {
         oQ[(wave * NKT + t) * 64 + lane] = aQ[t];
@@ -601,10 +604,11 @@ __global__ __launch_bounds__(256, K >= 256 ? 1 : 2) void bwd_vprod_kernel(BwdPar
     }
 #pragma unroll
     for (int st = 0; st < NT; ++st)
+        if (st <= wave) { // wave-uniform
+            floatx4 a = aA[st];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 16 * wave + 4 * lg + i, sc = 16 * st + lr;
-            oA[r * C + sc] = sc <= r ? aA[st][i] : 0.f;
+            for (int i = 0; i < 4; ++i) a[i] = 16 * st + lr <= 16 * wave + 4 * lg + i ? a[i] : 0.f;
+            oA[(wave * NT + st) * 64 + lane] = a;
         }
     // dgam: a row's 16 columns of every slice were staged by the 16 lanes 16 g .. 16 g + 15
 #pragma unroll
@@ -648,9 +652,18 @@ __global__ __launch_bounds__(256, K >= 256 ? 1 : 2) void bwd_vprod_kernel(BwdPar
     const int64_t vo = (int64_t)bi * p.svb + (int64_t)hv * p.svh + (int64_t)(n * C) * p.svt;
     const int rv = (int)p.svt;
     const __amdgpu_buffer_rsrc_t Rv = rows_rsrc(p.v + vo, rv, cv, V), Rw = rows_rsrc(p.w + vo, rv, cv, V);
+    const __amdgpu_buffer_rsrc_t Rdv = rows_rsrc(bp.dv + vo, rv, cv, V), Rdw = rows_rsrc(bp.dw + vo, rv, cv, V);
+    // this wave's [C][SP] tile: v, w, dv, dw move as 16-byte row pieces (lane
+    // l: row 16 m + l / 4, columns 4 (l % 4) .. + 3 of the 16-column tile) and
+    // are read or written there in accumulator layout (rows 4 lg + i, column
+    // lr): 8 loads and 8 stores per value column tile where per-element
+    // accesses took 64
+    float(*sX)[SP] = reinterpret_cast<float(*)[SP]>(smem + SM::oX) + wave * C;
+    const int xr = lane >> 2, xc = 4 * (lane & 3);
 #pragma unroll 1
     for (int ct = wave; ct < NCT; ct += 4) {
         const bool kcol = ct < NKT;
+        const int vc = ct - NKT;
         floatx4 xb[NT]; // B fragments X[16 st + 4 g + j][column lr]
         float vv[NT][4], ww[NT][4];
         if (kcol) {
@@ -660,16 +673,28 @@ __global__ __launch_bounds__(256, K >= 256 ? 1 : 2) void bwd_vprod_kernel(BwdPar
                 for (int j = 0; j < 4; ++j) xb[st][j] = sR[16 * st + 4 * lg + j][16 * ct + lr];
         } else {
 #pragma unroll
-            for (int st = 0; st < NT; ++st) xb[st] = dvn[((ct - NKT) * NT + st) * 64 + lane];
+            for (int st = 0; st < NT; ++st) xb[st] = dvn[(vc * NT + st) * 64 + lane];
+            floatx4 v4[NT], w4[NT];
+#pragma unroll
+            for (int m = 0; m < NT; ++m) {
+                const int o = (16 * m + xr) * rv + 16 * vc + xc;
+                v4[m] = bld4(Rv, o);
+                w4[m] = bld4(Rw, o);
+            }
+#pragma unroll
+            for (int m = 0; m < NT; ++m) *reinterpret_cast<floatx4 *>(&sX[16 * m + xr][xc]) = v4[m];
 #pragma unroll
             for (int rt = 0; rt < NT; ++rt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int o = (16 * rt + 4 * lg + i) * rv + 16 * (ct - NKT) + lr;
-                    vv[rt][i] = bld1(Rv, o);
-                    ww[rt][i] = bld1(Rw, o);
-                }
+                for (int i = 0; i < 4; ++i) vv[rt][i] = sX[16 * rt + 4 * lg + i][lr];
+#pragma unroll
+            for (int m = 0; m < NT; ++m) *reinterpret_cast<floatx4 *>(&sX[16 * m + xr][xc]) = w4[m];
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ww[rt][i] = sX[16 * rt + 4 * lg + i][lr];
         }
+        floatx4 dr[NT]; // dRv tiles of a value column tile
 #pragma unroll
         for (int rt = 0; rt < NT; ++rt) {
             floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -681,48 +706,57 @@ __global__ __launch_bounds__(256, K >= 256 ? 1 : 2) void bwd_vprod_kernel(BwdPar
 #pragma unroll
                 for (int i = 0; i < 4; ++i) sR[16 * rt + 4 * lg + i][16 * ct + lr] = acc[i];
             } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = 16 * rt + 4 * lg + i;
-                    if (r < cv) {
-                        const int64_t o = vo + (int64_t)r * p.svt + 16 * (ct - NKT) + lr;
-                        bp.dv[o] = acc[i] * ww[rt][i];
-                        bp.dw[o] = acc[i] * vv[rt][i];
-                    }
-                }
+                dr[rt] = acc;
             }
+        }
+        if (!kcol) { // dv = dRv * w, then dw = dRv * v, out as 16-byte row pieces
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sX[16 * rt + 4 * lg + i][lr] = dr[rt][i] * ww[rt][i];
+#pragma unroll
+            for (int m = 0; m < NT; ++m)
+                bst4(Rdv, (16 * m + xr) * rv + 16 * vc + xc, *reinterpret_cast<const floatx4 *>(&sX[16 * m + xr][xc]));
+#pragma unroll
+            for (int rt = 0; rt < NT; ++rt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sX[16 * rt + 4 * lg + i][lr] = dr[rt][i] * vv[rt][i];
+#pragma unroll
+            for (int m = 0; m < NT; ++m)
+                bst4(Rdw, (16 * m + xr) * rv + 16 * vc + xc, *reinterpret_cast<const floatx4 *>(&sX[16 * m + xr][xc]));
         }
     }
     __syncthreads(); // sR holds dRk
 
-    // dA_kk tiles (rt, st): -(dRk W^T + Ai^T dUU) on the lower tiles, zero above
+    // dA_kk tiles (rt, st), st <= rt (the decay kernel reads no other): the
+    // j-th of the ten, j = rt (rt + 1) / 2 + st, goes to wave j % 4 (three or
+    // two tiles each); -(dRk W^T + Ai^T dUU), zero on and above the diagonal,
+    // as fragments
     const floatx4 *Wf = reinterpret_cast<const floatx4 *>(p.ws_w) + (size_t)cid * (C * K / 4);
-    float *dakk = bp.ws_dakk + (size_t)cid * C * C;
+    floatx4 *dakk = reinterpret_cast<floatx4 *>(bp.ws_dakk) + (size_t)cid * (C * C / 4);
 #pragma unroll 1
-    for (int tl = wave; tl < NT * NT; tl += 4) {
-        const int rt = tl / NT, st = tl % NT;
+    for (int j = wave; j < NLT; j += 4) {
+        int rt = 0;
+        while ((rt + 1) * (rt + 2) / 2 <= j) ++rt;
+        const int st = j - rt * (rt + 1) / 2;
+        floatx4 wb[NKT], ub[NT], ab[NT];
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) wb[kt] = Wf[(st * NKT + kt) * 64 + lane];
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt) {
+            ub[mt] = mt >= rt ? sUU[(mt * NT + st) * 64 + lane] : floatx4{0.f, 0.f, 0.f, 0.f};
+            ab[mt] = mt >= rt ? Aif[(mt * NT + rt) * 64 + lane] : floatx4{0.f, 0.f, 0.f, 0.f}; // Ai^T (rt, mt)
+        }
         floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-        if (st <= rt) {
-            floatx4 wb[NKT], ub[NT], ab[NT];
 #pragma unroll
-            for (int kt = 0; kt < NKT; ++kt) wb[kt] = Wf[(st * NKT + kt) * 64 + lane];
+        for (int kt = 0; kt < NKT; ++kt) // A: dRk rows 16 rt + lr; B: W^T = W's A fragment (st, kt)
+            acc = mfma4x(*reinterpret_cast<const floatx4 *>(&sR[16 * rt + lr][16 * kt + 4 * lg]), wb[kt], acc);
 #pragma unroll
-            for (int mt = 0; mt < NT; ++mt) {
-                ub[mt] = mt >= rt ? sUU[(mt * NT + st) * 64 + lane] : floatx4{0.f, 0.f, 0.f, 0.f};
-                ab[mt] = mt >= rt ? Aif[(mt * NT + rt) * 64 + lane] : floatx4{0.f, 0.f, 0.f, 0.f}; // Ai^T (rt, mt)
-            }
+        for (int mt = 0; mt < NT; ++mt)
+            if (mt >= rt) acc = mfma4x(ab[mt], ub[mt], acc);
 #pragma unroll
-            for (int kt = 0; kt < NKT; ++kt) // A: dRk rows 16 rt + lr; B: W^T = W's A fragment (st, kt)
-                acc = mfma4x(*reinterpret_cast<const floatx4 *>(&sR[16 * rt + lr][16 * kt + 4 * lg]), wb[kt], acc);
-#pragma unroll
-            for (int mt = 0; mt < NT; ++mt)
-                if (mt >= rt) acc = mfma4x(ab[mt], ub[mt], acc);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 16 * rt + 4 * lg + i, s2 = 16 * st + lr;
-            dakk[r * C + s2] = s2 < r ? -acc[i] : 0.f;
-        }
+        for (int i = 0; i < 4; ++i) acc[i] = 16 * st + lr < 16 * rt + 4 * lg + i ? -acc[i] : 0.f;
+        dakk[(rt * NT + st) * 64 + lane] = acc;
     }
 }
 
@@ -788,12 +822,21 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
             vals[i] = acc;
         }
         sTot[seg][c] = acc;
+        // dA_qk, dA_kk: the fragments of the lower block triangle (tile (rt, st),
+        // lane (g, c): rows 16 rt + 4 g .. + 3 of column 16 st + c), the only
+        // tiles read below, into row-major LDS
         const floatx4 *da = reinterpret_cast<const floatx4 *>(bp.ws_daqk + (size_t)cid * C * C);
         const floatx4 *dk = reinterpret_cast<const floatx4 *>(bp.ws_dakk + (size_t)cid * C * C);
         for (int f = tid; f < C * C / 4; f += NTH) {
-            const int r = f / (C / 4), c4 = f % (C / 4);
-            *reinterpret_cast<floatx4 *>(&sDA[r][4 * c4]) = da[f];
-            *reinterpret_cast<floatx4 *>(&sDK[r][4 * c4]) = dk[f];
+            const int tile = f >> 6, rt = tile / NT, st = tile % NT; // wave-uniform (NTH % 64 == 0)
+            if (st > rt) continue;
+            const int l = f & 63, r0 = 16 * rt + 4 * (l >> 4), c = 16 * st + (l & 15);
+            const floatx4 a = da[f], b = dk[f];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sDA[r0 + i][c] = a[i];
+                sDK[r0 + i][c] = b[i];
+            }
         }
         __syncthreads();
         float off = 0.f;

@@ -39,6 +39,12 @@ __device__ __forceinline__ void bst1(__amdgpu_buffer_rsrc_t r, int idx, float v)
 __device__ __forceinline__ floatx4 bld4(__amdgpu_buffer_rsrc_t r, int idx) {
     return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, idx * 4, 0, 0));
 }
+// 16 bytes through a rows_rsrc resource (idx a multiple of 4 within a row):
+// dropped past its last valid row.
+__device__ __forceinline__ void bst4(__amdgpu_buffer_rsrc_t r, int idx, floatx4 v) {
+    typedef int intx4 __attribute__((ext_vector_type(4)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(intx4, v), r, idx * 4, 0, 0);
+}
 
 __device__ __forceinline__ floatx4 mfma4(float4 a, floatx4 b, floatx4 c) {
     c = mfma16(a.x, b[0], c);
