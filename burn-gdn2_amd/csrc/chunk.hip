@@ -1254,9 +1254,10 @@ bool split_segments(const ChunkParams &p, bool wide_pass1, ChunkParams *q) {
     return true;
 }
 
-// A second stream per device (default priority, non-blocking) with a fork
-// and a join event, for the split's segment-0 walk beside pass 1.  Created on
-// first use, never while the caller's stream is capturing (then, and if
+// A second stream per device (default priority, non-blocking; on the device
+// of the caller's stream) with a fork and a join event, for the split's
+// segment-0 walk beside pass 1.  Created on first use, never while the
+// caller's stream is capturing (then, and if
 // creation fails, the two launches run in order on the caller's stream: the
 // same kernels and results).  One mutex keeps each record/wait/launch/record/
 // wait sequence whole when several host threads launch.
@@ -1270,27 +1271,29 @@ std::mutex g_aux_mu;
 AuxStream g_aux[kMaxDevices];
 
 AuxStream *aux_stream(hipStream_t s) { // called with g_aux_mu held
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    hipDevice_t dev = 0; // the device of the caller's stream, where its kernels run
+    if (hipStreamGetDevice(s, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
     AuxStream &a = g_aux[dev];
     if (a.s) return &a;
     if (a.tried) return nullptr;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
     a.tried = true;
-    if (hipStreamCreateWithFlags(&a.s, hipStreamNonBlocking) != hipSuccess) {
-        a.s = nullptr;
-        return nullptr;
-    }
-    if (hipEventCreateWithFlags(&a.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&a.join, hipEventDisableTiming) != hipSuccess) {
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return nullptr;
+    bool ok = hipStreamCreateWithFlags(&a.s, hipStreamNonBlocking) == hipSuccess;
+    if (!ok) a.s = nullptr;
+    ok = ok && hipEventCreateWithFlags(&a.fork, hipEventDisableTiming) == hipSuccess &&
+         hipEventCreateWithFlags(&a.join, hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
         if (a.fork) (void)hipEventDestroy(a.fork);
-        (void)hipStreamDestroy(a.s);
+        if (a.s) (void)hipStreamDestroy(a.s);
         a = AuxStream{};
         a.tried = true;
-        return nullptr;
     }
-    return &a;
+    if (cur != dev) (void)hipSetDevice(cur);
+    return ok ? &a : nullptr;
 }
 
 // on_aux(stream) after the work queued on s so far, beside on_s(s); s then
