@@ -231,6 +231,55 @@ def test_chunk_split_first_segment_matches_recurrence(gpu, case):
     assert eo < TOL and es < TOL
 
 
+def test_split_forward_from_two_host_threads(gpu):
+    """Two host threads launch the split forward at once, each on a stream of
+    its own: the library's second stream and its fork and join events are
+    shared per device, so each thread's fork/join sequence must stay whole.
+    Each result equals the same call made alone, bit for bit."""
+    import threading
+
+    import torch
+
+    import gdn2_amd
+
+    B, Hk, HV, T, K, V = 1, 8, 16, 9000, 128, 128
+    assert split_plan(B, HV, T, K, V)[1] is not None
+    sets = []
+    for seed in (11, 12):
+        rng = np.random.default_rng(seed)
+        q, k, v, g, b, w = rand_inputs(rng, B, Hk, HV, T, K, V, g_lo=-0.05, g_hi=-0.005)
+        S0 = (rng.standard_normal((B, HV, K, V)) * 0.3).astype(np.float32)
+        sets.append(_dev(gpu, q, k, v, g, b, w, S0))
+    scale = K ** -0.5
+    ref = []
+    for d in sets:
+        o, S = gdn2_amd.chunk_wy_forward(*d, scale, chunk_size=64)
+        torch.cuda.synchronize()
+        ref.append((o.clone(), S.clone()))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    got, errors = [None, None], []
+    start = threading.Barrier(2)
+
+    def run(i):
+        try:
+            with torch.cuda.stream(streams[i]):
+                start.wait()
+                for _ in range(3):
+                    got[i] = gdn2_amd.chunk_wy_forward(*sets[i], scale, chunk_size=64)
+                streams[i].synchronize()
+        except Exception as e:  # surfaced below, in the test's own thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i in range(2):
+        assert torch.equal(got[i][0], ref[i][0]) and torch.equal(got[i][1], ref[i][1]), f"thread {i}"
+
+
 def test_chunk_strided_views_and_in_place_state(gpu):
     """q/k/g/b/v/w as [B, H, T, D] views of [B, T, H, D] storage and out
     written straight into [B, T, HV, V] (no permute copies)."""
