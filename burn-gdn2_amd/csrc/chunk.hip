@@ -155,43 +155,54 @@ __global__ __launch_bounds__(512, K > 128 ? 2 : 4) void chunk_intra_kernel(Chunk
             *reinterpret_cast<floatx4 *>(&sK[row][4 * c4]) = kreg[i];
         }
         __syncthreads();
-        float off = 0.f;
+        float off = 0.f, later = 0.f;
         for (int s2 = 0; s2 < seg; ++s2) off += sTot[s2][c];
+        for (int s2 = seg + 1; s2 < NSEG; ++s2) later += sTot[s2][c];
 #pragma unroll
         for (int i = 0; i < RPS; ++i) sG[seg * RPS + i][c] = (vals[i] + off) * kLog2e;
+        // Kd = k exp(G_last - G), this thread's rows of channel c, with the
+        // exponent summed from the chunk's end: the segment's own later rows
+        // (acc - vals[i]) plus the later segments' totals.  Formed as the
+        // difference of the two cumulative sums (the reference's form,
+        // src/forward.rs:271-274) it carries their rounding at |G| up to 64 |g|:
+        // at strong decay (|G| near 2900 in log2 units, f32 spacing 2.4e-4) that
+        // is ~1e-4 relative in every factor, the last tokens' (the largest)
+        // included.  Kd^T as A-operand fragments (kb, tt): lane (g, r) holds
+        // Kd[16 tt + 4 g + j][16 kb + r], four rows per 16-byte store.  The
+        // training variant's Kd, fragments (tt, kb) with lane (g, r) holding
+        // Kd[16 tt + r][16 kb + 4 g + j], takes a 4 x 4 transpose among the
+        // four lanes of consecutive channels (two quad exchanges) first, then
+        // one 16-byte store per row.
+        {
+            static_assert(RPS % 4 == 0, "four rows per store");
+            floatx4 *Kf = reinterpret_cast<floatx4 *>(p.ws_kdt) + cid * (C * K / 4);
+            floatx4 *Kdf = reinterpret_cast<floatx4 *>(p.ws_kd) + cid * (C * K / 4);
+            const int kb = c / 16, r = c % 16, qi = lane & 3; // c % 4 == lane % 4
+#pragma unroll
+            for (int q4 = 0; q4 < RPS / 4; ++q4) {
+                const int t0 = seg * RPS + 4 * q4; // rows t0 .. t0 + 3: one tile, one lane group
+                floatx4 val;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int i = 4 * q4 + j;
+                    val[j] = sK[t0 + j][c] * fast_exp2((acc - vals[i] + later) * kLog2e);
+                }
+                st_stream(Kf + (kb * NT + t0 / 16) * 64 + 16 * ((t0 % 16) / 4) + r, val);
+                if (TRAIN) {
+                    // lane qi of the quad holds rows t0 .. t0 + 3 of channel c;
+                    // afterwards row t0 + qi of channels c - qi .. c - qi + 3
+                    floatx4 x = val;
+                    quad_swap_halves(x, (qi & 2) != 0);
+                    quad_swap_pairs(x, (qi & 1) != 0);
+                    const int t = t0 + qi;
+                    st_stream(Kdf + ((t / 16) * NKT + kb) * 64 + 16 * ((c % 16) / 4) + t % 16, x);
+                }
+            }
+        }
         __syncthreads();
     }
-    // Kd^T = (k exp(G_last - G))^T as A-operand fragments (kb, tt): lane
-    // (g, r) holds Kd[16 tt + 4 g + j][16 kb + r]; and exp(G_last).  k comes
-    // from LDS, so the chunk's k is read from memory once.
-    {
-        floatx4 *Kf = reinterpret_cast<floatx4 *>(p.ws_kdt) + cid * (C * K / 4);
-        constexpr int KDF = NKT * NT / NW; // fragments per wave
-#pragma unroll
-        for (int j = 0; j < KDF; ++j) {
-            const int f = wave + NW * j, kb = f / NT, tt = f % NT, ch = 16 * kb + lr;
-            const float gl = sG[C - 1][ch];
-            floatx4 val;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * tt + 4 * lg + i;
-                val[i] = sK[t][ch] * fast_exp2(gl - sG[t][ch]);
-            }
-            st_stream(Kf + f * 64 + lane, val);
-        }
-        if (tid < K) p.ws_gam[cid * K + tid] = fast_exp2(sG[C - 1][tid]);
-        if (TRAIN) { // Kd as A-operand fragments (tt, kb): lane (g, r) holds Kd[16 tt + r][16 kb + 4 g + j]
-            floatx4 *Kdf = reinterpret_cast<floatx4 *>(p.ws_kd) + cid * (C * K / 4);
-#pragma unroll
-            for (int j = 0; j < KDF; ++j) {
-                const int f = wave + NW * j, tt = f / NKT, kb = f % NKT, c0 = 16 * kb + 4 * lg, t = 16 * tt + lr;
-                const floatx4 gl = *reinterpret_cast<const floatx4 *>(&sG[C - 1][c0]);
-                const floatx4 gt = *reinterpret_cast<const floatx4 *>(&sG[t][c0]);
-                const floatx4 kt = *reinterpret_cast<const floatx4 *>(&sK[t][c0]);
-                st_stream(Kdf + f * 64 + lane, kt * exp2v(gl - gt));
-            }
-        }
-    }
+    if (tid < K) p.ws_gam[cid * K + tid] = fast_exp2(sG[C - 1][tid]); // exp(G_last)
+
     // The score products' reference per (row tile, channel): Gb = G at the end
     // of the previous tile (0 for the first); for a mid-range span the middle
     // of the tile's range, (Gb + G_end) / 2, for the whole row tile. Its

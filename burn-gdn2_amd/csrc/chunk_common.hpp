@@ -96,6 +96,36 @@ __device__ __forceinline__ floatx4 exp2v(floatx4 x) {
     return floatx4{fast_exp2(x[0]), fast_exp2(x[1]), fast_exp2(x[2]), fast_exp2(x[3])};
 }
 
+// The two steps of a 4 x 4 transpose among the four lanes of a quad, whose
+// lane i holds row i (elements 0 .. 3): afterwards lane i holds column i.
+// Step 1, partner i ^ 2 (dpp quad_perm [2, 3, 0, 1]): the lower two lanes
+// trade elements 2, 3 for the partner's 0, 1.  Step 2, partner i ^ 1
+// (quad_perm [1, 0, 3, 2]): the even lanes trade elements 1, 3 for the
+// partner's 0, 2.  Every lane of the wave must be active.
+template <int CTRL> __device__ __forceinline__ float quad_perm(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ void quad_swap_halves(floatx4 &x, bool upper) { // upper = i & 2
+    const float r0 = quad_perm<0x4E>(upper ? x[0] : x[2]), r1 = quad_perm<0x4E>(upper ? x[1] : x[3]);
+    if (upper) {
+        x[0] = r0;
+        x[1] = r1;
+    } else {
+        x[2] = r0;
+        x[3] = r1;
+    }
+}
+__device__ __forceinline__ void quad_swap_pairs(floatx4 &x, bool odd) { // odd = i & 1
+    const float r0 = quad_perm<0xB1>(odd ? x[0] : x[1]), r1 = quad_perm<0xB1>(odd ? x[2] : x[3]);
+    if (odd) {
+        x[0] = r0;
+        x[2] = r1;
+    } else {
+        x[1] = r0;
+        x[3] = r1;
+    }
+}
+
 // Direct global -> LDS copy of one float4 per lane (global_load_lds_dwordx4):
 // lane l of the calling wave writes wave_base[l]; wave_base is wave-uniform.
 // The copy counts in vmcnt: wait with vm_wait0() before the barrier that

@@ -17,7 +17,10 @@ to 31 per token |G| nears 2000 (log2 units) by a chunk's end, where the f32
 spacing is 1.2e-4, so those terms carry relative errors near 1e-4 in any
 kernel that forms them from such sums; dg, a sum of such terms (|k * dk| up
 to ~5 here) that nearly cancel (|dg| ~ 1), would meet a bound on its own
-magnitude only by a few percent, or not, in the strongest cases."""
+magnitude only by a few percent, or not, in the strongest cases.
+GDN2_SWEEP_CASES (default 2) sets the cases per shape for a deeper run."""
+import os
+
 import numpy as np
 import pytest
 
@@ -46,7 +49,9 @@ def _draw(K, V, i):
                 s0=float(rng.choice([0.0, 0.5])), dst=bool(rng.integers(2)), seed=int(rng.integers(1 << 30)))
 
 
-CASES = [(K, V, i) for K, V in SHAPES for i in range(2)]
+# cases per shape: 2 by default; GDN2_SWEEP_CASES raises it for a deeper run
+NCASES = int(os.environ.get("GDN2_SWEEP_CASES", "2"))
+CASES = [(K, V, i) for K, V in SHAPES for i in range(NCASES)]
 
 
 @pytest.mark.parametrize("K,V,i", CASES, ids=[f"K{K}V{V}-{i}" for K, V, i in CASES])
