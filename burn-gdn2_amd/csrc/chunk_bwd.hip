@@ -786,9 +786,13 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
     const ChunkParams &p = bp.f;
     constexpr int NTH = K * 4, NSEG = NTH / K, RPS = C / NSEG; // cumsum: NSEG row segments per channel
     constexpr int KP = K + 4, CP = C + 4;
-    __shared__ __attribute__((aligned(16))) float sG[C][KP]; // G (log2 units), then dG
+    // sG: per row the cumulative sum of g from its tile's first row (nats),
+    // then dG; G (log2 units) = (sG + sOff) * log2 e, sOff the sum of the
+    // tiles before (the tiles are the scan's segments: NSEG == NT)
+    __shared__ __attribute__((aligned(16))) float sG[C][KP];
     __shared__ __attribute__((aligned(16))) float sDA[C][CP], sDK[C][CP];
-    __shared__ float sTot[NSEG][K];
+    __shared__ float sTot[NSEG][K], sOff[NSEG][K];
+    static_assert(NSEG == NT && RPS == 16, "one scan segment per row tile");
     const int cid = blockIdx.x, bh = cid / p.NC, n = cid % p.NC;
     const int bi = bh / p.HV, hv = bh % p.HV, hk = hv / p.rep;
     const int cv = min(C, p.T - n * C);
@@ -819,7 +823,7 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
 #pragma unroll
         for (int i = 0; i < RPS; ++i) {
             acc += vals[i];
-            vals[i] = acc;
+            sG[seg * RPS + i][c] = acc;
         }
         sTot[seg][c] = acc;
         // dA_qk, dA_kk: the fragments of the lower block triangle (tile (rt, st),
@@ -841,11 +845,11 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
         __syncthreads();
         float off = 0.f;
         for (int s2 = 0; s2 < seg; ++s2) off += sTot[s2][c];
-#pragma unroll
-        for (int i = 0; i < RPS; ++i) sG[seg * RPS + i][c] = (vals[i] + off) * kLog2e;
+        sOff[seg][c] = off;
         __syncthreads();
     }
-    const float gl = sG[C - 1][ch];
+    // G at row r of this lane's channel, log2 units
+    auto Gat = [&](int r) { return (sG[r][ch] + sOff[r / 16][ch]) * kLog2e; };
     // Gb_t: G at the end of tile t-1, or, for a span in (96, 192], the middle
     // of tile t's range, (Gb_t + G_end) / 2, as in the forward: the diagonal
     // factors then lie in [2^-96, 2^96] and the off-diagonal column factors
@@ -854,7 +858,7 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
     bool msk[NT]; // diagonal block of tile t beyond 192: exact pairwise terms
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        const float b0 = t ? sG[16 * t - 1][ch] : 0.f, ge = sG[16 * t + 15][ch];
+        const float b0 = t ? Gat(16 * t - 1) : 0.f, ge = Gat(16 * t + 15);
         const float span = b0 - ge;
         msk[t] = span > 192.f;
         gb[t] = (span > 96.f && span <= 192.f) ? 0.5f * (b0 + ge) : b0;
@@ -890,10 +894,10 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
     // and adds their products to the column sums of every column tile <= t;
     // column tile t then has all its terms (they come from row tiles >= t), so
     // the step finishes it with the row sums of row tile t and tile t's
-    // elementwise terms.  Those overwrite tile t's rows of G with dG: only this
-    // wave reads this channel's G, every later use of tile t's G is from
-    // registers, and the pairwise terms that read G from LDS (row and column
-    // sums of tile t's diagonal block) come before in the same step.
+    // elementwise terms.  Those overwrite tile t's rows of sG with dG: only
+    // this wave reads this channel's sG, later steps read tiles < t only, the
+    // pairwise terms of tile t's diagonal block read it earlier in the step,
+    // and each elementwise row reads its own tile-local sum before writing.
     floatx4 ckt[NT]; // column sums of column tiles 0 .. t
 #pragma unroll
     for (int t = 0; t < NT; ++t) ckt[t] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -901,7 +905,7 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
     for (int t = NT - 1; t >= 0; --t) {
         float gt[4]; // G at this lane's rows of tile t
 #pragma unroll
-        for (int j = 0; j < 4; ++j) gt[j] = sG[16 * t + 4 * lg + j][ch];
+        for (int j = 0; j < 4; ++j) gt[j] = Gat(16 * t + 4 * lg + j);
         floatx4 bq, bb; // column operands of row tile t
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -920,7 +924,7 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
                 floatx4 wd, kt, a1, a2;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    wd[j] = (ct == t && msk[t]) ? 0.f : fast_exp2(gb[t] - sG[16 * ct + 4 * lg + j][ch]);
+                    wd[j] = (ct == t && msk[t]) ? 0.f : fast_exp2(gb[t] - Gat(16 * ct + 4 * lg + j));
                     kt[j] = kv[ct][j] * wd[j];
                     a1[j] = sDA[16 * t + 4 * lg + j][16 * ct + lr];
                     a2[j] = sDK[16 * t + 4 * lg + j][16 * ct + lr];
@@ -959,7 +963,7 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
                         const int s = 4 * sg + u;
-                        const float gs = sG[16 * t + s][ch];
+                        const float gs = Gat(16 * t + s);
                         const float ks = __shfl(kv[t][u], 16 * sg + lr, 64);
                         float cs = 0.f;
 #pragma unroll
@@ -982,10 +986,18 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
         const floatx4 ck = ckt[t];
         const floatx4 fqg = dqg[(t * NKT + wave) * 64 + lane], fkd = dkd[(t * NKT + wave) * 64 + lane];
         const floatx4 frk = drk[(t * NKT + wave) * 64 + lane];
+        // e^{G_last - G_r} from the sum of g after row r: the rest of tile t
+        // (its total less row r's tile-local sum) and the tiles after it, added
+        // at that sum's own magnitude, where gl - G_r would subtract two sums
+        // from the chunk's start rounded at theirs
+        const float tot = sTot[t][ch];
+        float later = 0.f;
+#pragma unroll
+        for (int u = t + 1; u < NT; ++u) later += sTot[u][ch];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 16 * t + 4 * lg + i;
-            const float eG = fast_exp2(gt[i]), eKd = fast_exp2(gl - gt[i]);
+            const float eG = fast_exp2(gt[i]), eKd = fast_exp2((tot - sG[r][ch] + later) * kLog2e);
             const float vqg = fqg[i], vkd = fkd[i], vrk = frk[i];
             const int o = r * rq_ + ch;
             const float qr = bld1(Rq, o), kr = kv[t][i], br = bld1(Rb, o);
@@ -1011,6 +1023,9 @@ __global__ __launch_bounds__(K * 4, K >= 256 ? 4 : K / 32) void bwd_decay_kernel
         tot += sG[16 * lg + m][ch];
         part[m] = tot;
     }
+    // G_last from the last tile's total (its last row's tile-local sum; that
+    // row of sG holds dG by now)
+    const float gl = (sTot[NT - 1][ch] + sOff[NT - 1][ch]) * kLog2e;
     float after = kt_sum + bp.ws_dgam[(size_t)cid * K + ch] * fast_exp2(gl);
 #pragma unroll
     for (int j = 1; j < 4; ++j) {
