@@ -18,7 +18,9 @@ spacing is 1.2e-4, so those terms carry relative errors near 1e-4 in any
 kernel that forms them from such sums; dg, a sum of such terms (|k * dk| up
 to ~5 here) that nearly cancel (|dg| ~ 1), would meet a bound on its own
 magnitude only by a few percent, or not, in the strongest cases.
-GDN2_SWEEP_CASES (default 2) sets the cases per shape for a deeper run."""
+GDN2_SWEEP_CASES (default 50, 600 cases in about 10 s) sets the cases per
+shape for a deeper run; the cases are seeded, so a deeper run repeats these
+and adds more."""
 import os
 
 import numpy as np
@@ -49,8 +51,8 @@ def _draw(K, V, i):
                 s0=float(rng.choice([0.0, 0.5])), dst=bool(rng.integers(2)), seed=int(rng.integers(1 << 30)))
 
 
-# cases per shape: 2 by default; GDN2_SWEEP_CASES raises it for a deeper run
-NCASES = int(os.environ.get("GDN2_SWEEP_CASES", "2"))
+# cases per shape: 50 by default; GDN2_SWEEP_CASES sets it
+NCASES = int(os.environ.get("GDN2_SWEEP_CASES", "50"))
 CASES = [(K, V, i) for K, V in SHAPES for i in range(NCASES)]
 
 
